@@ -1,0 +1,412 @@
+// attention.hip - grouped-query attention over a KV cache on gfx950.
+//
+// Semantics follow CpuBackend.attentionGqa / computeAttentionGroup
+// (backend/cpu/aljabr-backend-cpu/.../CpuBackend.java:1546-1748): per query
+// row, online softmax over the visible keys; bottom-right causal alignment
+// (key limit = Sk - Sq + qi + 1); an additive mask entry of -inf skips the key;
+// a row with no visible key yields 0.
+//
+// Split-K design (head_dim 64 or 128). Work item = (batch, kv head, query
+// row); its key range is cut into `splits` chunks, one workgroup each. A
+// workgroup serves all G = Hq/Hkv query heads of its KV head, so every K/V
+// byte is read once per query row. Inside a workgroup, a key row of D fp16
+// values is read by D/8 lanes (16 bytes each); the wave's lane groups walk
+// interleaved keys in tiles of 4, keep (max, sum, o[8]) per head in
+// registers, and reduce q.k across the group's lanes with DPP. Group states
+// are merged through LDS; with one split the workgroup writes the normalised
+// output, otherwise (m, l, o) partials go to scratch and a merge kernel
+// combines splits. Scores use exp2 with log2(e) folded into the query.
+#include <cmath>
+
+#include "device.hpp"
+#include "internal.hpp"
+#include "kernels.hpp"
+
+namespace aljabr {
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kTile = 4;
+
+template <int LPK>
+__device__ __forceinline__ float group_sum(float v) {
+    // Sum over the LPK lanes of a key group (LPK = 8 or 16, aligned groups).
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    if constexpr (LPK == 16) v += dpp_f32<0x140>(v);
+    return v;
+}
+
+template <bool F16>
+__device__ __forceinline__ void load8(const void *base, long long idx, float (&r)[8]) {
+    if constexpr (F16) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + idx);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+            r[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+        }
+    } else {
+        const float4 a = *reinterpret_cast<const float4 *>(static_cast<const float *>(base) + idx);
+        const float4 b = *reinterpret_cast<const float4 *>(static_cast<const float *>(base) + idx + 4);
+        r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
+        r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
+    }
+}
+
+// grid: x = split, y = kv head * Sq + query row, z = batch. WAVES*64 threads.
+template <int D, int G, bool F16, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, int splits, int chunk,
+                                                                float *__restrict__ part) {
+    constexpr int LPK = D / 8;                 // lanes per key row
+    constexpr int GPW = 64 / LPK;              // key groups per wave
+    constexpr int NG = GPW * WAVES;            // key groups per workgroup
+    extern __shared__ float smem[];            // [NG][G][D + 2]
+
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y / p.Sq;
+    const int qi = blockIdx.y % p.Sq;
+    const int b = blockIdx.z;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int grp = wave * GPW + lane / LPK;   // key group in workgroup
+    const int sub = lane % LPK;                // 8-dim slice of the row
+
+    const int sk = p.kv_len ? p.kv_len[b] : p.Sk;
+    int limit = sk;
+    if (p.causal) {
+        const int c = sk - p.Sq + qi + 1;
+        limit = c < sk ? c : sk;
+    }
+    const int k_begin = split * chunk;
+    int k_end = k_begin + chunk;
+    if (k_end > limit) k_end = limit;
+
+    // Query slices, pre-scaled so that exp2(q.k) == exp(score).
+    float qv[G][8];
+    const float qs = p.scale * kLog2e;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int h = kvh * G + g;
+        const float *qp = p.q + ((static_cast<long long>(b) * p.Hq + h) * p.Sq + qi) * D + sub * 8;
+        const float4 a = *reinterpret_cast<const float4 *>(qp);
+        const float4 c = *reinterpret_cast<const float4 *>(qp + 4);
+        qv[g][0] = a.x * qs; qv[g][1] = a.y * qs; qv[g][2] = a.z * qs; qv[g][3] = a.w * qs;
+        qv[g][4] = c.x * qs; qv[g][5] = c.y * qs; qv[g][6] = c.z * qs; qv[g][7] = c.w * qs;
+    }
+
+    float m[G], l[G], o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[g][i] = 0.0f;
+    }
+
+    const long long head_base = (static_cast<long long>(b) * p.Hkv + kvh) * p.cap * D + sub * 8;
+    const float *mrow = p.mask ? p.mask + static_cast<long long>(qi) * p.Sk : nullptr;
+
+    for (int t0 = k_begin + grp * kTile; t0 < k_end; t0 += NG * kTile) {
+        float kr[kTile][8], vr[kTile][8];
+        bool valid[kTile];
+#pragma unroll
+        for (int t = 0; t < kTile; ++t) {
+            const int key = t0 + t;
+            valid[t] = key < k_end;
+            const int kk = valid[t] ? key : k_begin;
+            load8<F16>(p.k, head_base + static_cast<long long>(kk) * D, kr[t]);
+            load8<F16>(p.v, head_base + static_cast<long long>(kk) * D, vr[t]);
+        }
+        float add[kTile];
+#pragma unroll
+        for (int t = 0; t < kTile; ++t) {
+            add[t] = 0.0f;
+            if (mrow && valid[t]) add[t] = mrow[t0 + t] * kLog2e;
+            if (!valid[t]) add[t] = -INFINITY;
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float s[kTile];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < kTile; ++t) {
+                float d = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) d = fmaf(qv[g][i], kr[t][i], d);
+                d = group_sum<LPK>(d);
+                s[t] = d + add[t];
+                tmax = fmaxf(tmax, s[t]);
+            }
+            const float mn = fmaxf(m[g], tmax);
+            if (mn == -INFINITY) continue;             // nothing visible yet
+            const float alpha = m[g] == -INFINITY ? 0.0f : exp2f(m[g] - mn);
+            float psum = 0.0f;
+            float pr[kTile];
+#pragma unroll
+            for (int t = 0; t < kTile; ++t) {
+                pr[t] = s[t] == -INFINITY ? 0.0f : exp2f(s[t] - mn);
+                psum += pr[t];
+            }
+            l[g] = fmaf(l[g], alpha, psum);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float acc = o[g][i] * alpha;
+#pragma unroll
+                for (int t = 0; t < kTile; ++t) acc = fmaf(pr[t], vr[t][i], acc);
+                o[g][i] = acc;
+            }
+            m[g] = mn;
+        }
+    }
+
+    // Publish group states: smem[grp][g][0..D) = o, [D] = m, [D+1] = l.
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float *st = smem + (grp * G + g) * (D + 2);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st[sub * 8 + i] = o[g][i];
+        if (sub == 0) {
+            st[D] = m[g];
+            st[D + 1] = l[g];
+        }
+    }
+    __syncthreads();
+
+    // Merge the NG group states; one thread per (head, dim).
+    for (int idx = threadIdx.x; idx < G * D; idx += WAVES * 64) {
+        const int g = idx / D, dd = idx % D;
+        float M = -INFINITY;
+        for (int gr = 0; gr < NG; ++gr) M = fmaxf(M, smem[(gr * G + g) * (D + 2) + D]);
+        float L = 0.0f, O = 0.0f;
+        if (M != -INFINITY) {
+            for (int gr = 0; gr < NG; ++gr) {
+                const float *st = smem + (gr * G + g) * (D + 2);
+                const float mg = st[D];
+                if (mg == -INFINITY) continue;
+                const float w = exp2f(mg - M);
+                L = fmaf(st[D + 1], w, L);
+                O = fmaf(st[dd], w, O);
+            }
+        }
+        const int h = kvh * G + g;
+        const long long row = (static_cast<long long>(b) * p.Hq + h) * p.Sq + qi;
+        if (splits == 1) {
+            p.out[row * D + dd] = L == 0.0f ? 0.0f : O / L;
+        } else {
+            float *pp = part + (row * splits + split) * (D + 2);
+            pp[dd] = O;
+            if (dd == 0) {
+                pp[D] = M;
+                pp[D + 1] = L;
+            }
+        }
+    }
+}
+
+// Merge split partials: one workgroup of D threads per query row.
+template <int D>
+__global__ __launch_bounds__(D) void attn_merge_kernel(float *__restrict__ out, const float *__restrict__ part,
+                                                      int splits) {
+    const long long row = blockIdx.x;
+    const int dd = threadIdx.x;
+    const float *pp = part + row * splits * (D + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < splits; ++s) M = fmaxf(M, pp[s * (D + 2) + D]);
+    float L = 0.0f, O = 0.0f;
+    if (M != -INFINITY) {
+        for (int s = 0; s < splits; ++s) {
+            const float ms = pp[s * (D + 2) + D];
+            if (ms == -INFINITY) continue;
+            const float w = exp2f(ms - M);
+            L = fmaf(pp[s * (D + 2) + D + 1], w, L);
+            O = fmaf(pp[s * (D + 2) + dd], w, O);
+        }
+    }
+    out[row * D + dd] = L == 0.0f ? 0.0f : O / L;
+}
+
+// Any head_dim: one thread per (batch, query head, query row, output dim).
+// Each thread runs computeAttentionGroup's loop for its own dimension,
+// including the double-precision denominator and weighted value.
+template <bool F16>
+__device__ __forceinline__ float kv_at(const void *base, long long i) {
+    if constexpr (F16) return f16_bits_to_f32(static_cast<const uint16_t *>(base)[i]);
+    else return static_cast<const float *>(base)[i];
+}
+
+template <bool F16>
+__global__ __launch_bounds__(64) void attn_generic_kernel(AttnParams p) {
+    const long long tid = static_cast<long long>(blockIdx.x) * 64 + threadIdx.x;
+    const int D = p.D;
+    const long long total = static_cast<long long>(p.B) * p.Hq * p.Sq * D;
+    if (tid >= total) return;
+    const int j = static_cast<int>(tid % D);
+    const long long idx = tid / D;   // query row
+    const int qi = static_cast<int>(idx % p.Sq);
+    const int h = static_cast<int>((idx / p.Sq) % p.Hq);
+    const int b = static_cast<int>(idx / (static_cast<long long>(p.Sq) * p.Hq));
+    const int kvh = h / (p.Hq / p.Hkv);
+    const int sk = p.kv_len ? p.kv_len[b] : p.Sk;
+    int limit = sk;
+    if (p.causal) {
+        const int c = sk - p.Sq + qi + 1;
+        limit = c < sk ? c : sk;
+    }
+    const float *qr = p.q + idx * D;
+    const long long kb = (static_cast<long long>(b) * p.Hkv + kvh) * p.cap * D;
+    float running = -INFINITY;
+    double den = 0.0, weighted = 0.0;
+    for (int ki = 0; ki < limit; ++ki) {
+        const float add = p.mask ? p.mask[static_cast<long long>(qi) * p.Sk + ki] : 0.0f;
+        if (add == -INFINITY) continue;
+        float dot = 0.0f;
+        for (int e = 0; e < D; ++e) dot = fmaf(qr[e], kv_at<F16>(p.k, kb + static_cast<long long>(ki) * D + e), dot);
+        const float score = dot * p.scale + add;
+        float next;
+        double prev_s, cur_s;
+        if (isfinite(score)) {
+            if (score > running) {
+                prev_s = exp(static_cast<double>(running - score));
+                cur_s = 1.0;
+                next = score;
+            } else {
+                prev_s = 1.0;
+                cur_s = exp(static_cast<double>(score - running));
+                next = running;
+            }
+        } else {
+            next = fmaxf(running, score);
+            prev_s = running == -INFINITY ? 0.0 : exp(static_cast<double>(running - next));
+            cur_s = exp(static_cast<double>(score - next));
+        }
+        den = den * prev_s + cur_s;
+        weighted = weighted * prev_s + cur_s * kv_at<F16>(p.v, kb + static_cast<long long>(ki) * D + j);
+        running = next;
+    }
+    p.out[idx * D + j] = den == 0.0 ? 0.0f : static_cast<float>(weighted / den);
+}
+
+__global__ void mask_check_kernel(const float *__restrict__ mask, long long n, int *__restrict__ bad) {
+    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) {
+        const float v = mask[i];
+        if (v != v || v == INFINITY) atomicOr(bad, 1);
+    }
+}
+
+__global__ void zero_i32_kernel(int *p) { *p = 0; }
+
+template <int D, int G, bool F16>
+int launch_split(const AttnParams &p, int splits, int chunk, float *part, hipStream_t s) {
+    constexpr int WAVES = (G <= 4) ? 4 : 2;
+    constexpr int NG = (64 / (D / 8)) * WAVES;
+    const size_t lds = static_cast<size_t>(NG) * G * (D + 2) * sizeof(float);
+    const dim3 grid(splits, p.Hkv * p.Sq, p.B);
+    hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES>), grid, dim3(WAVES * 64), lds, s, p, splits, chunk, part);
+    if (splits > 1) {
+        const unsigned rows = static_cast<unsigned>(static_cast<long long>(p.B) * p.Hq * p.Sq);
+        hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(rows), dim3(D), 0, s, p.out, part, splits);
+    }
+    return ALJABR_ROCM_OK;
+}
+
+template <int D, bool F16>
+int launch_g(const AttnParams &p, int G, int splits, int chunk, float *part, hipStream_t s) {
+    switch (G) {
+    case 1: return launch_split<D, 1, F16>(p, splits, chunk, part, s);
+    case 2: return launch_split<D, 2, F16>(p, splits, chunk, part, s);
+    case 4: return launch_split<D, 4, F16>(p, splits, chunk, part, s);
+    case 8: return launch_split<D, 8, F16>(p, splits, chunk, part, s);
+    default: return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "no split attention kernel for %d query heads per KV head", G);
+    }
+}
+
+}  // namespace
+
+// Enqueue attention (no sync). Chooses the split-K kernels for D in {64,128}
+// with G in {1,2,4,8} and 16-byte aligned rows, the generic kernel otherwise.
+int enqueue_attention(const AttnParams &p) {
+    hipStream_t s = current_stream();
+    const int G = p.Hq / p.Hkv;
+    const bool fast = (p.D == 64 || p.D == 128) && (G == 1 || G == 2 || G == 4 || G == 8) && aligned(p.q, 16) &&
+                      aligned(p.k, 16) && aligned(p.v, 16);
+    if (!fast) {
+        const long long n = static_cast<long long>(p.B) * p.Hq * p.Sq * p.D;
+        const dim3 grid(static_cast<unsigned>((n + 63) / 64));
+        if (p.kv_f16)
+            hipLaunchKernelGGL(attn_generic_kernel<true>, grid, dim3(64), 0, s, p);
+        else
+            hipLaunchKernelGGL(attn_generic_kernel<false>, grid, dim3(64), 0, s, p);
+        return ALJABR_ROCM_OK;
+    }
+    // Enough workgroups to cover the CUs about twice, chunks of >= 64 keys.
+    const long long items = static_cast<long long>(p.B) * p.Hkv * p.Sq;
+    const int keys = p.kv_len ? p.cap : p.Sk;
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    long long want = (2LL * cus + items - 1) / items;
+    const long long max_splits = (keys + 63) / 64;
+    if (want > max_splits) want = max_splits;
+    if (want < 1) want = 1;
+    int splits = static_cast<int>(want);
+    int chunk = (keys + splits - 1) / splits;
+    chunk = (chunk + 15) & ~15;
+    splits = (keys + chunk - 1) / chunk;
+    if (splits < 1) splits = 1;
+    float *part = nullptr;
+    if (splits > 1) {
+        const size_t bytes = static_cast<size_t>(p.B) * p.Hq * p.Sq * splits * (p.D + 2) * sizeof(float);
+        part = static_cast<float *>(stream_scratch(bytes));
+        if (!part) return ALJABR_ROCM_ERR_BUFFER;
+    }
+    if (p.D == 64)
+        return p.kv_f16 ? launch_g<64, true>(p, G, splits, chunk, part, s) : launch_g<64, false>(p, G, splits, chunk, part, s);
+    return p.kv_f16 ? launch_g<128, true>(p, G, splits, chunk, part, s) : launch_g<128, false>(p, G, splits, chunk, part, s);
+}
+
+}  // namespace aljabr
+
+using namespace aljabr;
+
+extern "C" int aljabr_rocm_attention_gqa(void *out, const void *Q, const void *K, const void *V, const void *mask,
+                                         int B, int Hq, int Hkv, int Sq, int Sk, int D, int kvType, float scale,
+                                         int causal) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(out && Q && K && V, "out, Q, K and V must be non-null device pointers");
+    ALJ_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Sq > 0 && Sk > 0 && D > 0 && Hq % Hkv == 0,
+                "GQA expects Q[B,Hq,Sq,D], K/V[B,Hkv,Sk,D] with Hq divisible by Hkv");
+    if (kvType != ALJABR_ROCM_TYPE_F32 && kvType != ALJABR_ROCM_TYPE_F16)
+        return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "attention: K/V type %d is not F32 or F16", kvType);
+    hipStream_t s = current_stream();
+    if (mask) {
+        // CpuBackend.validateAttentionMask: NaN or +inf anywhere is rejected.
+        int *flag = static_cast<int *>(stream_scratch(sizeof(int)));
+        if (!flag) return ALJABR_ROCM_ERR_BUFFER;
+        const long long n = static_cast<long long>(Sq) * Sk;
+        hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(1), 0, s, flag);
+        hipLaunchKernelGGL(mask_check_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                           static_cast<const float *>(mask), n, flag);
+        int bad = 0;
+        hipError_t e = hipMemcpyAsync(&bad, flag, sizeof(int), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "attention mask check: %s", hipGetErrorString(e));
+        if (bad) return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "attention mask values must not be NaN or positive infinity");
+    }
+    AttnParams p{};
+    p.out = static_cast<float *>(out);
+    p.q = static_cast<const float *>(Q);
+    p.k = K;
+    p.v = V;
+    p.mask = static_cast<const float *>(mask);
+    p.kv_len = nullptr;
+    p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Sq = Sq; p.Sk = Sk; p.D = D; p.cap = Sk;
+    p.scale = scale > 0.0f ? scale : static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));
+    p.causal = causal != 0;
+    p.kv_f16 = kvType == ALJABR_ROCM_TYPE_F16;
+    int rc = enqueue_attention(p);
+    if (rc) return rc;
+    return finish_launch("attention_gqa");
+}

@@ -1,0 +1,128 @@
+// device.hpp - gfx950 device helpers: wave64 DPP reductions, exact format
+// conversions and the NF4 codebook.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace aljabr {
+
+constexpr int kWave = 64;
+
+// DPP-modified move: lanes outside row_mask keep `old` (0 here).
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, false));
+}
+
+// Sum within each 16-lane DPP row; every lane of the row receives the row sum.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);  // row_half_mirror
+    v += dpp_f32<0x140>(v);  // row_mirror
+    return v;
+}
+
+// Max within each 16-lane DPP row (identity -inf is never produced: every
+// lane of a row is a source for the mirrors used here).
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0xB1, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x4E, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x141, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x140, 0xf, 0xf, false)));
+    return v;
+}
+
+// Full wave64 sum, returned uniformly (read from lane 63).
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    v += dpp_f32<0x142, 0xA>(v);  // row_bcast:15 -> rows 1 and 3
+    v += dpp_f32<0x143, 0xC>(v);  // row_bcast:31 -> rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = row16_max(v);
+    float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// ({hi,lo} >> shift)[31:0], shift in [0,31] (v_alignbit_b32).
+__device__ __forceinline__ uint32_t funnel_shift_right(uint32_t hi, uint32_t lo, uint32_t shift) {
+    return __builtin_amdgcn_alignbit(hi, lo, shift);
+}
+
+// binary16 -> binary32 exactly as GgufQuantTables.f16ToF32Slow: integer-only,
+// so the result does not depend on the FP16 denormal mode; NaN -> 0x7FC00000.
+__device__ __forceinline__ float f16_bits_to_f32_exact(uint32_t h) {
+    uint32_t sign = (h >> 15) & 1u, exponent = (h >> 10) & 0x1fu, mantissa = h & 0x3ffu;
+    uint32_t bits;
+    if (exponent == 0) {
+        if (mantissa == 0) {
+            bits = sign << 31;
+        } else {
+            // value = mantissa * 2^-24: normalise the 10-bit mantissa.
+            int lz = __builtin_clz(mantissa) - 21;          // shifts to bring the top bit to bit 10
+            uint32_t m = (mantissa << lz) & 0x3ffu;
+            uint32_t e = 113u - (uint32_t)lz;                // 127 - 14 - lz
+            bits = (sign << 31) | (e << 23) | (m << 13);
+        }
+    } else if (exponent == 31) {
+        bits = mantissa == 0 ? ((sign << 31) | 0x7f800000u) : 0x7fc00000u;
+    } else {
+        bits = (sign << 31) | ((exponent + 112u) << 23) | (mantissa << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+// Hardware binary16 -> binary32 (used in hot loops; scales are normal numbers).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
+}
+
+// GGUFWriter.floatToHalfBits: truncate to 10 mantissa bits, add one ulp when
+// the first dropped bit is set; overflow -> inf/0x7C01; tiny -> signed zero.
+__device__ __forceinline__ uint32_t f32_to_f16_writer(float v) {
+    uint32_t bits = __float_as_uint(v);
+    uint32_t sign = (bits >> 16) & 0x8000u;
+    int exponent = (int)((bits >> 23) & 0xffu) - 127 + 15;
+    uint32_t mantissa = bits & 0x7fffffu;
+    if (exponent >= 31) return sign | 0x7c00u | (mantissa == 0 ? 0u : 1u);
+    if (exponent <= 0) {
+        if (exponent < -10) return sign;
+        uint32_t full = mantissa | 0x800000u;
+        int shift = 14 - exponent;
+        uint32_t hm = full >> shift;
+        if ((full >> (shift - 1)) & 1u) hm += 1;
+        return sign | hm;
+    }
+    uint32_t half = sign | ((uint32_t)exponent << 10) | (mantissa >> 13);
+    if (mantissa & 0x1000u) half += 1;
+    return half;
+}
+
+// java.lang.Math.round(float): floor(v + 1/2) exactly (done in double), NaN -> 0.
+__device__ __forceinline__ int java_round(float v) {
+    if (v != v) return 0;
+    double r = floor((double)v + 0.5);
+    if (r >= 2147483647.0) return 2147483647;
+    if (r <= -2147483648.0) return (int)(-2147483647 - 1);
+    return (int)r;
+}
+
+// NormalFloat-4 codebook, STC/DequantizationKernel.java:23-28 (16 fp32 levels).
+__device__ __forceinline__ float nf4_level(int c) {
+    constexpr float t[16] = {
+        -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+        -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+        0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+        0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+    return t[c];
+}
+
+}  // namespace aljabr

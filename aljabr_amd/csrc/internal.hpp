@@ -1,0 +1,54 @@
+// internal.hpp - host-side plumbing shared by the C-ABI entry points.
+//
+// Status codes, the thread-local error message, the calling thread's stream and
+// the per-stream scratch arena. Kernels live in the *.hip files that include
+// this header; no entry point allocates torch memory or calls back into Python.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/aljabr_rocm.h"
+
+namespace aljabr {
+
+// Records `msg` as this thread's last error and returns `status`.
+int fail(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// ALJABR_ROCM_OK when the library is initialised and the calling thread is
+// bound to the library device; otherwise the failing status (message set).
+int ensure_ready();
+
+// The calling thread's stream (set_stream override or library-owned stream).
+hipStream_t current_stream();
+
+// After enqueuing work: checks the launch, and in synchronous mode waits for
+// the stream and reports asynchronous device errors.
+int finish_launch(const char *what);
+
+// Device scratch owned by the library for the calling thread's stream; grows
+// monotonically. Stream order makes reuse by later calls on the same stream
+// safe. Returns nullptr (and records an error) on allocation failure.
+void *stream_scratch(size_t bytes);
+
+// Number of compute units of the initialised device (for grid sizing).
+int device_cu_count();
+
+inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace aljabr
+
+#define ALJ_CHECK_READY()                          \
+    do {                                           \
+        int _rc = ::aljabr::ensure_ready();        \
+        if (_rc != ALJABR_ROCM_OK) return _rc;     \
+    } while (0)
+
+#define ALJ_REQUIRE(cond, ...)                                              \
+    do {                                                                    \
+        if (!(cond)) return ::aljabr::fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, __VA_ARGS__); \
+    } while (0)

@@ -1,0 +1,506 @@
+// matvec.hip - batch-1 and small-M (M <= 8) dequant-fused matvec for NF4,
+// GGUF Q4_0, GGUF Q8_0 and fp16 rows on gfx950.
+//
+// Shape: C[m][n] = sum_k A[m][k] * W[n][k], W [N,K] row-major (the
+// "transposed right" convention of MTLJ/MetalComputeBackend.java:435-470).
+//
+// Mapping. One wave64 owns R consecutive rows. The K axis is walked in wave
+// chunks: every lane takes one 16-byte slice of packed weights per row per
+// chunk (NF4: 32 codes; Q4_0 and Q8_0: one GGUF block), so a chunk is one fully
+// coalesced 1 KiB (NF4) / 64-block span per row. Each lane dequantizes in
+// registers (NF4 through a 16-entry LDS codebook, conflict-free because at most
+// 16 distinct words are read; GGUF codes through v_cvt_f32_ubyte), multiplies
+// by the fp32 activations it loaded for its slice (reused across the R rows),
+// and keeps per-row partials. One DPP wave reduction per row ends the kernel.
+// All arithmetic is fp32 (no packed-fp32 instructions: the build disables them).
+#include "device.hpp"
+#include "internal.hpp"
+#include "kernels.hpp"
+
+namespace aljabr {
+namespace {
+
+constexpr int kThreads = 256;   // 4 waves per workgroup
+
+// ---------------------------------------------------------------------------
+// NF4: codes u8 [N*K/2] (even element in the high nibble), absmax fp32 over
+// the flat element index / blockSize (STC/DequantizationKernel.java:84-102).
+// Fast path: K % 32 == 0, blockSize a power of two >= 32.
+// ---------------------------------------------------------------------------
+template <int M, int R>
+__global__ __launch_bounds__(kThreads) void nf4_matvec_kernel(float *__restrict__ y, const float *__restrict__ x,
+                                                              const uint8_t *__restrict__ codes,
+                                                              const float *__restrict__ absmax, int N, int K,
+                                                              int bs_shift) {
+    __shared__ float lut[16];
+    if (threadIdx.x < 16) lut[threadIdx.x] = nf4_level(threadIdx.x);
+    __syncthreads();
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row0 = ((blockIdx.x * kThreads + threadIdx.x) / kWave) * R;
+    if (row0 >= N) return;
+    const size_t row_bytes = static_cast<size_t>(K) >> 1;
+    const char *lut_bytes = reinterpret_cast<const char *>(lut);
+
+    float acc[M][R];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+    for (int k0 = lane * 32; k0 < K; k0 += kWave * 32) {
+        uint4 c[R];
+        float s[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = min(row0 + r, N - 1);
+            c[r] = *reinterpret_cast<const uint4 *>(codes + row * row_bytes + (k0 >> 1));
+            s[r] = absmax[(static_cast<size_t>(row) * K + k0) >> bs_shift];
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float xv[32];
+            const float4 *xp = reinterpret_cast<const float4 *>(x + static_cast<size_t>(m) * K + k0);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float4 t = xp[i];
+                xv[4 * i + 0] = t.x;
+                xv[4 * i + 1] = t.y;
+                xv[4 * i + 2] = t.z;
+                xv[4 * i + 3] = t.w;
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t w[4] = {c[r].x, c[r].y, c[r].z, c[r].w};
+                float p = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // Byte addresses into the 16-float codebook: nibble * 4.
+                    const uint32_t hi4 = (w[i] >> 2) & 0x3C3C3C3Cu;
+                    const uint32_t lo4 = (w[i] << 2) & 0x3C3C3C3Cu;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const float vh = *reinterpret_cast<const float *>(lut_bytes + ((hi4 >> (8 * t)) & 0xffu));
+                        const float vl = *reinterpret_cast<const float *>(lut_bytes + ((lo4 >> (8 * t)) & 0xffu));
+                        p = fmaf(vh, xv[8 * i + 2 * t], p);
+                        p = fmaf(vl, xv[8 * i + 2 * t + 1], p);
+                    }
+                }
+                acc[m][r] = fmaf(p, s[r], acc[m][r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = wave_sum(acc[m][r]);
+            if (lane == 0 && row0 + r < N) y[static_cast<size_t>(m) * N + row0 + r] = v;
+        }
+}
+
+// Any K / even blockSize: one wave per (row, token), lanes stride over bytes.
+__global__ __launch_bounds__(kThreads) void nf4_matvec_generic_kernel(float *__restrict__ y,
+                                                                      const float *__restrict__ x,
+                                                                      const uint8_t *__restrict__ codes,
+                                                                      const float *__restrict__ absmax, int N,
+                                                                      int K, int M, int bs) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int task = (blockIdx.x * kThreads + threadIdx.x) / kWave;
+    if (task >= N * M) return;
+    const int n = task % N, m = task / N;
+    const size_t base = static_cast<size_t>(n) * K;
+    const float *xr = x + static_cast<size_t>(m) * K;
+    float acc = 0.0f;
+    for (int k = lane; k < K; k += kWave) {
+        const size_t e = base + k;
+        const uint8_t b = codes[e >> 1];
+        const int code = (e & 1) ? (b & 15) : (b >> 4);
+        acc = fmaf(nf4_level(code) * absmax[e / bs], xr[k], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[static_cast<size_t>(m) * N + n] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// GGUF block loads. A Q4_0 block is 18 bytes ({f16 d; u8 qs[16]}), a Q8_0 block
+// 34 bytes; both start at even addresses, so their code bytes start either on
+// a dword boundary or 2 bytes past one. Each lane reads the dwords that cover
+// its codes and realigns them with v_alignbit_b32; the last two code bytes
+// are fetched with a 16-bit load when the block is misaligned, so no read ever
+// passes the end of the block.
+// ---------------------------------------------------------------------------
+template <int NDW>
+__device__ __forceinline__ void load_gguf_codes(const uint8_t *blk, uint32_t (&q)[NDW], float &d) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(blk + 2);
+    const uint32_t off = static_cast<uint32_t>(a & 3u);   // 0 or 2
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(a - off);
+    uint32_t dw[NDW + 1];
+#pragma unroll
+    for (int i = 0; i < NDW; ++i) dw[i] = p[i];
+    uint32_t dbits;
+    if (off) {
+        dw[NDW] = *reinterpret_cast<const uint16_t *>(blk + 2 + 4 * NDW - 2);
+        dbits = dw[0] & 0xffffu;
+    } else {
+        dw[NDW] = 0;
+        dbits = *reinterpret_cast<const uint16_t *>(blk);
+    }
+    const uint32_t sh = off * 8u;
+#pragma unroll
+    for (int i = 0; i < NDW; ++i) q[i] = funnel_shift_right(dw[i + 1], dw[i], sh);
+    d = f16_bits_to_f32(dbits);
+}
+
+// Q4_0: byte j low nibble -> element j, high nibble -> element 16+j
+// (GRT/GgufBlockDequantizer.java:403-416). sum (q-8) x = sum q x - 8 sum x.
+template <int M, int R>
+__global__ __launch_bounds__(kThreads) void q4_0_matvec_kernel(float *__restrict__ y, const float *__restrict__ x,
+                                                               const uint8_t *__restrict__ w, int N, int K) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row0 = ((blockIdx.x * kThreads + threadIdx.x) / kWave) * R;
+    if (row0 >= N) return;
+    const int nblk = K >> 5;
+    const size_t row_bytes = static_cast<size_t>(nblk) * 18;
+    float acc[M][R];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+    for (int b = lane; b < nblk; b += kWave) {
+        uint32_t q[R][4];
+        float d[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = min(row0 + r, N - 1);
+            load_gguf_codes<4>(w + row * row_bytes + static_cast<size_t>(b) * 18, q[r], d[r]);
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float xv[32];
+            const float4 *xp = reinterpret_cast<const float4 *>(x + static_cast<size_t>(m) * K + b * 32);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float4 t = xp[i];
+                xv[4 * i + 0] = t.x;
+                xv[4 * i + 1] = t.y;
+                xv[4 * i + 2] = t.z;
+                xv[4 * i + 3] = t.w;
+            }
+            float xs = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) xs += xv[i];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float p = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t lo = q[r][i] & 0x0F0F0F0Fu;
+                    const uint32_t hi = (q[r][i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        p = fmaf(static_cast<float>((lo >> (8 * t)) & 0xffu), xv[4 * i + t], p);
+                        p = fmaf(static_cast<float>((hi >> (8 * t)) & 0xffu), xv[16 + 4 * i + t], p);
+                    }
+                }
+                acc[m][r] = fmaf(d[r], fmaf(-8.0f, xs, p), acc[m][r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = wave_sum(acc[m][r]);
+            if (lane == 0 && row0 + r < N) y[static_cast<size_t>(m) * N + row0 + r] = v;
+        }
+}
+
+// Q8_0: int8 codes (GRT/GgufBlockDequantizer.java:231-265). Bytes are biased
+// to unsigned (xor 0x80) so each converts with one v_cvt_f32_ubyte:
+// sum q x = sum (q+128) x - 128 sum x.
+template <int M, int R>
+__global__ __launch_bounds__(kThreads) void q8_0_matvec_kernel(float *__restrict__ y, const float *__restrict__ x,
+                                                               const uint8_t *__restrict__ w, int N, int K) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row0 = ((blockIdx.x * kThreads + threadIdx.x) / kWave) * R;
+    if (row0 >= N) return;
+    const int nblk = K >> 5;
+    const size_t row_bytes = static_cast<size_t>(nblk) * 34;
+    float acc[M][R];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+    for (int b = lane; b < nblk; b += kWave) {
+        uint32_t q[R][8];
+        float d[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = min(row0 + r, N - 1);
+            load_gguf_codes<8>(w + row * row_bytes + static_cast<size_t>(b) * 34, q[r], d[r]);
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float xv[32];
+            const float4 *xp = reinterpret_cast<const float4 *>(x + static_cast<size_t>(m) * K + b * 32);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float4 t = xp[i];
+                xv[4 * i + 0] = t.x;
+                xv[4 * i + 1] = t.y;
+                xv[4 * i + 2] = t.z;
+                xv[4 * i + 3] = t.w;
+            }
+            float xs = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) xs += xv[i];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float p = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t u = q[r][i] ^ 0x80808080u;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        p = fmaf(static_cast<float>((u >> (8 * t)) & 0xffu), xv[4 * i + t], p);
+                }
+                acc[m][r] = fmaf(d[r], fmaf(-128.0f, xs, p), acc[m][r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = wave_sum(acc[m][r]);
+            if (lane == 0 && row0 + r < N) y[static_cast<size_t>(m) * N + row0 + r] = v;
+        }
+}
+
+// fp16 rows (LM head, GRT/GgufDenseRows.java:70-90): 8 halves per lane per chunk.
+template <int M, int R>
+__global__ __launch_bounds__(kThreads) void f16_matvec_kernel(float *__restrict__ y, const float *__restrict__ x,
+                                                              const uint16_t *__restrict__ w, int N, int K) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row0 = ((blockIdx.x * kThreads + threadIdx.x) / kWave) * R;
+    if (row0 >= N) return;
+    float acc[M][R];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+    for (int k0 = lane * 8; k0 < K; k0 += kWave * 8) {
+        uint4 c[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = min(row0 + r, N - 1);
+            c[r] = *reinterpret_cast<const uint4 *>(w + static_cast<size_t>(row) * K + k0);
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float4 *xp = reinterpret_cast<const float4 *>(x + static_cast<size_t>(m) * K + k0);
+            const float4 xa = xp[0], xb = xp[1];
+            const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t h[4] = {c[r].x, c[r].y, c[r].z, c[r].w};
+                float p = acc[m][r];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    p = fmaf(f16_bits_to_f32(h[i] & 0xffffu), xv[2 * i], p);
+                    p = fmaf(f16_bits_to_f32(h[i] >> 16), xv[2 * i + 1], p);
+                }
+                acc[m][r] = p;
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = wave_sum(acc[m][r]);
+            if (lane == 0 && row0 + r < N) y[static_cast<size_t>(m) * N + row0 + r] = v;
+        }
+}
+
+// fp16 rows with K % 8 != 0 or misaligned rows.
+__global__ __launch_bounds__(kThreads) void f16_matvec_generic_kernel(float *__restrict__ y,
+                                                                      const float *__restrict__ x,
+                                                                      const uint16_t *__restrict__ w, int N, int K,
+                                                                      int M) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int task = (blockIdx.x * kThreads + threadIdx.x) / kWave;
+    if (task >= N * M) return;
+    const int n = task % N, m = task / N;
+    float acc = 0.0f;
+    for (int k = lane; k < K; k += kWave)
+        acc = fmaf(f16_bits_to_f32(w[static_cast<size_t>(n) * K + k]), x[static_cast<size_t>(m) * K + k], acc);
+    acc = wave_sum(acc);
+    if (lane == 0) y[static_cast<size_t>(m) * N + n] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// launch helpers
+// ---------------------------------------------------------------------------
+inline unsigned grid_for(int waves) { return static_cast<unsigned>((waves + 3) / 4); }
+
+// Rows per wave: enough waves to cover every CU several times.
+inline int pick_rows(int N) { return N >= 8192 ? 2 : 1; }
+
+template <template <int, int> class>
+struct Tag {};
+
+#define ALJ_DISPATCH_MR(KERNEL, M, R, GRID, ...)                                             \
+    do {                                                                                     \
+        switch ((M) * 8 + (R)) {                                                             \
+        case 1 * 8 + 1: hipLaunchKernelGGL((KERNEL<1, 1>), GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+        case 1 * 8 + 2: hipLaunchKernelGGL((KERNEL<1, 2>), GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+        case 1 * 8 + 4: hipLaunchKernelGGL((KERNEL<1, 4>), GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+        case 2 * 8 + 1: hipLaunchKernelGGL((KERNEL<2, 1>), GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+        case 3 * 8 + 1: hipLaunchKernelGGL((KERNEL<3, 1>), GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+        case 4 * 8 + 1: hipLaunchKernelGGL((KERNEL<4, 1>), GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+        case 5 * 8 + 1: hipLaunchKernelGGL((KERNEL<5, 1>), GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+        case 6 * 8 + 1: hipLaunchKernelGGL((KERNEL<6, 1>), GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+        case 7 * 8 + 1: hipLaunchKernelGGL((KERNEL<7, 1>), GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+        case 8 * 8 + 1: hipLaunchKernelGGL((KERNEL<8, 1>), GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+        default: return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "no %s kernel for M=%d R=%d", #KERNEL, (M), (R)); \
+        }                                                                                    \
+    } while (0)
+
+int log2_exact(int v) {
+    if (v <= 0 || (v & (v - 1))) return -1;
+    int s = 0;
+    while ((1 << s) < v) ++s;
+    return s;
+}
+
+}  // namespace
+
+// Enqueue C[M][N] for M <= 8 (no sync); used by the entry points and the
+// decode driver. Returns a status.
+int enqueue_nf4_small(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs,
+                      int M) {
+    hipStream_t s = current_stream();
+    const int shift = log2_exact(bs);
+    const bool fast = (K % 32 == 0) && shift >= 5 && aligned(Bq, 16) && aligned(A, 16);
+    if (!fast) {
+        hipLaunchKernelGGL(nf4_matvec_generic_kernel, dim3(grid_for(N * M)), dim3(kThreads), 0, s, C, A, Bq, absmax,
+                           N, K, M, bs);
+        return ALJABR_ROCM_OK;
+    }
+    const int R = M == 1 ? pick_rows(N) : 1;
+    const dim3 grid(grid_for((N + R - 1) / R));
+    ALJ_DISPATCH_MR(nf4_matvec_kernel, M, R, grid, C, A, Bq, absmax, N, K, shift);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_gguf_small(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M) {
+    hipStream_t s = current_stream();
+    if (type != ALJABR_ROCM_TYPE_F16 && (!aligned(A, 16) || !aligned(B, 4)))
+        return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "GGUF matvec needs A 16-byte and B 4-byte aligned");
+    const int R = M == 1 ? pick_rows(N) : 1;
+    const dim3 grid(grid_for((N + R - 1) / R));
+    if (type == ALJABR_ROCM_TYPE_Q4_0) {
+        ALJ_DISPATCH_MR(q4_0_matvec_kernel, M, R, grid, C, A, B, N, K);
+    } else if (type == ALJABR_ROCM_TYPE_Q8_0) {
+        ALJ_DISPATCH_MR(q8_0_matvec_kernel, M, R, grid, C, A, B, N, K);
+    } else {
+        const uint16_t *W = reinterpret_cast<const uint16_t *>(B);
+        if (K % 8 == 0 && aligned(B, 16)) {
+            ALJ_DISPATCH_MR(f16_matvec_kernel, M, R, grid, C, A, W, N, K);
+        } else {
+            hipLaunchKernelGGL(f16_matvec_generic_kernel, dim3(grid_for(N * M)), dim3(kThreads), 0, s, C, A, W, N, K,
+                               M);
+        }
+    }
+    return ALJABR_ROCM_OK;
+}
+
+}  // namespace aljabr
+
+using namespace aljabr;
+
+namespace aljabr {
+
+// M > 8 slices run the small-M kernels per slice of 8 tokens (weights are
+// re-read per slice); the MFMA path takes over at its threshold.
+int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M) {
+    for (int m0 = 0; m0 < M; m0 += 8) {
+        const int mm = M - m0 < 8 ? M - m0 : 8;
+        int rc = enqueue_nf4_small(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, Bq, absmax, K, N,
+                                   bs, mm);
+        if (rc != ALJABR_ROCM_OK) return rc;
+    }
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M) {
+    for (int m0 = 0; m0 < M; m0 += 8) {
+        const int mm = M - m0 < 8 ? M - m0 : 8;
+        int rc = enqueue_gguf_small(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, B, K, N, type,
+                                    mm);
+        if (rc != ALJABR_ROCM_OK) return rc;
+    }
+    return ALJABR_ROCM_OK;
+}
+
+}  // namespace aljabr
+
+namespace {
+
+int check_common(const void *C, const void *A, const void *B, int K, int N, int batch) {
+    ALJ_REQUIRE(C && A && B, "C, A and B must be non-null device pointers");
+    ALJ_REQUIRE(K > 0 && N > 0 && batch > 0, "bad dimensions K=%d N=%d batch=%d", K, N, batch);
+    return ALJABR_ROCM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aljabr_rocm_matvec_tb_batch_nf4(void *C, const void *A, const void *B_packed, const void *absmax, int K, int N,
+                                    int blockSize, int batchSize) {
+    ALJ_CHECK_READY();
+    int rc = check_common(C, A, B_packed, K, N, batchSize);
+    if (rc) return rc;
+    ALJ_REQUIRE(absmax, "absmax must be a non-null device pointer");
+    ALJ_REQUIRE(blockSize > 0 && blockSize % 2 == 0, "NF4 blockSize must be positive and even (got %d)", blockSize);
+    rc = enqueue_matmul_nf4(static_cast<float *>(C), static_cast<const float *>(A), static_cast<const uint8_t *>(B_packed),
+                 static_cast<const float *>(absmax), K, N, blockSize, batchSize);
+    if (rc) return rc;
+    return finish_launch("matvec_tb_batch_nf4");
+}
+
+int aljabr_rocm_matvec_tb_nf4(void *C, const void *A, const void *B_packed, const void *absmax, int K, int N,
+                              int blockSize) {
+    return aljabr_rocm_matvec_tb_batch_nf4(C, A, B_packed, absmax, K, N, blockSize, 1);
+}
+
+int aljabr_rocm_matvec_tb_batch(void *C, const void *A, const void *B, int K, int N, int type, int batchSize) {
+    ALJ_CHECK_READY();
+    int rc = check_common(C, A, B, K, N, batchSize);
+    if (rc) return rc;
+    if (type != ALJABR_ROCM_TYPE_Q4_0 && type != ALJABR_ROCM_TYPE_Q8_0 && type != ALJABR_ROCM_TYPE_F16)
+        return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "matvec_tb_batch: unsupported type %d", type);
+    if (type != ALJABR_ROCM_TYPE_F16) ALJ_REQUIRE(K % 32 == 0, "GGUF rows are whole 32-element blocks (K=%d)", K);
+    rc = enqueue_matmul_gguf(static_cast<float *>(C), static_cast<const float *>(A), static_cast<const uint8_t *>(B), K, N, type,
+                  batchSize);
+    if (rc) return rc;
+    return finish_launch("matvec_tb_batch");
+}
+
+int aljabr_rocm_matvec_tb_q4_0(void *C, const void *A, const void *B, int K, int N) {
+    return aljabr_rocm_matvec_tb_batch(C, A, B, K, N, ALJABR_ROCM_TYPE_Q4_0, 1);
+}
+
+int aljabr_rocm_matvec_tb_q8_0(void *C, const void *A, const void *B, int K, int N) {
+    return aljabr_rocm_matvec_tb_batch(C, A, B, K, N, ALJABR_ROCM_TYPE_Q8_0, 1);
+}
+
+int aljabr_rocm_matvec_tb_half(void *C, const void *A, const void *B, int K, int N) {
+    return aljabr_rocm_matvec_tb_batch(C, A, B, K, N, ALJABR_ROCM_TYPE_F16, 1);
+}
+
+}  // extern "C"

@@ -1,0 +1,235 @@
+// ops.hip - decode-step element-wise kernels (fp32): RMSNorm, split-half RoPE,
+// SwiGLU, residual add, argmax, token-embedding gather and fp16 KV append.
+//
+// Arithmetic follows GLD/tensor/GGUFVectorOps.java (engine/gguf/aljabr-gguf-core/
+// src/main/java/tech/kayys/aljabr/gguf/loader/tensor): rmsNorm :211-234,
+// swiGLU :333-338, rope :383-440, addInPlace :108-116. Transcendentals that
+// the reference evaluates in double (Math.sqrt/exp/pow/cos/sin) are evaluated
+// in double here too.
+#include <cmath>
+
+#include "device.hpp"
+#include "internal.hpp"
+#include "kernels.hpp"
+
+namespace aljabr {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < static_cast<int>(blockDim.x >> 6); ++i) t += red[i];
+    __syncthreads();
+    return t;
+}
+
+// One workgroup per row.
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ x,
+                                                           const float *__restrict__ w, int len, float eps) {
+    __shared__ float red[kThreads / 64];
+    const float *xr = x + static_cast<long long>(blockIdx.x) * len;
+    float *orow = out + static_cast<long long>(blockIdx.x) * len;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < len; i += kThreads) ss = fmaf(xr[i], xr[i], ss);
+    ss = block_sum(ss, red);
+    const float scale = 1.0f / static_cast<float>(sqrt(static_cast<double>(ss / static_cast<float>(len) + eps)));
+    for (int i = threadIdx.x; i < len; i += kThreads) orow[i] = (xr[i] * scale) * w[i];
+}
+
+// One thread per (row, head, pair i < half).
+__global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ x, const int *__restrict__ pos, int rows,
+                                                        int n_heads, int head_dim, float base) {
+    const int half = head_dim / 2;
+    const long long t = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+    const long long total = static_cast<long long>(rows) * n_heads * half;
+    if (t >= total) return;
+    const int i = static_cast<int>(t % half);
+    const long long rh = t / half;   // row * n_heads + head
+    const int row = static_cast<int>(rh / n_heads);
+    const float exponent = -2.0f * static_cast<float>(i) / static_cast<float>(head_dim);
+    const float inv_freq = static_cast<float>(pow(static_cast<double>(base), static_cast<double>(exponent)));
+    const float theta = static_cast<float>(pos[row]) * inv_freq;
+    const float c = static_cast<float>(cos(static_cast<double>(theta)));
+    const float s = static_cast<float>(sin(static_cast<double>(theta)));
+    float *p = x + rh * head_dim;
+    const float x0 = p[i], x1 = p[i + half];
+    p[i] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
+    p[i + half] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+}
+
+__global__ __launch_bounds__(kThreads) void swiglu_kernel(float *__restrict__ dst, const float *__restrict__ gate,
+                                                          const float *__restrict__ up, long long n) {
+    const long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const float g = gate[i];
+    const float sg = g / (1.0f + static_cast<float>(exp(-static_cast<double>(g))));
+    dst[i] = sg * up[i];
+}
+
+__global__ __launch_bounds__(kThreads) void add_kernel(float *__restrict__ a, const float *__restrict__ b, long long n) {
+    const long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i < n) a[i] += b[i];
+}
+
+// One 1024-thread workgroup per row; ties resolve to the lowest index.
+__global__ __launch_bounds__(1024) void argmax_kernel(int *__restrict__ out, const float *__restrict__ x, int cols) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const float *row = x + static_cast<long long>(blockIdx.x) * cols;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < cols; i += 1024) {
+        const float v = row[i];
+        if (v > best || (v == best && i < bi)) {
+            best = v;
+            bi = i;
+        }
+    }
+    // Wave reduction with index tie-break.
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov > best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[w] = best;
+        si[w] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 16; ++k)
+            if (sv[k] > best || (sv[k] == best && si[k] < bi)) {
+                best = sv[k];
+                bi = si[k];
+            }
+        out[blockIdx.x] = bi == 0x7fffffff ? 0 : bi;
+    }
+}
+
+// x[b][:] = embed[tokens[b]][:]
+__global__ __launch_bounds__(kThreads) void embed_kernel(float *__restrict__ x, const float *__restrict__ embed,
+                                                         const int *__restrict__ tokens, int dim, int vocab) {
+    const int b = blockIdx.y;
+    int t = tokens[b];
+    t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i < dim; i += gridDim.x * kThreads)
+        x[static_cast<long long>(b) * dim + i] = embed[static_cast<long long>(t) * dim + i];
+}
+
+// cache[b][h][pos[b]][d] = fp16(src[b][h*D + d]) (round to nearest even).
+__global__ __launch_bounds__(kThreads) void kv_append_kernel(uint16_t *__restrict__ cache, const float *__restrict__ src,
+                                                             const int *__restrict__ pos, int n_kv, int head_dim,
+                                                             int cap) {
+    const int b = blockIdx.y;
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n_kv * head_dim) return;
+    const int h = i / head_dim, d = i % head_dim;
+    const _Float16 v = static_cast<_Float16>(src[static_cast<long long>(b) * n_kv * head_dim + i]);
+    cache[((static_cast<long long>(b) * n_kv + h) * cap + pos[b]) * head_dim + d] = __builtin_bit_cast(uint16_t, v);
+}
+
+inline unsigned blocks_for(long long n) { return static_cast<unsigned>((n + kThreads - 1) / kThreads); }
+
+}  // namespace
+
+int enqueue_rmsnorm(float *out, const float *x, const float *w, int rows, int len, float eps) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, current_stream(), out, x, w, len, eps);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_rope(float *x, const int *pos, int rows, int n_heads, int head_dim, float base) {
+    const long long total = static_cast<long long>(rows) * n_heads * (head_dim / 2);
+    hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(total)), dim3(kThreads), 0, current_stream(), x, pos, rows, n_heads,
+                       head_dim, base);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_swiglu(float *dst, const float *gate, const float *up, long long n) {
+    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, current_stream(), dst, gate, up, n);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_add(float *a, const float *b, long long n) {
+    hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, current_stream(), a, b, n);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_argmax(int *out, const float *x, int rows, int cols) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(1024), 0, current_stream(), out, x, cols);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_embed(float *x, const float *embed, const int *tokens, int batch, int dim, int vocab) {
+    const unsigned gx = static_cast<unsigned>((dim + kThreads - 1) / kThreads);
+    hipLaunchKernelGGL(embed_kernel, dim3(gx, batch), dim3(kThreads), 0, current_stream(), x, embed, tokens, dim, vocab);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_kv_append(uint16_t *cache, const float *src, const int *pos, int batch, int n_kv, int head_dim, int cap) {
+    const unsigned gx = static_cast<unsigned>((n_kv * head_dim + kThreads - 1) / kThreads);
+    hipLaunchKernelGGL(kv_append_kernel, dim3(gx, batch), dim3(kThreads), 0, current_stream(), cache, src, pos, n_kv,
+                       head_dim, cap);
+    return ALJABR_ROCM_OK;
+}
+
+}  // namespace aljabr
+
+using namespace aljabr;
+
+extern "C" {
+
+int aljabr_rocm_rmsnorm(void *out, const void *x, const void *w, int rows, int len, float eps) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(out && x && w, "out, x and w must be non-null device pointers");
+    ALJ_REQUIRE(rows > 0 && len > 0, "bad dimensions rows=%d len=%d", rows, len);
+    ALJ_REQUIRE(eps >= 0.0f, "eps must be non-negative");
+    enqueue_rmsnorm(static_cast<float *>(out), static_cast<const float *>(x), static_cast<const float *>(w), rows, len,
+                    eps);
+    return finish_launch("rmsnorm");
+}
+
+int aljabr_rocm_rope(void *x, const void *positions, int rows, int nHeads, int headDim, float base) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(x && positions, "x and positions must be non-null device pointers");
+    ALJ_REQUIRE(rows > 0 && nHeads > 0 && headDim >= 2 && headDim % 2 == 0, "invalid RoPE dimensions");
+    ALJ_REQUIRE(std::isfinite(base) && base > 1.0f, "RoPE frequency base must be finite and greater than one");
+    enqueue_rope(static_cast<float *>(x), static_cast<const int *>(positions), rows, nHeads, headDim, base);
+    return finish_launch("rope");
+}
+
+int aljabr_rocm_swiglu(void *dst, const void *gate, const void *up, long long n) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(dst && gate && up, "dst, gate and up must be non-null device pointers");
+    ALJ_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return ALJABR_ROCM_OK;
+    enqueue_swiglu(static_cast<float *>(dst), static_cast<const float *>(gate), static_cast<const float *>(up), n);
+    return finish_launch("swiglu");
+}
+
+int aljabr_rocm_add_inplace(void *a, const void *b, long long n) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(a && b, "a and b must be non-null device pointers");
+    ALJ_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return ALJABR_ROCM_OK;
+    enqueue_add(static_cast<float *>(a), static_cast<const float *>(b), n);
+    return finish_launch("add_inplace");
+}
+
+int aljabr_rocm_argmax(void *out_i32, const void *x, int rows, int cols) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(out_i32 && x, "out and x must be non-null device pointers");
+    ALJ_REQUIRE(rows > 0 && cols > 0, "bad dimensions rows=%d cols=%d", rows, cols);
+    enqueue_argmax(static_cast<int *>(out_i32), static_cast<const float *>(x), rows, cols);
+    return finish_launch("argmax");
+}
+
+}  // extern "C"

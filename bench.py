@@ -1,0 +1,241 @@
+"""Headline benchmark: NF4 dequant-fused matvec HBM GB/s at Llama-3-8B MLP
+shapes on one MI355X, plus the Llama-3-8B-shaped NF4 decode tokens/s.
+
+A step is one pass of the hot path over one batch: the three MLP projections of
+one Llama-3-8B layer at batch 1 (gate 14336x4096, up 14336x4096, down
+4096x14336; NF4, block 64, fp32 absmax, fp32 activations)
+configs[1] at M=1. Weights rotate through enough distinct copies (>= 512 MB)
+that the Infinity Cache cannot serve them; all inputs are resident in HBM
+before the timed region. `value` is algorithmic bytes moved per second.
+
+Prints ONE JSON line. `python bench.py --gpus N --steps K --warmup W`.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+K_MODEL, FFN = 4096, 14336
+BLOCK = 64
+
+
+def nf4_bytes(n: int, k: int, m: int = 1) -> int:
+    """Algorithmic bytes of one NF4 matvec: codes + absmax + x + y."""
+    return n * k // 2 + (n * k // BLOCK) * 4 + m * k * 4 + m * n * 4
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough for 512 MB)")
+    ap.add_argument("--no-decode", action="store_true", help="skip the Llama decode measurement")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--decode-steps", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def make_mlp_copies(abi, torch, copies: int):
+    from aljabr_amd.llama import nf4_quantize_device
+    g = torch.Generator(device="cuda:0").manual_seed(2024)
+    mats = []
+    for _ in range(copies):
+        layer = []
+        for n, k in ((FFN, K_MODEL), (FFN, K_MODEL), (K_MODEL, FFN)):
+            w = torch.randn(n * k, generator=g, device="cuda:0").mul_(0.02)
+            c, a = nf4_quantize_device(w, BLOCK)
+            del w
+            layer.append((c, a, n, k))
+        mats.append(layer)
+    torch.cuda.synchronize()
+    return mats
+
+
+def time_mlp(abi, torch, stream, mats, steps: int, warmup: int):
+    lib = abi.load()
+    x = torch.randn(K_MODEL, device="cuda:0")
+    h = torch.randn(FFN, device="cuda:0")
+    outs = [torch.empty(FFN, device="cuda:0"), torch.empty(FFN, device="cuda:0"), torch.empty(K_MODEL, device="cuda:0")]
+    ins = [x, x, h]
+    torch.cuda.synchronize()
+
+    def step(i):
+        for j, (c, a, n, k) in enumerate(mats[i % len(mats)]):
+            rc = lib.aljabr_rocm_matvec_tb_nf4(outs[j].data_ptr(), ins[j].data_ptr(), c.data_ptr(), a.data_ptr(),
+                                                k, n, BLOCK)
+            if rc:
+                abi.check(rc, "aljabr_rocm_matvec_tb_nf4")
+
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(steps):
+            step(warmup + i)
+        end.record(stream)
+        end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end)   # ms
+
+
+def cpu_baseline(seconds: float):
+    """Oracle (C restatement of the reference CPU path) on a bounded sample:
+    repeated MLP steps (gate, up, down NF4 matvecs at batch 1) for ~`seconds`."""
+    import numpy as np
+    import oracle
+    threads = oracle.threads()
+    mats = []
+    for i, (n, k) in enumerate(((FFN, K_MODEL), (FFN, K_MODEL), (K_MODEL, FFN))):
+        codes, absmax = oracle.nf4_quantize(oracle.normal(100 + i, n * k, 0.0, 0.02), BLOCK)
+        mats.append((codes, absmax, n, k))
+    xs = {K_MODEL: oracle.normal(7, K_MODEL), FFN: oracle.normal(8, FFN)}
+    oracle.nf4_matvec(*mats[0][:2], xs[K_MODEL], FFN, K_MODEL, BLOCK, threads)   # warm
+    done, t0 = 0, time.perf_counter()
+    while True:
+        for codes, absmax, n, k in mats:
+            oracle.nf4_matvec(codes, absmax, xs[k], n, k, BLOCK, threads)
+        done += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    step_bytes = sum(nf4_bytes(n, k) for _, _, n, k in mats)
+    return {"value": round(step_bytes * done / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{done} MLP steps (3 NF4 matvecs each: 14336x4096, 14336x4096, 4096x14336, batch 1), "
+                      f"{dt:.1f} s, oracle C restatement, OpenMP row chunks = 2 x {threads} threads"}
+
+
+def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, weights, cfg):
+    from aljabr_amd.llama import DeviceLlama
+    max_seq = ctx + steps + 8
+    model = DeviceLlama(cfg, weights, max_batch=batch, max_seq=max_seq)
+    # Context of `ctx` tokens: fill the fp16 KV cache with N(0,1) values.
+    kp, vp = model.kv_cache_ptrs()
+    total = model.kv_cache_elems()
+    chunk = 1 << 26
+    g = torch.Generator(device="cuda:0").manual_seed(77)
+    for base_ptr in (kp, vp):
+        off = 0
+        while off < total:
+            n = min(chunk, total - off)
+            r = torch.randn(n, generator=g, device="cuda:0").half()
+            torch.cuda.synchronize()
+            abi.call("aljabr_rocm_memcpy_d2d", base_ptr + 2 * off, r.data_ptr(), 2 * n)
+            abi.call("aljabr_rocm_synchronize")
+            off += n
+            del r
+    tok = torch.randint(0, cfg["vocab"], (batch,), dtype=torch.int32, device="cuda:0",
+                        generator=torch.Generator(device="cuda:0").manual_seed(5))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        pos = torch.full((batch,), ctx, dtype=torch.int32, device="cuda:0")
+        tok = model.decode(tok, pos, batch)          # warm-up step
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        positions = [torch.full((batch,), ctx + 1 + i, dtype=torch.int32, device="cuda:0") for i in range(steps)]
+        torch.cuda.synchronize()
+        start.record(stream)
+        for i in range(steps):
+            tok = model.decode(tok, positions[i], batch)
+        end.record(stream)
+        end.synchronize()
+    ms = start.elapsed_time(end) / steps
+    model.close()
+    return {"batch": batch, "context": ctx, "ms_per_step": round(ms, 3), "tokens_per_s": round(batch * 1000.0 / ms, 1)}
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(no multi-GPU path: every box has one MI355X).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from aljabr_amd import abi
+    abi.init(0)
+    # One stream for torch (memory plumbing) and the C ABI, so their work is
+    # ordered and the HIP events below time the kernels' own stream.
+    stream = torch.cuda.Stream()
+    abi.call("aljabr_rocm_set_stream", stream.cuda_stream)
+    abi.call("aljabr_rocm_set_sync_mode", 0)
+    with torch.cuda.stream(stream):
+        run(args, abi, torch, stream)
+
+
+def run(args, abi, torch, stream) -> None:
+    step_bytes = nf4_bytes(FFN, K_MODEL) * 2 + nf4_bytes(K_MODEL, FFN)
+    copies = args.copies or max(2, -(-512_000_000 // step_bytes))
+    log(f"building {copies} NF4 MLP weight copies ({copies * step_bytes / 1e6:.0f} MB)")
+    mats = make_mlp_copies(abi, torch, copies)
+    log(f"timing {args.steps} steps after {args.warmup} warmup")
+    ms = time_mlp(abi, torch, stream, mats, args.steps, args.warmup)
+    launches = 3 * args.steps
+    per_launch_ms = ms / launches
+    gbs = step_bytes * args.steps / (ms / 1e3) / 1e9
+    per_launch_bytes = nf4_bytes(FFN, K_MODEL)   # all three launches move 33,030,144 + x + y bytes
+    achieved = per_launch_bytes / (per_launch_ms / 1e3) / 1e9
+    del mats
+    torch.cuda.empty_cache()
+
+    result = {
+        "metric": "NF4 matvec HBM GB/s (% peak) + Llama-3-8B-shape NF4 decode tokens/s, 1 GPU",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "nf4->f32",
+        "data": "synthetic: NF4 weights quantized on device from N(0,0.02), x ~ N(0,1), "
+                f"{copies} rotating weight copies ({copies * step_bytes / 1e6:.0f} MB)",
+        "config": {"workload": "nf4_mlp_matvec_llama3_8b_batch1",
+                   "shapes": ["14336x4096", "14336x4096", "4096x14336"], "nf4_block": BLOCK,
+                   "batch": 1, "parallelism": "none (1 GPU)"},
+        "pct_peak_hbm": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "nf4_matvec_kernel", "bytes_per_launch": per_launch_bytes,
+                     "avg_launch_us": round(per_launch_ms * 1e3, 3)},
+    }
+
+    if not args.no_decode:
+        from aljabr_amd.llama import LLAMA3_8B, random_weights
+        log("building random-init Llama-3-8B-shaped NF4 model")
+        t0 = time.perf_counter()
+        weights = random_weights(LLAMA3_8B, seed=1)
+        log(f"model built in {time.perf_counter() - t0:.1f} s")
+        dec = []
+        for batch in (1, 32):
+            log(f"decode batch {batch}, context 2048")
+            dec.append(decode_bench(abi, torch, stream, batch, 2048, args.decode_steps, weights, LLAMA3_8B))
+        result["decode"] = dec
+        del weights
+        torch.cuda.empty_cache()
+
+    if not args.no_cpu:
+        log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,244 @@
+/*
+ * aljabr_rocm.h - C ABI of Aljabr's MI355X (gfx950) quantized-inference path.
+ *
+ * This is the drop-in boundary a Java provider binds through the JDK Foreign
+ * Function & Memory API (SymbolLookup.libraryLookup + Linker.downcallHandle),
+ * exactly as MetalBinding binds libaljabr_metal
+ * (backend/metal/aljabr-backend-metal/src/main/java/tech/kayys/aljabr/metal/binding/MetalBinding.java:205-230,1799-1818).
+ * Every entry point takes plain pointers and sizes and returns an int status.
+ *
+ * Pointers named C/A/B/out/Q/K/V/x/y are DEVICE pointers (from
+ * aljabr_rocm_alloc or any HIP allocation on the initialised device); host
+ * pointers appear only in the memcpy and info calls. Reference citations are
+ * relative to the andalus-ai/aljabr tree; MTLC = backend/metal/aljabr-backend-metal/src/main/cpp/metal.
+ *
+ * Execution model. Work is enqueued on the calling thread's stream (one
+ * library-owned HIP stream per thread, or the stream set by
+ * aljabr_rocm_set_stream). With sync mode on (the default, matching the
+ * reference contract that every native call returns after completion) each
+ * compute call waits for its stream before returning and reports device
+ * errors; with sync mode off calls are stream-ordered and
+ * aljabr_rocm_synchronize() waits. Concurrent calls from different threads use
+ * different streams and never share scratch memory.
+ */
+#ifndef ALJABR_ROCM_H
+#define ALJABR_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: the Metal ABI's codes (MTLC/aljabr_metal_matvec_api.m:506-520,
+ * MTLC/aljabr_metal_matvec_dispatch.m:644-662) plus a HIP runtime error. ---- */
+#define ALJABR_ROCM_OK 0
+#define ALJABR_ROCM_ERR_NOT_INITIALIZED (-1)
+#define ALJABR_ROCM_ERR_BAD_ARGUMENT (-2)   /* bad dimensions, null or misaligned pointer */
+#define ALJABR_ROCM_ERR_UNSUPPORTED (-3)    /* no kernel for this type/shape ("missing pipeline") */
+#define ALJABR_ROCM_ERR_BUFFER (-4)         /* allocation or copy failure */
+#define ALJABR_ROCM_ERR_DEVICE (-5)         /* HIP runtime / launch / execution error */
+
+/* ---- weight type ids: GGML ids as used by aljabr_metal_matvec_tb_batch
+ * (MTLC/aljabr_metal_matvec_api.m:1091-1100; engine/gguf/aljabr-gguf-core/.../core/GgmlType.java:12,17),
+ * plus NF4, which has no GGML id (the reference's DType has no NF4 entry). ---- */
+#define ALJABR_ROCM_TYPE_F32 0
+#define ALJABR_ROCM_TYPE_F16 1
+#define ALJABR_ROCM_TYPE_Q4_0 2
+#define ALJABR_ROCM_TYPE_Q8_0 8
+#define ALJABR_ROCM_TYPE_NF4 100
+
+/* ======================================================================== */
+/* lifecycle and device                                                      */
+/* ======================================================================== */
+
+/* Select device `ordinal`, check it is gfx950 (this library carries gfx950
+ * code objects only) and create the context. Idempotent for the same ordinal.
+ * Replaces the Metal init that MetalComputeBackend runs at session open
+ * (backend/metal/.../MetalComputeBackend.java:127-145). */
+int aljabr_rocm_init(int ordinal);
+/* Release every library-owned stream and scratch buffer. Idempotent. */
+int aljabr_rocm_shutdown(void);
+int aljabr_rocm_is_initialized(void);
+/* Number of visible HIP devices (0 when no GPU); does not need init. */
+int aljabr_rocm_device_count(int *count);
+
+typedef struct aljabr_rocm_device_info {
+    char name[256];
+    char arch[64];             /* e.g. "gfx950:sramecc+:xnack-" */
+    uint64_t total_bytes;
+    uint64_t free_bytes;
+    int32_t compute_units;
+    int32_t wavefront_size;
+    int32_t clock_khz;
+    int32_t memory_clock_khz;
+    int32_t memory_bus_width;
+    int32_t l2_bytes;
+    int32_t runtime_version;
+    int32_t driver_version;
+} aljabr_rocm_device_info;
+
+/* Fills DeviceDescriptor's fields (spi/aljabr-spi-core/.../DeviceDescriptor.java:10-37). */
+int aljabr_rocm_device_info_get(int ordinal, aljabr_rocm_device_info *info);
+
+/* Thread-local message for the last non-zero status on this thread. */
+const char *aljabr_rocm_last_error(void);
+/* Library version as major*10000 + minor*100 + patch. */
+int aljabr_rocm_version(void);
+
+/* ======================================================================== */
+/* streams and memory (TensorStorage lifetime: one alloc <-> one free)        */
+/* ======================================================================== */
+
+/* Bind the calling thread to an existing hipStream_t (NULL: back to the
+ * library's own stream for this thread). */
+int aljabr_rocm_set_stream(void *hip_stream);
+int aljabr_rocm_get_stream(void **hip_stream);
+/* 1 (default): compute calls return after completion; 0: stream-ordered. Per thread. */
+int aljabr_rocm_set_sync_mode(int synchronous);
+int aljabr_rocm_synchronize(void);
+
+/* Device allocation backing RocmDeviceStorage; the final TensorStorage.release()
+ * maps to aljabr_rocm_free (plugins/ml/aljabr-tensor/.../memory/TensorStorage.java:21-41). */
+int aljabr_rocm_alloc(size_t bytes, void **device_ptr);
+int aljabr_rocm_free(void *device_ptr);
+/* ComputeBackend.copyFromHost (plugins/ml/aljabr-tensor/.../backend/ComputeBackend.java:151-162). */
+int aljabr_rocm_memcpy_h2d(void *device_dst, const void *host_src, size_t bytes);
+int aljabr_rocm_memcpy_d2h(void *host_dst, const void *device_src, size_t bytes);
+int aljabr_rocm_memcpy_d2d(void *device_dst, const void *device_src, size_t bytes);
+/* Byte fill with a kernel (never a memset node, so callers may capture it). */
+int aljabr_rocm_fill_u8(void *device_dst, int value, size_t bytes);
+
+/* ======================================================================== */
+/* quantized matvec / small-M GEMM: C[m][n] = sum_k A[m][k] * W[n][k]         */
+/* W is [N,K] row-major ("transposed right", MTLJ/MetalComputeBackend.java:435-470). */
+/* ======================================================================== */
+
+/* NF4, batch 1. B_packed: N*K/2 bytes, byte j = (code[2j] << 4) | code[2j+1];
+ * absmax: fp32 per blockSize elements over the flat [N,K] index.
+ * Replaces aljabr_metal_matvec_tb_nf4 (MTLC/aljabr_metal_matvec_api.h:59-61). */
+int aljabr_rocm_matvec_tb_nf4(void *C, const void *A, const void *B_packed,
+                              const void *absmax, int K, int N, int blockSize);
+/* GGUF Q4_0 blocks {f16 d; u8 qs[16]} (no Metal counterpart; the GGUF CPU
+ * runtime's GgufQ32RawDot.dotRowQ4_0 rows, engine/gguf/.../runtime/GgufQ32RawDot.java:34-67). */
+int aljabr_rocm_matvec_tb_q4_0(void *C, const void *A, const void *B, int K, int N);
+/* GGUF Q8_0 blocks {f16 d; i8 qs[32]}; replaces aljabr_metal_matvec_tb_q8_0
+ * (MTLC/aljabr_metal_matvec_api.h:55). */
+int aljabr_rocm_matvec_tb_q8_0(void *C, const void *A, const void *B, int K, int N);
+/* fp16 rows (LM head); replaces aljabr_metal_matvec_tb_half (MTLC/aljabr_metal_matvec_api.h:32-33). */
+int aljabr_rocm_matvec_tb_half(void *C, const void *A, const void *B, int K, int N);
+
+/* A[batchSize][K] fp32 -> C[batchSize][N] fp32 with W read once per call.
+ * type: ALJABR_ROCM_TYPE_{Q4_0,Q8_0,F16}. Replaces aljabr_metal_matvec_tb_batch
+ * (MTLC/aljabr_metal_matvec_api.h:93-94). batchSize < 16 runs the
+ * wavefront-reduction kernels, batchSize >= 16 the MFMA kernels. */
+int aljabr_rocm_matvec_tb_batch(void *C, const void *A, const void *B, int K,
+                                int N, int type, int batchSize);
+/* NF4 variant of the above (the Metal ABI has no NF4 batch entry). */
+int aljabr_rocm_matvec_tb_batch_nf4(void *C, const void *A, const void *B_packed,
+                                    const void *absmax, int K, int N,
+                                    int blockSize, int batchSize);
+
+/* ======================================================================== */
+/* codecs                                                                    */
+/* ======================================================================== */
+
+/* Decode `numel` weights to fp32, bit-exact with the reference decoders:
+ * NF4 STC/DequantizationKernel.java:84-102 (absmax/blockSize used), Q4_0
+ * GgufBlockDequantizer.java:33-37,403-416 (+0.0f), Q8_0 :231-265, F16
+ * GgufQuantTables.java:143-165. STC = engine/safetensor/aljabr-safetensor-core/.../core/tensor. */
+int aljabr_rocm_dequantize(void *dst_f32, const void *src, const void *absmax,
+                           long long numel, int type, int blockSize);
+/* Encode fp32 weights. Q4_0/Q8_0 follow GGUFWriter.encodeQ4_0/encodeQ8_0
+ * bit-for-bit (engine/gguf/aljabr-gguf-core/.../writer/GGUFWriter.java:163-209,360-387);
+ * NF4 uses per-block absmax and nearest-level codes (the reference's NF4
+ * quantizer is not in its tree). F16 uses the writer's half rounding. */
+int aljabr_rocm_quantize(void *dst, void *absmax_out, const void *src_f32,
+                         long long numel, int type, int blockSize);
+
+/* ======================================================================== */
+/* attention                                                                 */
+/* ======================================================================== */
+
+/* Dense GQA attention with CpuBackend.attentionGqa semantics
+ * (backend/cpu/.../CpuBackend.java:1546-1748): Q[B,Hq,Sq,D] fp32,
+ * K/V[B,Hkv,Sk,D] (kvType F32 or F16), optional additive mask [Sq,Sk] fp32
+ * (NULL for none; NaN/+inf entries are rejected with -2), bottom-right causal
+ * alignment, scale = 1/sqrt(D) when scale <= 0. out[B,Hq,Sq,D] fp32.
+ * Split-K online softmax; D must be 64 or 128 (else -3). */
+int aljabr_rocm_attention_gqa(void *out, const void *Q, const void *K, const void *V,
+                              const void *mask, int B, int Hq, int Hkv, int Sq,
+                              int Sk, int D, int kvType, float scale, int causal);
+
+/* ======================================================================== */
+/* decode-step element-wise ops (fp32)                                       */
+/* ======================================================================== */
+
+/* out[r] = x[r] * 1/sqrt(mean(x[r]^2)+eps) * w, rows of `len`
+ * (GGUFVectorOps.rmsNorm, engine/gguf/.../loader/tensor/GGUFVectorOps.java:211-234). */
+int aljabr_rocm_rmsnorm(void *out, const void *x, const void *w, int rows, int len, float eps);
+/* In-place split-half RoPE over `rows` token rows of nHeads*headDim values,
+ * position pos[r] (device int32) for row r (GGUFVectorOps.java:383-440). */
+int aljabr_rocm_rope(void *x, const void *positions, int rows, int nHeads,
+                     int headDim, float base);
+/* dst = silu(gate) * up (GGUFVectorOps.java:333-338). */
+int aljabr_rocm_swiglu(void *dst, const void *gate, const void *up, long long n);
+/* a += b (GGUFVectorOps.addInPlace, GGUFVectorOps.java:108-116). */
+int aljabr_rocm_add_inplace(void *a, const void *b, long long n);
+/* out[r] = argmax(x[r]) over `cols` (first index on ties), rows of fp32. */
+int aljabr_rocm_argmax(void *out_i32, const void *x, int rows, int cols);
+
+/* ======================================================================== */
+/* Llama-shaped NF4 decode step (whole step device-resident)                 */
+/* ======================================================================== */
+
+typedef struct aljabr_rocm_llama_config {
+    int32_t layers, dim, ffn, n_heads, n_kv_heads, head_dim, vocab, max_seq;
+    int32_t nf4_block;      /* NF4 absmax block size */
+    int32_t max_batch;      /* sequences decoded together */
+    float rope_base, eps;
+} aljabr_rocm_llama_config;
+
+/* Device pointers to one model's weights. Projection weights are NF4 [out,in]
+ * codes + fp32 absmax; norms fp32; token embedding fp32 [vocab,dim]; LM head
+ * fp16 [vocab,dim]. Per-layer pointer arrays are HOST arrays of `layers`
+ * device pointers. */
+typedef struct aljabr_rocm_llama_weights {
+    const void *tok_embed;
+    const void *const *attn_norm, *const *ffn_norm;
+    const void *const *wq, *const *wk, *const *wv, *const *wo;
+    const void *const *wq_absmax, *const *wk_absmax, *const *wv_absmax, *const *wo_absmax;
+    const void *const *w_gate, *const *w_up, *const *w_down;
+    const void *const *w_gate_absmax, *const *w_up_absmax, *const *w_down_absmax;
+    const void *out_norm;
+    const void *lm_head;
+} aljabr_rocm_llama_weights;
+
+typedef struct aljabr_rocm_llama aljabr_rocm_llama;
+
+/* Create a decode session: copies the pointer tables and allocates the fp16 KV
+ * cache [layers][max_batch][n_kv_heads][max_seq][head_dim] and activations.
+ * Weights stay owned by the caller. (GgufDecodePass + KVCache,
+ * engine/gguf/aljabr-gguf-java/.../GgufDecodePass.java:183-592.) */
+int aljabr_rocm_llama_create(const aljabr_rocm_llama_config *cfg,
+                             const aljabr_rocm_llama_weights *w,
+                             aljabr_rocm_llama **out);
+int aljabr_rocm_llama_destroy(aljabr_rocm_llama *model);
+/* One greedy decode step for `batch` sequences: tokens[b] (device int32) at
+ * positions[b] (device int32, < max_seq). Writes logits[batch][vocab] fp32 (may
+ * be NULL) and next_tokens[batch] (device int32). */
+int aljabr_rocm_llama_decode(aljabr_rocm_llama *model, const void *tokens,
+                             const void *positions, int batch, void *logits,
+                             void *next_tokens);
+/* Device pointer of the session's final hidden state [batch][dim] fp32. */
+int aljabr_rocm_llama_hidden(aljabr_rocm_llama *model, void **hidden);
+/* Device pointers of the fp16 K and V caches, each
+ * [layers][max_batch][n_kv_heads][max_seq][head_dim], for loading a prefix
+ * (the role of KVCacheSession's committed prefix, core/aljabr-core/.../cache/KVCacheSession.java:95-105). */
+int aljabr_rocm_llama_kv_cache(aljabr_rocm_llama *model, void **k_cache, void **v_cache);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

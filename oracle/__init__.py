@@ -1,0 +1,327 @@
+"""CPU oracle for Aljabr's quantized-inference hot path.
+
+TEST INFRASTRUCTURE ONLY. This package is the checker for the HIP kernels and
+the timed CPU baseline: only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg may import it. The product package
+(``aljabr_amd``) never imports, loads or falls back to anything here.
+
+The arithmetic lives in ``aljabr_oracle.c`` (a C restatement of the reference's
+Java CPU path; each function cites the reference file:line it follows). This
+module only binds it with ctypes and adds numpy conveniences.
+
+Parity status of each oracle function (what pins it) is in ``aljabr_oracle.h``.
+``orc_nf4_quantize`` is PARITY UNPINNED against the reference (its quantizer is
+absent from the reference tree); it is pinned only by the decode(encode(w))
+nearest-level invariant.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libaljabr_oracle.so")
+_lib = None
+
+QTYPE_Q4_0 = 2
+QTYPE_Q8_0 = 8
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc); returns the library path."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_F = ctypes.c_float
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    sig = {
+        "orc_f16_to_f32": (_F, [ctypes.c_uint16]),
+        "orc_f32_to_f16_writer": (ctypes.c_uint16, [_F]),
+        "orc_java_round": (_I32, [_F]),
+        "orc_nf4_dequant": (None, [_P, _P, _I64, _I32, _P]),
+        "orc_nf4_quantize": (None, [_P, _I64, _I32, _P, _P]),
+        "orc_nf4_matvec": (None, [_P, _P, _I32, _P, _I64, _I64, _I32, _P, ctypes.c_int]),
+        "orc_q4_0_quantize": (None, [_P, _I64, _P]),
+        "orc_q8_0_quantize": (None, [_P, _I64, _P]),
+        "orc_q4_0_dequant": (None, [_P, _I64, _P]),
+        "orc_q8_0_dequant": (None, [_P, _I64, _P]),
+        "orc_q4_0_dot_row": (_F, [_P, _I32, _P]),
+        "orc_q8_0_dot_row": (_F, [_P, _I32, _P]),
+        "orc_q4_0_matvec": (None, [_P, _P, _I64, _I64, _I32, _P, ctypes.c_int]),
+        "orc_q8_0_matvec": (None, [_P, _P, _I64, _I64, _I32, _P, ctypes.c_int]),
+        "orc_f16_matvec": (None, [_P, _P, _I64, _I64, _I32, _P, ctypes.c_int]),
+        "orc_attention_gqa": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                                            ctypes.c_int, _P, ctypes.c_int]),
+        "orc_rmsnorm": (None, [_P, _P, _P, _I32, _F]),
+        "orc_rope": (None, [_P, _I32, _I32, _I32, _F]),
+        "orc_swiglu": (None, [_P, _P, _P, _I32]),
+        "orc_softmax": (None, [_P, _I32]),
+        "orc_llama_decode": (_I32, [_P, _P, _I32, _I32, _P, _P, _P, _P, ctypes.c_int]),
+        "orc_fill_normal": (None, [ctypes.c_uint64, _F, _F, _P, _I64]),
+        "orc_fill_uniform_int": (None, [ctypes.c_uint64, _I32, _P, _I64]),
+        "orc_max_threads": (ctypes.c_int, []),
+        "orc_round_f16": (_F, [_F]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def threads() -> int:
+    return int(lib().orc_max_threads())
+
+
+# ---- generator ------------------------------------------------------------
+
+def normal(seed: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(int(n), dtype=np.float32)
+    lib().orc_fill_normal(seed & ((1 << 64) - 1), mean, std, _ptr(out), out.size)
+    return out
+
+
+def uniform_int(seed: int, bound: int, n: int) -> np.ndarray:
+    out = np.empty(int(n), dtype=np.int32)
+    lib().orc_fill_uniform_int(seed & ((1 << 64) - 1), bound, _ptr(out), out.size)
+    return out
+
+
+# ---- scalars --------------------------------------------------------------
+
+def f16_to_f32(h: int) -> float:
+    return float(lib().orc_f16_to_f32(h))
+
+
+def f32_to_f16_writer(v: float) -> int:
+    return int(lib().orc_f32_to_f16_writer(v))
+
+
+def java_round(v: float) -> int:
+    return int(lib().orc_java_round(v))
+
+
+# ---- NF4 ------------------------------------------------------------------
+
+NF4_TABLE = np.array([
+    -1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+    -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+    0.07958029955625534, 0.16093020141124725, 0.24611230194568634, 0.33791524171829224,
+    0.44070982933044434, 0.5626170039176941, 0.7229568362236023, 1.0], dtype=np.float32)
+
+
+def nf4_quantize(w: np.ndarray, group: int = 64):
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    codes = np.empty((w.size + 1) // 2, dtype=np.uint8)
+    absmax = np.empty((w.size + group - 1) // group, dtype=np.float32)
+    lib().orc_nf4_quantize(_ptr(w), w.size, group, _ptr(codes), _ptr(absmax))
+    return codes, absmax
+
+
+def nf4_dequant(codes: np.ndarray, absmax: np.ndarray, numel: int, group: int = 64) -> np.ndarray:
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    absmax = np.ascontiguousarray(absmax, dtype=np.float32)
+    out = np.empty(int(numel), dtype=np.float32)
+    lib().orc_nf4_dequant(_ptr(codes), _ptr(absmax), out.size, group, _ptr(out))
+    return out
+
+
+def nf4_matvec(codes, absmax, x: np.ndarray, n: int, k: int, group: int = 64,
+               nthreads: int | None = None) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = x.size // k
+    y = np.empty(m * n, dtype=np.float32)
+    lib().orc_nf4_matvec(_ptr(np.ascontiguousarray(codes)), _ptr(np.ascontiguousarray(absmax)),
+                         group, _ptr(x), n, k, m, _ptr(y), nthreads or threads())
+    return y.reshape(m, n) if m > 1 else y
+
+
+# ---- GGUF Q4_0 / Q8_0 -----------------------------------------------------
+
+def block_bytes(qtype: int) -> int:
+    return {QTYPE_Q4_0: 18, QTYPE_Q8_0: 34}[qtype]
+
+
+def quantize(qtype: int, w: np.ndarray) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    out = np.empty(w.size // 32 * block_bytes(qtype), dtype=np.uint8)
+    fn = lib().orc_q4_0_quantize if qtype == QTYPE_Q4_0 else lib().orc_q8_0_quantize
+    fn(_ptr(w), w.size, _ptr(out))
+    return out
+
+
+def dequant(qtype: int, blocks: np.ndarray, numel: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.empty(int(numel), dtype=np.float32)
+    fn = lib().orc_q4_0_dequant if qtype == QTYPE_Q4_0 else lib().orc_q8_0_dequant
+    fn(_ptr(blocks), out.size, _ptr(out))
+    return out
+
+
+def dot_row(qtype: int, row: np.ndarray, x: np.ndarray) -> float:
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    fn = lib().orc_q4_0_dot_row if qtype == QTYPE_Q4_0 else lib().orc_q8_0_dot_row
+    return float(fn(_ptr(row), x.size, _ptr(x)))
+
+
+def q_matvec(qtype: int, w: np.ndarray, x: np.ndarray, n: int, k: int,
+             nthreads: int | None = None) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = x.size // k
+    y = np.empty(m * n, dtype=np.float32)
+    fn = lib().orc_q4_0_matvec if qtype == QTYPE_Q4_0 else lib().orc_q8_0_matvec
+    fn(_ptr(np.ascontiguousarray(w)), _ptr(x), n, k, m, _ptr(y), nthreads or threads())
+    return y.reshape(m, n) if m > 1 else y
+
+
+def f16_matvec(w_bits: np.ndarray, x: np.ndarray, n: int, k: int,
+               nthreads: int | None = None) -> np.ndarray:
+    w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = x.size // k
+    y = np.empty(m * n, dtype=np.float32)
+    lib().orc_f16_matvec(_ptr(w_bits), _ptr(x), n, k, m, _ptr(y), nthreads or threads())
+    return y.reshape(m, n) if m > 1 else y
+
+
+# ---- attention ------------------------------------------------------------
+
+def attention_gqa(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask=None, causal=False,
+                  nthreads: int | None = None) -> np.ndarray:
+    """q [B,Hq,Sq,D], k/v [B,Hkv,Sk,D] float32 -> out [B,Hq,Sq,D]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    b, hq, sq, d = q.shape
+    hkv, sk = k.shape[1], k.shape[2]
+    out = np.empty_like(q)
+    mp = 0
+    if mask is not None:
+        mask = np.ascontiguousarray(mask, dtype=np.float32)
+        mp = _ptr(mask)
+    rc = lib().orc_attention_gqa(_ptr(q), _ptr(k), _ptr(v), mp or None, b, hq, hkv, sq, sk, d,
+                                 int(bool(causal)), _ptr(out), nthreads or threads())
+    if rc != 0:
+        raise ValueError("GQA expects Q[B,Hq,Sq,D], K/V[B,Hkv,Sk,D] and a finite, non-NaN mask")
+    return out
+
+
+# ---- element-wise ---------------------------------------------------------
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows = x.reshape(-1, w.size)
+    out = np.empty_like(rows)
+    for r in range(rows.shape[0]):
+        row = np.ascontiguousarray(rows[r])
+        o = np.empty_like(row)
+        lib().orc_rmsnorm(_ptr(row), _ptr(w), _ptr(o), w.size, eps)
+        out[r] = o
+    return out.reshape(x.shape)
+
+
+def rope(x: np.ndarray, n_heads: int, head_dim: int, pos: int, base: float) -> np.ndarray:
+    y = np.array(x, dtype=np.float32, copy=True).reshape(-1)
+    lib().orc_rope(_ptr(y), n_heads, head_dim, pos, base)
+    return y.reshape(np.shape(x))
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    gate = np.ascontiguousarray(gate, dtype=np.float32).reshape(-1)
+    up = np.ascontiguousarray(up, dtype=np.float32).reshape(-1)
+    out = np.empty_like(gate)
+    lib().orc_swiglu(_ptr(gate), _ptr(up), _ptr(out), gate.size)
+    return out
+
+
+def softmax(a: np.ndarray) -> np.ndarray:
+    y = np.array(a, dtype=np.float32, copy=True).reshape(-1)
+    lib().orc_softmax(_ptr(y), y.size)
+    return y
+
+
+# ---- Llama-shaped decode step ---------------------------------------------
+
+class _LlamaCfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "layers", "dim", "ffn", "n_heads", "n_kv_heads", "head_dim", "vocab", "max_seq",
+        "nf4_group", "kv_f16")] + [("rope_base", ctypes.c_float), ("eps", ctypes.c_float)]
+
+
+_VP = ctypes.c_void_p
+
+
+class _LlamaWeights(ctypes.Structure):
+    _fields_ = [("tok_embed", _VP), ("attn_norm", _VP), ("ffn_norm", _VP),
+                ("wq", _VP), ("wk", _VP), ("wv", _VP), ("wo", _VP),
+                ("wq_s", _VP), ("wk_s", _VP), ("wv_s", _VP), ("wo_s", _VP),
+                ("w_gate", _VP), ("w_up", _VP), ("w_down", _VP),
+                ("w_gate_s", _VP), ("w_up_s", _VP), ("w_down_s", _VP),
+                ("out_norm", _VP), ("lm_head", _VP)]
+
+
+class LlamaOracle:
+    """Single-sequence decode with the oracle (GgufDecodePass restated).
+
+    ``weights`` maps names to numpy arrays: tok_embed [vocab*dim] f32,
+    lm_head [vocab*dim] u16 (fp16 bits), out_norm [dim] f32 and per-layer lists
+    attn_norm, ffn_norm (f32) and wq/wk/wv/wo/w_gate/w_up/w_down (codes u8)
+    with their *_s absmax (f32)."""
+
+    LAYER_KEYS = ("attn_norm", "ffn_norm", "wq", "wk", "wv", "wo", "wq_s", "wk_s", "wv_s", "wo_s",
+                  "w_gate", "w_up", "w_down", "w_gate_s", "w_up_s", "w_down_s")
+
+    def __init__(self, cfg: dict, weights: dict, kv_f16: bool = True):
+        self.cfg = _LlamaCfg(cfg["layers"], cfg["dim"], cfg["ffn"], cfg["n_heads"], cfg["n_kv_heads"],
+                             cfg["head_dim"], cfg["vocab"], cfg["max_seq"], cfg["nf4_block"], int(kv_f16),
+                             cfg["rope_base"], cfg["eps"])
+        self._keep = []
+        w = _LlamaWeights()
+        for key in ("tok_embed", "out_norm", "lm_head"):
+            arr = np.ascontiguousarray(weights[key])
+            self._keep.append(arr)
+            setattr(w, key, arr.ctypes.data)
+        for key in self.LAYER_KEYS:
+            arrs = [np.ascontiguousarray(a) for a in weights[key]]
+            self._keep.extend(arrs)
+            table = (ctypes.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+            self._keep.append(table)
+            setattr(w, key, ctypes.cast(table, ctypes.c_void_p).value)
+        self.weights = w
+        kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+        self.k_cache = np.zeros(cfg["layers"] * cfg["max_seq"] * kvd, np.float32)
+        self.v_cache = np.zeros_like(self.k_cache)
+        self.dim, self.vocab = cfg["dim"], cfg["vocab"]
+
+    def decode(self, token: int, pos: int, nthreads: int | None = None):
+        logits = np.empty(self.vocab, np.float32)
+        hidden = np.empty(self.dim, np.float32)
+        nxt = lib().orc_llama_decode(ctypes.byref(self.cfg), ctypes.byref(self.weights), token, pos,
+                                     _ptr(self.k_cache), _ptr(self.v_cache), _ptr(logits), _ptr(hidden),
+                                     nthreads or threads())
+        return int(nxt), logits, hidden

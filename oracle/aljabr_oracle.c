@@ -1,0 +1,680 @@
+/*
+ * aljabr_oracle.c - CPU restatement of Aljabr's quantized-inference hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see aljabr_oracle.h): the checker for the HIP
+ * kernels and the timed CPU baseline. Nothing under aljabr_amd/ may use it.
+ *
+ * Built with -ffp-contract=off so that a*b+c is a rounded multiply followed by
+ * a rounded add, as Java evaluates it (Java never fuses unless Math.fma or a
+ * Vector API fma() is written). Citations are file:line in andalus-ai/aljabr;
+ * the path abbreviations are listed in aljabr_oracle.h.
+ */
+#include "aljabr_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* scalar conversions                                                        */
+/* ------------------------------------------------------------------------ */
+
+static inline float bits_to_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint32_t f32_to_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+/* GRT/GgufQuantTables.java:143-165. Normal numbers rebias the exponent,
+ * subnormals are mantissa/1024 * 2^-14, any NaN becomes the canonical NaN. */
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (h >> 15) & 1u;
+    uint32_t exponent = (h >> 10) & 0x1fu;
+    uint32_t mantissa = h & 0x3ffu;
+    if (exponent == 0) {
+        if (mantissa == 0) return sign ? -0.0f : 0.0f;
+        float value = ldexpf((float)mantissa / 1024.0f, -14);
+        return sign ? -value : value;
+    }
+    if (exponent == 31) {
+        if (mantissa == 0) return sign ? -INFINITY : INFINITY;
+        return bits_to_f32(0x7fc00000u);
+    }
+    return bits_to_f32((sign << 31) | ((exponent + 112u) << 23) | (mantissa << 13));
+}
+
+/* GWR/GGUFWriter.java:360-387. Truncate the fp32 mantissa to 10 bits and add
+ * one ulp when the first dropped bit is set (round half away from zero in
+ * magnitude); overflow maps to inf (or to 0x7C01 when any mantissa bit is set),
+ * exponents below -24 flush to a signed zero. */
+uint16_t orc_f32_to_f16_writer(float v) {
+    uint32_t bits = f32_to_bits(v);
+    uint32_t sign = (bits >> 16) & 0x8000u;
+    int32_t exponent = (int32_t)((bits >> 23) & 0xffu) - 127 + 15;
+    uint32_t mantissa = bits & 0x7fffffu;
+    if (exponent >= 31) {
+        return (uint16_t)(sign | 0x7c00u | (mantissa == 0 ? 0u : 1u));
+    }
+    if (exponent <= 0) {
+        if (exponent < -10) return (uint16_t)sign;
+        uint32_t full = mantissa | 0x800000u;
+        int32_t shift = 14 - exponent;
+        uint32_t half_mantissa = full >> shift;
+        if ((full >> (shift - 1)) & 1u) half_mantissa += 1;
+        return (uint16_t)(sign | half_mantissa);
+    }
+    uint32_t half = sign | ((uint32_t)exponent << 10) | (mantissa >> 13);
+    if (mantissa & 0x1000u) half += 1;
+    return (uint16_t)half;
+}
+
+/* Math.round(float): floor(a + 1/2) evaluated exactly. A float plus 0.5 is
+ * exact in double for every |a| < 2^52, so the double sum has no rounding. */
+int32_t orc_java_round(float v) {
+    if (isnan(v)) return 0;
+    double r = floor((double)v + 0.5);
+    if (r >= 2147483647.0) return 2147483647;
+    if (r <= -2147483648.0) return (int32_t)(-2147483647 - 1);
+    return (int32_t)r;
+}
+
+/* ------------------------------------------------------------------------ */
+/* threading helpers (GRT/GgufParallelConfig.java:64-73: chunks = 2*threads)  */
+/* ------------------------------------------------------------------------ */
+
+int orc_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+typedef void (*row_task)(const void *ctx, int64_t row_begin, int64_t row_end);
+
+static void run_row_chunks(int64_t rows, int threads, row_task task, const void *ctx) {
+    if (threads < 1) threads = 1;
+    int64_t chunks = rows < 2LL * threads ? rows : 2LL * threads;
+    if (chunks <= 1) {
+        task(ctx, 0, rows);
+        return;
+    }
+    int64_t per = rows / chunks, extra = rows % chunks;
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
+#endif
+    for (int64_t c = 0; c < chunks; c++) {
+        int64_t begin = c * per + (c < extra ? c : extra);
+        int64_t end = begin + per + (c < extra ? 1 : 0);
+        task(ctx, begin, end);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* NF4                                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* STC/DequantizationKernel.java:23-28 (the bitsandbytes NormalFloat-4 levels). */
+const float ORC_NF4_TABLE[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+
+/* STC/DequantizationKernel.java:84-102 */
+void orc_nf4_dequant(const uint8_t *codes, const float *absmax, int64_t numel,
+                     int32_t group_size, float *dst) {
+    int64_t bytes = (numel + 1) / 2;
+    for (int64_t j = 0; j < bytes; j++) {
+        uint8_t b = codes[j];
+        float s = absmax[(j * 2) / group_size];
+        dst[2 * j] = ORC_NF4_TABLE[(b >> 4) & 15] * s;
+        if (2 * j + 1 < numel) dst[2 * j + 1] = ORC_NF4_TABLE[b & 15] * s;
+    }
+}
+
+static uint8_t nf4_nearest(float v) {
+    /* Levels are sorted; pick the first level whose upper midpoint is >= v. */
+    for (int c = 0; c < 15; c++) {
+        float mid = (ORC_NF4_TABLE[c] + ORC_NF4_TABLE[c + 1]) * 0.5f;
+        if (v <= mid) return (uint8_t)c;
+    }
+    return 15;
+}
+
+void orc_nf4_quantize(const float *w, int64_t numel, int32_t group_size,
+                      uint8_t *codes, float *absmax) {
+    int64_t groups = (numel + group_size - 1) / group_size;
+    for (int64_t g = 0; g < groups; g++) {
+        int64_t begin = g * group_size, end = begin + group_size;
+        if (end > numel) end = numel;
+        float m = 0.0f;
+        for (int64_t i = begin; i < end; i++) {
+            float a = fabsf(w[i]);
+            if (a > m) m = a;
+        }
+        absmax[g] = m;
+    }
+    memset(codes, 0, (size_t)((numel + 1) / 2));
+    for (int64_t i = 0; i < numel; i++) {
+        float m = absmax[i / group_size];
+        uint8_t c = m == 0.0f ? 7 : nf4_nearest(w[i] / m);
+        if ((i & 1) == 0) codes[i >> 1] |= (uint8_t)(c << 4);
+        else codes[i >> 1] |= c;
+    }
+}
+
+/* 16-lane fp32 dot with a pairwise lane reduction. */
+static float dot16(const float *a, const float *b, int64_t n) {
+    float lanes[16] = {0};
+    int64_t i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int l = 0; l < 16; l++) lanes[l] += a[i + l] * b[i + l];
+    for (int w = 8; w >= 1; w >>= 1)
+        for (int l = 0; l < w; l++) lanes[l] += lanes[l + w];
+    float r = lanes[0];
+    for (; i < n; i++) r += a[i] * b[i];
+    return r;
+}
+
+typedef struct {
+    const uint8_t *codes; const float *absmax; int32_t group;
+    const float *x; int64_t n, k; int32_t m; float *y;
+} nf4_mv_ctx;
+
+static void nf4_mv_rows(const void *vctx, int64_t r0, int64_t r1) {
+    const nf4_mv_ctx *c = (const nf4_mv_ctx *)vctx;
+    float *row = (float *)malloc((size_t)c->k * sizeof(float));
+    for (int64_t n = r0; n < r1; n++) {
+        int64_t flat = n * c->k;
+        /* Dequantize the row exactly as the flat-matrix decode would. */
+        for (int64_t kk = 0; kk < c->k; kk++) {
+            int64_t e = flat + kk;
+            uint8_t b = c->codes[e >> 1];
+            int code = (e & 1) ? (b & 15) : (b >> 4);
+            row[kk] = ORC_NF4_TABLE[code] * c->absmax[e / c->group];
+        }
+        for (int32_t mm = 0; mm < c->m; mm++)
+            c->y[(int64_t)mm * c->n + n] = dot16(row, c->x + (int64_t)mm * c->k, c->k);
+    }
+    free(row);
+}
+
+void orc_nf4_matvec(const uint8_t *codes, const float *absmax, int32_t group_size,
+                    const float *x, int64_t n_rows, int64_t k_cols, int32_t m,
+                    float *y, int threads) {
+    nf4_mv_ctx c = {codes, absmax, group_size, x, n_rows, k_cols, m, y};
+    run_row_chunks(n_rows, threads, nf4_mv_rows, &c);
+}
+
+/* ------------------------------------------------------------------------ */
+/* GGUF Q4_0 / Q8_0                                                          */
+/* ------------------------------------------------------------------------ */
+
+static float max_abs(const float *v, int n) {
+    float m = 0.0f;
+    for (int i = 0; i < n; i++) {
+        float a = fabsf(v[i]);
+        m = a > m ? a : m;
+    }
+    return m;
+}
+
+static int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+static void put_le16(uint8_t *p, uint16_t v) { p[0] = (uint8_t)(v & 0xff); p[1] = (uint8_t)(v >> 8); }
+static uint16_t get_le16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* GWR/GGUFWriter.java:179-209: fp32 scale = maxAbs/7 is used to quantize, the
+ * fp16 (writer rounding) copy is stored; byte i = (hi+8)<<4 | (lo+8) with lo
+ * from element i and hi from element 16+i. */
+void orc_q4_0_quantize(const float *w, int64_t numel, uint8_t *out) {
+    for (int64_t blk = 0; blk < numel / 32; blk++) {
+        const float *v = w + blk * 32;
+        uint8_t *o = out + blk * 18;
+        float scale = max_abs(v, 32) / 7.0f;
+        put_le16(o, orc_f32_to_f16_writer(scale));
+        for (int i = 0; i < 16; i++) {
+            int lo = scale == 0.0f ? 0 : clampi(orc_java_round(v[i] / scale), -8, 7);
+            int hi = scale == 0.0f ? 0 : clampi(orc_java_round(v[16 + i] / scale), -8, 7);
+            o[2 + i] = (uint8_t)(((hi + 8) << 4) | (lo + 8));
+        }
+    }
+}
+
+/* GWR/GGUFWriter.java:163-177 */
+void orc_q8_0_quantize(const float *w, int64_t numel, uint8_t *out) {
+    for (int64_t blk = 0; blk < numel / 32; blk++) {
+        const float *v = w + blk * 32;
+        uint8_t *o = out + blk * 34;
+        float scale = max_abs(v, 32) / 127.0f;
+        put_le16(o, orc_f32_to_f16_writer(scale));
+        for (int i = 0; i < 32; i++) {
+            int q = scale == 0.0f ? 0 : orc_java_round(v[i] / scale);
+            o[2 + i] = (uint8_t)(clampi(q, -127, 127) & 0xff);
+        }
+    }
+}
+
+/* GRT/GgufBlockDequantizer.java:33-37 with bias 0.0f and zero point 8,
+ * :366-416 lane order. */
+void orc_q4_0_dequant(const uint8_t *blocks, int64_t numel, float *dst) {
+    for (int64_t blk = 0; blk < numel / 32; blk++) {
+        const uint8_t *b = blocks + blk * 18;
+        float d = orc_f16_to_f32(get_le16(b));
+        float *o = dst + blk * 32;
+        for (int j = 0; j < 16; j++) {
+            int q = b[2 + j];
+            o[j] = (float)((q & 15) - 8) * d + 0.0f;
+            o[16 + j] = (float)((q >> 4) - 8) * d + 0.0f;
+        }
+    }
+}
+
+/* GRT/GgufBlockDequantizer.java:231-265 */
+void orc_q8_0_dequant(const uint8_t *blocks, int64_t numel, float *dst) {
+    for (int64_t blk = 0; blk < numel / 32; blk++) {
+        const uint8_t *b = blocks + blk * 34;
+        float d = orc_f16_to_f32(get_le16(b));
+        for (int j = 0; j < 32; j++) dst[blk * 32 + j] = (float)(int8_t)b[2 + j] * d;
+    }
+}
+
+/* GRT/GgufQ32RawDot.java:454-463: one packed byte contributes its low nibble
+ * against x[index] and its high nibble against x[16+index]. */
+static inline float q4_pair(const uint8_t *q, int index, const float *x) {
+    int b = q[index];
+    return (float)((b & 15) - 8) * x[index] + (float)((b >> 4) - 8) * x[16 + index];
+}
+
+/* GRT/GgufQ32RawDot.java:428-450: four partials over bytes {i, i+4, i+8, i+12}. */
+static float q4_0_unscaled_block(const uint8_t *q, const float *x) {
+    float s0 = q4_pair(q, 0, x) + q4_pair(q, 4, x) + q4_pair(q, 8, x) + q4_pair(q, 12, x);
+    float s1 = q4_pair(q, 1, x) + q4_pair(q, 5, x) + q4_pair(q, 9, x) + q4_pair(q, 13, x);
+    float s2 = q4_pair(q, 2, x) + q4_pair(q, 6, x) + q4_pair(q, 10, x) + q4_pair(q, 14, x);
+    float s3 = q4_pair(q, 3, x) + q4_pair(q, 7, x) + q4_pair(q, 11, x) + q4_pair(q, 15, x);
+    return s0 + s1 + s2 + s3;
+}
+
+/* GRT/GgufQ32RawDot.java:342-349 */
+static float q4_0_block(const uint8_t *blk, const float *x) {
+    return orc_f16_to_f32(get_le16(blk)) * q4_0_unscaled_block(blk + 2, x);
+}
+
+/* GRT/GgufQ32RawDot.java:34-67 */
+float orc_q4_0_dot_row(const uint8_t *row, int32_t columns, const float *x) {
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    int blocks = columns / 32, b = 0;
+    for (; b <= blocks - 4; b += 4) {
+        s0 += q4_0_block(row + (b + 0) * 18, x + (b + 0) * 32);
+        s1 += q4_0_block(row + (b + 1) * 18, x + (b + 1) * 32);
+        s2 += q4_0_block(row + (b + 2) * 18, x + (b + 2) * 32);
+        s3 += q4_0_block(row + (b + 3) * 18, x + (b + 3) * 32);
+    }
+    float sum = s0 + s1 + s2 + s3;
+    for (; b < blocks; b++) sum += q4_0_block(row + b * 18, x + b * 32);
+    return sum;
+}
+
+/* GRT/GgufQ8RawDot.java:784-830: four partials over byte lanes {i, i+4, ...}
+ * combined two products at a time. */
+static float q8_unscaled_block(const uint8_t *q, const float *x) {
+    float s[4];
+    for (int lane = 0; lane < 4; lane++) {
+        float acc = (float)(int8_t)q[lane] * x[lane] + (float)(int8_t)q[lane + 4] * x[lane + 4];
+        for (int base = 8; base < 32; base += 8)
+            acc += (float)(int8_t)q[base + lane] * x[base + lane]
+                   + (float)(int8_t)q[base + lane + 4] * x[base + lane + 4];
+        s[lane] = acc;
+    }
+    return s[0] + s[1] + s[2] + s[3];
+}
+
+/* GRT/GgufQ8RawDot.java:138-185 */
+float orc_q8_0_dot_row(const uint8_t *row, int32_t columns, const float *x) {
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    int blocks = columns / 32, b = 0;
+    for (; b <= blocks - 4; b += 4) {
+        for (int u = 0; u < 4; u++) {
+            const uint8_t *blk = row + (b + u) * 34;
+            float v = orc_f16_to_f32(get_le16(blk)) * q8_unscaled_block(blk + 2, x + (b + u) * 32);
+            if (u == 0) s0 += v; else if (u == 1) s1 += v; else if (u == 2) s2 += v; else s3 += v;
+        }
+    }
+    float sum = s0 + s1 + s2 + s3;
+    for (; b < blocks; b++) {
+        const uint8_t *blk = row + b * 34;
+        sum += orc_f16_to_f32(get_le16(blk)) * q8_unscaled_block(blk + 2, x + b * 32);
+    }
+    return sum;
+}
+
+typedef struct {
+    const uint8_t *w; const float *x; int64_t n, k; int32_t m; float *y; int type;
+} q_mv_ctx;
+
+static void q_mv_rows(const void *vctx, int64_t r0, int64_t r1) {
+    const q_mv_ctx *c = (const q_mv_ctx *)vctx;
+    int64_t row_bytes = (c->k / 32) * (c->type == 2 ? 18 : 34);
+    for (int64_t n = r0; n < r1; n++) {
+        const uint8_t *row = c->w + n * row_bytes;
+        for (int32_t mm = 0; mm < c->m; mm++) {
+            const float *x = c->x + (int64_t)mm * c->k;
+            c->y[(int64_t)mm * c->n + n] = c->type == 2 ? orc_q4_0_dot_row(row, (int32_t)c->k, x)
+                                                        : orc_q8_0_dot_row(row, (int32_t)c->k, x);
+        }
+    }
+}
+
+void orc_q4_0_matvec(const uint8_t *w, const float *x, int64_t n_rows,
+                     int64_t k_cols, int32_t m, float *y, int threads) {
+    q_mv_ctx c = {w, x, n_rows, k_cols, m, y, 2};
+    run_row_chunks(n_rows, threads, q_mv_rows, &c);
+}
+
+void orc_q8_0_matvec(const uint8_t *w, const float *x, int64_t n_rows,
+                     int64_t k_cols, int32_t m, float *y, int threads) {
+    q_mv_ctx c = {w, x, n_rows, k_cols, m, y, 8};
+    run_row_chunks(n_rows, threads, q_mv_rows, &c);
+}
+
+/* GRT/GgufDenseDot.java:289-320: element i of the unrolled body feeds
+ * accumulator i % 4; the four are summed, then the tail is added. */
+static float f16_dot_row(const uint16_t *row, int64_t k, const float *x) {
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t i = 0;
+    for (; i + 16 <= k; i += 16)
+        for (int j = 0; j < 16; j++) s[j & 3] += orc_f16_to_f32(row[i + j]) * x[i + j];
+    float sum = s[0] + s[1] + s[2] + s[3];
+    for (; i < k; i++) sum += orc_f16_to_f32(row[i]) * x[i];
+    return sum;
+}
+
+typedef struct { const uint16_t *w; const float *x; int64_t n, k; int32_t m; float *y; } f16_mv_ctx;
+
+static void f16_mv_rows(const void *vctx, int64_t r0, int64_t r1) {
+    const f16_mv_ctx *c = (const f16_mv_ctx *)vctx;
+    for (int64_t n = r0; n < r1; n++)
+        for (int32_t mm = 0; mm < c->m; mm++)
+            c->y[(int64_t)mm * c->n + n] = f16_dot_row(c->w + n * c->k, c->k, c->x + (int64_t)mm * c->k);
+}
+
+void orc_f16_matvec(const uint16_t *w, const float *x, int64_t n_rows,
+                    int64_t k_cols, int32_t m, float *y, int threads) {
+    f16_mv_ctx c = {w, x, n_rows, k_cols, m, y};
+    run_row_chunks(n_rows, threads, f16_mv_rows, &c);
+}
+
+/* ------------------------------------------------------------------------ */
+/* attention                                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* CPU/CpuBackend.java:1668-1748 for one (batch, query head) group. */
+static void attention_group(const float *q, const float *k, const float *v,
+                            const float *mask, float *out, int64_t group,
+                            int64_t key_group, int64_t sq, int64_t sk, int64_t d,
+                            float scale, int causal, double *weighted) {
+    int64_t q_base = group * sq * d;
+    int64_t k_base = key_group * sk * d;
+    for (int64_t qi = 0; qi < sq; qi++) {
+        for (int64_t j = 0; j < d; j++) weighted[j] = 0.0;
+        float running_max = -INFINITY;
+        double denominator = 0.0;
+        int64_t causal_limit = sk - sq + qi;
+        int64_t key_limit = causal ? (sk < causal_limit + 1 ? sk : causal_limit + 1) : sk;
+        for (int64_t ki = 0; ki < key_limit; ki++) {
+            float additive = mask ? mask[qi * sk + ki] : 0.0f;
+            if (additive == -INFINITY) continue;
+            float score = dot16(q + q_base + qi * d, k + k_base + ki * d, d) * scale + additive;
+            float next_max;
+            double previous_scale, current_scale;
+            if (isfinite(score)) {
+                if (score > running_max) {
+                    previous_scale = exp((double)(running_max - score));
+                    current_scale = 1.0;
+                    next_max = score;
+                } else {
+                    previous_scale = 1.0;
+                    current_scale = exp((double)(score - running_max));
+                    next_max = running_max;
+                }
+            } else {
+                next_max = running_max > score ? running_max : score;
+                if (isnan(running_max) || isnan(score)) next_max = NAN;
+                previous_scale = running_max == -INFINITY ? 0.0 : exp((double)(running_max - next_max));
+                current_scale = exp((double)(score - next_max));
+            }
+            denominator = denominator * previous_scale + current_scale;
+            for (int64_t j = 0; j < d; j++)
+                weighted[j] = weighted[j] * previous_scale + current_scale * (double)v[k_base + ki * d + j];
+            running_max = next_max;
+        }
+        for (int64_t j = 0; j < d; j++)
+            out[q_base + qi * d + j] = denominator == 0.0 ? 0.0f : (float)(weighted[j] / denominator);
+    }
+}
+
+int orc_attention_gqa(const float *q, const float *k, const float *v,
+                      const float *mask, int64_t b, int64_t hq, int64_t hkv,
+                      int64_t sq, int64_t sk, int64_t d, int causal,
+                      float *out, int threads) {
+    /* CPU/CpuBackend.java:1566-1587 shape and mask validation. */
+    if (b <= 0 || hq <= 0 || hkv <= 0 || sq <= 0 || sk <= 0 || d <= 0 || hq % hkv != 0) return -2;
+    if (mask) {
+        for (int64_t i = 0; i < sq * sk; i++)
+            if (isnan(mask[i]) || mask[i] == INFINITY) return -2;
+    }
+    float scale = (float)(1.0 / sqrt((double)d));
+    int64_t groups = b * hq;
+    int64_t per_kv = hq / hkv;
+    (void)threads;
+#ifdef _OPENMP
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+#endif
+    {
+        double *weighted = (double *)malloc((size_t)d * sizeof(double));
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (int64_t g = 0; g < groups; g++) {
+            int64_t head = g % hq;
+            int64_t kv_head = head / per_kv;
+            attention_group(q, k, v, mask, out, g, (g / hq) * hkv + kv_head, sq, sk, d,
+                            scale, causal, weighted);
+        }
+        free(weighted);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* decode-step element-wise ops                                              */
+/* ------------------------------------------------------------------------ */
+
+/* GLD/tensor/GGUFVectorOps.java:211-234: fused-multiply-add sum of squares in
+ * vector lanes (16 here), 1/sqrt in double, then (x * scale) * w. */
+void orc_rmsnorm(const float *x, const float *w, float *out, int32_t len, float eps) {
+    float lanes[16] = {0};
+    int32_t i = 0;
+    for (; i + 16 <= len; i += 16)
+        for (int l = 0; l < 16; l++) lanes[l] = fmaf(x[i + l], x[i + l], lanes[l]);
+    for (int s = 8; s >= 1; s >>= 1)
+        for (int l = 0; l < s; l++) lanes[l] += lanes[l + s];
+    float ss = lanes[0];
+    for (; i < len; i++) ss += x[i] * x[i];
+    float scale = 1.0f / (float)sqrt((double)(ss / (float)len + eps));
+    for (int32_t j = 0; j < len; j++) out[j] = (x[j] * scale) * w[j];
+}
+
+/* GLD/tensor/GGUFVectorOps.java:383-440 (no frequency factors, full rotary). */
+void orc_rope(float *x, int32_t n_heads, int32_t head_dim, int32_t pos, float base) {
+    int32_t half = head_dim / 2;
+    float *table = (float *)malloc((size_t)head_dim * sizeof(float));
+    for (int32_t i = 0; i < half; i++) {
+        float exponent = -2.0f * (float)i / (float)head_dim;
+        float inv_freq = (float)pow((double)base, (double)exponent);
+        float theta = ((float)pos * inv_freq) / 1.0f;
+        table[i] = (float)cos((double)theta);
+        table[half + i] = (float)sin((double)theta);
+    }
+    for (int32_t h = 0; h < n_heads; h++) {
+        float *p = x + (int64_t)h * head_dim;
+        for (int32_t i = 0; i < half; i++) {
+            float c = table[i], s = table[half + i];
+            float x0 = p[i], x1 = p[i + half];
+            p[i] = x0 * c - x1 * s;
+            p[i + half] = x0 * s + x1 * c;
+        }
+    }
+    free(table);
+}
+
+/* GLD/tensor/GGUFVectorOps.java:333-338 */
+void orc_swiglu(const float *gate, const float *up, float *dst, int32_t len) {
+    for (int32_t i = 0; i < len; i++) {
+        float g = gate[i] / (1.0f + (float)exp(-(double)gate[i]));
+        dst[i] = g * up[i];
+    }
+}
+
+/* GLD/tensor/GGUFVectorOps.java:302-317 */
+void orc_softmax(float *a, int32_t len) {
+    float mx = a[0];
+    for (int32_t i = 1; i < len; i++) if (a[i] > mx) mx = a[i];
+    float sum = 0.0f;
+    for (int32_t i = 0; i < len; i++) {
+        a[i] = (float)exp((double)(a[i] - mx));
+        sum += a[i];
+    }
+    float inv = 1.0f / sum;
+    for (int32_t i = 0; i < len; i++) a[i] *= inv;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Llama-shaped decode step                                                  */
+/* ------------------------------------------------------------------------ */
+
+static void nf4_mv(const uint8_t *codes, const float *absmax, int32_t group, const float *x,
+                   int64_t n, int64_t k, float *y, int threads) {
+    orc_nf4_matvec(codes, absmax, group, x, n, k, 1, y, threads);
+}
+
+/* GJB/GgufDecodePass.java:297-505 (per-op path, no optional norms/scales),
+ * GJB/GgufDecodeAttentionExecution.java:70-106 (per-head two-pass softmax),
+ * GJB/GgufLogitsProcessor.java:26-48 (final norm + LM head, no soft-cap). */
+int32_t orc_llama_decode(const orc_llama_cfg *cfg, const orc_llama_weights *w,
+                         int32_t token, int32_t pos, float *k_cache,
+                         float *v_cache, float *logits, float *hidden,
+                         int threads) {
+    const int32_t dim = cfg->dim, hd = cfg->head_dim, nh = cfg->n_heads, nkv = cfg->n_kv_heads;
+    const int32_t kvd = nkv * hd, qd = nh * hd, ffn = cfg->ffn, g = cfg->nf4_group;
+    float *x = hidden;
+    float *xb = (float *)malloc((size_t)dim * 4), *q = (float *)malloc((size_t)qd * 4);
+    float *kk = (float *)malloc((size_t)kvd * 4), *vv = (float *)malloc((size_t)kvd * 4);
+    float *att = (float *)malloc((size_t)qd * 4), *scores = (float *)malloc((size_t)(pos + 1) * 4);
+    float *gate = (float *)malloc((size_t)ffn * 4), *up = (float *)malloc((size_t)ffn * 4);
+    float *hb = (float *)malloc((size_t)ffn * 4);
+    memcpy(x, w->tok_embed + (int64_t)token * dim, (size_t)dim * 4);
+    float scale = (float)(1.0 / sqrt((double)hd));
+    for (int32_t l = 0; l < cfg->layers; l++) {
+        orc_rmsnorm(x, w->attn_norm[l], xb, dim, cfg->eps);
+        nf4_mv(w->wq[l], w->wq_s[l], g, xb, qd, dim, q, threads);
+        nf4_mv(w->wk[l], w->wk_s[l], g, xb, kvd, dim, kk, threads);
+        nf4_mv(w->wv[l], w->wv_s[l], g, xb, kvd, dim, vv, threads);
+        orc_rope(q, nh, hd, pos, cfg->rope_base);
+        orc_rope(kk, nkv, hd, pos, cfg->rope_base);
+        float *kc = k_cache + (int64_t)l * cfg->max_seq * kvd;
+        float *vc = v_cache + (int64_t)l * cfg->max_seq * kvd;
+        for (int32_t j = 0; j < kvd; j++) {
+            kc[(int64_t)pos * kvd + j] = cfg->kv_f16 ? orc_round_f16(kk[j]) : kk[j];
+            vc[(int64_t)pos * kvd + j] = cfg->kv_f16 ? orc_round_f16(vv[j]) : vv[j];
+        }
+        int32_t seq = pos + 1;
+        for (int32_t h = 0; h < nh; h++) {
+            int32_t kvh = h / (nh / nkv);
+            for (int32_t p = 0; p < seq; p++)
+                scores[p] = dot16(q + (int64_t)h * hd, kc + (int64_t)p * kvd + kvh * hd, hd) * scale;
+            orc_softmax(scores, seq);
+            float *o = att + (int64_t)h * hd;
+            for (int32_t j = 0; j < hd; j++) o[j] = 0.0f;
+            for (int32_t p = 0; p < seq; p++) {
+                const float *vr = vc + (int64_t)p * kvd + kvh * hd;
+                for (int32_t j = 0; j < hd; j++) o[j] += scores[p] * vr[j];
+            }
+        }
+        nf4_mv(w->wo[l], w->wo_s[l], g, att, dim, qd, xb, threads);
+        for (int32_t j = 0; j < dim; j++) x[j] += xb[j];
+        orc_rmsnorm(x, w->ffn_norm[l], xb, dim, cfg->eps);
+        nf4_mv(w->w_gate[l], w->w_gate_s[l], g, xb, ffn, dim, gate, threads);
+        nf4_mv(w->w_up[l], w->w_up_s[l], g, xb, ffn, dim, up, threads);
+        orc_swiglu(gate, up, hb, ffn);
+        nf4_mv(w->w_down[l], w->w_down_s[l], g, hb, dim, ffn, xb, threads);
+        for (int32_t j = 0; j < dim; j++) x[j] += xb[j];
+    }
+    orc_rmsnorm(x, w->out_norm, xb, dim, cfg->eps);
+    orc_f16_matvec(w->lm_head, xb, cfg->vocab, dim, 1, logits, threads);
+    int32_t best = 0;
+    for (int32_t i = 1; i < cfg->vocab; i++) if (logits[i] > logits[best]) best = i;
+    free(xb); free(q); free(kk); free(vv); free(att); free(scores); free(gate); free(up); free(hb);
+    return best;
+}
+
+/* IEEE binary16 round-to-nearest-even, returned widened to binary32. */
+float orc_round_f16(float v) {
+    uint32_t b = f32_to_bits(v);
+    uint32_t sign = b & 0x80000000u;
+    uint32_t a = b & 0x7fffffffu;
+    if (a >= 0x7f800000u) return v;                      /* inf / nan unchanged */
+    float f = bits_to_f32(a);
+    float r;
+    if (f >= 65520.0f) {
+        r = INFINITY;                                    /* rounds past the largest half */
+    } else if (f < 6.103515625e-05f) {
+        /* subnormal half: quantum 2^-24; nearbyint rounds half to even */
+        r = (float)(nearbyint((double)f * 16777216.0) / 16777216.0);
+    } else {
+        int e;
+        frexpf(f, &e);                                   /* f = m * 2^e, m in [0.5, 1) */
+        double q = ldexp(1.0, e - 11);                   /* half ulp spacing at this binade */
+        r = (float)(nearbyint((double)f / q) * q);
+    }
+    return bits_to_f32(f32_to_bits(r) | sign);
+}
+
+/* ------------------------------------------------------------------------ */
+/* generator                                                                 */
+/* ------------------------------------------------------------------------ */
+
+static inline uint64_t splitmix64(uint64_t *state) {
+    uint64_t z = (*state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static inline double unit_open(uint64_t *state) {
+    /* (0, 1]: never zero, so log() is finite. */
+    return ((double)(splitmix64(state) >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+}
+
+void orc_fill_normal(uint64_t seed, float mean, float std, float *out, int64_t n) {
+    uint64_t state = seed;
+    const double two_pi = 6.283185307179586476925286766559;
+    int64_t i = 0;
+    for (; i + 1 < n; i += 2) {
+        double r = sqrt(-2.0 * log(unit_open(&state)));
+        double t = two_pi * unit_open(&state);
+        out[i] = (float)(mean + std * r * cos(t));
+        out[i + 1] = (float)(mean + std * r * sin(t));
+    }
+    if (i < n) {
+        double r = sqrt(-2.0 * log(unit_open(&state)));
+        double t = two_pi * unit_open(&state);
+        out[i] = (float)(mean + std * r * cos(t));
+    }
+}
+
+void orc_fill_uniform_int(uint64_t seed, int32_t bound, int32_t *out, int64_t n) {
+    uint64_t state = seed;
+    for (int64_t i = 0; i < n; i++) out[i] = (int32_t)(splitmix64(&state) % (uint64_t)bound);
+}

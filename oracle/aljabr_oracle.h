@@ -1,0 +1,173 @@
+/*
+ * aljabr_oracle.h - CPU restatement of Aljabr's quantized-inference hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP path and
+ * the timed CPU baseline in bench.py. Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg may load it; the product (aljabr_amd/) never
+ * links, loads or falls back to it.
+ *
+ * Every function names the reference file:line it restates. Paths are relative
+ * to the andalus-ai/aljabr tree:
+ *   STC = engine/safetensor/aljabr-safetensor-core/src/main/java/tech/kayys/aljabr/safetensor/core/tensor
+ *   GRT = engine/gguf/aljabr-gguf-core/src/main/java/tech/kayys/aljabr/gguf/runtime
+ *   GWR = engine/gguf/aljabr-gguf-core/src/main/java/tech/kayys/aljabr/gguf/writer
+ *   GLD = engine/gguf/aljabr-gguf-core/src/main/java/tech/kayys/aljabr/gguf/loader
+ *   CPU = backend/cpu/aljabr-backend-cpu/src/main/java/tech/kayys/aljabr/backend/cpu
+ *   GJB = engine/gguf/aljabr-gguf-java/src/main/java/tech/kayys/aljabr/gguf/javabackend
+ *
+ * Parity status per function (what pins it) is listed beside each prototype.
+ */
+#ifndef ALJABR_ORACLE_H
+#define ALJABR_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar conversions ------------------------------------------------ */
+
+/* GRT/GgufQuantTables.java:143-165 (f16ToF32Slow). Pinned: exhaustive 65536
+ * comparison with the IEEE binary16 definition (numpy float16). */
+float orc_f16_to_f32(uint16_t h);
+
+/* GWR/GGUFWriter.java:360-387 (floatToHalfBits, round-half-up at bit 12).
+ * Pinned: closed-form cases (exact halves, ties, subnormals, overflow). */
+uint16_t orc_f32_to_f16_writer(float v);
+
+/* java.lang.Math.round(float): nearest int, ties toward +inf, NaN -> 0,
+ * saturating. Pinned: ties, negative ties, 0.49999997f. */
+int32_t orc_java_round(float v);
+
+/* ---- NF4 ---------------------------------------------------------------- */
+
+/* STC/DequantizationKernel.java:23-28 */
+extern const float ORC_NF4_TABLE[16];
+
+/* STC/DequantizationKernel.java:84-102. Byte j holds element 2j in the high
+ * nibble and 2j+1 in the low nibble; the scale index is (2j)/groupSize over the
+ * flat element index. Pinned: closed form (one fp32 multiply) and the special
+ * cases code 7 -> 0, codes 0/15 -> -/+absmax. */
+void orc_nf4_dequant(const uint8_t *codes, const float *absmax, int64_t numel,
+                     int32_t group_size, float *dst);
+
+/* NF4 encoder. The reference's quantizer is absent from its tree (the BnB
+ * adapter moved out), so this is build-defined: per-group absmax, value/absmax
+ * rounded to the nearest codebook level, exact midpoint -> lower code.
+ * PARITY UNPINNED against the reference; pinned only by the invariant
+ * decode(encode(w)) == nearest level * absmax. */
+void orc_nf4_quantize(const float *w, int64_t numel, int32_t group_size,
+                      uint8_t *codes, float *absmax);
+
+/* NF4 linear y[m,n] = sum_k x[m,k] * W[n,k], W = dequantized NF4 (fp32),
+ * restating STC/AccelOps.java:392-463 (JIT dequant then an fp32 GEMV/GEMM).
+ * The GEMV itself is Apple Accelerate there (third-party, absent); this uses a
+ * 16-lane fp32 dot per row. Pinned against a float64 brute force in tests. */
+void orc_nf4_matvec(const uint8_t *codes, const float *absmax, int32_t group_size,
+                    const float *x, int64_t n_rows, int64_t k_cols, int32_t m,
+                    float *y, int threads);
+
+/* ---- GGUF Q4_0 / Q8_0 --------------------------------------------------- */
+
+/* GWR/GGUFWriter.java:179-209 (encodeQ4_0, quantize4, maxAbs). numel % 32 == 0. */
+void orc_q4_0_quantize(const float *w, int64_t numel, uint8_t *out);
+/* GWR/GGUFWriter.java:163-177 (encodeQ8_0). numel % 32 == 0. */
+void orc_q8_0_quantize(const float *w, int64_t numel, uint8_t *out);
+
+/* GRT/GgufBlockDequantizer.java:33-37,366-416 (low nibble -> j, high -> j+16,
+ * (q-8)*d + 0.0f). Pinned: GgufQ32Test/GgufNibFx known answers. */
+void orc_q4_0_dequant(const uint8_t *blocks, int64_t numel, float *dst);
+/* GRT/GgufBlockDequantizer.java:231-265 (int8 * d). Pinned: GgufQ8Test. */
+void orc_q8_0_dequant(const uint8_t *blocks, int64_t numel, float *dst);
+
+/* GRT/GgufQ32RawDot.java:34-67,342-349,428-463: four block accumulators, four
+ * intra-block lane partials, same fp32 operation order. */
+float orc_q4_0_dot_row(const uint8_t *row, int32_t columns, const float *x);
+/* GRT/GgufQ8RawDot.java:138-185,784-830 (scalar path). */
+float orc_q8_0_dot_row(const uint8_t *row, int32_t columns, const float *x);
+
+/* Row-parallel matvec / batched matvec: y[m*N + n] = dot(row n, x[m*K ...]).
+ * Row chunks = min(rows, 2*threads) as GRT/GgufParallelConfig.java:64-73. */
+void orc_q4_0_matvec(const uint8_t *w, const float *x, int64_t n_rows,
+                     int64_t k_cols, int32_t m, float *y, int threads);
+void orc_q8_0_matvec(const uint8_t *w, const float *x, int64_t n_rows,
+                     int64_t k_cols, int32_t m, float *y, int threads);
+
+/* fp16 rows (LM head): GRT/GgufDenseRows.java:70-90. */
+void orc_f16_matvec(const uint16_t *w, const float *x, int64_t n_rows,
+                    int64_t k_cols, int32_t m, float *y, int threads);
+
+/* ---- attention ---------------------------------------------------------- */
+
+/* CPU/CpuBackend.java:1546-1748 (attentionGqa + computeAttentionGroup):
+ * Q[B,Hq,Sq,D], K/V[B,Hkv,Sk,D] fp32, optional additive mask [Sq,Sk], causal
+ * bottom-right alignment, online softmax with double denominators and double
+ * weighted values. Returns 0, or -2 on invalid shapes/mask (the reference's
+ * IllegalArgumentException). Pinned: CpuBatchedAttentionTest and
+ * CpuBackendStorageTest known answers. */
+int orc_attention_gqa(const float *q, const float *k, const float *v,
+                      const float *mask, int64_t b, int64_t hq, int64_t hkv,
+                      int64_t sq, int64_t sk, int64_t d, int causal,
+                      float *out, int threads);
+
+/* ---- decode-step element-wise ops --------------------------------------- */
+
+/* GLD/tensor/GGUFVectorOps.java:211-234 */
+void orc_rmsnorm(const float *x, const float *w, float *out, int32_t len, float eps);
+/* GLD/tensor/GGUFVectorOps.java:383-440 (split-half, fp32 table). */
+void orc_rope(float *x, int32_t n_heads, int32_t head_dim, int32_t pos, float base);
+/* GLD/tensor/GGUFVectorOps.java:333-338 */
+void orc_swiglu(const float *gate, const float *up, float *dst, int32_t len);
+/* GLD/tensor/GGUFVectorOps.java:302-317 */
+void orc_softmax(float *a, int32_t len);
+
+/* ---- Llama-shaped decode step ------------------------------------------- */
+
+typedef struct orc_llama_cfg {
+    int32_t layers, dim, ffn, n_heads, n_kv_heads, head_dim, vocab, max_seq;
+    int32_t nf4_group;
+    int32_t kv_f16;      /* 1: K/V rounded to binary16 (nearest-even) when stored */
+    float rope_base, eps;
+} orc_llama_cfg;
+
+/* Weights for one model, all host pointers. Per-layer arrays are indexed by
+ * layer. Projection weights are NF4 [out, in]; the LM head is fp16
+ * [vocab, dim]; embeddings fp32 [vocab, dim]. */
+typedef struct orc_llama_weights {
+    const float *tok_embed;
+    const float *const *attn_norm;
+    const float *const *ffn_norm;
+    const uint8_t *const *wq, *const *wk, *const *wv, *const *wo;
+    const float *const *wq_s, *const *wk_s, *const *wv_s, *const *wo_s;
+    const uint8_t *const *w_gate, *const *w_up, *const *w_down;
+    const float *const *w_gate_s, *const *w_up_s, *const *w_down_s;
+    const float *out_norm;
+    const uint16_t *lm_head;
+} orc_llama_weights;
+
+/* One decode position for one sequence, GJB/GgufDecodePass.java:297-505 and
+ * GJB/GgufLogitsProcessor.java:26-48: the KV caches are fp32 [layers][max_seq]
+ * [n_kv_heads*head_dim]. Writes logits[vocab] and the final hidden state
+ * x[dim]; returns the greedy token. */
+int32_t orc_llama_decode(const orc_llama_cfg *cfg, const orc_llama_weights *w,
+                         int32_t token, int32_t pos, float *k_cache,
+                         float *v_cache, float *logits, float *hidden,
+                         int threads);
+
+/* binary32 -> binary16 -> binary32 with round-to-nearest-even (IEEE). */
+float orc_round_f16(float v);
+
+/* ---- deterministic generator -------------------------------------------- */
+
+/* SplitMix64 -> Box-Muller (build-defined): out[i] = mean + std * N(0,1). */
+void orc_fill_normal(uint64_t seed, float mean, float std, float *out, int64_t n);
+/* SplitMix64 -> uniform integers in [0, bound). */
+void orc_fill_uniform_int(uint64_t seed, int32_t bound, int32_t *out, int64_t n);
+
+int orc_max_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

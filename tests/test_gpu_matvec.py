@@ -1,0 +1,128 @@
+"""GPU parity for the dequant-fused matvec / small-M GEMM (NF4, GGUF Q4_0 and
+Q8_0, fp16 rows) against the oracle on identical seeded inputs. Tolerance:
+relative L2 <= 1e-3 (fp32 outputs), the bar BASELINE.json sets."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+# (N, K): square, gate/up (14336x4096) and down (4096x14336) Llama-3-8B shapes,
+# plus small and ragged shapes.
+SHAPES = [(64, 128), (96, 2080), (4096, 4096), (14336, 4096), (4096, 14336)]
+
+
+def _nf4_case(oracle, n, k, group=64, seed=1):
+    w = oracle.normal(seed * 7919 + n + k, n * k, 0.0, 0.02)
+    codes, absmax = oracle.nf4_quantize(w, group)
+    return codes, absmax
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("m", [1, 4, 16, 64])
+def test_nf4_matvec(rocm, dev, oracle, n, k, m):
+    if m > 4 and n * k > 4096 * 4096 and m != 64:
+        pytest.skip("covered by m=64 at this size")
+    codes, absmax = _nf4_case(oracle, n, k)
+    x = oracle.normal(11 + m, m * k)
+    y_ref = oracle.nf4_matvec(codes, absmax, x, n, k, 64)
+    c, a, xd = dev.put(codes), dev.put(absmax), dev.put(x)
+    y = dev.empty(m * n)
+    rocm.call("aljabr_rocm_matvec_tb_batch_nf4", dev.ptr(y), dev.ptr(xd), dev.ptr(c), dev.ptr(a), k, n, 64, m)
+    assert rel_l2(dev.get(y), y_ref) <= TOL
+
+
+@pytest.mark.parametrize("group", [32, 128, 6])
+def test_nf4_other_block_sizes(rocm, dev, oracle, group):
+    n, k = 48, 384
+    codes, absmax = _nf4_case(oracle, n, k, group)
+    x = oracle.normal(5, k)
+    y_ref = oracle.nf4_matvec(codes, absmax, x, n, k, group)
+    c, a, xd = dev.put(codes), dev.put(absmax), dev.put(x)
+    y = dev.empty(n)
+    rocm.call("aljabr_rocm_matvec_tb_nf4", dev.ptr(y), dev.ptr(xd), dev.ptr(c), dev.ptr(a), k, n, group)
+    assert rel_l2(dev.get(y), y_ref) <= TOL
+
+
+def test_nf4_ragged_k_uses_generic_path(rocm, dev, oracle):
+    n, k = 33, 202                                         # K not a multiple of 32, odd row count
+    codes, absmax = _nf4_case(oracle, n, k, 64)
+    x = oracle.normal(8, 2 * k)
+    y_ref = oracle.nf4_matvec(codes, absmax, x, n, k, 64)
+    c, a, xd = dev.put(codes), dev.put(absmax), dev.put(x)
+    y = dev.empty(2 * n)
+    rocm.call("aljabr_rocm_matvec_tb_batch_nf4", dev.ptr(y), dev.ptr(xd), dev.ptr(c), dev.ptr(a), k, n, 64, 2)
+    assert rel_l2(dev.get(y), y_ref) <= TOL
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("n,k", [(64, 128), (7, 160), (4096, 4096), (14336, 4096)])
+@pytest.mark.parametrize("m", [1, 8, 16])
+def test_gguf_matvec(rocm, dev, oracle, qtype, n, k, m):
+    qt, ot = {"q4_0": (rocm.TYPE_Q4_0, oracle.QTYPE_Q4_0), "q8_0": (rocm.TYPE_Q8_0, oracle.QTYPE_Q8_0)}[qtype]
+    w = oracle.normal(31 + n + k, n * k, 0.0, 0.02)
+    enc = oracle.quantize(ot, w)
+    x = oracle.normal(37 + m, m * k)
+    y_ref = oracle.q_matvec(ot, enc, x, n, k)
+    wd, xd = dev.put(enc), dev.put(x)
+    y = dev.empty(m * n)
+    rocm.call("aljabr_rocm_matvec_tb_batch", dev.ptr(y), dev.ptr(xd), dev.ptr(wd), k, n, qt, m)
+    assert rel_l2(dev.get(y), y_ref) <= TOL
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+def test_gguf_reference_known_rows(rocm, dev, oracle, qtype):
+    import json, os
+    kats = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")))
+    k = kats["q4_0_rows" if qtype == "q4_0" else "q8_0_rows"]
+    entry = "aljabr_rocm_matvec_tb_q4_0" if qtype == "q4_0" else "aljabr_rocm_matvec_tb_q8_0"
+    wd = dev.put(np.array(k["blocks"], np.uint8))
+    xd = dev.put(np.ones(32, np.float32))
+    y = dev.empty(2)
+    rocm.call(entry, dev.ptr(y), dev.ptr(xd), dev.ptr(wd), 32, 2)
+    assert list(dev.get(y)) == k["dot_ones"]
+
+
+@pytest.mark.parametrize("n,k,m", [(50, 136, 1), (4096, 4096, 1), (128256 // 8, 4096, 2), (300, 4096, 32)])
+def test_f16_rows(rocm, dev, oracle, n, k, m):
+    w = oracle.normal(41 + n, n * k).astype(np.float16).view(np.uint16)
+    x = oracle.normal(43, m * k)
+    y_ref = oracle.f16_matvec(w, x, n, k)
+    wd, xd = dev.put(w), dev.put(x)
+    y = dev.empty(m * n)
+    rocm.call("aljabr_rocm_matvec_tb_batch", dev.ptr(y), dev.ptr(xd), dev.ptr(wd), k, n, rocm.TYPE_F16, m)
+    assert rel_l2(dev.get(y), y_ref) <= TOL
+
+
+def test_batched_equals_repeated_single_rows(rocm, dev, oracle):
+    """M-batched output equals M independent matvecs (the invariant the Metal
+    batch test asserts, MetalTripleBatchCorrectnessTest.java:44-100)."""
+    n, k, m = 512, 1024, 5
+    codes, absmax = _nf4_case(oracle, n, k)
+    x = oracle.normal(99, m * k)
+    c, a, xd = dev.put(codes), dev.put(absmax), dev.put(x)
+    yb = dev.empty(m * n)
+    rocm.call("aljabr_rocm_matvec_tb_batch_nf4", dev.ptr(yb), dev.ptr(xd), dev.ptr(c), dev.ptr(a), k, n, 64, m)
+    batched = dev.get(yb).reshape(m, n)
+    for i in range(m):
+        xi = dev.put(x[i * k:(i + 1) * k])
+        yi = dev.empty(n)
+        rocm.call("aljabr_rocm_matvec_tb_nf4", dev.ptr(yi), dev.ptr(xi), dev.ptr(c), dev.ptr(a), k, n, 64)
+        assert rel_l2(batched[i], dev.get(yi)) <= 2e-3
+
+
+def test_matvec_argument_errors(rocm, dev):
+    y = dev.empty(64)
+    with pytest.raises(rocm.RocmError) as e:
+        rocm.call("aljabr_rocm_matvec_tb_q4_0", dev.ptr(y), dev.ptr(y), dev.ptr(y), 48, 1)
+    assert e.value.status == rocm.ERR_BAD_ARGUMENT
+    with pytest.raises(rocm.RocmError) as e:
+        rocm.call("aljabr_rocm_matvec_tb_batch", dev.ptr(y), dev.ptr(y), dev.ptr(y), 32, 1, 12, 1)
+    assert e.value.status == rocm.ERR_UNSUPPORTED
+    with pytest.raises(rocm.RocmError) as e:
+        rocm.call("aljabr_rocm_matvec_tb_nf4", dev.ptr(y), dev.ptr(y), dev.ptr(y), dev.ptr(y), 64, 1, 7)
+    assert e.value.status == rocm.ERR_BAD_ARGUMENT
