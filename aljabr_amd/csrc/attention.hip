@@ -75,7 +75,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
     const int grp = wave * GPW + lane / LPK;   // key group in workgroup
     const int sub = lane % LPK;                // 8-dim slice of the row
 
-    const int sk = p.kv_len ? p.kv_len[b] : p.Sk;
+    const int sk = p.kv_len ? min(max(p.kv_len[b], 0), p.cap) : p.Sk;   // never past the cache
     int limit = sk;
     if (p.causal) {
         const int c = sk - p.Sq + qi + 1;
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(AttnParams p) {
     const int h = static_cast<int>((idx / p.Sq) % p.Hq);
     const int b = static_cast<int>(idx / (static_cast<long long>(p.Sq) * p.Hq));
     const int kvh = h / (p.Hq / p.Hkv);
-    const int sk = p.kv_len ? p.kv_len[b] : p.Sk;
+    const int sk = p.kv_len ? min(max(p.kv_len[b], 0), p.cap) : p.Sk;   // never past the cache
     int limit = sk;
     if (p.causal) {
         const int c = sk - p.Sq + qi + 1;

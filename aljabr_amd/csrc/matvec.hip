@@ -408,7 +408,7 @@ int enqueue_gguf_small(float *C, const float *A, const uint8_t *B, int K, int N,
         ALJ_DISPATCH_MR(q8_0_matvec_kernel, M, R, grid, C, A, B, N, K);
     } else {
         const uint16_t *W = reinterpret_cast<const uint16_t *>(B);
-        if (K % 8 == 0 && aligned(B, 16)) {
+        if (K % 8 == 0 && aligned(B, 16) && aligned(A, 16)) {
             ALJ_DISPATCH_MR(f16_matvec_kernel, M, R, grid, C, A, W, N, K);
         } else {
             hipLaunchKernelGGL(f16_matvec_generic_kernel, dim3(grid_for(N * M)), dim3(kThreads), 0, s, C, A, W, N, K,

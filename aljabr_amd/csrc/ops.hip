@@ -132,6 +132,7 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(uint16_t *__restric
     const int b = blockIdx.y;
     const int i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= n_kv * head_dim) return;
+    if (pos[b] < 0 || pos[b] >= cap) return;   // outside the cache: nothing to store
     const int h = i / head_dim, d = i % head_dim;
     const _Float16 v = static_cast<_Float16>(src[static_cast<long long>(b) * n_kv * head_dim + i]);
     cache[((static_cast<long long>(b) * n_kv + h) * cap + pos[b]) * head_dim + d] = __builtin_bit_cast(uint16_t, v);
