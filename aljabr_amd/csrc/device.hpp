@@ -10,6 +10,13 @@ namespace aljabr {
 
 constexpr int kWave = 64;
 
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (nontemporal hint: weights are read once per call).
+__device__ __forceinline__ u32x4 load_stream16(const void *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
+
 // DPP-modified move: lanes outside row_mask keep `old` (0 here).
 template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
 __device__ __forceinline__ float dpp_f32(float v) {
@@ -123,6 +130,20 @@ __device__ __forceinline__ float nf4_level(int c) {
         0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
         0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
     return t[c];
+}
+
+// Same value without a memory read (a select chain on the lane's index), for
+// kernels whose prologue must not wait on a constant-table load.
+__device__ __forceinline__ float nf4_level_sel(int c) {
+    constexpr float t[16] = {
+        -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+        -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+        0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+        0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+    float v = t[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) v = c == i ? t[i] : v;
+    return v;
 }
 
 }  // namespace aljabr

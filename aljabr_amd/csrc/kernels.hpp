@@ -24,6 +24,17 @@ int enqueue_attention(const AttnParams &p);
 // C[M][N] = A[M][K] . W[N][K]^T for any M (slices or MFMA chosen inside).
 int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M);
 int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M);
+// K-split tile kernels for M <= 2 (ALJABR_ROCM_ERR_UNSUPPORTED when the shape
+// or alignment does not fit them; nothing is enqueued then).
+int enqueue_nf4_tile(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
+                     int M);
+int enqueue_gguf_tile(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M);
+// Batch-1 NF4 kernel: T rows per workgroup, one wave per 2048-element K
+// chunk (K <= 16384, K % 32 == 0, block size >= 32).
+int enqueue_nf4_rows(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift);
+// Persistent double-buffered batch-1 kernels (K <= 16384).
+int enqueue_nf4_stream(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift);
+int enqueue_gguf_stream(float *C, const float *A, const uint8_t *B, int K, int N, int type);
 // Small-M (M <= 8) wavefront-reduction kernels.
 int enqueue_nf4_small(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M);
 int enqueue_gguf_small(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M);

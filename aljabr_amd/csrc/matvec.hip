@@ -390,6 +390,8 @@ int enqueue_nf4_small(float *C, const float *A, const uint8_t *Bq, const float *
                            N, K, M, bs);
         return ALJABR_ROCM_OK;
     }
+    if (M == 1 && enqueue_nf4_rows(C, A, Bq, absmax, K, N, shift) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
+    if (enqueue_nf4_tile(C, A, Bq, absmax, K, N, shift, M) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
     const int R = M == 1 ? pick_rows(N) : 1;
     const dim3 grid(grid_for((N + R - 1) / R));
     ALJ_DISPATCH_MR(nf4_matvec_kernel, M, R, grid, C, A, Bq, absmax, N, K, shift);
@@ -400,6 +402,8 @@ int enqueue_gguf_small(float *C, const float *A, const uint8_t *B, int K, int N,
     hipStream_t s = current_stream();
     if (type != ALJABR_ROCM_TYPE_F16 && (!aligned(A, 16) || !aligned(B, 4)))
         return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "GGUF matvec needs A 16-byte and B 4-byte aligned");
+    if (M == 1 && enqueue_gguf_stream(C, A, B, K, N, type) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
+    if (enqueue_gguf_tile(C, A, B, K, N, type, M) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
     const int R = M == 1 ? pick_rows(N) : 1;
     const dim3 grid(grid_for((N + R - 1) / R));
     if (type == ALJABR_ROCM_TYPE_Q4_0) {

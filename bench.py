@@ -25,6 +25,7 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 K_MODEL, FFN = 4096, 14336
 BLOCK = 64
+KERNEL = "nf4_rows_kernel"          # the batch-1 NF4 kernel these launches dispatch to
 
 
 def nf4_bytes(n: int, k: int, m: int = 1) -> int:
@@ -46,6 +47,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--decode-steps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 256 MiB device copy 20 times (FETCH_SIZE/WRITE_SIZE calibration)")
     return ap.parse_args()
 
 
@@ -121,6 +124,31 @@ def cpu_baseline(seconds: float):
                       f"{dt:.1f} s, oracle C restatement, OpenMP row chunks = 2 x {threads} threads"}
 
 
+def traffic_record(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor), or
+    None when no summary for this kernel is committed."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return int(rec["bytes_per_launch"]) if rec else None
+
+
+def copy_probe(torch, stream) -> None:
+    """A plain device copy of known size, for calibrating the HBM counters."""
+    n = 64 << 20                                   # 64 Mi floats = 256 MiB each way
+    a = torch.randn(n, device="cuda:0")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(20):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_each_way": 4 * n, "launches": 20}), flush=True)
+
+
 def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, weights, cfg):
     from aljabr_amd.llama import DeviceLlama
     max_seq = ctx + steps + 8
@@ -175,7 +203,10 @@ def main() -> None:
     abi.call("aljabr_rocm_set_stream", stream.cuda_stream)
     abi.call("aljabr_rocm_set_sync_mode", 0)
     with torch.cuda.stream(stream):
-        run(args, abi, torch, stream)
+        if args.copy_probe:
+            copy_probe(torch, stream)
+        else:
+            run(args, abi, torch, stream)
 
 
 def run(args, abi, torch, stream) -> None:
@@ -204,16 +235,17 @@ def run(args, abi, torch, stream) -> None:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "nf4->f32",
+        "dtype": "f32",
         "data": "synthetic: NF4 weights quantized on device from N(0,0.02), x ~ N(0,1), "
                 f"{copies} rotating weight copies ({copies * step_bytes / 1e6:.0f} MB)",
         "config": {"workload": "nf4_mlp_matvec_llama3_8b_batch1",
                    "shapes": ["14336x4096", "14336x4096", "4096x14336"], "nf4_block": BLOCK,
+                   "weights": "nf4 codes + fp32 absmax", "activations": "f32",
                    "batch": 1, "parallelism": "none (1 GPU)"},
         "pct_peak_hbm": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "nf4_matvec_kernel", "bytes_per_launch": per_launch_bytes,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_record(KERNEL),
+                     "kernel": KERNEL, "bytes_per_launch": per_launch_bytes,
                      "avg_launch_us": round(per_launch_ms * 1e3, 3)},
     }
 
