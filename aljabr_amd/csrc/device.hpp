@@ -50,6 +50,54 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Value of lane (lane ^ MASK): DPP quad permutes for 1 and 2, ds_swizzle
+// (bit mode, within 32 lanes) for 4, 8 and 16, ds_bpermute for 32.
+template <int MASK>
+__device__ __forceinline__ float lane_xor(float v) {
+    if constexpr (MASK == 1) return dpp_f32<0xB1>(v);      // quad_perm [1,0,3,2]
+    else if constexpr (MASK == 2) return dpp_f32<0x4E>(v); // quad_perm [2,3,0,1]
+    else if constexpr (MASK == 32) return __shfl_xor(v, 32);
+    else return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (MASK << 10) | 0x1F));
+}
+
+// Butterfly sum of T = 2^t per-lane values (T <= 16) over the wave: stage s
+// pairs each lane with lane ^ 2^s and keeps half of the values, so the whole
+// reduction costs ~3T/2 + 6 operations instead of T separate wave sums. On
+// return every lane holds the total of row wave_rows_index<T>(lane).
+template <int MASK, int N>
+__device__ __forceinline__ void fold_rows_stage(float *v, bool upper) {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+        const float lo = v[i], hi = v[i + N / 2];
+        v[i] = (upper ? hi : lo) + lane_xor<MASK>(upper ? lo : hi);
+    }
+}
+
+template <int T>
+__device__ __forceinline__ int wave_rows_index(int lane) {
+    static_assert(T == 1 || T == 2 || T == 4 || T == 8 || T == 16, "T must be a power of two <= 16");
+    int r = 0;
+    for (int s = 0; (1 << s) < T; ++s) r = (r << 1) | ((lane >> s) & 1);
+    return r;
+}
+
+template <int T>
+__device__ __forceinline__ float wave_sum_rows(float (&v)[T]) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (T >= 2) fold_rows_stage<1, T>(v, lane & 1);
+    if constexpr (T >= 4) fold_rows_stage<2, T / 2>(v, lane & 2);
+    if constexpr (T >= 8) fold_rows_stage<4, T / 4>(v, lane & 4);
+    if constexpr (T >= 16) fold_rows_stage<8, T / 8>(v, lane & 8);
+    float r = v[0];
+    if constexpr (T < 2) r += lane_xor<1>(r);
+    if constexpr (T < 4) r += lane_xor<2>(r);
+    if constexpr (T < 8) r += lane_xor<4>(r);
+    if constexpr (T < 16) r += lane_xor<8>(r);
+    r += lane_xor<16>(r);
+    r += lane_xor<32>(r);
+    return r;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     v = row16_max(v);
     float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));

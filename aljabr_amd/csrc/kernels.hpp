@@ -30,8 +30,13 @@ int enqueue_nf4_tile(float *C, const float *A, const uint8_t *Bq, const float *a
                      int M);
 int enqueue_gguf_tile(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M);
 // Batch-1 NF4 kernel: T rows per workgroup, one wave per 2048-element K
-// chunk (K <= 16384, K % 32 == 0, block size >= 32).
+// chunk (K <= 16384, K % 2048 == 0, block size >= 32).
 int enqueue_nf4_rows(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift);
+// Batch-1 NF4/Q4_0/Q8_0 kernel with a 256-entry pair table for 4-bit codes
+// (K % 2048 == 0, K <= 16384; NF4 block size >= 32, 16-byte aligned codes;
+// GGUF rows 4-byte aligned). `type` is an ALJABR_ROCM_TYPE_* id.
+int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax, int K, int N, int type,
+                 int bs_shift);
 // Persistent double-buffered batch-1 kernels (K <= 16384).
 int enqueue_nf4_stream(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift);
 int enqueue_gguf_stream(float *C, const float *A, const uint8_t *B, int K, int N, int type);

@@ -378,6 +378,16 @@ int log2_exact(int v) {
 
 }  // namespace
 
+// Batch-1 kernel family: 0 (default) = pair-table rows kernels, 1 = the
+// earlier per-format kernels (ALJABR_ROCM_BATCH1=1, kept for comparison).
+int batch1_kernel() {
+    static const int v = [] {
+        const char *e = getenv("ALJABR_ROCM_BATCH1");
+        return e && *e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
 // Enqueue C[M][N] for M <= 8 (no sync); used by the entry points and the
 // decode driver. Returns a status.
 int enqueue_nf4_small(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs,
@@ -390,6 +400,9 @@ int enqueue_nf4_small(float *C, const float *A, const uint8_t *Bq, const float *
                            N, K, M, bs);
         return ALJABR_ROCM_OK;
     }
+    if (M == 1 && batch1_kernel() != 1 &&
+        enqueue_rows(C, A, Bq, absmax, K, N, ALJABR_ROCM_TYPE_NF4, shift) == ALJABR_ROCM_OK)
+        return ALJABR_ROCM_OK;
     if (M == 1 && enqueue_nf4_rows(C, A, Bq, absmax, K, N, shift) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
     if (enqueue_nf4_tile(C, A, Bq, absmax, K, N, shift, M) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
     const int R = M == 1 ? pick_rows(N) : 1;
@@ -402,6 +415,9 @@ int enqueue_gguf_small(float *C, const float *A, const uint8_t *B, int K, int N,
     hipStream_t s = current_stream();
     if (type != ALJABR_ROCM_TYPE_F16 && (!aligned(A, 16) || !aligned(B, 4)))
         return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "GGUF matvec needs A 16-byte and B 4-byte aligned");
+    if (M == 1 && type != ALJABR_ROCM_TYPE_F16 && batch1_kernel() != 1 &&
+        enqueue_rows(C, A, B, nullptr, K, N, type, 0) == ALJABR_ROCM_OK)
+        return ALJABR_ROCM_OK;
     if (M == 1 && enqueue_gguf_stream(C, A, B, K, N, type) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
     if (enqueue_gguf_tile(C, A, B, K, N, type, M) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
     const int R = M == 1 ? pick_rows(N) : 1;

@@ -13,11 +13,12 @@
 // every outstanding load at a loop back-edge, so the T rows of a workgroup
 // are unrolled, with the loads of row t+PF issued before row t is computed.
 //
-// Workgroup = S waves (S = ceil(K/2048)); wave w owns K chunk w (32 weights,
+// Workgroup = S waves (S = K/2048); wave w owns K chunk w (32 weights,
 // 16 code bytes, per lane) for rows [row0, row0+T). Codebook lookups read the
 // fp32 level from LDS byte address nibble*4: one shift and one mask per four
-// nibbles pre-scale them, one v_bfe_u32 extracts each address. After T rows,
-// the S wave partials of each row meet in LDS once.
+// nibbles pre-scale them, one v_bfe_u32 extracts each address. After T rows
+// one butterfly reduces all T row sums across the wave, and the S wave
+// partials of each row meet in LDS once.
 #include "device.hpp"
 #include "internal.hpp"
 #include "kernels.hpp"
@@ -69,77 +70,54 @@ __global__ __launch_bounds__(kMaxWaves * 64) void nf4_rows_kernel(float *__restr
     static_assert(T <= 16 && PF >= 1, "tile shape");
     __shared__ float lut_f[16];
     __shared__ float part[kMaxWaves][16];
-    extern __shared__ float4 xstage[];           // 256 float4 (4 KiB) per wave
+    extern __shared__ float4 xstage[];           // 512 float4 (8 KiB) per wave
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int S = blockDim.x >> 6;
     const int row0 = blockIdx.x * T;
-    const int k0 = wave * kChunk + lane * 32;
-    const bool active = k0 < K;
-    const int kc = min(k0, K - 32);              // inactive lanes load a valid word, weighted 0
+    const int k0 = wave * kChunk + lane * 32;    // K % 2048 == 0: every lane is in range
     const size_t row_bytes = static_cast<size_t>(K) >> 1;
 
-    // Per-row load addresses; rows past N re-read row N-1 (results dropped).
-    // Everything below is branch-free so the loads stay in issue order.
-    const uint8_t *qp = codes + (kc >> 1);
-    const size_t sidx = static_cast<size_t>(kc);
-    u32x4 q[T];
-    float sc[T];
     // Activations: lane L needs floats [32L, 32L+32) of the wave's chunk.
-    // Coalesced float4 loads (float4 f = 64j + lane) are transposed through a
-    // 4 KiB per-wave LDS window in two halves (lanes 0-31, then 32-63); local
-    // float4 g is stored at slot (g/8)*8 + ((g%8) ^ ((g/8)%8)), so both the
-    // stores and the 8 ds_read_b128 per lane are bank-conflict free.
-    const int chunk_f4 = min(kChunk, K - wave * kChunk) >> 2;
+    // Coalesced float4 loads (float4 f = 64j + lane) are transposed through
+    // the wave's LDS window; float4 f is stored at slot (f/8)*8 + ((f%8) ^
+    // ((f/8)%8)), so both the stores and the 8 ds_read_b128 per lane are
+    // bank-conflict free. Activation loads go out first: vmcnt retires in
+    // order, so waiting for them leaves the weight loads below in flight.
     const float4 *xw = reinterpret_cast<const float4 *>(x + wave * kChunk);
     float4 xl[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int f = 64 * j + lane;
-        const float4 v = xw[min(f, chunk_f4 - 1)];
-        const bool in = f < chunk_f4;
-        xl[j] = make_float4(in ? v.x : 0.0f, in ? v.y : 0.0f, in ? v.z : 0.0f, in ? v.w : 0.0f);
-    }
-    // The first PF rows of weights are in flight during the staging below.
-    // Activation loads are issued first: vmcnt retires in order, so waiting
-    // for them then leaves the weight loads outstanding.
+    for (int j = 0; j < 8; ++j) xl[j] = xw[64 * j + lane];
+
+    // Per-row load addresses; rows past N re-read row N-1 (results dropped).
+    // Everything below is branch-free so the loads stay in issue order.
+    const uint8_t *qp = codes + (k0 >> 1);
+    u32x4 q[T];
+    float sc[T];
 #pragma unroll
     for (int t = 0; t < PF && t < T; ++t) {
         const int row = min(row0 + t, N - 1);
         q[t] = load_stream16(qp + row * row_bytes);
-        sc[t] = absmax[(static_cast<size_t>(row) * K + sidx) >> bs_shift];
+        sc[t] = absmax[(static_cast<size_t>(row) * K + k0) >> bs_shift];
     }
 
     const float level = nf4_level_sel(threadIdx.x & 15);
     if (threadIdx.x < 16) lut_f[threadIdx.x] = level;
-    float4 *win = xstage + wave * 256;
-    const int l = lane & 31;
+    float4 *win = xstage + wave * 512;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int f = 64 * j + lane;
+        win[(f >> 3) * 8 + ((f & 7) ^ ((f >> 3) & 7))] = xl[j];
+    }
+    __syncthreads();
     float xv[32];
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        if (half) __syncthreads();               // window reads of half 0 done
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int g = 64 * j + lane;         // local float4 index in this half
-            win[(g >> 3) * 8 + ((g & 7) ^ ((g >> 3) & 7))] = xl[4 * half + j];
-        }
-        __syncthreads();
-        const bool mine = (lane >> 5) == half;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 v = win[l * 8 + (i ^ (l & 7))];
-            if (half == 0) {
-                xv[4 * i + 0] = v.x;
-                xv[4 * i + 1] = v.y;
-                xv[4 * i + 2] = v.z;
-                xv[4 * i + 3] = v.w;
-            } else {
-                xv[4 * i + 0] = mine ? v.x : xv[4 * i + 0];
-                xv[4 * i + 1] = mine ? v.y : xv[4 * i + 1];
-                xv[4 * i + 2] = mine ? v.z : xv[4 * i + 2];
-                xv[4 * i + 3] = mine ? v.w : xv[4 * i + 3];
-            }
-        }
+    for (int i = 0; i < 8; ++i) {
+        const float4 v = win[lane * 8 + (i ^ (lane & 7))];
+        xv[4 * i + 0] = v.x;
+        xv[4 * i + 1] = v.y;
+        xv[4 * i + 2] = v.z;
+        xv[4 * i + 3] = v.w;
     }
     const char *lut = reinterpret_cast<const char *>(lut_f);
 
@@ -149,20 +127,16 @@ __global__ __launch_bounds__(kMaxWaves * 64) void nf4_rows_kernel(float *__restr
         if (t + PF < T) {
             const int row = min(row0 + t + PF, N - 1);
             q[t + PF] = load_stream16(qp + row * row_bytes);
-            sc[t + PF] = absmax[(static_cast<size_t>(row) * K + sidx) >> bs_shift];
+            sc[t + PF] = absmax[(static_cast<size_t>(row) * K + k0) >> bs_shift];
         }
-        const float d = nf4_word_dot(q[t], xv, lut) * sc[t];
-        acc[t] = active ? d : 0.0f;
+        acc[t] = nf4_word_dot(q[t], xv, lut) * sc[t];
         // Keep the written pipeline: without these the compiler defers every
         // row's arithmetic to the end and holds all lookups in registers.
         asm volatile("" : "+v"(acc[t]));
         __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-        const float v = wave_sum(acc[t]);
-        if (lane == 0) part[wave][t] = v;
-    }
+    const float tot = wave_sum_rows<T>(acc);
+    if (lane < T) part[wave][wave_rows_index<T>(lane)] = tot;
     __syncthreads();
     if (threadIdx.x < T && row0 + static_cast<int>(threadIdx.x) < N) {
         float v = 0.0f;
@@ -183,7 +157,7 @@ int env_int(const char *name, int dflt) {
 int enqueue_nf4_rows(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift) {
     static const int env_t = env_int("ALJABR_ROCM_NF4_T", 0);
     const int S = (K + kChunk - 1) / kChunk;
-    if (K % 32 != 0 || S > kMaxWaves || bs_shift < 5 || !aligned(Bq, 16) || !aligned(A, 16))
+    if (K % kChunk != 0 || S > kMaxWaves || bs_shift < 5 || !aligned(Bq, 16) || !aligned(A, 16))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     int T = env_t;
@@ -197,7 +171,7 @@ int enqueue_nf4_rows(float *C, const float *A, const uint8_t *Bq, const float *a
     }
     hipStream_t s = current_stream();
     const dim3 grid((N + T - 1) / T), block(64 * S);
-    const size_t lds = static_cast<size_t>(S) * 256 * sizeof(float4);
+    const size_t lds = static_cast<size_t>(S) * 512 * sizeof(float4);
     switch (T) {
     case 16: hipLaunchKernelGGL((nf4_rows_kernel<16, 4>), grid, block, lds, s, C, A, Bq, absmax, N, K, bs_shift); break;
     case 8: hipLaunchKernelGGL((nf4_rows_kernel<8, 4>), grid, block, lds, s, C, A, Bq, absmax, N, K, bs_shift); break;

@@ -1,0 +1,390 @@
+// matvec_rows.hip - batch-1 matvec for NF4, Q4_0 and Q8_0 rows, K split
+// across the waves of a workgroup, T rows per wave pipelined in straight-line
+// code.
+//
+// Formats (reference layouts):
+//   NF4  codes u8[N*K/2], byte j = (code[2j] << 4) | code[2j+1], absmax fp32
+//        per 2^k >= 32 elements of the flat [N,K] index
+//        (STC/DequantizationKernel.java:84-102);
+//   Q4_0 18-byte blocks {f16 d; u8 qs[16]}, qs[j] low nibble -> element j,
+//        high nibble -> element j+16, value (q-8)*d
+//        (GRT/GgufBlockDequantizer.java:33-37,403-416);
+//   Q8_0 34-byte blocks {f16 d; i8 qs[32]} (GRT/GgufBlockDequantizer.java:231-265).
+//
+// Decoding is the bottleneck once the weights stream at HBM speed, so every
+// choice below cuts VALU instructions per weight:
+//   * 4-bit formats decode a whole code BYTE (two weights) with one LDS read of
+//     a float2 from a 256-entry pair table. The table is replicated 32 times,
+//     entry e of replica r at byte address e*256 + r*8, so lane l reads replica
+//     l%32 and a wave's reads never conflict; and the address is one v_perm_b32
+//     (code byte into bits 8-15, the lane's r*8 into bits 0-7). Per weight:
+//     half a v_perm, half an LDS read, one FMA.
+//   * Q8_0 converts with v_cvt_f32_ubyte on q^0x80 (= q+128) and subtracts
+//     128*sum(x) per block: one convert and one FMA per weight.
+//   * Activations are staged once per workgroup with coalesced loads through
+//     a swizzled LDS window (conflict-free), then live in registers: lane l
+//     owns the 32 weights [32l, 32l+32) of its wave's 2048-element K chunk.
+//   * Rows are unrolled with the loads of row t+PF issued before row t is
+//     computed (the compiler drains all loads at a loop back-edge), and the T
+//     row sums are reduced across the wave by one butterfly.
+//
+// Workgroup = W (8 or 16) waves: G = W/S row groups of S = K/2048 K-chunk
+// waves (waves beyond S*G only help with set-up). Q4_0/Q8_0 rows are read per lane PAIR:
+// lanes 2m and 2m+1 own blocks 2m, 2m+1, 36 (Q4_0) or 68 (Q8_0) bytes that
+// start 4-byte aligned when K % 64 == 0, so each lane loads dwords that lie
+// inside its pair and realigns its block with v_alignbit.
+#include "device.hpp"
+#include "internal.hpp"
+#include "kernels.hpp"
+
+namespace aljabr {
+namespace {
+
+constexpr int kChunk = 2048;
+constexpr int kMaxWaves = 16;
+constexpr int kFmtNF4 = 0, kFmtQ4 = 1, kFmtQ8 = 2;
+constexpr int kPairBytes = 256 * 256;          // 256 entries x 32 replicas x float2
+
+typedef unsigned int u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4a4 load_stream16_a4(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4a4 *>(p));
+}
+__device__ __forceinline__ uint32_t load_stream4(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+}
+
+// Per-lane raw data of one row.
+template <int FMT> struct RowWords;
+template <> struct RowWords<kFmtNF4> { u32x4 q; float s; };
+template <> struct RowWords<kFmtQ4> { u32x4a4 a; uint32_t b; };
+template <> struct RowWords<kFmtQ8> { u32x4a4 a, b; uint32_t c; };
+
+struct RowsArgs {
+    float *y;
+    const float *x;
+    const uint8_t *w;
+    const float *absmax;   // NF4 only
+    int N, K, bs_shift, S, G;
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_row(RowWords<FMT> &d, const RowsArgs &a, int row, int k0, int lane_blk) {
+    if constexpr (FMT == kFmtNF4) {
+        const size_t row_bytes = static_cast<size_t>(a.K) >> 1;
+        d.q = load_stream16(a.w + row * row_bytes + (k0 >> 1));
+        d.s = a.absmax[(static_cast<size_t>(row) * a.K + k0) >> a.bs_shift];
+    } else {
+        constexpr int BB = FMT == kFmtQ4 ? 18 : 34;
+        const size_t row_bytes = static_cast<size_t>(a.K >> 5) * BB;
+        // Pair start (4-byte aligned) + 16 (Q4_0) or 32 (Q8_0) for the odd lane.
+        const uint8_t *p = a.w + row * row_bytes + static_cast<size_t>(lane_blk >> 1) * (2 * BB) +
+                           (lane_blk & 1) * (BB - 2);
+        if constexpr (FMT == kFmtQ4) {
+            d.a = load_stream16_a4(p);
+            d.b = load_stream4(p + 16);
+        } else {
+            d.a = load_stream16_a4(p);
+            d.b = load_stream16_a4(p + 16);
+            d.c = load_stream4(p + 32);
+        }
+    }
+}
+
+// LDS address of the pair-table entry for byte BYTE of `w`, replica in `cl`.
+template <int BYTE>
+__device__ __forceinline__ uint32_t pair_addr(uint32_t w, uint32_t cl) {
+    return __builtin_amdgcn_perm(w, cl, 0x0C0C0000u | ((4u + BYTE) << 8));
+}
+
+__device__ __forceinline__ float2 pair_at(const char *tbl, uint32_t addr) {
+    return *reinterpret_cast<const float2 *>(tbl + addr);
+}
+
+// sum over the lane's 32 weights of w*x, before the row/block scale.
+template <int FMT>
+__device__ __forceinline__ float row_dot(const RowWords<FMT> &d, const float (&xv)[32], float xsum, bool odd,
+                                         uint32_t cl, const char *tbl, float &scale) {
+    if constexpr (FMT == kFmtNF4) {
+        const uint32_t wv[4] = {d.q.x, d.q.y, d.q.z, d.q.w};
+        float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float2 e0 = pair_at(tbl, pair_addr<0>(wv[i], cl));
+            const float2 e1 = pair_at(tbl, pair_addr<1>(wv[i], cl));
+            const float2 e2 = pair_at(tbl, pair_addr<2>(wv[i], cl));
+            const float2 e3 = pair_at(tbl, pair_addr<3>(wv[i], cl));
+            p0 = fmaf(e0.x, xv[8 * i + 0], p0);
+            p1 = fmaf(e0.y, xv[8 * i + 1], p1);
+            p0 = fmaf(e1.x, xv[8 * i + 2], p0);
+            p1 = fmaf(e1.y, xv[8 * i + 3], p1);
+            p0 = fmaf(e2.x, xv[8 * i + 4], p0);
+            p1 = fmaf(e2.y, xv[8 * i + 5], p1);
+            p0 = fmaf(e3.x, xv[8 * i + 6], p0);
+            p1 = fmaf(e3.y, xv[8 * i + 7], p1);
+        }
+        scale = d.s;
+        return p0 + p1;
+    } else {
+        // Realign: even lane's block starts 2 bytes into its first dword
+        // (d = low half, codes from byte 2), odd lane's block starts 2 bytes
+        // before it (d = high half of dword 0, codes from dword 1).
+        constexpr int NW = FMT == kFmtQ4 ? 4 : 8;
+        uint32_t dw[NW + 1];
+        dw[0] = d.a.x; dw[1] = d.a.y; dw[2] = d.a.z; dw[3] = d.a.w;
+        if constexpr (FMT == kFmtQ4) {
+            dw[4] = d.b;
+        } else {
+            dw[4] = d.b.x; dw[5] = d.b.y; dw[6] = d.b.z; dw[7] = d.b.w; dw[8] = d.c;
+        }
+        uint32_t qw[NW];
+#pragma unroll
+        for (int i = 0; i < NW; ++i) qw[i] = odd ? dw[i + 1] : funnel_shift_right(dw[i + 1], dw[i], 16);
+        scale = f16_bits_to_f32(odd ? (dw[0] >> 16) : (dw[0] & 0xffffu));
+        if constexpr (FMT == kFmtQ4) {
+            float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float2 e0 = pair_at(tbl, pair_addr<0>(qw[i], cl));
+                const float2 e1 = pair_at(tbl, pair_addr<1>(qw[i], cl));
+                const float2 e2 = pair_at(tbl, pair_addr<2>(qw[i], cl));
+                const float2 e3 = pair_at(tbl, pair_addr<3>(qw[i], cl));
+                p0 = fmaf(e0.x, xv[4 * i + 0], p0);
+                p1 = fmaf(e0.y, xv[16 + 4 * i + 0], p1);
+                p0 = fmaf(e1.x, xv[4 * i + 1], p0);
+                p1 = fmaf(e1.y, xv[16 + 4 * i + 1], p1);
+                p0 = fmaf(e2.x, xv[4 * i + 2], p0);
+                p1 = fmaf(e2.y, xv[16 + 4 * i + 2], p1);
+                p0 = fmaf(e3.x, xv[4 * i + 3], p0);
+                p1 = fmaf(e3.y, xv[16 + 4 * i + 3], p1);
+            }
+            return p0 + p1;
+        } else {
+            float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t u = qw[i] ^ 0x80808080u;      // int8 q -> q + 128 as u8
+                p0 = fmaf(static_cast<float>(u & 0xffu), xv[4 * i + 0], p0);
+                p1 = fmaf(static_cast<float>((u >> 8) & 0xffu), xv[4 * i + 1], p1);
+                p0 = fmaf(static_cast<float>((u >> 16) & 0xffu), xv[4 * i + 2], p0);
+                p1 = fmaf(static_cast<float>(u >> 24), xv[4 * i + 3], p1);
+            }
+            return fmaf(-128.0f, xsum, p0 + p1);
+        }
+    }
+}
+
+// Pair table: slot i holds entry e = i/32 of replica i%32. NF4 bytes are (even code << 4) | odd code -> (level[hi],
+// level[lo]); Q4_0 low nibble -> element j, high -> j+16 -> (lo-8, hi-8).
+template <int FMT, int NT>
+__device__ __forceinline__ void build_pair_table(float2 *tbl2, int tid) {
+    static_assert(NT == 512 || NT == 1024, "table build assumes 512 or 1024 threads");
+    constexpr float kNF4[16] = {
+        -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+        -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+        0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+        0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+    // Slot i = tid + NT*k: low nibble (i/32)%16 = (tid/32)%16, high nibble
+    // i/512 = (NT/512)*k + tid/512.
+    const int lo = (tid >> 5) & 15;
+    const bool h1 = NT == 1024 && (tid >> 9);
+    const float vlo = FMT == kFmtNF4 ? nf4_level_sel(lo) : static_cast<float>(lo - 8);
+#pragma unroll
+    for (int k = 0; k < 8192 / NT; ++k) {
+        const int hi0 = (NT / 512) * k;
+        const float vhi = FMT == kFmtNF4 ? (h1 ? kNF4[hi0 + 1] : kNF4[hi0])
+                                         : static_cast<float>(hi0 - 8) + (h1 ? 1.0f : 0.0f);
+        tbl2[tid + NT * k] = FMT == kFmtNF4 ? make_float2(vhi, vlo) : make_float2(vlo, vhi);
+    }
+}
+
+template <int FMT, int T, int PF, int W>
+__global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
+    static_assert(T >= 1 && T <= 16 && PF >= 1 && (W == 8 || W == 16), "tile shape");
+    constexpr int TP = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16;   // butterfly width
+    extern __shared__ float4 smem[];    // 4-bit: pair table (x windows alias it); Q8_0: x windows
+    __shared__ float part[W][16];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int S = a.S;
+    const int chunk = wave % S;
+    const int grp = wave / S;
+    float2 *tbl2 = reinterpret_cast<float2 *>(smem);
+
+    if (grp >= a.G) {
+        // Helper wave (when S does not divide 8): takes part in the table
+        // build and meets the same four workgroup barriers, nothing else.
+        __syncthreads();                                     // 1: x staged
+        __syncthreads();                                     // 2: x read
+        if constexpr (FMT != kFmtQ8) build_pair_table<FMT, W * 64>(tbl2, tid);
+        __syncthreads();                                     // 3: table built
+        __syncthreads();                                     // 4: partials written
+        return;
+    }
+
+    const bool stager = grp == 0;                // one wave per chunk stages x
+    // Row t of this wave's group is row0 + t*rstride: at any moment all
+    // workgroups read neighbouring rows, so the chip sweeps the matrix front
+    // to back as one streaming read (the DRAM- and TLB-friendly order)
+    // instead of 1000 separate sequential streams.
+    const int row0 = blockIdx.x * a.G + grp;
+    const int rstride = gridDim.x * a.G;
+    const int k0 = chunk * kChunk + lane * 32;
+    const int lane_blk = chunk * 64 + lane;      // Q4_0/Q8_0 block index in the row
+
+    // Activations first (vmcnt retires in order: waiting for them then
+    // leaves the weight loads in flight).
+    const f32x4 *xw = reinterpret_cast<const f32x4 *>(a.x + chunk * kChunk);
+    f32x4 xl[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xl[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (stager) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xl[j] = xw[64 * j + lane];
+    }
+    RowWords<FMT> rw[T];
+#pragma unroll
+    for (int t = 0; t < PF && t < T; ++t) load_row<FMT>(rw[t], a, min(row0 + t * rstride, a.N - 1), k0, lane_blk);
+
+    // Stage x: float4 f of chunk c at slot c*512 + (f/8)*8 + ((f%8) ^ ((f/8)%8)).
+    if (stager) {
+        f32x4 *win = reinterpret_cast<f32x4 *>(smem) + chunk * 512;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int f = 64 * j + lane;
+            win[(f >> 3) * 8 + ((f & 7) ^ ((f >> 3) & 7))] = xl[j];
+        }
+    }
+    __syncthreads();                                         // 1
+    float xv[32];
+    {
+        const f32x4 *win = reinterpret_cast<const f32x4 *>(smem) + chunk * 512;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const f32x4 v = win[lane * 8 + (i ^ (lane & 7))];
+            xv[4 * i + 0] = v.x;
+            xv[4 * i + 1] = v.y;
+            xv[4 * i + 2] = v.z;
+            xv[4 * i + 3] = v.w;
+        }
+    }
+    float xsum = 0.0f;
+    if constexpr (FMT == kFmtQ8) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) xsum += xv[i];
+    }
+    __syncthreads();                                         // 2: the table overwrites the x windows
+    if constexpr (FMT != kFmtQ8) build_pair_table<FMT, W * 64>(tbl2, tid);
+    __syncthreads();                                         // 3
+
+    const char *tbl = reinterpret_cast<const char *>(smem);
+    const uint32_t cl = (lane & 31) * 8;
+    const bool odd = lane & 1;
+    float acc[TP];
+#pragma unroll
+    for (int t = T; t < TP; ++t) acc[t] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        if (t + PF < T) load_row<FMT>(rw[t + PF], a, min(row0 + (t + PF) * rstride, a.N - 1), k0, lane_blk);
+        float scale;
+        const float dot = row_dot<FMT>(rw[t], xv, xsum, odd, cl, tbl, scale);
+        acc[t] = dot * scale;
+        // Keep the written pipeline: without these the compiler defers every
+        // row's arithmetic to the end and holds all lookups in registers.
+        asm volatile("" : "+v"(acc[t]));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const float tot = wave_sum_rows<TP>(acc);
+    if (lane < TP) part[wave][wave_rows_index<TP>(lane)] = tot;
+    __syncthreads();                                         // 4
+    // The S chunk waves of group g are waves g*S .. g*S+S-1.
+    if (chunk == 0 && lane < T && row0 + lane * rstride < a.N) {
+        float v = 0.0f;
+        for (int c = 0; c < S; ++c) v += part[grp * S + c][lane];
+        a.y[row0 + lane * rstride] = v;
+    }
+}
+
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+template <int FMT, int T, int PF, int W>
+void launch_cfg(const RowsArgs &args, hipStream_t s) {
+    static const int pad = env_int("ALJABR_ROCM_ROWS_LDS", 0);   // dynamic LDS floor (bytes), sweeps only
+    const void *fn = reinterpret_cast<const void *>(rows_kernel<FMT, T, PF, W>);
+    size_t lds = FMT == kFmtQ8 ? static_cast<size_t>(args.S) * 512 * sizeof(float4) : kPairBytes;
+    if (pad > 0 && static_cast<size_t>(pad) > lds && pad <= 150 * 1024) lds = pad;
+    static bool lds_set = false;                 // the attribute is per kernel, per process
+    if (!lds_set) {
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+        lds_set = true;
+    }
+    const int rows_per_wg = args.G * T;
+    const dim3 grid((args.N + rows_per_wg - 1) / rows_per_wg), block(W * 64);
+    hipLaunchKernelGGL((rows_kernel<FMT, T, PF, W>), grid, block, lds, s, args);
+}
+
+// T rows per wave (even, 2..16), loads PF = min(T, 4) rows ahead, 8 waves.
+template <int FMT>
+void launch_rows(RowsArgs args, int T, hipStream_t s) {
+    args.G = 8 / args.S;
+    switch (T) {
+    case 16: launch_cfg<FMT, 16, 4, 8>(args, s); break;
+    case 14: launch_cfg<FMT, 14, 4, 8>(args, s); break;
+    case 12: launch_cfg<FMT, 12, 4, 8>(args, s); break;
+    case 10: launch_cfg<FMT, 10, 4, 8>(args, s); break;
+    case 8: launch_cfg<FMT, 8, 4, 8>(args, s); break;
+    case 7: launch_cfg<FMT, 7, 4, 8>(args, s); break;
+    case 6: launch_cfg<FMT, 6, 4, 8>(args, s); break;
+    case 4: launch_cfg<FMT, 4, 2, 8>(args, s); break;
+    default: launch_cfg<FMT, 2, 2, 8>(args, s); break;
+    }
+}
+
+// Rows per wave: the per-workgroup set-up (activation staging, the 64 KiB
+// pair table) is paid once per workgroup, and measured on MI355X the fastest
+// shape is one 8-wave workgroup per CU, each taking N/CUs rows: T =
+// ceil(N / (G * CUs)) rounded up to even, at most 16 (beyond that more
+// workgroups). ALJABR_ROCM_ROWS_T overrides for sweeps.
+int pick_rows_t(int N, int S) {
+    static const int env_t = env_int("ALJABR_ROCM_ROWS_T", 0);
+    if (env_t >= 2 && env_t <= 16 && (env_t % 2 == 0 || env_t == 7)) return env_t;
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const long long per = static_cast<long long>(8 / S) * cus;
+    int t = static_cast<int>((N + per - 1) / per);
+    t = (t + 1) & ~1;
+    return t < 2 ? 2 : t > 16 ? 16 : t;
+}
+
+}  // namespace
+
+int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax, int K, int N, int type,
+                 int bs_shift) {
+    const int S = K / kChunk;
+    if (K % kChunk != 0 || S < 1 || S > 8 || !aligned(A, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    int fmt;
+    if (type == ALJABR_ROCM_TYPE_NF4) {
+        if (bs_shift < 5 || !aligned(W, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        fmt = kFmtNF4;
+    } else if (type == ALJABR_ROCM_TYPE_Q4_0 || type == ALJABR_ROCM_TYPE_Q8_0) {
+        if (!aligned(W, 4)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        fmt = type == ALJABR_ROCM_TYPE_Q4_0 ? kFmtQ4 : kFmtQ8;
+    } else {
+        return ALJABR_ROCM_ERR_UNSUPPORTED;
+    }
+    RowsArgs args{C, A, W, absmax, N, K, bs_shift, S, 0};
+    const int T = pick_rows_t(N, S);
+    hipStream_t s = current_stream();
+    switch (fmt) {
+    case kFmtNF4: launch_rows<kFmtNF4>(args, T, s); break;
+    case kFmtQ4: launch_rows<kFmtQ4>(args, T, s); break;
+    default: launch_rows<kFmtQ8>(args, T, s); break;
+    }
+    return ALJABR_ROCM_OK;
+}
+
+}  // namespace aljabr

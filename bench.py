@@ -25,7 +25,7 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 K_MODEL, FFN = 4096, 14336
 BLOCK = 64
-KERNEL = "nf4_rows_kernel"          # the batch-1 NF4 kernel these launches dispatch to
+KERNEL = "rows_kernel"              # the batch-1 kernel these launches dispatch to (matvec_rows.hip)
 
 
 def nf4_bytes(n: int, k: int, m: int = 1) -> int:

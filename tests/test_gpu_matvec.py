@@ -74,6 +74,34 @@ def test_gguf_matvec(rocm, dev, oracle, qtype, n, k, m):
     assert rel_l2(dev.get(y), y_ref) <= TOL
 
 
+# Batch-1 rows kernels (K % 2048 == 0): every K-chunk count S = K/2048 from 1
+# to 8 (S = 3, 5, 6, 7 leave helper waves in the workgroup), row counts that
+# do not fill the last workgroup, and the Llama down shape for the GGUF types.
+ROWS_SHAPES = [(1, 2048), (100, 2048), (333, 6144), (77, 10240), (58, 12288), (129, 14336), (130, 16384),
+               (4096, 14336)]
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "q4_0", "q8_0"])
+@pytest.mark.parametrize("n,k", ROWS_SHAPES)
+def test_batch1_rows_kernels(rocm, dev, oracle, fmt, n, k):
+    w = oracle.normal(53 + n + k, n * k, 0.0, 0.02)
+    x = oracle.normal(59 + k, k)
+    y = dev.empty(n)
+    if fmt == "nf4":
+        codes, absmax = oracle.nf4_quantize(w, 64)
+        y_ref = oracle.nf4_matvec(codes, absmax, x, n, k, 64)
+        c, a, xd = dev.put(codes), dev.put(absmax), dev.put(x)
+        rocm.call("aljabr_rocm_matvec_tb_nf4", dev.ptr(y), dev.ptr(xd), dev.ptr(c), dev.ptr(a), k, n, 64)
+    else:
+        ot = oracle.QTYPE_Q4_0 if fmt == "q4_0" else oracle.QTYPE_Q8_0
+        enc = oracle.quantize(ot, w)
+        y_ref = oracle.q_matvec(ot, enc, x, n, k)
+        wd, xd = dev.put(enc), dev.put(x)
+        fn = "aljabr_rocm_matvec_tb_q4_0" if fmt == "q4_0" else "aljabr_rocm_matvec_tb_q8_0"
+        rocm.call(fn, dev.ptr(y), dev.ptr(xd), dev.ptr(wd), k, n)
+    assert rel_l2(dev.get(y), y_ref) <= TOL
+
+
 @pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
 def test_gguf_reference_known_rows(rocm, dev, oracle, qtype):
     import json, os
