@@ -37,6 +37,9 @@ int enqueue_nf4_rows(float *C, const float *A, const uint8_t *Bq, const float *a
 // GGUF rows 4-byte aligned). `type` is an ALJABR_ROCM_TYPE_* id.
 int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax, int K, int N, int type,
                  int bs_shift);
+// NF4 small-M GEMM on MFMA (2 <= M <= 64, K % 512 == 0, block size 64).
+int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
+                     int M);
 // Persistent double-buffered batch-1 kernels (K <= 16384).
 int enqueue_nf4_stream(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift);
 int enqueue_gguf_stream(float *C, const float *A, const uint8_t *B, int K, int N, int type);

@@ -378,6 +378,15 @@ int log2_exact(int v) {
 
 }  // namespace
 
+// Small-M GEMMs use the MFMA kernel unless ALJABR_ROCM_MFMA=0.
+bool mfma_enabled() {
+    static const bool v = [] {
+        const char *e = getenv("ALJABR_ROCM_MFMA");
+        return !(e && *e == '0');
+    }();
+    return v;
+}
+
 // Batch-1 kernel family: 0 (default) = pair-table rows kernels, 1 = the
 // earlier per-format kernels (ALJABR_ROCM_BATCH1=1, kept for comparison).
 int batch1_kernel() {
@@ -447,6 +456,27 @@ namespace aljabr {
 // M > 8 slices run the small-M kernels per slice of 8 tokens (weights are
 // re-read per slice); the MFMA path takes over at its threshold.
 int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M) {
+    // M >= 2 on the matrix cores when the shape allows, 64 tokens per pass.
+    if (M >= 2 && mfma_enabled()) {
+        const int shift = log2_exact(bs);
+        bool ok = true;
+        for (int m0 = 0; m0 < M && ok; m0 += 64) {
+            const int mm = M - m0 < 64 ? M - m0 : 64;
+            if (mm < 2) break;                   // a last single row takes the batch-1 path below
+            const int rc = enqueue_nf4_mfma(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, Bq,
+                                            absmax, K, N, shift, mm);
+            if (rc != ALJABR_ROCM_OK) {
+                if (m0 != 0) return rc;          // the shape checks do not depend on m0
+                ok = false;
+            }
+        }
+        if (ok) {
+            const int done = M - (M % 64 == 1 ? 1 : 0);
+            if (done == M) return ALJABR_ROCM_OK;
+            return enqueue_nf4_small(C + static_cast<size_t>(done) * N, A + static_cast<size_t>(done) * K, Bq,
+                                     absmax, K, N, bs, 1);
+        }
+    }
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mm = M - m0 < 8 ? M - m0 : 8;
         int rc = enqueue_nf4_small(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, Bq, absmax, K, N,

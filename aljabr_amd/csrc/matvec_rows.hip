@@ -41,7 +41,6 @@ namespace aljabr {
 namespace {
 
 constexpr int kChunk = 2048;
-constexpr int kMaxWaves = 16;
 constexpr int kFmtNF4 = 0, kFmtQ4 = 1, kFmtQ8 = 2;
 constexpr int kPairBytes = 256 * 256;          // 256 entries x 32 replicas x float2
 

@@ -74,6 +74,26 @@ def test_gguf_matvec(rocm, dev, oracle, qtype, n, k, m):
     assert rel_l2(dev.get(y), y_ref) <= TOL
 
 
+# NF4 small-M GEMM on the matrix cores (2 <= M <= 64 per pass, K % 512 == 0):
+# M across the m-tile boundaries (32, 64) and past one pass (65, 100), ragged
+# N, K-slices of 512 and 256, and the Llama MLP shapes at M = 16 and 64.
+@pytest.mark.parametrize("n,k,m", [(300, 1024, 2), (300, 1024, 3), (257, 2048, 8), (300, 1024, 31), (300, 1024, 32),
+                                   (300, 1024, 33), (129, 512, 64), (300, 1024, 65), (77, 1536, 100),
+                                   (14336, 4096, 16), (4096, 14336, 64)])
+def test_nf4_mfma_small_m(rocm, dev, oracle, n, k, m):
+    codes, absmax = _nf4_case(oracle, n, k, seed=3)
+    x = oracle.normal(71 + m, m * k)
+    y_ref = oracle.nf4_matvec(codes, absmax, x, n, k, 64).ravel()
+    c, a, xd = dev.put(codes), dev.put(absmax), dev.put(x)
+    y = dev.empty(m * n)
+    rocm.call("aljabr_rocm_matvec_tb_batch_nf4", dev.ptr(y), dev.ptr(xd), dev.ptr(c), dev.ptr(a), k, n, 64, m)
+    got = dev.get(y)
+    assert rel_l2(got, y_ref) <= TOL
+    # every token row on its own, so one wrong m-tile cannot hide in the total
+    for i in range(m):
+        assert rel_l2(got[i * n:(i + 1) * n], y_ref[i * n:(i + 1) * n]) <= TOL, i
+
+
 # Batch-1 rows kernels (K % 2048 == 0): every K-chunk count S = K/2048 from 1
 # to 8 (S = 3, 5, 6, 7 leave helper waves in the workgroup), row counts that
 # do not fill the last workgroup, and the Llama down shape for the GGUF types.
