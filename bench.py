@@ -47,6 +47,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--decode-steps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the small-M GEMM and attention measurements (BASELINE configs 2 and 4)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 20 times (FETCH_SIZE/WRITE_SIZE calibration)")
     return ap.parse_args()
@@ -122,6 +124,90 @@ def cpu_baseline(seconds: float):
             "kind": "port",
             "sample": f"{done} MLP steps (3 NF4 matvecs each: 14336x4096, 14336x4096, 4096x14336, batch 1), "
                       f"{dt:.1f} s, oracle C restatement, OpenMP row chunks = 2 x {threads} threads"}
+
+
+def small_m_bench(abi, torch, stream, ms=(1, 4, 16, 64), launches=60):
+    """NF4 small-M GEMM at the MLP shapes, M tokens per
+    launch (M >= 2 runs on the matrix cores). Weights rotate over >= 512 MB.
+    Returns per-shape, per-M launch time, algorithmic GB/s and TFLOP/s."""
+    lib = abi.load()
+    out = {}
+    for n, k in ((FFN, K_MODEL), (K_MODEL, FFN)):
+        per = n * k // 2 + n * k // BLOCK * 4
+        copies = max(2, -(-520_000_000 // per))
+        from aljabr_amd.llama import nf4_quantize_device
+        g = torch.Generator(device="cuda:0").manual_seed(3)
+        bufs = [nf4_quantize_device(torch.randn(n * k, generator=g, device="cuda:0").mul_(0.02), BLOCK)
+                for _ in range(copies)]
+        for m in ms:
+            x = torch.randn(m * k, device="cuda:0")
+            y = torch.empty(m * n, device="cuda:0")
+            torch.cuda.synchronize()
+
+            def launch(i):
+                c, a = bufs[i % copies]
+                rc = lib.aljabr_rocm_matvec_tb_batch_nf4(y.data_ptr(), x.data_ptr(), c.data_ptr(), a.data_ptr(),
+                                                         k, n, BLOCK, m)
+                if rc:
+                    abi.check(rc, "aljabr_rocm_matvec_tb_batch_nf4")
+            for i in range(5):
+                launch(i)
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for i in range(launches):
+                launch(i)
+            end.record(stream)
+            end.synchronize()
+            us = start.elapsed_time(end) * 1000.0 / launches
+            alg = per + m * (k + n) * 4
+            out[f"{n}x{k}_m{m}"] = {"us": round(us, 2), "GBs": round(alg / us / 1e3, 1),
+                                    "TFLOPs": round(2.0 * m * n * k / us / 1e6, 1)}
+        del bufs
+        torch.cuda.empty_cache()
+    return out
+
+
+def attention_bench(abi, torch, stream, launches=20):
+    """GQA decode attention, Hq=32, Hkv=8, D=128, fp16
+    K/V ~N(0,1), one query token per sequence, scale 1/sqrt(128). Small
+    configurations rotate through a >= 1 GiB K/V pool so the caches cannot
+    serve them. Returns launch time and algorithmic GB/s (K + V + Q + O)."""
+    lib = abi.load()
+    hq, hkv, d = 32, 8, 128
+    out = {}
+    pool_elems = 1 << 29                                   # 1 GiB of fp16 per K and V pool
+    for b, sk in ((1, 512), (16, 512), (64, 512), (1, 4096), (16, 4096), (64, 4096), (1, 32768), (16, 32768),
+                  (64, 32768)):
+        kv = b * hkv * sk * d
+        elems = max(kv, pool_elems)
+        kpool = torch.randn(elems, device="cuda:0", dtype=torch.float16)
+        vpool = torch.randn(elems, device="cuda:0", dtype=torch.float16)
+        q = torch.randn(b * hq * d, device="cuda:0")
+        o = torch.empty(b * hq * d, device="cuda:0")
+        slots = max(1, elems // kv)
+        torch.cuda.synchronize()
+
+        def launch(i):
+            off = (i % slots) * kv * 2
+            rc = lib.aljabr_rocm_attention_gqa(o.data_ptr(), q.data_ptr(), kpool.data_ptr() + off,
+                                               vpool.data_ptr() + off, None, b, hq, hkv, 1, sk, d,
+                                               abi.TYPE_F16, 0.0, 1)
+            if rc:
+                abi.check(rc, "aljabr_rocm_attention_gqa")
+        for i in range(3):
+            launch(i)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(launches):
+            launch(i)
+        end.record(stream)
+        end.synchronize()
+        us = start.elapsed_time(end) * 1000.0 / launches
+        alg = 2 * kv * 2 + 2 * b * hq * d * 4
+        out[f"b{b}_s{sk}"] = {"us": round(us, 2), "GBs": round(alg / us / 1e3, 1)}
+        del kpool, vpool
+        torch.cuda.empty_cache()
+    return out
 
 
 def traffic_record(kernel: str):
@@ -248,6 +334,12 @@ def run(args, abi, torch, stream) -> None:
                      "kernel": KERNEL, "bytes_per_launch": per_launch_bytes,
                      "avg_launch_us": round(per_launch_ms * 1e3, 3)},
     }
+
+    if not args.no_extra:
+        log("small-M NF4 GEMM (M = 1, 4, 16, 64)")
+        result["small_m_gemm"] = small_m_bench(abi, torch, stream)
+        log("GQA decode attention")
+        result["attention"] = attention_bench(abi, torch, stream)
 
     if not args.no_decode:
         from aljabr_amd.llama import LLAMA3_8B, random_weights
