@@ -41,6 +41,30 @@ def _compile(src: str) -> str:
     return obj
 
 
+HOST_SRC = os.path.join(HERE, "host")
+SPI_LIB = os.path.join(HERE, "libaljabr_rocm_spi.so")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+CXX = os.environ.get("CXX") or shutil.which("g++") or "g++"
+
+
+def build_spi(verbose: bool = True) -> str:
+    """The C++ Backend-SPI mirror (host/*.cpp) over the C ABI. It binds
+    libaljabr_rocm.so with dlopen when a session opens, so it links no HIP."""
+    srcs = sorted(glob.glob(os.path.join(HOST_SRC, "*.cpp")))
+    tmp = SPI_LIB + ".tmp"
+    cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", f"-I{INCLUDE}", *srcs, "-ldl",
+           "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed for the SPI mirror:\n{res.stderr}")
+    if res.stderr.strip():
+        sys.stderr.write(res.stderr)
+    os.replace(tmp, SPI_LIB)
+    if verbose:
+        print(f"built {SPI_LIB}")
+    return SPI_LIB
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
@@ -57,6 +81,7 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(sources)} sources")
+    build_spi(verbose)
     return LIB
 
 
