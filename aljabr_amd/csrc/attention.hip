@@ -60,7 +60,8 @@ __device__ __forceinline__ void load8(const void *base, long long idx, float (&r
 // grid: x = split, y = kv head * Sq + query row, z = batch. WAVES*64 threads.
 template <int D, int G, bool F16, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, int splits, int chunk,
-                                                                float *__restrict__ part) {
+                                                                float *__restrict__ part_o,
+                                                                float *__restrict__ part_ml) {
     constexpr int LPK = D / 8;                 // lanes per key row
     constexpr int GPW = 64 / LPK;              // key groups per wave
     constexpr int NG = GPW * WAVES;            // key groups per workgroup
@@ -197,36 +198,71 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
         if (splits == 1) {
             p.out[row * D + dd] = L == 0.0f ? 0.0f : O / L;
         } else {
-            float *pp = part + (row * splits + split) * (D + 2);
-            pp[dd] = O;
+            part_o[(row * splits + split) * D + dd] = O;
             if (dd == 0) {
-                pp[D] = M;
-                pp[D + 1] = L;
+                part_ml[(row * splits + split) * 2] = M;
+                part_ml[(row * splits + split) * 2 + 1] = L;
             }
         }
     }
 }
 
-// Merge split partials: one workgroup of D threads per query row.
+// Merge split partials: one 256-thread workgroup per query row. D/4 lanes
+// take one split's o as float4s, so 256/(D/4) splits are read at once; each
+// lane group folds its splits with online rescaling, and the groups are
+// combined through LDS.
 template <int D>
-__global__ __launch_bounds__(D) void attn_merge_kernel(float *__restrict__ out, const float *__restrict__ part,
-                                                      int splits) {
+__global__ __launch_bounds__(256) void attn_merge_kernel(float *__restrict__ out, const float *__restrict__ part_o,
+                                                        const float *__restrict__ part_ml, int splits) {
+    constexpr int LPS = D / 4;          // lanes per split
+    constexpr int SG = 256 / LPS;       // splits in flight
+    __shared__ float st[SG][D + 2];
     const long long row = blockIdx.x;
-    const int dd = threadIdx.x;
-    const float *pp = part + row * splits * (D + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < splits; ++s) M = fmaxf(M, pp[s * (D + 2) + D]);
-    float L = 0.0f, O = 0.0f;
-    if (M != -INFINITY) {
-        for (int s = 0; s < splits; ++s) {
-            const float ms = pp[s * (D + 2) + D];
-            if (ms == -INFINITY) continue;
-            const float w = exp2f(ms - M);
-            L = fmaf(pp[s * (D + 2) + D + 1], w, L);
-            O = fmaf(pp[s * (D + 2) + dd], w, O);
-        }
+    const int sg = threadIdx.x / LPS, j = threadIdx.x % LPS;
+    const float *po = part_o + row * splits * D;
+    const float *pm = part_ml + row * splits * 2;
+    float m = -INFINITY, l = 0.0f;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s = sg; s < splits; s += SG) {
+        const float ms = pm[2 * s], ls = pm[2 * s + 1];
+        const float4 os = *reinterpret_cast<const float4 *>(po + s * D + 4 * j);
+        const float mn = fmaxf(m, ms);
+        if (mn == -INFINITY) continue;
+        const float a = m == -INFINITY ? 0.0f : exp2f(m - mn);
+        const float b = ms == -INFINITY ? 0.0f : exp2f(ms - mn);
+        l = fmaf(l, a, ls * b);
+        o.x = fmaf(o.x, a, os.x * b);
+        o.y = fmaf(o.y, a, os.y * b);
+        o.z = fmaf(o.z, a, os.z * b);
+        o.w = fmaf(o.w, a, os.w * b);
+        m = mn;
     }
-    out[row * D + dd] = L == 0.0f ? 0.0f : O / L;
+    st[sg][4 * j] = o.x;
+    st[sg][4 * j + 1] = o.y;
+    st[sg][4 * j + 2] = o.z;
+    st[sg][4 * j + 3] = o.w;
+    if (j == 0) {
+        st[sg][D] = m;
+        st[sg][D + 1] = l;
+    }
+    __syncthreads();
+    for (int dd = threadIdx.x; dd < D; dd += 256) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < SG; ++g) M = fmaxf(M, st[g][D]);
+        float L = 0.0f, O = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int g = 0; g < SG; ++g) {
+                const float mg = st[g][D];
+                if (mg == -INFINITY) continue;
+                const float w = exp2f(mg - M);
+                L = fmaf(st[g][D + 1], w, L);
+                O = fmaf(st[g][dd], w, O);
+            }
+        }
+        out[row * D + dd] = L == 0.0f ? 0.0f : O / L;
+    }
 }
 
 // Any head_dim: one thread per (batch, query head, query row, output dim).
@@ -306,11 +342,15 @@ int launch_split(const AttnParams &p, int splits, int chunk, float *part, hipStr
     constexpr int NG = (64 / (D / 8)) * WAVES;
     const size_t lds = static_cast<size_t>(NG) * G * (D + 2) * sizeof(float);
     const dim3 grid(splits, p.Hkv * p.Sq, p.B);
-    hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES>), grid, dim3(WAVES * 64), lds, s, p, splits, chunk, part);
-    if (splits > 1) {
-        const unsigned rows = static_cast<unsigned>(static_cast<long long>(p.B) * p.Hq * p.Sq);
-        hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(rows), dim3(D), 0, s, p.out, part, splits);
-    }
+    const long long rows = static_cast<long long>(p.B) * p.Hq * p.Sq;
+    // Partials: o as [rows][splits][D], then (m, l) as [rows][splits][2].
+    float *part_o = part;
+    float *part_ml = part ? part + rows * splits * D : nullptr;
+    hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES>), grid, dim3(WAVES * 64), lds, s, p, splits, chunk, part_o,
+                       part_ml);
+    if (splits > 1)
+        hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, p.out, part_o,
+                           part_ml, splits);
     return ALJABR_ROCM_OK;
 }
 

@@ -60,7 +60,7 @@ __device__ __forceinline__ float lane_xor(float v) {
     else return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (MASK << 10) | 0x1F));
 }
 
-// Butterfly sum of T = 2^t per-lane values (T <= 16) over the wave: stage s
+// Butterfly sum of T = 2^t per-lane values (T <= 32) over the wave: stage s
 // pairs each lane with lane ^ 2^s and keeps half of the values, so the whole
 // reduction costs ~3T/2 + 6 operations instead of T separate wave sums. On
 // return every lane holds the total of row wave_rows_index<T>(lane).
@@ -75,7 +75,7 @@ __device__ __forceinline__ void fold_rows_stage(float *v, bool upper) {
 
 template <int T>
 __device__ __forceinline__ int wave_rows_index(int lane) {
-    static_assert(T == 1 || T == 2 || T == 4 || T == 8 || T == 16, "T must be a power of two <= 16");
+    static_assert(T == 1 || T == 2 || T == 4 || T == 8 || T == 16 || T == 32, "T must be a power of two <= 32");
     int r = 0;
     for (int s = 0; (1 << s) < T; ++s) r = (r << 1) | ((lane >> s) & 1);
     return r;
@@ -88,12 +88,13 @@ __device__ __forceinline__ float wave_sum_rows(float (&v)[T]) {
     if constexpr (T >= 4) fold_rows_stage<2, T / 2>(v, lane & 2);
     if constexpr (T >= 8) fold_rows_stage<4, T / 4>(v, lane & 4);
     if constexpr (T >= 16) fold_rows_stage<8, T / 8>(v, lane & 8);
+    if constexpr (T >= 32) fold_rows_stage<16, T / 16>(v, lane & 16);
     float r = v[0];
     if constexpr (T < 2) r += lane_xor<1>(r);
     if constexpr (T < 4) r += lane_xor<2>(r);
     if constexpr (T < 8) r += lane_xor<4>(r);
     if constexpr (T < 16) r += lane_xor<8>(r);
-    r += lane_xor<16>(r);
+    if constexpr (T < 32) r += lane_xor<16>(r);
     r += lane_xor<32>(r);
     return r;
 }

@@ -40,6 +40,14 @@ int device_cu_count();
 
 inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// log2 of a power of two, -1 for anything else.
+inline int log2_exact(int v) {
+    if (v <= 0 || (v & (v - 1))) return -1;
+    int s = 0;
+    while ((1 << s) < v) ++s;
+    return s;
+}
+
 }  // namespace aljabr
 
 #define ALJ_CHECK_READY()                          \

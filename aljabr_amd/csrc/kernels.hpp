@@ -37,9 +37,28 @@ int enqueue_nf4_rows(float *C, const float *A, const uint8_t *Bq, const float *a
 // GGUF rows 4-byte aligned). `type` is an ALJABR_ROCM_TYPE_* id.
 int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax, int K, int N, int type,
                  int bs_shift);
-// NF4 small-M GEMM on MFMA (2 <= M <= 64, K % 512 == 0, block size 64).
+// One weight matrix of a fused batch-1 NF4 launch: y[0..n) = W[n][K] . x'.
+struct RowsOut {
+    float *y;
+    const uint8_t *w;
+    const float *absmax;
+    int n;
+    int silu;       // store silu(v) = v / (1 + exp(-v)) (not with accumulate)
+};
+constexpr int kRowsPlain = 0;   // x' = x
+constexpr int kRowsNorm = 1;    // x' = RMSNorm(x) with weight norm_w over the K elements
+constexpr int kRowsMul = 2;     // x' = x * x2
+// Batch-1 NF4 matvec of up to three matrices sharing K and the activations
+// (stacked rows, one launch), with an activation prologue and, when
+// `accumulate`, y += instead of y =. Same shape limits as enqueue_rows;
+// ALJABR_ROCM_ERR_UNSUPPORTED (nothing enqueued) outside them.
+int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const float *x2, const float *norm_w,
+                           float eps, int K, int bs_shift, int prologue, int accumulate);
+// NF4 small-M GEMM on MFMA (2 <= M <= 64, K % 512 == 0, block size 64). With
+// `accumulate` the products are added to C as it is (C += A . W^T), so a
+// caller that has C cleared or holding a residual saves the clearing launch.
 int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
-                     int M);
+                     int M, bool accumulate = false);
 // Persistent double-buffered batch-1 kernels (K <= 16384).
 int enqueue_nf4_stream(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift);
 int enqueue_gguf_stream(float *C, const float *A, const uint8_t *B, int K, int N, int type);
@@ -47,12 +66,23 @@ int enqueue_gguf_stream(float *C, const float *A, const uint8_t *B, int K, int N
 int enqueue_nf4_small(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M);
 int enqueue_gguf_small(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M);
 
-int enqueue_rmsnorm(float *out, const float *x, const float *w, int rows, int len, float eps);
+// Buffers (null entries skipped) that a kernel clears as a side job.
+struct ZeroList {
+    float *p[3];
+    long long n[3];
+};
+
+int enqueue_rmsnorm(float *out, const float *x, const float *w, int rows, int len, float eps,
+                    const ZeroList *zero = nullptr);
 int enqueue_rope(float *x, const int *pos, int rows, int n_heads, int head_dim, float base);
 int enqueue_swiglu(float *dst, const float *gate, const float *up, long long n);
 int enqueue_add(float *a, const float *b, long long n);
 int enqueue_argmax(int *out, const float *x, int rows, int cols);
 int enqueue_embed(float *x, const float *embed, const int *tokens, int batch, int dim, int vocab);
 int enqueue_kv_append(uint16_t *cache, const float *src, const int *pos, int batch, int n_kv, int head_dim, int cap);
+// RoPE on q [batch][nh][D] in place and on k, then k and v [batch][nkv][D]
+// appended as fp16 at row pos[b] of caches [batch][nkv][cap][D] (D/2 <= 1024).
+int enqueue_rope_append(float *q, const float *k, const float *v, uint16_t *kc, uint16_t *vc, const int *pos, int batch,
+                        int nh, int nkv, int head_dim, int cap, float base);
 
 }  // namespace aljabr

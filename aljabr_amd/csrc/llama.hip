@@ -42,6 +42,7 @@ struct aljabr_rocm_llama {
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
     float *gate = nullptr, *up = nullptr, *hb = nullptr, *logits = nullptr;
     int *kv_len = nullptr;
+    bool rows_fused = false;   // batch-1 layers as four fused NF4 launches (shapes and alignment allow it)
 };
 
 using namespace aljabr;
@@ -128,6 +129,17 @@ int aljabr_rocm_llama_create(const aljabr_rocm_llama_config *cfg, const aljabr_r
     m->hb = carve<float>(cur, B * c.ffn);
     m->logits = carve<float>(cur, B * c.vocab);
     m->kv_len = carve<int>(cur, B);
+    // Batch-1 fusion needs every K a multiple of 2048 (at most 16384), a
+    // power-of-two block of at least 32 and 16-byte aligned weights and norms.
+    const int qd_i = c.n_heads * c.head_dim;
+    const int shift = log2_exact(c.nf4_block);
+    auto k_ok = [](int k) { return k % 2048 == 0 && k / 2048 >= 1 && k / 2048 <= 8; };
+    bool fused = k_ok(c.dim) && k_ok(qd_i) && k_ok(c.ffn) && shift >= 5;
+    for (int l = 0; l < L && fused; ++l)
+        for (const auto *t : {&m->attn_norm, &m->ffn_norm, &m->wq, &m->wk, &m->wv, &m->wo, &m->w_gate, &m->w_up,
+                              &m->w_down})
+            fused = fused && aligned((*t)[l], 16);
+    m->rows_fused = fused;
     *out = m;
     return ALJABR_ROCM_OK;
 }
@@ -163,6 +175,7 @@ int aljabr_rocm_llama_decode(aljabr_rocm_llama *m, const void *tokens, const voi
     const int *tok = static_cast<const int *>(tokens);
     const int B = batch, dim = c.dim, hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv_heads;
     const int qd = nh * hd, kvd = nkv * hd, ffn = c.ffn, bs = c.nf4_block;
+    const int shift = log2_exact(bs);
     const size_t layer_cache = static_cast<size_t>(c.max_batch) * kvd * c.max_seq;
     float *lg = logits ? static_cast<float *>(logits) : m->logits;
     int rc;
@@ -172,21 +185,54 @@ int aljabr_rocm_llama_decode(aljabr_rocm_llama *m, const void *tokens, const voi
         if (rc != ALJABR_ROCM_OK) return rc;    \
     } while (0)
     hipStream_t s = current_stream();
+    // y = x . W^T (y cleared beforehand) or, with `residual`, y += x . W^T for
+    // B rows. The matrix cores' K-slices add straight into y in both cases;
+    // elsewhere y is written, or the products go to `tmp` and one add follows.
+    auto mm = [&](float *y, const float *x, const void *w, const void *sc, int K, int N, bool residual,
+                  float *tmp) -> int {
+        const uint8_t *wq = static_cast<const uint8_t *>(w);
+        const float *ws = static_cast<const float *>(sc);
+        if (B >= 2 && B <= 64 && shift >= 0) {
+            const int r = enqueue_nf4_mfma(y, x, wq, ws, K, N, shift, B, true);
+            if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
+        }
+        if (!residual) return enqueue_matmul_nf4(y, x, wq, ws, K, N, bs, B);
+        const int r = enqueue_matmul_nf4(tmp, x, wq, ws, K, N, bs, B);
+        if (r != ALJABR_ROCM_OK) return r;
+        return enqueue_add(y, tmp, static_cast<long long>(B) * N);
+    };
+    const bool fused1 = B == 1 && m->rows_fused;
     hipLaunchKernelGGL(lengths_from_positions, dim3((B + 63) / 64), dim3(64), 0, s, m->kv_len, pos, B);
     ALJ_TRY(enqueue_embed(m->x, static_cast<const float *>(m->tok_embed), tok, B, dim, c.vocab));
     for (int l = 0; l < c.layers; ++l) {
         auto W = [&](const std::vector<const void *> &t) { return static_cast<const uint8_t *>(t[l]); };
         auto S = [&](const std::vector<const void *> &t) { return static_cast<const float *>(t[l]); };
-        ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, S(m->attn_norm), B, dim, c.eps));
-        ALJ_TRY(enqueue_matmul_nf4(m->q, m->xb, W(m->wq), S(m->wq_s), dim, qd, bs, B));
-        ALJ_TRY(enqueue_matmul_nf4(m->k, m->xb, W(m->wk), S(m->wk_s), dim, kvd, bs, B));
-        ALJ_TRY(enqueue_matmul_nf4(m->v, m->xb, W(m->wv), S(m->wv_s), dim, kvd, bs, B));
-        ALJ_TRY(enqueue_rope(m->q, pos, B, nh, hd, c.rope_base));
-        ALJ_TRY(enqueue_rope(m->k, pos, B, nkv, hd, c.rope_base));
         uint16_t *kc = m->k_cache + l * layer_cache;
         uint16_t *vc = m->v_cache + l * layer_cache;
-        ALJ_TRY(enqueue_kv_append(kc, m->k, pos, B, nkv, hd, c.max_seq));
-        ALJ_TRY(enqueue_kv_append(vc, m->v, pos, B, nkv, hd, c.max_seq));
+        // Attention block: xb = RMSNorm(x); q, k, v = Wq/Wk/Wv xb.
+        if (fused1) {
+            const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq_s), qd, 0},
+                                    {m->k, W(m->wk), S(m->wk_s), kvd, 0},
+                                    {m->v, W(m->wv), S(m->wv_s), kvd, 0}};
+            ALJ_TRY(enqueue_nf4_rows_fused(qkv, 3, m->x, nullptr, S(m->attn_norm), c.eps, dim, shift, kRowsNorm, 0));
+        } else {
+            const ZeroList z{{m->q, m->k, m->v},
+                             {static_cast<long long>(B) * qd, static_cast<long long>(B) * kvd,
+                              static_cast<long long>(B) * kvd}};
+            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, S(m->attn_norm), B, dim, c.eps, &z));
+            ALJ_TRY(mm(m->q, m->xb, m->wq[l], m->wq_s[l], dim, qd, false, nullptr));
+            ALJ_TRY(mm(m->k, m->xb, m->wk[l], m->wk_s[l], dim, kvd, false, nullptr));
+            ALJ_TRY(mm(m->v, m->xb, m->wv[l], m->wv_s[l], dim, kvd, false, nullptr));
+        }
+        rc = enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base);
+        if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+            ALJ_TRY(enqueue_rope(m->q, pos, B, nh, hd, c.rope_base));
+            ALJ_TRY(enqueue_rope(m->k, pos, B, nkv, hd, c.rope_base));
+            ALJ_TRY(enqueue_kv_append(kc, m->k, pos, B, nkv, hd, c.max_seq));
+            ALJ_TRY(enqueue_kv_append(vc, m->v, pos, B, nkv, hd, c.max_seq));
+        } else if (rc != ALJABR_ROCM_OK) {
+            return rc;
+        }
         AttnParams ap{};
         ap.out = m->att;
         ap.q = m->q;
@@ -199,14 +245,29 @@ int aljabr_rocm_llama_decode(aljabr_rocm_llama *m, const void *tokens, const voi
         ap.causal = 0;
         ap.kv_f16 = 1;
         ALJ_TRY(enqueue_attention(ap));
-        ALJ_TRY(enqueue_matmul_nf4(m->xb, m->att, W(m->wo), S(m->wo_s), qd, dim, bs, B));
-        ALJ_TRY(enqueue_add(m->x, m->xb, static_cast<long long>(B) * dim));
-        ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, S(m->ffn_norm), B, dim, c.eps));
-        ALJ_TRY(enqueue_matmul_nf4(m->gate, m->xb, W(m->w_gate), S(m->w_gate_s), dim, ffn, bs, B));
-        ALJ_TRY(enqueue_matmul_nf4(m->up, m->xb, W(m->w_up), S(m->w_up_s), dim, ffn, bs, B));
-        ALJ_TRY(enqueue_swiglu(m->hb, m->gate, m->up, static_cast<long long>(B) * ffn));
-        ALJ_TRY(enqueue_matmul_nf4(m->xb, m->hb, W(m->w_down), S(m->w_down_s), ffn, dim, bs, B));
-        ALJ_TRY(enqueue_add(m->x, m->xb, static_cast<long long>(B) * dim));
+        // x += Wo att.
+        if (fused1) {
+            const RowsOut o = {m->x, W(m->wo), S(m->wo_s), dim, 0};
+            ALJ_TRY(enqueue_nf4_rows_fused(&o, 1, m->att, nullptr, nullptr, 0.0f, qd, shift, kRowsPlain, 1));
+        } else {
+            ALJ_TRY(mm(m->x, m->att, m->wo[l], m->wo_s[l], qd, dim, true, m->xb));
+        }
+        // MLP: x += Wdown (silu(Wgate xb) * Wup xb), xb = RMSNorm(x).
+        if (fused1) {
+            const RowsOut gu[2] = {{m->gate, W(m->w_gate), S(m->w_gate_s), ffn, 1},
+                                   {m->up, W(m->w_up), S(m->w_up_s), ffn, 0}};
+            ALJ_TRY(enqueue_nf4_rows_fused(gu, 2, m->x, nullptr, S(m->ffn_norm), c.eps, dim, shift, kRowsNorm, 0));
+            const RowsOut d = {m->x, W(m->w_down), S(m->w_down_s), dim, 0};
+            ALJ_TRY(enqueue_nf4_rows_fused(&d, 1, m->gate, m->up, nullptr, 0.0f, ffn, shift, kRowsMul, 1));
+        } else {
+            const ZeroList z{{m->gate, m->up, nullptr},
+                             {static_cast<long long>(B) * ffn, static_cast<long long>(B) * ffn, 0}};
+            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, S(m->ffn_norm), B, dim, c.eps, &z));
+            ALJ_TRY(mm(m->gate, m->xb, m->w_gate[l], m->w_gate_s[l], dim, ffn, false, nullptr));
+            ALJ_TRY(mm(m->up, m->xb, m->w_up[l], m->w_up_s[l], dim, ffn, false, nullptr));
+            ALJ_TRY(enqueue_swiglu(m->hb, m->gate, m->up, static_cast<long long>(B) * ffn));
+            ALJ_TRY(mm(m->x, m->hb, m->w_down[l], m->w_down_s[l], ffn, dim, true, m->xb));
+        }
     }
     ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, static_cast<const float *>(m->out_norm), B, dim, c.eps));
     ALJ_TRY(enqueue_matmul_gguf(lg, m->xb, static_cast<const uint8_t *>(m->lm_head), dim, c.vocab, ALJABR_ROCM_TYPE_F16,

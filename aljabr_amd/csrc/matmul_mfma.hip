@@ -274,13 +274,15 @@ void launch_mm(const MmArgs &args, hipStream_t s) {
 // K-slices of 512 (M <= 32) or 256 (two m-tiles) keep every operand of a
 // slice in registers without spills.
 int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
-                     int M) {
+                     int M, bool accumulate) {
     if (M < 2 || M > 64 || K % 512 != 0 || bs_shift != 6 || !aligned(Bq, 16) || !aligned(A, 16) ||
         !aligned(absmax, 16))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     hipStream_t s = current_stream();
     const long long total = static_cast<long long>(M) * N;
-    hipLaunchKernelGGL(zero_f32_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, C, total);
+    if (!accumulate)   // the K-slices add into C
+        hipLaunchKernelGGL(zero_f32_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, C,
+                           total);
     MmArgs args{C, A, Bq, absmax, M, N, K, bs_shift};
     const int wgs_n = (N + kMmRowsPerWg - 1) / kMmRowsPerWg;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;

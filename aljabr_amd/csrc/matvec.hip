@@ -369,13 +369,6 @@ struct Tag {};
         }                                                                                    \
     } while (0)
 
-int log2_exact(int v) {
-    if (v <= 0 || (v & (v - 1))) return -1;
-    int s = 0;
-    while ((1 << s) < v) ++s;
-    return s;
-}
-
 }  // namespace
 
 // Small-M GEMMs use the MFMA kernel unless ALJABR_ROCM_MFMA=0.

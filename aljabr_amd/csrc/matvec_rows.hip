@@ -60,25 +60,63 @@ template <> struct RowWords<kFmtNF4> { u32x4 q; float s; };
 template <> struct RowWords<kFmtQ4> { u32x4a4 a; uint32_t b; };
 template <> struct RowWords<kFmtQ8> { u32x4a4 a, b; uint32_t c; };
 
-struct RowsArgs {
-    float *y;
-    const float *x;
+// A launch covers up to three weight matrices of the same K stacked as one
+// row space (the decode step's Q/K/V or gate/up share one launch and one
+// activation staging); segment s owns rows [seg[s-1].end, seg[s].end).
+struct RowsSeg {
     const uint8_t *w;
     const float *absmax;   // NF4 only
+    float *y;
+    int end;               // one past the segment's last row in the stacked row space
+    int silu;              // store v / (1 + exp(-v)) instead of v (store epilogue only)
+};
+
+// Prologue applied to the activations while they are staged, and epilogue of
+// each row sum.
+constexpr int kXPlain = 0;     // x
+constexpr int kXNorm = 1;      // RMSNorm: (x * 1/sqrt(mean(x^2) + eps)) * norm_w
+constexpr int kXMul = 2;       // x * x2 (SwiGLU's product, with silu applied upstream)
+constexpr int kEStore = 0;     // y = v
+constexpr int kEAdd = 1;       // y += v (residual)
+
+struct RowsArgs {
+    RowsSeg seg[3];
+    const float *x;
+    const float *x2;       // kXMul
+    const float *norm_w;   // kXNorm
+    float eps;
     int N, K, bs_shift, S, G;
 };
 
+// Segment of stacked row r and its row within the segment.
+struct RowRef {
+    const uint8_t *w;
+    const float *absmax;
+    int local;
+};
+
+__device__ __forceinline__ RowRef row_ref(const RowsArgs &a, int r) {
+    const bool s1 = r >= a.seg[0].end, s2 = r >= a.seg[1].end;
+    RowRef f;
+    f.w = s2 ? a.seg[2].w : s1 ? a.seg[1].w : a.seg[0].w;
+    f.absmax = s2 ? a.seg[2].absmax : s1 ? a.seg[1].absmax : a.seg[0].absmax;
+    f.local = r - (s2 ? a.seg[1].end : s1 ? a.seg[0].end : 0);
+    return f;
+}
+
 template <int FMT>
 __device__ __forceinline__ void load_row(RowWords<FMT> &d, const RowsArgs &a, int row, int k0, int lane_blk) {
+    const RowRef f = row_ref(a, row);
+    const size_t local = static_cast<size_t>(f.local);
     if constexpr (FMT == kFmtNF4) {
         const size_t row_bytes = static_cast<size_t>(a.K) >> 1;
-        d.q = load_stream16(a.w + row * row_bytes + (k0 >> 1));
-        d.s = a.absmax[(static_cast<size_t>(row) * a.K + k0) >> a.bs_shift];
+        d.q = load_stream16(f.w + local * row_bytes + (k0 >> 1));
+        d.s = f.absmax[(local * a.K + k0) >> a.bs_shift];
     } else {
         constexpr int BB = FMT == kFmtQ4 ? 18 : 34;
         const size_t row_bytes = static_cast<size_t>(a.K >> 5) * BB;
         // Pair start (4-byte aligned) + 16 (Q4_0) or 32 (Q8_0) for the odd lane.
-        const uint8_t *p = a.w + row * row_bytes + static_cast<size_t>(lane_blk >> 1) * (2 * BB) +
+        const uint8_t *p = f.w + local * row_bytes + static_cast<size_t>(lane_blk >> 1) * (2 * BB) +
                            (lane_blk & 1) * (BB - 2);
         if constexpr (FMT == kFmtQ4) {
             d.a = load_stream16_a4(p);
@@ -198,15 +236,22 @@ __device__ __forceinline__ void build_pair_table(float2 *tbl2, int tid) {
     }
 }
 
-template <int FMT, int T, int PF, int W>
+__device__ __forceinline__ float silu_ref(float g) {
+    // GGUFVectorOps.swiGLU's gate: g / (1 + Math.exp(-g)), exp in double.
+    return g / (1.0f + static_cast<float>(exp(-static_cast<double>(g))));
+}
+
+template <int FMT, int T, int PF, int W, int XOP, int EPI>
 __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
-    static_assert(T >= 1 && T <= 16 && PF >= 1 && (W == 8 || W == 16), "tile shape");
-    constexpr int TP = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16;   // butterfly width
+    static_assert(T >= 1 && T <= 32 && PF >= 1 && (W == 8 || W == 16), "tile shape");
+    constexpr int TP = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : T <= 16 ? 16 : 32;   // butterfly width
     extern __shared__ float4 smem[];    // 4-bit: pair table (x windows alias it); Q8_0: x windows
-    __shared__ float part[W][16];
+    __shared__ float part[W][TP];
+    __shared__ float ssq[8];            // kXNorm: per-chunk sums of squares
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // Wave-uniform in a scalar register, so row and segment arithmetic is scalar.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int S = a.S;
     const int chunk = wave % S;
     const int grp = wave / S;
@@ -214,7 +259,8 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
 
     if (grp >= a.G) {
         // Helper wave (when S does not divide 8): takes part in the table
-        // build and meets the same four workgroup barriers, nothing else.
+        // build and meets the same workgroup barriers, nothing else.
+        if constexpr (XOP == kXNorm) __syncthreads();        // 0: chunk sums of squares
         __syncthreads();                                     // 1: x staged
         __syncthreads();                                     // 2: x read
         if constexpr (FMT != kFmtQ8) build_pair_table<FMT, W * 64>(tbl2, tid);
@@ -235,17 +281,55 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
 
     // Activations first (vmcnt retires in order: waiting for them then
     // leaves the weight loads in flight).
-    const f32x4 *xw = reinterpret_cast<const f32x4 *>(a.x + chunk * kChunk);
-    f32x4 xl[8];
+    const int xoff = chunk * kChunk;
+    f32x4 xl[8], xm[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) xl[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < 8; ++j) xl[j] = xm[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (stager) {
+        const f32x4 *xw = reinterpret_cast<const f32x4 *>(a.x + xoff);
 #pragma unroll
         for (int j = 0; j < 8; ++j) xl[j] = xw[64 * j + lane];
+        if constexpr (XOP != kXPlain) {
+            const f32x4 *mw = reinterpret_cast<const f32x4 *>((XOP == kXNorm ? a.norm_w : a.x2) + xoff);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xm[j] = mw[64 * j + lane];
+        }
     }
     RowWords<FMT> rw[T];
 #pragma unroll
     for (int t = 0; t < PF && t < T; ++t) load_row<FMT>(rw[t], a, min(row0 + t * rstride, a.N - 1), k0, lane_blk);
+
+    if constexpr (XOP == kXNorm) {
+        // RMSNorm over the whole row of K activations: chunk sums of squares
+        // through LDS, then x * (1/sqrt(mean + eps)) * w in the same order as
+        // the stand-alone RMSNorm kernel.
+        if (stager) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                ss = fmaf(xl[j].x, xl[j].x, ss);
+                ss = fmaf(xl[j].y, xl[j].y, ss);
+                ss = fmaf(xl[j].z, xl[j].z, ss);
+                ss = fmaf(xl[j].w, xl[j].w, ss);
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) ssq[chunk] = ss;
+        }
+        __syncthreads();                                     // 0
+        if (stager) {
+            float tot = 0.0f;
+            for (int c = 0; c < S; ++c) tot += ssq[c];
+            const float inv =
+                1.0f / static_cast<float>(sqrt(static_cast<double>(tot / static_cast<float>(a.K) + a.eps)));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xl[j] = (xl[j] * inv) * xm[j];
+        }
+    } else if constexpr (XOP == kXMul) {
+        if (stager) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xl[j] = xl[j] * xm[j];
+        }
+    }
 
     // Stage x: float4 f of chunk c at slot c*512 + (f/8)*8 + ((f%8) ^ ((f/8)%8)).
     if (stager) {
@@ -299,10 +383,19 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     if (lane < TP) part[wave][wave_rows_index<TP>(lane)] = tot;
     __syncthreads();                                         // 4
     // The S chunk waves of group g are waves g*S .. g*S+S-1.
-    if (chunk == 0 && lane < T && row0 + lane * rstride < a.N) {
+    const int r = row0 + lane * rstride;
+    if (chunk == 0 && lane < T && r < a.N) {
         float v = 0.0f;
         for (int c = 0; c < S; ++c) v += part[grp * S + c][lane];
-        a.y[row0 + lane * rstride] = v;
+        const bool s1 = r >= a.seg[0].end, s2 = r >= a.seg[1].end;
+        float *y = s2 ? a.seg[2].y : s1 ? a.seg[1].y : a.seg[0].y;
+        const int local = r - (s2 ? a.seg[1].end : s1 ? a.seg[0].end : 0);
+        if constexpr (EPI == kEAdd) {
+            y[local] += v;
+        } else {
+            const int act = s2 ? a.seg[2].silu : s1 ? a.seg[1].silu : a.seg[0].silu;
+            y[local] = act ? silu_ref(v) : v;
+        }
     }
 }
 
@@ -311,10 +404,10 @@ int env_int(const char *name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
-template <int FMT, int T, int PF, int W>
+template <int FMT, int T, int PF, int W, int XOP, int EPI>
 void launch_cfg(const RowsArgs &args, hipStream_t s) {
     static const int pad = env_int("ALJABR_ROCM_ROWS_LDS", 0);   // dynamic LDS floor (bytes), sweeps only
-    const void *fn = reinterpret_cast<const void *>(rows_kernel<FMT, T, PF, W>);
+    const void *fn = reinterpret_cast<const void *>(rows_kernel<FMT, T, PF, W, XOP, EPI>);
     size_t lds = FMT == kFmtQ8 ? static_cast<size_t>(args.S) * 512 * sizeof(float4) : kPairBytes;
     if (pad > 0 && static_cast<size_t>(pad) > lds && pad <= 150 * 1024) lds = pad;
     static bool lds_set = false;                 // the attribute is per kernel, per process
@@ -324,47 +417,58 @@ void launch_cfg(const RowsArgs &args, hipStream_t s) {
     }
     const int rows_per_wg = args.G * T;
     const dim3 grid((args.N + rows_per_wg - 1) / rows_per_wg), block(W * 64);
-    hipLaunchKernelGGL((rows_kernel<FMT, T, PF, W>), grid, block, lds, s, args);
+    hipLaunchKernelGGL((rows_kernel<FMT, T, PF, W, XOP, EPI>), grid, block, lds, s, args);
 }
 
-// T rows per wave (even, 2..16), loads PF = min(T, 4) rows ahead, 8 waves.
-template <int FMT>
+// T rows per wave (2..32), loads PF = min(T, 4) rows ahead, 8 waves.
+template <int FMT, int XOP, int EPI>
 void launch_rows(RowsArgs args, int T, hipStream_t s) {
     args.G = 8 / args.S;
     switch (T) {
-    case 16: launch_cfg<FMT, 16, 4, 8>(args, s); break;
-    case 14: launch_cfg<FMT, 14, 4, 8>(args, s); break;
-    case 12: launch_cfg<FMT, 12, 4, 8>(args, s); break;
-    case 10: launch_cfg<FMT, 10, 4, 8>(args, s); break;
-    case 8: launch_cfg<FMT, 8, 4, 8>(args, s); break;
-    case 7: launch_cfg<FMT, 7, 4, 8>(args, s); break;
-    case 6: launch_cfg<FMT, 6, 4, 8>(args, s); break;
-    case 4: launch_cfg<FMT, 4, 2, 8>(args, s); break;
-    default: launch_cfg<FMT, 2, 2, 8>(args, s); break;
+    case 32: launch_cfg<FMT, 32, 4, 8, XOP, EPI>(args, s); break;
+    case 28: launch_cfg<FMT, 28, 4, 8, XOP, EPI>(args, s); break;
+    case 24: launch_cfg<FMT, 24, 4, 8, XOP, EPI>(args, s); break;
+    case 20: launch_cfg<FMT, 20, 4, 8, XOP, EPI>(args, s); break;
+    case 16: launch_cfg<FMT, 16, 4, 8, XOP, EPI>(args, s); break;
+    case 14: launch_cfg<FMT, 14, 4, 8, XOP, EPI>(args, s); break;
+    case 12: launch_cfg<FMT, 12, 4, 8, XOP, EPI>(args, s); break;
+    case 10: launch_cfg<FMT, 10, 4, 8, XOP, EPI>(args, s); break;
+    case 8: launch_cfg<FMT, 8, 4, 8, XOP, EPI>(args, s); break;
+    case 7: launch_cfg<FMT, 7, 4, 8, XOP, EPI>(args, s); break;
+    case 6: launch_cfg<FMT, 6, 4, 8, XOP, EPI>(args, s); break;
+    case 4: launch_cfg<FMT, 4, 2, 8, XOP, EPI>(args, s); break;
+    default: launch_cfg<FMT, 2, 2, 8, XOP, EPI>(args, s); break;
     }
 }
 
 // Rows per wave: the per-workgroup set-up (activation staging, the 64 KiB
 // pair table) is paid once per workgroup, and measured on MI355X the fastest
 // shape is one 8-wave workgroup per CU, each taking N/CUs rows: T =
-// ceil(N / (G * CUs)) rounded up to even, at most 16 (beyond that more
-// workgroups). ALJABR_ROCM_ROWS_T overrides for sweeps.
-int pick_rows_t(int N, int S) {
+// ceil(N / (G * CUs)) rounded up to even (to a multiple of 4 above 16), at
+// most `cap` (beyond that more workgroups). ALJABR_ROCM_ROWS_T overrides for
+// sweeps.
+int pick_rows_t(int N, int S, int cap) {
     static const int env_t = env_int("ALJABR_ROCM_ROWS_T", 0);
-    if (env_t >= 2 && env_t <= 16 && (env_t % 2 == 0 || env_t == 7)) return env_t;
+    if (env_t >= 2 && env_t <= 32 && (env_t % 2 == 0 || env_t == 7) && (env_t <= 16 || env_t % 4 == 0))
+        return env_t;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     const long long per = static_cast<long long>(8 / S) * cus;
     int t = static_cast<int>((N + per - 1) / per);
     t = (t + 1) & ~1;
-    return t < 2 ? 2 : t > 16 ? 16 : t;
+    if (t > 16) t = (t + 3) & ~3;
+    return t < 2 ? 2 : t > cap ? cap : t;
+}
+
+bool rows_shape_ok(const float *A, int K) {
+    const int S = K / kChunk;
+    return K % kChunk == 0 && S >= 1 && S <= 8 && aligned(A, 16);
 }
 
 }  // namespace
 
 int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax, int K, int N, int type,
                  int bs_shift) {
-    const int S = K / kChunk;
-    if (K % kChunk != 0 || S < 1 || S > 8 || !aligned(A, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    if (!rows_shape_ok(A, K)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     int fmt;
     if (type == ALJABR_ROCM_TYPE_NF4) {
         if (bs_shift < 5 || !aligned(W, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
@@ -375,13 +479,60 @@ int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax
     } else {
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     }
-    RowsArgs args{C, A, W, absmax, N, K, bs_shift, S, 0};
-    const int T = pick_rows_t(N, S);
+    RowsArgs args{};
+    args.seg[0] = RowsSeg{W, absmax, C, N, 0};
+    args.seg[1].end = args.seg[2].end = 0x7fffffff;
+    args.x = A;
+    args.N = N;
+    args.K = K;
+    args.bs_shift = bs_shift;
+    args.S = K / kChunk;
+    const int T = pick_rows_t(N, args.S, 16);
     hipStream_t s = current_stream();
     switch (fmt) {
-    case kFmtNF4: launch_rows<kFmtNF4>(args, T, s); break;
-    case kFmtQ4: launch_rows<kFmtQ4>(args, T, s); break;
-    default: launch_rows<kFmtQ8>(args, T, s); break;
+    case kFmtNF4: launch_rows<kFmtNF4, kXPlain, kEStore>(args, T, s); break;
+    case kFmtQ4: launch_rows<kFmtQ4, kXPlain, kEStore>(args, T, s); break;
+    default: launch_rows<kFmtQ8, kXPlain, kEStore>(args, T, s); break;
+    }
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const float *x2, const float *norm_w,
+                           float eps, int K, int bs_shift, int prologue, int accumulate) {
+    if (nseg < 1 || nseg > 3 || !rows_shape_ok(x, K) || bs_shift < 5) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    if (prologue == kRowsNorm && (!norm_w || !aligned(norm_w, 16))) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    if (prologue == kRowsMul && (!x2 || !aligned(x2, 16))) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    RowsArgs args{};
+    long long end = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (i < nseg) {
+            if (!aligned(outs[i].w, 16) || outs[i].n <= 0 || (accumulate && outs[i].silu))
+                return ALJABR_ROCM_ERR_UNSUPPORTED;
+            end += outs[i].n;
+            if (end > 0x7ffffffeLL) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            args.seg[i] = RowsSeg{outs[i].w, outs[i].absmax, outs[i].y, static_cast<int>(end), outs[i].silu};
+        } else {
+            args.seg[i].end = 0x7fffffff;
+        }
+    }
+    args.x = x;
+    args.x2 = x2;
+    args.norm_w = norm_w;
+    args.eps = eps;
+    args.N = static_cast<int>(end);
+    args.K = K;
+    args.bs_shift = bs_shift;
+    args.S = K / kChunk;
+    const int T = pick_rows_t(args.N, args.S, 32);
+    hipStream_t s = current_stream();
+    if (accumulate) {
+        if (prologue == kRowsMul) launch_rows<kFmtNF4, kXMul, kEAdd>(args, T, s);
+        else if (prologue == kRowsPlain) launch_rows<kFmtNF4, kXPlain, kEAdd>(args, T, s);
+        else return ALJABR_ROCM_ERR_UNSUPPORTED;
+    } else {
+        if (prologue == kRowsNorm) launch_rows<kFmtNF4, kXNorm, kEStore>(args, T, s);
+        else if (prologue == kRowsPlain) launch_rows<kFmtNF4, kXPlain, kEStore>(args, T, s);
+        else return ALJABR_ROCM_ERR_UNSUPPORTED;
     }
     return ALJABR_ROCM_OK;
 }

@@ -28,17 +28,88 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     return t;
 }
 
-// One workgroup per row.
+// One workgroup per row. With len % 4 == 0 and 16-byte aligned rows every
+// thread issues its float4 loads back to back (four in flight) instead of one
+// dependent scalar load per trip. The workgroups also clear up to three
+// buffers (`zero`) for outputs that the next kernels accumulate into.
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ x,
-                                                           const float *__restrict__ w, int len, float eps) {
+                                                           const float *__restrict__ w, int len, float eps,
+                                                           ZeroList zero) {
     __shared__ float red[kThreads / 64];
     const float *xr = x + static_cast<long long>(blockIdx.x) * len;
     float *orow = out + static_cast<long long>(blockIdx.x) * len;
+    const bool vec = (len & 3) == 0 && ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(orow) |
+                                         reinterpret_cast<uintptr_t>(w)) & 15) == 0;
+    const int n4 = len >> 2;
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < len; i += kThreads) ss = fmaf(xr[i], xr[i], ss);
+    if (vec) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+        for (int base = threadIdx.x; base < n4; base += 4 * kThreads) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = base + u * kThreads;
+                v[u] = i < n4 ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                ss = fmaf(v[u].x, v[u].x, ss);
+                ss = fmaf(v[u].y, v[u].y, ss);
+                ss = fmaf(v[u].z, v[u].z, ss);
+                ss = fmaf(v[u].w, v[u].w, ss);
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < len; i += kThreads) ss = fmaf(xr[i], xr[i], ss);
+    }
     ss = block_sum(ss, red);
     const float scale = 1.0f / static_cast<float>(sqrt(static_cast<double>(ss / static_cast<float>(len) + eps)));
-    for (int i = threadIdx.x; i < len; i += kThreads) orow[i] = (xr[i] * scale) * w[i];
+    if (vec) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+        const float4 *w4 = reinterpret_cast<const float4 *>(w);
+        float4 *o4 = reinterpret_cast<float4 *>(orow);
+        for (int base = threadIdx.x; base < n4; base += 4 * kThreads) {
+            float4 v[4], g[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = base + u * kThreads;
+                if (i < n4) {
+                    v[u] = x4[i];
+                    g[u] = w4[i];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = base + u * kThreads;
+                if (i < n4)
+                    o4[i] = make_float4((v[u].x * scale) * g[u].x, (v[u].y * scale) * g[u].y,
+                                        (v[u].z * scale) * g[u].z, (v[u].w * scale) * g[u].w);
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < len; i += kThreads) orow[i] = (xr[i] * scale) * w[i];
+    }
+    const long long gtid = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+    const long long gsize = static_cast<long long>(gridDim.x) * kThreads;
+#pragma unroll
+    for (int b = 0; b < 3; ++b) {
+        float *p = zero.p[b];
+        if (!p) continue;
+        for (long long i = gtid; i < zero.n[b]; i += gsize) p[i] = 0.0f;
+    }
+}
+
+// Split-half rotation of the pair (i, i + D/2) at position `pos`
+// (GGUFVectorOps.rope :383-440): invFreq = base^(-2i/D) and cos/sin in double.
+__device__ __forceinline__ void rope_pair(float &x0, float &x1, int pos, int i, int head_dim, float base) {
+    const float exponent = -2.0f * static_cast<float>(i) / static_cast<float>(head_dim);
+    const float inv_freq = static_cast<float>(pow(static_cast<double>(base), static_cast<double>(exponent)));
+    const float theta = static_cast<float>(pos) * inv_freq;
+    const float c = static_cast<float>(cos(static_cast<double>(theta)));
+    const float s = static_cast<float>(sin(static_cast<double>(theta)));
+    const float a = x0, b = x1;
+    x0 = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+    x1 = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
 }
 
 // One thread per (row, head, pair i < half).
@@ -51,15 +122,49 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ x, c
     const int i = static_cast<int>(t % half);
     const long long rh = t / half;   // row * n_heads + head
     const int row = static_cast<int>(rh / n_heads);
-    const float exponent = -2.0f * static_cast<float>(i) / static_cast<float>(head_dim);
-    const float inv_freq = static_cast<float>(pow(static_cast<double>(base), static_cast<double>(exponent)));
-    const float theta = static_cast<float>(pos[row]) * inv_freq;
-    const float c = static_cast<float>(cos(static_cast<double>(theta)));
-    const float s = static_cast<float>(sin(static_cast<double>(theta)));
     float *p = x + rh * head_dim;
-    const float x0 = p[i], x1 = p[i + half];
-    p[i] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
-    p[i + half] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+    float x0 = p[i], x1 = p[i + half];
+    rope_pair(x0, x1, pos[row], i, head_dim, base);
+    p[i] = x0;
+    p[i + half] = x1;
+}
+
+__device__ __forceinline__ uint16_t to_f16_bits(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+// The decode step's RoPE + KV append in one launch: workgroup (slot, b) with
+// D/2 threads; slots [0, nh) rotate query heads in place, [nh, nh + nkv)
+// rotate key heads and store them as fp16 at cache row pos[b], and
+// [nh + nkv, nh + 2 nkv) store value heads. Same arithmetic as rope_kernel
+// followed by kv_append_kernel.
+__global__ void rope_append_kernel(float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+                                   uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, const int *__restrict__ pos,
+                                   int nh, int nkv, int head_dim, int cap, float base) {
+    const int slot = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
+    const int half = head_dim / 2;
+    const int p = pos[b];
+    if (slot < nh) {
+        float *x = q + (static_cast<long long>(b) * nh + slot) * head_dim;
+        float x0 = x[i], x1 = x[i + half];
+        rope_pair(x0, x1, p, i, head_dim, base);
+        x[i] = x0;
+        x[i + half] = x1;
+        return;
+    }
+    if (p < 0 || p >= cap) return;   // outside the cache: nothing to store
+    const int h = slot < nh + nkv ? slot - nh : slot - nh - nkv;
+    const long long src = (static_cast<long long>(b) * nkv + h) * head_dim;
+    const long long dst = ((static_cast<long long>(b) * nkv + h) * cap + p) * head_dim;
+    if (slot < nh + nkv) {
+        float x0 = k[src + i], x1 = k[src + i + half];
+        rope_pair(x0, x1, p, i, head_dim, base);
+        kc[dst + i] = to_f16_bits(x0);
+        kc[dst + i + half] = to_f16_bits(x1);
+    } else {
+        vc[dst + i] = to_f16_bits(v[src + i]);
+        vc[dst + i + half] = to_f16_bits(v[src + i + half]);
+    }
 }
 
 __global__ __launch_bounds__(kThreads) void swiglu_kernel(float *__restrict__ dst, const float *__restrict__ gate,
@@ -76,28 +181,49 @@ __global__ __launch_bounds__(kThreads) void add_kernel(float *__restrict__ a, co
     if (i < n) a[i] += b[i];
 }
 
-// One 1024-thread workgroup per row; ties resolve to the lowest index.
+__device__ __forceinline__ void argmax_take(float v, int i, float &best, int &bi) {
+    if (v > best || (v == best && i < bi)) {
+        best = v;
+        bi = i;
+    }
+}
+
+// One 1024-thread workgroup per row; ties resolve to the lowest index. Rows
+// of 16-byte aligned float4s are read eight loads per thread per trip.
 __global__ __launch_bounds__(1024) void argmax_kernel(int *__restrict__ out, const float *__restrict__ x, int cols) {
     __shared__ float sv[16];
     __shared__ int si[16];
     const float *row = x + static_cast<long long>(blockIdx.x) * cols;
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < cols; i += 1024) {
-        const float v = row[i];
-        if (v > best || (v == best && i < bi)) {
-            best = v;
-            bi = i;
+    if ((cols & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+        const float4 *r4 = reinterpret_cast<const float4 *>(row);
+        const int n4 = cols >> 2;
+        for (int base = threadIdx.x; base < n4; base += 8 * 1024) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = base + u * 1024;
+                v[u] = i < n4 ? r4[i] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (base + u * 1024 >= n4) break;
+                const int i = 4 * (base + u * 1024);
+                argmax_take(v[u].x, i, best, bi);
+                argmax_take(v[u].y, i + 1, best, bi);
+                argmax_take(v[u].z, i + 2, best, bi);
+                argmax_take(v[u].w, i + 3, best, bi);
+            }
         }
+    } else {
+        for (int i = threadIdx.x; i < cols; i += 1024) argmax_take(row[i], i, best, bi);
     }
     // Wave reduction with index tie-break.
     for (int off = 32; off >= 1; off >>= 1) {
         const float ov = __shfl_xor(best, off);
         const int oi = __shfl_xor(bi, off);
-        if (ov > best || (ov == best && oi < bi)) {
-            best = ov;
-            bi = oi;
-        }
+        argmax_take(ov, oi, best, bi);
     }
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
@@ -106,11 +232,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(int *__restrict__ out, con
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int k = 1; k < 16; ++k)
-            if (sv[k] > best || (sv[k] == best && si[k] < bi)) {
-                best = sv[k];
-                bi = si[k];
-            }
+        for (int k = 1; k < 16; ++k) argmax_take(sv[k], si[k], best, bi);
         out[blockIdx.x] = bi == 0x7fffffff ? 0 : bi;
     }
 }
@@ -142,8 +264,10 @@ inline unsigned blocks_for(long long n) { return static_cast<unsigned>((n + kThr
 
 }  // namespace
 
-int enqueue_rmsnorm(float *out, const float *x, const float *w, int rows, int len, float eps) {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, current_stream(), out, x, w, len, eps);
+int enqueue_rmsnorm(float *out, const float *x, const float *w, int rows, int len, float eps, const ZeroList *zero) {
+    ZeroList z{};
+    if (zero) z = *zero;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, current_stream(), out, x, w, len, eps, z);
     return ALJABR_ROCM_OK;
 }
 
@@ -172,6 +296,14 @@ int enqueue_argmax(int *out, const float *x, int rows, int cols) {
 int enqueue_embed(float *x, const float *embed, const int *tokens, int batch, int dim, int vocab) {
     const unsigned gx = static_cast<unsigned>((dim + kThreads - 1) / kThreads);
     hipLaunchKernelGGL(embed_kernel, dim3(gx, batch), dim3(kThreads), 0, current_stream(), x, embed, tokens, dim, vocab);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_rope_append(float *q, const float *k, const float *v, uint16_t *kc, uint16_t *vc, const int *pos, int batch,
+                        int nh, int nkv, int head_dim, int cap, float base) {
+    if (head_dim < 2 || head_dim % 2 != 0 || head_dim / 2 > 1024) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(rope_append_kernel, dim3(nh + 2 * nkv, batch), dim3(head_dim / 2), 0, current_stream(), q, k, v,
+                       kc, vc, pos, nh, nkv, head_dim, cap, base);
     return ALJABR_ROCM_OK;
 }
 

@@ -83,22 +83,32 @@ CONFIGS = [
          nf4_block=64, rope_base=500000.0, eps=1e-5),
     dict(layers=2, dim=1024, ffn=2048, n_heads=8, n_kv_heads=2, head_dim=128, vocab=4096,
          nf4_block=64, rope_base=500000.0, eps=1e-5),
+    # K = 2048 and 4096 everywhere: batch 1 runs the fused NF4 launches (RMSNorm
+    # prologue on Q/K/V and gate/up, silu epilogue, residual-add epilogues).
+    dict(layers=2, dim=2048, ffn=4096, n_heads=16, n_kv_heads=4, head_dim=128, vocab=1000,
+         nf4_block=64, rope_base=500000.0, eps=1e-5),
 ]
 
+# (config, batch): batch >= 2 takes the matrix-core GEMMs that add into
+# cleared or residual outputs; batch 1 the fused launches (config 2) or the
+# unfused composition (configs 0 and 1).
+CASES = [(0, 3), (1, 3), (0, 1), (2, 1), (2, 2)]
 
-@pytest.mark.parametrize("cfg", CONFIGS, ids=["hd64", "hd128"])
-def test_decode_step_matches_oracle(rocm, dev, oracle, cfg):
+
+@pytest.mark.parametrize("ci,batch", CASES, ids=[f"cfg{c}-b{b}" for c, b in CASES])
+def test_decode_step_matches_oracle(rocm, dev, oracle, ci, batch):
     import torch
     from aljabr_amd.llama import DeviceLlama, upload_weights
-    host = _host_model(oracle, cfg, seed=cfg["head_dim"])
-    batch, steps, max_seq = 3, 6, 16
+    cfg = CONFIGS[ci]
+    host = _host_model(oracle, cfg, seed=cfg["head_dim"] + ci)
+    steps, max_seq = 6, 16
     model = DeviceLlama(cfg, upload_weights(host), max_batch=batch, max_seq=max_seq)
     refs = [oracle.LlamaOracle(dict(cfg, max_seq=max_seq), host) for _ in range(batch)]
-    first = np.array([5, 17, 1999], np.int32) % cfg["vocab"]
+    first = (np.array([5, 17, 1999], np.int32) % cfg["vocab"])[:batch]
     # Sequences start at different steps, so one batch holds different
     # positions; before its start a sequence re-decodes position 0 with its
     # first token, which rewrites the same cache row (idempotent).
-    start = np.array([0, 1, 3], np.int32)
+    start = np.array([0, 1, 3], np.int32)[:batch]
     logits = torch.empty(batch * cfg["vocab"], dtype=torch.float32, device="cuda:0")
     cur = first.copy()
     for step in range(steps):
