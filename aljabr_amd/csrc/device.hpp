@@ -108,6 +108,13 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
+// operations, not for its global loads in flight (__syncthreads also drains
+// prefetched global loads, which a streaming loop cannot afford per tile).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // ({hi,lo} >> shift)[31:0], shift in [0,31] (v_alignbit_b32).
 __device__ __forceinline__ uint32_t funnel_shift_right(uint32_t hi, uint32_t lo, uint32_t shift) {
     return __builtin_amdgcn_alignbit(hi, lo, shift);

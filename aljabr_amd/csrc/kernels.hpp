@@ -59,6 +59,9 @@ int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const 
 // caller that has C cleared or holding a residual saves the clearing launch.
 int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
                      int M, bool accumulate = false);
+// fp16-weight small-M GEMM on MFMA (2 <= M <= 32, K in {512, 1024, 2048,
+// 4096}, W and A 16-byte aligned); deterministic (no atomics).
+int enqueue_f16_mfma(float *C, const float *A, const uint16_t *W, int K, int N, int M);
 // Persistent double-buffered batch-1 kernels (K <= 16384).
 int enqueue_nf4_stream(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift);
 int enqueue_gguf_stream(float *C, const float *A, const uint8_t *B, int K, int N, int type);

@@ -75,6 +75,20 @@ __device__ __forceinline__ half8 decode8(uint32_t w, uint32_t cl, const char *tb
     return __builtin_bit_cast(half8, r);
 }
 
+// Pair table: dword slot i = e*64 + r. Thread tid (of 512) fills slots
+// tid + 512k (k < 32): e = tid/64 + 8k, so its low nibble is tid/64 + 8*(k
+// odd) and its high nibble k/2.
+__device__ __forceinline__ void build_pair16_table(uint32_t *tbl_s, int tid) {
+    const float lo_a = nf4_level_sel(tid >> 6), lo_b = nf4_level_sel((tid >> 6) + 8);
+    constexpr float kNF4[16] = {
+        -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+        -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+        0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+        0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+#pragma unroll
+    for (int k = 0; k < 32; ++k) tbl_s[tid + kMmThreads * k] = pack_half2(kNF4[k >> 1], (k & 1) ? lo_b : lo_a);
+}
+
 // Loads of one work unit, coalesced (8 lanes read a whole 128-byte row
 // segment; the MFMA layout would touch 32 lines per instruction and stall
 // the texture path): instruction i covers rows 8i + lane/8 of the wave's
@@ -172,19 +186,7 @@ __global__ __launch_bounds__(kMmThreads) void nf4_mm_kernel(MmArgs a) {
 #pragma unroll
     for (int u = 0; u < W && u < U; ++u) issue_unit<ITERS, SB>(qc[u], sc[u / ITERS], a, r0[u / ITERS], u % ITERS, ks0, lane);
 
-    // Pair table: dword slot i = e*64 + r. Thread tid fills slots tid + 512k
-    // (k < 32): e = tid/64 + 8k, so its low nibble is tid/64 + 8*(k odd)
-    // and its high nibble k/2.
-    {
-        const float lo_a = nf4_level_sel(tid >> 6), lo_b = nf4_level_sel((tid >> 6) + 8);
-        constexpr float kNF4[16] = {
-            -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
-            -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
-            0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
-            0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
-#pragma unroll
-        for (int k = 0; k < 32; ++k) tbl_s[tid + kMmThreads * k] = pack_half2(kNF4[k >> 1], (k & 1) ? lo_b : lo_a);
-    }
+    build_pair16_table(tbl_s, tid);
     __syncthreads();
 
     const uint32_t cl = lane * 4;

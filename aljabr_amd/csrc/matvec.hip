@@ -480,6 +480,27 @@ int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float 
 }
 
 int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M) {
+    // fp16 rows with M >= 2 on the matrix cores, 32 tokens per pass.
+    if (type == ALJABR_ROCM_TYPE_F16 && M >= 2 && mfma_enabled()) {
+        const uint16_t *W = reinterpret_cast<const uint16_t *>(B);
+        bool ok = true;
+        for (int m0 = 0; m0 < M && ok; m0 += 32) {
+            const int mm = M - m0 < 32 ? M - m0 : 32;
+            int rc;
+            if (mm >= 2) {
+                rc = enqueue_f16_mfma(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, W, K, N, mm);
+                if (rc == ALJABR_ROCM_ERR_UNSUPPORTED && m0 == 0) {   // the shape checks do not depend on m0
+                    ok = false;
+                    break;
+                }
+            } else {
+                rc = enqueue_gguf_small(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, B, K, N,
+                                        type, 1);
+            }
+            if (rc != ALJABR_ROCM_OK) return rc;
+        }
+        if (ok) return ALJABR_ROCM_OK;
+    }
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mm = M - m0 < 8 ? M - m0 : 8;
         int rc = enqueue_gguf_small(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, B, K, N, type,

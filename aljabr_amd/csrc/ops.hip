@@ -32,9 +32,31 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 // thread issues its float4 loads back to back (four in flight) instead of one
 // dependent scalar load per trip. The workgroups also clear up to three
 // buffers (`zero`) for outputs that the next kernels accumulate into.
+__device__ __forceinline__ void zero_side_job(const ZeroList &zero) {
+    const long long gtid = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+    const long long gsize = static_cast<long long>(gridDim.x) * kThreads;
+#pragma unroll
+    for (int b = 0; b < 3; ++b) {
+        float *p = zero.p[b];
+        if (!p) continue;
+        const long long n = zero.n[b];
+        if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+            float4 *p4 = reinterpret_cast<float4 *>(p);
+            for (long long i = gtid; i < n / 4; i += gsize) p4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (long long i = (n / 4) * 4 + gtid; i < n; i += gsize) p[i] = 0.0f;
+        } else {
+            for (long long i = gtid; i < n; i += gsize) p[i] = 0.0f;
+        }
+    }
+}
+
+// Workgroups [0, rows) normalise one row each; workgroups beyond `rows` only
+// help with the clearing.
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ x,
-                                                           const float *__restrict__ w, int len, float eps,
+                                                           const float *__restrict__ w, int rows, int len, float eps,
                                                            ZeroList zero) {
+    zero_side_job(zero);
+    if (static_cast<int>(blockIdx.x) >= rows) return;
     __shared__ float red[kThreads / 64];
     const float *xr = x + static_cast<long long>(blockIdx.x) * len;
     float *orow = out + static_cast<long long>(blockIdx.x) * len;
@@ -88,14 +110,6 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(float *__restrict__ o
         }
     } else {
         for (int i = threadIdx.x; i < len; i += kThreads) orow[i] = (xr[i] * scale) * w[i];
-    }
-    const long long gtid = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
-    const long long gsize = static_cast<long long>(gridDim.x) * kThreads;
-#pragma unroll
-    for (int b = 0; b < 3; ++b) {
-        float *p = zero.p[b];
-        if (!p) continue;
-        for (long long i = gtid; i < zero.n[b]; i += gsize) p[i] = 0.0f;
     }
 }
 
@@ -167,13 +181,30 @@ __global__ void rope_append_kernel(float *__restrict__ q, const float *__restric
     }
 }
 
+__device__ __forceinline__ float swiglu_one(float g, float u) {
+    const float sg = g / (1.0f + static_cast<float>(exp(-static_cast<double>(g))));
+    return sg * u;
+}
+
+// Four elements per thread (float4) when all three arrays are 16-byte aligned.
 __global__ __launch_bounds__(kThreads) void swiglu_kernel(float *__restrict__ dst, const float *__restrict__ gate,
                                                           const float *__restrict__ up, long long n) {
-    const long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const float g = gate[i];
-    const float sg = g / (1.0f + static_cast<float>(exp(-static_cast<double>(g))));
-    dst[i] = sg * up[i];
+    const long long t = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+    const bool vec = ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(gate) |
+                       reinterpret_cast<uintptr_t>(up)) & 15) == 0;
+    if (vec) {
+        const long long i = 4 * t;
+        if (i + 3 < n) {
+            const float4 g = *reinterpret_cast<const float4 *>(gate + i);
+            const float4 u = *reinterpret_cast<const float4 *>(up + i);
+            *reinterpret_cast<float4 *>(dst + i) =
+                make_float4(swiglu_one(g.x, u.x), swiglu_one(g.y, u.y), swiglu_one(g.z, u.z), swiglu_one(g.w, u.w));
+        } else {
+            for (long long j = i; j < n; ++j) dst[j] = swiglu_one(gate[j], up[j]);
+        }
+    } else {
+        for (long long j = 4 * t; j < 4 * t + 4 && j < n; ++j) dst[j] = swiglu_one(gate[j], up[j]);
+    }
 }
 
 __global__ __launch_bounds__(kThreads) void add_kernel(float *__restrict__ a, const float *__restrict__ b, long long n) {
@@ -266,8 +297,15 @@ inline unsigned blocks_for(long long n) { return static_cast<unsigned>((n + kThr
 
 int enqueue_rmsnorm(float *out, const float *x, const float *w, int rows, int len, float eps, const ZeroList *zero) {
     ZeroList z{};
-    if (zero) z = *zero;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, current_stream(), out, x, w, len, eps, z);
+    long long zn = 0;
+    if (zero) {
+        z = *zero;
+        for (int b = 0; b < 3; ++b) zn += z.p[b] ? z.n[b] : 0;
+    }
+    // About 16 float4 stores per thread for the clearing.
+    const long long extra = (zn + 16LL * 4 * kThreads - 1) / (16LL * 4 * kThreads);
+    const unsigned grid = static_cast<unsigned>(rows + (extra > 1024 ? 1024 : extra));
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(grid), dim3(kThreads), 0, current_stream(), out, x, w, rows, len, eps, z);
     return ALJABR_ROCM_OK;
 }
 
@@ -279,7 +317,8 @@ int enqueue_rope(float *x, const int *pos, int rows, int n_heads, int head_dim, 
 }
 
 int enqueue_swiglu(float *dst, const float *gate, const float *up, long long n) {
-    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, current_stream(), dst, gate, up, n);
+    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for((n + 3) / 4)), dim3(kThreads), 0, current_stream(), dst, gate, up,
+                       n);
     return ALJABR_ROCM_OK;
 }
 

@@ -37,8 +37,8 @@ def test_rope_rows_and_positions(rocm, dev, oracle):
     assert np.array_equal(got[0], x.reshape(rows, -1)[0])       # position 0 is the identity
 
 
-def test_swiglu_and_add(rocm, dev, oracle):
-    n = 14336
+@pytest.mark.parametrize("n", [14336, 14339])
+def test_swiglu_and_add(rocm, dev, oracle, n):
     g, u = oracle.normal(4, n), oracle.normal(5, n)
     gd, ud, out = dev.put(g), dev.put(u), dev.empty(n)
     rocm.call("aljabr_rocm_swiglu", dev.ptr(out), dev.ptr(gd), dev.ptr(ud), n)

@@ -76,10 +76,15 @@ def test_gguf_matvec(rocm, dev, oracle, qtype, n, k, m):
 
 # NF4 small-M GEMM on the matrix cores (2 <= M <= 64 per pass, K % 512 == 0):
 # M across the m-tile boundaries (32, 64) and past one pass (65, 100), ragged
-# N, K-slices of 512 and 256, and the Llama MLP shapes at M = 16 and 64.
+# N, K-slices of 512 and 256, and the Llama MLP shapes at M = 16 and 64. K a
+# multiple of 2048 takes the persistent kernel: one K-range with an odd tile
+# count (257 x 2048), two or three K-ranges adding with atomics (1000 x 4096,
+# 300 x 6144), two-unit K-ranges (8200 x 4096: at least one tile per CU),
+# seven K-ranges (4096 x 14336) and two passes of 32 tokens (M = 33, 64).
 @pytest.mark.parametrize("n,k,m", [(300, 1024, 2), (300, 1024, 3), (257, 2048, 8), (300, 1024, 31), (300, 1024, 32),
                                    (300, 1024, 33), (129, 512, 64), (300, 1024, 65), (77, 1536, 100),
-                                   (14336, 4096, 16), (4096, 14336, 64)])
+                                   (14336, 4096, 16), (4096, 14336, 64), (1000, 4096, 5), (300, 6144, 17),
+                                   (8200, 4096, 32), (14336, 4096, 33), (257, 2048, 2)])
 def test_nf4_mfma_small_m(rocm, dev, oracle, n, k, m):
     codes, absmax = _nf4_case(oracle, n, k, seed=3)
     x = oracle.normal(71 + m, m * k)
@@ -144,6 +149,23 @@ def test_f16_rows(rocm, dev, oracle, n, k, m):
     y = dev.empty(m * n)
     rocm.call("aljabr_rocm_matvec_tb_batch", dev.ptr(y), dev.ptr(xd), dev.ptr(wd), k, n, rocm.TYPE_F16, m)
     assert rel_l2(dev.get(y), y_ref) <= TOL
+
+
+@pytest.mark.parametrize("n,k,m", [(1000, 512, 3), (4096 + 17, 1024, 32), (777, 2048, 33), (2048, 4096, 40),
+                                   (128256 // 8, 4096, 32), (100, 4096, 2)])
+def test_f16_mfma_small_m(rocm, dev, oracle, n, k, m):
+    """fp16 rows with M >= 2 on the matrix cores (activations rounded to fp16,
+    fp32 accumulation): every token row within the matvec tolerance, ragged
+    N tiles and M above one 32-row pass included."""
+    w = oracle.normal(51 + n, n * k).astype(np.float16).view(np.uint16)
+    x = oracle.normal(53 + m, m * k)
+    y_ref = np.asarray(oracle.f16_matvec(w, x, n, k)).ravel().reshape(m, n)
+    wd, xd = dev.put(w), dev.put(x)
+    y = dev.empty(m * n)
+    rocm.call("aljabr_rocm_matvec_tb_batch", dev.ptr(y), dev.ptr(xd), dev.ptr(wd), k, n, rocm.TYPE_F16, m)
+    got = dev.get(y).reshape(m, n)
+    for i in range(m):
+        assert rel_l2(got[i], y_ref[i]) <= TOL, i
 
 
 def test_batched_equals_repeated_single_rows(rocm, dev, oracle):
