@@ -17,6 +17,7 @@
 // output, otherwise (m, l, o) partials go to scratch and a merge kernel
 // combines splits. Scores use exp2 with log2(e) folded into the query.
 #include <cmath>
+#include <cstdlib>
 
 #include "device.hpp"
 #include "internal.hpp"
@@ -37,6 +38,38 @@ __device__ __forceinline__ float group_sum(float v) {
     v += dpp_f32<0x141>(v);
     if constexpr (LPK == 16) v += dpp_f32<0x140>(v);
     return v;
+}
+
+// Raw K/V slice of one key as loaded (8 fp16 or 8 fp32 values).
+template <bool F16> struct KvRaw;
+template <> struct KvRaw<true> { uint4 u; };
+template <> struct KvRaw<false> { float4 a, b; };
+
+template <bool F16>
+__device__ __forceinline__ KvRaw<F16> load_raw(const void *base, long long idx) {
+    KvRaw<F16> r;
+    if constexpr (F16) {
+        r.u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + idx);
+    } else {
+        r.a = *reinterpret_cast<const float4 *>(static_cast<const float *>(base) + idx);
+        r.b = *reinterpret_cast<const float4 *>(static_cast<const float *>(base) + idx + 4);
+    }
+    return r;
+}
+
+template <bool F16>
+__device__ __forceinline__ void raw_to_f32(const KvRaw<F16> &x, float (&r)[8]) {
+    if constexpr (F16) {
+        const uint32_t w[4] = {x.u.x, x.u.y, x.u.z, x.u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+            r[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+        }
+    } else {
+        r[0] = x.a.x; r[1] = x.a.y; r[2] = x.a.z; r[3] = x.a.w;
+        r[4] = x.b.x; r[5] = x.b.y; r[6] = x.b.z; r[7] = x.b.w;
+    }
 }
 
 template <bool F16>
@@ -76,13 +109,29 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
     const int grp = wave * GPW + lane / LPK;   // key group in workgroup
     const int sub = lane % LPK;                // 8-dim slice of the row
 
+    const int k_begin = split * chunk;
+    // Rows [k_begin, mem_end) exist in memory whatever the visible length,
+    // so the first tile's loads go out before kv_len has arrived.
+    const int mem_end = min(k_begin + chunk, p.kv_len ? p.cap : p.Sk);
+    const long long head_base = (static_cast<long long>(b) * p.Hkv + kvh) * p.cap * D + sub * 8;
+    KvRaw<F16> kn[kTile], vn[kTile];
+    auto issue = [&](int tbase) {
+#pragma unroll
+        for (int t = 0; t < kTile; ++t) {
+            const int key = tbase + t;
+            const int kk = key < mem_end ? key : k_begin;
+            kn[t] = load_raw<F16>(p.k, head_base + static_cast<long long>(kk) * D);
+            vn[t] = load_raw<F16>(p.v, head_base + static_cast<long long>(kk) * D);
+        }
+    };
+    issue(k_begin + grp * kTile);
+
     const int sk = p.kv_len ? min(max(p.kv_len[b], 0), p.cap) : p.Sk;   // never past the cache
     int limit = sk;
     if (p.causal) {
         const int c = sk - p.Sq + qi + 1;
         limit = c < sk ? c : sk;
     }
-    const int k_begin = split * chunk;
     int k_end = k_begin + chunk;
     if (k_end > limit) k_end = limit;
 
@@ -108,20 +157,27 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
         for (int i = 0; i < 8; ++i) o[g][i] = 0.0f;
     }
 
-    const long long head_base = (static_cast<long long>(b) * p.Hkv + kvh) * p.cap * D + sub * 8;
     const float *mrow = p.mask ? p.mask + static_cast<long long>(qi) * p.Sk : nullptr;
 
+    // Software pipeline: the next tile's K/V rows are loaded while this one
+    // is computed (the last trip loads a clamped, in-range tile it never
+    // uses: a conditional load would make the compiler drain the queue).
     for (int t0 = k_begin + grp * kTile; t0 < k_end; t0 += NG * kTile) {
         float kr[kTile][8], vr[kTile][8];
         bool valid[kTile];
 #pragma unroll
         for (int t = 0; t < kTile; ++t) {
-            const int key = t0 + t;
-            valid[t] = key < k_end;
-            const int kk = valid[t] ? key : k_begin;
-            load8<F16>(p.k, head_base + static_cast<long long>(kk) * D, kr[t]);
-            load8<F16>(p.v, head_base + static_cast<long long>(kk) * D, vr[t]);
+            valid[t] = t0 + t < k_end;
+            raw_to_f32<F16>(kn[t], kr[t]);
+            raw_to_f32<F16>(vn[t], vr[t]);
+            // Rows past the visible keys may hold anything (the first tile is
+            // loaded before the length is known, and cache rows beyond a
+            // sequence's length were never written): their values must not
+            // reach the sums, where 0 * NaN would still be NaN.
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vr[t][i] = valid[t] ? vr[t][i] : 0.0f;
         }
+        issue(t0 + NG * kTile);
         float add[kTile];
 #pragma unroll
         for (int t = 0; t < kTile; ++t) {
@@ -139,7 +195,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
 #pragma unroll
                 for (int i = 0; i < 8; ++i) d = fmaf(qv[g][i], kr[t][i], d);
                 d = group_sum<LPK>(d);
-                s[t] = d + add[t];
+                s[t] = valid[t] ? d + add[t] : -INFINITY;
                 tmax = fmaxf(tmax, s[t]);
             }
             const float mn = fmaxf(m[g], tmax);
@@ -383,11 +439,17 @@ int enqueue_attention(const AttnParams &p) {
             hipLaunchKernelGGL(attn_generic_kernel<false>, grid, dim3(64), 0, s, p);
         return ALJABR_ROCM_OK;
     }
-    // Enough workgroups to cover the CUs about twice, chunks of >= 64 keys.
+    // Enough workgroups to cover the CUs `per_cu` times, chunks of >= 64
+    // keys (ALJABR_ROCM_ATTN_WGS overrides per_cu, for sweeps).
+    static const int per_cu = [] {
+        const char *e = getenv("ALJABR_ROCM_ATTN_WGS");
+        const int v = e && *e ? atoi(e) : 2;
+        return v >= 1 && v <= 64 ? v : 2;
+    }();
     const long long items = static_cast<long long>(p.B) * p.Hkv * p.Sq;
     const int keys = p.kv_len ? p.cap : p.Sk;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-    long long want = (2LL * cus + items - 1) / items;
+    long long want = (static_cast<long long>(per_cu) * cus + items - 1) / items;
     const long long max_splits = (keys + 63) / 64;
     if (want > max_splits) want = max_splits;
     if (want < 1) want = 1;
@@ -403,8 +465,10 @@ int enqueue_attention(const AttnParams &p) {
         if (!part) return ALJABR_ROCM_ERR_BUFFER;
     }
     if (p.D == 64)
-        return p.kv_f16 ? launch_g<64, true>(p, G, splits, chunk, part, s) : launch_g<64, false>(p, G, splits, chunk, part, s);
-    return p.kv_f16 ? launch_g<128, true>(p, G, splits, chunk, part, s) : launch_g<128, false>(p, G, splits, chunk, part, s);
+        return p.kv_f16 ? launch_g<64, true>(p, G, splits, chunk, part, s)
+                        : launch_g<64, false>(p, G, splits, chunk, part, s);
+    return p.kv_f16 ? launch_g<128, true>(p, G, splits, chunk, part, s)
+                    : launch_g<128, false>(p, G, splits, chunk, part, s);
 }
 
 }  // namespace aljabr
