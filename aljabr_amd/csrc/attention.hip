@@ -279,19 +279,34 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(float *__restrict__ out
     const float *pm = part_ml + row * splits * 2;
     float m = -INFINITY, l = 0.0f;
     float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int s = sg; s < splits; s += SG) {
-        const float ms = pm[2 * s], ls = pm[2 * s + 1];
-        const float4 os = *reinterpret_cast<const float4 *>(po + s * D + 4 * j);
-        const float mn = fmaxf(m, ms);
-        if (mn == -INFINITY) continue;
-        const float a = m == -INFINITY ? 0.0f : exp2f(m - mn);
-        const float b = ms == -INFINITY ? 0.0f : exp2f(ms - mn);
-        l = fmaf(l, a, ls * b);
-        o.x = fmaf(o.x, a, os.x * b);
-        o.y = fmaf(o.y, a, os.y * b);
-        o.z = fmaf(o.z, a, os.z * b);
-        o.w = fmaf(o.w, a, os.w * b);
-        m = mn;
+    // Eight splits per trip with all their loads issued before any is used
+    // (one memory round trip per trip instead of one per split).
+    constexpr int U = 8;
+    for (int s0 = sg; s0 < splits; s0 += U * SG) {
+        float ms[U], ls[U];
+        float4 os[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = s0 + u * SG;
+            const int sc = s < splits ? s : sg;                 // in-range row, ignored below
+            ms[u] = pm[2 * sc];
+            ls[u] = pm[2 * sc + 1];
+            os[u] = *reinterpret_cast<const float4 *>(po + sc * D + 4 * j);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (s0 + u * SG >= splits) break;
+            const float mn = fmaxf(m, ms[u]);
+            if (mn == -INFINITY) continue;
+            const float a = m == -INFINITY ? 0.0f : exp2f(m - mn);
+            const float b = ms[u] == -INFINITY ? 0.0f : exp2f(ms[u] - mn);
+            l = fmaf(l, a, ls[u] * b);
+            o.x = fmaf(o.x, a, os[u].x * b);
+            o.y = fmaf(o.y, a, os[u].y * b);
+            o.z = fmaf(o.z, a, os[u].z * b);
+            o.w = fmaf(o.w, a, os[u].w * b);
+            m = mn;
+        }
     }
     st[sg][4 * j] = o.x;
     st[sg][4 * j + 1] = o.y;
