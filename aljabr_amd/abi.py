@@ -77,6 +77,12 @@ class LlamaWeights(ctypes.Structure):
 
 
 # name -> (restype, argtypes); every symbol declared in include/aljabr_rocm.h.
+class KernelStat(ctypes.Structure):
+    """aljabr_rocm_kernel_stat: one launch group of a profiled decode step."""
+    _fields_ = [("name", ctypes.c_char * 48), ("launches", ctypes.c_int32), ("us", ctypes.c_double),
+                ("bytes", ctypes.c_double)]
+
+
 SIGNATURES = {
     "aljabr_rocm_init": (_I, [_I]),
     "aljabr_rocm_shutdown": (_I, []),
@@ -113,6 +119,8 @@ SIGNATURES = {
                                       ctypes.POINTER(_P)]),
     "aljabr_rocm_llama_destroy": (_I, [_P]),
     "aljabr_rocm_llama_decode": (_I, [_P, _P, _P, _I, _P, _P]),
+    "aljabr_rocm_llama_decode_profile": (_I, [_P, _P, _P, _I, _P, _P, ctypes.POINTER(KernelStat), _I,
+                                              ctypes.POINTER(_I)]),
     "aljabr_rocm_llama_hidden": (_I, [_P, ctypes.POINTER(_P)]),
     "aljabr_rocm_llama_kv_cache": (_I, [_P, ctypes.POINTER(_P), ctypes.POINTER(_P)]),
 }

@@ -12,6 +12,7 @@
 // stream with no host round trip; sequences of a batch are decoded together,
 // so every weight byte is read once per step for the whole batch. The KV
 // cache is fp16 [layer][batch][kv_head][max_seq][head_dim].
+#include <algorithm>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -165,26 +166,73 @@ int aljabr_rocm_llama_kv_cache(aljabr_rocm_llama *m, void **k_cache, void **v_ca
     return ALJABR_ROCM_OK;
 }
 
-int aljabr_rocm_llama_decode(aljabr_rocm_llama *m, const void *tokens, const void *positions, int batch, void *logits,
-                             void *next_tokens) {
-    ALJ_CHECK_READY();
-    ALJ_REQUIRE(m && tokens && positions && next_tokens, "model, tokens, positions and next_tokens are required");
+}  // extern "C"
+
+namespace {
+
+// Optional per-launch-group timing of a step: an event after every group on
+// the step's stream, and the algorithmic bytes the group moves.
+struct StepProfiler {
+    std::vector<hipEvent_t> events;   // events[0] opens the step
+    std::vector<const char *> names;
+    std::vector<double> bytes;
+    size_t used = 0;
+    hipStream_t stream = nullptr;
+
+    int begin(hipStream_t s, size_t groups) {
+        stream = s;
+        while (events.size() < groups + 1) {
+            hipEvent_t e;
+            const hipError_t r = hipEventCreate(&e);
+            if (r != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "hipEventCreate: %s", hipGetErrorString(r));
+            events.push_back(e);
+        }
+        used = 0;
+        names.clear();
+        bytes.clear();
+        return record();
+    }
+    int record() {
+        if (used >= events.size()) return fail(ALJABR_ROCM_ERR_BUFFER, "decode profile: out of events");
+        const hipError_t r = hipEventRecord(events[used++], stream);
+        return r == hipSuccess ? ALJABR_ROCM_OK : fail(ALJABR_ROCM_ERR_DEVICE, "hipEventRecord: %s", hipGetErrorString(r));
+    }
+    int mark(const char *name, double b) {
+        names.push_back(name);
+        bytes.push_back(b);
+        return record();
+    }
+    ~StepProfiler() {
+        for (hipEvent_t e : events) (void)hipEventDestroy(e);
+    }
+};
+
+// NF4 weight bytes of an [n, k] matrix: codes + fp32 absmax.
+double nf4_w(long long n, long long k, int bs) { return static_cast<double>(n * k / 2 + n * k / bs * 4); }
+
+int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, float *lg, int *next,
+                StepProfiler *prof, const int *host_pos) {
     const aljabr_rocm_llama_config &c = m->cfg;
-    ALJ_REQUIRE(batch > 0 && batch <= c.max_batch, "batch %d outside [1, %d]", batch, c.max_batch);
-    const int *pos = static_cast<const int *>(positions);
-    const int *tok = static_cast<const int *>(tokens);
-    const int B = batch, dim = c.dim, hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv_heads;
+    const int dim = c.dim, hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv_heads;
     const int qd = nh * hd, kvd = nkv * hd, ffn = c.ffn, bs = c.nf4_block;
     const int shift = log2_exact(bs);
     const size_t layer_cache = static_cast<size_t>(c.max_batch) * kvd * c.max_seq;
-    float *lg = logits ? static_cast<float *>(logits) : m->logits;
+    const double f4 = 4.0;
     int rc;
 #define ALJ_TRY(expr)                           \
     do {                                        \
         rc = (expr);                            \
         if (rc != ALJABR_ROCM_OK) return rc;    \
     } while (0)
+#define ALJ_MARK(name, b)                                   \
+    do {                                                    \
+        if (prof) ALJ_TRY(prof->mark((name), (b)));         \
+    } while (0)
     hipStream_t s = current_stream();
+    // Visible keys summed over the batch (profiling only: bytes of the KV rows read).
+    double keys = 0.0;
+    if (host_pos)
+        for (int b = 0; b < B; ++b) keys += std::min(host_pos[b] + 1, c.max_seq);
     // y = x . W^T (y cleared beforehand) or, with `residual`, y += x . W^T for
     // B rows. The matrix cores' K-slices add straight into y in both cases;
     // elsewhere y is written, or the products go to `tmp` and one add follows.
@@ -201,9 +249,15 @@ int aljabr_rocm_llama_decode(aljabr_rocm_llama *m, const void *tokens, const voi
         if (r != ALJABR_ROCM_OK) return r;
         return enqueue_add(y, tmp, static_cast<long long>(B) * N);
     };
+    // Bytes of one B-row NF4 product: weights once, activations in, outputs
+    // out (read too when added into).
+    auto mm_bytes = [&](long long N, long long K, bool add) {
+        return nf4_w(N, K, bs) + B * (K + N * (add ? 2.0 : 1.0)) * f4;
+    };
     const bool fused1 = B == 1 && m->rows_fused;
     hipLaunchKernelGGL(lengths_from_positions, dim3((B + 63) / 64), dim3(64), 0, s, m->kv_len, pos, B);
     ALJ_TRY(enqueue_embed(m->x, static_cast<const float *>(m->tok_embed), tok, B, dim, c.vocab));
+    ALJ_MARK("embed", B * dim * 2.0 * f4);
     for (int l = 0; l < c.layers; ++l) {
         auto W = [&](const std::vector<const void *> &t) { return static_cast<const uint8_t *>(t[l]); };
         auto S = [&](const std::vector<const void *> &t) { return static_cast<const float *>(t[l]); };
@@ -215,14 +269,19 @@ int aljabr_rocm_llama_decode(aljabr_rocm_llama *m, const void *tokens, const voi
                                     {m->k, W(m->wk), S(m->wk_s), kvd, 0},
                                     {m->v, W(m->wv), S(m->wv_s), kvd, 0}};
             ALJ_TRY(enqueue_nf4_rows_fused(qkv, 3, m->x, nullptr, S(m->attn_norm), c.eps, dim, shift, kRowsNorm, 0));
+            ALJ_MARK("qkv_rows_rmsnorm", nf4_w(qd + 2LL * kvd, dim, bs) + (2.0 * dim + qd + 2 * kvd) * f4);
         } else {
             const ZeroList z{{m->q, m->k, m->v},
                              {static_cast<long long>(B) * qd, static_cast<long long>(B) * kvd,
                               static_cast<long long>(B) * kvd}};
             ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, S(m->attn_norm), B, dim, c.eps, &z));
+            ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * (qd + 2.0 * kvd)) * f4);
             ALJ_TRY(mm(m->q, m->xb, m->wq[l], m->wq_s[l], dim, qd, false, nullptr));
+            ALJ_MARK("q_gemm", mm_bytes(qd, dim, true));
             ALJ_TRY(mm(m->k, m->xb, m->wk[l], m->wk_s[l], dim, kvd, false, nullptr));
+            ALJ_MARK("kv_gemm", mm_bytes(kvd, dim, true));
             ALJ_TRY(mm(m->v, m->xb, m->wv[l], m->wv_s[l], dim, kvd, false, nullptr));
+            ALJ_MARK("kv_gemm", mm_bytes(kvd, dim, true));
         }
         rc = enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base);
         if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
@@ -233,6 +292,7 @@ int aljabr_rocm_llama_decode(aljabr_rocm_llama *m, const void *tokens, const voi
         } else if (rc != ALJABR_ROCM_OK) {
             return rc;
         }
+        ALJ_MARK("rope_kv_append", B * (2.0 * qd + 2.0 * kvd) * f4 + B * 2.0 * kvd * 2.0);
         AttnParams ap{};
         ap.out = m->att;
         ap.q = m->q;
@@ -245,36 +305,108 @@ int aljabr_rocm_llama_decode(aljabr_rocm_llama *m, const void *tokens, const voi
         ap.causal = 0;
         ap.kv_f16 = 1;
         ALJ_TRY(enqueue_attention(ap));
+        ALJ_MARK("attention", keys * nkv * hd * 2.0 * 2.0 + B * 2.0 * qd * f4);
         // x += Wo att.
         if (fused1) {
             const RowsOut o = {m->x, W(m->wo), S(m->wo_s), dim, 0};
             ALJ_TRY(enqueue_nf4_rows_fused(&o, 1, m->att, nullptr, nullptr, 0.0f, qd, shift, kRowsPlain, 1));
+            ALJ_MARK("wo_rows_add", mm_bytes(dim, qd, true));
         } else {
             ALJ_TRY(mm(m->x, m->att, m->wo[l], m->wo_s[l], qd, dim, true, m->xb));
+            ALJ_MARK("wo_gemm_add", mm_bytes(dim, qd, true));
         }
         // MLP: x += Wdown (silu(Wgate xb) * Wup xb), xb = RMSNorm(x).
         if (fused1) {
             const RowsOut gu[2] = {{m->gate, W(m->w_gate), S(m->w_gate_s), ffn, 1},
                                    {m->up, W(m->w_up), S(m->w_up_s), ffn, 0}};
             ALJ_TRY(enqueue_nf4_rows_fused(gu, 2, m->x, nullptr, S(m->ffn_norm), c.eps, dim, shift, kRowsNorm, 0));
+            ALJ_MARK("gate_up_rows_rmsnorm_silu", nf4_w(2LL * ffn, dim, bs) + (2.0 * dim + 2.0 * ffn) * f4);
             const RowsOut d = {m->x, W(m->w_down), S(m->w_down_s), dim, 0};
             ALJ_TRY(enqueue_nf4_rows_fused(&d, 1, m->gate, m->up, nullptr, 0.0f, ffn, shift, kRowsMul, 1));
+            ALJ_MARK("down_rows_mul_add", nf4_w(dim, ffn, bs) + (2.0 * ffn + 2.0 * dim) * f4);
         } else {
             const ZeroList z{{m->gate, m->up, nullptr},
                              {static_cast<long long>(B) * ffn, static_cast<long long>(B) * ffn, 0}};
             ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, S(m->ffn_norm), B, dim, c.eps, &z));
+            ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * 2.0 * ffn) * f4);
             ALJ_TRY(mm(m->gate, m->xb, m->w_gate[l], m->w_gate_s[l], dim, ffn, false, nullptr));
+            ALJ_MARK("gate_up_gemm", mm_bytes(ffn, dim, true));
             ALJ_TRY(mm(m->up, m->xb, m->w_up[l], m->w_up_s[l], dim, ffn, false, nullptr));
+            ALJ_MARK("gate_up_gemm", mm_bytes(ffn, dim, true));
             ALJ_TRY(enqueue_swiglu(m->hb, m->gate, m->up, static_cast<long long>(B) * ffn));
+            ALJ_MARK("swiglu", B * 3.0 * ffn * f4);
             ALJ_TRY(mm(m->x, m->hb, m->w_down[l], m->w_down_s[l], ffn, dim, true, m->xb));
+            ALJ_MARK("down_gemm_add", mm_bytes(dim, ffn, true));
         }
     }
     ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, static_cast<const float *>(m->out_norm), B, dim, c.eps));
+    ALJ_MARK("final_rmsnorm", (B * 2.0 * dim + dim) * f4);
     ALJ_TRY(enqueue_matmul_gguf(lg, m->xb, static_cast<const uint8_t *>(m->lm_head), dim, c.vocab, ALJABR_ROCM_TYPE_F16,
                                 B));
-    ALJ_TRY(enqueue_argmax(static_cast<int *>(next_tokens), lg, B, c.vocab));
+    ALJ_MARK("lm_head_f16", static_cast<double>(c.vocab) * dim * 2.0 + B * (static_cast<double>(dim) + c.vocab) * f4);
+    ALJ_TRY(enqueue_argmax(next, lg, B, c.vocab));
+    ALJ_MARK("argmax", B * static_cast<double>(c.vocab) * f4);
+#undef ALJ_MARK
 #undef ALJ_TRY
+    return ALJABR_ROCM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aljabr_rocm_llama_decode(aljabr_rocm_llama *m, const void *tokens, const void *positions, int batch, void *logits,
+                             void *next_tokens) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(m && tokens && positions && next_tokens, "model, tokens, positions and next_tokens are required");
+    ALJ_REQUIRE(batch > 0 && batch <= m->cfg.max_batch, "batch %d outside [1, %d]", batch, m->cfg.max_batch);
+    float *lg = logits ? static_cast<float *>(logits) : m->logits;
+    const int rc = decode_step(m, static_cast<const int *>(tokens), static_cast<const int *>(positions), batch, lg,
+                               static_cast<int *>(next_tokens), nullptr, nullptr);
+    if (rc != ALJABR_ROCM_OK) return rc;
     return finish_launch("llama_decode");
+}
+
+int aljabr_rocm_llama_decode_profile(aljabr_rocm_llama *m, const void *tokens, const void *positions, int batch,
+                                     void *logits, void *next_tokens, aljabr_rocm_kernel_stat *stats, int cap,
+                                     int *count) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(m && tokens && positions && next_tokens && stats && count && cap > 0,
+                "model, tokens, positions, next_tokens, stats and count are required");
+    ALJ_REQUIRE(batch > 0 && batch <= m->cfg.max_batch, "batch %d outside [1, %d]", batch, m->cfg.max_batch);
+    hipStream_t s = current_stream();
+    std::vector<int> host_pos(static_cast<size_t>(batch));
+    hipError_t e = hipMemcpyAsync(host_pos.data(), positions, sizeof(int) * batch, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "decode profile: positions: %s", hipGetErrorString(e));
+    StepProfiler prof;
+    int rc = prof.begin(s, static_cast<size_t>(m->cfg.layers) * 12 + 8);
+    if (rc != ALJABR_ROCM_OK) return rc;
+    float *lg = logits ? static_cast<float *>(logits) : m->logits;
+    rc = decode_step(m, static_cast<const int *>(tokens), static_cast<const int *>(positions), batch, lg,
+                     static_cast<int *>(next_tokens), &prof, host_pos.data());
+    if (rc != ALJABR_ROCM_OK) return rc;
+    e = hipEventSynchronize(prof.events[prof.used - 1]);
+    if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "decode profile: %s", hipGetErrorString(e));
+    int n = 0;
+    for (size_t i = 0; i < prof.names.size(); ++i) {
+        float ms = 0.0f;
+        e = hipEventElapsedTime(&ms, prof.events[i], prof.events[i + 1]);
+        if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "hipEventElapsedTime: %s", hipGetErrorString(e));
+        int k = 0;
+        while (k < n && std::strncmp(stats[k].name, prof.names[i], sizeof(stats[k].name)) != 0) ++k;
+        if (k == n) {
+            if (n == cap) continue;              // more groups than the caller has room for
+            std::memset(&stats[n], 0, sizeof(stats[n]));
+            std::strncpy(stats[n].name, prof.names[i], sizeof(stats[n].name) - 1);
+            ++n;
+        }
+        stats[k].launches += 1;
+        stats[k].us += 1000.0 * ms;
+        stats[k].bytes += prof.bytes[i];
+    }
+    *count = n;
+    return ALJABR_ROCM_OK;
 }
 
 }  // extern "C"

@@ -120,6 +120,22 @@ class DeviceLlama:
                  logits.data_ptr() if logits is not None else None, next_tokens.data_ptr())
         return next_tokens
 
+    def decode_profile(self, tokens, positions, batch: int, logits=None, next_tokens=None):
+        """One decode step with per-launch-group device times; returns
+        (next_tokens, [{"name", "launches", "us", "bytes"}, ...])."""
+        import torch
+        if next_tokens is None:
+            next_tokens = torch.empty(batch, dtype=torch.int32, device=tokens.device)
+        cap = 64
+        stats = (abi.KernelStat * cap)()
+        count = ctypes.c_int(0)
+        abi.call("aljabr_rocm_llama_decode_profile", self.handle, tokens.data_ptr(), positions.data_ptr(), batch,
+                 logits.data_ptr() if logits is not None else None, next_tokens.data_ptr(), stats, cap,
+                 ctypes.byref(count))
+        groups = [{"name": stats[i].name.decode(), "launches": stats[i].launches, "us": stats[i].us,
+                   "bytes": stats[i].bytes} for i in range(count.value)]
+        return next_tokens, groups
+
     def hidden_ptr(self) -> int:
         p = ctypes.c_void_p()
         abi.call("aljabr_rocm_llama_hidden", self.handle, ctypes.byref(p))

@@ -270,8 +270,21 @@ def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, weights, 
         end.record(stream)
         end.synchronize()
     ms = start.elapsed_time(end) / steps
+    # Per-kernel roofline breakdown: one more step with a HIP event after every
+    # launch group (device time per group; the events themselves add a little).
+    with torch.cuda.stream(stream):
+        pos = torch.full((batch,), ctx + 1 + steps, dtype=torch.int32, device="cuda:0")
+        _, groups = model.decode_profile(tok, pos, batch)
     model.close()
-    return {"batch": batch, "context": ctx, "ms_per_step": round(ms, 3), "tokens_per_s": round(batch * 1000.0 / ms, 1)}
+    prof_us = sum(g["us"] for g in groups)
+    kernels = []
+    for g in sorted(groups, key=lambda g: -g["us"]):
+        gbs = g["bytes"] / g["us"] / 1e3 if g["us"] > 0 else 0.0
+        kernels.append({"group": g["name"], "launches": g["launches"], "us": round(g["us"], 1),
+                        "share": round(g["us"] / prof_us, 3), "bytes": int(g["bytes"]), "GBs": round(gbs, 1),
+                        "frac": round(gbs / HBM_PEAK_GBS, 3)})
+    return {"batch": batch, "context": ctx, "ms_per_step": round(ms, 3), "tokens_per_s": round(batch * 1000.0 / ms, 1),
+            "profiled_ms": round(prof_us / 1e3, 3), "kernels": kernels}
 
 
 def main() -> None:

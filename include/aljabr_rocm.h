@@ -231,6 +231,23 @@ int aljabr_rocm_llama_destroy(aljabr_rocm_llama *model);
 int aljabr_rocm_llama_decode(aljabr_rocm_llama *model, const void *tokens,
                              const void *positions, int batch, void *logits,
                              void *next_tokens);
+/* Device time and algorithmic HBM bytes of one launch group of a decode step. */
+typedef struct aljabr_rocm_kernel_stat {
+    char name[48];          /* launch group, e.g. "attention" or "lm_head_f16" */
+    int32_t launches;       /* launches of this group in the step */
+    double us;              /* their summed device time in the step, microseconds */
+    double bytes;           /* algorithmic bytes they move (weights, activations, KV rows read and written) */
+} aljabr_rocm_kernel_stat;
+
+/* aljabr_rocm_llama_decode with a HIP event after every launch group: runs one
+ * step, waits for it, and fills up to `cap` stats aggregated by group name
+ * (*count = groups found). The events add a few microseconds per group, so the
+ * sum is above an unprofiled step. No counterpart in the reference: it is the
+ * per-kernel roofline breakdown of the decode step. */
+int aljabr_rocm_llama_decode_profile(aljabr_rocm_llama *model, const void *tokens,
+                                     const void *positions, int batch, void *logits,
+                                     void *next_tokens, aljabr_rocm_kernel_stat *stats,
+                                     int cap, int *count);
 /* Device pointer of the session's final hidden state [batch][dim] fp32. */
 int aljabr_rocm_llama_hidden(aljabr_rocm_llama *model, void **hidden);
 /* Device pointers of the fp16 K and V caches, each

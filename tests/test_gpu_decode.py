@@ -131,6 +131,39 @@ def test_decode_step_matches_oracle(rocm, dev, oracle, ci, batch):
     model.close()
 
 
+@pytest.mark.parametrize("ci,batch", [(2, 1), (0, 3)], ids=["fused-b1", "gemm-b3"])
+def test_decode_profile_matches_decode(rocm, dev, oracle, ci, batch):
+    """The profiled step computes what the plain step computes (same next
+    tokens and logits from the same cache state) and accounts every launch
+    group: weights of all layers once, the LM head, the visible KV rows."""
+    import torch
+    from aljabr_amd.llama import DeviceLlama, upload_weights, proj_shapes
+    cfg = CONFIGS[ci]
+    host = _host_model(oracle, cfg, seed=7 + ci)
+    w = upload_weights(host)
+    toks = dev.put(np.array([3, 11, 29], np.int32)[:batch])
+    pos = dev.put(np.zeros(batch, np.int32))      # position 0: the step reads only the row it writes
+    outs = []
+    for profiled in (False, True):
+        model = DeviceLlama(cfg, w, max_batch=batch, max_seq=8)
+        logits = torch.empty(batch * cfg["vocab"], dtype=torch.float32, device="cuda:0")
+        if profiled:
+            nxt, groups = model.decode_profile(toks, pos, batch, logits=logits)
+        else:
+            nxt = model.decode(toks, pos, batch, logits=logits)
+        outs.append((dev.get(nxt), dev.get(logits)))
+        model.close()
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert rel_l2(outs[1][1], outs[0][1]) <= 1e-5
+    names = {g["name"] for g in groups}
+    assert {"attention", "lm_head_f16", "argmax", "rope_kv_append"} <= names
+    assert all(g["us"] > 0 and g["launches"] > 0 for g in groups)
+    shapes = proj_shapes(cfg)
+    nf4 = sum(n * k // 2 + n * k // cfg["nf4_block"] * 4 for n, k in shapes.values()) * cfg["layers"]
+    total = sum(g["bytes"] for g in groups)
+    assert nf4 + cfg["vocab"] * cfg["dim"] * 2 < total < 1.2 * (nf4 + cfg["vocab"] * cfg["dim"] * 2) + 1e6
+
+
 def test_decode_rejects_bad_batch(rocm, dev, oracle):
     from aljabr_amd.llama import DeviceLlama, upload_weights
     cfg = CONFIGS[0]
