@@ -43,17 +43,26 @@ struct RowsOut {
     const uint8_t *w;
     const float *absmax;
     int n;
-    int silu;       // store silu(v) = v / (1 + exp(-v)) (not with accumulate)
 };
-constexpr int kRowsPlain = 0;   // x' = x
-constexpr int kRowsNorm = 1;    // x' = RMSNorm(x) with weight norm_w over the K elements
-constexpr int kRowsMul = 2;     // x' = x * x2
+// The sequence and caches of a Q/K/V launch that rotates and appends (one
+// sequence: pos[0]; caches of one layer [n_kv][cap][head_dim] fp16).
+struct RowsRope {
+    const int *pos;
+    uint16_t *kc, *vc;
+    int cap, head_dim;
+    float base;
+};
+constexpr int kRowsStore = 0;    // y = W x'
+constexpr int kRowsAdd = 1;      // y += W x' (residual; no norm prologue)
+constexpr int kRowsSwiGLU = 2;   // outs = {gate, up}: outs[0].y = silu(Wg x') * (Wu x')
+constexpr int kRowsRopeKV = 3;   // outs = {q, k, v}: q rotated into outs[0].y; k rotated and v appended to the caches
 // Batch-1 NF4 matvec of up to three matrices sharing K and the activations
-// (stacked rows, one launch), with an activation prologue and, when
-// `accumulate`, y += instead of y =. Same shape limits as enqueue_rows;
-// ALJABR_ROCM_ERR_UNSUPPORTED (nothing enqueued) outside them.
-int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const float *x2, const float *norm_w,
-                           float eps, int K, int bs_shift, int prologue, int accumulate);
+// (stacked rows, one launch). x' = RMSNorm(x) with weight norm_w when norm_w
+// is non-null (over the K elements), else x. Same shape limits as
+// enqueue_rows, even row counts; ALJABR_ROCM_ERR_UNSUPPORTED (nothing
+// enqueued) outside them.
+int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
+                           int bs_shift, int epilogue, const RowsRope *rope = nullptr);
 // NF4 small-M GEMM on MFMA (2 <= M <= 64, K % 512 == 0, block size 64). With
 // `accumulate` the products are added to C as it is (C += A . W^T), so a
 // caller that has C cleared or holding a residual saves the clearing launch.

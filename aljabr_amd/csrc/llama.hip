@@ -263,13 +263,22 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         auto S = [&](const std::vector<const void *> &t) { return static_cast<const float *>(t[l]); };
         uint16_t *kc = m->k_cache + l * layer_cache;
         uint16_t *vc = m->v_cache + l * layer_cache;
-        // Attention block: xb = RMSNorm(x); q, k, v = Wq/Wk/Wv xb.
+        // Attention block: xb = RMSNorm(x); q, k, v = Wq/Wk/Wv xb; RoPE on
+        // q and k; k and v appended to the cache.
         if (fused1) {
-            const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq_s), qd, 0},
-                                    {m->k, W(m->wk), S(m->wk_s), kvd, 0},
-                                    {m->v, W(m->wv), S(m->wv_s), kvd, 0}};
-            ALJ_TRY(enqueue_nf4_rows_fused(qkv, 3, m->x, nullptr, S(m->attn_norm), c.eps, dim, shift, kRowsNorm, 0));
-            ALJ_MARK("qkv_rows_rmsnorm", nf4_w(qd + 2LL * kvd, dim, bs) + (2.0 * dim + qd + 2 * kvd) * f4);
+            const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq_s), qd},
+                                    {m->k, W(m->wk), S(m->wk_s), kvd},
+                                    {m->v, W(m->wv), S(m->wv_s), kvd}};
+            const RowsRope rope{pos, kc, vc, c.max_seq, hd, c.rope_base};
+            rc = enqueue_nf4_rows_fused(qkv, 3, m->x, S(m->attn_norm), c.eps, dim, shift, kRowsRopeKV, &rope);
+            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {     // e.g. a head size that is not a power of two
+                ALJ_TRY(enqueue_nf4_rows_fused(qkv, 3, m->x, S(m->attn_norm), c.eps, dim, shift, kRowsStore));
+                ALJ_TRY(enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base));
+            } else if (rc != ALJABR_ROCM_OK) {
+                return rc;
+            }
+            ALJ_MARK("qkv_rows_rmsnorm_rope_append",
+                     nf4_w(qd + 2LL * kvd, dim, bs) + (2.0 * dim + qd) * f4 + 2.0 * kvd * 2.0);
         } else {
             const ZeroList z{{m->q, m->k, m->v},
                              {static_cast<long long>(B) * qd, static_cast<long long>(B) * kvd,
@@ -283,16 +292,18 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             ALJ_TRY(mm(m->v, m->xb, m->wv[l], m->wv_s[l], dim, kvd, false, nullptr));
             ALJ_MARK("kv_gemm", mm_bytes(kvd, dim, true));
         }
-        rc = enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base);
-        if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
-            ALJ_TRY(enqueue_rope(m->q, pos, B, nh, hd, c.rope_base));
-            ALJ_TRY(enqueue_rope(m->k, pos, B, nkv, hd, c.rope_base));
-            ALJ_TRY(enqueue_kv_append(kc, m->k, pos, B, nkv, hd, c.max_seq));
-            ALJ_TRY(enqueue_kv_append(vc, m->v, pos, B, nkv, hd, c.max_seq));
-        } else if (rc != ALJABR_ROCM_OK) {
-            return rc;
+        if (!fused1) {
+            rc = enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base);
+            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                ALJ_TRY(enqueue_rope(m->q, pos, B, nh, hd, c.rope_base));
+                ALJ_TRY(enqueue_rope(m->k, pos, B, nkv, hd, c.rope_base));
+                ALJ_TRY(enqueue_kv_append(kc, m->k, pos, B, nkv, hd, c.max_seq));
+                ALJ_TRY(enqueue_kv_append(vc, m->v, pos, B, nkv, hd, c.max_seq));
+            } else if (rc != ALJABR_ROCM_OK) {
+                return rc;
+            }
+            ALJ_MARK("rope_kv_append", B * (2.0 * qd + 2.0 * kvd) * f4 + B * 2.0 * kvd * 2.0);
         }
-        ALJ_MARK("rope_kv_append", B * (2.0 * qd + 2.0 * kvd) * f4 + B * 2.0 * kvd * 2.0);
         AttnParams ap{};
         ap.out = m->att;
         ap.q = m->q;
@@ -308,8 +319,8 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         ALJ_MARK("attention", keys * nkv * hd * 2.0 * 2.0 + B * 2.0 * qd * f4);
         // x += Wo att.
         if (fused1) {
-            const RowsOut o = {m->x, W(m->wo), S(m->wo_s), dim, 0};
-            ALJ_TRY(enqueue_nf4_rows_fused(&o, 1, m->att, nullptr, nullptr, 0.0f, qd, shift, kRowsPlain, 1));
+            const RowsOut o = {m->x, W(m->wo), S(m->wo_s), dim};
+            ALJ_TRY(enqueue_nf4_rows_fused(&o, 1, m->att, nullptr, 0.0f, qd, shift, kRowsAdd));
             ALJ_MARK("wo_rows_add", mm_bytes(dim, qd, true));
         } else {
             ALJ_TRY(mm(m->x, m->att, m->wo[l], m->wo_s[l], qd, dim, true, m->xb));
@@ -317,13 +328,21 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         }
         // MLP: x += Wdown (silu(Wgate xb) * Wup xb), xb = RMSNorm(x).
         if (fused1) {
-            const RowsOut gu[2] = {{m->gate, W(m->w_gate), S(m->w_gate_s), ffn, 1},
-                                   {m->up, W(m->w_up), S(m->w_up_s), ffn, 0}};
-            ALJ_TRY(enqueue_nf4_rows_fused(gu, 2, m->x, nullptr, S(m->ffn_norm), c.eps, dim, shift, kRowsNorm, 0));
-            ALJ_MARK("gate_up_rows_rmsnorm_silu", nf4_w(2LL * ffn, dim, bs) + (2.0 * dim + 2.0 * ffn) * f4);
-            const RowsOut d = {m->x, W(m->w_down), S(m->w_down_s), dim, 0};
-            ALJ_TRY(enqueue_nf4_rows_fused(&d, 1, m->gate, m->up, nullptr, 0.0f, ffn, shift, kRowsMul, 1));
-            ALJ_MARK("down_rows_mul_add", nf4_w(dim, ffn, bs) + (2.0 * ffn + 2.0 * dim) * f4);
+            const RowsOut gu[2] = {{m->hb, W(m->w_gate), S(m->w_gate_s), ffn},
+                                   {nullptr, W(m->w_up), S(m->w_up_s), ffn}};
+            rc = enqueue_nf4_rows_fused(gu, 2, m->x, S(m->ffn_norm), c.eps, dim, shift, kRowsSwiGLU);
+            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {     // row count the paired waves do not divide
+                const RowsOut gu2[2] = {{m->gate, W(m->w_gate), S(m->w_gate_s), ffn},
+                                        {m->up, W(m->w_up), S(m->w_up_s), ffn}};
+                ALJ_TRY(enqueue_nf4_rows_fused(gu2, 2, m->x, S(m->ffn_norm), c.eps, dim, shift, kRowsStore));
+                ALJ_TRY(enqueue_swiglu(m->hb, m->gate, m->up, ffn));
+            } else if (rc != ALJABR_ROCM_OK) {
+                return rc;
+            }
+            ALJ_MARK("gate_up_rows_rmsnorm_swiglu", nf4_w(2LL * ffn, dim, bs) + (2.0 * dim + ffn) * f4);
+            const RowsOut d = {m->x, W(m->w_down), S(m->w_down_s), dim};
+            ALJ_TRY(enqueue_nf4_rows_fused(&d, 1, m->hb, nullptr, 0.0f, ffn, shift, kRowsAdd));
+            ALJ_MARK("down_rows_add", mm_bytes(dim, ffn, true));
         } else {
             const ZeroList z{{m->gate, m->up, nullptr},
                              {static_cast<long long>(B) * ffn, static_cast<long long>(B) * ffn, 0}};

@@ -24,9 +24,10 @@
 //   * Activations are staged once per workgroup with coalesced loads through
 //     a swizzled LDS window (conflict-free), then live in registers: lane l
 //     owns the 32 weights [32l, 32l+32) of its wave's 2048-element K chunk.
-//   * Rows are unrolled with the loads of row t+PF issued before row t is
-//     computed (the compiler drains all loads at a loop back-edge), and the T
-//     row sums are reduced across the wave by one butterfly.
+//   * Each wave streams T contiguous rows, unrolled with the loads of row
+//     t+PF issued before row t is computed (the compiler drains all loads at
+//     a loop back-edge), and the T row sums are reduced across the wave by
+//     one butterfly.
 //
 // Workgroup = W (8 or 16) waves: G = W/S row groups of S = K/2048 K-chunk
 // waves (waves beyond S*G only help with set-up). Q4_0/Q8_0 rows are read per lane PAIR:
@@ -62,61 +63,93 @@ template <> struct RowWords<kFmtQ8> { u32x4a4 a, b; uint32_t c; };
 
 // A launch covers up to three weight matrices of the same K stacked as one
 // row space (the decode step's Q/K/V or gate/up share one launch and one
-// activation staging); segment s owns rows [seg[s-1].end, seg[s].end).
+// activation staging); segment s owns rows [seg[s-1].end, seg[s].end), or,
+// for the SwiGLU epilogue, stacked row 2i is row i of segment 0 and 2i+1 row
+// i of segment 1 (so a gate row and its up row meet in one wave).
 struct RowsSeg {
     const uint8_t *w;
     const float *absmax;   // NF4 only
     float *y;
     int end;               // one past the segment's last row in the stacked row space
-    int silu;              // store v / (1 + exp(-v)) instead of v (store epilogue only)
 };
 
 // Prologue applied to the activations while they are staged, and epilogue of
-// each row sum.
+// the row sums.
 constexpr int kXPlain = 0;     // x
 constexpr int kXNorm = 1;      // RMSNorm: (x * 1/sqrt(mean(x^2) + eps)) * norm_w
-constexpr int kXMul = 2;       // x * x2 (SwiGLU's product, with silu applied upstream)
 constexpr int kEStore = 0;     // y = v
 constexpr int kEAdd = 1;       // y += v (residual)
+constexpr int kESwiGLU = 2;    // interleaved gate/up pairs: y = silu(gate) * up
+constexpr int kERopeKV = 3;    // Q/K/V pairs: RoPE on q (stored) and k, k and v appended to the fp16 caches
 
 struct RowsArgs {
     RowsSeg seg[3];
     const float *x;
-    const float *x2;       // kXMul
     const float *norm_w;   // kXNorm
     float eps;
+    // kERopeKV (one sequence): position, this layer's caches [n_kv][cap][D],
+    // D = 2^hd_shift.
+    const int *pos;
+    uint16_t *kc, *vc;
+    int cap, hd_shift;
+    float rope_base;
     int N, K, bs_shift, S, G;
 };
 
-// Segment of stacked row r and its row within the segment.
+// Segment of stacked row r and its row within the segment. The row map
+// follows from the epilogue at compile time (per-row runtime tests cost the
+// plain kernel over a microsecond): kESwiGLU interleaves two segments,
+// kERopeKV pairs the rows of each q and k head. Segments are picked with the
+// two comparisons directly (scalar selects).
 struct RowRef {
-    const uint8_t *w;
-    const float *absmax;
+    bool s1, s2;           // segment 1 or 2 (neither: segment 0)
     int local;
 };
 
+template <int EPI, int T>
 __device__ __forceinline__ RowRef row_ref(const RowsArgs &a, int r) {
-    const bool s1 = r >= a.seg[0].end, s2 = r >= a.seg[1].end;
     RowRef f;
-    f.w = s2 ? a.seg[2].w : s1 ? a.seg[1].w : a.seg[0].w;
-    f.absmax = s2 ? a.seg[2].absmax : s1 ? a.seg[1].absmax : a.seg[0].absmax;
-    f.local = r - (s2 ? a.seg[1].end : s1 ? a.seg[0].end : 0);
+    if constexpr (EPI == kESwiGLU) {
+        // A wave's T rows are T/2 consecutive gate rows, then the same T/2 up
+        // rows: both matrices are read as contiguous runs.
+        const int blk = r / T, t = r - blk * T;
+        f.s1 = t >= T / 2;
+        f.s2 = false;
+        f.local = blk * (T / 2) + (f.s1 ? t - T / 2 : t);
+    } else {
+        f.s1 = r >= a.seg[0].end;
+        f.s2 = r >= a.seg[1].end;
+        f.local = r - (f.s2 ? a.seg[1].end : f.s1 ? a.seg[0].end : 0);
+        if constexpr (EPI == kERopeKV) {
+            if (!f.s2) {
+                const int hd = 1 << a.hd_shift, q = f.local & (hd - 1);
+                f.local = (f.local - q) + (q >> 1) + (q & 1) * (hd >> 1);
+            }
+        }
+    }
     return f;
 }
 
-template <int FMT>
+template <class T>
+__device__ __forceinline__ T seg_pick(const RowRef &f, T a0, T a1, T a2) {
+    return f.s2 ? a2 : f.s1 ? a1 : a0;
+}
+
+template <int FMT, int EPI, int T>
 __device__ __forceinline__ void load_row(RowWords<FMT> &d, const RowsArgs &a, int row, int k0, int lane_blk) {
-    const RowRef f = row_ref(a, row);
+    const RowRef f = row_ref<EPI, T>(a, row);
     const size_t local = static_cast<size_t>(f.local);
+    const uint8_t *w = seg_pick(f, a.seg[0].w, a.seg[1].w, a.seg[2].w);
     if constexpr (FMT == kFmtNF4) {
+        const float *absmax = seg_pick(f, a.seg[0].absmax, a.seg[1].absmax, a.seg[2].absmax);
         const size_t row_bytes = static_cast<size_t>(a.K) >> 1;
-        d.q = load_stream16(f.w + local * row_bytes + (k0 >> 1));
-        d.s = f.absmax[(local * a.K + k0) >> a.bs_shift];
+        d.q = load_stream16(w + local * row_bytes + (k0 >> 1));
+        d.s = absmax[(local * a.K + k0) >> a.bs_shift];
     } else {
         constexpr int BB = FMT == kFmtQ4 ? 18 : 34;
         const size_t row_bytes = static_cast<size_t>(a.K >> 5) * BB;
         // Pair start (4-byte aligned) + 16 (Q4_0) or 32 (Q8_0) for the odd lane.
-        const uint8_t *p = f.w + local * row_bytes + static_cast<size_t>(lane_blk >> 1) * (2 * BB) +
+        const uint8_t *p = w + local * row_bytes + static_cast<size_t>(lane_blk >> 1) * (2 * BB) +
                            (lane_blk & 1) * (BB - 2);
         if constexpr (FMT == kFmtQ4) {
             d.a = load_stream16_a4(p);
@@ -241,6 +274,24 @@ __device__ __forceinline__ float silu_ref(float g) {
     return g / (1.0f + static_cast<float>(exp(-static_cast<double>(g))));
 }
 
+// Split-half RoPE of the pair (i, i + D/2) at position `pos` exactly as the
+// stand-alone RoPE kernel (GGUFVectorOps.rope :383-440): base^(-2i/D) and
+// cos/sin in double, products rounded separately.
+__device__ __forceinline__ void rope_rotate(float &x0, float &x1, int pos, int i, int head_dim, float base) {
+    const float exponent = -2.0f * static_cast<float>(i) / static_cast<float>(head_dim);
+    const float inv_freq = static_cast<float>(pow(static_cast<double>(base), static_cast<double>(exponent)));
+    const float theta = static_cast<float>(pos) * inv_freq;
+    const float c = static_cast<float>(cos(static_cast<double>(theta)));
+    const float s = static_cast<float>(sin(static_cast<double>(theta)));
+    const float a = x0, b = x1;
+    x0 = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+    x1 = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
 template <int FMT, int T, int PF, int W, int XOP, int EPI>
 __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     static_assert(T >= 1 && T <= 32 && PF >= 1 && (W == 8 || W == 16), "tile shape");
@@ -270,12 +321,11 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     }
 
     const bool stager = grp == 0;                // one wave per chunk stages x
-    // Row t of this wave's group is row0 + t*rstride: at any moment all
-    // workgroups read neighbouring rows, so the chip sweeps the matrix front
-    // to back as one streaming read (the DRAM- and TLB-friendly order)
-    // instead of 1000 separate sequential streams.
-    const int row0 = blockIdx.x * a.G + grp;
-    const int rstride = gridDim.x * a.G;
+    // Each wave streams the T contiguous rows row0 .. row0 + T-1 of the
+    // stacked row space (measured a few percent faster on MI355X than
+    // interleaving rows across the grid).
+    const int row0 = (blockIdx.x * a.G + grp) * T;
+    const int rstride = 1;
     const int k0 = chunk * kChunk + lane * 32;
     const int lane_blk = chunk * 64 + lane;      // Q4_0/Q8_0 block index in the row
 
@@ -289,15 +339,15 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
         const f32x4 *xw = reinterpret_cast<const f32x4 *>(a.x + xoff);
 #pragma unroll
         for (int j = 0; j < 8; ++j) xl[j] = xw[64 * j + lane];
-        if constexpr (XOP != kXPlain) {
-            const f32x4 *mw = reinterpret_cast<const f32x4 *>((XOP == kXNorm ? a.norm_w : a.x2) + xoff);
+        if constexpr (XOP == kXNorm) {
+            const f32x4 *mw = reinterpret_cast<const f32x4 *>(a.norm_w + xoff);
 #pragma unroll
             for (int j = 0; j < 8; ++j) xm[j] = mw[64 * j + lane];
         }
     }
     RowWords<FMT> rw[T];
 #pragma unroll
-    for (int t = 0; t < PF && t < T; ++t) load_row<FMT>(rw[t], a, min(row0 + t * rstride, a.N - 1), k0, lane_blk);
+    for (int t = 0; t < PF && t < T; ++t) load_row<FMT, EPI, T>(rw[t], a, min(row0 + t * rstride, a.N - 1), k0, lane_blk);
 
     if constexpr (XOP == kXNorm) {
         // RMSNorm over the whole row of K activations: chunk sums of squares
@@ -323,11 +373,6 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
                 1.0f / static_cast<float>(sqrt(static_cast<double>(tot / static_cast<float>(a.K) + a.eps)));
 #pragma unroll
             for (int j = 0; j < 8; ++j) xl[j] = (xl[j] * inv) * xm[j];
-        }
-    } else if constexpr (XOP == kXMul) {
-        if (stager) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) xl[j] = xl[j] * xm[j];
         }
     }
 
@@ -370,7 +415,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     for (int t = T; t < TP; ++t) acc[t] = 0.0f;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        if (t + PF < T) load_row<FMT>(rw[t + PF], a, min(row0 + (t + PF) * rstride, a.N - 1), k0, lane_blk);
+        if (t + PF < T) load_row<FMT, EPI, T>(rw[t + PF], a, min(row0 + (t + PF) * rstride, a.N - 1), k0, lane_blk);
         float scale;
         const float dot = row_dot<FMT>(rw[t], xv, xsum, odd, cl, tbl, scale);
         acc[t] = dot * scale;
@@ -383,18 +428,50 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     if (lane < TP) part[wave][wave_rows_index<TP>(lane)] = tot;
     __syncthreads();                                         // 4
     // The S chunk waves of group g are waves g*S .. g*S+S-1.
-    const int r = row0 + lane * rstride;
+    const int r = row0 + lane;
     if (chunk == 0 && lane < T && r < a.N) {
         float v = 0.0f;
         for (int c = 0; c < S; ++c) v += part[grp * S + c][lane];
-        const bool s1 = r >= a.seg[0].end, s2 = r >= a.seg[1].end;
-        float *y = s2 ? a.seg[2].y : s1 ? a.seg[1].y : a.seg[0].y;
-        const int local = r - (s2 ? a.seg[1].end : s1 ? a.seg[0].end : 0);
-        if constexpr (EPI == kEAdd) {
-            y[local] += v;
-        } else {
-            const int act = s2 ? a.seg[2].silu : s1 ? a.seg[1].silu : a.seg[0].silu;
-            y[local] = act ? silu_ref(v) : v;
+        if constexpr (EPI == kEStore || EPI == kEAdd) {
+            const RowRef f = row_ref<EPI, T>(a, r);
+            float *y = seg_pick(f, a.seg[0].y, a.seg[1].y, a.seg[2].y);
+            if constexpr (EPI == kEAdd) y[f.local] += v;
+            else y[f.local] = v;
+        } else if constexpr (EPI == kESwiGLU) {
+            // Lane t < T/2 holds gate row i, lane t + T/2 up row i.
+            if (lane < T / 2) {
+                float u = 0.0f;
+                for (int c = 0; c < S; ++c) u += part[grp * S + c][lane + T / 2];
+                a.seg[0].y[row_ref<EPI, T>(a, r).local] = silu_ref(v) * u;
+            }
+        } else if ((lane & 1) == 0) {
+            // RoPE pairs (r, r + 1): T is even and row0 even, so both are this
+            // wave's, and N is even.
+            float v1 = 0.0f;
+            for (int c = 0; c < S; ++c) v1 += part[grp * S + c][lane + 1];
+            {
+                const RowRef f = row_ref<EPI, T>(a, r);
+                const int p = a.pos[0];
+                const bool in_cache = p >= 0 && p < a.cap;
+                const int hd = 1 << a.hd_shift;
+                const int h = f.local >> a.hd_shift, i = f.local & (hd - 1);
+                if (!f.s1 && !f.s2) {                    // q: rotate, store fp32
+                    rope_rotate(v, v1, p, i, hd, a.rope_base);
+                    a.seg[0].y[f.local] = v;
+                    a.seg[0].y[f.local + (hd >> 1)] = v1;
+                } else if (!f.s2) {                      // k: rotate, append fp16
+                    rope_rotate(v, v1, p, i, hd, a.rope_base);
+                    if (in_cache) {
+                        uint16_t *dst = a.kc + (static_cast<size_t>(h) * a.cap + p) * hd + i;
+                        dst[0] = f32_to_f16_bits(v);
+                        dst[hd >> 1] = f32_to_f16_bits(v1);
+                    }
+                } else if (in_cache) {                   // v: rows local, local + 1, append fp16
+                    uint16_t *dst = a.vc + (static_cast<size_t>(h) * a.cap + p) * hd + i;
+                    dst[0] = f32_to_f16_bits(v);
+                    dst[1] = f32_to_f16_bits(v1);
+                }
+            }
         }
     }
 }
@@ -480,7 +557,7 @@ int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     }
     RowsArgs args{};
-    args.seg[0] = RowsSeg{W, absmax, C, N, 0};
+    args.seg[0] = RowsSeg{W, absmax, C, N};
     args.seg[1].end = args.seg[2].end = 0x7fffffff;
     args.x = A;
     args.N = N;
@@ -497,42 +574,70 @@ int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax
     return ALJABR_ROCM_OK;
 }
 
-int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const float *x2, const float *norm_w,
-                           float eps, int K, int bs_shift, int prologue, int accumulate) {
+int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
+                           int bs_shift, int epilogue, const RowsRope *rope) {
     if (nseg < 1 || nseg > 3 || !rows_shape_ok(x, K) || bs_shift < 5) return ALJABR_ROCM_ERR_UNSUPPORTED;
-    if (prologue == kRowsNorm && (!norm_w || !aligned(norm_w, 16))) return ALJABR_ROCM_ERR_UNSUPPORTED;
-    if (prologue == kRowsMul && (!x2 || !aligned(x2, 16))) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    if (norm_w && !aligned(norm_w, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     RowsArgs args{};
+    if (epilogue == kRowsSwiGLU) {
+        // gate (segment 0) and up (segment 1) interleaved row by row.
+        if (nseg != 2 || outs[0].n != outs[1].n) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    } else if (epilogue == kRowsRopeKV) {
+        // q, k, v of one sequence; RoPE pairs of q and k meet in one wave.
+        const int hs = rope ? log2_exact(rope->head_dim) : -1;
+        if (nseg != 3 || !rope || !rope->pos || !rope->kc || !rope->vc || hs < 1 ||
+            outs[0].n % rope->head_dim != 0 || outs[1].n % rope->head_dim != 0 || outs[1].n != outs[2].n)
+            return ALJABR_ROCM_ERR_UNSUPPORTED;
+        args.pos = rope->pos;
+        args.kc = rope->kc;
+        args.vc = rope->vc;
+        args.cap = rope->cap;
+        args.hd_shift = hs;
+        args.rope_base = rope->base;
+    } else if (epilogue != kRowsStore && epilogue != kRowsAdd) {
+        return ALJABR_ROCM_ERR_UNSUPPORTED;
+    }
     long long end = 0;
     for (int i = 0; i < 3; ++i) {
         if (i < nseg) {
-            if (!aligned(outs[i].w, 16) || outs[i].n <= 0 || (accumulate && outs[i].silu))
-                return ALJABR_ROCM_ERR_UNSUPPORTED;
+            if (!aligned(outs[i].w, 16) || outs[i].n <= 0 || (outs[i].n & 1)) return ALJABR_ROCM_ERR_UNSUPPORTED;
             end += outs[i].n;
             if (end > 0x7ffffffeLL) return ALJABR_ROCM_ERR_UNSUPPORTED;
-            args.seg[i] = RowsSeg{outs[i].w, outs[i].absmax, outs[i].y, static_cast<int>(end), outs[i].silu};
+            args.seg[i] = RowsSeg{outs[i].w, outs[i].absmax, outs[i].y, static_cast<int>(end)};
         } else {
             args.seg[i].end = 0x7fffffff;
         }
     }
     args.x = x;
-    args.x2 = x2;
     args.norm_w = norm_w;
     args.eps = eps;
     args.N = static_cast<int>(end);
     args.K = K;
     args.bs_shift = bs_shift;
     args.S = K / kChunk;
-    const int T = pick_rows_t(args.N, args.S, 32);
+    int T = pick_rows_t(args.N, args.S, 32);
+    if (T & 1) ++T;                              // the paired epilogues need both rows of a pair in one wave
+    if (epilogue == kRowsSwiGLU && (outs[0].n % (T / 2)) != 0)
+        return ALJABR_ROCM_ERR_UNSUPPORTED;      // every wave's gate run must be whole
     hipStream_t s = current_stream();
-    if (accumulate) {
-        if (prologue == kRowsMul) launch_rows<kFmtNF4, kXMul, kEAdd>(args, T, s);
-        else if (prologue == kRowsPlain) launch_rows<kFmtNF4, kXPlain, kEAdd>(args, T, s);
-        else return ALJABR_ROCM_ERR_UNSUPPORTED;
-    } else {
-        if (prologue == kRowsNorm) launch_rows<kFmtNF4, kXNorm, kEStore>(args, T, s);
-        else if (prologue == kRowsPlain) launch_rows<kFmtNF4, kXPlain, kEStore>(args, T, s);
-        else return ALJABR_ROCM_ERR_UNSUPPORTED;
+    const bool norm = norm_w != nullptr;
+    switch (epilogue) {
+    case kRowsStore:
+        if (norm) launch_rows<kFmtNF4, kXNorm, kEStore>(args, T, s);
+        else launch_rows<kFmtNF4, kXPlain, kEStore>(args, T, s);
+        break;
+    case kRowsAdd:
+        if (norm) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        launch_rows<kFmtNF4, kXPlain, kEAdd>(args, T, s);
+        break;
+    case kRowsSwiGLU:
+        if (!norm) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        launch_rows<kFmtNF4, kXNorm, kESwiGLU>(args, T, s);
+        break;
+    default:
+        if (!norm) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        launch_rows<kFmtNF4, kXNorm, kERopeKV>(args, T, s);
+        break;
     }
     return ALJABR_ROCM_OK;
 }

@@ -156,7 +156,8 @@ def test_decode_profile_matches_decode(rocm, dev, oracle, ci, batch):
     assert np.array_equal(outs[0][0], outs[1][0])
     assert rel_l2(outs[1][1], outs[0][1]) <= 1e-5
     names = {g["name"] for g in groups}
-    assert {"attention", "lm_head_f16", "argmax", "rope_kv_append"} <= names
+    assert {"attention", "lm_head_f16", "argmax"} <= names
+    assert any("rope" in n for n in names)       # stand-alone, or fused into the Q/K/V launch
     assert all(g["us"] > 0 and g["launches"] > 0 for g in groups)
     shapes = proj_shapes(cfg)
     nf4 = sum(n * k // 2 + n * k // cfg["nf4_block"] * 4 for n, k in shapes.values()) * cfg["layers"]
