@@ -119,6 +119,7 @@ SIGNATURES = {
                                       ctypes.POINTER(_P)]),
     "aljabr_rocm_llama_destroy": (_I, [_P]),
     "aljabr_rocm_llama_decode": (_I, [_P, _P, _P, _I, _P, _P]),
+    "aljabr_rocm_llama_decode_graph": (_I, [_P, _P, _P, _I, _P, _P]),
     "aljabr_rocm_llama_decode_profile": (_I, [_P, _P, _P, _I, _P, _P, ctypes.POINTER(KernelStat), _I,
                                               ctypes.POINTER(_I)]),
     "aljabr_rocm_llama_hidden": (_I, [_P, ctypes.POINTER(_P)]),

@@ -438,6 +438,13 @@ int launch_g(const AttnParams &p, int G, int splits, int chunk, float *part, hip
 
 }  // namespace
 
+// Chunks hold at least 64 keys (rounded to 16), so there are at most
+// ceil(keys / 64) + 1 splits.
+size_t attention_scratch_bytes(int B, int Hq, int Sq, int D, int keys) {
+    const size_t splits = static_cast<size_t>((keys + 63) / 64) + 1;
+    return static_cast<size_t>(B) * Hq * Sq * splits * (D + 2) * sizeof(float);
+}
+
 // Enqueue attention (no sync). Chooses the split-K kernels for D in {64,128}
 // with G in {1,2,4,8} and 16-byte aligned rows, the generic kernel otherwise.
 int enqueue_attention(const AttnParams &p) {
@@ -476,7 +483,7 @@ int enqueue_attention(const AttnParams &p) {
     float *part = nullptr;
     if (splits > 1) {
         const size_t bytes = static_cast<size_t>(p.B) * p.Hq * p.Sq * splits * (p.D + 2) * sizeof(float);
-        part = static_cast<float *>(stream_scratch(bytes));
+        part = p.scratch && bytes <= p.scratch_bytes ? p.scratch : static_cast<float *>(stream_scratch(bytes));
         if (!part) return ALJABR_ROCM_ERR_BUFFER;
     }
     if (p.D == 64)

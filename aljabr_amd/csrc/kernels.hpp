@@ -17,9 +17,14 @@ struct AttnParams {
     float scale;
     int causal;
     int kv_f16;
+    float *scratch;         // split partials: caller-owned (graph-safe) when it holds attention_scratch_bytes(),
+    size_t scratch_bytes;   // else (null or too small) the stream's scratch
 };
 
 int enqueue_attention(const AttnParams &p);
+// Upper bound of the split-partial bytes enqueue_attention needs for B
+// sequences of Hq heads, Sq query rows, head size D and `keys` cached keys.
+size_t attention_scratch_bytes(int B, int Hq, int Sq, int D, int keys);
 
 // C[M][N] = A[M][K] . W[N][K]^T for any M (slices or MFMA chosen inside).
 int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M);

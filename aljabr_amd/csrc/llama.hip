@@ -30,6 +30,16 @@ __global__ void lengths_from_positions(int *__restrict__ len, const int *__restr
     if (i < n) len[i] = pos[i] + 1;
 }
 
+// dst_a[i] = src_a[i], dst_b[i] = src_b[i] for i < n (either pair may be null).
+__global__ void copy_i32_pairs(int *__restrict__ dst_a, const int *__restrict__ src_a, int *__restrict__ dst_b,
+                               const int *__restrict__ src_b, int n) {
+    const int i = blockIdx.x * 64 + threadIdx.x;
+    if (i < n) {
+        if (dst_a) dst_a[i] = src_a[i];
+        if (dst_b) dst_b[i] = src_b[i];
+    }
+}
+
 }  // namespace
 }  // namespace aljabr
 
@@ -43,7 +53,16 @@ struct aljabr_rocm_llama {
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
     float *gate = nullptr, *up = nullptr, *hb = nullptr, *logits = nullptr;
     int *kv_len = nullptr;
-    bool rows_fused = false;   // batch-1 layers as four fused NF4 launches (shapes and alignment allow it)
+    int *tok_in = nullptr, *pos_in = nullptr, *next_out = nullptr;   // graph replays read and write these
+    float *attn_scratch = nullptr;   // split-attention partials (owned: a captured graph keeps the address)
+    size_t attn_scratch_bytes = 0;
+    bool rows_fused = false;   // batch-1 layers as fused NF4 launches (shapes and alignment allow it)
+    // Captured decode steps, by batch size (and the logits buffer they write).
+    struct Graph {
+        hipGraphExec_t exec = nullptr;
+        float *logits = nullptr;
+    };
+    std::vector<Graph> graphs;
 };
 
 using namespace aljabr;
@@ -110,7 +129,9 @@ int aljabr_rocm_llama_create(const aljabr_rocm_llama_config *cfg, const aljabr_r
     const size_t bytes = 2 * ((cache_elems * 2 + 255) & ~size_t(255)) +
                          ((B * c.dim * 4 + 255) & ~size_t(255)) * 2 + ((B * qd * 4 + 255) & ~size_t(255)) * 2 +
                          ((B * kvd * 4 + 255) & ~size_t(255)) * 2 + ((B * c.ffn * 4 + 255) & ~size_t(255)) * 3 +
-                         ((B * c.vocab * 4 + 255) & ~size_t(255)) + ((B * 4 + 255) & ~size_t(255)) + 256;
+                         ((B * c.vocab * 4 + 255) & ~size_t(255)) + ((B * 4 + 255) & ~size_t(255)) * 4 +
+                         ((attention_scratch_bytes(c.max_batch, c.n_heads, 1, c.head_dim, c.max_seq) + 255) &
+                          ~size_t(255)) + 256;
     hipError_t e = hipMalloc(&m->arena, bytes);
     if (e != hipSuccess) {
         delete m;
@@ -130,6 +151,12 @@ int aljabr_rocm_llama_create(const aljabr_rocm_llama_config *cfg, const aljabr_r
     m->hb = carve<float>(cur, B * c.ffn);
     m->logits = carve<float>(cur, B * c.vocab);
     m->kv_len = carve<int>(cur, B);
+    m->tok_in = carve<int>(cur, B);
+    m->pos_in = carve<int>(cur, B);
+    m->next_out = carve<int>(cur, B);
+    m->attn_scratch_bytes = attention_scratch_bytes(c.max_batch, c.n_heads, 1, c.head_dim, c.max_seq);
+    m->attn_scratch = carve<float>(cur, m->attn_scratch_bytes / sizeof(float));
+    m->graphs.resize(static_cast<size_t>(c.max_batch) + 1);
     // Batch-1 fusion needs every K a multiple of 2048 (at most 16384), a
     // power-of-two block of at least 32 and 16-byte aligned weights and norms.
     const int qd_i = c.n_heads * c.head_dim;
@@ -148,6 +175,8 @@ int aljabr_rocm_llama_create(const aljabr_rocm_llama_config *cfg, const aljabr_r
 int aljabr_rocm_llama_destroy(aljabr_rocm_llama *m) {
     if (!m) return ALJABR_ROCM_OK;
     ALJ_CHECK_READY();
+    for (auto &g : m->graphs)
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
     if (m->arena) (void)hipFree(m->arena);
     delete m;
     return ALJABR_ROCM_OK;
@@ -315,6 +344,8 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         ap.scale = static_cast<float>(1.0 / sqrt(static_cast<double>(hd)));
         ap.causal = 0;
         ap.kv_f16 = 1;
+        ap.scratch = m->attn_scratch;
+        ap.scratch_bytes = m->attn_scratch_bytes;
         ALJ_TRY(enqueue_attention(ap));
         ALJ_MARK("attention", keys * nkv * hd * 2.0 * 2.0 + B * 2.0 * qd * f4);
         // x += Wo att.
@@ -384,6 +415,55 @@ int aljabr_rocm_llama_decode(aljabr_rocm_llama *m, const void *tokens, const voi
                                static_cast<int *>(next_tokens), nullptr, nullptr);
     if (rc != ALJABR_ROCM_OK) return rc;
     return finish_launch("llama_decode");
+}
+
+int aljabr_rocm_llama_decode_graph(aljabr_rocm_llama *m, const void *tokens, const void *positions, int batch,
+                                   void *logits, void *next_tokens) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(m && tokens && positions && next_tokens, "model, tokens, positions and next_tokens are required");
+    ALJ_REQUIRE(batch > 0 && batch <= m->cfg.max_batch, "batch %d outside [1, %d]", batch, m->cfg.max_batch);
+    hipStream_t s = current_stream();
+    float *lg = logits ? static_cast<float *>(logits) : m->logits;
+    const dim3 grid((batch + 63) / 64);
+    hipLaunchKernelGGL(copy_i32_pairs, grid, dim3(64), 0, s, m->tok_in, static_cast<const int *>(tokens), m->pos_in,
+                       static_cast<const int *>(positions), batch);
+    aljabr_rocm_llama::Graph &g = m->graphs[static_cast<size_t>(batch)];
+    if (g.exec && g.logits != lg) {              // another logits buffer: capture again
+        (void)hipGraphExecDestroy(g.exec);
+        g.exec = nullptr;
+    }
+    int rc;
+    if (g.exec) {
+        const hipError_t e = hipGraphLaunch(g.exec, s);
+        if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "hipGraphLaunch: %s", hipGetErrorString(e));
+    } else {
+        // First step of this batch size: run it eagerly (which also sizes
+        // every lazily allocated resource), then capture the same launches
+        // without running them. The captured step reads the staged inputs,
+        // so replays serve any tokens and positions.
+        rc = decode_step(m, m->tok_in, m->pos_in, batch, lg, m->next_out, nullptr, nullptr);
+        if (rc != ALJABR_ROCM_OK) return rc;
+        hipGraph_t graph = nullptr;
+        hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "hipStreamBeginCapture: %s", hipGetErrorString(e));
+        rc = decode_step(m, m->tok_in, m->pos_in, batch, lg, m->next_out, nullptr, nullptr);
+        e = hipStreamEndCapture(s, &graph);
+        if (rc != ALJABR_ROCM_OK) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return rc;
+        }
+        if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "hipStreamEndCapture: %s", hipGetErrorString(e));
+        e = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (e != hipSuccess) {
+            g.exec = nullptr;
+            return fail(ALJABR_ROCM_ERR_DEVICE, "hipGraphInstantiate: %s", hipGetErrorString(e));
+        }
+        g.logits = lg;
+    }
+    hipLaunchKernelGGL(copy_i32_pairs, grid, dim3(64), 0, s, static_cast<int *>(next_tokens), m->next_out,
+                       static_cast<int *>(nullptr), static_cast<const int *>(nullptr), batch);
+    return finish_launch("llama_decode_graph");
 }
 
 int aljabr_rocm_llama_decode_profile(aljabr_rocm_llama *m, const void *tokens, const void *positions, int batch,

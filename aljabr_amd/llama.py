@@ -120,6 +120,15 @@ class DeviceLlama:
                  logits.data_ptr() if logits is not None else None, next_tokens.data_ptr())
         return next_tokens
 
+    def decode_graph(self, tokens, positions, batch: int, logits=None, next_tokens=None):
+        """decode() replayed from the session's captured HIP graph of the step."""
+        import torch
+        if next_tokens is None:
+            next_tokens = torch.empty(batch, dtype=torch.int32, device=tokens.device)
+        abi.call("aljabr_rocm_llama_decode_graph", self.handle, tokens.data_ptr(), positions.data_ptr(), batch,
+                 logits.data_ptr() if logits is not None else None, next_tokens.data_ptr())
+        return next_tokens
+
     def decode_profile(self, tokens, positions, batch: int, logits=None, next_tokens=None):
         """One decode step with per-launch-group device times; returns
         (next_tokens, [{"name", "launches", "us", "bytes"}, ...])."""

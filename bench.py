@@ -237,7 +237,7 @@ def copy_probe(torch, stream) -> None:
 
 def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, weights, cfg):
     from aljabr_amd.llama import DeviceLlama
-    max_seq = ctx + steps + 8
+    max_seq = ctx + 2 * steps + 8
     model = DeviceLlama(cfg, weights, max_batch=batch, max_seq=max_seq)
     # Context of `ctx` tokens: fill the fp16 KV cache with N(0,1) values.
     kp, vp = model.kv_cache_ptrs()
@@ -257,23 +257,31 @@ def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, weights, 
     tok = torch.randint(0, cfg["vocab"], (batch,), dtype=torch.int32, device="cuda:0",
                         generator=torch.Generator(device="cuda:0").manual_seed(5))
     torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        pos = torch.full((batch,), ctx, dtype=torch.int32, device="cuda:0")
-        tok = model.decode(tok, pos, batch)          # warm-up step
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        positions = [torch.full((batch,), ctx + 1 + i, dtype=torch.int32, device="cuda:0") for i in range(steps)]
-        torch.cuda.synchronize()
-        start.record(stream)
-        for i in range(steps):
-            tok = model.decode(tok, positions[i], batch)
-        end.record(stream)
-        end.synchronize()
-    ms = start.elapsed_time(end) / steps
+    def timed(step_fn, first_pos):
+        nonlocal tok
+        with torch.cuda.stream(stream):
+            pos = torch.full((batch,), first_pos, dtype=torch.int32, device="cuda:0")
+            tok = step_fn(tok, pos, batch)           # warm-up step (captures the graph)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            positions = [torch.full((batch,), first_pos + 1 + i, dtype=torch.int32, device="cuda:0")
+                         for i in range(steps)]
+            torch.cuda.synchronize()
+            start.record(stream)
+            for i in range(steps):
+                tok = step_fn(tok, positions[i], batch)
+            end.record(stream)
+            end.synchronize()
+        return start.elapsed_time(end) / steps
+
+    # Every step appends one row per sequence, so the two timings cover
+    # contexts ctx .. ctx + steps and ctx + steps + 1 .. ctx + 2 steps + 1.
+    ms_eager = timed(model.decode, ctx)
+    ms = timed(model.decode_graph, ctx + steps + 1)
     # Per-kernel roofline breakdown: one more step with a HIP event after every
     # launch group (device time per group; the events themselves add a little).
     with torch.cuda.stream(stream):
-        pos = torch.full((batch,), ctx + 1 + steps, dtype=torch.int32, device="cuda:0")
+        pos = torch.full((batch,), ctx + 2 * steps + 2, dtype=torch.int32, device="cuda:0")
         _, groups = model.decode_profile(tok, pos, batch)
     model.close()
     prof_us = sum(g["us"] for g in groups)
@@ -284,6 +292,8 @@ def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, weights, 
                         "share": round(g["us"] / prof_us, 3), "bytes": int(g["bytes"]), "GBs": round(gbs, 1),
                         "frac": round(gbs / HBM_PEAK_GBS, 3)})
     return {"batch": batch, "context": ctx, "ms_per_step": round(ms, 3), "tokens_per_s": round(batch * 1000.0 / ms, 1),
+            "path": "captured HIP graph of the whole step",
+            "ms_per_step_eager": round(ms_eager, 3), "tokens_per_s_eager": round(batch * 1000.0 / ms_eager, 1),
             "profiled_ms": round(prof_us / 1e3, 3), "kernels": kernels}
 
 

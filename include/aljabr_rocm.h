@@ -231,6 +231,16 @@ int aljabr_rocm_llama_destroy(aljabr_rocm_llama *model);
 int aljabr_rocm_llama_decode(aljabr_rocm_llama *model, const void *tokens,
                              const void *positions, int batch, void *logits,
                              void *next_tokens);
+/* aljabr_rocm_llama_decode replayed from a HIP graph of the whole step: the
+ * first call for a batch size (and logits buffer) runs the step and captures
+ * it; later calls copy tokens and positions into the session, replay the
+ * graph and copy the next tokens out (three submissions instead of one per
+ * kernel). Same results as aljabr_rocm_llama_decode; the stream must not be
+ * the null stream. No counterpart in the reference (the Metal runner issues
+ * per-op dispatches, MTLC/aljabr_metal_matvec_api.h:161-217). */
+int aljabr_rocm_llama_decode_graph(aljabr_rocm_llama *model, const void *tokens,
+                                   const void *positions, int batch, void *logits,
+                                   void *next_tokens);
 /* Device time and algorithmic HBM bytes of one launch group of a decode step. */
 typedef struct aljabr_rocm_kernel_stat {
     char name[48];          /* launch group, e.g. "attention" or "lm_head_f16" */

@@ -165,6 +165,37 @@ def test_decode_profile_matches_decode(rocm, dev, oracle, ci, batch):
     assert nf4 + cfg["vocab"] * cfg["dim"] * 2 < total < 1.2 * (nf4 + cfg["vocab"] * cfg["dim"] * 2) + 1e6
 
 
+@pytest.mark.parametrize("ci,batch", [(2, 1), (0, 3)], ids=["fused-b1", "gemm-b3"])
+def test_decode_graph_replays_match_eager(rocm, dev, oracle, ci, batch):
+    """The captured whole-step graph against eager steps of a twin session:
+    six replays (the first call captures), each followed by eager work and a
+    synchronisation, every replay checked (tokens equal, logits equal up to
+    the matrix cores' atomic summation order), and a change of logits buffer
+    (a second capture)."""
+    import torch
+    from aljabr_amd.llama import DeviceLlama, upload_weights
+    cfg = CONFIGS[ci]
+    host = _host_model(oracle, cfg, seed=21 + ci)
+    w = upload_weights(host)
+    eager = DeviceLlama(cfg, w, max_batch=batch, max_seq=16)
+    graph = DeviceLlama(cfg, w, max_batch=batch, max_seq=16)
+    cur = (np.array([5, 17, 1999], np.int32) % cfg["vocab"])[:batch]
+    le = torch.empty(batch * cfg["vocab"], dtype=torch.float32, device="cuda:0")
+    lg = [torch.empty_like(le), torch.empty_like(le)]
+    tol = 0.0 if batch == 1 else 1e-5
+    for step in range(6):
+        pos = np.full(batch, step, np.int32)
+        te = eager.decode(dev.put(cur), dev.put(pos), batch, logits=le)
+        tg = graph.decode_graph(dev.put(cur), dev.put(pos), batch, logits=lg[step // 4])
+        torch.cuda.synchronize()
+        got_e, got_g = dev.get(te), dev.get(tg)
+        assert np.array_equal(got_e, got_g), step
+        assert rel_l2(dev.get(lg[step // 4]), dev.get(le)) <= tol, step
+        cur = got_e.astype(np.int32)
+    eager.close()
+    graph.close()
+
+
 def test_decode_rejects_bad_batch(rocm, dev, oracle):
     from aljabr_amd.llama import DeviceLlama, upload_weights
     cfg = CONFIGS[0]
