@@ -110,6 +110,12 @@ SIGNATURES = {
     "aljabr_rocm_dequantize": (_I, [_P, _P, _P, _LL, _I, _I]),
     "aljabr_rocm_quantize": (_I, [_P, _P, _P, _LL, _I, _I]),
     "aljabr_rocm_attention_gqa": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I]),
+    "aljabr_rocm_paged_attention": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _F]),
+    "aljabr_rocm_paged_attention_windowed": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _I,
+                                                  _I, _F]),
+    "aljabr_rocm_paged_attention_gqa": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _F]),
+    "aljabr_rocm_paged_attention_gqa_windowed": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I,
+                                                      _I, _I, _F]),
     "aljabr_rocm_rmsnorm": (_I, [_P, _P, _P, _I, _I, _F]),
     "aljabr_rocm_rope": (_I, [_P, _P, _I, _I, _I, _F]),
     "aljabr_rocm_swiglu": (_I, [_P, _P, _P, _LL]),

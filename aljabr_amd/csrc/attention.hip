@@ -91,7 +91,30 @@ __device__ __forceinline__ void load8(const void *base, long long idx, float (&r
 }
 
 // grid: x = split, y = kv head * Sq + query row, z = batch. WAVES*64 threads.
-template <int D, int G, bool F16, int WAVES>
+// Visible key range [lo, hi) of query row qi for a sequence of sk keys.
+__device__ __forceinline__ void key_range(const AttnParams &p, int sk, int qi, int &lo, int &hi) {
+    if (p.paged_bounds) {
+        // MTLC/aljabr_metal_attention.m:146-160,192-200.
+        int qpos = p.query_start + qi;
+        if (p.causal && p.window <= 0 && p.query_start == 0 && sk >= p.Sq) qpos = sk - p.Sq + qi;
+        int upper = p.causal ? qpos : sk - 1;
+        if (upper >= sk) upper = sk - 1;
+        int lower = p.window > 0 ? qpos - p.window + 1 : 0;
+        if (lower < 0) lower = 0;
+        lo = lower;
+        hi = upper + 1;
+    } else {
+        // CPU/CpuBackend.java:1690-1700: bottom-right causal limit.
+        lo = 0;
+        hi = sk;
+        if (p.causal) {
+            const int c = sk - p.Sq + qi + 1;
+            hi = c < sk ? c : sk;
+        }
+    }
+}
+
+template <int D, int G, bool F16, int WAVES, bool PAGED>
 __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, int splits, int chunk,
                                                                 float *__restrict__ part_o,
                                                                 float *__restrict__ part_ml) {
@@ -110,30 +133,49 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
     const int sub = lane % LPK;                // 8-dim slice of the row
 
     const int k_begin = split * chunk;
-    // Rows [k_begin, mem_end) exist in memory whatever the visible length,
-    // so the first tile's loads go out before kv_len has arrived.
-    const int mem_end = min(k_begin + chunk, p.kv_len ? p.cap : p.Sk);
+    // Element offset of key row `key` (this lane's 8-value slice).
     const long long head_base = (static_cast<long long>(b) * p.Hkv + kvh) * p.cap * D + sub * 8;
+    const int *btab = PAGED ? p.block_table + static_cast<long long>(b) * p.max_blocks : nullptr;
+    auto row_at = [&](int key) -> long long {
+        if constexpr (PAGED) {
+            const int blk = key / p.block_size;
+            const int phys = max(btab[blk], 0);
+            return ((static_cast<long long>(phys) * p.Hkv + kvh) * p.block_size + (key - blk * p.block_size)) * D +
+                   sub * 8;
+        } else {
+            return head_base + static_cast<long long>(key) * D;
+        }
+    };
     KvRaw<F16> kn[kTile], vn[kTile];
+    int mem_end;                                 // keys below this are rows that exist
     auto issue = [&](int tbase) {
 #pragma unroll
         for (int t = 0; t < kTile; ++t) {
             const int key = tbase + t;
-            const int kk = key < mem_end ? key : k_begin;
-            kn[t] = load_raw<F16>(p.k, head_base + static_cast<long long>(kk) * D);
-            vn[t] = load_raw<F16>(p.v, head_base + static_cast<long long>(kk) * D);
+            const long long r = row_at(key < mem_end ? key : k_begin);
+            kn[t] = load_raw<F16>(p.k, r);
+            vn[t] = load_raw<F16>(p.v, r);
         }
     };
-    issue(k_begin + grp * kTile);
-
-    const int sk = p.kv_len ? min(max(p.kv_len[b], 0), p.cap) : p.Sk;   // never past the cache
-    int limit = sk;
-    if (p.causal) {
-        const int c = sk - p.Sq + qi + 1;
-        limit = c < sk ? c : sk;
+    int sk;
+    if constexpr (PAGED) {
+        // Blocks past the sequence's length may not exist: read the length
+        // first, and a split past it loads nothing (clamped keys fall back
+        // to k_begin, which must then be a row of the sequence).
+        sk = max(p.kv_len[b], 0);
+        mem_end = min(k_begin + chunk, sk);
+        if (k_begin < sk) issue(k_begin + grp * kTile);
+    } else {
+        // Rows [k_begin, mem_end) exist in memory whatever the visible length,
+        // so the first tile's loads go out before kv_len has arrived.
+        mem_end = min(k_begin + chunk, p.kv_len ? p.cap : p.Sk);
+        issue(k_begin + grp * kTile);
+        sk = p.kv_len ? min(max(p.kv_len[b], 0), p.cap) : p.Sk;   // never past the cache
     }
+    int k_lo, k_hi;
+    key_range(p, sk, qi, k_lo, k_hi);
     int k_end = k_begin + chunk;
-    if (k_end > limit) k_end = limit;
+    if (k_end > k_hi) k_end = k_hi;
 
     // Query slices, pre-scaled so that exp2(q.k) == exp(score).
     float qv[G][8];
@@ -141,7 +183,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const int h = kvh * G + g;
-        const float *qp = p.q + ((static_cast<long long>(b) * p.Hq + h) * p.Sq + qi) * D + sub * 8;
+        const float *qp = p.q + b * p.q_sb + h * p.q_sh + qi * p.q_sq + sub * 8;
         const float4 a = *reinterpret_cast<const float4 *>(qp);
         const float4 c = *reinterpret_cast<const float4 *>(qp + 4);
         qv[g][0] = a.x * qs; qv[g][1] = a.y * qs; qv[g][2] = a.z * qs; qv[g][3] = a.w * qs;
@@ -167,7 +209,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
         bool valid[kTile];
 #pragma unroll
         for (int t = 0; t < kTile; ++t) {
-            valid[t] = t0 + t < k_end;
+            valid[t] = t0 + t < k_end && (!PAGED || t0 + t >= k_lo);   // only the paged rule has a lower bound
             raw_to_f32<F16>(kn[t], kr[t]);
             raw_to_f32<F16>(vn[t], vr[t]);
             // Rows past the visible keys may hold anything (the first tile is
@@ -195,6 +237,11 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
 #pragma unroll
                 for (int i = 0; i < 8; ++i) d = fmaf(qv[g][i], kr[t][i], d);
                 d = group_sum<LPK>(d);
+                if (PAGED && p.soft_cap > 0.0f) {
+                    // d = score * log2(e): cap the score, then back to base 2.
+                    const float cap = p.soft_cap;
+                    d = cap * tanhf(d / (kLog2e * cap)) * kLog2e;
+                }
                 s[t] = valid[t] ? d + add[t] : -INFINITY;
                 tmax = fmaxf(tmax, s[t]);
             }
@@ -252,7 +299,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
         const int h = kvh * G + g;
         const long long row = (static_cast<long long>(b) * p.Hq + h) * p.Sq + qi;
         if (splits == 1) {
-            p.out[row * D + dd] = L == 0.0f ? 0.0f : O / L;
+            p.out[b * p.q_sb + h * p.q_sh + qi * p.q_sq + dd] = L == 0.0f ? 0.0f : O / (L + p.norm_eps);
         } else {
             part_o[(row * splits + split) * D + dd] = O;
             if (dd == 0) {
@@ -268,12 +315,16 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
 // lane group folds its splits with online rescaling, and the groups are
 // combined through LDS.
 template <int D>
-__global__ __launch_bounds__(256) void attn_merge_kernel(float *__restrict__ out, const float *__restrict__ part_o,
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, const float *__restrict__ part_o,
                                                         const float *__restrict__ part_ml, int splits) {
     constexpr int LPS = D / 4;          // lanes per split
     constexpr int SG = 256 / LPS;       // splits in flight
     __shared__ float st[SG][D + 2];
-    const long long row = blockIdx.x;
+    const long long row = blockIdx.x;   // (b * Hq + h) * Sq + qi
+    const int qi = static_cast<int>(row % p.Sq);
+    const int h = static_cast<int>((row / p.Sq) % p.Hq);
+    const int bb = static_cast<int>(row / (static_cast<long long>(p.Sq) * p.Hq));
+    float *out = p.out + bb * p.q_sb + h * p.q_sh + qi * p.q_sq;
     const int sg = threadIdx.x / LPS, j = threadIdx.x % LPS;
     const float *po = part_o + row * splits * D;
     const float *pm = part_ml + row * splits * 2;
@@ -332,7 +383,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(float *__restrict__ out
                 O = fmaf(st[g][dd], w, O);
             }
         }
-        out[row * D + dd] = L == 0.0f ? 0.0f : O / L;
+        out[dd] = L == 0.0f ? 0.0f : O / (L + p.norm_eps);
     }
 }
 
@@ -352,27 +403,35 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(AttnParams p) {
     const long long total = static_cast<long long>(p.B) * p.Hq * p.Sq * D;
     if (tid >= total) return;
     const int j = static_cast<int>(tid % D);
-    const long long idx = tid / D;   // query row
+    const long long idx = tid / D;   // query row (b * Hq + h) * Sq + qi
     const int qi = static_cast<int>(idx % p.Sq);
     const int h = static_cast<int>((idx / p.Sq) % p.Hq);
     const int b = static_cast<int>(idx / (static_cast<long long>(p.Sq) * p.Hq));
     const int kvh = h / (p.Hq / p.Hkv);
-    const int sk = p.kv_len ? min(max(p.kv_len[b], 0), p.cap) : p.Sk;   // never past the cache
-    int limit = sk;
-    if (p.causal) {
-        const int c = sk - p.Sq + qi + 1;
-        limit = c < sk ? c : sk;
-    }
-    const float *qr = p.q + idx * D;
-    const long long kb = (static_cast<long long>(b) * p.Hkv + kvh) * p.cap * D;
+    const int sk = p.block_table ? max(p.kv_len[b], 0)
+                                 : (p.kv_len ? min(max(p.kv_len[b], 0), p.cap) : p.Sk);   // never past the cache
+    int lo, hi;
+    key_range(p, sk, qi, lo, hi);
+    const float *qr = p.q + b * p.q_sb + h * p.q_sh + qi * p.q_sq;
+    auto row_at = [&](int ki) -> long long {
+        if (p.block_table) {
+            const int blk = ki / p.block_size;
+            const int phys = max(p.block_table[static_cast<long long>(b) * p.max_blocks + blk], 0);
+            return ((static_cast<long long>(phys) * p.Hkv + kvh) * p.block_size + (ki - blk * p.block_size)) * D;
+        }
+        return ((static_cast<long long>(b) * p.Hkv + kvh) * p.cap + ki) * D;
+    };
     float running = -INFINITY;
     double den = 0.0, weighted = 0.0;
-    for (int ki = 0; ki < limit; ++ki) {
+    for (int ki = lo; ki < hi; ++ki) {
         const float add = p.mask ? p.mask[static_cast<long long>(qi) * p.Sk + ki] : 0.0f;
         if (add == -INFINITY) continue;
+        const long long kb = row_at(ki);
         float dot = 0.0f;
-        for (int e = 0; e < D; ++e) dot = fmaf(qr[e], kv_at<F16>(p.k, kb + static_cast<long long>(ki) * D + e), dot);
-        const float score = dot * p.scale + add;
+        for (int e = 0; e < D; ++e) dot = fmaf(qr[e], kv_at<F16>(p.k, kb + e), dot);
+        float score = dot * p.scale;
+        if (p.soft_cap > 0.0f) score = p.soft_cap * tanhf(score / p.soft_cap);
+        score += add;
         float next;
         double prev_s, cur_s;
         if (isfinite(score)) {
@@ -391,10 +450,11 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(AttnParams p) {
             cur_s = exp(static_cast<double>(score - next));
         }
         den = den * prev_s + cur_s;
-        weighted = weighted * prev_s + cur_s * kv_at<F16>(p.v, kb + static_cast<long long>(ki) * D + j);
+        weighted = weighted * prev_s + cur_s * kv_at<F16>(p.v, kb + j);
         running = next;
     }
-    p.out[idx * D + j] = den == 0.0 ? 0.0f : static_cast<float>(weighted / den);
+    p.out[b * p.q_sb + h * p.q_sh + qi * p.q_sq + j] =
+        den == 0.0 ? 0.0f : static_cast<float>(weighted / (den + static_cast<double>(p.norm_eps)));
 }
 
 __global__ void mask_check_kernel(const float *__restrict__ mask, long long n, int *__restrict__ bad) {
@@ -407,7 +467,7 @@ __global__ void mask_check_kernel(const float *__restrict__ mask, long long n, i
 
 __global__ void zero_i32_kernel(int *p) { *p = 0; }
 
-template <int D, int G, bool F16>
+template <int D, int G, bool F16, bool PAGED>
 int launch_split(const AttnParams &p, int splits, int chunk, float *part, hipStream_t s) {
     constexpr int WAVES = (G <= 4) ? 4 : 2;
     constexpr int NG = (64 / (D / 8)) * WAVES;
@@ -417,23 +477,29 @@ int launch_split(const AttnParams &p, int splits, int chunk, float *part, hipStr
     // Partials: o as [rows][splits][D], then (m, l) as [rows][splits][2].
     float *part_o = part;
     float *part_ml = part ? part + rows * splits * D : nullptr;
-    hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES>), grid, dim3(WAVES * 64), lds, s, p, splits, chunk, part_o,
-                       part_ml);
+    hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES, PAGED>), grid, dim3(WAVES * 64), lds, s, p, splits, chunk,
+                       part_o, part_ml);
     if (splits > 1)
-        hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, p.out, part_o,
+        hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, p, part_o,
                            part_ml, splits);
     return ALJABR_ROCM_OK;
 }
 
-template <int D, bool F16>
+template <int D, bool F16, bool PAGED>
 int launch_g(const AttnParams &p, int G, int splits, int chunk, float *part, hipStream_t s) {
     switch (G) {
-    case 1: return launch_split<D, 1, F16>(p, splits, chunk, part, s);
-    case 2: return launch_split<D, 2, F16>(p, splits, chunk, part, s);
-    case 4: return launch_split<D, 4, F16>(p, splits, chunk, part, s);
-    case 8: return launch_split<D, 8, F16>(p, splits, chunk, part, s);
+    case 1: return launch_split<D, 1, F16, PAGED>(p, splits, chunk, part, s);
+    case 2: return launch_split<D, 2, F16, PAGED>(p, splits, chunk, part, s);
+    case 4: return launch_split<D, 4, F16, PAGED>(p, splits, chunk, part, s);
+    case 8: return launch_split<D, 8, F16, PAGED>(p, splits, chunk, part, s);
     default: return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "no split attention kernel for %d query heads per KV head", G);
     }
+}
+
+template <int D, bool F16>
+int launch_paged(const AttnParams &p, int G, int splits, int chunk, float *part, hipStream_t s) {
+    return p.block_table ? launch_g<D, F16, true>(p, G, splits, chunk, part, s)
+                         : launch_g<D, F16, false>(p, G, splits, chunk, part, s);
 }
 
 }  // namespace
@@ -447,11 +513,18 @@ size_t attention_scratch_bytes(int B, int Hq, int Sq, int D, int keys) {
 
 // Enqueue attention (no sync). Chooses the split-K kernels for D in {64,128}
 // with G in {1,2,4,8} and 16-byte aligned rows, the generic kernel otherwise.
-int enqueue_attention(const AttnParams &p) {
+int enqueue_attention(const AttnParams &p_in) {
     hipStream_t s = current_stream();
+    AttnParams p = p_in;
+    if (p.q_sq == 0) {                           // default layout [B][Hq][Sq][D]
+        p.q_sq = p.D;
+        p.q_sh = static_cast<long long>(p.Sq) * p.D;
+        p.q_sb = static_cast<long long>(p.Hq) * p.Sq * p.D;
+    }
     const int G = p.Hq / p.Hkv;
     const bool fast = (p.D == 64 || p.D == 128) && (G == 1 || G == 2 || G == 4 || G == 8) && aligned(p.q, 16) &&
-                      aligned(p.k, 16) && aligned(p.v, 16);
+                      aligned(p.out, 16) && aligned(p.k, 16) && aligned(p.v, 16) && p.q_sq % 4 == 0 &&
+                      p.q_sh % 4 == 0 && p.q_sb % 4 == 0;
     if (!fast) {
         const long long n = static_cast<long long>(p.B) * p.Hq * p.Sq * p.D;
         const dim3 grid(static_cast<unsigned>((n + 63) / 64));
@@ -469,7 +542,7 @@ int enqueue_attention(const AttnParams &p) {
         return v >= 1 && v <= 64 ? v : 2;
     }();
     const long long items = static_cast<long long>(p.B) * p.Hkv * p.Sq;
-    const int keys = p.kv_len ? p.cap : p.Sk;
+    const int keys = p.block_table ? p.max_blocks * p.block_size : (p.kv_len ? p.cap : p.Sk);
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     long long want = (static_cast<long long>(per_cu) * cus + items - 1) / items;
     const long long max_splits = (keys + 63) / 64;
@@ -487,10 +560,10 @@ int enqueue_attention(const AttnParams &p) {
         if (!part) return ALJABR_ROCM_ERR_BUFFER;
     }
     if (p.D == 64)
-        return p.kv_f16 ? launch_g<64, true>(p, G, splits, chunk, part, s)
-                        : launch_g<64, false>(p, G, splits, chunk, part, s);
-    return p.kv_f16 ? launch_g<128, true>(p, G, splits, chunk, part, s)
-                    : launch_g<128, false>(p, G, splits, chunk, part, s);
+        return p.kv_f16 ? launch_paged<64, true>(p, G, splits, chunk, part, s)
+                        : launch_paged<64, false>(p, G, splits, chunk, part, s);
+    return p.kv_f16 ? launch_paged<128, true>(p, G, splits, chunk, part, s)
+                    : launch_paged<128, false>(p, G, splits, chunk, part, s);
 }
 
 }  // namespace aljabr
@@ -536,3 +609,114 @@ extern "C" int aljabr_rocm_attention_gqa(void *out, const void *Q, const void *K
     if (rc) return rc;
     return finish_launch("attention_gqa");
 }
+
+namespace aljabr {
+namespace {
+
+// Paged-table validation of aljabr_metal_attention_impl's CPU path
+// (MTLC/aljabr_metal_attention.m:203-226): a sequence may not need more than
+// max_blocks blocks, and every block it uses must be a non-negative index.
+__global__ void paged_check_kernel(const int *__restrict__ block_table, const int *__restrict__ context_lens, int B,
+                                   int block_size, int max_blocks, int *__restrict__ bad) {
+    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= static_cast<long long>(B) * max_blocks) return;
+    const int b = static_cast<int>(i / max_blocks), blk = static_cast<int>(i % max_blocks);
+    const int ctx = context_lens[b];
+    if (ctx <= 0) return;
+    const long long need = (static_cast<long long>(ctx) + block_size - 1) / block_size;
+    if (blk == 0 && need > max_blocks) atomicOr(bad, 1);
+    if (blk < need && block_table[i] < 0) atomicOr(bad, 1);
+}
+
+int paged_attention(void *out, const void *Q, const void *K_cache, const void *V_cache, const int *block_table,
+                    const int *context_lens, int B, int T, int H, int H_kv, int D, int block_size, int max_blocks,
+                    float scale, int is_causal, int query_start_pos, int sliding_window, float soft_cap) {
+    ALJ_CHECK_READY();
+    // Status codes as aljabr_metal_attention_impl (MTLC/aljabr_metal_attention.m:166-172).
+    if (H_kv <= 0 || H % H_kv != 0)
+        return fail(ALJABR_ROCM_ERR_NOT_INITIALIZED, "paged attention: H=%d is not a multiple of H_kv=%d", H, H_kv);
+    if (B <= 0 || T <= 0 || H <= 0 || D <= 0 || block_size <= 0 || max_blocks <= 0)
+        return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "paged attention: dimensions must be positive");
+    ALJ_REQUIRE(out && Q && K_cache && V_cache && block_table && context_lens,
+                "out, Q, K_cache, V_cache, block_table and context_lens must be non-null device pointers");
+    ALJ_REQUIRE(static_cast<long long>(max_blocks) * block_size < (1LL << 31), "max_blocks * block_size too large");
+    hipStream_t s = current_stream();
+    int *flag = static_cast<int *>(stream_scratch(sizeof(int)));
+    if (!flag) return ALJABR_ROCM_ERR_BUFFER;
+    const long long n = static_cast<long long>(B) * max_blocks;
+    hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(1), 0, s, flag);
+    hipLaunchKernelGGL(paged_check_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, block_table,
+                       context_lens, B, block_size, max_blocks, flag);
+    int bad = 0;
+    hipError_t e = hipMemcpyAsync(&bad, flag, sizeof(int), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "paged attention table check: %s", hipGetErrorString(e));
+    if (bad)
+        return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT,
+                    "paged attention: a context needs more than max_blocks blocks or a block index is negative");
+    AttnParams p{};
+    p.out = static_cast<float *>(out);
+    p.q = static_cast<const float *>(Q);
+    p.k = K_cache;
+    p.v = V_cache;
+    p.kv_len = context_lens;
+    p.B = B; p.Hq = H; p.Hkv = H_kv; p.Sq = T; p.D = D;
+    p.Sk = max_blocks * block_size;
+    p.cap = 0;
+    p.scale = scale;
+    p.causal = is_causal != 0;
+    p.kv_f16 = 0;
+    p.block_table = block_table;
+    p.block_size = block_size;
+    p.max_blocks = max_blocks;
+    p.paged_bounds = 1;
+    p.query_start = query_start_pos;
+    p.window = sliding_window;
+    p.soft_cap = soft_cap;
+    p.norm_eps = 1e-9f;                          // inv_sum = 1 / (sum + 1e-9)
+    // Q and out are [B][T][H][D].
+    p.q_sq = static_cast<long long>(H) * D;
+    p.q_sh = D;
+    p.q_sb = static_cast<long long>(T) * H * D;
+    const int rc = enqueue_attention(p);
+    if (rc) return rc;
+    return finish_launch("paged_attention");
+}
+
+}  // namespace
+}  // namespace aljabr
+
+extern "C" {
+
+int aljabr_rocm_paged_attention(void *out, const void *Q, const void *K_cache, const void *V_cache,
+                                const int *block_table, const int *context_lens, int B, int T, int H, int D,
+                                int block_size, int max_blocks, float scale, int is_causal, float soft_cap) {
+    return paged_attention(out, Q, K_cache, V_cache, block_table, context_lens, B, T, H, H, D, block_size, max_blocks,
+                           scale, is_causal, 0, 0, soft_cap);
+}
+
+int aljabr_rocm_paged_attention_windowed(void *out, const void *Q, const void *K_cache, const void *V_cache,
+                                         const int *block_table, const int *context_lens, int B, int T, int H, int D,
+                                         int block_size, int max_blocks, float scale, int is_causal,
+                                         int query_start_pos, int sliding_window, float soft_cap) {
+    return paged_attention(out, Q, K_cache, V_cache, block_table, context_lens, B, T, H, H, D, block_size, max_blocks,
+                           scale, is_causal, query_start_pos, sliding_window, soft_cap);
+}
+
+int aljabr_rocm_paged_attention_gqa(void *out, const void *Q, const void *K_cache, const void *V_cache,
+                                    const int *block_table, const int *context_lens, int B, int T, int H, int H_kv,
+                                    int D, int block_size, int max_blocks, float scale, int is_causal,
+                                    float soft_cap) {
+    return paged_attention(out, Q, K_cache, V_cache, block_table, context_lens, B, T, H, H_kv, D, block_size,
+                           max_blocks, scale, is_causal, 0, 0, soft_cap);
+}
+
+int aljabr_rocm_paged_attention_gqa_windowed(void *out, const void *Q, const void *K_cache, const void *V_cache,
+                                             const int *block_table, const int *context_lens, int B, int T, int H,
+                                             int H_kv, int D, int block_size, int max_blocks, float scale,
+                                             int is_causal, int query_start_pos, int sliding_window, float soft_cap) {
+    return paged_attention(out, Q, K_cache, V_cache, block_table, context_lens, B, T, H, H_kv, D, block_size,
+                           max_blocks, scale, is_causal, query_start_pos, sliding_window, soft_cap);
+}
+
+}  // extern "C"

@@ -8,15 +8,27 @@
 namespace aljabr {
 
 struct AttnParams {
-    float *out;             // [B][Hq][Sq][D] fp32
-    const float *q;         // [B][Hq][Sq][D] fp32
-    const void *k, *v;      // [B][Hkv][cap][D], fp16 or fp32
+    float *out;             // fp32, same layout as q
+    const float *q;         // fp32; [B][Hq][Sq][D] unless the strides below say otherwise
+    const void *k, *v;      // [B][Hkv][cap][D] (or paged, below), fp16 or fp32
     const float *mask;      // [Sq][Sk] additive, or null
     const int *kv_len;      // per-batch visible key count (device), or null for Sk
     int B, Hq, Hkv, Sq, Sk, D, cap;
     float scale;
     int causal;
     int kv_f16;
+    // Paged caches [phys][Hkv][block_size][D]: key j of sequence b is row
+    // j % block_size of block block_table[b * max_blocks + j / block_size].
+    const int *block_table; // null: contiguous caches
+    int block_size, max_blocks;
+    // Key range rule of the paged Metal ABI (MTLC/aljabr_metal_attention.m:146-160,
+    // :192-200) instead of CpuBackend's: query position query_start + qi
+    // (bottom-right when causal without a window and query_start == 0),
+    // optional sliding window.
+    int paged_bounds, query_start, window;
+    float soft_cap;         // > 0: score = soft_cap * tanh(score / soft_cap)
+    float norm_eps;         // output = O / (L + norm_eps)
+    long long q_sb, q_sh, q_sq;   // element strides of q and out (0: [B][Hq][Sq][D])
     float *scratch;         // split partials: caller-owned (graph-safe) when it holds attention_scratch_bytes(),
     size_t scratch_bytes;   // else (null or too small) the stream's scratch
 };

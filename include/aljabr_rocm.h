@@ -171,6 +171,39 @@ int aljabr_rocm_attention_gqa(void *out, const void *Q, const void *K, const voi
                               const void *mask, int B, int Hq, int Hkv, int Sq,
                               int Sk, int D, int kvType, float scale, int causal);
 
+/* Paged-KV attention with the argument lists of the Metal bridge
+ * (MTLC/aljabr_metal_attention.h:14-36, semantics of aljabr_metal_attention_impl,
+ * MTLC/aljabr_metal_attention.m:146-355): Q and out [B,T,H,D] fp32; K/V caches
+ * fp32 [num_blocks][H_kv][block_size][D]; key j of sequence b is row j % block_size of
+ * block block_table[b*max_blocks + j/block_size]; context_lens[b] keys per sequence
+ * (<= 0: zero output). Query t sits at query_start_pos + t, or at
+ * context_len - T + t when causal with no window and query_start_pos == 0; causal
+ * keys reach up to that position, a sliding window > 0 starts at position - window
+ * + 1. soft_cap > 0 caps scores as soft_cap * tanh(score / soft_cap); weights are
+ * exp(s - max) / (sum + 1e-9). Status -1 when H is not a multiple of H_kv (as
+ * Metal), -2 for non-positive sizes, a context longer than max_blocks blocks or a
+ * negative block index. All pointers are device pointers; the call checks the
+ * table on the device and waits for that check. */
+int aljabr_rocm_paged_attention(void *out, const void *Q, const void *K_cache, const void *V_cache,
+                                const int *block_table, const int *context_lens, int B, int T, int H,
+                                int D, int block_size, int max_blocks, float scale, int is_causal,
+                                float soft_cap);
+int aljabr_rocm_paged_attention_windowed(void *out, const void *Q, const void *K_cache,
+                                         const void *V_cache, const int *block_table,
+                                         const int *context_lens, int B, int T, int H, int D,
+                                         int block_size, int max_blocks, float scale, int is_causal,
+                                         int query_start_pos, int sliding_window, float soft_cap);
+int aljabr_rocm_paged_attention_gqa(void *out, const void *Q, const void *K_cache, const void *V_cache,
+                                    const int *block_table, const int *context_lens, int B, int T,
+                                    int H, int H_kv, int D, int block_size, int max_blocks,
+                                    float scale, int is_causal, float soft_cap);
+int aljabr_rocm_paged_attention_gqa_windowed(void *out, const void *Q, const void *K_cache,
+                                             const void *V_cache, const int *block_table,
+                                             const int *context_lens, int B, int T, int H, int H_kv,
+                                             int D, int block_size, int max_blocks, float scale,
+                                             int is_causal, int query_start_pos, int sliding_window,
+                                             float soft_cap);
+
 /* ======================================================================== */
 /* decode-step element-wise ops (fp32)                                       */
 /* ======================================================================== */

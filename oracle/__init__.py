@@ -71,6 +71,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "orc_f16_matvec": (None, [_P, _P, _I64, _I64, _I32, _P, ctypes.c_int]),
         "orc_attention_gqa": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                             ctypes.c_int, _P, ctypes.c_int]),
+        "orc_paged_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F,
+                                               _I32, _I32, _I32, _F, _P]),
         "orc_rmsnorm": (None, [_P, _P, _P, _I32, _F]),
         "orc_rope": (None, [_P, _I32, _I32, _I32, _F]),
         "orc_swiglu": (None, [_P, _P, _P, _I32]),
@@ -228,6 +230,25 @@ def attention_gqa(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask=None, causal
     if rc != 0:
         raise ValueError("GQA expects Q[B,Hq,Sq,D], K/V[B,Hkv,Sk,D] and a finite, non-NaN mask")
     return out
+
+
+def paged_attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, block_table: np.ndarray,
+                    context_lens: np.ndarray, scale: float, causal: bool = True, query_start_pos: int = 0,
+                    sliding_window: int = 0, soft_cap: float = 0.0):
+    """q [B,T,H,D], caches [blocks,Hkv,block_size,D] float32, block_table
+    [B,max_blocks] int32, context_lens [B] int32 -> (status, out [B,T,H,D])."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    kc = np.ascontiguousarray(kc, dtype=np.float32)
+    vc = np.ascontiguousarray(vc, dtype=np.float32)
+    bt = np.ascontiguousarray(block_table, dtype=np.int32)
+    cl = np.ascontiguousarray(context_lens, dtype=np.int32)
+    b, t, h, d = q.shape
+    hkv, bs = kc.shape[1], kc.shape[2]
+    out = np.full_like(q, np.nan)
+    rc = lib().orc_paged_attention(_ptr(q), _ptr(kc), _ptr(vc), _ptr(bt), _ptr(cl), b, t, h, hkv, d, bs,
+                                   bt.shape[1], scale, int(bool(causal)), query_start_pos, sliding_window,
+                                   soft_cap, _ptr(out))
+    return rc, out
 
 
 # ---- element-wise ---------------------------------------------------------

@@ -487,6 +487,74 @@ int orc_attention_gqa(const float *q, const float *k, const float *v,
     return 0;
 }
 
+/* Paged-KV attention of the Metal bridge's CPU path
+ * (MTLC/aljabr_metal_attention.m:146-160 resolve_attention_bounds, :162-355
+ * aljabr_metal_attention_impl): Q/out [B,T,H,D], caches [phys][H_kv][bs][D]
+ * through block_table[b*max_blocks + blk]; float scores dot*scale, optional
+ * soft cap, exp(s - max), weights * 1/(sum + 1e-9), float weighted V sums. */
+int orc_paged_attention(const float *q, const float *kc, const float *vc, const int32_t *block_table,
+                        const int32_t *context_lens, int32_t b_n, int32_t t_n, int32_t h_n, int32_t hkv,
+                        int32_t d, int32_t block_size, int32_t max_blocks, float scale, int32_t is_causal,
+                        int32_t query_start_pos, int32_t sliding_window, float soft_cap, float *out) {
+    if (hkv <= 0 || h_n % hkv != 0) return -1;
+    if (b_n <= 0 || t_n <= 0 || h_n <= 0 || d <= 0 || block_size <= 0 || max_blocks <= 0) return -2;
+    int32_t group = h_n / hkv;
+    for (int32_t b = 0; b < b_n; b++) {
+        int32_t ctx = context_lens[b];
+        float *bo = out + (int64_t)b * t_n * h_n * d;
+        if (ctx <= 0) {
+            memset(bo, 0, (size_t)t_n * h_n * d * sizeof(float));
+            continue;
+        }
+        int32_t nblk = (ctx + block_size - 1) / block_size;
+        if (nblk > max_blocks) return -2;
+        for (int32_t blk = 0; blk < nblk; blk++)
+            if (block_table[(int64_t)b * max_blocks + blk] < 0) return -2;
+        float *row = (float *)malloc((size_t)ctx * sizeof(float));
+        for (int32_t h = 0; h < h_n; h++) {
+            int32_t kvh = h / group;
+            for (int32_t t = 0; t < t_n; t++) {
+                const float *qh = q + (((int64_t)b * t_n + t) * h_n + h) * d;
+                float *oh = bo + ((int64_t)t * h_n + h) * d;
+                int32_t qpos = query_start_pos;
+                if (is_causal && sliding_window <= 0 && query_start_pos == 0 && ctx >= t_n) qpos = ctx - t_n;
+                int32_t abs_pos = qpos + t;
+                int32_t upper = is_causal ? abs_pos : ctx - 1;
+                if (upper >= ctx) upper = ctx - 1;
+                int32_t lower = sliding_window > 0 ? abs_pos - sliding_window + 1 : 0;
+                if (lower < 0) lower = 0;
+                memset(oh, 0, (size_t)d * sizeof(float));
+                if (upper < lower) continue;
+                float mx = -1e30f;
+                for (int32_t s = lower; s <= upper; s++) {
+                    int64_t phys = block_table[(int64_t)b * max_blocks + s / block_size];
+                    const float *kh = kc + ((phys * hkv + kvh) * block_size + s % block_size) * d;
+                    float dot = 0.0f;
+                    for (int32_t e = 0; e < d; e++) dot += qh[e] * kh[e];
+                    float score = dot * scale;
+                    if (soft_cap > 0.0f) score = soft_cap * tanhf(score / soft_cap);
+                    row[s] = score;
+                    if (score > mx) mx = score;
+                }
+                float sum = 0.0f;
+                for (int32_t s = lower; s <= upper; s++) {
+                    row[s] = expf(row[s] - mx);
+                    sum += row[s];
+                }
+                float inv = 1.0f / (sum + 1e-9f);
+                for (int32_t s = lower; s <= upper; s++) row[s] *= inv;
+                for (int32_t s = lower; s <= upper; s++) {
+                    int64_t phys = block_table[(int64_t)b * max_blocks + s / block_size];
+                    const float *vh = vc + ((phys * hkv + kvh) * block_size + s % block_size) * d;
+                    for (int32_t e = 0; e < d; e++) oh[e] += row[s] * vh[e];
+                }
+            }
+        }
+        free(row);
+    }
+    return 0;
+}
+
 /* ------------------------------------------------------------------------ */
 /* decode-step element-wise ops                                              */
 /* ------------------------------------------------------------------------ */

@@ -110,6 +110,11 @@ int orc_attention_gqa(const float *q, const float *k, const float *v,
                       const float *mask, int64_t b, int64_t hq, int64_t hkv,
                       int64_t sq, int64_t sk, int64_t d, int causal,
                       float *out, int threads);
+/* Paged-KV attention, MTLC/aljabr_metal_attention.m:146-355 (CPU bridge path). */
+int orc_paged_attention(const float *q, const float *kc, const float *vc, const int32_t *block_table,
+                        const int32_t *context_lens, int32_t b_n, int32_t t_n, int32_t h_n, int32_t hkv,
+                        int32_t d, int32_t block_size, int32_t max_blocks, float scale, int32_t is_causal,
+                        int32_t query_start_pos, int32_t sliding_window, float soft_cap, float *out);
 
 /* ---- decode-step element-wise ops --------------------------------------- */
 

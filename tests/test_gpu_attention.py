@@ -132,3 +132,86 @@ def test_full_size_b64_s32768_spot_rows(rocm, dev, oracle):
         assert rel_l2(o[bi:bi + 1, kvh * 4:(kvh + 1) * 4], ref) <= TOL
     del k, v
     torch.cuda.empty_cache()
+
+
+# ---- paged KV (the Metal bridge's ABI) -------------------------------------
+
+def _paged_inputs(oracle, b, t, h, hkv, d, bs, mb, ctx, seed):
+    q = oracle.normal(seed, b * t * h * d).reshape(b, t, h, d)
+    kc = oracle.normal(seed + 1, b * mb * hkv * bs * d).reshape(b * mb, hkv, bs, d)
+    vc = oracle.normal(seed + 2, b * mb * hkv * bs * d).reshape(b * mb, hkv, bs, d)
+    table = np.random.default_rng(seed).permutation(b * mb).astype(np.int32).reshape(b, mb)
+    return q, kc, vc, table, np.array(ctx, np.int32)
+
+
+def run_paged(rocm, dev, q, kc, vc, table, cl, scale, causal=1, qsp=0, window=0, cap=0.0, fill=np.nan):
+    b, t, h, d = q.shape
+    hkv, bs = kc.shape[1], kc.shape[2]
+    out = dev.put(np.full(q.size, fill, np.float32))
+    # Keep every device buffer referenced until the call returns: a freed
+    # temporary's memory is handed to the next upload.
+    bufs = [dev.put(a) for a in (q, kc, vc, table, cl)]
+    args = [dev.ptr(out)] + [dev.ptr(t_) for t_ in bufs] + [b, t, h, hkv, d, bs, table.shape[1], scale, causal]
+    if qsp or window:
+        rocm.call("aljabr_rocm_paged_attention_gqa_windowed", *args, qsp, window, cap)
+    else:
+        rocm.call("aljabr_rocm_paged_attention_gqa", *args, cap)
+    return dev.get(out).reshape(q.shape)
+
+
+# (B, T, H, Hkv, D, block size, max blocks, context lengths, causal, query start, window, soft cap):
+# decode and short prefill rows, every split-kernel grouping and the generic
+# kernel (D = 80), ragged and empty contexts, windows and soft caps.
+PAGED = [
+    (1, 1, 32, 8, 128, 16, 130, [2049], 1, 0, 0, 0.0),
+    (3, 1, 32, 8, 128, 32, 20, [600, 0, 17], 1, 0, 0, 0.0),
+    (2, 4, 8, 8, 64, 16, 12, [150, 5], 1, 0, 0, 30.0),
+    (2, 1, 16, 2, 128, 16, 40, [613, 301], 1, 612, 64, 0.0),
+    (1, 3, 8, 1, 64, 8, 16, [100], 0, 0, 0, 0.0),
+    (2, 2, 12, 4, 80, 16, 8, [100, 33], 1, 0, 0, 5.0),
+]
+
+
+@pytest.mark.parametrize("case", PAGED, ids=[f"paged{i}" for i in range(len(PAGED))])
+def test_paged_attention_matches_oracle(rocm, dev, oracle, case):
+    b, t, h, hkv, d, bs, mb, ctx, causal, qsp, window, cap = case
+    q, kc, vc, table, cl = _paged_inputs(oracle, b, t, h, hkv, d, bs, mb, ctx, seed=sum(ctx) + d)
+    scale = 1.0 / np.sqrt(d)
+    rc, ref = oracle.paged_attention(q, kc, vc, table, cl, scale, causal, qsp, window, cap)
+    assert rc == 0
+    out = run_paged(rocm, dev, q, kc, vc, table, cl, scale, causal, qsp, window, cap)
+    assert rel_l2(out, ref) <= TOL
+    for bi, c in enumerate(ctx):
+        if c <= 0:
+            assert np.all(out[bi] == 0)
+
+
+def test_paged_attention_zero_length_context_zero_fills(rocm, dev, oracle):
+    """MetalBindingNativeFallbackTest.nativeAttentionZeroLengthContextZeroFillsOutput
+    (backend/metal/.../MetalBindingNativeFallbackTest.java:109-150): out starts at 42."""
+    q = np.ones((1, 2, 1, 64), np.float32)
+    kc = np.zeros((1, 1, 4, 64), np.float32)
+    out = run_paged(rocm, dev, q, kc, kc, np.zeros((1, 1), np.int32), np.zeros(1, np.int32), 1.0, fill=42.0)
+    assert np.array_equal(out, np.zeros_like(out))
+
+
+def test_paged_attention_statuses(rocm, dev, oracle):
+    q, kc, vc, table, cl = _paged_inputs(oracle, 1, 1, 8, 2, 64, 16, 4, [40], seed=3)
+    bufs = [dev.put(a) for a in (q, q, kc, vc, table, cl)]
+    with pytest.raises(rocm.RocmError) as e:           # H not a multiple of H_kv: -1, as the Metal bridge
+        rocm.call("aljabr_rocm_paged_attention_gqa", *[dev.ptr(t_) for t_ in bufs], 1, 1, 8, 3, 64, 16, 4,
+                  0.125, 1, 0.0)
+    assert e.value.status == -1
+    bad = table.copy()
+    bad[0, 1] = -4                                     # a block the context uses
+    with pytest.raises(rocm.RocmError) as e:
+        run_paged(rocm, dev, q, kc, vc, bad, cl, 0.125)
+    assert e.value.status == rocm.ERR_BAD_ARGUMENT
+    with pytest.raises(rocm.RocmError) as e:           # 65 keys need 5 blocks of 16, the table has 4
+        run_paged(rocm, dev, q, kc, vc, table, np.array([65], np.int32), 0.125)
+    assert e.value.status == rocm.ERR_BAD_ARGUMENT
+    bad[0, 3] = -1                                     # unused entries are not checked
+    bad[0, 1] = table[0, 1]
+    out = run_paged(rocm, dev, q, kc, vc, bad, np.array([40], np.int32), 0.125)
+    rc, ref = oracle.paged_attention(q, kc, vc, bad, np.array([40], np.int32), 0.125)
+    assert rc == 0 and rel_l2(out, ref) <= TOL

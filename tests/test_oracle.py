@@ -309,6 +309,89 @@ def test_attention_vs_float64_softmax(oracle):
     assert np.allclose(out2[0, 0, 0], v[0, 0].mean(axis=0), atol=1e-5)
 
 
+def _paged_case(oracle, b, t, h, hkv, d, bs, max_blocks, ctx, seed):
+    """Random q and a contiguous K/V per sequence, scattered into physical
+    blocks through a random permutation."""
+    q = oracle.normal(seed, b * t * h * d).reshape(b, t, h, d)
+    kv_len = max_blocks * bs
+    k = oracle.normal(seed + 1, b * hkv * kv_len * d).reshape(b, hkv, kv_len, d)
+    v = oracle.normal(seed + 2, b * hkv * kv_len * d).reshape(b, hkv, kv_len, d)
+    perm = np.random.default_rng(seed).permutation(b * max_blocks).astype(np.int32)
+    table = perm.reshape(b, max_blocks)
+    kc = np.zeros((b * max_blocks, hkv, bs, d), np.float32)
+    vc = np.zeros_like(kc)
+    for bi in range(b):
+        for blk in range(max_blocks):
+            kc[table[bi, blk]] = k[bi, :, blk * bs:(blk + 1) * bs]
+            vc[table[bi, blk]] = v[bi, :, blk * bs:(blk + 1) * bs]
+    return q, k, v, kc, vc, table, np.array(ctx, np.int32)
+
+
+def test_paged_attention_zero_length_context_zero_fills(oracle):
+    """MetalBindingNativeFallbackTest.nativeAttentionZeroLengthContextZeroFillsOutput
+    (backend/metal/.../MetalBindingNativeFallbackTest.java:109-150)."""
+    q = np.ones((1, 2, 1, 2), np.float32)
+    kc = np.zeros((1, 1, 4, 2), np.float32)
+    rc, out = oracle.paged_attention(q, kc, kc, np.zeros((1, 1), np.int32), np.zeros(1, np.int32), 1.0, True)
+    assert rc == 0 and np.array_equal(out, np.zeros_like(out))
+
+
+def test_paged_attention_matches_dense_oracle(oracle):
+    """Through any block permutation, causal paged attention without window or
+    cap is the dense attention of the (pinned) CpuBackend restatement on the
+    first context_len keys, bottom-right aligned."""
+    b, t, h, hkv, d, bs, mb = 2, 3, 8, 2, 16, 8, 5
+    ctx = [37, 9]
+    q, k, v, kc, vc, table, cl = _paged_case(oracle, b, t, h, hkv, d, bs, mb, ctx, 61)
+    rc, out = oracle.paged_attention(q, kc, vc, table, cl, 1.0 / math.sqrt(d), True)
+    assert rc == 0
+    for bi in range(b):
+        dense = oracle.attention_gqa(q[bi:bi + 1].transpose(0, 2, 1, 3), k[bi:bi + 1, :, :ctx[bi]],
+                                     v[bi:bi + 1, :, :ctx[bi]], None, True)
+        assert rel_l2(out[bi], dense[0].transpose(1, 0, 2)) < 1e-5
+    # moving the blocks to other physical slots (and the table with them)
+    # gives the same bits
+    perm = np.random.default_rng(5).permutation(b * mb).astype(np.int32)
+    kc3 = np.empty_like(kc)
+    vc3 = np.empty_like(vc)
+    kc3[perm] = kc
+    vc3[perm] = vc
+    rc3, out3 = oracle.paged_attention(q, kc3, vc3, perm[table], cl, 1.0 / math.sqrt(d), True)
+    assert rc3 == 0 and np.array_equal(out3, out)
+
+
+def test_paged_attention_window_cap_and_errors(oracle):
+    b, t, h, hkv, d, bs, mb = 1, 1, 4, 4, 8, 4, 4
+    q, k, v, kc, vc, table, cl = _paged_case(oracle, b, t, h, hkv, d, bs, mb, [13], 71)
+    sc = 1.0 / math.sqrt(d)
+    # sliding window W at query position 12 (a window disables the bottom-right
+    # default, so the position is passed): the last W keys only
+    rc, out = oracle.paged_attention(q, kc, vc, table, cl, sc, True, 12, 5)
+    dense = oracle.attention_gqa(q.transpose(0, 2, 1, 3), k[:, :, 8:13], v[:, :, 8:13], None, False)
+    assert rc == 0 and rel_l2(out, dense.transpose(0, 2, 1, 3)) < 1e-5
+    # window 1: exactly the value row of the query position
+    rc, out = oracle.paged_attention(q, kc, vc, table, cl, sc, True, 12, 1)
+    assert rc == 0 and np.allclose(out[0, 0], v[0, :, 12], atol=1e-6)
+    # a cap far above every score changes nothing; identical keys give the mean of V for any cap
+    _, base = oracle.paged_attention(q, kc, vc, table, cl, sc, True)
+    _, capped = oracle.paged_attention(q, kc, vc, table, cl, sc, True, 0, 0, 1e6)
+    assert rel_l2(capped, base) < 1e-6
+    kc_same = np.repeat(kc[:, :, :1], bs, axis=2)
+    kc_same[:] = kc_same[table[0, 0]]
+    _, flat = oracle.paged_attention(q, kc_same, vc, table, cl, sc, True, 0, 0, 0.5)
+    assert np.allclose(flat[0, 0], v[0, :, :13].mean(axis=1), atol=1e-5)
+    # explicit query position without causal bottom-right alignment
+    rc, early = oracle.paged_attention(q, kc, vc, table, cl, sc, True, 3, 0)
+    dense = oracle.attention_gqa(q.transpose(0, 2, 1, 3), k[:, :, :4], v[:, :, :4], None, False)
+    assert rc == 0 and rel_l2(early, dense.transpose(0, 2, 1, 3)) < 1e-5
+    # statuses of aljabr_metal_attention_impl
+    assert oracle.paged_attention(q.reshape(1, 1, 4, 8)[:, :, :3], kc, vc, table, cl, sc)[0] == -1
+    bad = table.copy()
+    bad[0, 2] = -1
+    assert oracle.paged_attention(q, kc, vc, bad, cl, sc)[0] == -2
+    assert oracle.paged_attention(q, kc, vc, table, np.array([17], np.int32), sc)[0] == -2
+
+
 # ---------------------------------------------------------- decode-step ops
 
 def test_vector_ops_known_answers(oracle):
