@@ -85,6 +85,10 @@ int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const 
 // caller that has C cleared or holding a residual saves the clearing launch.
 int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
                      int M, bool accumulate = false);
+// The same over up to three matrices of one K stacked in one launch (all but
+// the last with a multiple of 32 rows); outs[i].y is [M][outs[i].n].
+int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M,
+                           bool accumulate);
 // fp16-weight small-M GEMM on MFMA (2 <= M <= 32, K in {512, 1024, 2048,
 // 4096}, W and A 16-byte aligned); deterministic (no atomics).
 int enqueue_f16_mfma(float *C, const float *A, const uint16_t *W, int K, int N, int M);

@@ -314,12 +314,20 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                               static_cast<long long>(B) * kvd}};
             ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, S(m->attn_norm), B, dim, c.eps, &z));
             ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * (qd + 2.0 * kvd)) * f4);
-            ALJ_TRY(mm(m->q, m->xb, m->wq[l], m->wq_s[l], dim, qd, false, nullptr));
-            ALJ_MARK("q_gemm", mm_bytes(qd, dim, true));
-            ALJ_TRY(mm(m->k, m->xb, m->wk[l], m->wk_s[l], dim, kvd, false, nullptr));
-            ALJ_MARK("kv_gemm", mm_bytes(kvd, dim, true));
-            ALJ_TRY(mm(m->v, m->xb, m->wv[l], m->wv_s[l], dim, kvd, false, nullptr));
-            ALJ_MARK("kv_gemm", mm_bytes(kvd, dim, true));
+            // Q, K and V in one matrix-core launch where the shapes allow.
+            const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq_s), qd},
+                                    {m->k, W(m->wk), S(m->wk_s), kvd},
+                                    {m->v, W(m->wv), S(m->wv_s), kvd}};
+            rc = B >= 2 && B <= 64 ? enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, true)
+                                   : ALJABR_ROCM_ERR_UNSUPPORTED;
+            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                ALJ_TRY(mm(m->q, m->xb, m->wq[l], m->wq_s[l], dim, qd, false, nullptr));
+                ALJ_TRY(mm(m->k, m->xb, m->wk[l], m->wk_s[l], dim, kvd, false, nullptr));
+                ALJ_TRY(mm(m->v, m->xb, m->wv[l], m->wv_s[l], dim, kvd, false, nullptr));
+            } else if (rc != ALJABR_ROCM_OK) {
+                return rc;
+            }
+            ALJ_MARK("qkv_gemm", mm_bytes(qd + 2LL * kvd, dim, true));
         }
         if (!fused1) {
             rc = enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base);
@@ -379,10 +387,17 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                              {static_cast<long long>(B) * ffn, static_cast<long long>(B) * ffn, 0}};
             ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, S(m->ffn_norm), B, dim, c.eps, &z));
             ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * 2.0 * ffn) * f4);
-            ALJ_TRY(mm(m->gate, m->xb, m->w_gate[l], m->w_gate_s[l], dim, ffn, false, nullptr));
-            ALJ_MARK("gate_up_gemm", mm_bytes(ffn, dim, true));
-            ALJ_TRY(mm(m->up, m->xb, m->w_up[l], m->w_up_s[l], dim, ffn, false, nullptr));
-            ALJ_MARK("gate_up_gemm", mm_bytes(ffn, dim, true));
+            const RowsOut gu[2] = {{m->gate, W(m->w_gate), S(m->w_gate_s), ffn},
+                                   {m->up, W(m->w_up), S(m->w_up_s), ffn}};
+            rc = B >= 2 && B <= 64 ? enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, true)
+                                   : ALJABR_ROCM_ERR_UNSUPPORTED;
+            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                ALJ_TRY(mm(m->gate, m->xb, m->w_gate[l], m->w_gate_s[l], dim, ffn, false, nullptr));
+                ALJ_TRY(mm(m->up, m->xb, m->w_up[l], m->w_up_s[l], dim, ffn, false, nullptr));
+            } else if (rc != ALJABR_ROCM_OK) {
+                return rc;
+            }
+            ALJ_MARK("gate_up_gemm", mm_bytes(2LL * ffn, dim, true));
             ALJ_TRY(enqueue_swiglu(m->hb, m->gate, m->up, static_cast<long long>(B) * ffn));
             ALJ_MARK("swiglu", B * 3.0 * ffn * f4);
             ALJ_TRY(mm(m->x, m->hb, m->w_down[l], m->w_down_s[l], ffn, dim, true, m->xb));

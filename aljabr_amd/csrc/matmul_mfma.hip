@@ -45,13 +45,41 @@ constexpr int kMmThreads = kMmWaves * 64;
 constexpr int kMmRowsPerWg = kMmWaves * 32;
 constexpr int kTableBytes = 256 * 64 * 4;       // 256 entries x 64 replicas x fp16 pair
 
+// Up to three weight matrices of the same K stacked as one row space (the
+// decode step's Q/K/V or gate/up in one launch): segment s owns stacked rows
+// [end[s-1], end[s]); every segment but the last holds a multiple of 32 rows,
+// so a 32-row tile never straddles two.
 struct MmArgs {
-    float *y;
+    float *y[3];
     const float *x;
+    const uint8_t *w[3];
+    const float *absmax[3];
+    int end[3];
+    int nseg;
+    int M, N, K, bs_shift;   // N: stacked rows
+};
+
+// The segment of a tile starting at stacked row r0 (past the end: the last
+// segment, with local rows past its end).
+struct TileRef {
     const uint8_t *w;
     const float *absmax;
-    int M, N, K, bs_shift;
+    float *y;
+    int local0, n;
 };
+
+__device__ __forceinline__ TileRef tile_ref(const MmArgs &a, int r0) {
+    int s = (r0 >= a.end[0]) + (r0 >= a.end[1]);
+    if (s > a.nseg - 1) s = a.nseg - 1;
+    const int start = s == 0 ? 0 : s == 1 ? a.end[0] : a.end[1];
+    TileRef t;
+    t.w = s == 0 ? a.w[0] : s == 1 ? a.w[1] : a.w[2];
+    t.absmax = s == 0 ? a.absmax[0] : s == 1 ? a.absmax[1] : a.absmax[2];
+    t.y = s == 0 ? a.y[0] : s == 1 ? a.y[1] : a.y[2];
+    t.local0 = r0 - start;
+    t.n = (s == 0 ? a.end[0] : s == 1 ? a.end[1] : a.end[2]) - start;
+    return t;
+}
 
 __device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
     const _Float16 a = static_cast<_Float16>(lo), b = static_cast<_Float16>(hi);
@@ -95,11 +123,11 @@ __device__ __forceinline__ void build_pair16_table(uint32_t *tbl_s, int tid) {
 // 32-row tile, bytes 16*(lane%8) of iteration it's segment. The first unit
 // of a tile also loads its SB scales: lane covers row lane/2, half lane%2.
 template <int ITERS, int SB>
-__device__ __forceinline__ void issue_unit(u32x4 (&q)[4], float (&sc)[SB / 2], const MmArgs &a, int r0, int it,
-                                           int ks0, int lane) {
+__device__ __forceinline__ void issue_unit(u32x4 (&q)[4], float (&sc)[SB / 2], const MmArgs &a, const TileRef &tr,
+                                           int it, int ks0, int lane) {
     if (it == 0) {
-        const int srow = min(r0 + (lane >> 1), a.N - 1);
-        const float *sp = a.absmax + ((static_cast<size_t>(srow) * a.K + ks0) >> 6) + (SB / 2) * (lane & 1);
+        const int srow = min(tr.local0 + (lane >> 1), tr.n - 1);
+        const float *sp = tr.absmax + ((static_cast<size_t>(srow) * a.K + ks0) >> 6) + (SB / 2) * (lane & 1);
         if constexpr (SB / 2 == 4) {
             const f32x4 v = *reinterpret_cast<const f32x4 *>(sp);
             sc[0] = v.x; sc[1] = v.y; sc[2] = v.z; sc[3] = v.w;
@@ -111,8 +139,8 @@ __device__ __forceinline__ void issue_unit(u32x4 (&q)[4], float (&sc)[SB / 2], c
     const size_t row_bytes = static_cast<size_t>(a.K) >> 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int row = min(r0 + 8 * i + (lane >> 3), a.N - 1);
-        q[i] = *reinterpret_cast<const u32x4 *>(a.w + row * row_bytes + (ks0 >> 1) + 128 * it + 16 * (lane & 7));
+        const int row = min(tr.local0 + 8 * i + (lane >> 3), tr.n - 1);
+        q[i] = *reinterpret_cast<const u32x4 *>(tr.w + row * row_bytes + (ks0 >> 1) + 128 * it + 16 * (lane & 7));
     }
     __builtin_amdgcn_sched_barrier(0);           // keep units in issue order
 }
@@ -178,13 +206,13 @@ __global__ __launch_bounds__(kMmThreads) void nf4_mm_kernel(MmArgs a) {
     // once stalls the wave at issue until most of it has arrived).
     constexpr int U = NT * ITERS;
     constexpr int W = 2;
-    int r0[NT];
+    TileRef tr[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) r0[t] = blockIdx.x * (kMmRowsPerWg * NT) + t * kMmRowsPerWg + wave * 32;
+    for (int t = 0; t < NT; ++t) tr[t] = tile_ref(a, blockIdx.x * (kMmRowsPerWg * NT) + t * kMmRowsPerWg + wave * 32);
     u32x4 qc[U][4];
     float sc[NT][SB / 2];
 #pragma unroll
-    for (int u = 0; u < W && u < U; ++u) issue_unit<ITERS, SB>(qc[u], sc[u / ITERS], a, r0[u / ITERS], u % ITERS, ks0, lane);
+    for (int u = 0; u < W && u < U; ++u) issue_unit<ITERS, SB>(qc[u], sc[u / ITERS], a, tr[u / ITERS], u % ITERS, ks0, lane);
 
     build_pair16_table(tbl_s, tid);
     __syncthreads();
@@ -194,7 +222,8 @@ __global__ __launch_bounds__(kMmThreads) void nf4_mm_kernel(MmArgs a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         if (u + W < U)
-            issue_unit<ITERS, SB>(qc[u + W], sc[(u + W) / ITERS], a, r0[(u + W) / ITERS], (u + W) % ITERS, ks0, lane);
+            issue_unit<ITERS, SB>(qc[u + W], sc[(u + W) / ITERS], a, tr[(u + W) / ITERS], (u + W) % ITERS, ks0,
+                                      lane);
         const int t = u / ITERS, it = u % ITERS;
         if (it == 0) {
             // Scales of this tile to the MFMA layout: row nl, all SB blocks.
@@ -238,14 +267,14 @@ __global__ __launch_bounds__(kMmThreads) void nf4_mm_kernel(MmArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         }
         if (it == ITERS - 1) {
-            const int n = r0[t] + nl;
-            if (n < a.N) {
+            const int n = tr[t].local0 + nl;
+            if (n < tr[t].n) {
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int m = 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
-                        if (m < a.M) unsafeAtomicAdd(a.y + static_cast<size_t>(m) * a.N + n, acc[mt][r]);
+                        if (m < a.M) unsafeAtomicAdd(tr[t].y + static_cast<size_t>(m) * tr[t].n + n, acc[mt][r]);
                     }
             }
         }
@@ -275,17 +304,41 @@ void launch_mm(const MmArgs &args, hipStream_t s) {
 // M in [2, 64], K % 512 == 0, block size 64, codes, absmax and x 16-byte aligned.
 // K-slices of 512 (M <= 32) or 256 (two m-tiles) keep every operand of a
 // slice in registers without spills.
-int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
-                     int M, bool accumulate) {
-    if (M < 2 || M > 64 || K % 512 != 0 || bs_shift != 6 || !aligned(Bq, 16) || !aligned(A, 16) ||
-        !aligned(absmax, 16))
+int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M,
+                           bool accumulate) {
+    if (nseg < 1 || nseg > 3 || M < 2 || M > 64 || K % 512 != 0 || bs_shift != 6 || !aligned(A, 16))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
+    MmArgs args{};
+    long long end = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (i < nseg) {
+            const RowsOut &o = outs[i];
+            if (o.n <= 0 || !aligned(o.w, 16) || !aligned(o.absmax, 16) || (i < nseg - 1 && o.n % 32 != 0))
+                return ALJABR_ROCM_ERR_UNSUPPORTED;
+            end += o.n;
+            if (end > 0x7fff0000LL) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            args.y[i] = o.y;
+            args.w[i] = o.w;
+            args.absmax[i] = o.absmax;
+            args.end[i] = static_cast<int>(end);
+        } else {
+            args.end[i] = 0x7fffffff;
+        }
+    }
+    args.nseg = nseg;
+    args.x = A;
+    args.M = M;
+    args.N = static_cast<int>(end);
+    args.K = K;
+    args.bs_shift = bs_shift;
     hipStream_t s = current_stream();
-    const long long total = static_cast<long long>(M) * N;
-    if (!accumulate)   // the K-slices add into C
-        hipLaunchKernelGGL(zero_f32_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, C,
-                           total);
-    MmArgs args{C, A, Bq, absmax, M, N, K, bs_shift};
+    if (!accumulate)   // the K-slices add into the outputs
+        for (int i = 0; i < nseg; ++i) {
+            const long long total = static_cast<long long>(M) * outs[i].n;
+            hipLaunchKernelGGL(zero_f32_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s,
+                               outs[i].y, total);
+        }
+    const int N = args.N;
     const int wgs_n = (N + kMmRowsPerWg - 1) / kMmRowsPerWg;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     // One generation of workgroups (one per CU): the fewest row tiles per
@@ -301,6 +354,12 @@ int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *a
         else launch_mm<2, 256, 4>(args, s);
     }
     return ALJABR_ROCM_OK;
+}
+
+int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
+                     int M, bool accumulate) {
+    const RowsOut o{C, Bq, absmax, N};
+    return enqueue_nf4_mfma_multi(&o, 1, A, K, bs_shift, M, accumulate);
 }
 
 }  // namespace aljabr

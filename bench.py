@@ -40,8 +40,9 @@ def log(msg: str) -> None:
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=600)
+    ap.add_argument("--warmup", type=int, default=600,
+                    help="untimed MLP steps first (the GPU takes ~15 ms of load to reach its steady clocks)")
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough for 512 MB)")
     ap.add_argument("--no-decode", action="store_true", help="skip the Llama decode measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -51,6 +52,8 @@ def parse() -> argparse.Namespace:
                     help="skip the small-M GEMM and attention measurements (BASELINE configs 2 and 4)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 20 times (FETCH_SIZE/WRITE_SIZE calibration)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode-step measurement (for profiling runs; prints its own JSON line)")
     return ap.parse_args()
 
 
@@ -297,6 +300,22 @@ def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, weights, 
             "profiled_ms": round(prof_us / 1e3, 3), "kernels": kernels}
 
 
+def decode_runs(args, abi, torch, stream):
+    """random-init Llama-3-8B-shaped NF4 decode at batch 1 and 32, context 2048."""
+    from aljabr_amd.llama import LLAMA3_8B, random_weights
+    log("building random-init Llama-3-8B-shaped NF4 model")
+    t0 = time.perf_counter()
+    weights = random_weights(LLAMA3_8B, seed=1)
+    log(f"model built in {time.perf_counter() - t0:.1f} s")
+    dec = []
+    for batch in (1, 32):
+        log(f"decode batch {batch}, context 2048")
+        dec.append(decode_bench(abi, torch, stream, batch, 2048, args.decode_steps, weights, LLAMA3_8B))
+    del weights
+    torch.cuda.empty_cache()
+    return dec
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -314,6 +333,8 @@ def main() -> None:
     with torch.cuda.stream(stream):
         if args.copy_probe:
             copy_probe(torch, stream)
+        elif args.decode_only:
+            print(json.dumps({"decode": decode_runs(args, abi, torch, stream)}), flush=True)
         else:
             run(args, abi, torch, stream)
 
@@ -365,18 +386,7 @@ def run(args, abi, torch, stream) -> None:
         result["attention"] = attention_bench(abi, torch, stream)
 
     if not args.no_decode:
-        from aljabr_amd.llama import LLAMA3_8B, random_weights
-        log("building random-init Llama-3-8B-shaped NF4 model")
-        t0 = time.perf_counter()
-        weights = random_weights(LLAMA3_8B, seed=1)
-        log(f"model built in {time.perf_counter() - t0:.1f} s")
-        dec = []
-        for batch in (1, 32):
-            log(f"decode batch {batch}, context 2048")
-            dec.append(decode_bench(abi, torch, stream, batch, 2048, args.decode_steps, weights, LLAMA3_8B))
-        result["decode"] = dec
-        del weights
-        torch.cuda.empty_cache()
+        result["decode"] = decode_runs(args, abi, torch, stream)
 
     if not args.no_cpu:
         log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
