@@ -28,6 +28,8 @@ TYPE_F32 = 0
 TYPE_F16 = 1
 TYPE_Q4_0 = 2
 TYPE_Q8_0 = 8
+TYPE_Q4_K = 12
+TYPE_Q6_K = 14
 TYPE_NF4 = 100
 
 _P = ctypes.c_void_p
@@ -105,6 +107,10 @@ SIGNATURES = {
     "aljabr_rocm_matvec_tb_q4_0": (_I, [_P, _P, _P, _I, _I]),
     "aljabr_rocm_matvec_tb_q8_0": (_I, [_P, _P, _P, _I, _I]),
     "aljabr_rocm_matvec_tb_half": (_I, [_P, _P, _P, _I, _I]),
+    "aljabr_rocm_matvec_tb_q4_k": (_I, [_P, _P, _P, _I, _I]),
+    "aljabr_rocm_matvec_tb_q6_k": (_I, [_P, _P, _P, _I, _I]),
+    "aljabr_rocm_matvec_tb_q4_k_softcap": (_I, [_P, _P, _P, _I, _I, ctypes.c_float]),
+    "aljabr_rocm_matvec_tb_q6_k_softcap": (_I, [_P, _P, _P, _I, _I, ctypes.c_float]),
     "aljabr_rocm_matvec_tb_batch": (_I, [_P, _P, _P, _I, _I, _I, _I]),
     "aljabr_rocm_matvec_tb_batch_nf4": (_I, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "aljabr_rocm_dequantize": (_I, [_P, _P, _P, _LL, _I, _I]),

@@ -5,6 +5,8 @@
 //   NF4  STC/DequantizationKernel.java:84-102     T[nibble] * absmax[(2j)/bs]
 //   Q4_0 GRT/GgufBlockDequantizer.java:33-37,403-416  (q-8)*d + 0.0f  (+0.0f turns -0 into +0)
 //   Q8_0 GRT/GgufBlockDequantizer.java:231-265    (int8)q * d
+//   Q4_K GRT/GgufKBlockDequantizer.java:32-90      (d*sc)*q - dmin*min (0 for a zero min code or dmin == 0)
+//   Q6_K GRT/GgufKBlockDequantizer.java:320-425    (d*scale)*(q6-32)
 //   F16  GRT/GgufQuantTables.java:143-165         (canonical NaN)
 // Encoders reproduce GWR/GGUFWriter.java:163-209,360-387 bit for bit (fp32
 // scale for quantizing, writer-rounded fp16 scale stored, Java Math.round).
@@ -54,6 +56,57 @@ __global__ __launch_bounds__(kThreads) void q8_0_dequant_kernel(float *__restric
     const uint8_t *b = src + blk * 34;
     const float d = f16_bits_to_f32_exact(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
     for (int j = 0; j < 32; ++j) dst[blk * 32 + j] = __fmul_rn(static_cast<float>(static_cast<int8_t>(b[2 + j])), d);
+}
+
+// One thread per 32-element sub-block of a Q4_K super-block.
+__global__ __launch_bounds__(kThreads) void q4_k_dequant_kernel(float *__restrict__ dst, const uint8_t *__restrict__ src,
+                                                                long long nsub) {
+    const long long t = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+    if (t >= nsub) return;
+    const uint8_t *b = src + (t >> 3) * 144;
+    const int sub = static_cast<int>(t & 7);
+    const float d = f16_bits_to_f32_exact(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
+    const float dmin = f16_bits_to_f32_exact(static_cast<uint32_t>(b[2]) | (static_cast<uint32_t>(b[3]) << 8));
+    const uint8_t *sc = b + 4;
+    int scale, mn;
+    if (sub < 4) {
+        scale = sc[sub] & 63;
+        mn = sc[sub + 4] & 63;
+    } else {
+        scale = (sc[sub + 4] & 0x0F) | ((sc[sub - 4] >> 6) << 4);
+        mn = (sc[sub + 4] >> 4) | ((sc[sub] >> 6) << 4);
+    }
+    const float d1 = __fmul_rn(d, static_cast<float>(scale));
+    const float m1 = (dmin == 0.0f || mn == 0) ? 0.0f : __fmul_rn(dmin, static_cast<float>(mn));
+    // Sub-block 2c + h: low (h = 0) or high (h = 1) nibbles of qs[32c .. 32c+32).
+    const uint8_t *q = b + 16 + 32 * (sub >> 1);
+    const int shift = 4 * (sub & 1);
+    float *o = dst + (t << 5);
+    for (int l = 0; l < 32; ++l)
+        o[l] = __fsub_rn(__fmul_rn(d1, static_cast<float>((q[l] >> shift) & 0x0F)), m1);
+}
+
+// One thread per 16-element scale group of a Q6_K super-block.
+__global__ __launch_bounds__(kThreads) void q6_k_dequant_kernel(float *__restrict__ dst, const uint8_t *__restrict__ src,
+                                                                long long ngroups) {
+    const long long t = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+    if (t >= ngroups) return;
+    const uint8_t *b = src + (t >> 4) * 210;
+    const int g = static_cast<int>(t & 15);             // elements 16g .. 16g+15
+    const int h = g >> 3, quad = (g >> 1) & 3, l0 = 16 * (g & 1);
+    const float d = f16_bits_to_f32_exact(static_cast<uint32_t>(b[208]) | (static_cast<uint32_t>(b[209]) << 8));
+    const float scale = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(b[192 + g])));
+    // Quadrant quad of half h: ql[64h + 32*(quad & 1) + l], nibble quad >> 1,
+    // qh[32h + l] bits 2*quad.
+    const uint8_t *ql = b + 64 * h + 32 * (quad & 1);
+    const uint8_t *qh = b + 128 + 32 * h;
+    const int nib = 4 * (quad >> 1), hs = 2 * quad;
+    float *o = dst + (t << 4);
+    for (int i = 0; i < 16; ++i) {
+        const int l = l0 + i;
+        const int q = (((ql[l] >> nib) & 0x0F) | (((qh[l] >> hs) & 3) << 4)) - 32;
+        o[i] = __fmul_rn(scale, static_cast<float>(q));
+    }
 }
 
 __global__ __launch_bounds__(kThreads) void f16_dequant_kernel(float *__restrict__ dst, const uint16_t *__restrict__ src,
@@ -193,6 +246,16 @@ int aljabr_rocm_dequantize(void *dst_f32, const void *src, const void *absmax, l
         ALJ_REQUIRE(numel % 32 == 0, "Q8_0 numel must be a multiple of 32");
         hipLaunchKernelGGL(q8_0_dequant_kernel, dim3(blocks_for(numel / 32)), dim3(kThreads), 0, s, dst, in,
                            numel / 32);
+        break;
+    case ALJABR_ROCM_TYPE_Q4_K:
+        ALJ_REQUIRE(numel % 256 == 0, "Q4_K numel must be a multiple of 256");
+        hipLaunchKernelGGL(q4_k_dequant_kernel, dim3(blocks_for(numel / 32)), dim3(kThreads), 0, s, dst, in,
+                           numel / 32);
+        break;
+    case ALJABR_ROCM_TYPE_Q6_K:
+        ALJ_REQUIRE(numel % 256 == 0, "Q6_K numel must be a multiple of 256");
+        hipLaunchKernelGGL(q6_k_dequant_kernel, dim3(blocks_for(numel / 16)), dim3(kThreads), 0, s, dst, in,
+                           numel / 16);
         break;
     case ALJABR_ROCM_TYPE_F16:
         hipLaunchKernelGGL(f16_dequant_kernel, dim3(blocks_for(numel)), dim3(kThreads), 0, s, dst,

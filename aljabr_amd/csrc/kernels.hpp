@@ -41,6 +41,10 @@ size_t attention_scratch_bytes(int B, int Hq, int Sq, int D, int keys);
 // C[M][N] = A[M][K] . W[N][K]^T for any M (slices or MFMA chosen inside).
 int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M);
 int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M);
+// GGUF Q4_K / Q6_K rows (K % 256 == 0, A and W 16-byte aligned), any M.
+int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M);
+// y = cap * tanh(y / cap) elementwise.
+int enqueue_softcap(float *y, long long n, float cap);
 // K-split tile kernels for M <= 2 (ALJABR_ROCM_ERR_UNSUPPORTED when the shape
 // or alignment does not fit them; nothing is enqueued then).
 int enqueue_nf4_tile(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
@@ -49,9 +53,10 @@ int enqueue_gguf_tile(float *C, const float *A, const uint8_t *B, int K, int N, 
 // Batch-1 NF4 kernel: T rows per workgroup, one wave per 2048-element K
 // chunk (K <= 16384, K % 2048 == 0, block size >= 32).
 int enqueue_nf4_rows(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift);
-// Batch-1 NF4/Q4_0/Q8_0 kernel with a 256-entry pair table for 4-bit codes
-// (K % 2048 == 0, K <= 16384; NF4 block size >= 32, 16-byte aligned codes;
-// GGUF rows 4-byte aligned). `type` is an ALJABR_ROCM_TYPE_* id.
+// Batch-1 NF4/Q4_0/Q8_0/Q4_K/Q6_K kernel, a 256-entry pair table for NF4 and
+// Q4_0 codes (K % 2048 == 0, K <= 16384; NF4 block size >= 32, 16-byte
+// aligned codes; Q4_0/Q8_0 rows 4-byte aligned, K-quant rows 16-byte
+// aligned). `type` is an ALJABR_ROCM_TYPE_* id.
 int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax, int K, int N, int type,
                  int bs_shift);
 // One weight matrix of a fused batch-1 NF4 launch: y[0..n) = W[n][K] . x'.

@@ -480,6 +480,7 @@ int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float 
 }
 
 int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M) {
+    if (type == ALJABR_ROCM_TYPE_Q4_K || type == ALJABR_ROCM_TYPE_Q6_K) return enqueue_matmul_kquant(C, A, B, K, N, type, M);
     // fp16 rows with M >= 2 on the matrix cores, 32 tokens per pass.
     if (type == ALJABR_ROCM_TYPE_F16 && M >= 2 && mfma_enabled()) {
         const uint16_t *W = reinterpret_cast<const uint16_t *>(B);
@@ -546,9 +547,11 @@ int aljabr_rocm_matvec_tb_batch(void *C, const void *A, const void *B, int K, in
     ALJ_CHECK_READY();
     int rc = check_common(C, A, B, K, N, batchSize);
     if (rc) return rc;
-    if (type != ALJABR_ROCM_TYPE_Q4_0 && type != ALJABR_ROCM_TYPE_Q8_0 && type != ALJABR_ROCM_TYPE_F16)
+    const bool kq = type == ALJABR_ROCM_TYPE_Q4_K || type == ALJABR_ROCM_TYPE_Q6_K;
+    if (type != ALJABR_ROCM_TYPE_Q4_0 && type != ALJABR_ROCM_TYPE_Q8_0 && type != ALJABR_ROCM_TYPE_F16 && !kq)
         return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "matvec_tb_batch: unsupported type %d", type);
-    if (type != ALJABR_ROCM_TYPE_F16) ALJ_REQUIRE(K % 32 == 0, "GGUF rows are whole 32-element blocks (K=%d)", K);
+    if (kq) ALJ_REQUIRE(K % 256 == 0, "K-quant rows are whole 256-element super-blocks (K=%d)", K);
+    else if (type != ALJABR_ROCM_TYPE_F16) ALJ_REQUIRE(K % 32 == 0, "GGUF rows are whole 32-element blocks (K=%d)", K);
     rc = enqueue_matmul_gguf(static_cast<float *>(C), static_cast<const float *>(A), static_cast<const uint8_t *>(B), K, N, type,
                   batchSize);
     if (rc) return rc;
@@ -565,6 +568,45 @@ int aljabr_rocm_matvec_tb_q8_0(void *C, const void *A, const void *B, int K, int
 
 int aljabr_rocm_matvec_tb_half(void *C, const void *A, const void *B, int K, int N) {
     return aljabr_rocm_matvec_tb_batch(C, A, B, K, N, ALJABR_ROCM_TYPE_F16, 1);
+}
+
+int aljabr_rocm_matvec_tb_q4_k(void *C, const void *A, const void *B, int K, int N) {
+    return aljabr_rocm_matvec_tb_batch(C, A, B, K, N, ALJABR_ROCM_TYPE_Q4_K, 1);
+}
+
+int aljabr_rocm_matvec_tb_q6_k(void *C, const void *A, const void *B, int K, int N) {
+    return aljabr_rocm_matvec_tb_batch(C, A, B, K, N, ALJABR_ROCM_TYPE_Q6_K, 1);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The soft-capped variants run the matvec and then the cap in the same stream
+// (as Metal's fallback path does when it has no fused pipeline).
+int matvec_softcap(void *C, const void *A, const void *B, int K, int N, int type, float cap) {
+    ALJ_CHECK_READY();
+    int rc = check_common(C, A, B, K, N, 1);
+    if (rc) return rc;
+    ALJ_REQUIRE(K % 256 == 0, "K-quant rows are whole 256-element super-blocks (K=%d)", K);
+    ALJ_REQUIRE(!(cap != cap), "cap must not be NaN");
+    rc = enqueue_matmul_kquant(static_cast<float *>(C), static_cast<const float *>(A), static_cast<const uint8_t *>(B),
+                               K, N, type, 1);
+    if (rc) return rc;
+    if (cap > 0.0f) enqueue_softcap(static_cast<float *>(C), N, cap);
+    return finish_launch("matvec_tb_softcap");
+}
+
+}  // namespace
+
+extern "C" {
+
+int aljabr_rocm_matvec_tb_q4_k_softcap(void *C, const void *A, const void *B, int K, int N, float cap) {
+    return matvec_softcap(C, A, B, K, N, ALJABR_ROCM_TYPE_Q4_K, cap);
+}
+
+int aljabr_rocm_matvec_tb_q6_k_softcap(void *C, const void *A, const void *B, int K, int N, float cap) {
+    return matvec_softcap(C, A, B, K, N, ALJABR_ROCM_TYPE_Q6_K, cap);
 }
 
 }  // extern "C"

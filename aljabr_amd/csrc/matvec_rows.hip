@@ -9,7 +9,9 @@
 //   Q4_0 18-byte blocks {f16 d; u8 qs[16]}, qs[j] low nibble -> element j,
 //        high nibble -> element j+16, value (q-8)*d
 //        (GRT/GgufBlockDequantizer.java:33-37,403-416);
-//   Q8_0 34-byte blocks {f16 d; i8 qs[32]} (GRT/GgufBlockDequantizer.java:231-265).
+//   Q8_0 34-byte blocks {f16 d; i8 qs[32]} (GRT/GgufBlockDequantizer.java:231-265);
+//   Q4_K / Q6_K 144- / 210-byte super-blocks of 256 weights, 8 lanes per
+//        super-block (layouts and lane split in kquant.hpp).
 //
 // Decoding is the bottleneck once the weights stream at HBM speed, so every
 // choice below cuts VALU instructions per weight:
@@ -21,6 +23,10 @@
 //     half a v_perm, half an LDS read, one FMA.
 //   * Q8_0 converts with v_cvt_f32_ubyte on q^0x80 (= q+128) and subtracts
 //     128*sum(x) per block: one convert and one FMA per weight.
+//   * Q4_K / Q6_K mask the nibbles (and merge Q6_K's two high bits) four
+//     bytes at a time and convert with v_cvt_f32_ubyte; the per-sub-block
+//     scale is applied to the lane's two partial dots, the Q4_K min and the
+//     Q6_K -32 offset through the lane's activation sums.
 //   * Activations are staged once per workgroup with coalesced loads through
 //     a swizzled LDS window (conflict-free), then live in registers: lane l
 //     owns the 32 weights [32l, 32l+32) of its wave's 2048-element K chunk.
@@ -37,12 +43,15 @@
 #include "device.hpp"
 #include "internal.hpp"
 #include "kernels.hpp"
+#include "kquant.hpp"
 
 namespace aljabr {
 namespace {
 
 constexpr int kChunk = 2048;
-constexpr int kFmtNF4 = 0, kFmtQ4 = 1, kFmtQ8 = 2;
+constexpr int kFmtNF4 = 0, kFmtQ4 = 1, kFmtQ8 = 2, kFmtQ4K = 3, kFmtQ6K = 4;
+constexpr bool kquant_fmt(int f) { return f == kFmtQ4K || f == kFmtQ6K; }
+constexpr bool pair_table_fmt(int f) { return f == kFmtNF4 || f == kFmtQ4; }
 constexpr int kPairBytes = 256 * 256;          // 256 entries x 32 replicas x float2
 
 typedef unsigned int u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -60,6 +69,23 @@ template <int FMT> struct RowWords;
 template <> struct RowWords<kFmtNF4> { u32x4 q; float s; };
 template <> struct RowWords<kFmtQ4> { u32x4a4 a; uint32_t b; };
 template <> struct RowWords<kFmtQ8> { u32x4a4 a, b; uint32_t c; };
+template <> struct RowWords<kFmtQ4K> : Q4KWords {};
+template <> struct RowWords<kFmtQ6K> : Q6KWords {};
+
+// Float4 f of the wave's 2048-element activation chunk that fills xv[4i..4i+4)
+// of `lane`: 32 consecutive elements, or for the K-quants the lane's 16 low
+// then 16 high elements of its super-block.
+template <int FMT>
+__device__ __forceinline__ int x_f4(int lane, int i) {
+    if constexpr (FMT == kFmtQ4K || FMT == kFmtQ6K) {
+        const int j = lane & 7;
+        const int e = 256 * (lane >> 3) + (FMT == kFmtQ4K ? q4k_lo_elem(j) : q6k_lo_elem(j)) +
+                      (i >= 4 ? (FMT == kFmtQ4K ? kQ4KHigh : kQ6KHigh) : 0);
+        return (e >> 2) + (i & 3);
+    } else {
+        return lane * 8 + i;
+    }
+}
 
 // A launch covers up to three weight matrices of the same K stacked as one
 // row space (the decode step's Q/K/V or gate/up share one launch and one
@@ -145,6 +171,13 @@ __device__ __forceinline__ void load_row(RowWords<FMT> &d, const RowsArgs &a, in
         const size_t row_bytes = static_cast<size_t>(a.K) >> 1;
         d.q = load_stream16(w + local * row_bytes + (k0 >> 1));
         d.s = absmax[(local * a.K + k0) >> a.bs_shift];
+    } else if constexpr (kquant_fmt(FMT)) {
+        // lane_blk = chunk*64 + lane: super-block lane_blk/8 of the row, lane j = lane_blk%8.
+        constexpr int BB = FMT == kFmtQ4K ? kQ4KBytes : kQ6KBytes;
+        const size_t row_bytes = static_cast<size_t>(a.K >> 8) * BB;
+        const uint8_t *blk = w + local * row_bytes + static_cast<size_t>(lane_blk >> 3) * BB;
+        if constexpr (FMT == kFmtQ4K) load_q4k(d, blk, lane_blk & 7);
+        else load_q6k(d, blk, lane_blk & 7);
     } else {
         constexpr int BB = FMT == kFmtQ4 ? 18 : 34;
         const size_t row_bytes = static_cast<size_t>(a.K >> 5) * BB;
@@ -174,9 +207,21 @@ __device__ __forceinline__ float2 pair_at(const char *tbl, uint32_t addr) {
 
 // sum over the lane's 32 weights of w*x, before the row/block scale.
 template <int FMT>
-__device__ __forceinline__ float row_dot(const RowWords<FMT> &d, const float (&xv)[32], float xsum, bool odd,
-                                         uint32_t cl, const char *tbl, float &scale) {
-    if constexpr (FMT == kFmtNF4) {
+__device__ __forceinline__ float row_dot(const RowWords<FMT> &d, const float (&xv)[32], float xsum, float xsum2,
+                                         bool odd, uint32_t cl, const char *tbl, float &scale) {
+    if constexpr (kquant_fmt(FMT)) {
+        // xsum / xsum2: sums of the lane's low / high activations.
+        const int j = __lane_id() & 7;
+        float plo, phi;
+        scale = 1.0f;
+        if constexpr (FMT == kFmtQ4K) {
+            q4k_dots(d.q, xv, xv + 16, plo, phi);
+            return k_combine<false>(q4k_scales(d.hdr, j), plo, phi, xsum, xsum2);
+        } else {
+            q6k_dots(d, j, xv, xv + 16, plo, phi);
+            return k_combine<true>(q6k_scales(d, j), plo, phi, xsum, xsum2);
+        }
+    } else if constexpr (FMT == kFmtNF4) {
         const uint32_t wv[4] = {d.q.x, d.q.y, d.q.z, d.q.w};
         float p0 = 0.0f, p1 = 0.0f;
 #pragma unroll
@@ -314,7 +359,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
         if constexpr (XOP == kXNorm) __syncthreads();        // 0: chunk sums of squares
         __syncthreads();                                     // 1: x staged
         __syncthreads();                                     // 2: x read
-        if constexpr (FMT != kFmtQ8) build_pair_table<FMT, W * 64>(tbl2, tid);
+        if constexpr (pair_table_fmt(FMT)) build_pair_table<FMT, W * 64>(tbl2, tid);
         __syncthreads();                                     // 3: table built
         __syncthreads();                                     // 4: partials written
         return;
@@ -391,20 +436,27 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
         const f32x4 *win = reinterpret_cast<const f32x4 *>(smem) + chunk * 512;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const f32x4 v = win[lane * 8 + (i ^ (lane & 7))];
+            const int f = x_f4<FMT>(lane, i);
+            const f32x4 v = win[(f >> 3) * 8 + ((f & 7) ^ ((f >> 3) & 7))];
             xv[4 * i + 0] = v.x;
             xv[4 * i + 1] = v.y;
             xv[4 * i + 2] = v.z;
             xv[4 * i + 3] = v.w;
         }
     }
-    float xsum = 0.0f;
+    float xsum = 0.0f, xsum2 = 0.0f;
     if constexpr (FMT == kFmtQ8) {
 #pragma unroll
         for (int i = 0; i < 32; ++i) xsum += xv[i];
+    } else if constexpr (kquant_fmt(FMT)) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            xsum += xv[i];
+            xsum2 += xv[16 + i];
+        }
     }
     __syncthreads();                                         // 2: the table overwrites the x windows
-    if constexpr (FMT != kFmtQ8) build_pair_table<FMT, W * 64>(tbl2, tid);
+    if constexpr (pair_table_fmt(FMT)) build_pair_table<FMT, W * 64>(tbl2, tid);
     __syncthreads();                                         // 3
 
     const char *tbl = reinterpret_cast<const char *>(smem);
@@ -417,7 +469,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     for (int t = 0; t < T; ++t) {
         if (t + PF < T) load_row<FMT, EPI, T>(rw[t + PF], a, min(row0 + (t + PF) * rstride, a.N - 1), k0, lane_blk);
         float scale;
-        const float dot = row_dot<FMT>(rw[t], xv, xsum, odd, cl, tbl, scale);
+        const float dot = row_dot<FMT>(rw[t], xv, xsum, xsum2, odd, cl, tbl, scale);
         acc[t] = dot * scale;
         // Keep the written pipeline: without these the compiler defers every
         // row's arithmetic to the end and holds all lookups in registers.
@@ -485,7 +537,7 @@ template <int FMT, int T, int PF, int W, int XOP, int EPI>
 void launch_cfg(const RowsArgs &args, hipStream_t s) {
     static const int pad = env_int("ALJABR_ROCM_ROWS_LDS", 0);   // dynamic LDS floor (bytes), sweeps only
     const void *fn = reinterpret_cast<const void *>(rows_kernel<FMT, T, PF, W, XOP, EPI>);
-    size_t lds = FMT == kFmtQ8 ? static_cast<size_t>(args.S) * 512 * sizeof(float4) : kPairBytes;
+    size_t lds = pair_table_fmt(FMT) ? kPairBytes : static_cast<size_t>(args.S) * 512 * sizeof(float4);
     if (pad > 0 && static_cast<size_t>(pad) > lds && pad <= 150 * 1024) lds = pad;
     static bool lds_set = false;                 // the attribute is per kernel, per process
     if (!lds_set) {
@@ -553,6 +605,9 @@ int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax
     } else if (type == ALJABR_ROCM_TYPE_Q4_0 || type == ALJABR_ROCM_TYPE_Q8_0) {
         if (!aligned(W, 4)) return ALJABR_ROCM_ERR_UNSUPPORTED;
         fmt = type == ALJABR_ROCM_TYPE_Q4_0 ? kFmtQ4 : kFmtQ8;
+    } else if (type == ALJABR_ROCM_TYPE_Q4_K || type == ALJABR_ROCM_TYPE_Q6_K) {
+        if (!aligned(W, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        fmt = type == ALJABR_ROCM_TYPE_Q4_K ? kFmtQ4K : kFmtQ6K;
     } else {
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     }
@@ -569,6 +624,8 @@ int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax
     switch (fmt) {
     case kFmtNF4: launch_rows<kFmtNF4, kXPlain, kEStore>(args, T, s); break;
     case kFmtQ4: launch_rows<kFmtQ4, kXPlain, kEStore>(args, T, s); break;
+    case kFmtQ4K: launch_rows<kFmtQ4K, kXPlain, kEStore>(args, T, s); break;
+    case kFmtQ6K: launch_rows<kFmtQ6K, kXPlain, kEStore>(args, T, s); break;
     default: launch_rows<kFmtQ8, kXPlain, kEStore>(args, T, s); break;
     }
     return ALJABR_ROCM_OK;

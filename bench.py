@@ -170,6 +170,62 @@ def small_m_bench(abi, torch, stream, ms=(1, 4, 16, 64), launches=60):
     return out
 
 
+def kquant_blocks(torch, qtype, n, k, g):
+    """Synthetic GGUF Q4_K (type 12) / Q6_K (14) rows on the device: every code
+    byte uniform, fp16 block scales finite and ~1/256 (dmin >= 0)."""
+    bb = 144 if qtype == 12 else 210
+    nb = n * k // 256
+    b = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, device="cuda:0", generator=g)
+    d = (torch.rand(nb, generator=g, device="cuda:0") * 0.75 + 0.25).mul_(1.0 / 256).half()
+    if qtype == 12:
+        dmin = torch.rand(nb, generator=g, device="cuda:0").mul_(1.0 / 256).half()
+        b[:, 0:2] = d.view(torch.uint8).view(nb, 2)
+        b[:, 2:4] = dmin.view(torch.uint8).view(nb, 2)
+    else:
+        b[:, 208:210] = d.view(torch.uint8).view(nb, 2)
+    return b.view(-1)
+
+
+def kquant_bench(abi, torch, stream, ms=(1, 4, 8), launches=60):
+    """GGUF K-quant matvec / small-M GEMM (the quantization of production GGUF
+    files) at the Llama-3-8B MLP shapes; weights rotate over >= 512 MB.
+    Returns per type, shape and M the launch time and algorithmic GB/s
+    (weight blocks once + activations in and out)."""
+    lib = abi.load()
+    out = {}
+    for qtype, name, bb in ((12, "q4_k", 144), (14, "q6_k", 210)):
+        for n, k in ((FFN, K_MODEL), (K_MODEL, FFN)):
+            per = n * k // 256 * bb
+            copies = max(2, -(-520_000_000 // per))
+            g = torch.Generator(device="cuda:0").manual_seed(5)
+            bufs = [kquant_blocks(torch, qtype, n, k, g) for _ in range(copies)]
+            for m in ms:
+                x = torch.randn(m * k, device="cuda:0")
+                y = torch.empty(m * n, device="cuda:0")
+                torch.cuda.synchronize()
+
+                def launch(i):
+                    rc = lib.aljabr_rocm_matvec_tb_batch(y.data_ptr(), x.data_ptr(), bufs[i % copies].data_ptr(),
+                                                         k, n, qtype, m)
+                    if rc:
+                        abi.check(rc, "aljabr_rocm_matvec_tb_batch")
+                for i in range(20):
+                    launch(i)
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                for i in range(launches):
+                    launch(i)
+                end.record(stream)
+                end.synchronize()
+                us = start.elapsed_time(end) * 1000.0 / launches
+                alg = per + m * (k + n) * 4
+                out[f"{name}_{n}x{k}_m{m}"] = {"us": round(us, 2), "GBs": round(alg / us / 1e3, 1),
+                                               "frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 3)}
+            del bufs
+            torch.cuda.empty_cache()
+    return out
+
+
 def attention_bench(abi, torch, stream, launches=20):
     """GQA decode attention, Hq=32, Hkv=8, D=128, fp16
     K/V ~N(0,1), one query token per sequence, scale 1/sqrt(128). Small
@@ -384,6 +440,8 @@ def run(args, abi, torch, stream) -> None:
         result["small_m_gemm"] = small_m_bench(abi, torch, stream)
         log("GQA decode attention")
         result["attention"] = attention_bench(abi, torch, stream)
+        log("GGUF K-quant matvec (Q4_K, Q6_K; M = 1, 4, 8)")
+        result["gguf_kquant"] = kquant_bench(abi, torch, stream)
 
     if not args.no_decode:
         result["decode"] = decode_runs(args, abi, torch, stream)

@@ -47,6 +47,8 @@ extern "C" {
 #define ALJABR_ROCM_TYPE_F16 1
 #define ALJABR_ROCM_TYPE_Q4_0 2
 #define ALJABR_ROCM_TYPE_Q8_0 8
+#define ALJABR_ROCM_TYPE_Q4_K 12
+#define ALJABR_ROCM_TYPE_Q6_K 14
 #define ALJABR_ROCM_TYPE_NF4 100
 
 /* ======================================================================== */
@@ -128,9 +130,21 @@ int aljabr_rocm_matvec_tb_q4_0(void *C, const void *A, const void *B, int K, int
 int aljabr_rocm_matvec_tb_q8_0(void *C, const void *A, const void *B, int K, int N);
 /* fp16 rows (LM head); replaces aljabr_metal_matvec_tb_half (MTLC/aljabr_metal_matvec_api.h:32-33). */
 int aljabr_rocm_matvec_tb_half(void *C, const void *A, const void *B, int K, int N);
+/* GGUF K-quants, rows of K/256 super-blocks: Q4_K 144-byte blocks {f16 d;
+ * f16 dmin; u8 scales[12]; u8 qs[128]}, Q6_K 210-byte blocks {u8 ql[128];
+ * u8 qh[64]; i8 scales[16]; f16 d} (engine/gguf/.../runtime/GgufKBlockDequantizer.java:32-90,320-425).
+ * K must be a multiple of 256 (-2 otherwise); A and B 16-byte aligned.
+ * Replace aljabr_metal_matvec_tb_q4_k / _q6_k (MTLC/aljabr_metal_matvec_api.h:48-55). */
+int aljabr_rocm_matvec_tb_q4_k(void *C, const void *A, const void *B, int K, int N);
+int aljabr_rocm_matvec_tb_q6_k(void *C, const void *A, const void *B, int K, int N);
+/* The same with the output soft cap C[n] = cap * tanh(C[n] / cap) when cap > 0
+ * (MTLC/aljabr_metal_matvec_api.m:448-505; aljabr_softcap_kernel,
+ * MTLC/aljabr_metal_kernel_source.m:111-118). */
+int aljabr_rocm_matvec_tb_q4_k_softcap(void *C, const void *A, const void *B, int K, int N, float cap);
+int aljabr_rocm_matvec_tb_q6_k_softcap(void *C, const void *A, const void *B, int K, int N, float cap);
 
 /* A[batchSize][K] fp32 -> C[batchSize][N] fp32 with W read once per call.
- * type: ALJABR_ROCM_TYPE_{Q4_0,Q8_0,F16}. Replaces aljabr_metal_matvec_tb_batch
+ * type: ALJABR_ROCM_TYPE_{Q4_0,Q8_0,Q4_K,Q6_K,F16}. Replaces aljabr_metal_matvec_tb_batch
  * (MTLC/aljabr_metal_matvec_api.h:93-94). batchSize < 16 runs the
  * wavefront-reduction kernels, batchSize >= 16 the MFMA kernels. */
 int aljabr_rocm_matvec_tb_batch(void *C, const void *A, const void *B, int K,
@@ -146,7 +160,8 @@ int aljabr_rocm_matvec_tb_batch_nf4(void *C, const void *A, const void *B_packed
 
 /* Decode `numel` weights to fp32, bit-exact with the reference decoders:
  * NF4 STC/DequantizationKernel.java:84-102 (absmax/blockSize used), Q4_0
- * GgufBlockDequantizer.java:33-37,403-416 (+0.0f), Q8_0 :231-265, F16
+ * GgufBlockDequantizer.java:33-37,403-416 (+0.0f), Q8_0 :231-265, Q4_K and Q6_K
+ * GgufKBlockDequantizer.java:32-90,320-425 (numel % 256 == 0), F16
  * GgufQuantTables.java:143-165. STC = engine/safetensor/aljabr-safetensor-core/.../core/tensor. */
 int aljabr_rocm_dequantize(void *dst_f32, const void *src, const void *absmax,
                            long long numel, int type, int blockSize);

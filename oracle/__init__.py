@@ -28,6 +28,8 @@ _lib = None
 
 QTYPE_Q4_0 = 2
 QTYPE_Q8_0 = 8
+QTYPE_Q4_K = 12
+QTYPE_Q6_K = 14
 
 
 def build() -> str:
@@ -69,6 +71,13 @@ def _declare(L: ctypes.CDLL) -> None:
         "orc_q4_0_matvec": (None, [_P, _P, _I64, _I64, _I32, _P, ctypes.c_int]),
         "orc_q8_0_matvec": (None, [_P, _P, _I64, _I64, _I32, _P, ctypes.c_int]),
         "orc_f16_matvec": (None, [_P, _P, _I64, _I64, _I32, _P, ctypes.c_int]),
+        "orc_q4_k_dequant": (None, [_P, _I64, _P]),
+        "orc_q6_k_dequant": (None, [_P, _I64, _P]),
+        "orc_q4_k_dot_row": (_F, [_P, _I32, _P]),
+        "orc_q6_k_dot_row": (_F, [_P, _I32, _P]),
+        "orc_q4_k_matvec": (None, [_P, _P, _I64, _I64, _I32, _P, ctypes.c_int]),
+        "orc_q6_k_matvec": (None, [_P, _P, _I64, _I64, _I32, _P, ctypes.c_int]),
+        "orc_softcap": (None, [_P, _I64, _F]),
         "orc_attention_gqa": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                             ctypes.c_int, _P, ctypes.c_int]),
         "orc_paged_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F,
@@ -164,10 +173,22 @@ def nf4_matvec(codes, absmax, x: np.ndarray, n: int, k: int, group: int = 64,
 # ---- GGUF Q4_0 / Q8_0 -----------------------------------------------------
 
 def block_bytes(qtype: int) -> int:
-    return {QTYPE_Q4_0: 18, QTYPE_Q8_0: 34}[qtype]
+    return {QTYPE_Q4_0: 18, QTYPE_Q8_0: 34, QTYPE_Q4_K: 144, QTYPE_Q6_K: 210}[qtype]
+
+
+def block_elems(qtype: int) -> int:
+    return 256 if qtype in (QTYPE_Q4_K, QTYPE_Q6_K) else 32
+
+
+_NAMES = {QTYPE_Q4_0: "q4_0", QTYPE_Q8_0: "q8_0", QTYPE_Q4_K: "q4_k", QTYPE_Q6_K: "q6_k"}
+
+
+def _fn(qtype: int, what: str):
+    return getattr(lib(), f"orc_{_NAMES[qtype]}_{what}")
 
 
 def quantize(qtype: int, w: np.ndarray) -> np.ndarray:
+    """GGUFWriter's Q4_0/Q8_0 encoders (the reference writes no K-quants)."""
     w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
     out = np.empty(w.size // 32 * block_bytes(qtype), dtype=np.uint8)
     fn = lib().orc_q4_0_quantize if qtype == QTYPE_Q4_0 else lib().orc_q8_0_quantize
@@ -178,16 +199,14 @@ def quantize(qtype: int, w: np.ndarray) -> np.ndarray:
 def dequant(qtype: int, blocks: np.ndarray, numel: int) -> np.ndarray:
     blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
     out = np.empty(int(numel), dtype=np.float32)
-    fn = lib().orc_q4_0_dequant if qtype == QTYPE_Q4_0 else lib().orc_q8_0_dequant
-    fn(_ptr(blocks), out.size, _ptr(out))
+    _fn(qtype, "dequant")(_ptr(blocks), out.size, _ptr(out))
     return out
 
 
 def dot_row(qtype: int, row: np.ndarray, x: np.ndarray) -> float:
     row = np.ascontiguousarray(row, dtype=np.uint8)
     x = np.ascontiguousarray(x, dtype=np.float32)
-    fn = lib().orc_q4_0_dot_row if qtype == QTYPE_Q4_0 else lib().orc_q8_0_dot_row
-    return float(fn(_ptr(row), x.size, _ptr(x)))
+    return float(_fn(qtype, "dot_row")(_ptr(row), x.size, _ptr(x)))
 
 
 def q_matvec(qtype: int, w: np.ndarray, x: np.ndarray, n: int, k: int,
@@ -195,9 +214,34 @@ def q_matvec(qtype: int, w: np.ndarray, x: np.ndarray, n: int, k: int,
     x = np.ascontiguousarray(x, dtype=np.float32)
     m = x.size // k
     y = np.empty(m * n, dtype=np.float32)
-    fn = lib().orc_q4_0_matvec if qtype == QTYPE_Q4_0 else lib().orc_q8_0_matvec
-    fn(_ptr(np.ascontiguousarray(w)), _ptr(x), n, k, m, _ptr(y), nthreads or threads())
+    _fn(qtype, "matvec")(_ptr(np.ascontiguousarray(w)), _ptr(x), n, k, m, _ptr(y), nthreads or threads())
     return y.reshape(m, n) if m > 1 else y
+
+
+def softcap(y: np.ndarray, cap: float) -> np.ndarray:
+    y = np.array(y, dtype=np.float32, copy=True, order="C")
+    lib().orc_softcap(_ptr(y), y.size, cap)
+    return y
+
+
+def random_k_blocks(qtype: int, nblocks: int, seed: int, scale: float = 1.0 / 256) -> np.ndarray:
+    """Random Q4_K/Q6_K super-blocks: every code byte uniform, the fp16 block
+    scales finite and of size ~`scale` (positive d; Q4_K dMin >= 0, as a
+    quantizer writes them). Test and benchmark data, not a quantizer."""
+    rng = np.random.default_rng(seed)
+    bb = block_bytes(qtype)
+    blocks = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+    d = (rng.uniform(0.25, 1.0, size=nblocks) * scale).astype(np.float16).view(np.uint16)
+    if qtype == QTYPE_Q4_K:
+        dmin = (rng.uniform(0.0, 1.0, size=nblocks) * scale).astype(np.float16).view(np.uint16)
+        blocks[:, 0] = d & 0xFF
+        blocks[:, 1] = d >> 8
+        blocks[:, 2] = dmin & 0xFF
+        blocks[:, 3] = dmin >> 8
+    else:
+        blocks[:, 208] = d & 0xFF
+        blocks[:, 209] = d >> 8
+    return blocks.reshape(-1)
 
 
 def f16_matvec(w_bits: np.ndarray, x: np.ndarray, n: int, k: int,

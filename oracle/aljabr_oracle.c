@@ -349,19 +349,196 @@ float orc_q8_0_dot_row(const uint8_t *row, int32_t columns, const float *x) {
     return sum;
 }
 
+/* ---- GGUF K-quants: Q4_K (144-byte super-blocks of 256) and Q6_K (210) ---- */
+
+/* GRT/GgufKQuantLayout.java:38-66: 6-bit scale and min codes of sub-block
+ * idx (0..7) from the 12 packed bytes. */
+static void q4_k_scale_min(const uint8_t *s, int idx, int *sc, int *mn) {
+    if (idx < 4) {
+        *sc = s[idx] & 63;
+        *mn = s[idx + 4] & 63;
+    } else {
+        *sc = (s[idx + 4] & 0x0F) | ((s[idx - 4] >> 6) << 4);
+        *mn = (s[idx + 4] >> 4) | ((s[idx] >> 6) << 4);
+    }
+}
+
+/* GRT/GgufKBlockDequantizer.java:32-90 with GRT/GgufKQuantLayout.java:68-70
+ * (a zero min code contributes 0 whatever dMin holds, NaN included). */
+void orc_q4_k_dequant(const uint8_t *blocks, int64_t numel, float *dst) {
+    for (int64_t blk = 0; blk < numel / 256; blk++) {
+        const uint8_t *b = blocks + blk * 144;
+        const float d = orc_f16_to_f32(get_le16(b));
+        const float dmin = orc_f16_to_f32(get_le16(b + 2));
+        const uint8_t *q = b + 16;
+        float *o = dst + blk * 256;
+        for (int j = 0; j < 4; j++) {
+            int sc1, mn1, sc2, mn2;
+            q4_k_scale_min(b + 4, 2 * j, &sc1, &mn1);
+            q4_k_scale_min(b + 4, 2 * j + 1, &sc2, &mn2);
+            const float d1 = d * (float)sc1, d2 = d * (float)sc2;
+            float m1 = 0.0f, m2 = 0.0f;
+            if (dmin != 0.0f) {
+                m1 = mn1 == 0 ? 0.0f : dmin * (float)mn1;
+                m2 = mn2 == 0 ? 0.0f : dmin * (float)mn2;
+            }
+            for (int l = 0; l < 32; l++) {
+                o[64 * j + l] = d1 * (float)(q[32 * j + l] & 0x0F) - m1;
+                o[64 * j + 32 + l] = d2 * (float)(q[32 * j + l] >> 4) - m2;
+            }
+        }
+    }
+}
+
+/* GRT/GgufKBlockDequantizer.java:320-425: ql[128] low nibbles, qh[64] two-bit
+ * high parts, int8 scales[16], f16 d at byte 208; element e of half h
+ * (128 elements) takes scale index 8h + (e % 128) / 16. */
+void orc_q6_k_dequant(const uint8_t *blocks, int64_t numel, float *dst) {
+    for (int64_t blk = 0; blk < numel / 256; blk++) {
+        const uint8_t *b = blocks + blk * 210;
+        const float d = orc_f16_to_f32(get_le16(b + 208));
+        float *o = dst + blk * 256;
+        for (int h = 0; h < 2; h++) {
+            const uint8_t *ql = b + 64 * h, *qh = b + 128 + 32 * h;
+            const int8_t *sc = (const int8_t *)(b + 192 + 8 * h);
+            for (int l = 0; l < 32; l++) {
+                const int is = l / 16;
+                const float s1 = d * (float)sc[is], s2 = d * (float)sc[is + 2];
+                const float s3 = d * (float)sc[is + 4], s4 = d * (float)sc[is + 6];
+                const int q1 = ((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                const int q2 = ((ql[32 + l] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                const int q4 = ((ql[32 + l] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                o[128 * h + l] = s1 * (float)q1;
+                o[128 * h + 32 + l] = s2 * (float)q2;
+                o[128 * h + 64 + l] = s3 * (float)q3;
+                o[128 * h + 96 + l] = s4 * (float)q4;
+            }
+        }
+    }
+}
+
+/* GRT/GgufQ4RawDot.java:38-148 (dotRowQ4K): per 64-element chunk, integer
+ * nibble dots against x accumulated eight products at a time, then
+ * d1*dot1 + d2*dot2 and, for non-zero min codes of a block with dMin != 0,
+ * - dMin*min*sum(x). */
+float orc_q4_k_dot_row(const uint8_t *row, int32_t columns, const float *x) {
+    float sum = 0.0f;
+    for (int blk = 0; blk < columns / 256; blk++) {
+        const uint8_t *b = row + (int64_t)blk * 144;
+        const float *v = x + (int64_t)blk * 256;
+        const float d = orc_f16_to_f32(get_le16(b));
+        const float dmin = orc_f16_to_f32(get_le16(b + 2));
+        const int has_mins = dmin != 0.0f;
+        const uint8_t *q = b + 16;
+        for (int j = 0; j < 4; j++) {
+            int sc1, mn1, sc2, mn2;
+            q4_k_scale_min(b + 4, 2 * j, &sc1, &mn1);
+            q4_k_scale_min(b + 4, 2 * j + 1, &sc2, &mn2);
+            if (!has_mins) mn1 = mn2 = 0;
+            const float d1 = d * (float)sc1, d2 = d * (float)sc2;
+            float vs1 = 0.0f, vs2 = 0.0f, qd1 = 0.0f, qd2 = 0.0f;
+            const float *v1 = v + 64 * j, *v2 = v + 64 * j + 32;
+            for (int i = 0; i < 32; i += 8) {
+                float t1 = 0.0f, t2 = 0.0f, u1 = 0.0f, u2 = 0.0f;
+                for (int e = 0; e < 8; e++) {
+                    const int qb = q[32 * j + i + e];
+                    const float p1 = (float)(qb & 0x0F) * v1[i + e];
+                    const float p2 = (float)(qb >> 4) * v2[i + e];
+                    t1 = e == 0 ? p1 : t1 + p1;
+                    t2 = e == 0 ? p2 : t2 + p2;
+                    u1 = e == 0 ? v1[i + e] : u1 + v1[i + e];
+                    u2 = e == 0 ? v2[i + e] : u2 + v2[i + e];
+                }
+                qd1 += t1;
+                qd2 += t2;
+                if (mn1 != 0) vs1 += u1;
+                if (mn2 != 0) vs2 += u2;
+            }
+            sum += d1 * qd1 + d2 * qd2;
+            if (mn1 != 0) sum -= dmin * (float)mn1 * vs1;
+            if (mn2 != 0) sum -= dmin * (float)mn2 * vs2;
+        }
+    }
+    return sum;
+}
+
+/* GRT/GgufQ6RawDot.java:403-514 (dotRowQ6KHalf): 16 elements per quadrant,
+ * quadrant dots scaled by d*scale and summed. */
+static float q6_k_half(const uint8_t *ql, const uint8_t *qh, const float *v, int off, float s1, float s2,
+                       float s3, float s4) {
+    float qd1 = 0.0f, qd2 = 0.0f, qd3 = 0.0f, qd4 = 0.0f;
+    for (int i = off; i < off + 16; i += 8) {
+        float t1 = 0.0f, t2 = 0.0f, t3 = 0.0f, t4 = 0.0f;
+        for (int e = 0; e < 8; e++) {
+            const int l = i + e;
+            const float p1 = (float)(((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32) * v[l];
+            const float p2 = (float)(((ql[32 + l] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32) * v[32 + l];
+            const float p3 = (float)(((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32) * v[64 + l];
+            const float p4 = (float)(((ql[32 + l] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32) * v[96 + l];
+            t1 = e == 0 ? p1 : t1 + p1;
+            t2 = e == 0 ? p2 : t2 + p2;
+            t3 = e == 0 ? p3 : t3 + p3;
+            t4 = e == 0 ? p4 : t4 + p4;
+        }
+        qd1 += t1;
+        qd2 += t2;
+        qd3 += t3;
+        qd4 += t4;
+    }
+    return s1 * qd1 + s2 * qd2 + s3 * qd3 + s4 * qd4;
+}
+
+/* GRT/GgufQ6RawDot.java:77-133 (one super-block: four half sums). */
+static float q6_k_block(const uint8_t *b, const float *v) {
+    const float d = orc_f16_to_f32(get_le16(b + 208));
+    const int8_t *sc = (const int8_t *)(b + 192);
+    float s[4];
+    for (int part = 0; part < 4; part++) {
+        const int h = part >> 1, off = (part & 1) * 16, base = 8 * h + (part & 1);
+        s[part] = q6_k_half(b + 64 * h, b + 128 + 32 * h, v + 128 * h, off, d * (float)sc[base],
+                            d * (float)sc[base + 2], d * (float)sc[base + 4], d * (float)sc[base + 6]);
+    }
+    return s[0] + s[1] + s[2] + s[3];
+}
+
+/* GRT/GgufQ6RawDot.java:33-75 (dotRowQ6K: four block accumulators). */
+float orc_q6_k_dot_row(const uint8_t *row, int32_t columns, const float *x) {
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    const int blocks = columns / 256;
+    int b = 0;
+    for (; b <= blocks - 4; b += 4) {
+        s0 += q6_k_block(row + (int64_t)(b + 0) * 210, x + (int64_t)(b + 0) * 256);
+        s1 += q6_k_block(row + (int64_t)(b + 1) * 210, x + (int64_t)(b + 1) * 256);
+        s2 += q6_k_block(row + (int64_t)(b + 2) * 210, x + (int64_t)(b + 2) * 256);
+        s3 += q6_k_block(row + (int64_t)(b + 3) * 210, x + (int64_t)(b + 3) * 256);
+    }
+    float sum = s0 + s1 + s2 + s3;
+    for (; b < blocks; b++) sum += q6_k_block(row + (int64_t)b * 210, x + (int64_t)b * 256);
+    return sum;
+}
+
 typedef struct {
     const uint8_t *w; const float *x; int64_t n, k; int32_t m; float *y; int type;
 } q_mv_ctx;
 
 static void q_mv_rows(const void *vctx, int64_t r0, int64_t r1) {
     const q_mv_ctx *c = (const q_mv_ctx *)vctx;
-    int64_t row_bytes = (c->k / 32) * (c->type == 2 ? 18 : 34);
+    int64_t row_bytes = c->type == 12 ? (c->k / 256) * 144
+                      : c->type == 14 ? (c->k / 256) * 210
+                                      : (c->k / 32) * (c->type == 2 ? 18 : 34);
     for (int64_t n = r0; n < r1; n++) {
         const uint8_t *row = c->w + n * row_bytes;
         for (int32_t mm = 0; mm < c->m; mm++) {
             const float *x = c->x + (int64_t)mm * c->k;
-            c->y[(int64_t)mm * c->n + n] = c->type == 2 ? orc_q4_0_dot_row(row, (int32_t)c->k, x)
-                                                        : orc_q8_0_dot_row(row, (int32_t)c->k, x);
+            float v;
+            switch (c->type) {
+            case 2: v = orc_q4_0_dot_row(row, (int32_t)c->k, x); break;
+            case 12: v = orc_q4_k_dot_row(row, (int32_t)c->k, x); break;
+            case 14: v = orc_q6_k_dot_row(row, (int32_t)c->k, x); break;
+            default: v = orc_q8_0_dot_row(row, (int32_t)c->k, x); break;
+            }
+            c->y[(int64_t)mm * c->n + n] = v;
         }
     }
 }
@@ -376,6 +553,25 @@ void orc_q8_0_matvec(const uint8_t *w, const float *x, int64_t n_rows,
                      int64_t k_cols, int32_t m, float *y, int threads) {
     q_mv_ctx c = {w, x, n_rows, k_cols, m, y, 8};
     run_row_chunks(n_rows, threads, q_mv_rows, &c);
+}
+
+void orc_q4_k_matvec(const uint8_t *w, const float *x, int64_t n_rows,
+                     int64_t k_cols, int32_t m, float *y, int threads) {
+    q_mv_ctx c = {w, x, n_rows, k_cols, m, y, 12};
+    run_row_chunks(n_rows, threads, q_mv_rows, &c);
+}
+
+void orc_q6_k_matvec(const uint8_t *w, const float *x, int64_t n_rows,
+                     int64_t k_cols, int32_t m, float *y, int threads) {
+    q_mv_ctx c = {w, x, n_rows, k_cols, m, y, 14};
+    run_row_chunks(n_rows, threads, q_mv_rows, &c);
+}
+
+/* Output soft cap of aljabr_metal_matvec_tb_q4_k_softcap / _q6_k_softcap
+ * (MTLC/aljabr_metal_matvec_api.m:448-505 with aljabr_softcap_kernel,
+ * MTLC/aljabr_metal_kernel_source.m:111-118): y = cap * tanh(y / cap). */
+void orc_softcap(float *y, int64_t n, float cap) {
+    for (int64_t i = 0; i < n; i++) y[i] = cap * (float)tanh((double)(y[i] / cap));
 }
 
 /* GRT/GgufDenseDot.java:289-320: element i of the unrolled body feeds

@@ -94,6 +94,31 @@ void orc_q4_0_matvec(const uint8_t *w, const float *x, int64_t n_rows,
 void orc_q8_0_matvec(const uint8_t *w, const float *x, int64_t n_rows,
                      int64_t k_cols, int32_t m, float *y, int threads);
 
+/* ---- GGUF K-quants Q4_K / Q6_K ------------------------------------------ */
+
+/* GRT/GgufKBlockDequantizer.java:32-90 + GRT/GgufKQuantLayout.java:38-70
+ * (144-byte super-blocks: f16 d, f16 dMin, 12 bytes of 6-bit scale/min codes,
+ * 128 bytes of nibbles; d*sc*q - dMin*min, a zero min code contributing 0).
+ * numel % 256 == 0. Pinned: GgufQ4KPrepTest/GgufQ4KMixTest/GgufKZeroMinTest
+ * known answers, the GgufQ4CalcFx lane-order rows, and round trips of
+ * independently packed scale/min codes (tests/test_oracle.py). */
+void orc_q4_k_dequant(const uint8_t *blocks, int64_t numel, float *dst);
+/* GRT/GgufKBlockDequantizer.java:320-425 (210-byte super-blocks: ql[128],
+ * qh[64], int8 scales[16], f16 d; (q6 - 32) * d * scale[e / 16]). Pinned:
+ * GgufQ6KPrepTest known answers, GgufQ6LaneFx lane-order rows, per-16 scale
+ * closed form. */
+void orc_q6_k_dequant(const uint8_t *blocks, int64_t numel, float *dst);
+/* GRT/GgufQ4RawDot.java:38-148 (d1*dot1 + d2*dot2 - dMin*min*sum(x)). */
+float orc_q4_k_dot_row(const uint8_t *row, int32_t columns, const float *x);
+/* GRT/GgufQ6RawDot.java:33-133,403-514. */
+float orc_q6_k_dot_row(const uint8_t *row, int32_t columns, const float *x);
+void orc_q4_k_matvec(const uint8_t *w, const float *x, int64_t n_rows,
+                     int64_t k_cols, int32_t m, float *y, int threads);
+void orc_q6_k_matvec(const uint8_t *w, const float *x, int64_t n_rows,
+                     int64_t k_cols, int32_t m, float *y, int threads);
+/* y = cap * tanh(y / cap): MTLC/aljabr_metal_kernel_source.m:111-118. */
+void orc_softcap(float *y, int64_t n, float cap);
+
 /* fp16 rows (LM head): GRT/GgufDenseRows.java:70-90. */
 void orc_f16_matvec(const uint16_t *w, const float *x, int64_t n_rows,
                     int64_t k_cols, int32_t m, float *y, int threads);

@@ -97,6 +97,71 @@ def main() -> None:
         "tolerance": 1.0e-3,
     }
 
+    # ---- K-quants. Block builders of GRTT/GgufQ4Fx.java:11-58,
+    # GRTT/GgufQ4CalcFx.java:11-49, GRTT/GgufQ6Fx.java:11-52 and
+    # GRTT/GgufQ6LaneFx.java:11-61, written out as bytes; the expected values
+    # are the ones those tests assert (or the fixture's own expected rows).
+    def q4k_header(d_bits, dmin_bits, scales):
+        return [d_bits & 0xFF, d_bits >> 8, dmin_bits & 0xFF, dmin_bits >> 8] + list(scales)
+
+    q4k_simple_scales = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]
+    q4k_mins_scales = [1, 1, 1, 1, 2, 2, 2, 2, 0x21, 0x21, 0x21, 0x21]
+    simple = q4k_header(0x3C00, 0, q4k_simple_scales) + [0x21] * 128
+    with_mins = q4k_header(0x3C00, 0x3800, q4k_mins_scales) + [0x21] * 128
+    nan_dmin = q4k_header(0x3C00, 0x7E00, q4k_simple_scales) + [0x21] * 128
+    kats["q4_k_rows"] = {
+        "source": "GRTT/GgufQ4KPrepTest.java:22-40,67-84; GRTT/GgufQ4KMixTest.java:21-43; "
+                  "GRTT/GgufKZeroMinTest.java:20-52",
+        "simple": simple,               # d=1, dMin=0, every scale 1, no mins: dot(ones) = 1*128 + 2*128
+        "with_mins": with_mins,         # d=1, dMin=0.5, scale 1, min 2 (-1.0): dot(ones) = 0*128 + 1*128
+        "nan_dmin_zero_mins": nan_dmin, # dMin NaN with every min code 0: no min term, as simple
+        "dot_ones": {"simple": 384.0, "with_mins": 128.0, "nan_dmin_zero_mins": 384.0},
+    }
+
+    lane_q = [(i & 0x0F) | ((15 - (i & 0x0F)) << 4) for i in range(128)]
+    def q4k_lane_row(has_mins):
+        row = [0.0] * 256
+        for sb in range(0, 256, 64):
+            qb = (sb // 64) * 32
+            for i in range(32):
+                low = (qb + i) & 0x0F
+                row[sb + i] = float(low - 1 if has_mins else low)
+                row[sb + 32 + i] = float((15 - low) - 1 if has_mins else 15 - low)
+        return row
+    kats["q4_k_lane_order"] = {
+        "source": "GRTT/GgufQ4Fx.java:37-58; GRTT/GgufQ4CalcFx.java:11-49",
+        "no_mins": {"block": q4k_header(0x3C00, 0, q4k_simple_scales) + lane_q,
+                    "expected_row": q4k_lane_row(False)},
+        "mins": {"block": q4k_header(0x3C00, 0x3800, q4k_mins_scales) + lane_q,
+                 "expected_row": q4k_lane_row(True)},
+    }
+
+    def q6k_block(low_packed, high_packed, scale):
+        return [low_packed] * 128 + [high_packed] * 64 + [scale & 0xFF] * 16 + [0x00, 0x3C]
+    kats["q6_k_rows"] = {
+        "source": "GRTT/GgufQ6Fx.java:11-27; GRTT/GgufQ6KPrepTest.java:19-36",
+        "ones": q6k_block(0x11, 0xAA, 1),     # q6 = 1 | 2<<4 = 33 -> 1.0 everywhere
+        "twos": q6k_block(0x22, 0xAA, 1),     # q6 = 34 -> 2.0 everywhere: dot(ones) = 512
+        "dot_ones": {"ones": 256.0, "twos": 512.0},
+    }
+
+    q6_low = [(i & 0x0F) | ((15 - (i & 0x0F)) << 4) for i in range(128)]
+    q6_high = [(i * 53 + 0xA7) & 0xFF for i in range(64)]
+    q6_row = [0.0] * 256
+    for sb in range(0, 256, 128):
+        lb, hb = (sb // 128) * 64, (sb // 128) * 32
+        for i in range(32):
+            la, lbv, hbits = q6_low[lb + i], q6_low[lb + 32 + i], q6_high[hb + i]
+            q6_row[sb + i] = float(((la & 0x0F) | ((hbits & 3) << 4)) - 32)
+            q6_row[sb + 32 + i] = float(((lbv & 0x0F) | (((hbits >> 2) & 3) << 4)) - 32)
+            q6_row[sb + 64 + i] = float(((la >> 4) | (((hbits >> 4) & 3) << 4)) - 32)
+            q6_row[sb + 96 + i] = float(((lbv >> 4) | (((hbits >> 6) & 3) << 4)) - 32)
+    kats["q6_k_lane_order"] = {
+        "source": "GRTT/GgufQ6Fx.java:29-52; GRTT/GgufQ6LaneFx.java:11-61",
+        "block": q6_low + q6_high + [1] * 16 + [0x00, 0x3C],
+        "expected_row": q6_row,
+    }
+
     # CPUT/CpuBatchedAttentionTest.java (all through CpuBackend.attention ->
     # attentionGqa with Hq == Hkv): shapes [B,H,S,D].
     att = []
