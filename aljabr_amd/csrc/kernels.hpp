@@ -38,11 +38,16 @@ int enqueue_attention(const AttnParams &p);
 // sequences of Hq heads, Sq query rows, head size D and `keys` cached keys.
 size_t attention_scratch_bytes(int B, int Hq, int Sq, int D, int keys);
 
+// Small-M GEMMs use the matrix-core kernels unless ALJABR_ROCM_MFMA=0.
+bool mfma_enabled();
 // C[M][N] = A[M][K] . W[N][K]^T for any M (slices or MFMA chosen inside).
 int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M);
 int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M);
 // GGUF Q4_K / Q6_K rows (K % 256 == 0, A and W 16-byte aligned), any M.
 int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M);
+// Q4_K / Q6_K small-M GEMM on MFMA (2 <= M <= 32, K % 512 == 0, A and W
+// 16-byte aligned; ALJABR_ROCM_ERR_UNSUPPORTED otherwise, nothing enqueued).
+int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M);
 // y = cap * tanh(y / cap) elementwise.
 int enqueue_softcap(float *y, long long n, float cap);
 // K-split tile kernels for M <= 2 (ALJABR_ROCM_ERR_UNSUPPORTED when the shape

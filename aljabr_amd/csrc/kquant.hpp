@@ -77,22 +77,28 @@ struct KScales {
 __device__ __forceinline__ KScales q4k_scales(const u32x4 &hdr, int j) {
     const float d = f16_bits_to_f32(hdr.x & 0xffffu);
     const float dmin = f16_bits_to_f32(hdr.x >> 16);
-    const bool upper = j >= 4;                  // sub-blocks 4..7: codes split over three bytes
-    int sc[2], mn[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        const int k = (2 * (j >> 1) + s) & 3;
-        const uint32_t a0 = hdr.y >> (8 * k), a1 = hdr.z >> (8 * k), a2 = hdr.w >> (8 * k);
-        sc[s] = upper ? static_cast<int>((a2 & 0xfu) | ((a0 >> 2) & 0x30u)) : static_cast<int>(a0 & 63u);
-        mn[s] = upper ? static_cast<int>(((a2 >> 4) & 0xfu) | ((a1 >> 2) & 0x30u)) : static_cast<int>(a1 & 63u);
+    // Sub-blocks 2c and 2c+1 (c = j/2) sit in bytes k = 2(c%2) and k+1 of
+    // each scale dword; 4..7 (j >= 4) split their codes over three bytes.
+    const uint32_t o = 16 * ((j >> 1) & 1);
+    uint32_t sc0, sc1, mn0, mn1;
+    if (j < 4) {
+        sc0 = __builtin_amdgcn_ubfe(hdr.y, o, 6);
+        sc1 = __builtin_amdgcn_ubfe(hdr.y, o + 8, 6);
+        mn0 = __builtin_amdgcn_ubfe(hdr.z, o, 6);
+        mn1 = __builtin_amdgcn_ubfe(hdr.z, o + 8, 6);
+    } else {
+        sc0 = __builtin_amdgcn_ubfe(hdr.w, o, 4) | (__builtin_amdgcn_ubfe(hdr.y, o + 6, 2) << 4);
+        sc1 = __builtin_amdgcn_ubfe(hdr.w, o + 8, 4) | (__builtin_amdgcn_ubfe(hdr.y, o + 14, 2) << 4);
+        mn0 = __builtin_amdgcn_ubfe(hdr.w, o + 4, 4) | (__builtin_amdgcn_ubfe(hdr.z, o + 6, 2) << 4);
+        mn1 = __builtin_amdgcn_ubfe(hdr.w, o + 12, 4) | (__builtin_amdgcn_ubfe(hdr.z, o + 14, 2) << 4);
     }
     KScales r;
-    r.dlo = d * static_cast<float>(sc[0]);
-    r.dhi = d * static_cast<float>(sc[1]);
+    r.dlo = d * static_cast<float>(sc0);
+    r.dhi = d * static_cast<float>(sc1);
     // dmin * min only where the code is non-zero (a NaN dmin with a zero
     // code adds nothing, GRT/GgufKQuantLayout.java:68-70).
-    r.mlo = mn[0] != 0 ? dmin * static_cast<float>(mn[0]) : 0.0f;
-    r.mhi = mn[1] != 0 ? dmin * static_cast<float>(mn[1]) : 0.0f;
+    r.mlo = mn0 != 0 ? dmin * static_cast<float>(mn0) : 0.0f;
+    r.mhi = mn1 != 0 ? dmin * static_cast<float>(mn1) : 0.0f;
     return r;
 }
 

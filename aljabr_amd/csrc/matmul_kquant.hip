@@ -1,0 +1,397 @@
+// matmul_kquant.hip - GGUF Q4_K / Q6_K small-M GEMM on the matrix cores:
+// Y[M,N] = X[M,K] . W[N,K]^T for 2 <= M <= 32 per pass (a decode batch), W in
+// K-quant super-blocks (layouts in kquant.hpp). W is read from HBM once for
+// all M tokens.
+//
+// MFMA v_mfma_f32_32x32x16_f16 with fp32 accumulation. A = X split into two
+// fp16 parts, x = hi + lo (hi = fp16(x), lo = fp16(x - hi)): each B fragment
+// is multiplied by both, which carries x to ~2^-22 instead of fp16's 2^-11.
+// B = W^T (32 weight rows per wave as the output columns) holds small exact
+// integers in fp16; the super-block scale stays fp32 on the accumulators:
+//   Q4_K  B = q * sc (q <= 15, sc <= 63: <= 945, exact), one MFMA pair per
+//         32-element sub-block; the min term sum_s dmin * m_s * sum(x in s)
+//         is one more MFMA pair per super-block, A = the split per-sub-block
+//         sums of x, B = the 6-bit min codes; then C += d * C_q - dmin * C_min.
+//   Q6_K  B = (q - 32) * scale (|.| <= 4096; exact below 2048, else rounded
+//         to an even integer, relative error <= 2^-11), one MFMA pair per
+//         16-element scale group; C += d * C_q.
+// Codes become fp16 integers with v_perm against a constant 0x64 byte: the
+// half 0x64qq is 1024 + qq exactly. Q4_K low nibbles give 1024 + q, high
+// nibbles (masked in place) 1024 + 16q, and one packed fp16 FMA removes the
+// offset and applies the scale without rounding: (1024 + q) * sc - 1024 * sc,
+// (1024 + 16q) * (sc/16) - 64 * sc. Q6_K: (1024 + q) - 1056, then * scale.
+//
+// Operand layout (32x32x16): lane l supplies A[m = l%32][8*(l/32) + e] and
+// B[8*(l/32) + e][n = l%32]; accumulator r is C[8*(r/4) + 4*(l/32) + r%4][l%32].
+// One MFMA step covers 16 consecutive elements of a row, lane half h the 8
+// at 8h: for Q4_K sub-block s = 2c + t (t: low/high nibbles of qs[32c ..
+// 32c+32)) step j reads qs[32c + 16j + 8h .. +8]; for Q6_K group g (elements
+// 16g .. 16g+15) reads the ql/qh bytes of those elements.
+//
+// Work split as the NF4 kernel: a workgroup is 8 waves x 32 rows and one
+// K-slice of KS elements; weights are loaded coalesced (whole row segments
+// per lane group) and transposed through per-wave LDS rows, two work units
+// (one super-block of the wave's 32 rows) ahead; K-slices add their partial
+// sums into Y with float atomics (Y is zeroed first).
+#include "device.hpp"
+#include "internal.hpp"
+#include "kernels.hpp"
+#include "kquant.hpp"
+
+namespace aljabr {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kRowsPerWg = kWaves * 32;
+
+struct KqArgs {
+    float *y;
+    const float *x;
+    const uint8_t *w;
+    int M, N, K;
+};
+
+template <bool Q6> struct KqGeom {
+    static constexpr int BB = Q6 ? kQ6KBytes : kQ4KBytes;
+    static constexpr int SEGS = Q6 ? 14 : 9;      // 16-byte pieces of a row's block (Q6_K: 13 + the 2-byte d)
+    static constexpr int STR = Q6 ? 216 : 152;    // staging row stride: 8-byte aligned, conflict-free 8-byte reads
+    static constexpr int LOADS = (32 * SEGS + 63) / 64;
+};
+
+__device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
+    const _Float16 a = static_cast<_Float16>(lo), b = static_cast<_Float16>(hi);
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+
+__device__ __forceinline__ uint32_t pk_fma_exact(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2v, a),
+                                                                  __builtin_bit_cast(half2v, b),
+                                                                  __builtin_bit_cast(half2v, c)));
+}
+
+// Halves 0x64bb from bytes 2i and 2i+1 of `w`: v_perm against a constant
+// 0x64 byte (selector values 0-3 pick bytes of w, 4 the constant).
+template <int I>
+__device__ __forceinline__ uint32_t magic_pair(uint32_t w) {
+    constexpr uint32_t b0 = 2 * I, b1 = 2 * I + 1;
+    return __builtin_amdgcn_perm(0x64646464u, w, 0x04000400u | (b1 << 16) | b0);
+}
+
+// B fragment of 8 codes held one per byte in (w0, w1) as 0x64qq halves,
+// mapped by one packed fp16 FMA each: v * mul + add.
+__device__ __forceinline__ half8 fma_frag(uint32_t w0, uint32_t w1, uint32_t mul2, uint32_t add2) {
+    u32x4v r;
+    r.x = pk_fma_exact(magic_pair<0>(w0), mul2, add2);
+    r.y = pk_fma_exact(magic_pair<1>(w0), mul2, add2);
+    r.z = pk_fma_exact(magic_pair<0>(w1), mul2, add2);
+    r.w = pk_fma_exact(magic_pair<1>(w1), mul2, add2);
+    return __builtin_bit_cast(half8, r);
+}
+
+// Six-bit codes (one per byte of w0, w1) -> half8 of (q - 32) * scale.
+__device__ __forceinline__ half8 q6_frag(uint32_t w0, uint32_t w1, uint32_t sc2) {
+    constexpr uint32_t kMinus1056 = 0xE420E420u;     // fp16 -1056 in both halves
+    const uint32_t p[4] = {magic_pair<0>(w0), magic_pair<1>(w0), magic_pair<0>(w1), magic_pair<1>(w1)};
+    u32x4v r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v v = __builtin_bit_cast(half2v, p[i]) + __builtin_bit_cast(half2v, kMinus1056);
+        r[i] = __builtin_bit_cast(uint32_t, v * __builtin_bit_cast(half2v, sc2));
+    }
+    return __builtin_bit_cast(half8, r);
+}
+
+// fp16 bits of a small integer in both halves, times `mul` (a power of two).
+__device__ __forceinline__ uint32_t int_half2(uint32_t v, float mul) {
+    const _Float16 h = static_cast<_Float16>(static_cast<float>(v) * mul);
+    const uint32_t b = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h));
+    return b | (b << 16);
+}
+
+__device__ __forceinline__ uint32_t half_bits(float v) {
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v)));
+}
+
+template <bool Q6, int KS>
+constexpr size_t kq_lds_bytes() {
+    // x slice split in two fp16 parts (2 x [32][KS+8]) + Q4_K sub-block sums
+    // (2 x [32][KS/32+8]) + per-wave staging rows.
+    return 2 * (static_cast<size_t>(32) * (KS + 8) * 2 + (Q6 ? 0 : static_cast<size_t>(32) * (KS / 32 + 8) * 2)) +
+           static_cast<size_t>(kWaves) * 32 * KqGeom<Q6>::STR;
+}
+
+// Coalesced loads of one unit (the wave's 32 rows x one super-block): piece
+// p = 64i + lane is 16-byte segment p % SEGS of row p / SEGS (Q6_K: the last
+// piece is bytes 194..209, read for its last two bytes, d, so that no load
+// leaves the block).
+template <bool Q6>
+__device__ __forceinline__ void issue_unit(u32x4 (&q)[KqGeom<Q6>::LOADS], const KqArgs &a, int row0, int sb,
+                                           int lane) {
+    using G = KqGeom<Q6>;
+    const size_t row_bytes = static_cast<size_t>(a.K >> 8) * G::BB;
+#pragma unroll
+    for (int i = 0; i < G::LOADS; ++i) {
+        const int p = min(64 * i + lane, 32 * G::SEGS - 1);
+        const int r = p / G::SEGS, seg = p - r * G::SEGS;
+        const int row = min(row0 + r, a.N - 1);
+        const uint8_t *src = a.w + static_cast<size_t>(row) * row_bytes + static_cast<size_t>(sb) * G::BB + 16 * seg;
+        if constexpr (Q6) {
+            q[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4u *>(seg == G::SEGS - 1 ? src - 14 : src));
+        } else {
+            q[i] = load_stream16(src);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool Q6>
+__device__ __forceinline__ void stage_unit(uint8_t *st, const u32x4 (&q)[KqGeom<Q6>::LOADS], int lane) {
+    using G = KqGeom<Q6>;
+#pragma unroll
+    for (int i = 0; i < G::LOADS; ++i) {
+        const int p = 64 * i + lane;
+        if (p < 32 * G::SEGS) {
+            const int r = p / G::SEGS, seg = p - r * G::SEGS;
+            uint8_t *dst = st + r * G::STR + 16 * seg;
+            if (Q6 && seg == G::SEGS - 1) {
+                *reinterpret_cast<uint16_t *>(dst) = static_cast<uint16_t>(q[i].w >> 16);   // d at 208
+            } else {
+                *reinterpret_cast<u32x2v *>(dst) = u32x2v{q[i].x, q[i].y};
+                *reinterpret_cast<u32x2v *>(dst + 8) = u32x2v{q[i].z, q[i].w};
+            }
+        }
+    }
+}
+
+template <bool Q6, int KS, int NT>
+__global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
+    using G = KqGeom<Q6>;
+    constexpr int SBS = KS / 256;                // super-blocks per slice
+    constexpr int RS = KS + 8;                   // x row stride (halves)
+    constexpr int XSS = KS / 32 + 8;             // sub-block-sum row stride (halves)
+    extern __shared__ uint8_t smem[];
+    // x as hi and lo fp16 rows; Q4_K: split sub-block sums.
+    _Float16 *xh = reinterpret_cast<_Float16 *>(smem);
+    _Float16 *xl = xh + 32 * RS;
+    _Float16 *sh = xl + 32 * RS;
+    _Float16 *sl = sh + (Q6 ? 0 : 32 * XSS);
+    uint8_t *stage_base = reinterpret_cast<uint8_t *>(sl + (Q6 ? 0 : 32 * XSS));
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int h = lane >> 5;
+    const int nl = lane & 31;
+    uint8_t *st = stage_base + wave * (32 * G::STR);
+    const int ks0 = blockIdx.y * KS;
+
+    // Activation slice -> split fp16 rows (rows >= M zero); Q4_K also the
+    // split sums of each 32-element sub-block.
+    constexpr int XF4 = 32 * (KS / 4) / kThreads;
+    static_assert(32 * (KS / 4) % kThreads == 0 && (KS / 4) % 8 == 0, "x slice split");
+#pragma unroll
+    for (int j = 0; j < XF4; ++j) {
+        const int i = tid + kThreads * j;
+        const int m = i / (KS / 4), c = i % (KS / 4);
+        f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (m < a.M) v = *reinterpret_cast<const f32x4 *>(a.x + static_cast<size_t>(m) * a.K + ks0 + 4 * c);
+        const uint32_t p0 = pack_half2(v.x, v.y), p1 = pack_half2(v.z, v.w);
+        const half2v h0 = __builtin_bit_cast(half2v, p0), h1 = __builtin_bit_cast(half2v, p1);
+        const uint32_t q0 = pack_half2(v.x - static_cast<float>(h0.x), v.y - static_cast<float>(h0.y));
+        const uint32_t q1 = pack_half2(v.z - static_cast<float>(h1.x), v.w - static_cast<float>(h1.y));
+        *reinterpret_cast<uint2 *>(xh + m * RS + 4 * c) = make_uint2(p0, p1);
+        *reinterpret_cast<uint2 *>(xl + m * RS + 4 * c) = make_uint2(q0, q1);
+        if constexpr (!Q6) {
+            float t = (v.x + v.y) + (v.z + v.w);
+            // 8 consecutive float4s (lanes c%8 = 0..7 of one row) form a sub-block.
+            t += __shfl_xor(t, 1);
+            t += __shfl_xor(t, 2);
+            t += __shfl_xor(t, 4);
+            if ((c & 7) == 0) {
+                const _Float16 th = static_cast<_Float16>(t);
+                sh[m * XSS + (c >> 3)] = th;
+                sl[m * XSS + (c >> 3)] = static_cast<_Float16>(t - static_cast<float>(th));
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    constexpr int U = NT * SBS;
+    constexpr int W = 2;
+    int row0[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) row0[t] = blockIdx.x * (kRowsPerWg * NT) + t * kRowsPerWg + wave * 32;
+    u32x4 qc[U][G::LOADS];
+#pragma unroll
+    for (int u = 0; u < W && u < U; ++u) issue_unit<Q6>(qc[u], a, row0[u / SBS], ks0 / 256 + u % SBS, lane);
+    __syncthreads();
+
+    f32x16 acc = {};
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        if (u + W < U) issue_unit<Q6>(qc[u + W], a, row0[(u + W) / SBS], ks0 / 256 + (u + W) % SBS, lane);
+        const int t = u / SBS, sbl = u % SBS;
+        if (sbl == 0) acc = f32x16{};
+        stage_unit<Q6>(st, qc[u], lane);
+        const uint8_t *row = st + nl * G::STR;   // this lane's weight row
+        const _Float16 *xrh = xh + nl * RS + 256 * sbl + 8 * h;
+        const _Float16 *xrl = xl + nl * RS + 256 * sbl + 8 * h;
+        f32x16 cq = {};
+        float d;
+        if constexpr (!Q6) {
+            const u32x2v h01 = *reinterpret_cast<const u32x2v *>(row);
+            const u32x2v h23 = *reinterpret_cast<const u32x2v *>(row + 8);
+            const uint32_t sw0 = h01.y, sw1 = h23.x, sw2 = h23.y;   // the 12 scale/min bytes
+            d = f16_bits_to_f32(h01.x & 0xffffu);
+            float dmin = f16_bits_to_f32(h01.x >> 16);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                // Sub-blocks 2c (low nibbles) and 2c+1 (high nibbles) of qs[32c .. 32c+32).
+                uint32_t sc0, sc1;
+                if (c < 2) {
+                    sc0 = __builtin_amdgcn_ubfe(sw0, 16 * c, 6);
+                    sc1 = __builtin_amdgcn_ubfe(sw0, 16 * c + 8, 6);
+                } else {
+                    sc0 = __builtin_amdgcn_ubfe(sw2, 16 * (c - 2), 4) | (__builtin_amdgcn_ubfe(sw0, 16 * (c - 2) + 6, 2) << 4);
+                    sc1 = __builtin_amdgcn_ubfe(sw2, 16 * (c - 2) + 8, 4) |
+                          (__builtin_amdgcn_ubfe(sw0, 16 * (c - 2) + 14, 2) << 4);
+                }
+                const uint32_t mul_lo = int_half2(sc0, 1.0f), add_lo = int_half2(sc0, -1024.0f);
+                const uint32_t mul_hi = int_half2(sc1, 0.0625f), add_hi = int_half2(sc1, -64.0f);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const u32x2v b = *reinterpret_cast<const u32x2v *>(row + 16 + 32 * c + 16 * j + 8 * h);
+                    const half8 blo = fma_frag(b.x & 0x0f0f0f0fu, b.y & 0x0f0f0f0fu, mul_lo, add_lo);
+                    const half8 bhi = fma_frag(b.x & 0xf0f0f0f0u, b.y & 0xf0f0f0f0u, mul_hi, add_hi);
+                    const int e_lo = 64 * c + 16 * j, e_hi = e_lo + 32;
+                    cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xrh + e_lo), blo, cq, 0, 0, 0);
+                    cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xrl + e_lo), blo, cq, 0, 0, 0);
+                    cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xrh + e_hi), bhi, cq, 0, 0, 0);
+                    cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xrl + e_hi), bhi, cq, 0, 0, 0);
+                }
+            }
+            // A block whose min codes are all zero has no min term, whatever
+            // dmin holds (GRT/GgufQ4RawDot.java:38-148; a NaN dmin adds nothing).
+            if (sw1 == 0 && (sw2 & 0xf0f0f0f0u) == 0) dmin = 0.0f;
+            // Min term: A = split sub-block sums of this super-block (lane half
+            // 0; half 1 supplies zeros), B = min codes.
+            half8 amh = {}, aml = {}, bm = {};
+            if (h == 0) {
+                amh = *reinterpret_cast<const half8 *>(sh + nl * XSS + 8 * sbl);
+                aml = *reinterpret_cast<const half8 *>(sl + nl * XSS + 8 * sbl);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    bm[s] = static_cast<_Float16>(static_cast<float>(__builtin_amdgcn_ubfe(sw1, 8 * s, 6)));
+                    bm[s + 4] = static_cast<_Float16>(static_cast<float>(
+                        __builtin_amdgcn_ubfe(sw2, 8 * s + 4, 4) | (__builtin_amdgcn_ubfe(sw1, 8 * s + 6, 2) << 4)));
+                }
+            }
+            f32x16 cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(amh, bm, f32x16{}, 0, 0, 0);
+            cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(aml, bm, cm, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] = fmaf(-dmin, cm[r], acc[r]);
+        } else {
+            d = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(row + 208));
+            const u32x2v s01 = *reinterpret_cast<const u32x2v *>(row + 192);
+            const u32x2v s23 = *reinterpret_cast<const u32x2v *>(row + 200);
+            const uint32_t scw[4] = {s01.x, s01.y, s23.x, s23.y};
+#pragma unroll
+            for (int H = 0; H < 2; ++H) {
+#pragma unroll
+                for (int l16 = 0; l16 < 2; ++l16) {
+                    // Elements 128H + 32q + 16*l16 + 8h + e for quadrants q = 0..3:
+                    // ql bytes 64H + 32(q&1) + l, nibble q>>1; qh byte 32H + l, bits 2q.
+                    const int l = 16 * l16 + 8 * h;
+                    const u32x2v qa = *reinterpret_cast<const u32x2v *>(row + 64 * H + l);
+                    const u32x2v qb = *reinterpret_cast<const u32x2v *>(row + 64 * H + 32 + l);
+                    const u32x2v qh = *reinterpret_cast<const u32x2v *>(row + 128 + 32 * H + l);
+                    uint32_t six[4][2];
+#pragma unroll
+                    for (int w = 0; w < 2; ++w) {
+                        const uint32_t A = w ? qa.y : qa.x, B = w ? qb.y : qb.x, Q = w ? qh.y : qh.x;
+                        six[0][w] = (A & 0x0f0f0f0fu) | ((Q << 4) & 0x30303030u);
+                        six[1][w] = (B & 0x0f0f0f0fu) | ((Q << 2) & 0x30303030u);
+                        six[2][w] = ((A >> 4) & 0x0f0f0f0fu) | (Q & 0x30303030u);
+                        six[3][w] = ((B >> 4) & 0x0f0f0f0fu) | ((Q >> 2) & 0x30303030u);
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int g = 8 * H + 2 * q + l16;   // scale group of these 16 elements
+                        const int sv = static_cast<int8_t>((scw[g >> 2] >> (8 * (g & 3))) & 0xffu);
+                        const _Float16 svh = static_cast<_Float16>(static_cast<float>(sv));
+                        const uint32_t sb = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, svh));
+                        const half8 bf = q6_frag(six[q][0], six[q][1], sb | (sb << 16));
+                        cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xrh + 16 * g), bf, cq, 0, 0, 0);
+                        cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xrl + 16 * g), bf, cq, 0, 0, 0);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = fmaf(d, cq[r], acc[r]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (sbl == SBS - 1) {
+            const int n = row0[t] + nl;
+            if (n < a.N) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (m < a.M) unsafeAtomicAdd(a.y + static_cast<size_t>(m) * a.N + n, acc[r]);
+                }
+            }
+        }
+    }
+}
+
+__global__ void kq_zero_kernel(float *p, long long n) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
+}
+
+template <bool Q6, int KS, int NT>
+void launch_kq(const KqArgs &args, hipStream_t s) {
+    static bool lds_set = false;                 // the attribute is per kernel, per process
+    const void *fn = reinterpret_cast<const void *>(kq_mm_kernel<Q6, KS, NT>);
+    const size_t lds = kq_lds_bytes<Q6, KS>();
+    if (!lds_set) {
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        lds_set = true;
+    }
+    const dim3 grid((args.N + kRowsPerWg * NT - 1) / (kRowsPerWg * NT), args.K / KS), block(kThreads);
+    hipLaunchKernelGGL((kq_mm_kernel<Q6, KS, NT>), grid, block, lds, s, args);
+}
+
+}  // namespace
+
+// 2 <= M <= 32, K % 512 == 0, A and W 16-byte aligned.
+int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M) {
+    if ((type != ALJABR_ROCM_TYPE_Q4_K && type != ALJABR_ROCM_TYPE_Q6_K) || M < 2 || M > 32 || K % 512 != 0 ||
+        N < 1 || !aligned(A, 16) || !aligned(W, 16))
+        return ALJABR_ROCM_ERR_UNSUPPORTED;
+    const KqArgs args{C, A, W, M, N, K};
+    hipStream_t s = current_stream();
+    const long long total = static_cast<long long>(M) * N;
+    hipLaunchKernelGGL(kq_zero_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, C, total);
+    const int wgs_n = (N + kRowsPerWg - 1) / kRowsPerWg;
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const long long units = static_cast<long long>(wgs_n) * (K / 512);
+    const bool two = units > cus;
+    if (type == ALJABR_ROCM_TYPE_Q4_K) {
+        if (two) launch_kq<false, 512, 2>(args, s);
+        else launch_kq<false, 512, 1>(args, s);
+    } else {
+        if (two) launch_kq<true, 512, 2>(args, s);
+        else launch_kq<true, 512, 1>(args, s);
+    }
+    return ALJABR_ROCM_OK;
+}
+
+}  // namespace aljabr

@@ -118,7 +118,20 @@ int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int
     if (M == 1 && enqueue_rows(C, A, W, nullptr, K, N, type, 0) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
     hipStream_t s = current_stream();
     const bool q6 = type == ALJABR_ROCM_TYPE_Q6_K;
-    for (int m0 = 0; m0 < M; m0 += 8) {
+    int m0 = 0;
+    if (M >= 2 && K % 512 == 0 && mfma_enabled()) {
+        // Matrix cores, 32 tokens per pass; a last single token takes the rows kernel.
+        for (; M - m0 >= 2; m0 += 32) {
+            const int mm = M - m0 < 32 ? M - m0 : 32;
+            const int rc = enqueue_kquant_mfma(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, W,
+                                               K, N, type, mm);
+            if (rc != ALJABR_ROCM_OK) return rc;
+        }
+        if (m0 < M && enqueue_rows(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, W, nullptr, K,
+                                   N, type, 0) == ALJABR_ROCM_OK)
+            return ALJABR_ROCM_OK;
+    }
+    for (; m0 < M; m0 += 8) {
         const int mm = M - m0 < 8 ? M - m0 : 8;
         float *c = C + static_cast<size_t>(m0) * N;
         const float *a = A + static_cast<size_t>(m0) * K;

@@ -51,7 +51,7 @@ namespace {
 constexpr int kChunk = 2048;
 constexpr int kFmtNF4 = 0, kFmtQ4 = 1, kFmtQ8 = 2, kFmtQ4K = 3, kFmtQ6K = 4;
 constexpr bool kquant_fmt(int f) { return f == kFmtQ4K || f == kFmtQ6K; }
-constexpr bool pair_table_fmt(int f) { return f == kFmtNF4 || f == kFmtQ4; }
+constexpr bool pair_table_fmt(int f) { return f == kFmtNF4 || f == kFmtQ4 || f == kFmtQ4K; }
 constexpr int kPairBytes = 256 * 256;          // 256 entries x 32 replicas x float2
 
 typedef unsigned int u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -215,8 +215,25 @@ __device__ __forceinline__ float row_dot(const RowWords<FMT> &d, const float (&x
         float plo, phi;
         scale = 1.0f;
         if constexpr (FMT == kFmtQ4K) {
-            q4k_dots(d.q, xv, xv + 16, plo, phi);
-            return k_combine<false>(q4k_scales(d.hdr, j), plo, phi, xsum, xsum2);
+            // Pair table of raw nibbles: byte -> (low, high) as floats.
+            const uint32_t wv[4] = {d.q.x, d.q.y, d.q.z, d.q.w};
+            float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float2 e0 = pair_at(tbl, pair_addr<0>(wv[i], cl));
+                const float2 e1 = pair_at(tbl, pair_addr<1>(wv[i], cl));
+                const float2 e2 = pair_at(tbl, pair_addr<2>(wv[i], cl));
+                const float2 e3 = pair_at(tbl, pair_addr<3>(wv[i], cl));
+                p0 = fmaf(e0.x, xv[4 * i + 0], p0);
+                p1 = fmaf(e0.y, xv[16 + 4 * i + 0], p1);
+                p0 = fmaf(e1.x, xv[4 * i + 1], p0);
+                p1 = fmaf(e1.y, xv[16 + 4 * i + 1], p1);
+                p0 = fmaf(e2.x, xv[4 * i + 2], p0);
+                p1 = fmaf(e2.y, xv[16 + 4 * i + 2], p1);
+                p0 = fmaf(e3.x, xv[4 * i + 3], p0);
+                p1 = fmaf(e3.y, xv[16 + 4 * i + 3], p1);
+            }
+            return k_combine<false>(q4k_scales(d.hdr, j), p0, p1, xsum, xsum2);
         } else {
             q6k_dots(d, j, xv, xv + 16, plo, phi);
             return k_combine<true>(q6k_scales(d, j), plo, phi, xsum, xsum2);
@@ -291,7 +308,7 @@ __device__ __forceinline__ float row_dot(const RowWords<FMT> &d, const float (&x
 }
 
 // Pair table: slot i holds entry e = i/32 of replica i%32. NF4 bytes are (even code << 4) | odd code -> (level[hi],
-// level[lo]); Q4_0 low nibble -> element j, high -> j+16 -> (lo-8, hi-8).
+// level[lo]); Q4_0 low nibble -> element j, high -> j+16 -> (lo-8, hi-8); Q4_K (lo, hi).
 template <int FMT, int NT>
 __device__ __forceinline__ void build_pair_table(float2 *tbl2, int tid) {
     static_assert(NT == 512 || NT == 1024, "table build assumes 512 or 1024 threads");
@@ -304,12 +321,13 @@ __device__ __forceinline__ void build_pair_table(float2 *tbl2, int tid) {
     // i/512 = (NT/512)*k + tid/512.
     const int lo = (tid >> 5) & 15;
     const bool h1 = NT == 1024 && (tid >> 9);
-    const float vlo = FMT == kFmtNF4 ? nf4_level_sel(lo) : static_cast<float>(lo - 8);
+    constexpr int zp = FMT == kFmtQ4 ? 8 : 0;   // Q4_0 zero point
+    const float vlo = FMT == kFmtNF4 ? nf4_level_sel(lo) : static_cast<float>(lo - zp);
 #pragma unroll
     for (int k = 0; k < 8192 / NT; ++k) {
         const int hi0 = (NT / 512) * k;
         const float vhi = FMT == kFmtNF4 ? (h1 ? kNF4[hi0 + 1] : kNF4[hi0])
-                                         : static_cast<float>(hi0 - 8) + (h1 ? 1.0f : 0.0f);
+                                         : static_cast<float>(hi0 - zp) + (h1 ? 1.0f : 0.0f);
         tbl2[tid + NT * k] = FMT == kFmtNF4 ? make_float2(vhi, vlo) : make_float2(vlo, vhi);
     }
 }

@@ -75,6 +75,30 @@ def test_kquant_matvec(rocm, dev, oracle, qtype, n, k, m):
         assert rel_l2(got[i * n:(i + 1) * n], y_ref[i * n:(i + 1) * n]) <= TOL, i
 
 
+# Matrix-core path (2 <= M <= 32 per pass, K % 512 == 0): M across the pass
+# boundary (33 = 32 + a batch-1 row, 40 = 32 + 8), ragged N, the MLP shapes,
+# and the Q4_K header cases (NaN dmin with zero min codes, dmin 0, -0).
+@pytest.mark.parametrize("qtype", ["q4_k", "q6_k"])
+@pytest.mark.parametrize("n,k,m", [(300, 512, 2), (257, 1024, 5), (300, 2048, 16), (77, 1536, 31), (129, 4096, 32),
+                                   (300, 1024, 33), (100, 3072, 40), (14336, 4096, 8), (4096, 14336, 32)])
+def test_kquant_mfma(rocm, dev, oracle, qtype, n, k, m):
+    qt = TYPES[qtype]
+    blocks = _blocks(oracle, qt, n, k, seed=3 * n + k + m)
+    if qt == 12:
+        special = _special_q4k_blocks(6, 17).reshape(6, 144)
+        b = blocks.reshape(-1, 144)
+        b[:5] = special[:5]                     # the first row's first super-blocks
+    x = oracle.normal(61 + m + k, m * k)
+    y_ref = oracle.q_matvec(qt, blocks, x, n, k).ravel()
+    wd, xd = dev.put(blocks), dev.put(x)
+    y = dev.empty(m * n)
+    rocm.call("aljabr_rocm_matvec_tb_batch", dev.ptr(y), dev.ptr(xd), dev.ptr(wd), k, n, qt, m)
+    got = dev.get(y)
+    assert np.isfinite(got).all()
+    for i in range(m):
+        assert rel_l2(got[i * n:(i + 1) * n], y_ref[i * n:(i + 1) * n]) <= TOL, i
+
+
 @pytest.mark.parametrize("qtype", ["q4_k", "q6_k"])
 @pytest.mark.parametrize("n,k", [(1, 2048), (100, 2048), (333, 6144), (77, 10240), (4096, 14336)])
 def test_kquant_batch1_entry_points(rocm, dev, oracle, qtype, n, k):
