@@ -78,6 +78,26 @@ class LlamaWeights(ctypes.Structure):
     ]
 
 
+class Tensor(ctypes.Structure):
+    """aljabr_rocm_tensor: device data, type id, and (NF4) absmax and block size."""
+    _fields_ = [("data", _P), ("absmax", _P), ("type", ctypes.c_int32), ("block_size", ctypes.c_int32)]
+
+
+_TP = ctypes.POINTER(Tensor)
+
+
+class LlamaTensors(ctypes.Structure):
+    """aljabr_rocm_llama_tensors: a typed session's weights."""
+    _fields_ = [
+        ("tok_embed", Tensor),
+        ("attn_norm", _PP), ("ffn_norm", _PP),
+        ("wq", _TP), ("wk", _TP), ("wv", _TP), ("wo", _TP),
+        ("w_gate", _TP), ("w_up", _TP), ("w_down", _TP),
+        ("out_norm", _P),
+        ("lm_head", Tensor),
+    ]
+
+
 # name -> (restype, argtypes); every symbol declared in include/aljabr_rocm.h.
 class KernelStat(ctypes.Structure):
     """aljabr_rocm_kernel_stat: one launch group of a profiled decode step."""
@@ -129,6 +149,21 @@ SIGNATURES = {
     "aljabr_rocm_argmax": (_I, [_P, _P, _I, _I]),
     "aljabr_rocm_llama_create": (_I, [ctypes.POINTER(LlamaConfig), ctypes.POINTER(LlamaWeights),
                                       ctypes.POINTER(_P)]),
+    "aljabr_rocm_llama_create_typed": (_I, [ctypes.POINTER(LlamaConfig), ctypes.POINTER(LlamaTensors),
+                                            ctypes.POINTER(_P)]),
+    "aljabr_rocm_llama_create_gguf": (_I, [ctypes.c_char_p, _I, _I, ctypes.POINTER(_P)]),
+    "aljabr_rocm_llama_config_get": (_I, [_P, ctypes.POINTER(LlamaConfig)]),
+    "aljabr_rocm_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "aljabr_rocm_gguf_close": (_I, [_P]),
+    "aljabr_rocm_gguf_tensor_count": (_I, [_P, ctypes.POINTER(ctypes.c_int64)]),
+    "aljabr_rocm_gguf_find_tensor": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+    "aljabr_rocm_gguf_tensor_info": (_I, [_P, ctypes.c_int64, ctypes.c_char_p, _I, ctypes.POINTER(ctypes.c_int32),
+                                          ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int64),
+                                          ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "aljabr_rocm_gguf_tensor_data": (_I, [_P, ctypes.c_int64, ctypes.POINTER(_P)]),
+    "aljabr_rocm_gguf_meta_int": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+    "aljabr_rocm_gguf_meta_float": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "aljabr_rocm_gguf_meta_string": (_I, [_P, ctypes.c_char_p, ctypes.c_char_p, _I]),
     "aljabr_rocm_llama_destroy": (_I, [_P]),
     "aljabr_rocm_llama_decode": (_I, [_P, _P, _P, _I, _P, _P]),
     "aljabr_rocm_llama_decode_graph": (_I, [_P, _P, _P, _I, _P, _P]),

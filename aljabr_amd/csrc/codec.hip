@@ -11,6 +11,7 @@
 // Encoders reproduce GWR/GGUFWriter.java:163-209,360-387 bit for bit (fp32
 // scale for quantizing, writer-rounded fp16 scale stored, Java Math.round).
 // Every multiply uses __fmul_rn so the compiler cannot contract it.
+#include "dequant.hpp"
 #include "device.hpp"
 #include "internal.hpp"
 
@@ -38,75 +39,27 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(float *__restrict
 __global__ __launch_bounds__(kThreads) void q4_0_dequant_kernel(float *__restrict__ dst, const uint8_t *__restrict__ src,
                                                                 long long nblocks) {
     const long long blk = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
-    if (blk >= nblocks) return;
-    const uint8_t *b = src + blk * 18;
-    const float d = f16_bits_to_f32_exact(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
-    float *o = dst + blk * 32;
-    for (int j = 0; j < 16; ++j) {
-        const int q = b[2 + j];
-        o[j] = __fadd_rn(__fmul_rn(static_cast<float>((q & 15) - 8), d), 0.0f);
-        o[16 + j] = __fadd_rn(__fmul_rn(static_cast<float>((q >> 4) - 8), d), 0.0f);
-    }
+    if (blk < nblocks) dq_q4_0_block(src + blk * 18, dst + blk * 32);
 }
 
 __global__ __launch_bounds__(kThreads) void q8_0_dequant_kernel(float *__restrict__ dst, const uint8_t *__restrict__ src,
                                                                 long long nblocks) {
     const long long blk = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
-    if (blk >= nblocks) return;
-    const uint8_t *b = src + blk * 34;
-    const float d = f16_bits_to_f32_exact(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
-    for (int j = 0; j < 32; ++j) dst[blk * 32 + j] = __fmul_rn(static_cast<float>(static_cast<int8_t>(b[2 + j])), d);
+    if (blk < nblocks) dq_q8_0_block(src + blk * 34, dst + blk * 32);
 }
 
 // One thread per 32-element sub-block of a Q4_K super-block.
 __global__ __launch_bounds__(kThreads) void q4_k_dequant_kernel(float *__restrict__ dst, const uint8_t *__restrict__ src,
                                                                 long long nsub) {
     const long long t = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
-    if (t >= nsub) return;
-    const uint8_t *b = src + (t >> 3) * 144;
-    const int sub = static_cast<int>(t & 7);
-    const float d = f16_bits_to_f32_exact(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
-    const float dmin = f16_bits_to_f32_exact(static_cast<uint32_t>(b[2]) | (static_cast<uint32_t>(b[3]) << 8));
-    const uint8_t *sc = b + 4;
-    int scale, mn;
-    if (sub < 4) {
-        scale = sc[sub] & 63;
-        mn = sc[sub + 4] & 63;
-    } else {
-        scale = (sc[sub + 4] & 0x0F) | ((sc[sub - 4] >> 6) << 4);
-        mn = (sc[sub + 4] >> 4) | ((sc[sub] >> 6) << 4);
-    }
-    const float d1 = __fmul_rn(d, static_cast<float>(scale));
-    const float m1 = (dmin == 0.0f || mn == 0) ? 0.0f : __fmul_rn(dmin, static_cast<float>(mn));
-    // Sub-block 2c + h: low (h = 0) or high (h = 1) nibbles of qs[32c .. 32c+32).
-    const uint8_t *q = b + 16 + 32 * (sub >> 1);
-    const int shift = 4 * (sub & 1);
-    float *o = dst + (t << 5);
-    for (int l = 0; l < 32; ++l)
-        o[l] = __fsub_rn(__fmul_rn(d1, static_cast<float>((q[l] >> shift) & 0x0F)), m1);
+    if (t < nsub) dq_q4_k_sub(src + (t >> 3) * 144, static_cast<int>(t & 7), dst + (t << 5));
 }
 
 // One thread per 16-element scale group of a Q6_K super-block.
 __global__ __launch_bounds__(kThreads) void q6_k_dequant_kernel(float *__restrict__ dst, const uint8_t *__restrict__ src,
                                                                 long long ngroups) {
     const long long t = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
-    if (t >= ngroups) return;
-    const uint8_t *b = src + (t >> 4) * 210;
-    const int g = static_cast<int>(t & 15);             // elements 16g .. 16g+15
-    const int h = g >> 3, quad = (g >> 1) & 3, l0 = 16 * (g & 1);
-    const float d = f16_bits_to_f32_exact(static_cast<uint32_t>(b[208]) | (static_cast<uint32_t>(b[209]) << 8));
-    const float scale = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(b[192 + g])));
-    // Quadrant quad of half h: ql[64h + 32*(quad & 1) + l], nibble quad >> 1,
-    // qh[32h + l] bits 2*quad.
-    const uint8_t *ql = b + 64 * h + 32 * (quad & 1);
-    const uint8_t *qh = b + 128 + 32 * h;
-    const int nib = 4 * (quad >> 1), hs = 2 * quad;
-    float *o = dst + (t << 4);
-    for (int i = 0; i < 16; ++i) {
-        const int l = l0 + i;
-        const int q = (((ql[l] >> nib) & 0x0F) | (((qh[l] >> hs) & 3) << 4)) - 32;
-        o[i] = __fmul_rn(scale, static_cast<float>(q));
-    }
+    if (t < ngroups) dq_q6_k_group(src + (t >> 4) * 210, static_cast<int>(t & 15), dst + (t << 4));
 }
 
 __global__ __launch_bounds__(kThreads) void f16_dequant_kernel(float *__restrict__ dst, const uint16_t *__restrict__ src,

@@ -43,6 +43,11 @@ bool mfma_enabled();
 // C[M][N] = A[M][K] . W[N][K]^T for any M (slices or MFMA chosen inside).
 int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M);
 int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M);
+int enqueue_matmul_f32(float *C, const float *A, const float *W, int K, int N, int M);
+// Any weight type of the library (NF4 with its absmax and block size, GGUF
+// F32/F16/Q4_0/Q8_0/Q4_K/Q6_K).
+int enqueue_matmul_typed(float *C, const float *A, const void *W, const float *absmax, int type, int bs, int K, int N,
+                         int M);
 // GGUF Q4_K / Q6_K rows (K % 256 == 0, A and W 16-byte aligned), any M.
 int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M);
 // Q4_K / Q6_K small-M GEMM on MFMA (2 <= M <= 32, K % 512 == 0, A and W
@@ -122,6 +127,9 @@ int enqueue_swiglu(float *dst, const float *gate, const float *up, long long n);
 int enqueue_add(float *a, const float *b, long long n);
 int enqueue_argmax(int *out, const float *x, int rows, int cols);
 int enqueue_embed(float *x, const float *embed, const int *tokens, int batch, int dim, int vocab);
+// x[b] = row tokens[b] of a [vocab][dim] table of type F32, F16, Q4_0, Q8_0,
+// Q4_K or Q6_K, decoded bit-exactly (dim a multiple of the type's block).
+int enqueue_embed_typed(float *x, const void *table, int type, const int *tokens, int batch, int dim, int vocab);
 int enqueue_kv_append(uint16_t *cache, const float *src, const int *pos, int batch, int n_kv, int head_dim, int cap);
 // RoPE on q [batch][nh][D] in place and on k, then k and v [batch][nkv][D]
 // appended as fp16 at row pos[b] of caches [batch][nkv][cap][D] (D/2 <= 1024).

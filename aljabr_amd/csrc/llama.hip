@@ -1,4 +1,5 @@
-// llama.hip - device-resident Llama-style decode step over NF4 weights.
+// llama.hip - device-resident Llama-style decode step over NF4 or GGUF-typed
+// weights (F32, F16, Q4_0, Q8_0, Q4_K, Q6_K; any mix per matrix).
 //
 // Composition follows GgufDecodePass.forward's per-op path
 // (engine/gguf/aljabr-gguf-java/src/main/java/tech/kayys/aljabr/gguf/javabackend/
@@ -14,10 +15,13 @@
 // cache is fp16 [layer][batch][kv_head][max_seq][head_dim].
 #include <algorithm>
 #include <cstring>
+#include <memory>
 #include <new>
+#include <string>
 #include <vector>
 
 #include "device.hpp"
+#include "gguf.hpp"
 #include "internal.hpp"
 #include "kernels.hpp"
 
@@ -44,10 +48,19 @@ __global__ void copy_i32_pairs(int *__restrict__ dst_a, const int *__restrict__ 
 }  // namespace aljabr
 
 struct aljabr_rocm_llama {
+    // A weight matrix: device data, its ALJABR_ROCM_TYPE_* and (NF4) absmax.
+    struct T {
+        const uint8_t *w = nullptr;
+        const float *s = nullptr;
+        int type = ALJABR_ROCM_TYPE_NF4;
+    };
     aljabr_rocm_llama_config cfg;
-    std::vector<const void *> attn_norm, ffn_norm, wq, wk, wv, wo, wq_s, wk_s, wv_s, wo_s;
-    std::vector<const void *> w_gate, w_up, w_down, w_gate_s, w_up_s, w_down_s;
-    const void *tok_embed = nullptr, *out_norm = nullptr, *lm_head = nullptr;
+    std::vector<const float *> attn_norm, ffn_norm;
+    std::vector<T> wq, wk, wv, wo, w_gate, w_up, w_down;
+    T tok_embed, lm_head;
+    const float *out_norm = nullptr;
+    bool all_nf4 = true;      // every projection NF4 with cfg.nf4_block: the fused NF4 launches apply
+    void *weights_owned = nullptr;   // device weights the session allocated (GGUF loader), freed with it
     void *arena = nullptr;   // one allocation for the KV cache and activations
     uint16_t *k_cache = nullptr, *v_cache = nullptr;
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
@@ -76,13 +89,46 @@ T *carve(char *&cursor, size_t count) {
     return p;
 }
 
-bool copy_table(std::vector<const void *> &dst, const void *const *src, int n) {
-    if (!src) return false;
-    dst.assign(src, src + n);
-    for (const void *p : dst)
-        if (!p) return false;
+bool matvec_type(int t) {
+    return t == ALJABR_ROCM_TYPE_NF4 || t == ALJABR_ROCM_TYPE_F32 || t == ALJABR_ROCM_TYPE_F16 ||
+           t == ALJABR_ROCM_TYPE_Q4_0 || t == ALJABR_ROCM_TYPE_Q8_0 || t == ALJABR_ROCM_TYPE_Q4_K ||
+           t == ALJABR_ROCM_TYPE_Q6_K;
+}
+
+// Elements per quantization block of a GGUF type (the row length must be a
+// multiple), 1 for F32/F16.
+int type_block(int t) {
+    switch (t) {
+    case ALJABR_ROCM_TYPE_Q4_0:
+    case ALJABR_ROCM_TYPE_Q8_0: return 32;
+    case ALJABR_ROCM_TYPE_Q4_K:
+    case ALJABR_ROCM_TYPE_Q6_K: return 256;
+    default: return 1;
+    }
+}
+
+// Copies one typed matrix; rows of `k` elements must be whole blocks.
+bool take_tensor(aljabr_rocm_llama::T &dst, const aljabr_rocm_tensor &src, int k, int nf4_block) {
+    if (!src.data || !matvec_type(src.type) || k % type_block(src.type) != 0) return false;
+    if (src.type == ALJABR_ROCM_TYPE_NF4 && (!src.absmax || (src.block_size != 0 && src.block_size != nf4_block)))
+        return false;
+    dst.w = static_cast<const uint8_t *>(src.data);
+    dst.s = static_cast<const float *>(src.absmax);
+    dst.type = src.type;
     return true;
 }
+
+int validate_config(const aljabr_rocm_llama_config &c) {
+    ALJ_REQUIRE(c.layers > 0 && c.dim > 0 && c.ffn > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.head_dim > 0 &&
+                    c.vocab > 0 && c.max_seq > 0 && c.max_batch > 0 && c.nf4_block > 0,
+                "llama config dimensions must be positive");
+    ALJ_REQUIRE(c.n_heads % c.n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
+    ALJ_REQUIRE(c.head_dim % 2 == 0 && c.nf4_block % 2 == 0, "head_dim and nf4_block must be even");
+    ALJ_REQUIRE(c.rope_base > 1.0f && c.eps >= 0.0f, "rope_base must exceed 1 and eps be non-negative");
+    return ALJABR_ROCM_OK;
+}
+
+int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_tensors *w, aljabr_rocm_llama **out);
 
 }  // namespace
 
@@ -93,34 +139,97 @@ int aljabr_rocm_llama_create(const aljabr_rocm_llama_config *cfg, const aljabr_r
     ALJ_CHECK_READY();
     ALJ_REQUIRE(cfg && w && out, "cfg, weights and out must be non-null");
     *out = nullptr;
-    const aljabr_rocm_llama_config &c = *cfg;
-    ALJ_REQUIRE(c.layers > 0 && c.dim > 0 && c.ffn > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.head_dim > 0 &&
-                    c.vocab > 0 && c.max_seq > 0 && c.max_batch > 0 && c.nf4_block > 0,
-                "llama config dimensions must be positive");
-    ALJ_REQUIRE(c.n_heads % c.n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
-    ALJ_REQUIRE(c.head_dim % 2 == 0 && c.nf4_block % 2 == 0, "head_dim and nf4_block must be even");
-    ALJ_REQUIRE(c.rope_base > 1.0f && c.eps >= 0.0f, "rope_base must exceed 1 and eps be non-negative");
+    int rc = validate_config(*cfg);
+    if (rc != ALJABR_ROCM_OK) return rc;
     ALJ_REQUIRE(w->tok_embed && w->out_norm && w->lm_head, "embedding, output norm and LM head are required");
+    const int L = cfg->layers;
+    ALJ_REQUIRE(w->attn_norm && w->ffn_norm && w->wq && w->wk && w->wv && w->wo && w->w_gate && w->w_up && w->w_down &&
+                    w->wq_absmax && w->wk_absmax && w->wv_absmax && w->wo_absmax && w->w_gate_absmax &&
+                    w->w_up_absmax && w->w_down_absmax,
+                "every per-layer weight table must be non-null");
+    // The NF4 layout as typed tensors (fp32 embedding, fp16 LM head).
+    std::vector<aljabr_rocm_tensor> t(static_cast<size_t>(7) * L);
+    auto nf4 = [&](const void *data, const void *absmax) {
+        return aljabr_rocm_tensor{data, absmax, ALJABR_ROCM_TYPE_NF4, cfg->nf4_block};
+    };
+    for (int l = 0; l < L; ++l) {
+        t[0 * L + l] = nf4(w->wq[l], w->wq_absmax[l]);
+        t[1 * L + l] = nf4(w->wk[l], w->wk_absmax[l]);
+        t[2 * L + l] = nf4(w->wv[l], w->wv_absmax[l]);
+        t[3 * L + l] = nf4(w->wo[l], w->wo_absmax[l]);
+        t[4 * L + l] = nf4(w->w_gate[l], w->w_gate_absmax[l]);
+        t[5 * L + l] = nf4(w->w_up[l], w->w_up_absmax[l]);
+        t[6 * L + l] = nf4(w->w_down[l], w->w_down_absmax[l]);
+    }
+    aljabr_rocm_llama_tensors tw{};
+    tw.tok_embed = aljabr_rocm_tensor{w->tok_embed, nullptr, ALJABR_ROCM_TYPE_F32, 0};
+    tw.attn_norm = w->attn_norm;
+    tw.ffn_norm = w->ffn_norm;
+    tw.wq = &t[0 * L];
+    tw.wk = &t[1 * L];
+    tw.wv = &t[2 * L];
+    tw.wo = &t[3 * L];
+    tw.w_gate = &t[4 * L];
+    tw.w_up = &t[5 * L];
+    tw.w_down = &t[6 * L];
+    tw.out_norm = w->out_norm;
+    tw.lm_head = aljabr_rocm_tensor{w->lm_head, nullptr, ALJABR_ROCM_TYPE_F16, 0};
+    return create_session(*cfg, &tw, out);
+}
 
+int aljabr_rocm_llama_create_typed(const aljabr_rocm_llama_config *cfg, const aljabr_rocm_llama_tensors *w,
+                                   aljabr_rocm_llama **out) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(cfg && w && out, "cfg, weights and out must be non-null");
+    *out = nullptr;
+    const int rc = validate_config(*cfg);
+    if (rc != ALJABR_ROCM_OK) return rc;
+    return create_session(*cfg, w, out);
+}
+
+}  // extern "C"
+
+namespace {
+
+int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_tensors *w, aljabr_rocm_llama **out) {
+    ALJ_REQUIRE(w->out_norm && w->attn_norm && w->ffn_norm && w->wq && w->wk && w->wv && w->wo && w->w_gate &&
+                    w->w_up && w->w_down,
+                "output norm and every per-layer table are required");
     aljabr_rocm_llama *m = new (std::nothrow) aljabr_rocm_llama();
     if (!m) return fail(ALJABR_ROCM_ERR_BUFFER, "out of host memory");
     m->cfg = c;
     const int L = c.layers;
-    bool ok = copy_table(m->attn_norm, w->attn_norm, L) && copy_table(m->ffn_norm, w->ffn_norm, L) &&
-              copy_table(m->wq, w->wq, L) && copy_table(m->wk, w->wk, L) && copy_table(m->wv, w->wv, L) &&
-              copy_table(m->wo, w->wo, L) && copy_table(m->wq_s, w->wq_absmax, L) &&
-              copy_table(m->wk_s, w->wk_absmax, L) && copy_table(m->wv_s, w->wv_absmax, L) &&
-              copy_table(m->wo_s, w->wo_absmax, L) && copy_table(m->w_gate, w->w_gate, L) &&
-              copy_table(m->w_up, w->w_up, L) && copy_table(m->w_down, w->w_down, L) &&
-              copy_table(m->w_gate_s, w->w_gate_absmax, L) && copy_table(m->w_up_s, w->w_up_absmax, L) &&
-              copy_table(m->w_down_s, w->w_down_absmax, L);
+    const int qd_i = c.n_heads * c.head_dim, kvd_i = c.n_kv_heads * c.head_dim;
+    bool ok = true;
+    m->attn_norm.resize(L);
+    m->ffn_norm.resize(L);
+    for (auto *v : {&m->wq, &m->wk, &m->wv, &m->wo, &m->w_gate, &m->w_up, &m->w_down}) v->resize(L);
+    for (int l = 0; l < L && ok; ++l) {
+        m->attn_norm[l] = static_cast<const float *>(w->attn_norm[l]);
+        m->ffn_norm[l] = static_cast<const float *>(w->ffn_norm[l]);
+        ok = m->attn_norm[l] && m->ffn_norm[l] && take_tensor(m->wq[l], w->wq[l], c.dim, c.nf4_block) &&
+             take_tensor(m->wk[l], w->wk[l], c.dim, c.nf4_block) && take_tensor(m->wv[l], w->wv[l], c.dim, c.nf4_block) &&
+             take_tensor(m->wo[l], w->wo[l], qd_i, c.nf4_block) &&
+             take_tensor(m->w_gate[l], w->w_gate[l], c.dim, c.nf4_block) &&
+             take_tensor(m->w_up[l], w->w_up[l], c.dim, c.nf4_block) &&
+             take_tensor(m->w_down[l], w->w_down[l], c.ffn, c.nf4_block);
+    }
+    (void)kvd_i;
+    const int et = w->tok_embed.type;
+    ok = ok && w->tok_embed.data && et != ALJABR_ROCM_TYPE_NF4 && matvec_type(et) && c.dim % type_block(et) == 0 &&
+         take_tensor(m->lm_head, w->lm_head, c.dim, c.nf4_block);
     if (!ok) {
         delete m;
-        return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "every per-layer weight pointer must be non-null");
+        return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT,
+                    "every weight must be non-null, of a supported type, with rows of whole blocks "
+                    "(the embedding F32/F16/Q4_0/Q8_0/Q4_K/Q6_K; NF4 with absmax and the config's block size)");
     }
-    m->tok_embed = w->tok_embed;
-    m->out_norm = w->out_norm;
-    m->lm_head = w->lm_head;
+    m->tok_embed.w = static_cast<const uint8_t *>(w->tok_embed.data);
+    m->tok_embed.type = et;
+    m->out_norm = static_cast<const float *>(w->out_norm);
+    for (int l = 0; l < L; ++l)
+        for (const auto *v : {&m->wq, &m->wk, &m->wv, &m->wo, &m->w_gate, &m->w_up, &m->w_down})
+            m->all_nf4 = m->all_nf4 && (*v)[l].type == ALJABR_ROCM_TYPE_NF4;
 
     const size_t B = static_cast<size_t>(c.max_batch);
     const size_t kvd = static_cast<size_t>(c.n_kv_heads) * c.head_dim;
@@ -157,18 +266,239 @@ int aljabr_rocm_llama_create(const aljabr_rocm_llama_config *cfg, const aljabr_r
     m->attn_scratch_bytes = attention_scratch_bytes(c.max_batch, c.n_heads, 1, c.head_dim, c.max_seq);
     m->attn_scratch = carve<float>(cur, m->attn_scratch_bytes / sizeof(float));
     m->graphs.resize(static_cast<size_t>(c.max_batch) + 1);
-    // Batch-1 fusion needs every K a multiple of 2048 (at most 16384), a
+    // Batch-1 NF4 fusion needs every K a multiple of 2048 (at most 16384), a
     // power-of-two block of at least 32 and 16-byte aligned weights and norms.
-    const int qd_i = c.n_heads * c.head_dim;
     const int shift = log2_exact(c.nf4_block);
     auto k_ok = [](int k) { return k % 2048 == 0 && k / 2048 >= 1 && k / 2048 <= 8; };
-    bool fused = k_ok(c.dim) && k_ok(qd_i) && k_ok(c.ffn) && shift >= 5;
-    for (int l = 0; l < L && fused; ++l)
-        for (const auto *t : {&m->attn_norm, &m->ffn_norm, &m->wq, &m->wk, &m->wv, &m->wo, &m->w_gate, &m->w_up,
-                              &m->w_down})
-            fused = fused && aligned((*t)[l], 16);
+    bool fused = m->all_nf4 && k_ok(c.dim) && k_ok(qd_i) && k_ok(c.ffn) && shift >= 5;
+    for (int l = 0; l < L && fused; ++l) {
+        fused = aligned(m->attn_norm[l], 16) && aligned(m->ffn_norm[l], 16);
+        for (const auto *t : {&m->wq, &m->wk, &m->wv, &m->wo, &m->w_gate, &m->w_up, &m->w_down})
+            fused = fused && aligned((*t)[l].w, 16);
+    }
     m->rows_fused = fused;
     *out = m;
+    return ALJABR_ROCM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+}  // extern "C"
+
+namespace {
+
+// binary16 bits -> binary32 (exact; NaN -> canonical quiet NaN).
+float half_to_float(uint16_t h) {
+    const uint32_t sign = (h >> 15) & 1u, e = (h >> 10) & 0x1fu, mant = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 0) {
+        if (mant == 0) {
+            bits = sign << 31;
+        } else {
+            int lz = 0;
+            uint32_t mm = mant;
+            while (!(mm & 0x400u)) {
+                mm <<= 1;
+                ++lz;
+            }
+            bits = (sign << 31) | ((113u - static_cast<uint32_t>(lz)) << 23) | ((mm & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        bits = mant == 0 ? ((sign << 31) | 0x7f800000u) : 0x7fc00000u;
+    } else {
+        bits = (sign << 31) | ((e + 112u) << 23) | (mant << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+// Metadata lookups of a Llama-family GGUF file ("{arch}.key").
+struct GgufMeta {
+    const GgufFile &g;
+    std::string arch;
+    bool num(const std::string &key, double &v) const {
+        const GgufValue *x = g.find(arch + "." + key);
+        if (!x || x->type == 8 || x->type == 9) return false;
+        v = (x->type == 6 || x->type == 12) ? x->f : static_cast<double>(x->i);
+        return true;
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int aljabr_rocm_llama_create_gguf(const char *path, int max_batch, int max_seq, aljabr_rocm_llama **out) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(path && out && max_batch > 0, "path, out and a positive max_batch are required");
+    *out = nullptr;
+    GgufFile *raw = nullptr;
+    int rc = gguf_open(path, &raw);
+    if (rc != ALJABR_ROCM_OK) return rc;
+    std::unique_ptr<GgufFile> g(raw);
+    GgufMeta meta{*g, "llama"};
+    if (const GgufValue *a = g->find("general.architecture"))
+        if (a->type == 8) meta.arch = a->s;
+    double v;
+    aljabr_rocm_llama_config c{};
+    auto need = [&](const char *key, int32_t &dst) {
+        if (!meta.num(key, v)) return false;
+        dst = static_cast<int32_t>(v);
+        return true;
+    };
+    if (!need("block_count", c.layers) || !need("embedding_length", c.dim) || !need("feed_forward_length", c.ffn) ||
+        !need("attention.head_count", c.n_heads))
+        return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "gguf: %s lacks %s.block_count / embedding_length / "
+                    "feed_forward_length / attention.head_count", path, meta.arch.c_str());
+    c.n_kv_heads = meta.num("attention.head_count_kv", v) ? static_cast<int32_t>(v) : c.n_heads;
+    c.head_dim = meta.num("attention.key_length", v) ? static_cast<int32_t>(v)
+                                                       : (c.n_heads > 0 ? c.dim / c.n_heads : 0);
+    c.rope_base = meta.num("rope.freq_base", v) ? static_cast<float>(v) : 10000.0f;
+    c.eps = meta.num("attention.layer_norm_rms_epsilon", v) ? static_cast<float>(v) : 1e-5f;
+    c.max_seq = max_seq > 0 ? max_seq : (meta.num("context_length", v) ? static_cast<int32_t>(v) : 0);
+    c.max_batch = max_batch;
+    c.nf4_block = 64;
+    if (meta.num("rope.dimension_count", v) && static_cast<int32_t>(v) != c.head_dim)
+        return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "gguf: %s rotates %d of %d head dimensions (partial RoPE)", path,
+                    static_cast<int>(v), c.head_dim);
+    // Tensors the decode step does not apply: refuse rather than decode a
+    // different model.
+    for (const char *extra : {"blk.0.attn_q_norm.weight", "blk.0.attn_k_norm.weight", "blk.0.post_attention_norm.weight",
+                              "blk.0.post_ffw_norm.weight", "rope_freqs.weight", "blk.0.rope_freqs.weight",
+                              "blk.0.layer_output_scale.weight", "blk.0.attn_q.bias", "blk.0.attn_v_norm.weight"})
+        if (g->tensor(extra))
+            return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "gguf: %s has %s, which this decode step does not apply", path,
+                        extra);
+    const GgufTensor *emb = g->tensor("token_embd.weight");
+    ALJ_REQUIRE(emb && emb->n_dims == 2 && emb->dims[0] == c.dim, "gguf: %s: token_embd.weight must be [%d, vocab]",
+                path, c.dim);
+    c.vocab = static_cast<int32_t>(emb->dims[1]);
+    rc = validate_config(c);
+    if (rc != ALJABR_ROCM_OK) return rc;
+    const int L = c.layers;
+    const int64_t qd = static_cast<int64_t>(c.n_heads) * c.head_dim, kvd = static_cast<int64_t>(c.n_kv_heads) * c.head_dim;
+
+    // Every tensor the step reads, with its expected [K, N] shape (GGUF dims:
+    // ne0 = row length K, ne1 = rows N).
+    struct Need {
+        const GgufTensor *t;
+        int64_t k, n;
+        bool norm;
+    };
+    std::vector<Need> needs;
+    auto want = [&](const std::string &name, int64_t k, int64_t n, bool norm) -> int {
+        const GgufTensor *t = g->tensor(name);
+        if (!t) return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "gguf: %s: missing tensor %s", path, name.c_str());
+        const bool shape = norm ? (t->n_dims == 1 && t->dims[0] == k) : (t->n_dims == 2 && t->dims[0] == k && t->dims[1] == n);
+        if (!shape) return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "gguf: %s: tensor %s has the wrong shape", path, name.c_str());
+        const bool ok_type = norm ? (t->type == ALJABR_ROCM_TYPE_F32 || t->type == ALJABR_ROCM_TYPE_F16)
+                                  : matvec_type(t->type) && t->type != ALJABR_ROCM_TYPE_NF4 && k % type_block(t->type) == 0;
+        if (!ok_type)
+            return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "gguf: %s: tensor %s has type %d (supported: F32, F16, Q4_0, "
+                        "Q8_0, Q4_K, Q6_K)", path, name.c_str(), t->type);
+        needs.push_back({t, k, n, norm});
+        return ALJABR_ROCM_OK;
+    };
+    rc = want("token_embd.weight", c.dim, c.vocab, false);
+    for (int l = 0; l < L && rc == ALJABR_ROCM_OK; ++l) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        rc = want(b + "attn_norm.weight", c.dim, 1, true);
+        if (rc == ALJABR_ROCM_OK) rc = want(b + "attn_q.weight", c.dim, qd, false);
+        if (rc == ALJABR_ROCM_OK) rc = want(b + "attn_k.weight", c.dim, kvd, false);
+        if (rc == ALJABR_ROCM_OK) rc = want(b + "attn_v.weight", c.dim, kvd, false);
+        if (rc == ALJABR_ROCM_OK) rc = want(b + "attn_output.weight", qd, c.dim, false);
+        if (rc == ALJABR_ROCM_OK) rc = want(b + "ffn_norm.weight", c.dim, 1, true);
+        if (rc == ALJABR_ROCM_OK) rc = want(b + "ffn_gate.weight", c.dim, c.ffn, false);
+        if (rc == ALJABR_ROCM_OK) rc = want(b + "ffn_up.weight", c.dim, c.ffn, false);
+        if (rc == ALJABR_ROCM_OK) rc = want(b + "ffn_down.weight", c.ffn, c.dim, false);
+    }
+    if (rc == ALJABR_ROCM_OK) rc = want("output_norm.weight", c.dim, 1, true);
+    const bool tied = g->tensor("output.weight") == nullptr;     // LM head tied to the embedding
+    if (rc == ALJABR_ROCM_OK && !tied) rc = want("output.weight", c.dim, c.vocab, false);
+    if (rc != ALJABR_ROCM_OK) return rc;
+
+    // One device allocation for every tensor (norms as fp32), 256-byte aligned.
+    auto dev_bytes = [](const Need &n) { return n.norm ? static_cast<uint64_t>(n.k) * 4 : n.t->bytes; };
+    uint64_t total = 0;
+    for (const Need &n : needs) total += (dev_bytes(n) + 255) & ~uint64_t(255);
+    void *base = nullptr;
+    hipError_t e = hipMalloc(&base, total);
+    if (e != hipSuccess)
+        return fail(ALJABR_ROCM_ERR_BUFFER, "gguf: hipMalloc(%llu) for the weights: %s",
+                    static_cast<unsigned long long>(total), hipGetErrorString(e));
+    std::vector<const void *> dev(needs.size());
+    uint64_t off = 0;
+    std::vector<float> tmp;
+    for (size_t i = 0; i < needs.size() && e == hipSuccess; ++i) {
+        const Need &n = needs[i];
+        char *dst = static_cast<char *>(base) + off;
+        dev[i] = dst;
+        if (n.norm && n.t->type == ALJABR_ROCM_TYPE_F16) {
+            tmp.resize(static_cast<size_t>(n.k));
+            const uint16_t *h = reinterpret_cast<const uint16_t *>(g->data(*n.t));
+            for (int64_t j = 0; j < n.k; ++j) {
+                uint16_t bits;
+                std::memcpy(&bits, h + j, 2);
+                tmp[static_cast<size_t>(j)] = half_to_float(bits);
+            }
+            e = hipMemcpy(dst, tmp.data(), static_cast<size_t>(n.k) * 4, hipMemcpyHostToDevice);
+        } else {
+            e = hipMemcpy(dst, g->data(*n.t), static_cast<size_t>(dev_bytes(n)), hipMemcpyHostToDevice);
+        }
+        off += (dev_bytes(n) + 255) & ~uint64_t(255);
+    }
+    if (e != hipSuccess) {
+        (void)hipFree(base);
+        return fail(ALJABR_ROCM_ERR_DEVICE, "gguf: uploading weights: %s", hipGetErrorString(e));
+    }
+
+    // needs[] order: embedding, 9 per layer, output norm, [output].
+    auto tensor = [&](size_t i) { return aljabr_rocm_tensor{dev[i], nullptr, needs[i].t->type, 0}; };
+    std::vector<aljabr_rocm_tensor> t(static_cast<size_t>(7) * L);
+    std::vector<const void *> an(L), fn(L);
+    for (int l = 0; l < L; ++l) {
+        const size_t b = 1 + 9 * static_cast<size_t>(l);
+        an[l] = dev[b];
+        t[0 * L + l] = tensor(b + 1);
+        t[1 * L + l] = tensor(b + 2);
+        t[2 * L + l] = tensor(b + 3);
+        t[3 * L + l] = tensor(b + 4);
+        fn[l] = dev[b + 5];
+        t[4 * L + l] = tensor(b + 6);
+        t[5 * L + l] = tensor(b + 7);
+        t[6 * L + l] = tensor(b + 8);
+    }
+    const size_t on = 1 + 9 * static_cast<size_t>(L);
+    aljabr_rocm_llama_tensors tw{};
+    tw.tok_embed = tensor(0);
+    tw.attn_norm = an.data();
+    tw.ffn_norm = fn.data();
+    tw.wq = &t[0 * L];
+    tw.wk = &t[1 * L];
+    tw.wv = &t[2 * L];
+    tw.wo = &t[3 * L];
+    tw.w_gate = &t[4 * L];
+    tw.w_up = &t[5 * L];
+    tw.w_down = &t[6 * L];
+    tw.out_norm = dev[on];
+    tw.lm_head = tied ? tensor(0) : tensor(on + 1);
+    aljabr_rocm_llama *m = nullptr;
+    rc = create_session(c, &tw, &m);
+    if (rc != ALJABR_ROCM_OK) {
+        (void)hipFree(base);
+        return rc;
+    }
+    m->weights_owned = base;
+    *out = m;
+    return ALJABR_ROCM_OK;
+}
+
+int aljabr_rocm_llama_config_get(const aljabr_rocm_llama *m, aljabr_rocm_llama_config *cfg) {
+    ALJ_REQUIRE(m && cfg, "model and cfg must be non-null");
+    *cfg = m->cfg;
     return ALJABR_ROCM_OK;
 }
 
@@ -178,6 +508,7 @@ int aljabr_rocm_llama_destroy(aljabr_rocm_llama *m) {
     for (auto &g : m->graphs)
         if (g.exec) (void)hipGraphExecDestroy(g.exec);
     if (m->arena) (void)hipFree(m->arena);
+    if (m->weights_owned) (void)hipFree(m->weights_owned);
     delete m;
     return ALJABR_ROCM_OK;
 }
@@ -239,6 +570,21 @@ struct StepProfiler {
 // NF4 weight bytes of an [n, k] matrix: codes + fp32 absmax.
 double nf4_w(long long n, long long k, int bs) { return static_cast<double>(n * k / 2 + n * k / bs * 4); }
 
+// Weight bytes of an [n, k] matrix of any type.
+double weight_bytes(int type, long long n, long long k, int bs) {
+    const double e = static_cast<double>(n) * k;
+    switch (type) {
+    case ALJABR_ROCM_TYPE_NF4: return nf4_w(n, k, bs);
+    case ALJABR_ROCM_TYPE_F32: return 4.0 * e;
+    case ALJABR_ROCM_TYPE_F16: return 2.0 * e;
+    case ALJABR_ROCM_TYPE_Q4_0: return e / 32 * 18;
+    case ALJABR_ROCM_TYPE_Q8_0: return e / 32 * 34;
+    case ALJABR_ROCM_TYPE_Q4_K: return e / 256 * 144;
+    case ALJABR_ROCM_TYPE_Q6_K: return e / 256 * 210;
+    default: return 0.0;
+    }
+}
+
 int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, float *lg, int *next,
                 StepProfiler *prof, const int *host_pos) {
     const aljabr_rocm_llama_config &c = m->cfg;
@@ -262,46 +608,49 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
     double keys = 0.0;
     if (host_pos)
         for (int b = 0; b < B; ++b) keys += std::min(host_pos[b] + 1, c.max_seq);
-    // y = x . W^T (y cleared beforehand) or, with `residual`, y += x . W^T for
-    // B rows. The matrix cores' K-slices add straight into y in both cases;
-    // elsewhere y is written, or the products go to `tmp` and one add follows.
-    auto mm = [&](float *y, const float *x, const void *w, const void *sc, int K, int N, bool residual,
-                  float *tmp) -> int {
-        const uint8_t *wq = static_cast<const uint8_t *>(w);
-        const float *ws = static_cast<const float *>(sc);
-        if (B >= 2 && B <= 64 && shift >= 0) {
-            const int r = enqueue_nf4_mfma(y, x, wq, ws, K, N, shift, B, true);
+    using T = aljabr_rocm_llama::T;
+    // y = x . W^T or, with `residual`, y += x . W^T for B rows. NF4 on the
+    // matrix cores accumulates into y (which the NF4 path has cleared or
+    // holds the residual); otherwise y is written, or the products go to `tmp`
+    // and one add follows.
+    auto mm = [&](float *y, const float *x, const T &t, int K, int N, bool residual, float *tmp) -> int {
+        if (t.type == ALJABR_ROCM_TYPE_NF4 && B >= 2 && B <= 64 && shift >= 0 && m->all_nf4) {
+            const int r = enqueue_nf4_mfma(y, x, t.w, t.s, K, N, shift, B, true);
             if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
         }
-        if (!residual) return enqueue_matmul_nf4(y, x, wq, ws, K, N, bs, B);
-        const int r = enqueue_matmul_nf4(tmp, x, wq, ws, K, N, bs, B);
+        if (!residual) return enqueue_matmul_typed(y, x, t.w, t.s, t.type, bs, K, N, B);
+        const int r = enqueue_matmul_typed(tmp, x, t.w, t.s, t.type, bs, K, N, B);
         if (r != ALJABR_ROCM_OK) return r;
         return enqueue_add(y, tmp, static_cast<long long>(B) * N);
     };
-    // Bytes of one B-row NF4 product: weights once, activations in, outputs
-    // out (read too when added into).
-    auto mm_bytes = [&](long long N, long long K, bool add) {
-        return nf4_w(N, K, bs) + B * (K + N * (add ? 2.0 : 1.0)) * f4;
+    // Bytes of one B-row product: weights once, activations in, outputs out
+    // (read too when added into).
+    auto mm_bytes = [&](const T &t, long long N, long long K, bool add) {
+        return weight_bytes(t.type, N, K, bs) + B * (K + N * (add ? 2.0 : 1.0)) * f4;
     };
     const bool fused1 = B == 1 && m->rows_fused;
     hipLaunchKernelGGL(lengths_from_positions, dim3((B + 63) / 64), dim3(64), 0, s, m->kv_len, pos, B);
-    ALJ_TRY(enqueue_embed(m->x, static_cast<const float *>(m->tok_embed), tok, B, dim, c.vocab));
-    ALJ_MARK("embed", B * dim * 2.0 * f4);
+    if (m->tok_embed.type == ALJABR_ROCM_TYPE_F32)
+        ALJ_TRY(enqueue_embed(m->x, reinterpret_cast<const float *>(m->tok_embed.w), tok, B, dim, c.vocab));
+    else
+        ALJ_TRY(enqueue_embed_typed(m->x, m->tok_embed.w, m->tok_embed.type, tok, B, dim, c.vocab));
+    ALJ_MARK("embed", weight_bytes(m->tok_embed.type, B, dim, bs) + B * dim * f4);
     for (int l = 0; l < c.layers; ++l) {
-        auto W = [&](const std::vector<const void *> &t) { return static_cast<const uint8_t *>(t[l]); };
-        auto S = [&](const std::vector<const void *> &t) { return static_cast<const float *>(t[l]); };
+        auto W = [&](const std::vector<T> &t) { return t[l].w; };
+        auto S = [&](const std::vector<T> &t) { return t[l].s; };
+        const float *attn_norm = m->attn_norm[l], *ffn_norm = m->ffn_norm[l];
         uint16_t *kc = m->k_cache + l * layer_cache;
         uint16_t *vc = m->v_cache + l * layer_cache;
         // Attention block: xb = RMSNorm(x); q, k, v = Wq/Wk/Wv xb; RoPE on
         // q and k; k and v appended to the cache.
         if (fused1) {
-            const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq_s), qd},
-                                    {m->k, W(m->wk), S(m->wk_s), kvd},
-                                    {m->v, W(m->wv), S(m->wv_s), kvd}};
+            const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq), qd},
+                                    {m->k, W(m->wk), S(m->wk), kvd},
+                                    {m->v, W(m->wv), S(m->wv), kvd}};
             const RowsRope rope{pos, kc, vc, c.max_seq, hd, c.rope_base};
-            rc = enqueue_nf4_rows_fused(qkv, 3, m->x, S(m->attn_norm), c.eps, dim, shift, kRowsRopeKV, &rope);
+            rc = enqueue_nf4_rows_fused(qkv, 3, m->x, attn_norm, c.eps, dim, shift, kRowsRopeKV, &rope);
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {     // e.g. a head size that is not a power of two
-                ALJ_TRY(enqueue_nf4_rows_fused(qkv, 3, m->x, S(m->attn_norm), c.eps, dim, shift, kRowsStore));
+                ALJ_TRY(enqueue_nf4_rows_fused(qkv, 3, m->x, attn_norm, c.eps, dim, shift, kRowsStore));
                 ALJ_TRY(enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base));
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
@@ -312,22 +661,23 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             const ZeroList z{{m->q, m->k, m->v},
                              {static_cast<long long>(B) * qd, static_cast<long long>(B) * kvd,
                               static_cast<long long>(B) * kvd}};
-            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, S(m->attn_norm), B, dim, c.eps, &z));
+            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, attn_norm, B, dim, c.eps, m->all_nf4 ? &z : nullptr));
             ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * (qd + 2.0 * kvd)) * f4);
             // Q, K and V in one matrix-core launch where the shapes allow.
-            const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq_s), qd},
-                                    {m->k, W(m->wk), S(m->wk_s), kvd},
-                                    {m->v, W(m->wv), S(m->wv_s), kvd}};
-            rc = B >= 2 && B <= 64 ? enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, true)
-                                   : ALJABR_ROCM_ERR_UNSUPPORTED;
+            const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq), qd},
+                                    {m->k, W(m->wk), S(m->wk), kvd},
+                                    {m->v, W(m->wv), S(m->wv), kvd}};
+            rc = m->all_nf4 && B >= 2 && B <= 64 ? enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, true)
+                                                 : ALJABR_ROCM_ERR_UNSUPPORTED;
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
-                ALJ_TRY(mm(m->q, m->xb, m->wq[l], m->wq_s[l], dim, qd, false, nullptr));
-                ALJ_TRY(mm(m->k, m->xb, m->wk[l], m->wk_s[l], dim, kvd, false, nullptr));
-                ALJ_TRY(mm(m->v, m->xb, m->wv[l], m->wv_s[l], dim, kvd, false, nullptr));
+                ALJ_TRY(mm(m->q, m->xb, m->wq[l], dim, qd, false, nullptr));
+                ALJ_TRY(mm(m->k, m->xb, m->wk[l], dim, kvd, false, nullptr));
+                ALJ_TRY(mm(m->v, m->xb, m->wv[l], dim, kvd, false, nullptr));
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }
-            ALJ_MARK("qkv_gemm", mm_bytes(qd + 2LL * kvd, dim, true));
+            ALJ_MARK("qkv_gemm", mm_bytes(m->wq[l], qd, dim, true) + mm_bytes(m->wk[l], kvd, dim, true) +
+                                     mm_bytes(m->wv[l], kvd, dim, true) - 2.0 * B * dim * f4);
         }
         if (!fused1) {
             rc = enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base);
@@ -358,57 +708,57 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         ALJ_MARK("attention", keys * nkv * hd * 2.0 * 2.0 + B * 2.0 * qd * f4);
         // x += Wo att.
         if (fused1) {
-            const RowsOut o = {m->x, W(m->wo), S(m->wo_s), dim};
+            const RowsOut o = {m->x, W(m->wo), S(m->wo), dim};
             ALJ_TRY(enqueue_nf4_rows_fused(&o, 1, m->att, nullptr, 0.0f, qd, shift, kRowsAdd));
-            ALJ_MARK("wo_rows_add", mm_bytes(dim, qd, true));
+            ALJ_MARK("wo_rows_add", mm_bytes(m->wo[l], dim, qd, true));
         } else {
-            ALJ_TRY(mm(m->x, m->att, m->wo[l], m->wo_s[l], qd, dim, true, m->xb));
-            ALJ_MARK("wo_gemm_add", mm_bytes(dim, qd, true));
+            ALJ_TRY(mm(m->x, m->att, m->wo[l], qd, dim, true, m->xb));
+            ALJ_MARK("wo_gemm_add", mm_bytes(m->wo[l], dim, qd, true));
         }
         // MLP: x += Wdown (silu(Wgate xb) * Wup xb), xb = RMSNorm(x).
         if (fused1) {
-            const RowsOut gu[2] = {{m->hb, W(m->w_gate), S(m->w_gate_s), ffn},
-                                   {nullptr, W(m->w_up), S(m->w_up_s), ffn}};
-            rc = enqueue_nf4_rows_fused(gu, 2, m->x, S(m->ffn_norm), c.eps, dim, shift, kRowsSwiGLU);
+            const RowsOut gu[2] = {{m->hb, W(m->w_gate), S(m->w_gate), ffn},
+                                   {nullptr, W(m->w_up), S(m->w_up), ffn}};
+            rc = enqueue_nf4_rows_fused(gu, 2, m->x, ffn_norm, c.eps, dim, shift, kRowsSwiGLU);
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {     // row count the paired waves do not divide
-                const RowsOut gu2[2] = {{m->gate, W(m->w_gate), S(m->w_gate_s), ffn},
-                                        {m->up, W(m->w_up), S(m->w_up_s), ffn}};
-                ALJ_TRY(enqueue_nf4_rows_fused(gu2, 2, m->x, S(m->ffn_norm), c.eps, dim, shift, kRowsStore));
+                const RowsOut gu2[2] = {{m->gate, W(m->w_gate), S(m->w_gate), ffn},
+                                        {m->up, W(m->w_up), S(m->w_up), ffn}};
+                ALJ_TRY(enqueue_nf4_rows_fused(gu2, 2, m->x, ffn_norm, c.eps, dim, shift, kRowsStore));
                 ALJ_TRY(enqueue_swiglu(m->hb, m->gate, m->up, ffn));
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }
             ALJ_MARK("gate_up_rows_rmsnorm_swiglu", nf4_w(2LL * ffn, dim, bs) + (2.0 * dim + ffn) * f4);
-            const RowsOut d = {m->x, W(m->w_down), S(m->w_down_s), dim};
+            const RowsOut d = {m->x, W(m->w_down), S(m->w_down), dim};
             ALJ_TRY(enqueue_nf4_rows_fused(&d, 1, m->hb, nullptr, 0.0f, ffn, shift, kRowsAdd));
-            ALJ_MARK("down_rows_add", mm_bytes(dim, ffn, true));
+            ALJ_MARK("down_rows_add", mm_bytes(m->w_down[l], dim, ffn, true));
         } else {
             const ZeroList z{{m->gate, m->up, nullptr},
                              {static_cast<long long>(B) * ffn, static_cast<long long>(B) * ffn, 0}};
-            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, S(m->ffn_norm), B, dim, c.eps, &z));
+            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, ffn_norm, B, dim, c.eps, m->all_nf4 ? &z : nullptr));
             ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * 2.0 * ffn) * f4);
-            const RowsOut gu[2] = {{m->gate, W(m->w_gate), S(m->w_gate_s), ffn},
-                                   {m->up, W(m->w_up), S(m->w_up_s), ffn}};
-            rc = B >= 2 && B <= 64 ? enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, true)
-                                   : ALJABR_ROCM_ERR_UNSUPPORTED;
+            const RowsOut gu[2] = {{m->gate, W(m->w_gate), S(m->w_gate), ffn},
+                                   {m->up, W(m->w_up), S(m->w_up), ffn}};
+            rc = m->all_nf4 && B >= 2 && B <= 64 ? enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, true)
+                                                 : ALJABR_ROCM_ERR_UNSUPPORTED;
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
-                ALJ_TRY(mm(m->gate, m->xb, m->w_gate[l], m->w_gate_s[l], dim, ffn, false, nullptr));
-                ALJ_TRY(mm(m->up, m->xb, m->w_up[l], m->w_up_s[l], dim, ffn, false, nullptr));
+                ALJ_TRY(mm(m->gate, m->xb, m->w_gate[l], dim, ffn, false, nullptr));
+                ALJ_TRY(mm(m->up, m->xb, m->w_up[l], dim, ffn, false, nullptr));
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }
-            ALJ_MARK("gate_up_gemm", mm_bytes(2LL * ffn, dim, true));
+            ALJ_MARK("gate_up_gemm", mm_bytes(m->w_gate[l], ffn, dim, true) + mm_bytes(m->w_up[l], ffn, dim, true) -
+                                         B * dim * f4);
             ALJ_TRY(enqueue_swiglu(m->hb, m->gate, m->up, static_cast<long long>(B) * ffn));
             ALJ_MARK("swiglu", B * 3.0 * ffn * f4);
-            ALJ_TRY(mm(m->x, m->hb, m->w_down[l], m->w_down_s[l], ffn, dim, true, m->xb));
-            ALJ_MARK("down_gemm_add", mm_bytes(dim, ffn, true));
+            ALJ_TRY(mm(m->x, m->hb, m->w_down[l], ffn, dim, true, m->xb));
+            ALJ_MARK("down_gemm_add", mm_bytes(m->w_down[l], dim, ffn, true));
         }
     }
-    ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, static_cast<const float *>(m->out_norm), B, dim, c.eps));
+    ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, m->out_norm, B, dim, c.eps));
     ALJ_MARK("final_rmsnorm", (B * 2.0 * dim + dim) * f4);
-    ALJ_TRY(enqueue_matmul_gguf(lg, m->xb, static_cast<const uint8_t *>(m->lm_head), dim, c.vocab, ALJABR_ROCM_TYPE_F16,
-                                B));
-    ALJ_MARK("lm_head_f16", static_cast<double>(c.vocab) * dim * 2.0 + B * (static_cast<double>(dim) + c.vocab) * f4);
+    ALJ_TRY(enqueue_matmul_typed(lg, m->xb, m->lm_head.w, m->lm_head.s, m->lm_head.type, bs, dim, c.vocab, B));
+    ALJ_MARK(m->lm_head.type == ALJABR_ROCM_TYPE_F16 ? "lm_head_f16" : "lm_head", mm_bytes(m->lm_head, c.vocab, dim, false));
     ALJ_TRY(enqueue_argmax(next, lg, B, c.vocab));
     ALJ_MARK("argmax", B * static_cast<double>(c.vocab) * f4);
 #undef ALJ_MARK

@@ -12,9 +12,12 @@
 //         32-element sub-block; the min term sum_s dmin * m_s * sum(x in s)
 //         is one more MFMA pair per super-block, A = the split per-sub-block
 //         sums of x, B = the 6-bit min codes; then C += d * C_q - dmin * C_min.
-//   Q6_K  B = (q - 32) * scale (|.| <= 4096; exact below 2048, else rounded
-//         to an even integer, relative error <= 2^-11), one MFMA pair per
-//         16-element scale group; C += d * C_q.
+//   Q6_K  the int8 scale splits as sc = sl + (sc - sl), sl = sc & 15, so
+//         B_lo = (q - 32) * sl (|.| <= 480) and B_hi = (q - 32) * (sc - sl)
+//         (16 times an integer of |.| <= 256) are both exact in fp16; per
+//         16-element scale group x_hi meets B_lo and B_hi and x_lo their
+//         fp16 sum (whose rounding, 2^-12 of B, is scaled by x_lo ~ 2^-11 x);
+//         C += d * C_q.
 // Codes become fp16 integers with v_perm against a constant 0x64 byte: the
 // half 0x64qq is 1024 + qq exactly. Q4_K low nibbles give 1024 + q, high
 // nibbles (masked in place) 1024 + 16q, and one packed fp16 FMA removes the
@@ -97,21 +100,28 @@ __device__ __forceinline__ half8 fma_frag(uint32_t w0, uint32_t w1, uint32_t mul
     return __builtin_bit_cast(half8, r);
 }
 
-// Six-bit codes (one per byte of w0, w1) -> half8 of (q - 32) * scale.
-__device__ __forceinline__ half8 q6_frag(uint32_t w0, uint32_t w1, uint32_t sc2) {
+// Six-bit codes (one per byte of w0, w1) -> (q - 32) * sl, (q - 32) * sh16
+// (both exact) and their fp16 sum.
+__device__ __forceinline__ void q6_frags(uint32_t w0, uint32_t w1, uint32_t sl2, uint32_t sh2, half8 &blo, half8 &bhi,
+                                         half8 &bsum) {
     constexpr uint32_t kMinus1056 = 0xE420E420u;     // fp16 -1056 in both halves
     const uint32_t p[4] = {magic_pair<0>(w0), magic_pair<1>(w0), magic_pair<0>(w1), magic_pair<1>(w1)};
-    u32x4v r;
+    u32x4v lo, hi, sum;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const half2v v = __builtin_bit_cast(half2v, p[i]) + __builtin_bit_cast(half2v, kMinus1056);
-        r[i] = __builtin_bit_cast(uint32_t, v * __builtin_bit_cast(half2v, sc2));
+        const half2v a = v * __builtin_bit_cast(half2v, sl2), b = v * __builtin_bit_cast(half2v, sh2);
+        lo[i] = __builtin_bit_cast(uint32_t, a);
+        hi[i] = __builtin_bit_cast(uint32_t, b);
+        sum[i] = __builtin_bit_cast(uint32_t, a + b);
     }
-    return __builtin_bit_cast(half8, r);
+    blo = __builtin_bit_cast(half8, lo);
+    bhi = __builtin_bit_cast(half8, hi);
+    bsum = __builtin_bit_cast(half8, sum);
 }
 
 // fp16 bits of a small integer in both halves, times `mul` (a power of two).
-__device__ __forceinline__ uint32_t int_half2(uint32_t v, float mul) {
+__device__ __forceinline__ uint32_t int_half2(int v, float mul) {
     const _Float16 h = static_cast<_Float16>(static_cast<float>(v) * mul);
     const uint32_t b = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h));
     return b | (b << 16);
@@ -264,8 +274,10 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
                     sc1 = __builtin_amdgcn_ubfe(sw2, 16 * (c - 2) + 8, 4) |
                           (__builtin_amdgcn_ubfe(sw0, 16 * (c - 2) + 14, 2) << 4);
                 }
-                const uint32_t mul_lo = int_half2(sc0, 1.0f), add_lo = int_half2(sc0, -1024.0f);
-                const uint32_t mul_hi = int_half2(sc1, 0.0625f), add_hi = int_half2(sc1, -64.0f);
+                const uint32_t mul_lo = int_half2(static_cast<int>(sc0), 1.0f);
+                const uint32_t add_lo = int_half2(static_cast<int>(sc0), -1024.0f);
+                const uint32_t mul_hi = int_half2(static_cast<int>(sc1), 0.0625f);
+                const uint32_t add_hi = int_half2(static_cast<int>(sc1), -64.0f);
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const u32x2v b = *reinterpret_cast<const u32x2v *>(row + 16 + 32 * c + 16 * j + 8 * h);
@@ -326,11 +338,13 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
                     for (int q = 0; q < 4; ++q) {
                         const int g = 8 * H + 2 * q + l16;   // scale group of these 16 elements
                         const int sv = static_cast<int8_t>((scw[g >> 2] >> (8 * (g & 3))) & 0xffu);
-                        const _Float16 svh = static_cast<_Float16>(static_cast<float>(sv));
-                        const uint32_t sb = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, svh));
-                        const half8 bf = q6_frag(six[q][0], six[q][1], sb | (sb << 16));
-                        cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xrh + 16 * g), bf, cq, 0, 0, 0);
-                        cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xrl + 16 * g), bf, cq, 0, 0, 0);
+                        const int sl = sv & 15;
+                        half8 blo, bhi, bsum;
+                        q6_frags(six[q][0], six[q][1], int_half2(sl, 1.0f), int_half2(sv - sl, 1.0f), blo, bhi, bsum);
+                        const half8 ah = *reinterpret_cast<const half8 *>(xrh + 16 * g);
+                        cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, blo, cq, 0, 0, 0);
+                        cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bhi, cq, 0, 0, 0);
+                        cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xrl + 16 * g), bsum, cq, 0, 0, 0);
                     }
                 }
             }

@@ -341,6 +341,33 @@ __global__ __launch_bounds__(kThreads) void f16_matvec_generic_kernel(float *__r
     if (lane == 0) y[static_cast<size_t>(m) * N + n] = acc;
 }
 
+// fp32 weight rows (small GGUF models store some matrices unquantized): one
+// wave per (row, token), float4 loads when rows allow.
+__global__ __launch_bounds__(kThreads) void f32_matvec_kernel(float *__restrict__ y, const float *__restrict__ x,
+                                                              const float *__restrict__ w, int N, int K, int M,
+                                                              int vec4) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int task = (blockIdx.x * kThreads + threadIdx.x) / kWave;
+    if (task >= N * M) return;
+    const int n = task % N, m = task / N;
+    const float *wr = w + static_cast<size_t>(n) * K;
+    const float *xr = x + static_cast<size_t>(m) * K;
+    float acc = 0.0f;
+    if (vec4) {
+        for (int k = 4 * lane; k < K; k += 4 * kWave) {
+            const float4 a = *reinterpret_cast<const float4 *>(wr + k), b = *reinterpret_cast<const float4 *>(xr + k);
+            acc = fmaf(a.x, b.x, acc);
+            acc = fmaf(a.y, b.y, acc);
+            acc = fmaf(a.z, b.z, acc);
+            acc = fmaf(a.w, b.w, acc);
+        }
+    } else {
+        for (int k = lane; k < K; k += kWave) acc = fmaf(wr[k], xr[k], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[static_cast<size_t>(m) * N + n] = acc;
+}
+
 // ---------------------------------------------------------------------------
 // launch helpers
 // ---------------------------------------------------------------------------
@@ -509,6 +536,30 @@ int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N
         if (rc != ALJABR_ROCM_OK) return rc;
     }
     return ALJABR_ROCM_OK;
+}
+
+int enqueue_matmul_f32(float *C, const float *A, const float *W, int K, int N, int M) {
+    const long long tasks = static_cast<long long>(N) * M;
+    if (tasks > 0x7fffffffLL / 64) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    const int vec4 = K % 4 == 0 && aligned(A, 16) && aligned(W, 16);
+    hipLaunchKernelGGL(f32_matvec_kernel, dim3(grid_for(static_cast<int>(tasks))), dim3(kThreads), 0,
+                       current_stream(), C, A, W, N, K, M, vec4);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_matmul_typed(float *C, const float *A, const void *W, const float *absmax, int type, int bs, int K, int N,
+                         int M) {
+    const uint8_t *w = static_cast<const uint8_t *>(W);
+    switch (type) {
+    case ALJABR_ROCM_TYPE_NF4: return enqueue_matmul_nf4(C, A, w, absmax, K, N, bs, M);
+    case ALJABR_ROCM_TYPE_F32: return enqueue_matmul_f32(C, A, static_cast<const float *>(W), K, N, M);
+    case ALJABR_ROCM_TYPE_F16:
+    case ALJABR_ROCM_TYPE_Q4_0:
+    case ALJABR_ROCM_TYPE_Q8_0:
+    case ALJABR_ROCM_TYPE_Q4_K:
+    case ALJABR_ROCM_TYPE_Q6_K: return enqueue_matmul_gguf(C, A, w, K, N, type, M);
+    default: return ALJABR_ROCM_ERR_UNSUPPORTED;
+    }
 }
 
 }  // namespace aljabr

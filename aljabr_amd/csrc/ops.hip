@@ -8,6 +8,7 @@
 // in double here too.
 #include <cmath>
 
+#include "dequant.hpp"
 #include "device.hpp"
 #include "internal.hpp"
 #include "kernels.hpp"
@@ -278,6 +279,41 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(float *__restrict__ x, 
         x[static_cast<long long>(b) * dim + i] = embed[static_cast<long long>(t) * dim + i];
 }
 
+// One thread per 32 elements of row tokens[b]: a Q4_0 / Q8_0 block, a Q4_K
+// sub-block, two Q6_K scale groups, or 32 fp16 / fp32 values.
+__global__ __launch_bounds__(kThreads) void embed_typed_kernel(float *__restrict__ x, const uint8_t *__restrict__ table,
+                                                               int type, const int *__restrict__ tokens, int dim,
+                                                               int vocab, long long row_bytes) {
+    const int b = blockIdx.y;
+    const int u = blockIdx.x * kThreads + threadIdx.x;      // 32-element unit of the row
+    if (32 * u >= dim) return;
+    int t = tokens[b];
+    t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
+    const uint8_t *row = table + static_cast<long long>(t) * row_bytes;
+    float *o = x + static_cast<long long>(b) * dim + 32 * u;
+    switch (type) {
+    case ALJABR_ROCM_TYPE_Q4_0: dq_q4_0_block(row + 18LL * u, o); break;
+    case ALJABR_ROCM_TYPE_Q8_0: dq_q8_0_block(row + 34LL * u, o); break;
+    case ALJABR_ROCM_TYPE_Q4_K: dq_q4_k_sub(row + 144LL * (u >> 3), u & 7, o); break;
+    case ALJABR_ROCM_TYPE_Q6_K:
+        dq_q6_k_group(row + 210LL * (u >> 3), 2 * (u & 7), o);
+        dq_q6_k_group(row + 210LL * (u >> 3), 2 * (u & 7) + 1, o + 16);
+        break;
+    case ALJABR_ROCM_TYPE_F16: {
+        const uint16_t *h = reinterpret_cast<const uint16_t *>(row) + 32 * u;
+        const int n = dim - 32 * u < 32 ? dim - 32 * u : 32;
+        for (int i = 0; i < n; ++i) o[i] = f16_bits_to_f32_exact(h[i]);
+        break;
+    }
+    default: {
+        const float *f = reinterpret_cast<const float *>(row) + 32 * u;
+        const int n = dim - 32 * u < 32 ? dim - 32 * u : 32;
+        for (int i = 0; i < n; ++i) o[i] = f[i];
+        break;
+    }
+    }
+}
+
 // cache[b][h][pos[b]][d] = fp16(src[b][h*D + d]) (round to nearest even).
 __global__ __launch_bounds__(kThreads) void kv_append_kernel(uint16_t *__restrict__ cache, const float *__restrict__ src,
                                                              const int *__restrict__ pos, int n_kv, int head_dim,
@@ -335,6 +371,25 @@ int enqueue_argmax(int *out, const float *x, int rows, int cols) {
 int enqueue_embed(float *x, const float *embed, const int *tokens, int batch, int dim, int vocab) {
     const unsigned gx = static_cast<unsigned>((dim + kThreads - 1) / kThreads);
     hipLaunchKernelGGL(embed_kernel, dim3(gx, batch), dim3(kThreads), 0, current_stream(), x, embed, tokens, dim, vocab);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_embed_typed(float *x, const void *table, int type, const int *tokens, int batch, int dim, int vocab) {
+    long long row_bytes;
+    switch (type) {
+    case ALJABR_ROCM_TYPE_F32: row_bytes = 4LL * dim; break;
+    case ALJABR_ROCM_TYPE_F16: row_bytes = 2LL * dim; break;
+    case ALJABR_ROCM_TYPE_Q4_0: row_bytes = dim % 32 ? -1 : dim / 32 * 18LL; break;
+    case ALJABR_ROCM_TYPE_Q8_0: row_bytes = dim % 32 ? -1 : dim / 32 * 34LL; break;
+    case ALJABR_ROCM_TYPE_Q4_K: row_bytes = dim % 256 ? -1 : dim / 256 * 144LL; break;
+    case ALJABR_ROCM_TYPE_Q6_K: row_bytes = dim % 256 ? -1 : dim / 256 * 210LL; break;
+    default: row_bytes = -1; break;
+    }
+    if (row_bytes < 0) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    const int units = (dim + 31) / 32;
+    const unsigned gx = static_cast<unsigned>((units + kThreads - 1) / kThreads);
+    hipLaunchKernelGGL(embed_typed_kernel, dim3(gx, batch), dim3(kThreads), 0, current_stream(), x,
+                       static_cast<const uint8_t *>(table), type, tokens, dim, vocab, row_bytes);
     return ALJABR_ROCM_OK;
 }
 

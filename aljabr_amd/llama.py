@@ -111,6 +111,62 @@ class DeviceLlama:
         self.handle = handle
         self.max_batch, self.max_seq = max_batch, max_seq
 
+    @classmethod
+    def _wrap(cls, handle, cfg: dict, max_batch: int, max_seq: int, keep):
+        self = cls.__new__(cls)
+        self.cfg, self.weights, self._tables = dict(cfg), keep, []
+        self.handle, self.max_batch, self.max_seq = handle, max_batch, max_seq
+        return self
+
+    @classmethod
+    def from_gguf(cls, path: str, max_batch: int, max_seq: int = 0):
+        """A session over a Llama-family GGUF file (aljabr_rocm_llama_create_gguf):
+        the library uploads the file's tensors once and owns them."""
+        lib = abi.load()
+        handle = ctypes.c_void_p()
+        abi.check(lib.aljabr_rocm_llama_create_gguf(path.encode(), max_batch, max_seq, ctypes.byref(handle)),
+                  "aljabr_rocm_llama_create_gguf")
+        c = abi.LlamaConfig()
+        abi.check(lib.aljabr_rocm_llama_config_get(handle, ctypes.byref(c)), "aljabr_rocm_llama_config_get")
+        cfg = {name: getattr(c, name) for name, _ in abi.LlamaConfig._fields_}
+        return cls._wrap(handle, cfg, max_batch, c.max_seq, None)
+
+    @classmethod
+    def typed(cls, cfg: dict, weights: dict, max_batch: int, max_seq: int):
+        """A session over typed device weights (aljabr_rocm_llama_create_typed):
+        tok_embed and lm_head are (type, tensor) pairs, the PROJ lists hold
+        (type, tensor) or, for NF4, (TYPE_NF4, (codes, absmax)); attn_norm and
+        ffn_norm are lists of fp32 tensors, out_norm an fp32 tensor."""
+        lib = abi.load()
+        c = abi.LlamaConfig(cfg["layers"], cfg["dim"], cfg["ffn"], cfg["n_heads"], cfg["n_kv_heads"],
+                            cfg["head_dim"], cfg["vocab"], max_seq, cfg.get("nf4_block", 64), max_batch,
+                            cfg["rope_base"], cfg["eps"])
+        keep = []
+
+        def tensor(pair):
+            t, data = pair
+            if t == abi.TYPE_NF4:
+                codes, absmax = data
+                return abi.Tensor(codes.data_ptr(), absmax.data_ptr(), t, cfg.get("nf4_block", 64))
+            return abi.Tensor(data.data_ptr(), None, t, 0)
+
+        w = abi.LlamaTensors()
+        w.tok_embed = tensor(weights["tok_embed"])
+        w.lm_head = tensor(weights["lm_head"])
+        w.out_norm = weights["out_norm"].data_ptr()
+        for key in ("attn_norm", "ffn_norm"):
+            tab = (ctypes.c_void_p * cfg["layers"])(*[t.data_ptr() for t in weights[key]])
+            keep.append(tab)
+            setattr(w, key, ctypes.cast(tab, ctypes.POINTER(ctypes.c_void_p)))
+        for key in PROJ:
+            tab = (abi.Tensor * cfg["layers"])(*[tensor(p) for p in weights[key]])
+            keep.append(tab)
+            setattr(w, key, ctypes.cast(tab, ctypes.POINTER(abi.Tensor)))
+        handle = ctypes.c_void_p()
+        abi.check(lib.aljabr_rocm_llama_create_typed(ctypes.byref(c), ctypes.byref(w), ctypes.byref(handle)),
+                  "aljabr_rocm_llama_create_typed")
+        return cls._wrap(handle, dict(cfg, max_seq=max_seq), max_batch, max_seq, (weights, keep))
+
     def decode(self, tokens, positions, batch: int, logits=None, next_tokens=None):
         """tokens/positions: int32 device tensors; returns next_tokens (int32 device)."""
         import torch

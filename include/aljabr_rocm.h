@@ -279,6 +279,80 @@ int aljabr_rocm_llama_destroy(aljabr_rocm_llama *model);
 int aljabr_rocm_llama_decode(aljabr_rocm_llama *model, const void *tokens,
                              const void *positions, int batch, void *logits,
                              void *next_tokens);
+/* One weight tensor of a typed session: device data and its
+ * ALJABR_ROCM_TYPE_*; for NF4 also the fp32 absmax array and block size (0 or
+ * the config's nf4_block). Rows of K elements must be whole blocks of the
+ * type (32 for Q4_0/Q8_0, 256 for Q4_K/Q6_K). */
+typedef struct aljabr_rocm_tensor {
+    const void *data;
+    const void *absmax;
+    int32_t type;
+    int32_t block_size;
+} aljabr_rocm_tensor;
+
+/* Weights of a typed session (the GGUF runner's per-tensor types, e.g. a
+ * Q4_K_M file: Q4_K projections with Q6_K attn_v/ffn_down/output). Per-layer
+ * arrays are HOST arrays of `layers` entries; norms are fp32 device vectors.
+ * tok_embed: F32, F16, Q4_0, Q8_0, Q4_K or Q6_K; projections and lm_head:
+ * those or NF4. */
+typedef struct aljabr_rocm_llama_tensors {
+    aljabr_rocm_tensor tok_embed;                       /* [vocab, dim] */
+    const void *const *attn_norm, *const *ffn_norm;     /* [dim] fp32 */
+    const aljabr_rocm_tensor *wq, *wk, *wv, *wo;        /* [n_heads*head_dim|n_kv*head_dim, dim], [dim, n_heads*head_dim] */
+    const aljabr_rocm_tensor *w_gate, *w_up, *w_down;   /* [ffn, dim], [ffn, dim], [dim, ffn] */
+    const void *out_norm;                               /* [dim] fp32 */
+    aljabr_rocm_tensor lm_head;                         /* [vocab, dim] */
+} aljabr_rocm_llama_tensors;
+
+/* A decode session over typed weights (any mix per matrix), the GGUF decode
+ * runner's contract (GgufDecodePass over per-tensor GgmlTypes,
+ * engine/gguf/aljabr-gguf-java/.../GgufDecodePass.java:183-592, registered the
+ * way aljabr_metal_register_decode_layer takes per-matrix types,
+ * MTLC/aljabr_metal_matvec_api.h:244-282). All-NF4 weights take the same fused
+ * paths as aljabr_rocm_llama_create. Weights stay owned by the caller; every
+ * decode entry point below accepts the session. */
+int aljabr_rocm_llama_create_typed(const aljabr_rocm_llama_config *cfg,
+                                   const aljabr_rocm_llama_tensors *w,
+                                   aljabr_rocm_llama **out);
+
+/* ---- GGUF files ---------------------------------------------------------- */
+
+/* A GGUF file mapped read-only and parsed (header, metadata, tensor table),
+ * as the reference's GGUFParser reads it (engine/gguf/aljabr-gguf-core/.../
+ * loader/GGUFParser.java:18-63): versions 2 and 3, data at general.alignment
+ * (default 32). Host only: needs no device and no aljabr_rocm_init. Malformed
+ * or truncated files give -2, tensor types it cannot size -3. */
+typedef struct aljabr_rocm_gguf aljabr_rocm_gguf;
+int aljabr_rocm_gguf_open(const char *path, aljabr_rocm_gguf **out);
+int aljabr_rocm_gguf_close(aljabr_rocm_gguf *g);
+int aljabr_rocm_gguf_tensor_count(const aljabr_rocm_gguf *g, int64_t *n);
+int aljabr_rocm_gguf_find_tensor(const aljabr_rocm_gguf *g, const char *name, int64_t *index);
+/* dims[4] in GGUF order (dims[0] = row length); offset from the file start. */
+int aljabr_rocm_gguf_tensor_info(const aljabr_rocm_gguf *g, int64_t index, char *name, int name_cap,
+                                 int32_t *type, int32_t *n_dims, int64_t *dims, uint64_t *offset,
+                                 uint64_t *bytes);
+/* Host pointer into the mapping (valid until aljabr_rocm_gguf_close). */
+int aljabr_rocm_gguf_tensor_data(const aljabr_rocm_gguf *g, int64_t index, const void **host_data);
+/* Metadata by key: integers and bools (arrays: their length), numbers, strings. */
+int aljabr_rocm_gguf_meta_int(const aljabr_rocm_gguf *g, const char *key, int64_t *value);
+int aljabr_rocm_gguf_meta_float(const aljabr_rocm_gguf *g, const char *key, double *value);
+int aljabr_rocm_gguf_meta_string(const aljabr_rocm_gguf *g, const char *key, char *buf, int cap);
+
+/* A typed decode session from a Llama-family GGUF file: the configuration
+ * from {arch}.block_count / embedding_length / feed_forward_length /
+ * attention.head_count(_kv) / attention.key_length / rope.freq_base /
+ * attention.layer_norm_rms_epsilon (max_seq <= 0: {arch}.context_length), the
+ * tensors token_embd, blk.N.{attn_norm, attn_q, attn_k, attn_v, attn_output,
+ * ffn_norm, ffn_gate, ffn_up, ffn_down}, output_norm and output (absent: tied
+ * to token_embd), uploaded once into device memory the session owns. The
+ * reference path: GgufLayerWeightResolver.java:20-110 names, the Metal bridge's
+ * upload-once registration (GgufMetalBridge.java:701-749). Files with
+ * per-head norms, post norms, RoPE frequency tensors, partial RoPE or biases
+ * give -3: the step does not apply them. */
+int aljabr_rocm_llama_create_gguf(const char *path, int max_batch, int max_seq, aljabr_rocm_llama **out);
+/* The session's configuration (e.g. of a session made from a file). */
+int aljabr_rocm_llama_config_get(const aljabr_rocm_llama *m, aljabr_rocm_llama_config *cfg);
+
 /* aljabr_rocm_llama_decode replayed from a HIP graph of the whole step: the
  * first call for a batch size (and logits buffer) runs the step and captures
  * it; later calls copy tokens and positions into the session, replay the

@@ -87,6 +87,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "orc_swiglu": (None, [_P, _P, _P, _I32]),
         "orc_softmax": (None, [_P, _I32]),
         "orc_llama_decode": (_I32, [_P, _P, _I32, _I32, _P, _P, _P, _P, ctypes.c_int]),
+        "orc_llama_decode_typed": (_I32, [_P, _P, _I32, _I32, _P, _P, _P, _P, ctypes.c_int]),
         "orc_fill_normal": (None, [ctypes.c_uint64, _F, _F, _P, _I64]),
         "orc_fill_uniform_int": (None, [ctypes.c_uint64, _I32, _P, _I64]),
         "orc_max_threads": (ctypes.c_int, []),
@@ -389,4 +390,69 @@ class LlamaOracle:
         nxt = lib().orc_llama_decode(ctypes.byref(self.cfg), ctypes.byref(self.weights), token, pos,
                                      _ptr(self.k_cache), _ptr(self.v_cache), _ptr(logits), _ptr(hidden),
                                      nthreads or threads())
+        return int(nxt), logits, hidden
+
+
+class _Tensor(ctypes.Structure):
+    _fields_ = [("data", _VP), ("absmax", _VP), ("type", ctypes.c_int32), ("group", ctypes.c_int32)]
+
+
+class _LlamaTyped(ctypes.Structure):
+    _fields_ = [("tok_embed", _Tensor), ("attn_norm", _VP), ("ffn_norm", _VP),
+                ("wq", _VP), ("wk", _VP), ("wv", _VP), ("wo", _VP),
+                ("w_gate", _VP), ("w_up", _VP), ("w_down", _VP),
+                ("out_norm", _VP), ("lm_head", _Tensor)]
+
+
+class TypedLlamaOracle:
+    """Single-sequence decode over per-tensor types (GgufDecodePass over GGUF
+    GgmlTypes, restated): ``weights`` maps tok_embed, lm_head and the
+    per-layer lists wq, wk, wv, wo, w_gate, w_up, w_down to (type, array)
+    pairs (type ids as ALJABR_ROCM_TYPE_*: 0 F32, 1 F16 (uint16 bits), 2 Q4_0,
+    8 Q8_0, 12 Q4_K, 14 Q6_K (bytes)) and attn_norm, ffn_norm (lists) and
+    out_norm to fp32 arrays."""
+
+    MATS = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+
+    def __init__(self, cfg: dict, weights: dict, kv_f16: bool = True):
+        self.cfg = _LlamaCfg(cfg["layers"], cfg["dim"], cfg["ffn"], cfg["n_heads"], cfg["n_kv_heads"],
+                             cfg["head_dim"], cfg["vocab"], cfg["max_seq"], cfg.get("nf4_block", 64), int(kv_f16),
+                             cfg["rope_base"], cfg["eps"])
+        self._keep = []
+
+        def tensor(pair):
+            t, arr = pair
+            arr = np.ascontiguousarray(arr)
+            self._keep.append(arr)
+            return _Tensor(arr.ctypes.data, None, t, 0)
+
+        def table(arrs, ctype):
+            tab = (ctype * len(arrs))(*arrs)
+            self._keep.append(tab)
+            return ctypes.cast(tab, ctypes.c_void_p).value
+
+        w = _LlamaTyped()
+        w.tok_embed = tensor(weights["tok_embed"])
+        w.lm_head = tensor(weights["lm_head"])
+        norm = np.ascontiguousarray(weights["out_norm"], np.float32)
+        self._keep.append(norm)
+        w.out_norm = norm.ctypes.data
+        for key in ("attn_norm", "ffn_norm"):
+            arrs = [np.ascontiguousarray(a, np.float32) for a in weights[key]]
+            self._keep.extend(arrs)
+            setattr(w, key, table([a.ctypes.data for a in arrs], ctypes.c_void_p))
+        for key in self.MATS:
+            setattr(w, key, table([tensor(p) for p in weights[key]], _Tensor))
+        self.weights = w
+        kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+        self.k_cache = np.zeros(cfg["layers"] * cfg["max_seq"] * kvd, np.float32)
+        self.v_cache = np.zeros_like(self.k_cache)
+        self.dim, self.vocab = cfg["dim"], cfg["vocab"]
+
+    def decode(self, token: int, pos: int, nthreads: int | None = None):
+        logits = np.empty(self.vocab, np.float32)
+        hidden = np.empty(self.dim, np.float32)
+        nxt = lib().orc_llama_decode_typed(ctypes.byref(self.cfg), ctypes.byref(self.weights), token, pos,
+                                           _ptr(self.k_cache), _ptr(self.v_cache), _ptr(logits), _ptr(hidden),
+                                           nthreads or threads())
         return int(nxt), logits, hidden

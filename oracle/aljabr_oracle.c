@@ -818,33 +818,60 @@ void orc_softmax(float *a, int32_t len) {
 /* Llama-shaped decode step                                                  */
 /* ------------------------------------------------------------------------ */
 
-static void nf4_mv(const uint8_t *codes, const float *absmax, int32_t group, const float *x,
-                   int64_t n, int64_t k, float *y, int threads) {
-    orc_nf4_matvec(codes, absmax, group, x, n, k, 1, y, threads);
+/* y[n] = sum_k W[n][k] x[k] for one typed matrix (GgufDecodePass's per-type
+ * row dots: GRT/GgufMatVec.java:27-97 dispatching on the GgmlType). */
+static void typed_mv(const orc_tensor *t, const float *x, int64_t n, int64_t k, float *y, int threads) {
+    switch (t->type) {
+    case 100: orc_nf4_matvec((const uint8_t *)t->data, t->absmax, t->group, x, n, k, 1, y, threads); break;
+    case 2: orc_q4_0_matvec((const uint8_t *)t->data, x, n, k, 1, y, threads); break;
+    case 8: orc_q8_0_matvec((const uint8_t *)t->data, x, n, k, 1, y, threads); break;
+    case 12: orc_q4_k_matvec((const uint8_t *)t->data, x, n, k, 1, y, threads); break;
+    case 14: orc_q6_k_matvec((const uint8_t *)t->data, x, n, k, 1, y, threads); break;
+    case 1: orc_f16_matvec((const uint16_t *)t->data, x, n, k, 1, y, threads); break;
+    default: {                                   /* F32 rows */
+        const float *w = (const float *)t->data;
+        for (int64_t r = 0; r < n; r++) y[r] = dot16(w + r * k, x, k);
+        break;
+    }
+    }
 }
 
-/* GJB/GgufDecodePass.java:297-505 (per-op path, no optional norms/scales),
- * GJB/GgufDecodeAttentionExecution.java:70-106 (per-head two-pass softmax),
- * GJB/GgufLogitsProcessor.java:26-48 (final norm + LM head, no soft-cap). */
-int32_t orc_llama_decode(const orc_llama_cfg *cfg, const orc_llama_weights *w,
-                         int32_t token, int32_t pos, float *k_cache,
-                         float *v_cache, float *logits, float *hidden,
-                         int threads) {
+/* Row `row` of a typed [rows][dim] table decoded to fp32 (the embedding
+ * lookup: GgufDecodeStep's token_embd row dequantization). */
+static void typed_row(const orc_tensor *t, int64_t row, int64_t dim, float *out) {
+    switch (t->type) {
+    case 1: {
+        const uint16_t *h = (const uint16_t *)t->data + row * dim;
+        for (int64_t i = 0; i < dim; i++) out[i] = orc_f16_to_f32(h[i]);
+        break;
+    }
+    case 2: orc_q4_0_dequant((const uint8_t *)t->data + row * (dim / 32) * 18, dim, out); break;
+    case 8: orc_q8_0_dequant((const uint8_t *)t->data + row * (dim / 32) * 34, dim, out); break;
+    case 12: orc_q4_k_dequant((const uint8_t *)t->data + row * (dim / 256) * 144, dim, out); break;
+    case 14: orc_q6_k_dequant((const uint8_t *)t->data + row * (dim / 256) * 210, dim, out); break;
+    default: memcpy(out, (const float *)t->data + row * dim, (size_t)dim * 4); break;
+    }
+}
+
+int32_t orc_llama_decode_typed(const orc_llama_cfg *cfg, const orc_llama_typed *w,
+                               int32_t token, int32_t pos, float *k_cache,
+                               float *v_cache, float *logits, float *hidden,
+                               int threads) {
     const int32_t dim = cfg->dim, hd = cfg->head_dim, nh = cfg->n_heads, nkv = cfg->n_kv_heads;
-    const int32_t kvd = nkv * hd, qd = nh * hd, ffn = cfg->ffn, g = cfg->nf4_group;
+    const int32_t kvd = nkv * hd, qd = nh * hd, ffn = cfg->ffn;
     float *x = hidden;
     float *xb = (float *)malloc((size_t)dim * 4), *q = (float *)malloc((size_t)qd * 4);
     float *kk = (float *)malloc((size_t)kvd * 4), *vv = (float *)malloc((size_t)kvd * 4);
     float *att = (float *)malloc((size_t)qd * 4), *scores = (float *)malloc((size_t)(pos + 1) * 4);
     float *gate = (float *)malloc((size_t)ffn * 4), *up = (float *)malloc((size_t)ffn * 4);
     float *hb = (float *)malloc((size_t)ffn * 4);
-    memcpy(x, w->tok_embed + (int64_t)token * dim, (size_t)dim * 4);
+    typed_row(&w->tok_embed, token, dim, x);
     float scale = (float)(1.0 / sqrt((double)hd));
     for (int32_t l = 0; l < cfg->layers; l++) {
         orc_rmsnorm(x, w->attn_norm[l], xb, dim, cfg->eps);
-        nf4_mv(w->wq[l], w->wq_s[l], g, xb, qd, dim, q, threads);
-        nf4_mv(w->wk[l], w->wk_s[l], g, xb, kvd, dim, kk, threads);
-        nf4_mv(w->wv[l], w->wv_s[l], g, xb, kvd, dim, vv, threads);
+        typed_mv(&w->wq[l], xb, qd, dim, q, threads);
+        typed_mv(&w->wk[l], xb, kvd, dim, kk, threads);
+        typed_mv(&w->wv[l], xb, kvd, dim, vv, threads);
         orc_rope(q, nh, hd, pos, cfg->rope_base);
         orc_rope(kk, nkv, hd, pos, cfg->rope_base);
         float *kc = k_cache + (int64_t)l * cfg->max_seq * kvd;
@@ -866,24 +893,53 @@ int32_t orc_llama_decode(const orc_llama_cfg *cfg, const orc_llama_weights *w,
                 for (int32_t j = 0; j < hd; j++) o[j] += scores[p] * vr[j];
             }
         }
-        nf4_mv(w->wo[l], w->wo_s[l], g, att, dim, qd, xb, threads);
+        typed_mv(&w->wo[l], att, dim, qd, xb, threads);
         for (int32_t j = 0; j < dim; j++) x[j] += xb[j];
         orc_rmsnorm(x, w->ffn_norm[l], xb, dim, cfg->eps);
-        nf4_mv(w->w_gate[l], w->w_gate_s[l], g, xb, ffn, dim, gate, threads);
-        nf4_mv(w->w_up[l], w->w_up_s[l], g, xb, ffn, dim, up, threads);
+        typed_mv(&w->w_gate[l], xb, ffn, dim, gate, threads);
+        typed_mv(&w->w_up[l], xb, ffn, dim, up, threads);
         orc_swiglu(gate, up, hb, ffn);
-        nf4_mv(w->w_down[l], w->w_down_s[l], g, hb, dim, ffn, xb, threads);
+        typed_mv(&w->w_down[l], hb, dim, ffn, xb, threads);
         for (int32_t j = 0; j < dim; j++) x[j] += xb[j];
     }
     orc_rmsnorm(x, w->out_norm, xb, dim, cfg->eps);
-    orc_f16_matvec(w->lm_head, xb, cfg->vocab, dim, 1, logits, threads);
+    typed_mv(&w->lm_head, xb, cfg->vocab, dim, logits, threads);
     int32_t best = 0;
     for (int32_t i = 1; i < cfg->vocab; i++) if (logits[i] > logits[best]) best = i;
     free(xb); free(q); free(kk); free(vv); free(att); free(scores); free(gate); free(up); free(hb);
     return best;
 }
 
-/* IEEE binary16 round-to-nearest-even, returned widened to binary32. */
+/* The NF4 layout (fp32 embedding, NF4 projections, fp16 LM head) through the
+ * typed step. */
+int32_t orc_llama_decode(const orc_llama_cfg *cfg, const orc_llama_weights *w,
+                         int32_t token, int32_t pos, float *k_cache,
+                         float *v_cache, float *logits, float *hidden,
+                         int threads) {
+    const int32_t L = cfg->layers, g = cfg->nf4_group;
+    orc_tensor *t = (orc_tensor *)malloc(sizeof(orc_tensor) * 7 * (size_t)L);
+    for (int32_t l = 0; l < L; l++) {
+        const orc_tensor q = {w->wq[l], w->wq_s[l], 100, g}, k = {w->wk[l], w->wk_s[l], 100, g};
+        const orc_tensor v = {w->wv[l], w->wv_s[l], 100, g}, o = {w->wo[l], w->wo_s[l], 100, g};
+        const orc_tensor ga = {w->w_gate[l], w->w_gate_s[l], 100, g}, u = {w->w_up[l], w->w_up_s[l], 100, g};
+        const orc_tensor d = {w->w_down[l], w->w_down_s[l], 100, g};
+        t[0 * L + l] = q; t[1 * L + l] = k; t[2 * L + l] = v; t[3 * L + l] = o;
+        t[4 * L + l] = ga; t[5 * L + l] = u; t[6 * L + l] = d;
+    }
+    orc_llama_typed tw;
+    const orc_tensor emb = {w->tok_embed, NULL, 0, 0}, lm = {w->lm_head, NULL, 1, 0};
+    tw.tok_embed = emb;
+    tw.attn_norm = w->attn_norm;
+    tw.ffn_norm = w->ffn_norm;
+    tw.wq = t; tw.wk = t + L; tw.wv = t + 2 * L; tw.wo = t + 3 * L;
+    tw.w_gate = t + 4 * L; tw.w_up = t + 5 * L; tw.w_down = t + 6 * L;
+    tw.out_norm = w->out_norm;
+    tw.lm_head = lm;
+    const int32_t r = orc_llama_decode_typed(cfg, &tw, token, pos, k_cache, v_cache, logits, hidden, threads);
+    free(t);
+    return r;
+}
+
 float orc_round_f16(float v) {
     uint32_t b = f32_to_bits(v);
     uint32_t sign = b & 0x80000000u;

@@ -185,6 +185,30 @@ int32_t orc_llama_decode(const orc_llama_cfg *cfg, const orc_llama_weights *w,
                          float *v_cache, float *logits, float *hidden,
                          int threads);
 
+/* One weight tensor of a typed model: data, type (0 F32, 1 F16, 2 Q4_0,
+ * 8 Q8_0, 12 Q4_K, 14 Q6_K, 100 NF4 with absmax and group). */
+typedef struct orc_tensor {
+    const void *data;
+    const float *absmax;
+    int32_t type;
+    int32_t group;
+} orc_tensor;
+typedef struct orc_llama_typed {
+    orc_tensor tok_embed;
+    const float *const *attn_norm, *const *ffn_norm;
+    const orc_tensor *wq, *wk, *wv, *wo, *w_gate, *w_up, *w_down;
+    const float *out_norm;
+    orc_tensor lm_head;
+} orc_llama_typed;
+/* GJB/GgufDecodePass.java:183-592 over per-tensor GGUF types: the same step
+ * as orc_llama_decode (which runs through it) with each matvec dispatched on
+ * its type and the embedding row decoded from its type. Pinned through the
+ * per-type matvec and dequant checks and the NF4 decode tests. */
+int32_t orc_llama_decode_typed(const orc_llama_cfg *cfg, const orc_llama_typed *w,
+                               int32_t token, int32_t pos, float *k_cache,
+                               float *v_cache, float *logits, float *hidden,
+                               int threads);
+
 /* binary32 -> binary16 -> binary32 with round-to-nearest-even (IEEE). */
 float orc_round_f16(float v);
 
