@@ -95,6 +95,10 @@ constexpr int kRowsRopeKV = 3;   // outs = {q, k, v}: q rotated into outs[0].y; 
 // enqueued) outside them.
 int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
                            int bs_shift, int epilogue, const RowsRope *rope = nullptr);
+// The same for one weight type shared by the segments: NF4, Q4_0, Q8_0, Q4_K
+// or Q6_K (absmax and bs_shift for NF4 only).
+int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
+                       int bs_shift, int epilogue, const RowsRope *rope = nullptr);
 // NF4 small-M GEMM on MFMA (2 <= M <= 64, K % 512 == 0, block size 64). With
 // `accumulate` the products are added to C as it is (C += A . W^T), so a
 // caller that has C cleared or holding a residual saves the clearing launch.

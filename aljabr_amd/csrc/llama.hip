@@ -266,11 +266,19 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
     m->attn_scratch_bytes = attention_scratch_bytes(c.max_batch, c.n_heads, 1, c.head_dim, c.max_seq);
     m->attn_scratch = carve<float>(cur, m->attn_scratch_bytes / sizeof(float));
     m->graphs.resize(static_cast<size_t>(c.max_batch) + 1);
-    // Batch-1 NF4 fusion needs every K a multiple of 2048 (at most 16384), a
-    // power-of-two block of at least 32 and 16-byte aligned weights and norms.
+    // Batch-1 fusion (the rows kernels: NF4, Q4_0, Q8_0, Q4_K, Q6_K) needs
+    // every K a multiple of 2048 (at most 16384), for NF4 a power-of-two block
+    // of at least 32, and 16-byte aligned weights and norms.
     const int shift = log2_exact(c.nf4_block);
     auto k_ok = [](int k) { return k % 2048 == 0 && k / 2048 >= 1 && k / 2048 <= 8; };
-    bool fused = m->all_nf4 && k_ok(c.dim) && k_ok(qd_i) && k_ok(c.ffn) && shift >= 5;
+    auto rows_type = [&](int t) {
+        return (t == ALJABR_ROCM_TYPE_NF4 && shift >= 5) || t == ALJABR_ROCM_TYPE_Q4_0 || t == ALJABR_ROCM_TYPE_Q8_0 ||
+               t == ALJABR_ROCM_TYPE_Q4_K || t == ALJABR_ROCM_TYPE_Q6_K;
+    };
+    bool fused = k_ok(c.dim) && k_ok(qd_i) && k_ok(c.ffn);
+    for (int l = 0; l < L && fused; ++l)
+        for (const auto *t : {&m->wq, &m->wk, &m->wv, &m->wo, &m->w_gate, &m->w_up, &m->w_down})
+            fused = fused && rows_type((*t)[l].type);
     for (int l = 0; l < L && fused; ++l) {
         fused = aligned(m->attn_norm[l], 16) && aligned(m->ffn_norm[l], 16);
         for (const auto *t : {&m->wq, &m->wk, &m->wv, &m->wo, &m->w_gate, &m->w_up, &m->w_down})
@@ -647,16 +655,29 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq), qd},
                                     {m->k, W(m->wk), S(m->wk), kvd},
                                     {m->v, W(m->wv), S(m->wv), kvd}};
+            const int tq = m->wq[l].type, tk = m->wk[l].type, tv = m->wv[l].type;
             const RowsRope rope{pos, kc, vc, c.max_seq, hd, c.rope_base};
-            rc = enqueue_nf4_rows_fused(qkv, 3, m->x, attn_norm, c.eps, dim, shift, kRowsRopeKV, &rope);
-            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {     // e.g. a head size that is not a power of two
-                ALJ_TRY(enqueue_nf4_rows_fused(qkv, 3, m->x, attn_norm, c.eps, dim, shift, kRowsStore));
+            rc = tq == tk && tk == tv
+                     ? enqueue_rows_fused(tq, qkv, 3, m->x, attn_norm, c.eps, dim, shift, kRowsRopeKV, &rope)
+                     : ALJABR_ROCM_ERR_UNSUPPORTED;
+            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                // Mixed types (a Q6_K attn_v beside Q4_K q and k) or a head
+                // size the epilogue does not take: consecutive matrices of one
+                // type per launch, then RoPE and the append.
+                const int types[3] = {tq, tk, tv};
+                for (int i = 0; i < 3;) {
+                    int j = i + 1;
+                    while (j < 3 && types[j] == types[i]) ++j;
+                    ALJ_TRY(enqueue_rows_fused(types[i], qkv + i, j - i, m->x, attn_norm, c.eps, dim, shift, kRowsStore));
+                    i = j;
+                }
                 ALJ_TRY(enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base));
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }
             ALJ_MARK("qkv_rows_rmsnorm_rope_append",
-                     nf4_w(qd + 2LL * kvd, dim, bs) + (2.0 * dim + qd) * f4 + 2.0 * kvd * 2.0);
+                     weight_bytes(tq, qd, dim, bs) + weight_bytes(tk, kvd, dim, bs) + weight_bytes(tv, kvd, dim, bs) +
+                         (2.0 * dim + qd) * f4 + 2.0 * kvd * 2.0);
         } else {
             const ZeroList z{{m->q, m->k, m->v},
                              {static_cast<long long>(B) * qd, static_cast<long long>(B) * kvd,
@@ -709,7 +730,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         // x += Wo att.
         if (fused1) {
             const RowsOut o = {m->x, W(m->wo), S(m->wo), dim};
-            ALJ_TRY(enqueue_nf4_rows_fused(&o, 1, m->att, nullptr, 0.0f, qd, shift, kRowsAdd));
+            ALJ_TRY(enqueue_rows_fused(m->wo[l].type, &o, 1, m->att, nullptr, 0.0f, qd, shift, kRowsAdd));
             ALJ_MARK("wo_rows_add", mm_bytes(m->wo[l], dim, qd, true));
         } else {
             ALJ_TRY(mm(m->x, m->att, m->wo[l], qd, dim, true, m->xb));
@@ -719,18 +740,26 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         if (fused1) {
             const RowsOut gu[2] = {{m->hb, W(m->w_gate), S(m->w_gate), ffn},
                                    {nullptr, W(m->w_up), S(m->w_up), ffn}};
-            rc = enqueue_nf4_rows_fused(gu, 2, m->x, ffn_norm, c.eps, dim, shift, kRowsSwiGLU);
-            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {     // row count the paired waves do not divide
+            const int tg = m->w_gate[l].type, tu = m->w_up[l].type;
+            rc = tg == tu ? enqueue_rows_fused(tg, gu, 2, m->x, ffn_norm, c.eps, dim, shift, kRowsSwiGLU)
+                          : ALJABR_ROCM_ERR_UNSUPPORTED;
+            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {     // mixed types, or a row count the paired waves do not divide
                 const RowsOut gu2[2] = {{m->gate, W(m->w_gate), S(m->w_gate), ffn},
                                         {m->up, W(m->w_up), S(m->w_up), ffn}};
-                ALJ_TRY(enqueue_nf4_rows_fused(gu2, 2, m->x, ffn_norm, c.eps, dim, shift, kRowsStore));
+                if (tg == tu) {
+                    ALJ_TRY(enqueue_rows_fused(tg, gu2, 2, m->x, ffn_norm, c.eps, dim, shift, kRowsStore));
+                } else {
+                    ALJ_TRY(enqueue_rows_fused(tg, gu2, 1, m->x, ffn_norm, c.eps, dim, shift, kRowsStore));
+                    ALJ_TRY(enqueue_rows_fused(tu, gu2 + 1, 1, m->x, ffn_norm, c.eps, dim, shift, kRowsStore));
+                }
                 ALJ_TRY(enqueue_swiglu(m->hb, m->gate, m->up, ffn));
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }
-            ALJ_MARK("gate_up_rows_rmsnorm_swiglu", nf4_w(2LL * ffn, dim, bs) + (2.0 * dim + ffn) * f4);
+            ALJ_MARK("gate_up_rows_rmsnorm_swiglu",
+                     weight_bytes(tg, ffn, dim, bs) + weight_bytes(tu, ffn, dim, bs) + (2.0 * dim + ffn) * f4);
             const RowsOut d = {m->x, W(m->w_down), S(m->w_down), dim};
-            ALJ_TRY(enqueue_nf4_rows_fused(&d, 1, m->hb, nullptr, 0.0f, ffn, shift, kRowsAdd));
+            ALJ_TRY(enqueue_rows_fused(m->w_down[l].type, &d, 1, m->hb, nullptr, 0.0f, ffn, shift, kRowsAdd));
             ALJ_MARK("down_rows_add", mm_bytes(m->w_down[l], dim, ffn, true));
         } else {
             const ZeroList z{{m->gate, m->up, nullptr},

@@ -649,9 +649,44 @@ int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax
     return ALJABR_ROCM_OK;
 }
 
+namespace {
+
+template <int FMT>
+int launch_fused(RowsArgs &args, int T, int epilogue, bool norm, hipStream_t s) {
+    switch (epilogue) {
+    case kRowsStore:
+        if (norm) launch_rows<FMT, kXNorm, kEStore>(args, T, s);
+        else launch_rows<FMT, kXPlain, kEStore>(args, T, s);
+        return ALJABR_ROCM_OK;
+    case kRowsAdd:
+        if (norm) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        launch_rows<FMT, kXPlain, kEAdd>(args, T, s);
+        return ALJABR_ROCM_OK;
+    case kRowsSwiGLU:
+        if (!norm) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        launch_rows<FMT, kXNorm, kESwiGLU>(args, T, s);
+        return ALJABR_ROCM_OK;
+    default:
+        if (!norm) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        launch_rows<FMT, kXNorm, kERopeKV>(args, T, s);
+        return ALJABR_ROCM_OK;
+    }
+}
+
+}  // namespace
+
 int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
                            int bs_shift, int epilogue, const RowsRope *rope) {
-    if (nseg < 1 || nseg > 3 || !rows_shape_ok(x, K) || bs_shift < 5) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    return enqueue_rows_fused(ALJABR_ROCM_TYPE_NF4, outs, nseg, x, norm_w, eps, K, bs_shift, epilogue, rope);
+}
+
+int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
+                       int bs_shift, int epilogue, const RowsRope *rope) {
+    if (nseg < 1 || nseg > 3 || !rows_shape_ok(x, K)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    if (type == ALJABR_ROCM_TYPE_NF4 && bs_shift < 5) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    if (type != ALJABR_ROCM_TYPE_NF4 && type != ALJABR_ROCM_TYPE_Q4_0 && type != ALJABR_ROCM_TYPE_Q8_0 &&
+        type != ALJABR_ROCM_TYPE_Q4_K && type != ALJABR_ROCM_TYPE_Q6_K)
+        return ALJABR_ROCM_ERR_UNSUPPORTED;
     if (norm_w && !aligned(norm_w, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     RowsArgs args{};
     if (epilogue == kRowsSwiGLU) {
@@ -675,7 +710,8 @@ int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const 
     long long end = 0;
     for (int i = 0; i < 3; ++i) {
         if (i < nseg) {
-            if (!aligned(outs[i].w, 16) || outs[i].n <= 0 || (outs[i].n & 1)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            const size_t wa = (type == ALJABR_ROCM_TYPE_Q4_0 || type == ALJABR_ROCM_TYPE_Q8_0) ? 4 : 16;
+            if (!aligned(outs[i].w, wa) || outs[i].n <= 0 || (outs[i].n & 1)) return ALJABR_ROCM_ERR_UNSUPPORTED;
             end += outs[i].n;
             if (end > 0x7ffffffeLL) return ALJABR_ROCM_ERR_UNSUPPORTED;
             args.seg[i] = RowsSeg{outs[i].w, outs[i].absmax, outs[i].y, static_cast<int>(end)};
@@ -696,25 +732,13 @@ int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const 
         return ALJABR_ROCM_ERR_UNSUPPORTED;      // every wave's gate run must be whole
     hipStream_t s = current_stream();
     const bool norm = norm_w != nullptr;
-    switch (epilogue) {
-    case kRowsStore:
-        if (norm) launch_rows<kFmtNF4, kXNorm, kEStore>(args, T, s);
-        else launch_rows<kFmtNF4, kXPlain, kEStore>(args, T, s);
-        break;
-    case kRowsAdd:
-        if (norm) return ALJABR_ROCM_ERR_UNSUPPORTED;
-        launch_rows<kFmtNF4, kXPlain, kEAdd>(args, T, s);
-        break;
-    case kRowsSwiGLU:
-        if (!norm) return ALJABR_ROCM_ERR_UNSUPPORTED;
-        launch_rows<kFmtNF4, kXNorm, kESwiGLU>(args, T, s);
-        break;
-    default:
-        if (!norm) return ALJABR_ROCM_ERR_UNSUPPORTED;
-        launch_rows<kFmtNF4, kXNorm, kERopeKV>(args, T, s);
-        break;
+    switch (type) {
+    case ALJABR_ROCM_TYPE_NF4: return launch_fused<kFmtNF4>(args, T, epilogue, norm, s);
+    case ALJABR_ROCM_TYPE_Q4_0: return launch_fused<kFmtQ4>(args, T, epilogue, norm, s);
+    case ALJABR_ROCM_TYPE_Q8_0: return launch_fused<kFmtQ8>(args, T, epilogue, norm, s);
+    case ALJABR_ROCM_TYPE_Q4_K: return launch_fused<kFmtQ4K>(args, T, epilogue, norm, s);
+    default: return launch_fused<kFmtQ6K>(args, T, epilogue, norm, s);
     }
-    return ALJABR_ROCM_OK;
 }
 
 }  // namespace aljabr

@@ -54,6 +54,8 @@ def parse() -> argparse.Namespace:
                     help="only run a plain 256 MiB device copy 20 times (FETCH_SIZE/WRITE_SIZE calibration)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode-step measurement (for profiling runs; prints its own JSON line)")
+    ap.add_argument("--gguf-decode-only", action="store_true",
+                    help="run only the GGUF Q4_K_M decode measurement (for profiling)")
     return ap.parse_args()
 
 
@@ -294,10 +296,10 @@ def copy_probe(torch, stream) -> None:
     print(json.dumps({"copy_probe_bytes_each_way": 4 * n, "launches": 20}), flush=True)
 
 
-def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, weights, cfg):
-    from aljabr_amd.llama import DeviceLlama
+def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, make_model, cfg):
+    """make_model(max_batch, max_seq) -> DeviceLlama."""
     max_seq = ctx + 2 * steps + 8
-    model = DeviceLlama(cfg, weights, max_batch=batch, max_seq=max_seq)
+    model = make_model(batch, max_seq)
     # Context of `ctx` tokens: fill the fp16 KV cache with N(0,1) values.
     kp, vp = model.kv_cache_ptrs()
     total = model.kv_cache_elems()
@@ -358,7 +360,7 @@ def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, weights, 
 
 def decode_runs(args, abi, torch, stream):
     """random-init Llama-3-8B-shaped NF4 decode at batch 1 and 32, context 2048."""
-    from aljabr_amd.llama import LLAMA3_8B, random_weights
+    from aljabr_amd.llama import LLAMA3_8B, DeviceLlama, random_weights
     log("building random-init Llama-3-8B-shaped NF4 model")
     t0 = time.perf_counter()
     weights = random_weights(LLAMA3_8B, seed=1)
@@ -366,7 +368,52 @@ def decode_runs(args, abi, torch, stream):
     dec = []
     for batch in (1, 32):
         log(f"decode batch {batch}, context 2048")
-        dec.append(decode_bench(abi, torch, stream, batch, 2048, args.decode_steps, weights, LLAMA3_8B))
+        dec.append(decode_bench(abi, torch, stream, batch, 2048, args.decode_steps,
+                                lambda b, s: DeviceLlama(LLAMA3_8B, weights, max_batch=b, max_seq=s), LLAMA3_8B))
+    del weights
+    torch.cuda.empty_cache()
+    return dec
+
+
+# GGUF Q4_K_M layout of a Llama-3-8B file: Q4_K projections and embedding,
+# Q6_K attn_v, ffn_down and output.
+Q4_K_M = dict(tok_embed=12, wq=12, wk=12, wv=14, wo=12, w_gate=12, w_up=12, w_down=14, lm_head=14)
+
+
+def gguf_weights(torch, cfg: dict, types: dict, seed: int = 3) -> dict:
+    """Synthetic typed weights on the device for DeviceLlama.typed (random
+    K-quant codes with fp16 block scales ~1/256, fp32 norms near 1)."""
+    from aljabr_amd.llama import PROJ, proj_shapes
+    g = torch.Generator(device="cuda:0").manual_seed(seed)
+    shapes = proj_shapes(cfg)
+    w = {k: [] for k in PROJ}
+    w["attn_norm"], w["ffn_norm"] = [], []
+    for _ in range(cfg["layers"]):
+        for name in PROJ:
+            n, k = shapes[name]
+            w[name].append((types[name], kquant_blocks(torch, types[name], n, k, g)))
+        w["attn_norm"].append(1.0 + 0.1 * torch.randn(cfg["dim"], generator=g, device="cuda:0"))
+        w["ffn_norm"].append(1.0 + 0.1 * torch.randn(cfg["dim"], generator=g, device="cuda:0"))
+    w["out_norm"] = 1.0 + 0.1 * torch.randn(cfg["dim"], generator=g, device="cuda:0")
+    w["tok_embed"] = (types["tok_embed"], kquant_blocks(torch, types["tok_embed"], cfg["vocab"], cfg["dim"], g))
+    w["lm_head"] = (types["lm_head"], kquant_blocks(torch, types["lm_head"], cfg["vocab"], cfg["dim"], g))
+    torch.cuda.synchronize()
+    return w
+
+
+def gguf_decode_runs(args, abi, torch, stream):
+    """The GGUF runner path: a Llama-3-8B-shaped Q4_K_M session (typed
+    weights) decoding at batch 1 and 32, context 2048."""
+    from aljabr_amd.llama import LLAMA3_8B, DeviceLlama
+    log("building synthetic Llama-3-8B-shaped Q4_K_M model")
+    weights = gguf_weights(torch, LLAMA3_8B, Q4_K_M)
+    dec = []
+    for batch in (1, 32):
+        log(f"GGUF Q4_K_M decode batch {batch}, context 2048")
+        r = decode_bench(abi, torch, stream, batch, 2048, args.decode_steps,
+                         lambda b, s: DeviceLlama.typed(LLAMA3_8B, weights, max_batch=b, max_seq=s), LLAMA3_8B)
+        r["weights"] = "GGUF Q4_K_M layout (Q4_K; Q6_K attn_v, ffn_down, output), synthetic codes"
+        dec.append(r)
     del weights
     torch.cuda.empty_cache()
     return dec
@@ -391,6 +438,8 @@ def main() -> None:
             copy_probe(torch, stream)
         elif args.decode_only:
             print(json.dumps({"decode": decode_runs(args, abi, torch, stream)}), flush=True)
+        elif args.gguf_decode_only:
+            print(json.dumps({"decode_gguf_q4_k_m": gguf_decode_runs(args, abi, torch, stream)}), flush=True)
         else:
             run(args, abi, torch, stream)
 
@@ -445,6 +494,7 @@ def run(args, abi, torch, stream) -> None:
 
     if not args.no_decode:
         result["decode"] = decode_runs(args, abi, torch, stream)
+        result["decode_gguf_q4_k_m"] = gguf_decode_runs(args, abi, torch, stream)
 
     if not args.no_cpu:
         log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")

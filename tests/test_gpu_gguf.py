@@ -30,6 +30,12 @@ MIXES = {
                            w_up=gw.Q4_0, w_down=gw.Q4_0, lm_head=None)),
     "rows_k2048": (CFG_BIG, dict(tok_embed=gw.Q6_K, wq=gw.Q4_K, wk=gw.Q4_K, wv=gw.Q6_K, wo=gw.Q4_K,
                                  w_gate=gw.Q4_K, w_up=gw.Q4_K, w_down=gw.Q6_K, lm_head=gw.Q6_K)),
+    # Batch-1 fused launches per format: one-type Q/K/V (RoPE + append
+    # epilogue) in Q8_0 and Q6_K, Q4_0 and Q4_K residual adds, a mixed gate/up.
+    "rows_q8": (CFG_BIG, dict(tok_embed=gw.Q8_0, wq=gw.Q8_0, wk=gw.Q8_0, wv=gw.Q8_0, wo=gw.Q4_0, w_gate=gw.Q4_K,
+                              w_up=gw.Q4_K, w_down=gw.Q8_0, lm_head=gw.F16)),
+    "rows_q6_mixed": (CFG_BIG, dict(tok_embed=gw.F32, wq=gw.Q6_K, wk=gw.Q6_K, wv=gw.Q6_K, wo=gw.Q4_K,
+                                    w_gate=gw.Q4_K, w_up=gw.Q6_K, w_down=gw.Q4_0, lm_head=None)),
 }
 
 
@@ -65,7 +71,8 @@ def _run_against_oracle(dev, oracle, model, cfg, weights, batch, steps=5, graph=
 
 
 @pytest.mark.parametrize("name,batch", [("q4_k_m", 1), ("q4_k_m", 3), ("all_types", 1), ("all_types", 2),
-                                        ("tied_f16", 2), ("rows_k2048", 1), ("rows_k2048", 3)])
+                                        ("tied_f16", 2), ("rows_k2048", 1), ("rows_k2048", 3), ("rows_q8", 1),
+                                        ("rows_q6_mixed", 1), ("rows_q6_mixed", 2)])
 def test_gguf_file_decode_matches_oracle(rocm, dev, oracle, tmp_path, name, batch):
     from aljabr_amd.llama import DeviceLlama
     cfg, path, weights = _write(oracle, tmp_path, name)

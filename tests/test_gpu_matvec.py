@@ -190,9 +190,12 @@ def test_matvec_argument_errors(rocm, dev):
     with pytest.raises(rocm.RocmError) as e:
         rocm.call("aljabr_rocm_matvec_tb_q4_0", dev.ptr(y), dev.ptr(y), dev.ptr(y), 48, 1)
     assert e.value.status == rocm.ERR_BAD_ARGUMENT
-    with pytest.raises(rocm.RocmError) as e:
-        rocm.call("aljabr_rocm_matvec_tb_batch", dev.ptr(y), dev.ptr(y), dev.ptr(y), 32, 1, 12, 1)
+    with pytest.raises(rocm.RocmError) as e:                 # Q5_K: a GGUF type without a kernel here
+        rocm.call("aljabr_rocm_matvec_tb_batch", dev.ptr(y), dev.ptr(y), dev.ptr(y), 256, 1, 13, 1)
     assert e.value.status == rocm.ERR_UNSUPPORTED
+    with pytest.raises(rocm.RocmError) as e:                 # Q4_K rows must be whole super-blocks
+        rocm.call("aljabr_rocm_matvec_tb_batch", dev.ptr(y), dev.ptr(y), dev.ptr(y), 32, 1, 12, 1)
+    assert e.value.status == rocm.ERR_BAD_ARGUMENT
     with pytest.raises(rocm.RocmError) as e:
         rocm.call("aljabr_rocm_matvec_tb_nf4", dev.ptr(y), dev.ptr(y), dev.ptr(y), dev.ptr(y), 64, 1, 7)
     assert e.value.status == rocm.ERR_BAD_ARGUMENT
