@@ -53,6 +53,15 @@ int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int
 // Q4_K / Q6_K small-M GEMM on MFMA (2 <= M <= 32, K % 512 == 0, A and W
 // 16-byte aligned; ALJABR_ROCM_ERR_UNSUPPORTED otherwise, nothing enqueued).
 int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M);
+// The same over up to three matrices of one type and K stacked in one launch
+// (all but the last with a multiple of 32 rows); outs[i].y is [M][outs[i].n].
+// With `accumulate` the products are added to the outputs as they are.
+struct KqOut {
+    float *y;
+    const uint8_t *w;
+    int n;
+};
+int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate);
 // y = cap * tanh(y / cap) elementwise.
 int enqueue_softcap(float *y, long long n, float cap);
 // K-split tile kernels for M <= 2 (ALJABR_ROCM_ERR_UNSUPPORTED when the shape

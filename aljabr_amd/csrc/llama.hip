@@ -617,19 +617,49 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
     if (host_pos)
         for (int b = 0; b < B; ++b) keys += std::min(host_pos[b] + 1, c.max_seq);
     using T = aljabr_rocm_llama::T;
-    // y = x . W^T or, with `residual`, y += x . W^T for B rows. NF4 on the
-    // matrix cores accumulates into y (which the NF4 path has cleared or
-    // holds the residual); otherwise y is written, or the products go to `tmp`
-    // and one add follows.
+    // y = x . W^T or, with `residual`, y += x . W^T for B rows. NF4 and the
+    // K-quants on the matrix cores accumulate into y (which the caller has
+    // cleared, or which holds the residual); otherwise y is written, or the
+    // products go to `tmp` and one add follows.
+    auto kquant = [](int t) { return t == ALJABR_ROCM_TYPE_Q4_K || t == ALJABR_ROCM_TYPE_Q6_K; };
     auto mm = [&](float *y, const float *x, const T &t, int K, int N, bool residual, float *tmp) -> int {
         if (t.type == ALJABR_ROCM_TYPE_NF4 && B >= 2 && B <= 64 && shift >= 0 && m->all_nf4) {
             const int r = enqueue_nf4_mfma(y, x, t.w, t.s, K, N, shift, B, true);
+            if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
+        }
+        if (kquant(t.type) && B >= 2 && B <= 32) {
+            const KqOut o{y, t.w, N};
+            const int r = enqueue_kquant_mfma_multi(&o, 1, x, K, t.type, B, true);
             if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
         }
         if (!residual) return enqueue_matmul_typed(y, x, t.w, t.s, t.type, bs, K, N, B);
         const int r = enqueue_matmul_typed(tmp, x, t.w, t.s, t.type, bs, K, N, B);
         if (r != ALJABR_ROCM_OK) return r;
         return enqueue_add(y, tmp, static_cast<long long>(B) * N);
+    };
+    // Matrices of one layer block: runs of one type go to the matrix cores as
+    // one stacked launch where they can, the rest one by one.
+    auto mm_run = [&](float *const *ys, const T *const *ts, const int *ns, int cnt, const float *x, int K) -> int {
+        for (int i = 0; i < cnt;) {
+            int j = i + 1;
+            while (j < cnt && ts[j]->type == ts[i]->type) ++j;
+            int r = ALJABR_ROCM_ERR_UNSUPPORTED;
+            if ((ts[i]->type == ALJABR_ROCM_TYPE_Q4_K || ts[i]->type == ALJABR_ROCM_TYPE_Q6_K) && B >= 2 && B <= 32) {
+                KqOut o[3];
+                for (int k = i; k < j; ++k) o[k - i] = KqOut{ys[k], ts[k]->w, ns[k]};
+                r = enqueue_kquant_mfma_multi(o, j - i, x, K, ts[i]->type, B, true);
+            }
+            if (r == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                for (int k = i; k < j; ++k) {
+                    r = mm(ys[k], x, *ts[k], K, ns[k], false, nullptr);
+                    if (r != ALJABR_ROCM_OK) return r;
+                }
+            } else if (r != ALJABR_ROCM_OK) {
+                return r;
+            }
+            i = j;
+        }
+        return ALJABR_ROCM_OK;
     };
     // Bytes of one B-row product: weights once, activations in, outputs out
     // (read too when added into).
@@ -682,7 +712,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             const ZeroList z{{m->q, m->k, m->v},
                              {static_cast<long long>(B) * qd, static_cast<long long>(B) * kvd,
                               static_cast<long long>(B) * kvd}};
-            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, attn_norm, B, dim, c.eps, m->all_nf4 ? &z : nullptr));
+            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, attn_norm, B, dim, c.eps, &z));
             ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * (qd + 2.0 * kvd)) * f4);
             // Q, K and V in one matrix-core launch where the shapes allow.
             const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq), qd},
@@ -691,9 +721,10 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             rc = m->all_nf4 && B >= 2 && B <= 64 ? enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, true)
                                                  : ALJABR_ROCM_ERR_UNSUPPORTED;
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
-                ALJ_TRY(mm(m->q, m->xb, m->wq[l], dim, qd, false, nullptr));
-                ALJ_TRY(mm(m->k, m->xb, m->wk[l], dim, kvd, false, nullptr));
-                ALJ_TRY(mm(m->v, m->xb, m->wv[l], dim, kvd, false, nullptr));
+                float *const ys[3] = {m->q, m->k, m->v};
+                const T *const ts[3] = {&m->wq[l], &m->wk[l], &m->wv[l]};
+                const int ns[3] = {qd, kvd, kvd};
+                ALJ_TRY(mm_run(ys, ts, ns, 3, m->xb, dim));
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }
@@ -764,15 +795,17 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         } else {
             const ZeroList z{{m->gate, m->up, nullptr},
                              {static_cast<long long>(B) * ffn, static_cast<long long>(B) * ffn, 0}};
-            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, ffn_norm, B, dim, c.eps, m->all_nf4 ? &z : nullptr));
+            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, ffn_norm, B, dim, c.eps, &z));
             ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * 2.0 * ffn) * f4);
             const RowsOut gu[2] = {{m->gate, W(m->w_gate), S(m->w_gate), ffn},
                                    {m->up, W(m->w_up), S(m->w_up), ffn}};
             rc = m->all_nf4 && B >= 2 && B <= 64 ? enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, true)
                                                  : ALJABR_ROCM_ERR_UNSUPPORTED;
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
-                ALJ_TRY(mm(m->gate, m->xb, m->w_gate[l], dim, ffn, false, nullptr));
-                ALJ_TRY(mm(m->up, m->xb, m->w_up[l], dim, ffn, false, nullptr));
+                float *const ys[2] = {m->gate, m->up};
+                const T *const ts[2] = {&m->w_gate[l], &m->w_up[l]};
+                const int ns[2] = {ffn, ffn};
+                ALJ_TRY(mm_run(ys, ts, ns, 2, m->xb, dim));
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }

@@ -55,12 +55,37 @@ constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerWg = kWaves * 32;
 
+// Up to three weight matrices of the same type and K stacked as one row
+// space (the decode step's Q/K/V or gate/up in one launch): segment s owns
+// stacked rows [end[s-1], end[s]); all but the last hold a multiple of 32
+// rows, so a wave's 32-row tile never straddles two.
 struct KqArgs {
-    float *y;
+    float *y[3];
     const float *x;
-    const uint8_t *w;
-    int M, N, K;
+    const uint8_t *w[3];
+    int end[3];
+    int nseg;
+    int M, N, K;   // N: stacked rows
 };
+
+// The segment of the tile starting at stacked row r0.
+struct KqTile {
+    const uint8_t *w;
+    float *y;
+    int local0, n;
+};
+
+__device__ __forceinline__ KqTile kq_tile(const KqArgs &a, int r0) {
+    int s = (r0 >= a.end[0]) + (r0 >= a.end[1]);
+    if (s > a.nseg - 1) s = a.nseg - 1;
+    const int start = s == 0 ? 0 : s == 1 ? a.end[0] : a.end[1];
+    KqTile t;
+    t.w = s == 0 ? a.w[0] : s == 1 ? a.w[1] : a.w[2];
+    t.y = s == 0 ? a.y[0] : s == 1 ? a.y[1] : a.y[2];
+    t.local0 = r0 - start;
+    t.n = (s == 0 ? a.end[0] : s == 1 ? a.end[1] : a.end[2]) - start;
+    return t;
+}
 
 template <bool Q6> struct KqGeom {
     static constexpr int BB = Q6 ? kQ6KBytes : kQ4KBytes;
@@ -144,7 +169,7 @@ constexpr size_t kq_lds_bytes() {
 // piece is bytes 194..209, read for its last two bytes, d, so that no load
 // leaves the block).
 template <bool Q6>
-__device__ __forceinline__ void issue_unit(u32x4 (&q)[KqGeom<Q6>::LOADS], const KqArgs &a, int row0, int sb,
+__device__ __forceinline__ void issue_unit(u32x4 (&q)[KqGeom<Q6>::LOADS], const KqArgs &a, const KqTile &tr, int sb,
                                            int lane) {
     using G = KqGeom<Q6>;
     const size_t row_bytes = static_cast<size_t>(a.K >> 8) * G::BB;
@@ -152,8 +177,8 @@ __device__ __forceinline__ void issue_unit(u32x4 (&q)[KqGeom<Q6>::LOADS], const 
     for (int i = 0; i < G::LOADS; ++i) {
         const int p = min(64 * i + lane, 32 * G::SEGS - 1);
         const int r = p / G::SEGS, seg = p - r * G::SEGS;
-        const int row = min(row0 + r, a.N - 1);
-        const uint8_t *src = a.w + static_cast<size_t>(row) * row_bytes + static_cast<size_t>(sb) * G::BB + 16 * seg;
+        const int row = min(tr.local0 + r, tr.n - 1);
+        const uint8_t *src = tr.w + static_cast<size_t>(row) * row_bytes + static_cast<size_t>(sb) * G::BB + 16 * seg;
         if constexpr (Q6) {
             q[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4u *>(seg == G::SEGS - 1 ? src - 14 : src));
         } else {
@@ -236,18 +261,18 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
 
     constexpr int U = NT * SBS;
     constexpr int W = 2;
-    int row0[NT];
+    KqTile tr[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) row0[t] = blockIdx.x * (kRowsPerWg * NT) + t * kRowsPerWg + wave * 32;
+    for (int t = 0; t < NT; ++t) tr[t] = kq_tile(a, blockIdx.x * (kRowsPerWg * NT) + t * kRowsPerWg + wave * 32);
     u32x4 qc[U][G::LOADS];
 #pragma unroll
-    for (int u = 0; u < W && u < U; ++u) issue_unit<Q6>(qc[u], a, row0[u / SBS], ks0 / 256 + u % SBS, lane);
+    for (int u = 0; u < W && u < U; ++u) issue_unit<Q6>(qc[u], a, tr[u / SBS], ks0 / 256 + u % SBS, lane);
     __syncthreads();
 
     f32x16 acc = {};
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        if (u + W < U) issue_unit<Q6>(qc[u + W], a, row0[(u + W) / SBS], ks0 / 256 + (u + W) % SBS, lane);
+        if (u + W < U) issue_unit<Q6>(qc[u + W], a, tr[(u + W) / SBS], ks0 / 256 + (u + W) % SBS, lane);
         const int t = u / SBS, sbl = u % SBS;
         if (sbl == 0) acc = f32x16{};
         stage_unit<Q6>(st, qc[u], lane);
@@ -353,12 +378,12 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
         for (int r = 0; r < 16; ++r) acc[r] = fmaf(d, cq[r], acc[r]);
         __builtin_amdgcn_sched_barrier(0);
         if (sbl == SBS - 1) {
-            const int n = row0[t] + nl;
-            if (n < a.N) {
+            const int n = tr[t].local0 + nl;
+            if (n < tr[t].n) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int m = 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (m < a.M) unsafeAtomicAdd(a.y + static_cast<size_t>(m) * a.N + n, acc[r]);
+                    if (m < a.M) unsafeAtomicAdd(tr[t].y + static_cast<size_t>(m) * tr[t].n + n, acc[r]);
                 }
             }
         }
@@ -385,16 +410,40 @@ void launch_kq(const KqArgs &args, hipStream_t s) {
 
 }  // namespace
 
-// 2 <= M <= 32, K % 512 == 0, A and W 16-byte aligned.
-int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M) {
-    if ((type != ALJABR_ROCM_TYPE_Q4_K && type != ALJABR_ROCM_TYPE_Q6_K) || M < 2 || M > 32 || K % 512 != 0 ||
-        N < 1 || !aligned(A, 16) || !aligned(W, 16))
+// 2 <= M <= 32, K % 512 == 0, A and weights 16-byte aligned, up to three
+// matrices of one type (all but the last with a multiple of 32 rows).
+int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate) {
+    if ((type != ALJABR_ROCM_TYPE_Q4_K && type != ALJABR_ROCM_TYPE_Q6_K) || nseg < 1 || nseg > 3 || M < 2 || M > 32 ||
+        K % 512 != 0 || !aligned(A, 16))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
-    const KqArgs args{C, A, W, M, N, K};
+    KqArgs args{};
+    long long end = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (i < nseg) {
+            const KqOut &o = outs[i];
+            if (o.n <= 0 || !aligned(o.w, 16) || (i < nseg - 1 && o.n % 32 != 0)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            end += o.n;
+            if (end > 0x7fff0000LL) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            args.y[i] = o.y;
+            args.w[i] = o.w;
+            args.end[i] = static_cast<int>(end);
+        } else {
+            args.end[i] = 0x7fffffff;
+        }
+    }
+    args.nseg = nseg;
+    args.x = A;
+    args.M = M;
+    args.N = static_cast<int>(end);
+    args.K = K;
     hipStream_t s = current_stream();
-    const long long total = static_cast<long long>(M) * N;
-    hipLaunchKernelGGL(kq_zero_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, C, total);
-    const int wgs_n = (N + kRowsPerWg - 1) / kRowsPerWg;
+    if (!accumulate)   // the K-slices add into the outputs
+        for (int i = 0; i < nseg; ++i) {
+            const long long total = static_cast<long long>(M) * outs[i].n;
+            hipLaunchKernelGGL(kq_zero_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s,
+                               outs[i].y, total);
+        }
+    const int wgs_n = (args.N + kRowsPerWg - 1) / kRowsPerWg;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     const long long units = static_cast<long long>(wgs_n) * (K / 512);
     const bool two = units > cus;
@@ -406,6 +455,11 @@ int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N
         else launch_kq<true, 512, 1>(args, s);
     }
     return ALJABR_ROCM_OK;
+}
+
+int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M) {
+    const KqOut o{C, W, N};
+    return enqueue_kquant_mfma_multi(&o, 1, A, K, type, M, false);
 }
 
 }  // namespace aljabr
