@@ -56,6 +56,8 @@ def parse() -> argparse.Namespace:
                     help="only the decode-step measurement (for profiling runs; prints its own JSON line)")
     ap.add_argument("--gguf-decode-only", action="store_true",
                     help="run only the GGUF Q4_K_M decode measurement (for profiling)")
+    ap.add_argument("--kquant-only", action="store_true",
+                    help="run only the GGUF Q4_0/Q8_0 and K-quant matvec/GEMM measurements (for profiling)")
     return ap.parse_args()
 
 
@@ -169,6 +171,54 @@ def small_m_bench(abi, torch, stream, ms=(1, 4, 16, 64), launches=60):
                                     "TFLOPs": round(2.0 * m * n * k / us / 1e6, 1)}
         del bufs
         torch.cuda.empty_cache()
+    return out
+
+
+def gguf_q_bench(abi, torch, stream, ms=(1, 8), launches=60):
+    """GGUF Q4_0 / Q8_0 matvec at 4096x4096 and
+    14336x4096 from N(0, 0.02) weights (quantized on the device by the
+    GGUFWriter rules), x ~ N(0,1) at batch 1 and 8; weights rotate over
+    >= 512 MB. Launch time and algorithmic GB/s (blocks once + activations)."""
+    lib = abi.load()
+    out = {}
+    for qtype, name, bb in ((abi.TYPE_Q4_0, "q4_0", 18), (abi.TYPE_Q8_0, "q8_0", 34)):
+        for n, k in ((K_MODEL, K_MODEL), (FFN, K_MODEL)):
+            per = n * k // 32 * bb
+            copies = max(2, -(-520_000_000 // per))
+            g = torch.Generator(device="cuda:0").manual_seed(9)
+            bufs = []
+            for _ in range(copies):
+                w = torch.randn(n * k, generator=g, device="cuda:0").mul_(0.02)
+                q = torch.empty(per, dtype=torch.uint8, device="cuda:0")
+                torch.cuda.synchronize()
+                abi.call("aljabr_rocm_quantize", q.data_ptr(), None, w.data_ptr(), n * k, qtype, 0)
+                abi.call("aljabr_rocm_synchronize")
+                del w
+                bufs.append(q)
+            for m in ms:
+                x = torch.randn(m * k, device="cuda:0")
+                y = torch.empty(m * n, device="cuda:0")
+                torch.cuda.synchronize()
+
+                def launch(i):
+                    rc = lib.aljabr_rocm_matvec_tb_batch(y.data_ptr(), x.data_ptr(), bufs[i % copies].data_ptr(),
+                                                         k, n, qtype, m)
+                    if rc:
+                        abi.check(rc, "aljabr_rocm_matvec_tb_batch")
+                for i in range(20):
+                    launch(i)
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                for i in range(launches):
+                    launch(i)
+                end.record(stream)
+                end.synchronize()
+                us = start.elapsed_time(end) * 1000.0 / launches
+                alg = per + m * (k + n) * 4
+                out[f"{name}_{n}x{k}_m{m}"] = {"us": round(us, 2), "GBs": round(alg / us / 1e3, 1),
+                                               "frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 3)}
+            del bufs
+            torch.cuda.empty_cache()
     return out
 
 
@@ -438,6 +488,9 @@ def main() -> None:
             copy_probe(torch, stream)
         elif args.decode_only:
             print(json.dumps({"decode": decode_runs(args, abi, torch, stream)}), flush=True)
+        elif args.kquant_only:
+            print(json.dumps({"gguf_q4_0_q8_0": gguf_q_bench(abi, torch, stream),
+                              "gguf_kquant": kquant_bench(abi, torch, stream)}), flush=True)
         elif args.gguf_decode_only:
             print(json.dumps({"decode_gguf_q4_k_m": gguf_decode_runs(args, abi, torch, stream)}), flush=True)
         else:
@@ -489,6 +542,8 @@ def run(args, abi, torch, stream) -> None:
         result["small_m_gemm"] = small_m_bench(abi, torch, stream)
         log("GQA decode attention")
         result["attention"] = attention_bench(abi, torch, stream)
+        log("GGUF Q4_0 / Q8_0 matvec (M = 1, 8)")
+        result["gguf_q4_0_q8_0"] = gguf_q_bench(abi, torch, stream)
         log("GGUF K-quant matvec (Q4_K, Q6_K; M = 1, 4, 8)")
         result["gguf_kquant"] = kquant_bench(abi, torch, stream)
 
