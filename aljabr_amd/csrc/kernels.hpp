@@ -50,8 +50,12 @@ int enqueue_matmul_typed(float *C, const float *A, const void *W, const float *a
                          int M);
 // GGUF Q4_K / Q6_K rows (K % 256 == 0, A and W 16-byte aligned), any M.
 int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M);
-// Q4_K / Q6_K small-M GEMM on MFMA (2 <= M <= 32, K % 512 == 0, A and W
-// 16-byte aligned; ALJABR_ROCM_ERR_UNSUPPORTED otherwise, nothing enqueued).
+// GGUF block-format (Q4_K, Q6_K, Q4_0, Q8_0) small-M GEMM on MFMA
+// (2 <= M <= kquant_mfma_max_m(type): 32 for the K-quants, 8 for Q4_0 and
+// Q8_0; K % 512 == 0, A and W 16-byte aligned; ALJABR_ROCM_ERR_UNSUPPORTED
+// otherwise, nothing enqueued).
+bool kquant_mfma_type(int type);
+int kquant_mfma_max_m(int type);
 int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M);
 // The same over up to three matrices of one type and K stacked in one launch
 // (all but the last with a multiple of 32 rows); outs[i].y is [M][outs[i].n].

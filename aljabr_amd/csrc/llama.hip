@@ -618,16 +618,15 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         for (int b = 0; b < B; ++b) keys += std::min(host_pos[b] + 1, c.max_seq);
     using T = aljabr_rocm_llama::T;
     // y = x . W^T or, with `residual`, y += x . W^T for B rows. NF4 and the
-    // K-quants on the matrix cores accumulate into y (which the caller has
+    // GGUF block formats on the matrix cores accumulate into y (which the caller has
     // cleared, or which holds the residual); otherwise y is written, or the
     // products go to `tmp` and one add follows.
-    auto kquant = [](int t) { return t == ALJABR_ROCM_TYPE_Q4_K || t == ALJABR_ROCM_TYPE_Q6_K; };
     auto mm = [&](float *y, const float *x, const T &t, int K, int N, bool residual, float *tmp) -> int {
         if (t.type == ALJABR_ROCM_TYPE_NF4 && B >= 2 && B <= 64 && shift >= 0 && m->all_nf4) {
             const int r = enqueue_nf4_mfma(y, x, t.w, t.s, K, N, shift, B, true);
             if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
         }
-        if (kquant(t.type) && B >= 2 && B <= 32) {
+        if (kquant_mfma_type(t.type) && B >= 2 && B <= kquant_mfma_max_m(t.type)) {
             const KqOut o{y, t.w, N};
             const int r = enqueue_kquant_mfma_multi(&o, 1, x, K, t.type, B, true);
             if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
@@ -644,7 +643,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             int j = i + 1;
             while (j < cnt && ts[j]->type == ts[i]->type) ++j;
             int r = ALJABR_ROCM_ERR_UNSUPPORTED;
-            if ((ts[i]->type == ALJABR_ROCM_TYPE_Q4_K || ts[i]->type == ALJABR_ROCM_TYPE_Q6_K) && B >= 2 && B <= 32) {
+            if (kquant_mfma_type(ts[i]->type) && B >= 2 && B <= kquant_mfma_max_m(ts[i]->type)) {
                 KqOut o[3];
                 for (int k = i; k < j; ++k) o[k - i] = KqOut{ys[k], ts[k]->w, ns[k]};
                 r = enqueue_kquant_mfma_multi(o, j - i, x, K, ts[i]->type, B, true);

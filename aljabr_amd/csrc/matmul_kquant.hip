@@ -1,13 +1,13 @@
-// matmul_kquant.hip - GGUF Q4_K / Q6_K small-M GEMM on the matrix cores:
-// Y[M,N] = X[M,K] . W[N,K]^T for 2 <= M <= 32 per pass (a decode batch), W in
-// K-quant super-blocks (layouts in kquant.hpp). W is read from HBM once for
-// all M tokens.
+// matmul_kquant.hip - GGUF small-M GEMM on the matrix cores for the block
+// formats Q4_K, Q6_K, Q4_0 and Q8_0: Y[M,N] = X[M,K] . W[N,K]^T for
+// 2 <= M <= 32 per pass (a decode batch). W is read from HBM once for all M
+// tokens.
 //
 // MFMA v_mfma_f32_32x32x16_f16 with fp32 accumulation. A = X split into two
 // fp16 parts, x = hi + lo (hi = fp16(x), lo = fp16(x - hi)): each B fragment
 // is multiplied by both, which carries x to ~2^-22 instead of fp16's 2^-11.
 // B = W^T (32 weight rows per wave as the output columns) holds small exact
-// integers in fp16; the super-block scale stays fp32 on the accumulators:
+// integers in fp16; every fp16/fp32 block scale stays fp32 on the accumulators:
 //   Q4_K  B = q * sc (q <= 15, sc <= 63: <= 945, exact), one MFMA pair per
 //         32-element sub-block; the min term sum_s dmin * m_s * sum(x in s)
 //         is one more MFMA pair per super-block, A = the split per-sub-block
@@ -18,24 +18,33 @@
 //         16-element scale group x_hi meets B_lo and B_hi and x_lo their
 //         fp16 sum (whose rounding, 2^-12 of B, is scaled by x_lo ~ 2^-11 x);
 //         C += d * C_q.
+//   Q4_0  B = q - 8, Q8_0 B = q; per 32-element block C += d * C_b, where
+//         C_b is the block's two MFMA steps (x hi and lo each). These run
+//         2 <= M <= 8 tokens per pass, so only the accumulators of rows
+//         m < 8 (four per lane) are scaled.
 // Codes become fp16 integers with v_perm against a constant 0x64 byte: the
 // half 0x64qq is 1024 + qq exactly. Q4_K low nibbles give 1024 + q, high
 // nibbles (masked in place) 1024 + 16q, and one packed fp16 FMA removes the
 // offset and applies the scale without rounding: (1024 + q) * sc - 1024 * sc,
 // (1024 + 16q) * (sc/16) - 64 * sc. Q6_K: (1024 + q) - 1056, then * scale.
+// Q4_0: (1024 + q) - 1032 and (1024 + 16q) / 16 - 72; Q8_0 bytes are biased
+// by xor 0x80 and (1024 + q + 128) - 1152.
 //
 // Operand layout (32x32x16): lane l supplies A[m = l%32][8*(l/32) + e] and
 // B[8*(l/32) + e][n = l%32]; accumulator r is C[8*(r/4) + 4*(l/32) + r%4][l%32].
 // One MFMA step covers 16 consecutive elements of a row, lane half h the 8
 // at 8h: for Q4_K sub-block s = 2c + t (t: low/high nibbles of qs[32c ..
 // 32c+32)) step j reads qs[32c + 16j + 8h .. +8]; for Q6_K group g (elements
-// 16g .. 16g+15) reads the ql/qh bytes of those elements.
+// 16g .. 16g+15) reads the ql/qh bytes of those elements; Q4_0 block b reads
+// qs[8h .. 8h+8) once for both steps (low nibbles: elements 0..15, high:
+// 16..31); Q8_0 step j reads qs[16j + 8h .. +8].
 //
 // Work split as the NF4 kernel: a workgroup is 8 waves x 32 rows and one
-// K-slice of KS elements; weights are loaded coalesced (whole row segments
-// per lane group) and transposed through per-wave LDS rows, two work units
-// (one super-block of the wave's 32 rows) ahead; K-slices add their partial
-// sums into Y with float atomics (Y is zeroed first).
+// K-slice of KS elements; a work unit is the wave's 32 rows x 256 elements
+// (one K-quant super-block, eight Q4_0/Q8_0 blocks: 144, 210, 144 and 272
+// bytes a row). Weights are loaded coalesced (whole row segments per lane
+// group) and transposed through per-wave LDS rows, two units ahead; K-slices
+// add their partial sums into Y with float atomics (Y is zeroed first).
 #include "device.hpp"
 #include "internal.hpp"
 #include "kernels.hpp"
@@ -87,10 +96,16 @@ __device__ __forceinline__ KqTile kq_tile(const KqArgs &a, int r0) {
     return t;
 }
 
-template <bool Q6> struct KqGeom {
-    static constexpr int BB = Q6 ? kQ6KBytes : kQ4KBytes;
-    static constexpr int SEGS = Q6 ? 14 : 9;      // 16-byte pieces of a row's block (Q6_K: 13 + the 2-byte d)
-    static constexpr int STR = Q6 ? 216 : 152;    // staging row stride: 8-byte aligned, conflict-free 8-byte reads
+// Row formats of the kernel.
+enum : int { kFQ4K = 0, kFQ6K = 1, kFQ40 = 2, kFQ80 = 3 };
+
+template <int F> struct KqGeom {
+    // Bytes of a row's 256-element unit, its 16-byte pieces (Q6_K: 13 + the
+    // 2-byte d) and the staging row stride (8-byte aligned; an odd number of
+    // 8-byte words, so 32 rows' 8-byte reads hit distinct banks).
+    static constexpr int BB = F == kFQ4K ? kQ4KBytes : F == kFQ6K ? kQ6KBytes : F == kFQ40 ? 8 * 18 : 8 * 34;
+    static constexpr int SEGS = F == kFQ4K ? 9 : F == kFQ6K ? 14 : F == kFQ40 ? 9 : 17;
+    static constexpr int STR = F == kFQ4K ? 152 : F == kFQ6K ? 216 : F == kFQ40 ? 152 : 280;
     static constexpr int LOADS = (32 * SEGS + 63) / 64;
 };
 
@@ -156,22 +171,37 @@ __device__ __forceinline__ uint32_t half_bits(float v) {
     return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v)));
 }
 
-template <bool Q6, int KS>
+template <int F, int KS>
 constexpr size_t kq_lds_bytes() {
     // x slice split in two fp16 parts (2 x [32][KS+8]) + Q4_K sub-block sums
     // (2 x [32][KS/32+8]) + per-wave staging rows.
-    return 2 * (static_cast<size_t>(32) * (KS + 8) * 2 + (Q6 ? 0 : static_cast<size_t>(32) * (KS / 32 + 8) * 2)) +
-           static_cast<size_t>(kWaves) * 32 * KqGeom<Q6>::STR;
+    return 2 * (static_cast<size_t>(32) * (KS + 8) * 2 + (F != kFQ4K ? 0 : static_cast<size_t>(32) * (KS / 32 + 8) * 2)) +
+           static_cast<size_t>(kWaves) * 32 * KqGeom<F>::STR;
+}
+
+// Eight bytes at LDS byte address p, where p % 4 == al (0 or 2; a constant
+// once the caller's loops are unrolled), as two words.
+__device__ __forceinline__ void lds_bytes8(const uint8_t *p, int al, uint32_t &w0, uint32_t &w1) {
+    if (al == 0) {
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+        w0 = q[0];
+        w1 = q[1];
+    } else {
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(p - 2);
+        const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
+        w0 = __builtin_amdgcn_alignbyte(d1, d0, 2);
+        w1 = __builtin_amdgcn_alignbyte(d2, d1, 2);
+    }
 }
 
 // Coalesced loads of one unit (the wave's 32 rows x one super-block): piece
 // p = 64i + lane is 16-byte segment p % SEGS of row p / SEGS (Q6_K: the last
 // piece is bytes 194..209, read for its last two bytes, d, so that no load
 // leaves the block).
-template <bool Q6>
-__device__ __forceinline__ void issue_unit(u32x4 (&q)[KqGeom<Q6>::LOADS], const KqArgs &a, const KqTile &tr, int sb,
+template <int F>
+__device__ __forceinline__ void issue_unit(u32x4 (&q)[KqGeom<F>::LOADS], const KqArgs &a, const KqTile &tr, int sb,
                                            int lane) {
-    using G = KqGeom<Q6>;
+    using G = KqGeom<F>;
     const size_t row_bytes = static_cast<size_t>(a.K >> 8) * G::BB;
 #pragma unroll
     for (int i = 0; i < G::LOADS; ++i) {
@@ -179,7 +209,7 @@ __device__ __forceinline__ void issue_unit(u32x4 (&q)[KqGeom<Q6>::LOADS], const 
         const int r = p / G::SEGS, seg = p - r * G::SEGS;
         const int row = min(tr.local0 + r, tr.n - 1);
         const uint8_t *src = tr.w + static_cast<size_t>(row) * row_bytes + static_cast<size_t>(sb) * G::BB + 16 * seg;
-        if constexpr (Q6) {
+        if constexpr (F == kFQ6K) {
             q[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4u *>(seg == G::SEGS - 1 ? src - 14 : src));
         } else {
             q[i] = load_stream16(src);
@@ -188,16 +218,16 @@ __device__ __forceinline__ void issue_unit(u32x4 (&q)[KqGeom<Q6>::LOADS], const 
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool Q6>
-__device__ __forceinline__ void stage_unit(uint8_t *st, const u32x4 (&q)[KqGeom<Q6>::LOADS], int lane) {
-    using G = KqGeom<Q6>;
+template <int F>
+__device__ __forceinline__ void stage_unit(uint8_t *st, const u32x4 (&q)[KqGeom<F>::LOADS], int lane) {
+    using G = KqGeom<F>;
 #pragma unroll
     for (int i = 0; i < G::LOADS; ++i) {
         const int p = 64 * i + lane;
         if (p < 32 * G::SEGS) {
             const int r = p / G::SEGS, seg = p - r * G::SEGS;
             uint8_t *dst = st + r * G::STR + 16 * seg;
-            if (Q6 && seg == G::SEGS - 1) {
+            if (F == kFQ6K && seg == G::SEGS - 1) {
                 *reinterpret_cast<uint16_t *>(dst) = static_cast<uint16_t>(q[i].w >> 16);   // d at 208
             } else {
                 *reinterpret_cast<u32x2v *>(dst) = u32x2v{q[i].x, q[i].y};
@@ -207,9 +237,11 @@ __device__ __forceinline__ void stage_unit(uint8_t *st, const u32x4 (&q)[KqGeom<
     }
 }
 
-template <bool Q6, int KS, int NT>
+template <int F, int KS, int NT, int MT>
 __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
-    using G = KqGeom<Q6>;
+    using G = KqGeom<F>;
+    constexpr bool Q6 = F == kFQ6K;
+    constexpr bool SUMS = F == kFQ4K;            // the min term needs sub-block sums of x
     constexpr int SBS = KS / 256;                // super-blocks per slice
     constexpr int RS = KS + 8;                   // x row stride (halves)
     constexpr int XSS = KS / 32 + 8;             // sub-block-sum row stride (halves)
@@ -218,8 +250,8 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
     _Float16 *xh = reinterpret_cast<_Float16 *>(smem);
     _Float16 *xl = xh + 32 * RS;
     _Float16 *sh = xl + 32 * RS;
-    _Float16 *sl = sh + (Q6 ? 0 : 32 * XSS);
-    uint8_t *stage_base = reinterpret_cast<uint8_t *>(sl + (Q6 ? 0 : 32 * XSS));
+    _Float16 *sl = sh + (SUMS ? 32 * XSS : 0);
+    uint8_t *stage_base = reinterpret_cast<uint8_t *>(sl + (SUMS ? 32 * XSS : 0));
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -244,7 +276,7 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
         const uint32_t q1 = pack_half2(v.z - static_cast<float>(h1.x), v.w - static_cast<float>(h1.y));
         *reinterpret_cast<uint2 *>(xh + m * RS + 4 * c) = make_uint2(p0, p1);
         *reinterpret_cast<uint2 *>(xl + m * RS + 4 * c) = make_uint2(q0, q1);
-        if constexpr (!Q6) {
+        if constexpr (SUMS) {
             float t = (v.x + v.y) + (v.z + v.w);
             // 8 consecutive float4s (lanes c%8 = 0..7 of one row) form a sub-block.
             t += __shfl_xor(t, 1);
@@ -266,22 +298,56 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
     for (int t = 0; t < NT; ++t) tr[t] = kq_tile(a, blockIdx.x * (kRowsPerWg * NT) + t * kRowsPerWg + wave * 32);
     u32x4 qc[U][G::LOADS];
 #pragma unroll
-    for (int u = 0; u < W && u < U; ++u) issue_unit<Q6>(qc[u], a, tr[u / SBS], ks0 / 256 + u % SBS, lane);
+    for (int u = 0; u < W && u < U; ++u) issue_unit<F>(qc[u], a, tr[u / SBS], ks0 / 256 + u % SBS, lane);
     __syncthreads();
 
     f32x16 acc = {};
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        if (u + W < U) issue_unit<Q6>(qc[u + W], a, tr[(u + W) / SBS], ks0 / 256 + (u + W) % SBS, lane);
+        if (u + W < U) issue_unit<F>(qc[u + W], a, tr[(u + W) / SBS], ks0 / 256 + (u + W) % SBS, lane);
         const int t = u / SBS, sbl = u % SBS;
         if (sbl == 0) acc = f32x16{};
-        stage_unit<Q6>(st, qc[u], lane);
+        stage_unit<F>(st, qc[u], lane);
         const uint8_t *row = st + nl * G::STR;   // this lane's weight row
         const _Float16 *xrh = xh + nl * RS + 256 * sbl + 8 * h;
         const _Float16 *xrl = xl + nl * RS + 256 * sbl + 8 * h;
         f32x16 cq = {};
-        float d;
-        if constexpr (!Q6) {
+        float d = 1.0f;
+        if constexpr (F == kFQ40 || F == kFQ80) {
+            // Eight 32-element blocks: fp16 d, then 16 (Q4_0) or 32 (Q8_0) code bytes.
+            constexpr int BLK = F == kFQ40 ? 18 : 34;
+            static_assert(MT == 8, "Q4_0 / Q8_0 passes hold at most 8 tokens");
+            constexpr int RU = 4;                  // accumulators of rows m < 8
+            const uint32_t one = int_half2(1, 1.0f);
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const float db = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(row + BLK * b));
+                const int e0 = 256 * sbl + 32 * b + 8 * h;
+                f32x16 cb = {};
+                if constexpr (F == kFQ40) {
+                    uint32_t w0, w1;
+                    lds_bytes8(row + BLK * b + 2 + 8 * h, (BLK * b + 2) & 3, w0, w1);
+                    const half8 blo = fma_frag(w0 & 0x0f0f0f0fu, w1 & 0x0f0f0f0fu, one, int_half2(-1032, 1.0f));
+                    const half8 bhi = fma_frag(w0 & 0xf0f0f0f0u, w1 & 0xf0f0f0f0u, int_half2(1, 0.0625f),
+                                               int_half2(-72, 1.0f));
+                    cb = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xh + nl * RS + e0), blo, cb, 0, 0, 0);
+                    cb = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xl + nl * RS + e0), blo, cb, 0, 0, 0);
+                    cb = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xh + nl * RS + e0 + 16), bhi, cb, 0, 0, 0);
+                    cb = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xl + nl * RS + e0 + 16), bhi, cb, 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        uint32_t w0, w1;
+                        lds_bytes8(row + BLK * b + 2 + 16 * j + 8 * h, (BLK * b + 2) & 3, w0, w1);
+                        const half8 bq = fma_frag(w0 ^ 0x80808080u, w1 ^ 0x80808080u, one, int_half2(-1152, 1.0f));
+                        cb = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xh + nl * RS + e0 + 16 * j), bq, cb, 0, 0, 0);
+                        cb = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(xl + nl * RS + e0 + 16 * j), bq, cb, 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < RU; ++r) cq[r] = fmaf(db, cb[r], cq[r]);
+            }
+        } else if constexpr (!Q6) {
             const u32x2v h01 = *reinterpret_cast<const u32x2v *>(row);
             const u32x2v h23 = *reinterpret_cast<const u32x2v *>(row + 8);
             const uint32_t sw0 = h01.y, sw1 = h23.x, sw2 = h23.y;   // the 12 scale/min bytes
@@ -395,26 +461,42 @@ __global__ void kq_zero_kernel(float *p, long long n) {
     if (i < n) p[i] = 0.0f;
 }
 
-template <bool Q6, int KS, int NT>
+template <int F, int KS, int NT, int MT>
 void launch_kq(const KqArgs &args, hipStream_t s) {
     static bool lds_set = false;                 // the attribute is per kernel, per process
-    const void *fn = reinterpret_cast<const void *>(kq_mm_kernel<Q6, KS, NT>);
-    const size_t lds = kq_lds_bytes<Q6, KS>();
+    const void *fn = reinterpret_cast<const void *>(kq_mm_kernel<F, KS, NT, MT>);
+    const size_t lds = kq_lds_bytes<F, KS>();
     if (!lds_set) {
         (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         lds_set = true;
     }
     const dim3 grid((args.N + kRowsPerWg * NT - 1) / (kRowsPerWg * NT), args.K / KS), block(kThreads);
-    hipLaunchKernelGGL((kq_mm_kernel<Q6, KS, NT>), grid, block, lds, s, args);
+    hipLaunchKernelGGL((kq_mm_kernel<F, KS, NT, MT>), grid, block, lds, s, args);
+}
+
+template <int F, int MT>
+void launch_kq_nt(const KqArgs &args, bool two, hipStream_t s) {
+    if (two) launch_kq<F, 512, 2, MT>(args, s);
+    else launch_kq<F, 512, 1, MT>(args, s);
 }
 
 }  // namespace
 
-// 2 <= M <= 32, K % 512 == 0, A and weights 16-byte aligned, up to three
-// matrices of one type (all but the last with a multiple of 32 rows).
+bool kquant_mfma_type(int type) {
+    return type == ALJABR_ROCM_TYPE_Q4_K || type == ALJABR_ROCM_TYPE_Q6_K || type == ALJABR_ROCM_TYPE_Q4_0 ||
+           type == ALJABR_ROCM_TYPE_Q8_0;
+}
+
+int kquant_mfma_max_m(int type) {
+    return type == ALJABR_ROCM_TYPE_Q4_0 || type == ALJABR_ROCM_TYPE_Q8_0 ? 8 : 32;
+}
+
+// 2 <= M <= kquant_mfma_max_m(type), K % 512 == 0, A and weights 16-byte
+// aligned, up to three matrices of one type (all but the last with a
+// multiple of 32 rows).
 int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate) {
-    if ((type != ALJABR_ROCM_TYPE_Q4_K && type != ALJABR_ROCM_TYPE_Q6_K) || nseg < 1 || nseg > 3 || M < 2 || M > 32 ||
-        K % 512 != 0 || !aligned(A, 16))
+    if (!kquant_mfma_type(type) || nseg < 1 || nseg > 3 || M < 2 || M > kquant_mfma_max_m(type) || K % 512 != 0 ||
+        !aligned(A, 16))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     KqArgs args{};
     long long end = 0;
@@ -447,12 +529,11 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     const long long units = static_cast<long long>(wgs_n) * (K / 512);
     const bool two = units > cus;
-    if (type == ALJABR_ROCM_TYPE_Q4_K) {
-        if (two) launch_kq<false, 512, 2>(args, s);
-        else launch_kq<false, 512, 1>(args, s);
-    } else {
-        if (two) launch_kq<true, 512, 2>(args, s);
-        else launch_kq<true, 512, 1>(args, s);
+    switch (type) {
+    case ALJABR_ROCM_TYPE_Q4_K: launch_kq_nt<kFQ4K, 32>(args, two, s); break;
+    case ALJABR_ROCM_TYPE_Q6_K: launch_kq_nt<kFQ6K, 32>(args, two, s); break;
+    case ALJABR_ROCM_TYPE_Q4_0: launch_kq_nt<kFQ40, 8>(args, two, s); break;
+    default: launch_kq_nt<kFQ80, 8>(args, two, s); break;
     }
     return ALJABR_ROCM_OK;
 }

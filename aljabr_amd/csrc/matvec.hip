@@ -508,6 +508,20 @@ int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float 
 
 int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M) {
     if (type == ALJABR_ROCM_TYPE_Q4_K || type == ALJABR_ROCM_TYPE_Q6_K) return enqueue_matmul_kquant(C, A, B, K, N, type, M);
+    // Q4_0 / Q8_0 with M >= 2 on the matrix cores (K % 512, 16-byte aligned),
+    // 8 tokens per pass; a last single token takes the batch-1 path.
+    if ((type == ALJABR_ROCM_TYPE_Q4_0 || type == ALJABR_ROCM_TYPE_Q8_0) && M >= 2 && K % 512 == 0 &&
+        aligned(A, 16) && aligned(B, 16) && mfma_enabled()) {
+        int m0 = 0;
+        for (; M - m0 >= 2; m0 += 8) {
+            const int mm = M - m0 < 8 ? M - m0 : 8;
+            const int rc = enqueue_kquant_mfma(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, B, K,
+                                               N, type, mm);
+            if (rc != ALJABR_ROCM_OK) return rc;
+        }
+        if (m0 == M) return ALJABR_ROCM_OK;
+        return enqueue_gguf_small(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, B, K, N, type, 1);
+    }
     // fp16 rows with M >= 2 on the matrix cores, 32 tokens per pass.
     if (type == ALJABR_ROCM_TYPE_F16 && M >= 2 && mfma_enabled()) {
         const uint16_t *W = reinterpret_cast<const uint16_t *>(B);
