@@ -136,6 +136,10 @@ SIGNATURES = {
     "aljabr_rocm_dequantize": (_I, [_P, _P, _P, _LL, _I, _I]),
     "aljabr_rocm_quantize": (_I, [_P, _P, _P, _LL, _I, _I]),
     "aljabr_rocm_attention_gqa": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I]),
+    "aljabr_rocm_fa4_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _I, _F]),
+    "aljabr_rocm_fa4_attention_windowed": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _F, _I]),
+    "aljabr_rocm_fa4_sdpa_available": (_I, []),
+    "aljabr_rocm_fa4_bf16_available": (_I, []),
     "aljabr_rocm_paged_attention": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _F]),
     "aljabr_rocm_paged_attention_windowed": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _I,
                                                   _I, _F]),

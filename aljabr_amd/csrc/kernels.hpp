@@ -66,6 +66,9 @@ struct KqOut {
     int n;
 };
 int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate);
+// False when ALJABR_ROCM_FA_GENERIC=1 routes prefill attention through the
+// generic kernel.
+bool fa_prefill_enabled();
 // y = cap * tanh(y / cap) elementwise.
 int enqueue_softcap(float *y, long long n, float cap);
 // K-split tile kernels for M <= 2 (ALJABR_ROCM_ERR_UNSUPPORTED when the shape

@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -23,6 +24,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TF = 2500.0   # MI355X dense fp16 matrix-core peak
 K_MODEL, FFN = 4096, 14336
 BLOCK = 64
 KERNEL = "rows_kernel"              # the batch-1 kernel these launches dispatch to (matvec_rows.hip)
@@ -58,6 +60,8 @@ def parse() -> argparse.Namespace:
                     help="run only the GGUF Q4_K_M decode measurement (for profiling)")
     ap.add_argument("--kquant-only", action="store_true",
                     help="run only the GGUF Q4_0/Q8_0 and K-quant matvec/GEMM measurements (for profiling)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the prefill attention measurement (for profiling)")
     return ap.parse_args()
 
 
@@ -321,6 +325,44 @@ def attention_bench(abi, torch, stream, launches=20):
     return out
 
 
+def prefill_bench(abi, torch, stream, launches=5):
+    """Prefill (FA4) attention at the Llama-3-8B head layout: B = 1, 32 query
+    heads over 8 KV heads, D = 128, causal, T = S, fp32 Q/K/V ~ N(0,1),
+    scale 1/sqrt(128). Algorithmic flops = 4 * D * H * (visible (query, key)
+    pairs), against the fp16 dense matrix-core peak (the kernel issues three
+    fp16 MFMAs per product for fp32 accuracy)."""
+    lib = abi.load()
+    h, hkv, d = 32, 8, 128
+    out = {}
+    for t in (512, 2048, 8192):
+        q = torch.randn(t * h * d, device="cuda:0")
+        k = torch.randn(t * hkv * d, device="cuda:0")
+        v = torch.randn(t * hkv * d, device="cuda:0")
+        o = torch.empty_like(q)
+        torch.cuda.synchronize()
+
+        def launch():
+            rc = lib.aljabr_rocm_fa4_attention(o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), 1, t, t, h,
+                                               hkv, d, 1.0 / math.sqrt(d), 1, 0, 0.0)
+            if rc:
+                abi.check(rc, "aljabr_rocm_fa4_attention")
+        launch()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(launches):
+            launch()
+        end.record(stream)
+        end.synchronize()
+        us = start.elapsed_time(end) * 1000.0 / launches
+        pairs = t * (t + 1) // 2
+        flops = 4.0 * d * h * pairs
+        tf = flops / us / 1e6
+        out[f"t{t}"] = {"us": round(us, 1), "TFLOPs": round(tf, 1), "frac_fp16_peak": round(tf / MFMA_F16_PEAK_TF, 4)}
+        del q, k, v, o
+        torch.cuda.empty_cache()
+    return out
+
+
 def traffic_record(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
     summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor), or
@@ -491,6 +533,8 @@ def main() -> None:
         elif args.kquant_only:
             print(json.dumps({"gguf_q4_0_q8_0": gguf_q_bench(abi, torch, stream),
                               "gguf_kquant": kquant_bench(abi, torch, stream)}), flush=True)
+        elif args.prefill_only:
+            print(json.dumps({"prefill_attention": prefill_bench(abi, torch, stream)}), flush=True)
         elif args.gguf_decode_only:
             print(json.dumps({"decode_gguf_q4_k_m": gguf_decode_runs(args, abi, torch, stream)}), flush=True)
         else:
@@ -546,6 +590,8 @@ def run(args, abi, torch, stream) -> None:
         result["gguf_q4_0_q8_0"] = gguf_q_bench(abi, torch, stream)
         log("GGUF K-quant matvec (Q4_K, Q6_K; M = 1, 4, 8)")
         result["gguf_kquant"] = kquant_bench(abi, torch, stream)
+        log("prefill attention (T = S = 512, 2048, 8192)")
+        result["prefill_attention"] = prefill_bench(abi, torch, stream)
 
     if not args.no_decode:
         result["decode"] = decode_runs(args, abi, torch, stream)

@@ -220,6 +220,34 @@ int aljabr_rocm_paged_attention_gqa_windowed(void *out, const void *Q, const voi
                                              float soft_cap);
 
 /* ======================================================================== */
+/* Prefill attention (replaces MTLC/aljabr_metal_fa4.m:253-257,542-556)      */
+/* ======================================================================== */
+
+/* out[B,T,H,D] = softmax(scale * Q K^T) V per head, Q [B,T,H,D], K/V
+ * [B,S,H_kv,D] device pointers, all fp32, H % H_kv == 0 (query head h reads
+ * KV head h / (H / H_kv)). With is_causal, row t sees keys
+ * [0, min(max(S - T, 0) + t + 1, S)), the bottom-right limit of
+ * aljabr_metal_fa4.m:111-115; soft_cap > 0 maps each kept score to
+ * cap * tanh(score / cap) first. use_bf16 is accepted and ignored: results
+ * are fp32-accurate. Flash-style on the matrix cores for D = 64 and 128
+ * (16-byte aligned pointers), a generic kernel for other D <= 256.
+ * Replaces aljabr_metal_fa4_attention (same argument order). */
+int aljabr_rocm_fa4_attention(void *output, const void *query, const void *key, const void *value, int B, int T,
+                              int S, int H, int H_kv, int D, float scale, int is_causal, int use_bf16,
+                              float soft_cap);
+/* The same with a sliding window: row t sees keys [max(hi - window, 0), hi)
+ * where hi is the limit above (window <= 0: no window). No Metal
+ * counterpart; it serves the windowed prefill the GGUF runner otherwise runs
+ * on the CPU (GJB/GgufPrefillAttentionExecution.java:33-78). */
+int aljabr_rocm_fa4_attention_windowed(void *output, const void *query, const void *key, const void *value, int B,
+                                       int T, int S, int H, int H_kv, int D, float scale, int is_causal,
+                                       float soft_cap, int window);
+/* 1: the fused path is available (aljabr_metal_fa4_sdpa_available). */
+int aljabr_rocm_fa4_sdpa_available(void);
+/* 0: no reduced-precision bf16 arithmetic is offered (aljabr_metal_fa4_bf16_available). */
+int aljabr_rocm_fa4_bf16_available(void);
+
+/* ======================================================================== */
 /* decode-step element-wise ops (fp32)                                       */
 /* ======================================================================== */
 

@@ -80,6 +80,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "orc_softcap": (None, [_P, _I64, _F]),
         "orc_attention_gqa": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                             ctypes.c_int, _P, ctypes.c_int]),
+        "orc_fa4_attention": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F, _I32, _F, _I32,
+                                             _P]),
         "orc_paged_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F,
                                                _I32, _I32, _I32, _F, _P]),
         "orc_rmsnorm": (None, [_P, _P, _P, _I32, _F]),
@@ -294,6 +296,22 @@ def paged_attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, block_table: 
                                    bt.shape[1], scale, int(bool(causal)), query_start_pos, sliding_window,
                                    soft_cap, _ptr(out))
     return rc, out
+
+
+def fa4_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, causal: bool = True,
+                  soft_cap: float = 0.0, window: int = 0) -> np.ndarray:
+    """q [B,T,H,D], k/v [B,S,Hkv,D] float32 -> out [B,T,H,D] (FA4 prefill semantics)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    b, t, h, d = q.shape
+    s, hkv = k.shape[1], k.shape[2]
+    out = np.full_like(q, np.nan)
+    rc = lib().orc_fa4_attention(_ptr(q), _ptr(k), _ptr(v), b, t, s, h, hkv, d, scale, int(bool(causal)), soft_cap,
+                                 window, _ptr(out))
+    if rc != 0:
+        raise ValueError(f"orc_fa4_attention rejected the shape (status {rc})")
+    return out
 
 
 # ---- element-wise ---------------------------------------------------------

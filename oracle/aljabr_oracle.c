@@ -683,6 +683,63 @@ int orc_attention_gqa(const float *q, const float *k, const float *v,
     return 0;
 }
 
+/* FA4 prefill attention as the Metal backend's fallback computes it
+ * (MTLC/aljabr_metal_fa4.m:466-530): per (b, h) the scores scale * q.k over
+ * all S keys, keys from the causal limit on excluded
+ * (causal_limit_for_row, :111-115), the soft cap cap * tanh(s / cap) on the
+ * kept scores, softmax by exp(s - max) / sum, then the weighted sum of V rows.
+ * Sums are carried in double. */
+int orc_fa4_attention(const float *q, const float *k, const float *v, int32_t b_n, int32_t t_n, int32_t s_n,
+                      int32_t h_n, int32_t hkv, int32_t d, float scale, int32_t is_causal, float soft_cap,
+                      int32_t window, float *out) {
+    if (b_n <= 0 || t_n <= 0 || s_n <= 0 || h_n <= 0 || hkv <= 0 || d <= 0 || h_n % hkv != 0) return -1;
+    int32_t group = h_n / hkv;
+    float *row = (float *)malloc((size_t)s_n * sizeof(float));
+    double *acc = (double *)malloc((size_t)d * sizeof(double));
+    if (!row || !acc) {
+        free(row);
+        free(acc);
+        return -1;
+    }
+    for (int32_t b = 0; b < b_n; b++)
+        for (int32_t h = 0; h < h_n; h++) {
+            int32_t kvh = h / group;
+            for (int32_t t = 0; t < t_n; t++) {
+                const float *qr = q + (((int64_t)b * t_n + t) * h_n + h) * d;
+                float *orow = out + (((int64_t)b * t_n + t) * h_n + h) * d;
+                int32_t hi = s_n;
+                if (is_causal) {
+                    int32_t lim = (s_n > t_n ? s_n - t_n : 0) + t + 1;
+                    hi = lim < s_n ? lim : s_n;
+                }
+                int32_t lo = 0;
+                if (window > 0) lo = hi - window > 0 ? hi - window : 0;
+                float mx = -INFINITY;
+                for (int32_t s = lo; s < hi; s++) {
+                    const float *kr = k + (((int64_t)b * s_n + s) * hkv + kvh) * d;
+                    double dot = 0.0;
+                    for (int32_t e = 0; e < d; e++) dot += (double)qr[e] * kr[e];
+                    float sc = (float)dot * scale;
+                    if (soft_cap > 0.0f) sc = soft_cap * tanhf(sc / soft_cap);
+                    row[s] = sc;
+                    if (sc > mx) mx = sc;
+                }
+                double sum = 0.0;
+                for (int32_t e = 0; e < d; e++) acc[e] = 0.0;
+                for (int32_t s = lo; s < hi; s++) {
+                    double p = exp((double)row[s] - (double)mx);
+                    sum += p;
+                    const float *vr = v + (((int64_t)b * s_n + s) * hkv + kvh) * d;
+                    for (int32_t e = 0; e < d; e++) acc[e] += p * vr[e];
+                }
+                for (int32_t e = 0; e < d; e++) orow[e] = sum > 0.0 ? (float)(acc[e] / sum) : 0.0f;
+            }
+        }
+    free(row);
+    free(acc);
+    return 0;
+}
+
 /* Paged-KV attention of the Metal bridge's CPU path
  * (MTLC/aljabr_metal_attention.m:146-160 resolve_attention_bounds, :162-355
  * aljabr_metal_attention_impl): Q/out [B,T,H,D], caches [phys][H_kv][bs][D]

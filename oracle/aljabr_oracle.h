@@ -140,6 +140,14 @@ int orc_paged_attention(const float *q, const float *kc, const float *vc, const 
                         const int32_t *context_lens, int32_t b_n, int32_t t_n, int32_t h_n, int32_t hkv,
                         int32_t d, int32_t block_size, int32_t max_blocks, float scale, int32_t is_causal,
                         int32_t query_start_pos, int32_t sliding_window, float soft_cap, float *out);
+/* Prefill (FA4) attention, MTLC/aljabr_metal_fa4.m:111-115,466-530: Q/out
+ * [B,T,H,D], K/V [B,S,H_kv,D] float32; row t sees keys [lo, hi) with hi = S or,
+ * causal, min(max(S - T, 0) + t + 1, S); lo = 0, or max(hi - window, 0) for
+ * window > 0 (an extension the Metal entry point does not have). Returns 0,
+ * or -1 for a shape it rejects. */
+int orc_fa4_attention(const float *q, const float *k, const float *v, int32_t b_n, int32_t t_n, int32_t s_n,
+                      int32_t h_n, int32_t hkv, int32_t d, float scale, int32_t is_causal, float soft_cap,
+                      int32_t window, float *out);
 
 /* ---- decode-step element-wise ops --------------------------------------- */
 
