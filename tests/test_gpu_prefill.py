@@ -1,9 +1,10 @@
 """GPU parity of the prefill (FA4) attention entry points against the oracle
 on identical seeded inputs: relative L2 <= 1e-3 per case (fp32 outputs).
-Covers the matrix-core kernel (D = 64 and 128: causal T = S, chunked prefill
-S > T, T > S, partial tiles and blocks, MHA / GQA / G = 8, batches, soft cap,
-windows, non-causal) and the generic kernel (other D, unaligned pointers, the
-reference's uniform-attention fixture). At the Llama-3-8B prefill size the
+Covers the matrix-core kernel (D = 64 and 128, one and two row tiles per
+wave: causal T = S, chunked prefill S > T, T > S, partial tiles and blocks,
+MHA / GQA / G = 8, batches, soft cap, windows, non-causal) and the generic
+kernel (other D, unaligned pointers, the reference's uniform-attention
+fixture). At the Llama-3-8B prefill size the
 rows are checked one by one on a sample against one-row oracle problems."""
 from __future__ import annotations
 
@@ -47,6 +48,9 @@ CASES = [
     (1, 130, 257, 16, 2, 64, False),    # non-causal, G = 8
     (1, 1, 333, 8, 2, 128, True),       # one query row
     (3, 33, 40, 2, 2, 64, True),
+    # grids of at least four workgroups per CU take two 32-row tiles per wave
+    (8, 300, 300, 64, 8, 128, True),
+    (8, 260, 400, 64, 16, 64, True),
 ]
 
 
