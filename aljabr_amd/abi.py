@@ -136,6 +136,15 @@ SIGNATURES = {
     "aljabr_rocm_dequantize": (_I, [_P, _P, _P, _LL, _I, _I]),
     "aljabr_rocm_quantize": (_I, [_P, _P, _P, _LL, _I, _I]),
     "aljabr_rocm_attention_gqa": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I]),
+    "aljabr_rocm_safetensors_open": (_I, [ctypes.c_char_p, _P]),
+    "aljabr_rocm_safetensors_close": (_I, [_P]),
+    "aljabr_rocm_safetensors_tensor_count": (_I, [_P, _P]),
+    "aljabr_rocm_safetensors_find_tensor": (_I, [_P, ctypes.c_char_p, _P]),
+    "aljabr_rocm_safetensors_tensor_info": (_I, [_P, ctypes.c_int64, _P, _I, _P, _P, _P, _P]),
+    "aljabr_rocm_safetensors_tensor_data": (_I, [_P, ctypes.c_int64, _P]),
+    "aljabr_rocm_safetensors_meta": (_I, [_P, ctypes.c_char_p, _P, _I]),
+    "aljabr_rocm_safetensors_upload_nf4": (_I, [_P, ctypes.c_char_p, _P, _P, _P, _P, _P]),
+    "aljabr_rocm_llama_create_safetensors": (_I, [ctypes.c_char_p, _P, _P]),
     "aljabr_rocm_fa4_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _I, _F]),
     "aljabr_rocm_fa4_attention_windowed": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _F, _I]),
     "aljabr_rocm_fa4_sdpa_available": (_I, []),

@@ -23,6 +23,7 @@
 #include "device.hpp"
 #include "gguf.hpp"
 #include "internal.hpp"
+#include "safetensors.hpp"
 #include "kernels.hpp"
 
 namespace aljabr {
@@ -465,6 +466,197 @@ int aljabr_rocm_llama_create_gguf(const char *path, int max_batch, int max_seq, 
 
     // needs[] order: embedding, 9 per layer, output norm, [output].
     auto tensor = [&](size_t i) { return aljabr_rocm_tensor{dev[i], nullptr, needs[i].t->type, 0}; };
+    std::vector<aljabr_rocm_tensor> t(static_cast<size_t>(7) * L);
+    std::vector<const void *> an(L), fn(L);
+    for (int l = 0; l < L; ++l) {
+        const size_t b = 1 + 9 * static_cast<size_t>(l);
+        an[l] = dev[b];
+        t[0 * L + l] = tensor(b + 1);
+        t[1 * L + l] = tensor(b + 2);
+        t[2 * L + l] = tensor(b + 3);
+        t[3 * L + l] = tensor(b + 4);
+        fn[l] = dev[b + 5];
+        t[4 * L + l] = tensor(b + 6);
+        t[5 * L + l] = tensor(b + 7);
+        t[6 * L + l] = tensor(b + 8);
+    }
+    const size_t on = 1 + 9 * static_cast<size_t>(L);
+    aljabr_rocm_llama_tensors tw{};
+    tw.tok_embed = tensor(0);
+    tw.attn_norm = an.data();
+    tw.ffn_norm = fn.data();
+    tw.wq = &t[0 * L];
+    tw.wk = &t[1 * L];
+    tw.wv = &t[2 * L];
+    tw.wo = &t[3 * L];
+    tw.w_gate = &t[4 * L];
+    tw.w_up = &t[5 * L];
+    tw.w_down = &t[6 * L];
+    tw.out_norm = dev[on];
+    tw.lm_head = tied ? tensor(0) : tensor(on + 1);
+    aljabr_rocm_llama *m = nullptr;
+    rc = create_session(c, &tw, &m);
+    if (rc != ALJABR_ROCM_OK) {
+        (void)hipFree(base);
+        return rc;
+    }
+    m->weights_owned = base;
+    *out = m;
+    return ALJABR_ROCM_OK;
+}
+
+// A Llama model from a safetensors file with Hugging Face tensor names and
+// NF4 projections in the safetensor engine's convention (AccelWeightBridge.
+// java:184-222: "<name>.qweight" U8 [out, in/2] + "<name>.scales" fp32, group
+// 128), dense projections F32 / F16 / BF16 (BF16 widened to fp32 exactly),
+// norms and the embedding dense, the LM head dense, NF4 or tied to the
+// embedding. The architecture comes from `cfg` (a safetensors file carries
+// none); nf4_block is 128. Q and K rows are used as stored: the decode step's
+// RoPE rotates (i, i + head_dim/2) pairs, the Hugging Face layout.
+int aljabr_rocm_llama_create_safetensors(const char *path, const aljabr_rocm_llama_config *cfg,
+                                         aljabr_rocm_llama **out) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(path && cfg && out, "path, cfg and out must be non-null");
+    *out = nullptr;
+    StFile *raw = nullptr;
+    int rc = st_open(path, &raw);
+    if (rc != ALJABR_ROCM_OK) return rc;
+    std::unique_ptr<StFile> f(raw);
+    aljabr_rocm_llama_config c = *cfg;
+    c.nf4_block = 128;
+    rc = validate_config(c);
+    if (rc != ALJABR_ROCM_OK) return rc;
+    for (const char *extra : {"model.layers.0.self_attn.q_norm.weight", "model.layers.0.self_attn.k_norm.weight",
+                              "model.layers.0.self_attn.q_proj.bias", "model.layers.0.self_attn.k_proj.bias",
+                              "model.layers.0.self_attn.v_proj.bias", "model.layers.0.pre_feedforward_layernorm.weight",
+                              "model.layers.0.post_feedforward_layernorm.weight"})
+        if (f->find(extra))
+            return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "safetensors: %s has %s, which this decode step does not apply",
+                        path, extra);
+    const int L = c.layers;
+    const int64_t qd = static_cast<int64_t>(c.n_heads) * c.head_dim, kvd = static_cast<int64_t>(c.n_kv_heads) * c.head_dim;
+
+    // Every tensor the step reads: dense (`w`), or NF4 codes + scales.
+    struct Need {
+        const StTensor *w, *scales;
+        int64_t n, k;           // rows, row length (norms: n = 1)
+        int type;               // device type: F32, F16 or NF4
+        bool norm;
+    };
+    std::vector<Need> needs;
+    auto dense_type = [](int dt) {
+        return dt == kStF32 || dt == kStBF16 ? ALJABR_ROCM_TYPE_F32 : dt == kStF16 ? ALJABR_ROCM_TYPE_F16 : -1;
+    };
+    auto want_norm = [&](const std::string &name) -> int {
+        const StTensor *t = f->find(name);
+        if (!t) return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "safetensors: %s: missing tensor %s", path, name.c_str());
+        if (t->shape.size() != 1 || t->shape[0] != c.dim || dense_type(t->dtype) < 0)
+            return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "safetensors: %s: %s must be a [%d] F32/F16/BF16 vector", path,
+                        name.c_str(), c.dim);
+        needs.push_back({t, nullptr, 1, c.dim, ALJABR_ROCM_TYPE_F32, true});
+        return ALJABR_ROCM_OK;
+    };
+    auto want_matrix = [&](const std::string &base, int64_t n, int64_t k, bool allow_nf4) -> int {
+        const StTensor *q = f->find(base + ".qweight");
+        if (q) {
+            const StTensor *sc = f->find(base + ".scales");
+            if (!allow_nf4)
+                return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "safetensors: %s: %s is NF4, which the embedding rows cannot "
+                            "read", path, base.c_str());
+            if (!sc || q->dtype != kStU8 || q->shape.size() != 2 || q->shape[0] != n || 2 * q->shape[1] != k)
+                return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "safetensors: %s: %s.qweight must be U8 [%lld, %lld] with "
+                            "%s.scales", path, base.c_str(), static_cast<long long>(n), static_cast<long long>(k / 2),
+                            base.c_str());
+            if (sc->dtype != kStF32 || k % c.nf4_block != 0 ||
+                static_cast<int64_t>((sc->end - sc->begin) / 4) != n * k / c.nf4_block)
+                return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "safetensors: %s: %s.scales must hold one F32 absmax per "
+                            "%d weights", path, base.c_str(), c.nf4_block);
+            needs.push_back({q, sc, n, k, ALJABR_ROCM_TYPE_NF4, false});
+            return ALJABR_ROCM_OK;
+        }
+        const StTensor *t = f->find(base + ".weight");
+        if (!t) return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "safetensors: %s: missing tensor %s.weight / .qweight", path,
+                            base.c_str());
+        if (t->shape.size() != 2 || t->shape[0] != n || t->shape[1] != k || dense_type(t->dtype) < 0)
+            return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "safetensors: %s: %s.weight must be a [%lld, %lld] F32/F16/BF16 "
+                        "matrix", path, base.c_str(), static_cast<long long>(n), static_cast<long long>(k));
+        needs.push_back({t, nullptr, n, k, dense_type(t->dtype), false});
+        return ALJABR_ROCM_OK;
+    };
+    rc = want_matrix("model.embed_tokens", c.vocab, c.dim, false);
+    for (int l = 0; l < L && rc == ALJABR_ROCM_OK; ++l) {
+        const std::string b = "model.layers." + std::to_string(l) + ".";
+        rc = want_norm(b + "input_layernorm.weight");
+        if (rc == ALJABR_ROCM_OK) rc = want_matrix(b + "self_attn.q_proj", qd, c.dim, true);
+        if (rc == ALJABR_ROCM_OK) rc = want_matrix(b + "self_attn.k_proj", kvd, c.dim, true);
+        if (rc == ALJABR_ROCM_OK) rc = want_matrix(b + "self_attn.v_proj", kvd, c.dim, true);
+        if (rc == ALJABR_ROCM_OK) rc = want_matrix(b + "self_attn.o_proj", c.dim, qd, true);
+        if (rc == ALJABR_ROCM_OK) rc = want_norm(b + "post_attention_layernorm.weight");
+        if (rc == ALJABR_ROCM_OK) rc = want_matrix(b + "mlp.gate_proj", c.ffn, c.dim, true);
+        if (rc == ALJABR_ROCM_OK) rc = want_matrix(b + "mlp.up_proj", c.ffn, c.dim, true);
+        if (rc == ALJABR_ROCM_OK) rc = want_matrix(b + "mlp.down_proj", c.dim, c.ffn, true);
+    }
+    if (rc == ALJABR_ROCM_OK) rc = want_norm("model.norm.weight");
+    const bool tied = !f->find("lm_head.weight") && !f->find("lm_head.qweight");
+    if (rc == ALJABR_ROCM_OK && !tied) rc = want_matrix("lm_head", c.vocab, c.dim, true);
+    if (rc != ALJABR_ROCM_OK) return rc;
+
+    // One device allocation: dense tensors as F32 (BF16 widened) or F16,
+    // NF4 codes then absmax; 256-byte aligned pieces.
+    auto main_bytes = [](const Need &n) -> uint64_t {
+        const uint64_t e = static_cast<uint64_t>(n.n) * n.k;
+        return n.type == ALJABR_ROCM_TYPE_NF4 ? e / 2 : n.type == ALJABR_ROCM_TYPE_F16 ? 2 * e : 4 * e;
+    };
+    auto align = [](uint64_t v) { return (v + 255) & ~uint64_t(255); };
+    uint64_t total = 0;
+    for (const Need &n : needs) total += align(main_bytes(n)) + (n.scales ? align(n.scales->end - n.scales->begin) : 0);
+    void *base = nullptr;
+    hipError_t e = hipMalloc(&base, total);
+    if (e != hipSuccess)
+        return fail(ALJABR_ROCM_ERR_BUFFER, "safetensors: hipMalloc(%llu) for the weights: %s",
+                    static_cast<unsigned long long>(total), hipGetErrorString(e));
+    std::vector<const void *> dev(needs.size()), dev_s(needs.size(), nullptr);
+    uint64_t off = 0;
+    std::vector<float> tmp;
+    for (size_t i = 0; i < needs.size() && e == hipSuccess; ++i) {
+        const Need &n = needs[i];
+        char *dst = static_cast<char *>(base) + off;
+        dev[i] = dst;
+        const uint8_t *src = f->data(*n.w);
+        if (n.w->dtype == kStBF16 || (n.norm && n.w->dtype == kStF16)) {
+            const size_t cnt = static_cast<size_t>(n.n * n.k);
+            tmp.resize(cnt);
+            for (size_t j = 0; j < cnt; ++j) {
+                uint16_t bits;
+                std::memcpy(&bits, src + 2 * j, 2);
+                if (n.w->dtype == kStBF16) {
+                    const uint32_t wide = static_cast<uint32_t>(bits) << 16;
+                    std::memcpy(&tmp[j], &wide, 4);
+                } else {
+                    tmp[j] = half_to_float(bits);
+                }
+            }
+            e = hipMemcpy(dst, tmp.data(), cnt * 4, hipMemcpyHostToDevice);
+        } else {
+            e = hipMemcpy(dst, src, static_cast<size_t>(main_bytes(n)), hipMemcpyHostToDevice);
+        }
+        off += align(main_bytes(n));
+        if (n.scales && e == hipSuccess) {
+            char *sd = static_cast<char *>(base) + off;
+            dev_s[i] = sd;
+            e = hipMemcpy(sd, f->data(*n.scales), n.scales->end - n.scales->begin, hipMemcpyHostToDevice);
+            off += align(n.scales->end - n.scales->begin);
+        }
+    }
+    if (e != hipSuccess) {
+        (void)hipFree(base);
+        return fail(ALJABR_ROCM_ERR_DEVICE, "safetensors: uploading weights: %s", hipGetErrorString(e));
+    }
+
+    // needs[] order: embedding, 9 per layer, final norm, [lm_head].
+    auto tensor = [&](size_t i) {
+        return aljabr_rocm_tensor{dev[i], dev_s[i], needs[i].type, needs[i].type == ALJABR_ROCM_TYPE_NF4 ? c.nf4_block : 0};
+    };
     std::vector<aljabr_rocm_tensor> t(static_cast<size_t>(7) * L);
     std::vector<const void *> an(L), fn(L);
     for (int l = 0; l < L; ++l) {

@@ -132,6 +132,22 @@ class DeviceLlama:
         return cls._wrap(handle, cfg, max_batch, c.max_seq, None)
 
     @classmethod
+    def from_safetensors(cls, path: str, cfg: dict, max_batch: int, max_seq: int):
+        """A session over a safetensors file with Hugging Face Llama names and
+        NF4 or dense projections (aljabr_rocm_llama_create_safetensors); the
+        architecture comes from `cfg` (layers, dim, ffn, n_heads, n_kv_heads,
+        head_dim, vocab, rope_base, eps) and the library owns the weights."""
+        lib = abi.load()
+        c = abi.LlamaConfig(cfg["layers"], cfg["dim"], cfg["ffn"], cfg["n_heads"], cfg["n_kv_heads"],
+                            cfg["head_dim"], cfg["vocab"], max_seq, 128, max_batch, cfg["rope_base"], cfg["eps"])
+        handle = ctypes.c_void_p()
+        abi.check(lib.aljabr_rocm_llama_create_safetensors(path.encode(), ctypes.byref(c), ctypes.byref(handle)),
+                  "aljabr_rocm_llama_create_safetensors")
+        abi.check(lib.aljabr_rocm_llama_config_get(handle, ctypes.byref(c)), "aljabr_rocm_llama_config_get")
+        full = {name: getattr(c, name) for name, _ in abi.LlamaConfig._fields_}
+        return cls._wrap(handle, full, max_batch, max_seq, None)
+
+    @classmethod
     def typed(cls, cfg: dict, weights: dict, max_batch: int, max_seq: int):
         """A session over typed device weights (aljabr_rocm_llama_create_typed):
         tok_embed and lm_head are (type, tensor) pairs, the PROJ lists hold

@@ -220,6 +220,55 @@ int aljabr_rocm_paged_attention_gqa_windowed(void *out, const void *Q, const voi
                                              float soft_cap);
 
 /* ======================================================================== */
+/* safetensors files (replaces engine/safetensor/aljabr-safetensor-loader/   */
+/* .../SafetensorHeaderParser.java:13-160 and the NF4 path of                */
+/* aljabr-safetensor-bridge/.../AccelWeightBridge.java:184-222)              */
+/* ======================================================================== */
+
+/* dtype ids, in the order of the reference's SafetensorDType enum */
+#define ALJABR_ROCM_ST_BF16 0
+#define ALJABR_ROCM_ST_F16 1
+#define ALJABR_ROCM_ST_F32 2
+#define ALJABR_ROCM_ST_F64 3
+#define ALJABR_ROCM_ST_F8_E4M3 4
+#define ALJABR_ROCM_ST_F8_E5M2 5
+#define ALJABR_ROCM_ST_I8 6
+#define ALJABR_ROCM_ST_I16 7
+#define ALJABR_ROCM_ST_I32 8
+#define ALJABR_ROCM_ST_I64 9
+#define ALJABR_ROCM_ST_U8 10
+#define ALJABR_ROCM_ST_U16 11
+#define ALJABR_ROCM_ST_U32 12
+#define ALJABR_ROCM_ST_U64 13
+#define ALJABR_ROCM_ST_BOOL 14
+
+typedef struct aljabr_rocm_safetensors aljabr_rocm_safetensors;
+
+/* Maps `path` read-only and parses it: u64 little-endian header length (at
+ * most 100 MiB), JSON {name: {dtype, shape, data_offsets}, "__metadata__":
+ * {string: string}}; every range inside the file, equal to shape x dtype
+ * size, none overlapping. -2 with a message for a malformed file. */
+int aljabr_rocm_safetensors_open(const char *path, aljabr_rocm_safetensors **out);
+int aljabr_rocm_safetensors_close(aljabr_rocm_safetensors *f);
+int aljabr_rocm_safetensors_tensor_count(const aljabr_rocm_safetensors *f, int64_t *count);
+int aljabr_rocm_safetensors_find_tensor(const aljabr_rocm_safetensors *f, const char *name, int64_t *index);
+/* Name (NUL-terminated, truncated to name_cap), dtype id, rank, dims[8]
+ * (unused entries 0) and byte size of tensor `index`; outputs may be null. */
+int aljabr_rocm_safetensors_tensor_info(const aljabr_rocm_safetensors *f, int64_t index, char *name, int name_cap,
+                                        int32_t *dtype, int32_t *n_dims, int64_t *dims, uint64_t *bytes);
+/* Host pointer to the tensor's bytes inside the mapping (valid until close). */
+int aljabr_rocm_safetensors_tensor_data(const aljabr_rocm_safetensors *f, int64_t index, const void **host_data);
+/* Value of a "__metadata__" key into `value` (value_cap bytes, NUL-terminated). */
+int aljabr_rocm_safetensors_meta(const aljabr_rocm_safetensors *f, const char *key, char *value, int value_cap);
+/* The NF4 weight "<base_name>.qweight" (U8 [N, K/2], two codes a byte, high
+ * nibble first) + "<base_name>.scales" (F32, one absmax per 128 weights)
+ * copied to two new device buffers the caller frees with aljabr_rocm_free;
+ * rows = N, cols = K, block_size = 128, the layout every NF4 entry point
+ * takes (AccelWeightBridge.attachQuantizationMetadata). */
+int aljabr_rocm_safetensors_upload_nf4(const aljabr_rocm_safetensors *f, const char *base_name, void **codes,
+                                       void **absmax, int64_t *rows, int64_t *cols, int32_t *block_size);
+
+/* ======================================================================== */
 /* Prefill attention (replaces MTLC/aljabr_metal_fa4.m:253-257,542-556)      */
 /* ======================================================================== */
 
@@ -378,6 +427,18 @@ int aljabr_rocm_gguf_meta_string(const aljabr_rocm_gguf *g, const char *key, cha
  * per-head norms, post norms, RoPE frequency tensors, partial RoPE or biases
  * give -3: the step does not apply them. */
 int aljabr_rocm_llama_create_gguf(const char *path, int max_batch, int max_seq, aljabr_rocm_llama **out);
+/* A session from a safetensors file with Hugging Face Llama names
+ * (model.embed_tokens, model.layers.N.{input_layernorm, self_attn.{q,k,v,o}_proj,
+ * post_attention_layernorm, mlp.{gate,up,down}_proj}, model.norm, lm_head,
+ * absent: tied), architecture from `cfg` (nf4_block is forced to 128).
+ * Projections and the LM head are NF4 pairs "<name>.qweight" U8 +
+ * "<name>.scales" F32 (AccelWeightBridge.java:184-222) or dense ".weight"
+ * F32/F16/BF16 (BF16 widened to fp32); norms and the embedding dense. Q/K
+ * rows are used as stored (the step's RoPE rotates (i, i + head_dim/2)).
+ * Per-head norms or biases give -3. Weights are uploaded once into memory the
+ * session owns. */
+int aljabr_rocm_llama_create_safetensors(const char *path, const aljabr_rocm_llama_config *cfg,
+                                         aljabr_rocm_llama **out);
 /* The session's configuration (e.g. of a session made from a file). */
 int aljabr_rocm_llama_config_get(const aljabr_rocm_llama *m, aljabr_rocm_llama_config *cfg);
 

@@ -427,7 +427,8 @@ class TypedLlamaOracle:
     GgmlTypes, restated): ``weights`` maps tok_embed, lm_head and the
     per-layer lists wq, wk, wv, wo, w_gate, w_up, w_down to (type, array)
     pairs (type ids as ALJABR_ROCM_TYPE_*: 0 F32, 1 F16 (uint16 bits), 2 Q4_0,
-    8 Q8_0, 12 Q4_K, 14 Q6_K (bytes)) and attn_norm, ffn_norm (lists) and
+    8 Q8_0, 12 Q4_K, 14 Q6_K (bytes)), or (100, codes, absmax) triples for
+    NF4 with block cfg["nf4_block"], and attn_norm, ffn_norm (lists) and
     out_norm to fp32 arrays."""
 
     MATS = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
@@ -439,6 +440,13 @@ class TypedLlamaOracle:
         self._keep = []
 
         def tensor(pair):
+            if len(pair) == 3:                       # NF4: (100, codes, absmax), block cfg["nf4_block"]
+                t, arr, absmax = pair
+                absmax = np.ascontiguousarray(absmax, np.float32)
+                self._keep.append(absmax)
+                arr = np.ascontiguousarray(arr)
+                self._keep.append(arr)
+                return _Tensor(arr.ctypes.data, absmax.ctypes.data, t, cfg.get("nf4_block", 64))
             t, arr = pair
             arr = np.ascontiguousarray(arr)
             self._keep.append(arr)
