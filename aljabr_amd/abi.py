@@ -136,6 +136,11 @@ SIGNATURES = {
     "aljabr_rocm_dequantize": (_I, [_P, _P, _P, _LL, _I, _I]),
     "aljabr_rocm_quantize": (_I, [_P, _P, _P, _LL, _I, _I]),
     "aljabr_rocm_attention_gqa": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I]),
+    "aljabr_rocm_matvec_tb_pair": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
+    "aljabr_rocm_matvec_tb_triple": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I]),
+    "aljabr_rocm_matvec_tb_triple_batch": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I]),
+    "aljabr_rocm_ffn_gated_fused": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
+    "aljabr_rocm_ffn_gated_fused_batch": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I]),
     "aljabr_rocm_safetensors_open": (_I, [ctypes.c_char_p, _P]),
     "aljabr_rocm_safetensors_close": (_I, [_P]),
     "aljabr_rocm_safetensors_tensor_count": (_I, [_P, _P]),

@@ -220,6 +220,34 @@ int aljabr_rocm_paged_attention_gqa_windowed(void *out, const void *Q, const voi
                                              float soft_cap);
 
 /* ======================================================================== */
+/* Several matrices over one input (replaces MTLC/aljabr_metal_matvec_api.h: */
+/* 83-120): device pointers; types F32 0, F16 1, Q4_0 2, Q8_0 8, Q4_K 12,    */
+/* Q6_K 14. Matrices of one type share a launch.                             */
+/* ======================================================================== */
+
+/* C_i[N_i] = B_i[N_i][K] . A[K] for i = 0, 1 (the gate/up pair). */
+int aljabr_rocm_matvec_tb_pair(void *C0, void *C1, const void *A, const void *B0, const void *B1, int K, int N0,
+                               int N1, int type0, int type1);
+/* The same for three matrices (Q/K/V). */
+int aljabr_rocm_matvec_tb_triple(void *C0, void *C1, void *C2, const void *A, const void *B0, const void *B1,
+                                 const void *B2, int K, int N0, int N1, int N2, int type0, int type1, int type2);
+/* Batched: A [batchSize][K], C_i [batchSize][N_i]. */
+int aljabr_rocm_matvec_tb_triple_batch(void *C0, void *C1, void *C2, const void *A, const void *B0, const void *B1,
+                                       const void *B2, int K, int N0, int N1, int N2, int type0, int type1, int type2,
+                                       int batchSize);
+/* outDown[dim] = W_down[dim][ffnDim] . (act(W_gate . inA) * (W_up . inA)),
+ * act = SiLU (g / (1 + e^-g), 0 below -20, g above 20) or, for
+ * activationKind 2, the tanh GELU (0 below -10, g above 10); a non-finite
+ * product becomes 0 (aljabr_metal_kernel_source.m:72-108). inA and outDown
+ * are device pointers here (the Metal call copies host arrays). */
+int aljabr_rocm_ffn_gated_fused(void *outDown, const void *inA, const void *gateW, const void *upW, const void *downW,
+                                int dim, int ffnDim, int typeGate, int typeUp, int typeDown, int activationKind);
+/* Batched: inA, outDown [batchSize][dim]. */
+int aljabr_rocm_ffn_gated_fused_batch(void *outDown, const void *inA, const void *gateW, const void *upW,
+                                      const void *downW, int dim, int ffnDim, int typeGate, int typeUp, int typeDown,
+                                      int activationKind, int batchSize);
+
+/* ======================================================================== */
 /* safetensors files (replaces engine/safetensor/aljabr-safetensor-loader/   */
 /* .../SafetensorHeaderParser.java:13-160 and the NF4 path of                */
 /* aljabr-safetensor-bridge/.../AccelWeightBridge.java:184-222)              */

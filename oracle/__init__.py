@@ -316,6 +316,22 @@ def fa4_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, cau
 
 # ---- element-wise ---------------------------------------------------------
 
+def gated_activation(gate: np.ndarray, up: np.ndarray, kind: int) -> np.ndarray:
+    """The Metal FFN activation (MTLC/aljabr_metal_kernel_source.m:72-108;
+    kind 2 = GELU, else SiLU, as aljabr_metal_matvec_api.m picks the pipeline):
+    act(g) * up in fp32, with the cut-offs and non-finite -> 0."""
+    g = np.asarray(gate, np.float32).astype(np.float64)
+    if kind == 2:
+        inner = 0.79788456 * (g + 0.044715 * g ** 3)
+        act = np.where(g <= -10.0, 0.0, np.where(g >= 10.0, g, 0.5 * g * (1.0 + np.tanh(inner))))
+    else:
+        with np.errstate(over="ignore"):
+            act = np.where(g <= -20.0, 0.0, np.where(g >= 20.0, g, g / (1.0 + np.exp(-g))))
+    with np.errstate(invalid="ignore", over="ignore"):
+        y = (act * np.asarray(up, np.float64)).astype(np.float32)
+    return np.where(np.isfinite(y), y, np.float32(0.0))
+
+
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     w = np.ascontiguousarray(w, dtype=np.float32)

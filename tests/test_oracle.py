@@ -418,3 +418,16 @@ def test_rope_is_a_rotation(oracle):
     # Each (i, i+half) pair keeps its norm.
     xr, yr = x.reshape(8, 2, 64), y.reshape(8, 2, 64)
     assert np.allclose(np.hypot(xr[:, 0], xr[:, 1]), np.hypot(yr[:, 0], yr[:, 1]), rtol=1e-5)
+
+
+def test_gated_activation_closed_forms(oracle):
+    """SiLU(0) = 0, SiLU above 20 and GELU above 10 are the identity, below
+    the low cut-offs 0, non-finite products 0."""
+    g = np.array([0.0, 25.0, -25.0, 12.0, -12.0, 1.0], np.float32)
+    u = np.array([3.0, 2.0, 5.0, 1.0, 1.0, np.inf], np.float32)
+    s = oracle.gated_activation(g, u, 1)
+    np.testing.assert_array_equal(s[:3], [0.0, 50.0, 0.0])
+    assert s[5] == 0.0
+    e = oracle.gated_activation(g, u, 2)
+    np.testing.assert_array_equal(e[3:5], [12.0, 0.0])
+    assert abs(oracle.gated_activation(np.float32([1.0]), np.float32([1.0]), 0)[0] - 1 / (1 + np.exp(-1))) < 1e-7
