@@ -13,6 +13,7 @@
 #include <cerrno>
 #include <cstring>
 #include <new>
+#include <unordered_set>
 
 #include "internal.hpp"
 #include "safetensors.hpp"
@@ -274,9 +275,9 @@ int st_open(const char *path, StFile **out) {
     std::sort(order.begin(), order.end(), [](const StTensor *a, const StTensor *b) { return a->begin < b->begin; });
     for (size_t i = 1; i < order.size(); ++i)
         if (order[i]->begin < order[i - 1]->end) return bad("tensor data ranges overlap");
-    for (size_t i = 0; i < f->tensors.size(); ++i)
-        for (size_t j = i + 1; j < f->tensors.size(); ++j)
-            if (f->tensors[i].name == f->tensors[j].name) return bad("duplicate tensor name");
+    std::unordered_set<std::string> names;
+    for (const StTensor &t : f->tensors)
+        if (!names.insert(t.name).second) return bad("duplicate tensor name");
     *out = f;
     return ALJABR_ROCM_OK;
 }

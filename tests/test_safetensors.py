@@ -95,7 +95,8 @@ def _raw(path, header: dict, data: bytes, pad=b""):
 
 
 @pytest.mark.parametrize("case", ["short_data", "size_mismatch", "overlap", "dtype", "float_shape", "negative_dim",
-                                  "trailing", "not_object", "header_too_long", "missing_offsets", "bad_escape"])
+                                  "trailing", "not_object", "header_too_long", "missing_offsets", "bad_escape",
+                                  "duplicate"])
 def test_malformed_files_are_rejected(tmp_path, case):
     path = str(tmp_path / f"{case}.safetensors")
     ok = {"dtype": "F32", "shape": [2, 2], "data_offsets": [0, 16]}
@@ -124,6 +125,12 @@ def test_malformed_files_are_rejected(tmp_path, case):
             f.write(struct.pack("<Q", 1 << 40) + b"{}" + data)
     elif case == "missing_offsets":
         _raw(path, {"t": {"dtype": "F32", "shape": [2, 2]}}, data)
+    elif case == "duplicate":
+        with open(path, "wb") as f:
+            e = b'{"dtype": "F32", "shape": [2, 2], "data_offsets": [0, 16]}'
+            e2 = b'{"dtype": "F32", "shape": [2, 2], "data_offsets": [16, 32]}'
+            text = b'{"t": ' + e + b', "t": ' + e2 + b'}'
+            f.write(struct.pack("<Q", len(text)) + text + data)
     elif case == "bad_escape":
         with open(path, "wb") as f:
             text = b'{"t\\q": {"dtype": "F32", "shape": [2, 2], "data_offsets": [0, 16]}}'
