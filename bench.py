@@ -42,8 +42,8 @@ def log(msg: str) -> None:
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=600)
-    ap.add_argument("--warmup", type=int, default=600,
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=2000,
                     help="untimed MLP steps first (the GPU takes ~15 ms of load to reach its steady clocks)")
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough for 512 MB)")
     ap.add_argument("--no-decode", action="store_true", help="skip the Llama decode measurement")
