@@ -260,7 +260,9 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(RT =
         l[u] = 0.0f;
     }
     const int kt0 = g_lo / kKeys, kt1 = (g_hi + kKeys - 1) / kKeys;
-    if (kt0 < kt1) load_tile(kt0, lds);
+    // Tile kt lives in buffer kt & 1 (kt0 is odd when a window starts the
+    // workgroup's keys past an odd tile).
+    if (kt0 < kt1) load_tile(kt0, lds + (kt0 & 1) * BUF);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int kt = kt0; kt < kt1; ++kt) {

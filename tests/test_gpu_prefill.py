@@ -77,12 +77,17 @@ def test_fa4_soft_cap(rocm, dev, oracle, cap):
     assert rel_l2(got, ref) <= TOL
 
 
-@pytest.mark.parametrize("window", [1, 17, 64, 1000])
+# window 20: the second query block's keys start in tile 3 (an odd first tile).
+@pytest.mark.parametrize("window", [1, 17, 20, 64, 1000])
 def test_fa4_window(rocm, dev, oracle, window):
     q, k, v = _qkv(oracle, 1, 200, 230, 4, 2, 128, seed=101)
     got = _run(rocm, dev, q, k, v, 0.09, True, window=window)
     ref = oracle.fa4_attention(q, k, v, scale=0.09, causal=True, window=window)
     assert rel_l2(got, ref) <= TOL
+    # T = S: row t sees keys max(t + 1 - window, 0) .. t
+    q2, k2, v2 = _qkv(oracle, 2, 200, 200, 8, 2, 64, seed=103)
+    got = _run(rocm, dev, q2, k2, v2, 0.125, True, window=window)
+    assert rel_l2(got, oracle.fa4_attention(q2, k2, v2, scale=0.125, causal=True, window=window)) <= TOL
 
 
 @pytest.mark.parametrize("d", [2, 48, 80, 256])
