@@ -60,6 +60,8 @@ def parse() -> argparse.Namespace:
                     help="run only the GGUF Q4_K_M decode measurement (for profiling)")
     ap.add_argument("--kquant-only", action="store_true",
                     help="run only the GGUF Q4_0/Q8_0 and K-quant matvec/GEMM measurements (for profiling)")
+    ap.add_argument("--small-m-only", action="store_true",
+                    help="run only the NF4 small-M GEMM measurement (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill attention measurement (for profiling)")
     return ap.parse_args()
@@ -533,6 +535,8 @@ def main() -> None:
         elif args.kquant_only:
             print(json.dumps({"gguf_q4_0_q8_0": gguf_q_bench(abi, torch, stream),
                               "gguf_kquant": kquant_bench(abi, torch, stream)}), flush=True)
+        elif args.small_m_only:
+            print(json.dumps({"small_m_gemm": small_m_bench(abi, torch, stream)}), flush=True)
         elif args.prefill_only:
             print(json.dumps({"prefill_attention": prefill_bench(abi, torch, stream)}), flush=True)
         elif args.gguf_decode_only:
