@@ -115,6 +115,40 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Split-half RoPE angle of the pair (i, i + D/2), i < D/2, at position `pos`
+// (GGUFVectorOps.rope :383-440): invFreq = base^(-2i/D) in double rounded to
+// float, theta = pos * invFreq in float, cos and sin in double rounded to
+// float.
+__device__ __forceinline__ void rope_cos_sin(int pos, int i, int head_dim, float base, float &c, float &s) {
+    const float exponent = -2.0f * static_cast<float>(i) / static_cast<float>(head_dim);
+    const float inv_freq = static_cast<float>(pow(static_cast<double>(base), static_cast<double>(exponent)));
+    const float theta = static_cast<float>(pos) * inv_freq;
+    c = static_cast<float>(cos(static_cast<double>(theta)));
+    s = static_cast<float>(sin(static_cast<double>(theta)));
+}
+
+// Rotation of (x0, x1) by the angle with cosine c and sine s, each product
+// rounded separately.
+__device__ __forceinline__ void rope_apply(float &x0, float &x1, float c, float s) {
+    const float a = x0, b = x1;
+    x0 = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+    x1 = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+}
+
+// cos/sin of pair i at position p from a [cap][D/2] table of the values
+// rope_cos_sin gives (filled once per model), or computed when there is no
+// table or p is outside it.
+__device__ __forceinline__ void rope_angle(const float2 *table, int cap, int pos, int i, int head_dim, float base,
+                                           float &c, float &s) {
+    if (table && pos >= 0 && pos < cap) {
+        const float2 v = table[static_cast<long long>(pos) * (head_dim >> 1) + i];
+        c = v.x;
+        s = v.y;
+    } else {
+        rope_cos_sin(pos, i, head_dim, base, c, s);
+    }
+}
+
 // ({hi,lo} >> shift)[31:0], shift in [0,31] (v_alignbit_b32).
 __device__ __forceinline__ uint32_t funnel_shift_right(uint32_t hi, uint32_t lo, uint32_t shift) {
     return __builtin_amdgcn_alignbit(hi, lo, shift);

@@ -99,6 +99,7 @@ struct RowsRope {
     uint16_t *kc, *vc;
     int cap, head_dim;
     float base;
+    const float2 *cs;   // [cap][head_dim/2] cos/sin table (enqueue_rope_table), or null
 };
 constexpr int kRowsStore = 0;    // y = W x'
 constexpr int kRowsAdd = 1;      // y += W x' (residual; no norm prologue)
@@ -153,7 +154,11 @@ int enqueue_embed_typed(float *x, const void *table, int type, const int *tokens
 int enqueue_kv_append(uint16_t *cache, const float *src, const int *pos, int batch, int n_kv, int head_dim, int cap);
 // RoPE on q [batch][nh][D] in place and on k, then k and v [batch][nkv][D]
 // appended as fp16 at row pos[b] of caches [batch][nkv][cap][D] (D/2 <= 1024).
+// `cs` is a table from enqueue_rope_table for (cap, head_dim, base), or null.
 int enqueue_rope_append(float *q, const float *k, const float *v, uint16_t *kc, uint16_t *vc, const int *pos, int batch,
-                        int nh, int nkv, int head_dim, int cap, float base);
+                        int nh, int nkv, int head_dim, int cap, float base, const float2 *cs);
+// cs[p][i] = (cos, sin) of RoPE pair i at position p, p < cap, i < head_dim/2,
+// the values the RoPE kernels would compute for that position.
+int enqueue_rope_table(float2 *cs, int cap, int head_dim, float base);
 
 }  // namespace aljabr

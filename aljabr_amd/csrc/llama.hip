@@ -68,6 +68,7 @@ struct aljabr_rocm_llama {
     float *gate = nullptr, *up = nullptr, *hb = nullptr, *logits = nullptr;
     int *kv_len = nullptr;
     int *tok_in = nullptr, *pos_in = nullptr, *next_out = nullptr;   // graph replays read and write these
+    float2 *rope_cs = nullptr;   // [max_seq][head_dim/2] RoPE cos/sin, filled at creation
     float *attn_scratch = nullptr;   // split-attention partials (owned: a captured graph keeps the address)
     size_t attn_scratch_bytes = 0;
     bool rows_fused = false;   // batch-1 layers as fused NF4 launches (shapes and alignment allow it)
@@ -241,7 +242,9 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
                          ((B * kvd * 4 + 255) & ~size_t(255)) * 2 + ((B * c.ffn * 4 + 255) & ~size_t(255)) * 3 +
                          ((B * c.vocab * 4 + 255) & ~size_t(255)) + ((B * 4 + 255) & ~size_t(255)) * 4 +
                          ((attention_scratch_bytes(c.max_batch, c.n_heads, 1, c.head_dim, c.max_seq) + 255) &
-                          ~size_t(255)) + 256;
+                          ~size_t(255)) +
+                         ((static_cast<size_t>(c.max_seq) * (c.head_dim / 2) * sizeof(float2) + 255) & ~size_t(255)) +
+                         256;
     hipError_t e = hipMalloc(&m->arena, bytes);
     if (e != hipSuccess) {
         delete m;
@@ -266,6 +269,20 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
     m->next_out = carve<int>(cur, B);
     m->attn_scratch_bytes = attention_scratch_bytes(c.max_batch, c.n_heads, 1, c.head_dim, c.max_seq);
     m->attn_scratch = carve<float>(cur, m->attn_scratch_bytes / sizeof(float));
+    // The RoPE angles of every cache position, computed once: the decode
+    // step then reads cos/sin instead of evaluating double pow/cos/sin.
+    m->rope_cs = carve<float2>(cur, static_cast<size_t>(c.max_seq) * (c.head_dim / 2));
+    int trc = enqueue_rope_table(m->rope_cs, c.max_seq, c.head_dim, c.rope_base);
+    if (trc == ALJABR_ROCM_OK) trc = finish_launch("llama session: RoPE table");
+    if (trc == ALJABR_ROCM_OK) {
+        const hipError_t se = hipStreamSynchronize(current_stream());
+        if (se != hipSuccess) trc = fail(ALJABR_ROCM_ERR_DEVICE, "llama session: RoPE table: %s", hipGetErrorString(se));
+    }
+    if (trc != ALJABR_ROCM_OK) {
+        (void)hipFree(m->arena);
+        delete m;
+        return trc;
+    }
     m->graphs.resize(static_cast<size_t>(c.max_batch) + 1);
     // Batch-1 fusion (the rows kernels: NF4, Q4_0, Q8_0, Q4_K, Q6_K) needs
     // every K a multiple of 2048 (at most 16384), for NF4 a power-of-two block
@@ -291,10 +308,6 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
 }
 
 }  // namespace
-
-extern "C" {
-
-}  // extern "C"
 
 namespace {
 
@@ -877,7 +890,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                                     {m->k, W(m->wk), S(m->wk), kvd},
                                     {m->v, W(m->wv), S(m->wv), kvd}};
             const int tq = m->wq[l].type, tk = m->wk[l].type, tv = m->wv[l].type;
-            const RowsRope rope{pos, kc, vc, c.max_seq, hd, c.rope_base};
+            const RowsRope rope{pos, kc, vc, c.max_seq, hd, c.rope_base, m->rope_cs};
             rc = tq == tk && tk == tv
                      ? enqueue_rows_fused(tq, qkv, 3, m->x, attn_norm, c.eps, dim, shift, kRowsRopeKV, &rope)
                      : ALJABR_ROCM_ERR_UNSUPPORTED;
@@ -892,7 +905,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                     ALJ_TRY(enqueue_rows_fused(types[i], qkv + i, j - i, m->x, attn_norm, c.eps, dim, shift, kRowsStore));
                     i = j;
                 }
-                ALJ_TRY(enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base));
+                ALJ_TRY(enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base, m->rope_cs));
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }
@@ -923,7 +936,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                                      mm_bytes(m->wv[l], kvd, dim, true) - 2.0 * B * dim * f4);
         }
         if (!fused1) {
-            rc = enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base);
+            rc = enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base, m->rope_cs);
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
                 ALJ_TRY(enqueue_rope(m->q, pos, B, nh, hd, c.rope_base));
                 ALJ_TRY(enqueue_rope(m->k, pos, B, nkv, hd, c.rope_base));

@@ -119,6 +119,7 @@ struct RowsArgs {
     uint16_t *kc, *vc;
     int cap, hd_shift;
     float rope_base;
+    const float2 *rope_cs;   // [cap][D/2] cos/sin table, or null
     int N, K, bs_shift, S, G;
 };
 
@@ -337,18 +338,13 @@ __device__ __forceinline__ float silu_ref(float g) {
     return g / (1.0f + static_cast<float>(exp(-static_cast<double>(g))));
 }
 
-// Split-half RoPE of the pair (i, i + D/2) at position `pos` exactly as the
-// stand-alone RoPE kernel (GGUFVectorOps.rope :383-440): base^(-2i/D) and
-// cos/sin in double, products rounded separately.
-__device__ __forceinline__ void rope_rotate(float &x0, float &x1, int pos, int i, int head_dim, float base) {
-    const float exponent = -2.0f * static_cast<float>(i) / static_cast<float>(head_dim);
-    const float inv_freq = static_cast<float>(pow(static_cast<double>(base), static_cast<double>(exponent)));
-    const float theta = static_cast<float>(pos) * inv_freq;
-    const float c = static_cast<float>(cos(static_cast<double>(theta)));
-    const float s = static_cast<float>(sin(static_cast<double>(theta)));
-    const float a = x0, b = x1;
-    x0 = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-    x1 = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+// Split-half RoPE of the pair (i, i + D/2) at position `pos`, the same
+// arithmetic as the stand-alone RoPE kernel (GGUFVectorOps.rope :383-440).
+__device__ __forceinline__ void rope_rotate(float &x0, float &x1, const float2 *table, int cap, int pos, int i,
+                                            int head_dim, float base) {
+    float c, s;
+    rope_angle(table, cap, pos, i, head_dim, base, c, s);
+    rope_apply(x0, x1, c, s);
 }
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
@@ -526,11 +522,11 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
                 const int hd = 1 << a.hd_shift;
                 const int h = f.local >> a.hd_shift, i = f.local & (hd - 1);
                 if (!f.s1 && !f.s2) {                    // q: rotate, store fp32
-                    rope_rotate(v, v1, p, i, hd, a.rope_base);
+                    rope_rotate(v, v1, a.rope_cs, a.cap, p, i, hd, a.rope_base);
                     a.seg[0].y[f.local] = v;
                     a.seg[0].y[f.local + (hd >> 1)] = v1;
                 } else if (!f.s2) {                      // k: rotate, append fp16
-                    rope_rotate(v, v1, p, i, hd, a.rope_base);
+                    rope_rotate(v, v1, a.rope_cs, a.cap, p, i, hd, a.rope_base);
                     if (in_cache) {
                         uint16_t *dst = a.kc + (static_cast<size_t>(h) * a.cap + p) * hd + i;
                         dst[0] = f32_to_f16_bits(v);
@@ -704,6 +700,7 @@ int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, 
         args.cap = rope->cap;
         args.hd_shift = hs;
         args.rope_base = rope->base;
+        args.rope_cs = rope->cs;
     } else if (epilogue != kRowsStore && epilogue != kRowsAdd) {
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     }

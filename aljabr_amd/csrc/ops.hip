@@ -117,14 +117,20 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(float *__restrict__ o
 // Split-half rotation of the pair (i, i + D/2) at position `pos`
 // (GGUFVectorOps.rope :383-440): invFreq = base^(-2i/D) and cos/sin in double.
 __device__ __forceinline__ void rope_pair(float &x0, float &x1, int pos, int i, int head_dim, float base) {
-    const float exponent = -2.0f * static_cast<float>(i) / static_cast<float>(head_dim);
-    const float inv_freq = static_cast<float>(pow(static_cast<double>(base), static_cast<double>(exponent)));
-    const float theta = static_cast<float>(pos) * inv_freq;
-    const float c = static_cast<float>(cos(static_cast<double>(theta)));
-    const float s = static_cast<float>(sin(static_cast<double>(theta)));
-    const float a = x0, b = x1;
-    x0 = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-    x1 = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+    float c, s;
+    rope_cos_sin(pos, i, head_dim, base, c, s);
+    rope_apply(x0, x1, c, s);
+}
+
+// One thread per (position, pair): the decode step's cos/sin table.
+__global__ __launch_bounds__(kThreads) void rope_table_kernel(float2 *__restrict__ cs, int cap, int head_dim,
+                                                              float base) {
+    const int half = head_dim / 2;
+    const long long t = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+    if (t >= static_cast<long long>(cap) * half) return;
+    float c, s;
+    rope_cos_sin(static_cast<int>(t / half), static_cast<int>(t % half), head_dim, base, c, s);
+    cs[t] = make_float2(c, s);
 }
 
 // One thread per (row, head, pair i < half).
@@ -155,14 +161,16 @@ __device__ __forceinline__ uint16_t to_f16_bits(float v) {
 // followed by kv_append_kernel.
 __global__ void rope_append_kernel(float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
                                    uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, const int *__restrict__ pos,
-                                   int nh, int nkv, int head_dim, int cap, float base) {
+                                   int nh, int nkv, int head_dim, int cap, float base, const float2 *__restrict__ cs) {
     const int slot = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
     const int half = head_dim / 2;
     const int p = pos[b];
+    float c = 0.0f, s = 0.0f;
+    if (slot < nh + nkv) rope_angle(cs, cap, p, i, head_dim, base, c, s);
     if (slot < nh) {
         float *x = q + (static_cast<long long>(b) * nh + slot) * head_dim;
         float x0 = x[i], x1 = x[i + half];
-        rope_pair(x0, x1, p, i, head_dim, base);
+        rope_apply(x0, x1, c, s);
         x[i] = x0;
         x[i + half] = x1;
         return;
@@ -173,7 +181,7 @@ __global__ void rope_append_kernel(float *__restrict__ q, const float *__restric
     const long long dst = ((static_cast<long long>(b) * nkv + h) * cap + p) * head_dim;
     if (slot < nh + nkv) {
         float x0 = k[src + i], x1 = k[src + i + half];
-        rope_pair(x0, x1, p, i, head_dim, base);
+        rope_apply(x0, x1, c, s);
         kc[dst + i] = to_f16_bits(x0);
         kc[dst + i + half] = to_f16_bits(x1);
     } else {
@@ -394,10 +402,18 @@ int enqueue_embed_typed(float *x, const void *table, int type, const int *tokens
 }
 
 int enqueue_rope_append(float *q, const float *k, const float *v, uint16_t *kc, uint16_t *vc, const int *pos, int batch,
-                        int nh, int nkv, int head_dim, int cap, float base) {
+                        int nh, int nkv, int head_dim, int cap, float base, const float2 *cs) {
     if (head_dim < 2 || head_dim % 2 != 0 || head_dim / 2 > 1024) return ALJABR_ROCM_ERR_UNSUPPORTED;
     hipLaunchKernelGGL(rope_append_kernel, dim3(nh + 2 * nkv, batch), dim3(head_dim / 2), 0, current_stream(), q, k, v,
-                       kc, vc, pos, nh, nkv, head_dim, cap, base);
+                       kc, vc, pos, nh, nkv, head_dim, cap, base, cs);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_rope_table(float2 *cs, int cap, int head_dim, float base) {
+    if (head_dim < 2 || head_dim % 2 != 0 || cap <= 0) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    const long long n = static_cast<long long>(cap) * (head_dim / 2);
+    hipLaunchKernelGGL(rope_table_kernel, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                       current_stream(), cs, cap, head_dim, base);
     return ALJABR_ROCM_OK;
 }
 
