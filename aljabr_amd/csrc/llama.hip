@@ -891,14 +891,23 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                                     {m->v, W(m->wv), S(m->wv), kvd}};
             const int tq = m->wq[l].type, tk = m->wk[l].type, tv = m->wv[l].type;
             const RowsRope rope{pos, kc, vc, c.max_seq, hd, c.rope_base, m->rope_cs};
-            rc = tq == tk && tk == tv
-                     ? enqueue_rows_fused(tq, qkv, 3, m->x, attn_norm, c.eps, dim, shift, kRowsRopeKV, &rope)
-                     : ALJABR_ROCM_ERR_UNSUPPORTED;
+            // One launch per run of one type (a Q6_K attn_v beside Q4_K q and
+            // k takes two), the other segments left empty.
+            const int types[3] = {tq, tk, tv};
+            rc = ALJABR_ROCM_OK;
+            for (int i = 0; i < 3 && rc == ALJABR_ROCM_OK;) {
+                int j = i + 1;
+                while (j < 3 && types[j] == types[i]) ++j;
+                RowsOut part[3] = {qkv[0], qkv[1], qkv[2]};
+                for (int u = 0; u < 3; ++u)
+                    if (u < i || u >= j) part[u].n = 0;
+                rc = enqueue_rows_fused(types[i], part, 3, m->x, attn_norm, c.eps, dim, shift, kRowsRopeKV, &rope);
+                i = j;
+            }
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
-                // Mixed types (a Q6_K attn_v beside Q4_K q and k) or a head
-                // size the epilogue does not take: consecutive matrices of one
-                // type per launch, then RoPE and the append.
-                const int types[3] = {tq, tk, tv};
+                // A head size the epilogue does not take: plain launches, then
+                // RoPE and the append (they rewrite whatever an earlier launch
+                // of this loop stored, with the same values).
                 for (int i = 0; i < 3;) {
                     int j = i + 1;
                     while (j < 3 && types[j] == types[i]) ++j;

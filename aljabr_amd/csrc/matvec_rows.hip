@@ -690,9 +690,13 @@ int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, 
         if (nseg != 2 || outs[0].n != outs[1].n) return ALJABR_ROCM_ERR_UNSUPPORTED;
     } else if (epilogue == kRowsRopeKV) {
         // q, k, v of one sequence; RoPE pairs of q and k meet in one wave.
+        // Segments may be empty (n = 0), so that q, k and v of different
+        // types take one launch per type: the rows of an empty segment are
+        // never formed.
         const int hs = rope ? log2_exact(rope->head_dim) : -1;
-        if (nseg != 3 || !rope || !rope->pos || !rope->kc || !rope->vc || hs < 1 ||
-            outs[0].n % rope->head_dim != 0 || outs[1].n % rope->head_dim != 0 || outs[1].n != outs[2].n)
+        if (nseg != 3 || !rope || !rope->pos || !rope->kc || !rope->vc || hs < 1 || outs[0].n < 0 ||
+            outs[1].n < 0 || outs[2].n < 0 || outs[0].n % rope->head_dim != 0 || outs[1].n % rope->head_dim != 0 ||
+            outs[2].n % 2 != 0 || outs[0].n + outs[1].n + outs[2].n == 0)
             return ALJABR_ROCM_ERR_UNSUPPORTED;
         args.pos = rope->pos;
         args.kc = rope->kc;
