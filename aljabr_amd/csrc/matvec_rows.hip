@@ -712,7 +712,10 @@ int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, 
     for (int i = 0; i < 3; ++i) {
         if (i < nseg) {
             const size_t wa = (type == ALJABR_ROCM_TYPE_Q4_0 || type == ALJABR_ROCM_TYPE_Q8_0) ? 4 : 16;
-            if (!aligned(outs[i].w, wa) || outs[i].n <= 0 || (outs[i].n & 1)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            // Only the RoPE epilogue takes empty segments (checked above).
+            const bool empty_ok = epilogue == kRowsRopeKV && outs[i].n == 0;
+            if (!empty_ok && (!aligned(outs[i].w, wa) || outs[i].n <= 0 || (outs[i].n & 1)))
+                return ALJABR_ROCM_ERR_UNSUPPORTED;
             end += outs[i].n;
             if (end > 0x7ffffffeLL) return ALJABR_ROCM_ERR_UNSUPPORTED;
             args.seg[i] = RowsSeg{outs[i].w, outs[i].absmax, outs[i].y, static_cast<int>(end)};
