@@ -398,24 +398,8 @@ struct Tag {};
 
 }  // namespace
 
-// Small-M GEMMs use the MFMA kernel unless ALJABR_ROCM_MFMA=0.
-bool mfma_enabled() {
-    static const bool v = [] {
-        const char *e = getenv("ALJABR_ROCM_MFMA");
-        return !(e && *e == '0');
-    }();
-    return v;
-}
-
-// Batch-1 kernel family: 0 (default) = pair-table rows kernels, 1 = the
-// earlier per-format kernels (ALJABR_ROCM_BATCH1=1, kept for comparison).
-int batch1_kernel() {
-    static const int v = [] {
-        const char *e = getenv("ALJABR_ROCM_BATCH1");
-        return e && *e ? atoi(e) : 0;
-    }();
-    return v;
-}
+// Small-M GEMMs run on the matrix cores wherever their shape checks pass.
+bool mfma_enabled() { return true; }
 
 // Enqueue C[M][N] for M <= 8 (no sync); used by the entry points and the
 // decode driver. Returns a status.
@@ -429,8 +413,9 @@ int enqueue_nf4_small(float *C, const float *A, const uint8_t *Bq, const float *
                            N, K, M, bs);
         return ALJABR_ROCM_OK;
     }
-    if (M == 1 && batch1_kernel() != 1 &&
-        enqueue_rows(C, A, Bq, absmax, K, N, ALJABR_ROCM_TYPE_NF4, shift) == ALJABR_ROCM_OK)
+    // Batch 1: the rows kernel (K % 2048 == 0, at most 8 chunks), else the
+    // per-workgroup rows kernel (up to 16 chunks), else the tile kernel.
+    if (M == 1 && enqueue_rows(C, A, Bq, absmax, K, N, ALJABR_ROCM_TYPE_NF4, shift) == ALJABR_ROCM_OK)
         return ALJABR_ROCM_OK;
     if (M == 1 && enqueue_nf4_rows(C, A, Bq, absmax, K, N, shift) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
     if (enqueue_nf4_tile(C, A, Bq, absmax, K, N, shift, M) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
@@ -444,7 +429,7 @@ int enqueue_gguf_small(float *C, const float *A, const uint8_t *B, int K, int N,
     hipStream_t s = current_stream();
     if (type != ALJABR_ROCM_TYPE_F16 && (!aligned(A, 16) || !aligned(B, 4)))
         return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "GGUF matvec needs A 16-byte and B 4-byte aligned");
-    if (M == 1 && type != ALJABR_ROCM_TYPE_F16 && batch1_kernel() != 1 &&
+    if (M == 1 && type != ALJABR_ROCM_TYPE_F16 &&
         enqueue_rows(C, A, B, nullptr, K, N, type, 0) == ALJABR_ROCM_OK)
         return ALJABR_ROCM_OK;
     if (M == 1 && enqueue_gguf_stream(C, A, B, K, N, type) == ALJABR_ROCM_OK) return ALJABR_ROCM_OK;
@@ -513,13 +498,14 @@ int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N
     if ((type == ALJABR_ROCM_TYPE_Q4_0 || type == ALJABR_ROCM_TYPE_Q8_0) && M >= 2 && K % 512 == 0 &&
         aligned(A, 16) && aligned(B, 16) && mfma_enabled()) {
         int m0 = 0;
-        for (; M - m0 >= 2; m0 += 8) {
+        while (M - m0 >= 2) {
             const int mm = M - m0 < 8 ? M - m0 : 8;
             const int rc = enqueue_kquant_mfma(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, B, K,
                                                N, type, mm);
             if (rc != ALJABR_ROCM_OK) return rc;
+            m0 += mm;                            // the pass covered exactly mm tokens
         }
-        if (m0 == M) return ALJABR_ROCM_OK;
+        if (m0 == M) return ALJABR_ROCM_OK;      // otherwise exactly one token is left
         return enqueue_gguf_small(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, B, K, N, type, 1);
     }
     // fp16 rows with M >= 2 on the matrix cores, 32 tokens per pass.

@@ -121,11 +121,12 @@ int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int
     int m0 = 0;
     if (M >= 2 && K % 512 == 0 && mfma_enabled()) {
         // Matrix cores, 32 tokens per pass; a last single token takes the rows kernel.
-        for (; M - m0 >= 2; m0 += 32) {
+        while (M - m0 >= 2) {
             const int mm = M - m0 < 32 ? M - m0 : 32;
             const int rc = enqueue_kquant_mfma(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, W,
                                                K, N, type, mm);
             if (rc != ALJABR_ROCM_OK) return rc;
+            m0 += mm;
         }
         if (m0 < M && enqueue_rows(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, W, nullptr, K,
                                    N, type, 0) == ALJABR_ROCM_OK)

@@ -26,7 +26,7 @@ def _nf4_case(oracle, n, k, group=64, seed=1):
 @pytest.mark.parametrize("m", [1, 4, 16, 64])
 def test_nf4_matvec(rocm, dev, oracle, n, k, m):
     if m > 4 and n * k > 4096 * 4096 and m != 64:
-        pytest.skip("covered by m=64 at this size")
+        pytest.skip("M=16 at the MLP shapes runs in test_nf4_mfma_small_m (14336x4096 and 4096x14336)")
     codes, absmax = _nf4_case(oracle, n, k)
     x = oracle.normal(11 + m, m * k)
     y_ref = oracle.nf4_matvec(codes, absmax, x, n, k, 64)
@@ -109,7 +109,8 @@ def test_gguf_mfma_small_m(rocm, dev, oracle, qtype, n, k, m):
 # seven K-ranges (4096 x 14336) and two passes of 32 tokens (M = 33, 64).
 @pytest.mark.parametrize("n,k,m", [(300, 1024, 2), (300, 1024, 3), (257, 2048, 8), (300, 1024, 31), (300, 1024, 32),
                                    (300, 1024, 33), (129, 512, 64), (300, 1024, 65), (77, 1536, 100),
-                                   (14336, 4096, 16), (4096, 14336, 64), (1000, 4096, 5), (300, 6144, 17),
+                                   (14336, 4096, 16), (4096, 14336, 16), (4096, 14336, 64), (1000, 4096, 5),
+                                   (300, 6144, 17),
                                    (8200, 4096, 32), (14336, 4096, 33), (257, 2048, 2)])
 def test_nf4_mfma_small_m(rocm, dev, oracle, n, k, m):
     codes, absmax = _nf4_case(oracle, n, k, seed=3)
@@ -225,3 +226,43 @@ def test_matvec_argument_errors(rocm, dev):
     with pytest.raises(rocm.RocmError) as e:
         rocm.call("aljabr_rocm_matvec_tb_nf4", dev.ptr(y), dev.ptr(y), dev.ptr(y), dev.ptr(y), 64, 1, 7)
     assert e.value.status == rocm.ERR_BAD_ARGUMENT
+
+
+# Token-pass loops must cover exactly M rows: C rows at and past M keep a
+# sentinel and every row below M equals the oracle. M = 2..7 leave a short last
+# Q4_0/Q8_0 pass (8 tokens per pass), 10 a two-token pass, 31 and 33 a last
+# pass of 7 and a single trailing token, across every batched row format.
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "q4_k", "q6_k", "nf4", "f16"])
+@pytest.mark.parametrize("m", [2, 3, 5, 10, 31, 33])
+def test_batched_passes_stay_in_bounds(rocm, dev, oracle, fmt, m):
+    n, k, pad = 320, 1024, 3
+    w = oracle.normal(101 + m, n * k, 0.0, 0.02)
+    x = oracle.normal(103 + m, (m + pad) * k)
+    if fmt == "nf4":
+        codes, absmax = oracle.nf4_quantize(w, 64)
+        y_ref = np.asarray(oracle.nf4_matvec(codes, absmax, x[:m * k], n, k, 64)).ravel()
+    elif fmt == "f16":
+        enc = w.astype(np.float16).view(np.uint16)
+        y_ref = np.asarray(oracle.f16_matvec(enc, x[:m * k], n, k)).ravel()
+    else:
+        ot = {"q4_0": oracle.QTYPE_Q4_0, "q8_0": oracle.QTYPE_Q8_0, "q4_k": oracle.QTYPE_Q4_K,
+              "q6_k": oracle.QTYPE_Q6_K}[fmt]
+        if fmt in ("q4_k", "q6_k"):
+            enc = oracle.random_k_blocks(ot, n * k // 256, 107 + m)
+        else:
+            enc = oracle.quantize(ot, w)
+        y_ref = np.asarray(oracle.q_matvec(ot, enc, x[:m * k], n, k)).ravel()
+    sentinel = np.full((m + pad) * n, -12345.5, np.float32)
+    y, xd = dev.put(sentinel), dev.put(x)
+    if fmt == "nf4":
+        c, a = dev.put(codes), dev.put(absmax)
+        rocm.call("aljabr_rocm_matvec_tb_batch_nf4", dev.ptr(y), dev.ptr(xd), dev.ptr(c), dev.ptr(a), k, n, 64, m)
+    else:
+        qt = {"q4_0": rocm.TYPE_Q4_0, "q8_0": rocm.TYPE_Q8_0, "q4_k": rocm.TYPE_Q4_K, "q6_k": rocm.TYPE_Q6_K,
+              "f16": rocm.TYPE_F16}[fmt]
+        wd = dev.put(enc)
+        rocm.call("aljabr_rocm_matvec_tb_batch", dev.ptr(y), dev.ptr(xd), dev.ptr(wd), k, n, qt, m)
+    got = dev.get(y)
+    assert np.all(got[m * n:] == np.float32(-12345.5)), "rows past M were written"
+    for i in range(m):
+        assert rel_l2(got[i * n:(i + 1) * n], y_ref[i * n:(i + 1) * n]) <= TOL, i
