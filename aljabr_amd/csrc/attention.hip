@@ -534,13 +534,8 @@ int enqueue_attention(const AttnParams &p_in) {
             hipLaunchKernelGGL(attn_generic_kernel<false>, grid, dim3(64), 0, s, p);
         return ALJABR_ROCM_OK;
     }
-    // Enough workgroups to cover the CUs `per_cu` times, chunks of >= 64
-    // keys (ALJABR_ROCM_ATTN_WGS overrides per_cu, for sweeps).
-    static const int per_cu = [] {
-        const char *e = getenv("ALJABR_ROCM_ATTN_WGS");
-        const int v = e && *e ? atoi(e) : 2;
-        return v >= 1 && v <= 64 ? v : 2;
-    }();
+    // Enough workgroups to cover the CUs twice, chunks of >= 64 keys.
+    constexpr int per_cu = 2;
     const long long items = static_cast<long long>(p.B) * p.Hkv * p.Sq;
     const int keys = p.block_table ? p.max_blocks * p.block_size : (p.kv_len ? p.cap : p.Sk);
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;

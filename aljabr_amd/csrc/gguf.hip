@@ -177,7 +177,9 @@ int gguf_open(const char *path, GgufFile **out) {
     const uint64_t n_tensors = c.get<uint64_t>();
     const uint64_t n_kv = c.get<uint64_t>();
     if (n_tensors > g->size / 8 || n_kv > g->size / 8) return bad("implausible tensor or key count");
-    g->meta.reserve(static_cast<size_t>(n_kv));
+    // The tables grow as entries are read (every entry consumes file bytes),
+    // never from the counts alone; a failed host allocation is a status.
+    try {
     for (uint64_t i = 0; i < n_kv; ++i) {
         std::string key = c.str();
         const int type = static_cast<int>(c.get<uint32_t>());
@@ -185,7 +187,6 @@ int gguf_open(const char *path, GgufFile **out) {
         if (c.bad || !read_value(c, type, v)) return bad("truncated or malformed metadata");
         g->meta.emplace_back(std::move(key), std::move(v));
     }
-    g->tensors.reserve(static_cast<size_t>(n_tensors));
     for (uint64_t i = 0; i < n_tensors; ++i) {
         GgufTensor t;
         t.name = c.str();
@@ -210,12 +211,21 @@ int gguf_open(const char *path, GgufFile **out) {
         t.bytes = static_cast<uint64_t>(bytes);
         g->tensors.push_back(std::move(t));
     }
+    } catch (const std::bad_alloc &) {
+        delete g;
+        return fail(ALJABR_ROCM_ERR_BUFFER, "gguf: %s: out of host memory reading the header", path);
+    }
     uint64_t align = 32;
     if (const GgufValue *a = g->find("general.alignment"))
         if (a->type != 8 && a->type != 9 && a->i > 0) align = static_cast<uint64_t>(a->i);
+    if (align > g->size) return bad("general.alignment larger than the file");
     g->data_start = (c.pos() + align - 1) / align * align;
+    if (g->data_start > g->size) return bad("tensor data starts past the end of the file");
+    // data_start <= size, so size - data_start cannot wrap, and neither can
+    // the subtraction below once offset <= size - data_start.
     for (const auto &t : g->tensors)
-        if (t.offset % align != 0 || g->data_start + t.offset > g->size || t.bytes > g->size - g->data_start - t.offset)
+        if (t.offset % align != 0 || t.offset > g->size - g->data_start ||
+            t.bytes > g->size - g->data_start - t.offset)
             return bad("tensor data outside the file or misaligned");
     *out = g;
     return ALJABR_ROCM_OK;

@@ -66,9 +66,6 @@ struct KqOut {
     int n;
 };
 int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate);
-// False when ALJABR_ROCM_FA_GENERIC=1 routes prefill attention through the
-// generic kernel.
-bool fa_prefill_enabled();
 // y = cap * tanh(y / cap) elementwise.
 int enqueue_softcap(float *y, long long n, float cap);
 // K-split tile kernels for M <= 2 (ALJABR_ROCM_ERR_UNSUPPORTED when the shape
@@ -100,6 +97,7 @@ struct RowsRope {
     int cap, head_dim;
     float base;
     const float2 *cs;   // [cap][head_dim/2] cos/sin table (enqueue_rope_table), or null
+    int n_kv;           // KV heads in the caches ([n_kv][cap][head_dim] each)
 };
 constexpr int kRowsStore = 0;    // y = W x'
 constexpr int kRowsAdd = 1;      // y += W x' (residual; no norm prologue)
@@ -129,7 +127,6 @@ int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K,
 // 4096}, W and A 16-byte aligned); deterministic (no atomics).
 int enqueue_f16_mfma(float *C, const float *A, const uint16_t *W, int K, int N, int M);
 // Persistent double-buffered batch-1 kernels (K <= 16384).
-int enqueue_nf4_stream(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift);
 int enqueue_gguf_stream(float *C, const float *A, const uint8_t *B, int K, int N, int type);
 // Small-M (M <= 8) wavefront-reduction kernels.
 int enqueue_nf4_small(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M);

@@ -890,7 +890,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                                     {m->k, W(m->wk), S(m->wk), kvd},
                                     {m->v, W(m->wv), S(m->wv), kvd}};
             const int tq = m->wq[l].type, tk = m->wk[l].type, tv = m->wv[l].type;
-            const RowsRope rope{pos, kc, vc, c.max_seq, hd, c.rope_base, m->rope_cs};
+            const RowsRope rope{pos, kc, vc, c.max_seq, hd, c.rope_base, m->rope_cs, c.n_kv_heads};
             // One launch per run of one type (a Q6_K attn_v beside Q4_K q and
             // k takes two), the other segments left empty.
             const int types[3] = {tq, tk, tv};

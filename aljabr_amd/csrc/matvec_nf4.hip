@@ -145,30 +145,21 @@ __global__ __launch_bounds__(kMaxWaves * 64) void nf4_rows_kernel(float *__restr
     }
 }
 
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 }  // namespace
 
 // Rows per workgroup T: the largest of {16, 8, 4, 2} that still leaves ~12
-// waves per CU (ALJABR_ROCM_NF4_T overrides for sweeps).
+// waves per CU.
 int enqueue_nf4_rows(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift) {
-    static const int env_t = env_int("ALJABR_ROCM_NF4_T", 0);
     const int S = (K + kChunk - 1) / kChunk;
     if (K % kChunk != 0 || S > kMaxWaves || bs_shift < 5 || !aligned(Bq, 16) || !aligned(A, 16))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-    int T = env_t;
-    if (T != 2 && T != 4 && T != 8 && T != 16) {
-        T = 2;
-        for (int cand = 16; cand >= 2; cand >>= 1)
-            if (static_cast<long long>((N + cand - 1) / cand) * S >= 12LL * cus) {
-                T = cand;
-                break;
-            }
-    }
+    int T = 2;
+    for (int cand = 16; cand >= 2; cand >>= 1)
+        if (static_cast<long long>((N + cand - 1) / cand) * S >= 12LL * cus) {
+            T = cand;
+            break;
+        }
     hipStream_t s = current_stream();
     const dim3 grid((N + T - 1) / T), block(64 * S);
     const size_t lds = static_cast<size_t>(S) * 512 * sizeof(float4);

@@ -542,17 +542,10 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     }
 }
 
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 template <int FMT, int T, int PF, int W, int XOP, int EPI>
 void launch_cfg(const RowsArgs &args, hipStream_t s) {
-    static const int pad = env_int("ALJABR_ROCM_ROWS_LDS", 0);   // dynamic LDS floor (bytes), sweeps only
     const void *fn = reinterpret_cast<const void *>(rows_kernel<FMT, T, PF, W, XOP, EPI>);
-    size_t lds = pair_table_fmt(FMT) ? kPairBytes : static_cast<size_t>(args.S) * 512 * sizeof(float4);
-    if (pad > 0 && static_cast<size_t>(pad) > lds && pad <= 150 * 1024) lds = pad;
+    const size_t lds = pair_table_fmt(FMT) ? kPairBytes : static_cast<size_t>(args.S) * 512 * sizeof(float4);
     static bool lds_set = false;                 // the attribute is per kernel, per process
     if (!lds_set) {
         (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
@@ -588,12 +581,8 @@ void launch_rows(RowsArgs args, int T, hipStream_t s) {
 // pair table) is paid once per workgroup, and measured on MI355X the fastest
 // shape is one 8-wave workgroup per CU, each taking N/CUs rows: T =
 // ceil(N / (G * CUs)) rounded up to even (to a multiple of 4 above 16), at
-// most `cap` (beyond that more workgroups). ALJABR_ROCM_ROWS_T overrides for
-// sweeps.
+// most `cap` (beyond that more workgroups).
 int pick_rows_t(int N, int S, int cap) {
-    static const int env_t = env_int("ALJABR_ROCM_ROWS_T", 0);
-    if (env_t >= 2 && env_t <= 32 && (env_t % 2 == 0 || env_t == 7) && (env_t <= 16 || env_t % 4 == 0))
-        return env_t;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     const long long per = static_cast<long long>(8 / S) * cus;
     int t = static_cast<int>((N + per - 1) / per);
@@ -693,10 +682,15 @@ int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, 
         // Segments may be empty (n = 0), so that q, k and v of different
         // types take one launch per type: the rows of an empty segment are
         // never formed.
+        // k and v rows address cache head local / head_dim, so both hold
+        // whole heads, at most n_kv of them, and the same count when a launch
+        // carries both.
         const int hs = rope ? log2_exact(rope->head_dim) : -1;
-        if (nseg != 3 || !rope || !rope->pos || !rope->kc || !rope->vc || hs < 1 || outs[0].n < 0 ||
-            outs[1].n < 0 || outs[2].n < 0 || outs[0].n % rope->head_dim != 0 || outs[1].n % rope->head_dim != 0 ||
-            outs[2].n % 2 != 0 || outs[0].n + outs[1].n + outs[2].n == 0)
+        if (nseg != 3 || !rope || !rope->pos || !rope->kc || !rope->vc || hs < 1 || rope->n_kv < 1 ||
+            outs[0].n < 0 || outs[1].n < 0 || outs[2].n < 0 || outs[0].n % rope->head_dim != 0 ||
+            outs[1].n % rope->head_dim != 0 || outs[2].n % rope->head_dim != 0 ||
+            outs[1].n / rope->head_dim > rope->n_kv || outs[2].n / rope->head_dim > rope->n_kv ||
+            (outs[1].n > 0 && outs[2].n > 0 && outs[1].n != outs[2].n) || outs[0].n + outs[1].n + outs[2].n == 0)
             return ALJABR_ROCM_ERR_UNSUPPORTED;
         args.pos = rope->pos;
         args.kc = rope->kc;

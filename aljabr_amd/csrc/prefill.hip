@@ -489,7 +489,7 @@ int enqueue_fa4(const void *out, const void *q, const void *k, const void *v, in
     p.window = window > 0 ? window : 0;
     hipStream_t s = current_stream();
     const bool fast = (D == 64 || D == 128) && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
-                      aligned(out, 16) && fa_prefill_enabled();
+                      aligned(out, 16);
     if (fast) {
         // Two 32-row tiles per wave (one wave per SIMD) when that still gives
         // every CU four workgroups, whose uneven causal lengths then even
@@ -525,15 +525,6 @@ int enqueue_fa4(const void *out, const void *q, const void *k, const void *v, in
 
 }  // namespace
 
-// Set ALJABR_ROCM_FA_GENERIC=1 to route every prefill through the generic
-// kernel (a cross-check of the fast path).
-bool fa_prefill_enabled() {
-    static const bool on = [] {
-        const char *e = getenv("ALJABR_ROCM_FA_GENERIC");
-        return !(e && *e == '1');
-    }();
-    return on;
-}
 
 }  // namespace aljabr
 
