@@ -88,6 +88,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "orc_rope": (None, [_P, _I32, _I32, _I32, _F]),
         "orc_swiglu": (None, [_P, _P, _P, _I32]),
         "orc_softmax": (None, [_P, _I32]),
+        "orc_decode_attention": (None, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F]),
         "orc_llama_decode": (_I32, [_P, _P, _I32, _I32, _P, _P, _P, _P, ctypes.c_int]),
         "orc_llama_decode_typed": (_I32, [_P, _P, _I32, _I32, _P, _P, _P, _P, ctypes.c_int]),
         "orc_fill_normal": (None, [ctypes.c_uint64, _F, _F, _P, _I64]),
@@ -363,6 +364,21 @@ def softmax(a: np.ndarray) -> np.ndarray:
     y = np.array(a, dtype=np.float32, copy=True).reshape(-1)
     lib().orc_softmax(_ptr(y), y.size)
     return y
+
+
+def decode_attention(query: np.ndarray, keys: np.ndarray, values: np.ndarray, cache_head_stride: int,
+                     kv_heads: int, query_heads: int, head_dim: int, sequence_length: int,
+                     start_position: int, scale: float) -> np.ndarray:
+    """The decode runner's attention (orc_decode_attention): keys/values are
+    position-major [position][cache_head_stride] flat arrays."""
+    q = np.ascontiguousarray(query, np.float32).reshape(-1)
+    k = np.ascontiguousarray(keys, np.float32).reshape(-1)
+    v = np.ascontiguousarray(values, np.float32).reshape(-1)
+    out = np.empty(query_heads * head_dim, np.float32)
+    scores = np.empty(max(sequence_length - start_position, 1), np.float32)
+    lib().orc_decode_attention(_ptr(q), _ptr(out), _ptr(scores), _ptr(k), _ptr(v), cache_head_stride, kv_heads,
+                               query_heads, head_dim, sequence_length, start_position, scale)
+    return out
 
 
 # ---- Llama-shaped decode step ---------------------------------------------

@@ -875,6 +875,36 @@ void orc_softmax(float *a, int32_t len) {
 /* Llama-shaped decode step                                                  */
 /* ------------------------------------------------------------------------ */
 
+/* Single-token GQA attention over a position-major cache window, the decode
+ * runner's attention (GJB/GgufDecodeAttentionExecution.java:68-104): keys and
+ * values are [position][cache_head_stride], KV head h at offset h * head_dim;
+ * query head h reads KV head h / (query_heads / kv_heads); positions
+ * [start_position, sequence_length) are visible. Scores are the dot times
+ * `scale`, GGUFVectorOps.softmax normalises them (max, exp, 1/sum), and the
+ * value rows are added in position order (scaledAddInPlace). `scores` holds
+ * sequence_length - start_position floats. */
+void orc_decode_attention(const float *query, float *output, float *scores, const float *key_cache,
+                          const float *value_cache, int32_t cache_head_stride, int32_t kv_heads,
+                          int32_t query_heads, int32_t head_dim, int32_t sequence_length,
+                          int32_t start_position, float scale) {
+    const int32_t active = sequence_length - start_position;
+    for (int64_t i = 0; i < (int64_t)query_heads * head_dim; i++) output[i] = 0.0f;
+    for (int32_t h = 0; h < query_heads; h++) {
+        const int32_t kvh = h / (query_heads / kv_heads);
+        const float *q = query + (int64_t)h * head_dim;
+        for (int32_t p = start_position; p < sequence_length; p++)
+            scores[p - start_position] =
+                dot16(q, key_cache + (int64_t)p * cache_head_stride + (int64_t)kvh * head_dim, head_dim) * scale;
+        orc_softmax(scores, active);
+        float *o = output + (int64_t)h * head_dim;
+        for (int32_t p = start_position; p < sequence_length; p++) {
+            const float *vr = value_cache + (int64_t)p * cache_head_stride + (int64_t)kvh * head_dim;
+            const float s = scores[p - start_position];
+            for (int32_t j = 0; j < head_dim; j++) o[j] += s * vr[j];
+        }
+    }
+}
+
 /* y[n] = sum_k W[n][k] x[k] for one typed matrix (GgufDecodePass's per-type
  * row dots: GRT/GgufMatVec.java:27-97 dispatching on the GgmlType). */
 static void typed_mv(const orc_tensor *t, const float *x, int64_t n, int64_t k, float *y, int threads) {
@@ -937,19 +967,8 @@ int32_t orc_llama_decode_typed(const orc_llama_cfg *cfg, const orc_llama_typed *
             kc[(int64_t)pos * kvd + j] = cfg->kv_f16 ? orc_round_f16(kk[j]) : kk[j];
             vc[(int64_t)pos * kvd + j] = cfg->kv_f16 ? orc_round_f16(vv[j]) : vv[j];
         }
-        int32_t seq = pos + 1;
-        for (int32_t h = 0; h < nh; h++) {
-            int32_t kvh = h / (nh / nkv);
-            for (int32_t p = 0; p < seq; p++)
-                scores[p] = dot16(q + (int64_t)h * hd, kc + (int64_t)p * kvd + kvh * hd, hd) * scale;
-            orc_softmax(scores, seq);
-            float *o = att + (int64_t)h * hd;
-            for (int32_t j = 0; j < hd; j++) o[j] = 0.0f;
-            for (int32_t p = 0; p < seq; p++) {
-                const float *vr = vc + (int64_t)p * kvd + kvh * hd;
-                for (int32_t j = 0; j < hd; j++) o[j] += scores[p] * vr[j];
-            }
-        }
+        /* GgufDecodePass's attention: every cached position 0..pos, no window. */
+        orc_decode_attention(q, att, scores, kc, vc, kvd, nkv, nh, hd, pos + 1, 0, scale);
         typed_mv(&w->wo[l], att, dim, qd, xb, threads);
         for (int32_t j = 0; j < dim; j++) x[j] += xb[j];
         orc_rmsnorm(x, w->ffn_norm[l], xb, dim, cfg->eps);

@@ -162,6 +162,18 @@ void orc_softmax(float *a, int32_t len);
 
 /* ---- Llama-shaped decode step ------------------------------------------- */
 
+/* GJB/GgufDecodeAttentionExecution.java:68-104: single-token GQA attention
+ * over a position-major cache window ([position][cache_head_stride], KV head
+ * h at h * head_dim), positions [start_position, sequence_length) visible;
+ * `scores` holds sequence_length - start_position floats. The decode step's
+ * attention. Pinned by GgufDecodeAttentionExecutionTest.java:15-66 (GQA head
+ * mapping {15,15,150,150}, window {20,200}, {25}) and against the dense
+ * attention oracle (tests/test_oracle.py). */
+void orc_decode_attention(const float *query, float *output, float *scores, const float *key_cache,
+                          const float *value_cache, int32_t cache_head_stride, int32_t kv_heads,
+                          int32_t query_heads, int32_t head_dim, int32_t sequence_length,
+                          int32_t start_position, float scale);
+
 typedef struct orc_llama_cfg {
     int32_t layers, dim, ffn, n_heads, n_kv_heads, head_dim, vocab, max_seq;
     int32_t nf4_group;
@@ -210,8 +222,11 @@ typedef struct orc_llama_typed {
 } orc_llama_typed;
 /* GJB/GgufDecodePass.java:183-592 over per-tensor GGUF types: the same step
  * as orc_llama_decode (which runs through it) with each matvec dispatched on
- * its type and the embedding row decoded from its type. Pinned through the
- * per-type matvec and dequant checks and the NF4 decode tests. */
+ * its type and the embedding row decoded from its type. Its parts are pinned
+ * on their own (per-type matvec and dequant, RMSNorm/RoPE/SwiGLU KATs,
+ * orc_decode_attention's KATs); the composition is pinned by an independent
+ * full-sequence causal forward in numpy at every position and by closed forms
+ * (zero Wo and W_down; one layer at position 0) in tests/test_oracle.py. */
 int32_t orc_llama_decode_typed(const orc_llama_cfg *cfg, const orc_llama_typed *w,
                                int32_t token, int32_t pos, float *k_cache,
                                float *v_cache, float *logits, float *hidden,

@@ -270,6 +270,25 @@ def main() -> None:
                       "expected": [1, 2, 3, 4]},
     }
 
+    # GJBT/GgufDecodeAttentionExecutionTest.java:15-66: the decode runner's
+    # attention (GgufDecodeAttentionExecution.execute over position-major
+    # [position][cache_head_stride] arrays). Arguments in the order of the
+    # array form: cache_head_stride, kv_heads, query_heads, head_dim,
+    # sequence_length, start_position, scale. The session case (:48-66) reads
+    # positions 1..2 of a one-head cache holding values 10, 20, 30; its window
+    # is the same call on those three positions with start 1.
+    kats["decode_attention"] = [
+        {"source": "GJBT/GgufDecodeAttentionExecutionTest.java:15-29",
+         "query": [0.0] * 4, "keys": [0.0] * 4, "values": [10.0, 100.0, 20.0, 200.0],
+         "args": [2, 2, 4, 1, 2, 0, 1.0], "expected": [15.0, 15.0, 150.0, 150.0], "tolerance": 1e-6},
+        {"source": "GJBT/GgufDecodeAttentionExecutionTest.java:31-44",
+         "query": [0.0, 0.0], "keys": [0.0] * 4, "values": [10.0, 100.0, 20.0, 200.0],
+         "args": [2, 2, 2, 1, 2, 1, 1.0], "expected": [20.0, 200.0], "tolerance": 1e-6},
+        {"source": "GJBT/GgufDecodeAttentionExecutionTest.java:45-66",
+         "query": [0.0], "keys": [0.0] * 3, "values": [10.0, 20.0, 30.0],
+         "args": [1, 1, 1, 1, 3, 1, 1.0], "expected": [25.0], "tolerance": 1e-6},
+    ]
+
     with open(OUT, "w") as f:
         json.dump(kats, f, indent=1)
     print(f"wrote {OUT}")
