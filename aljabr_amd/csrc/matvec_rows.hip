@@ -52,7 +52,16 @@ constexpr int kChunk = 2048;
 constexpr int kFmtNF4 = 0, kFmtQ4 = 1, kFmtQ8 = 2, kFmtQ4K = 3, kFmtQ6K = 4;
 constexpr bool kquant_fmt(int f) { return f == kFmtQ4K || f == kFmtQ6K; }
 constexpr bool pair_table_fmt(int f) { return f == kFmtNF4 || f == kFmtQ4 || f == kFmtQ4K; }
-constexpr int kPairBytes = 256 * 256;          // 256 entries x 32 replicas x float2
+// Dynamic LDS: [0, kMainBytes) the pair table, [kMainBytes, 2 kMainBytes)
+// the activation windows (S windows of 8 KiB), then the wave partials and the
+// RMSNorm chunk sums. The table and the windows do not overlap, so the table
+// is built while the activations are still in flight and one barrier covers
+// both. The kernel declares no static LDS, so the table starts at address 0
+// and a lookup address is the v_perm result itself (a nonzero base costs one
+// v_add per lookup: the compiler cannot fold it into the ds_read offset
+// because the permuted address is not known to be non-negative).
+constexpr int kMainBytes = 256 * 256;   // 256 pair entries x 32 replicas x float2
+constexpr int kLdsBytes = 2 * kMainBytes;
 
 typedef unsigned int u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -162,29 +171,56 @@ __device__ __forceinline__ T seg_pick(const RowRef &f, T a0, T a1, T a2) {
     return f.s2 ? a2 : f.s1 ? a1 : a0;
 }
 
+// Per-lane byte offsets of a row's loads (loop-invariant): the row's address
+// is a wave-uniform base plus these, so every load takes the scalar-base form
+// and no row spends vector instructions on addresses.
+struct LaneOffsets {
+    uint32_t w;       // weight bytes from the row's chunk start
+    uint32_t s;       // NF4: absmax bytes from the row's chunk block
+};
+
+template <int FMT>
+__device__ __forceinline__ LaneOffsets lane_offsets(int lane, int bs_shift) {
+    LaneOffsets o{};
+    if constexpr (FMT == kFmtNF4) {
+        o.w = static_cast<uint32_t>(lane) * 16u;
+        o.s = (static_cast<uint32_t>(lane * 32) >> bs_shift) * 4u;
+    } else if constexpr (kquant_fmt(FMT)) {
+        constexpr uint32_t BB = FMT == kFmtQ4K ? kQ4KBytes : kQ6KBytes;
+        o.w = static_cast<uint32_t>(lane >> 3) * BB;
+    } else {
+        // Pair start (4-byte aligned) + 16 (Q4_0) or 32 (Q8_0) for the odd lane.
+        constexpr uint32_t BB = FMT == kFmtQ4 ? 18 : 34;
+        o.w = static_cast<uint32_t>(lane >> 1) * (2 * BB) + static_cast<uint32_t>(lane & 1) * (BB - 2);
+    }
+    return o;
+}
+
 template <int FMT, int EPI, int T>
-__device__ __forceinline__ void load_row(RowWords<FMT> &d, const RowsArgs &a, int row, int k0, int lane_blk) {
+__device__ __forceinline__ void load_row(RowWords<FMT> &d, const RowsArgs &a, int row, int chunk,
+                                         const LaneOffsets &o) {
     const RowRef f = row_ref<EPI, T>(a, row);
     const size_t local = static_cast<size_t>(f.local);
     const uint8_t *w = seg_pick(f, a.seg[0].w, a.seg[1].w, a.seg[2].w);
     if constexpr (FMT == kFmtNF4) {
+        // bs divides K here (bs <= 2048 = the chunk), so the row's blocks
+        // start at local * K / bs.
         const float *absmax = seg_pick(f, a.seg[0].absmax, a.seg[1].absmax, a.seg[2].absmax);
-        const size_t row_bytes = static_cast<size_t>(a.K) >> 1;
-        d.q = load_stream16(w + local * row_bytes + (k0 >> 1));
-        d.s = absmax[(local * a.K + k0) >> a.bs_shift];
+        const uint8_t *rw = w + local * (static_cast<size_t>(a.K) >> 1) + static_cast<size_t>(chunk) * (kChunk / 2);
+        const uint8_t *rs = reinterpret_cast<const uint8_t *>(
+            absmax + ((local * static_cast<size_t>(a.K) + static_cast<size_t>(chunk) * kChunk) >> a.bs_shift));
+        d.q = load_stream16(rw + o.w);
+        d.s = *reinterpret_cast<const float *>(rs + o.s);
     } else if constexpr (kquant_fmt(FMT)) {
-        // lane_blk = chunk*64 + lane: super-block lane_blk/8 of the row, lane j = lane_blk%8.
         constexpr int BB = FMT == kFmtQ4K ? kQ4KBytes : kQ6KBytes;
-        const size_t row_bytes = static_cast<size_t>(a.K >> 8) * BB;
-        const uint8_t *blk = w + local * row_bytes + static_cast<size_t>(lane_blk >> 3) * BB;
-        if constexpr (FMT == kFmtQ4K) load_q4k(d, blk, lane_blk & 7);
-        else load_q6k(d, blk, lane_blk & 7);
+        const uint8_t *rw = w + local * (static_cast<size_t>(a.K >> 8) * BB) + static_cast<size_t>(chunk) * (8 * BB);
+        const int j = __lane_id() & 7;
+        if constexpr (FMT == kFmtQ4K) load_q4k(d, rw + o.w, j);
+        else load_q6k(d, rw + o.w, j);
     } else {
         constexpr int BB = FMT == kFmtQ4 ? 18 : 34;
-        const size_t row_bytes = static_cast<size_t>(a.K >> 5) * BB;
-        // Pair start (4-byte aligned) + 16 (Q4_0) or 32 (Q8_0) for the odd lane.
-        const uint8_t *p = w + local * row_bytes + static_cast<size_t>(lane_blk >> 1) * (2 * BB) +
-                           (lane_blk & 1) * (BB - 2);
+        const uint8_t *rw = w + local * (static_cast<size_t>(a.K >> 5) * BB) + static_cast<size_t>(chunk) * (64 * BB);
+        const uint8_t *p = rw + o.w;
         if constexpr (FMT == kFmtQ4) {
             d.a = load_stream16_a4(p);
             d.b = load_stream4(p + 16);
@@ -202,8 +238,13 @@ __device__ __forceinline__ uint32_t pair_addr(uint32_t w, uint32_t cl) {
     return __builtin_amdgcn_perm(w, cl, 0x0C0C0000u | ((4u + BYTE) << 8));
 }
 
-__device__ __forceinline__ float2 pair_at(const char *tbl, uint32_t addr) {
-    return *reinterpret_cast<const float2 *>(tbl + addr);
+// The table sits at LDS address 0 (kMainBytes), so the byte address is the
+// LDS pointer itself; `tbl` is unused by the load.
+__device__ __forceinline__ float2 pair_at(const char *, uint32_t addr) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef const f32x2 __attribute__((address_space(3))) lds_f32x2;
+    const f32x2 v = *(lds_f32x2 *)(static_cast<uintptr_t>(addr));
+    return make_float2(v.x, v.y);
 }
 
 // sum over the lane's 32 weights of w*x, before the row/block scale.
@@ -351,13 +392,17 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
 
-template <int FMT, int T, int PF, int W, int XOP, int EPI>
+// P0 rows are requested before the set-up (table build, activation staging)
+// and PF rows stay in flight afterwards: a deeper prologue keeps HBM busy
+// while the activations arrive, a shallower steady state measured faster.
+template <int FMT, int T, int PF, int W, int XOP, int EPI, int P0>
 __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
-    static_assert(T >= 1 && T <= 32 && PF >= 1 && (W == 8 || W == 16), "tile shape");
+    static_assert(T >= 1 && T <= 32 && PF >= 1 && P0 >= PF && (W == 8 || W == 16), "tile shape");
     constexpr int TP = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : T <= 16 ? 16 : 32;   // butterfly width
-    extern __shared__ float4 smem[];    // 4-bit: pair table (x windows alias it); Q8_0: x windows
-    __shared__ float part[W][TP];
-    __shared__ float ssq[8];            // kXNorm: per-chunk sums of squares
+    extern __shared__ float4 smem[];    // see kMainBytes
+    float(*part)[TP] = reinterpret_cast<float(*)[TP]>(reinterpret_cast<char *>(smem) + kLdsBytes);
+    float *ssq = reinterpret_cast<float *>(reinterpret_cast<char *>(smem) + kLdsBytes) + W * TP;  // kXNorm
+    f32x4 *xwin = reinterpret_cast<f32x4 *>(reinterpret_cast<char *>(smem) + kMainBytes);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     // Wave-uniform in a scalar register, so row and segment arithmetic is scalar.
@@ -368,14 +413,12 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     float2 *tbl2 = reinterpret_cast<float2 *>(smem);
 
     if (grp >= a.G) {
-        // Helper wave (when S does not divide 8): takes part in the table
+        // Helper wave (when S does not divide W): takes part in the table
         // build and meets the same workgroup barriers, nothing else.
-        if constexpr (XOP == kXNorm) __syncthreads();        // 0: chunk sums of squares
-        __syncthreads();                                     // 1: x staged
-        __syncthreads();                                     // 2: x read
         if constexpr (pair_table_fmt(FMT)) build_pair_table<FMT, W * 64>(tbl2, tid);
-        __syncthreads();                                     // 3: table built
-        __syncthreads();                                     // 4: partials written
+        if constexpr (XOP == kXNorm) __syncthreads();        // 0: chunk sums of squares
+        __syncthreads();                                     // 1: table built, x staged
+        __syncthreads();                                     // 2: partials written
         return;
     }
 
@@ -385,8 +428,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     // interleaving rows across the grid).
     const int row0 = (blockIdx.x * a.G + grp) * T;
     const int rstride = 1;
-    const int k0 = chunk * kChunk + lane * 32;
-    const int lane_blk = chunk * 64 + lane;      // Q4_0/Q8_0 block index in the row
+    const LaneOffsets lo = lane_offsets<FMT>(lane, a.bs_shift);
 
     // Activations first (vmcnt retires in order: waiting for them then
     // leaves the weight loads in flight).
@@ -406,7 +448,9 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     }
     RowWords<FMT> rw[T];
 #pragma unroll
-    for (int t = 0; t < PF && t < T; ++t) load_row<FMT, EPI, T>(rw[t], a, min(row0 + t * rstride, a.N - 1), k0, lane_blk);
+    for (int t = 0; t < P0 && t < T; ++t) load_row<FMT, EPI, T>(rw[t], a, min(row0 + t * rstride, a.N - 1), chunk, lo);
+    // The table does not depend on the loads: build it while they fly.
+    if constexpr (pair_table_fmt(FMT)) build_pair_table<FMT, W * 64>(tbl2, tid);
 
     if constexpr (XOP == kXNorm) {
         // RMSNorm over the whole row of K activations: chunk sums of squares
@@ -437,17 +481,17 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
 
     // Stage x: float4 f of chunk c at slot c*512 + (f/8)*8 + ((f%8) ^ ((f/8)%8)).
     if (stager) {
-        f32x4 *win = reinterpret_cast<f32x4 *>(smem) + chunk * 512;
+        f32x4 *win = xwin + chunk * 512;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int f = 64 * j + lane;
             win[(f >> 3) * 8 + ((f & 7) ^ ((f >> 3) & 7))] = xl[j];
         }
     }
-    __syncthreads();                                         // 1
+    __syncthreads();                                         // 1: table built, x staged
     float xv[32];
     {
-        const f32x4 *win = reinterpret_cast<const f32x4 *>(smem) + chunk * 512;
+        const f32x4 *win = xwin + chunk * 512;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int f = x_f4<FMT>(lane, i);
@@ -469,9 +513,6 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
             xsum2 += xv[16 + i];
         }
     }
-    __syncthreads();                                         // 2: the table overwrites the x windows
-    if constexpr (pair_table_fmt(FMT)) build_pair_table<FMT, W * 64>(tbl2, tid);
-    __syncthreads();                                         // 3
 
     const char *tbl = reinterpret_cast<const char *>(smem);
     const uint32_t cl = (lane & 31) * 8;
@@ -481,7 +522,8 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     for (int t = T; t < TP; ++t) acc[t] = 0.0f;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        if (t + PF < T) load_row<FMT, EPI, T>(rw[t + PF], a, min(row0 + (t + PF) * rstride, a.N - 1), k0, lane_blk);
+        if (t + PF < T && t + PF >= P0)
+            load_row<FMT, EPI, T>(rw[t + PF], a, min(row0 + (t + PF) * rstride, a.N - 1), chunk, lo);
         float scale;
         const float dot = row_dot<FMT>(rw[t], xv, xsum, xsum2, odd, cl, tbl, scale);
         acc[t] = dot * scale;
@@ -492,7 +534,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     }
     const float tot = wave_sum_rows<TP>(acc);
     if (lane < TP) part[wave][wave_rows_index<TP>(lane)] = tot;
-    __syncthreads();                                         // 4
+    __syncthreads();                                         // 2: partials written
     // The S chunk waves of group g are waves g*S .. g*S+S-1.
     const int r = row0 + lane;
     if (chunk == 0 && lane < T && r < a.N) {
@@ -542,10 +584,11 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     }
 }
 
-template <int FMT, int T, int PF, int W, int XOP, int EPI>
+template <int FMT, int T, int PF, int W, int XOP, int EPI, int P0 = PF>
 void launch_cfg(const RowsArgs &args, hipStream_t s) {
-    const void *fn = reinterpret_cast<const void *>(rows_kernel<FMT, T, PF, W, XOP, EPI>);
-    const size_t lds = pair_table_fmt(FMT) ? kPairBytes : static_cast<size_t>(args.S) * 512 * sizeof(float4);
+    const void *fn = reinterpret_cast<const void *>(rows_kernel<FMT, T, PF, W, XOP, EPI, P0>);
+    constexpr int TP = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : T <= 16 ? 16 : 32;
+    const size_t lds = kLdsBytes + (W * TP + 8) * sizeof(float);
     static bool lds_set = false;                 // the attribute is per kernel, per process
     if (!lds_set) {
         (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
@@ -553,28 +596,36 @@ void launch_cfg(const RowsArgs &args, hipStream_t s) {
     }
     const int rows_per_wg = args.G * T;
     const dim3 grid((args.N + rows_per_wg - 1) / rows_per_wg), block(W * 64);
-    hipLaunchKernelGGL((rows_kernel<FMT, T, PF, W, XOP, EPI>), grid, block, lds, s, args);
+    hipLaunchKernelGGL((rows_kernel<FMT, T, PF, W, XOP, EPI, P0>), grid, block, lds, s, args);
 }
 
-// T rows per wave (2..32), loads PF = min(T, 4) rows ahead, 8 waves.
-template <int FMT, int XOP, int EPI>
-void launch_rows(RowsArgs args, int T, hipStream_t s) {
-    args.G = 8 / args.S;
+// T rows per wave (2..32), 8 waves; loads PF rows ahead: 3 when a wave's
+// chunk row is most of its row (S <= 2), 4 for longer rows (measured on the
+// Llama MLP shapes: 14336 x 4096 and 4096 x 14336).
+template <int FMT, int XOP, int EPI, int PF>
+void launch_rows_pf(const RowsArgs &args, int T, hipStream_t s) {
     switch (T) {
-    case 32: launch_cfg<FMT, 32, 4, 8, XOP, EPI>(args, s); break;
-    case 28: launch_cfg<FMT, 28, 4, 8, XOP, EPI>(args, s); break;
-    case 24: launch_cfg<FMT, 24, 4, 8, XOP, EPI>(args, s); break;
-    case 20: launch_cfg<FMT, 20, 4, 8, XOP, EPI>(args, s); break;
-    case 16: launch_cfg<FMT, 16, 4, 8, XOP, EPI>(args, s); break;
-    case 14: launch_cfg<FMT, 14, 4, 8, XOP, EPI>(args, s); break;
-    case 12: launch_cfg<FMT, 12, 4, 8, XOP, EPI>(args, s); break;
-    case 10: launch_cfg<FMT, 10, 4, 8, XOP, EPI>(args, s); break;
-    case 8: launch_cfg<FMT, 8, 4, 8, XOP, EPI>(args, s); break;
-    case 7: launch_cfg<FMT, 7, 4, 8, XOP, EPI>(args, s); break;
-    case 6: launch_cfg<FMT, 6, 4, 8, XOP, EPI>(args, s); break;
+    case 32: launch_cfg<FMT, 32, PF, 8, XOP, EPI>(args, s); break;
+    case 28: launch_cfg<FMT, 28, PF, 8, XOP, EPI>(args, s); break;
+    case 24: launch_cfg<FMT, 24, PF, 8, XOP, EPI>(args, s); break;
+    case 20: launch_cfg<FMT, 20, PF, 8, XOP, EPI>(args, s); break;
+    case 16: launch_cfg<FMT, 16, PF, 8, XOP, EPI>(args, s); break;
+    case 14: launch_cfg<FMT, 14, PF, 8, XOP, EPI>(args, s); break;
+    case 12: launch_cfg<FMT, 12, PF, 8, XOP, EPI>(args, s); break;
+    case 10: launch_cfg<FMT, 10, PF, 8, XOP, EPI>(args, s); break;
+    case 8: launch_cfg<FMT, 8, PF, 8, XOP, EPI>(args, s); break;
+    case 7: launch_cfg<FMT, 7, PF, 8, XOP, EPI>(args, s); break;
+    case 6: launch_cfg<FMT, 6, PF, 8, XOP, EPI>(args, s); break;
     case 4: launch_cfg<FMT, 4, 2, 8, XOP, EPI>(args, s); break;
     default: launch_cfg<FMT, 2, 2, 8, XOP, EPI>(args, s); break;
     }
+}
+
+template <int FMT, int XOP, int EPI>
+void launch_rows(RowsArgs args, int T, hipStream_t s) {
+    args.G = 8 / args.S;
+    if (args.S <= 2) launch_rows_pf<FMT, XOP, EPI, 3>(args, T, s);
+    else launch_rows_pf<FMT, XOP, EPI, 4>(args, T, s);
 }
 
 // Rows per wave: the per-workgroup set-up (activation staging, the 64 KiB
@@ -603,7 +654,9 @@ int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax
     if (!rows_shape_ok(A, K)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     int fmt;
     if (type == ALJABR_ROCM_TYPE_NF4) {
-        if (bs_shift < 5 || !aligned(W, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        // Blocks of 32 .. 2048 weights: a lane's 32 weights share one absmax
+        // and a chunk's blocks start on its first weight.
+        if (bs_shift < 5 || bs_shift > 11 || !aligned(W, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
         fmt = kFmtNF4;
     } else if (type == ALJABR_ROCM_TYPE_Q4_0 || type == ALJABR_ROCM_TYPE_Q8_0) {
         if (!aligned(W, 4)) return ALJABR_ROCM_ERR_UNSUPPORTED;
@@ -668,7 +721,7 @@ int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const 
 int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
                        int bs_shift, int epilogue, const RowsRope *rope) {
     if (nseg < 1 || nseg > 3 || !rows_shape_ok(x, K)) return ALJABR_ROCM_ERR_UNSUPPORTED;
-    if (type == ALJABR_ROCM_TYPE_NF4 && bs_shift < 5) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    if (type == ALJABR_ROCM_TYPE_NF4 && (bs_shift < 5 || bs_shift > 11)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     if (type != ALJABR_ROCM_TYPE_NF4 && type != ALJABR_ROCM_TYPE_Q4_0 && type != ALJABR_ROCM_TYPE_Q8_0 &&
         type != ALJABR_ROCM_TYPE_Q4_K && type != ALJABR_ROCM_TYPE_Q6_K)
         return ALJABR_ROCM_ERR_UNSUPPORTED;

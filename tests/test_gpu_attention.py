@@ -105,13 +105,17 @@ def test_more_queries_than_keys_gives_zero_rows(rocm, dev, oracle):
     assert np.all(out[:, :, :3] == 0) and rel_l2(out, ref) <= TOL
 
 
-def test_full_size_b64_s32768_spot_rows(rocm, dev, oracle):
-    """B=64, S=32768: 8 GiB of fp16 K/V generated on the device; three
-    (batch, kv-head) groups are checked against the oracle on their slices,
-    and every output row must be a convex combination of V (finite, bounded)."""
+# BASELINE configs[3] points too large for the oracle over every head: fp16
+# K/V generated on the device (8 GiB at B=64, S=32768), three (batch,
+# kv-head) groups checked against the oracle on their slices, and every
+# output row a convex combination of V (finite, bounded).
+@pytest.mark.parametrize("b,s", [(64, 32768), (16, 32768), (64, 4096)], ids=["b64-s32768", "b16-s32768",
+                                                                          "b64-s4096"])
+def test_full_size_spot_rows(rocm, dev, oracle, b, s):
     import torch
-    b, hq, hkv, s, d = 64, 32, 8, 32768, 128
-    gen = torch.Generator(device="cuda:0").manual_seed(1234)
+    hq, hkv, d = 32, 8, 128
+    print(f"\n[attention full size] B={b} S={s}", flush=True)
+    gen = torch.Generator(device="cuda:0").manual_seed(1234 + b + s)
     k = torch.randn((b, hkv, s, d), generator=gen, device="cuda:0", dtype=torch.float16)
     v = torch.randn((b, hkv, s, d), generator=gen, device="cuda:0", dtype=torch.float16)
     q = torch.randn((b, hq, 1, d), generator=gen, device="cuda:0", dtype=torch.float32)
@@ -124,7 +128,7 @@ def test_full_size_b64_s32768_spot_rows(rocm, dev, oracle):
     assert np.all(np.isfinite(o))
     vmax = float(v.abs().max().item())
     assert np.abs(o).max() <= vmax + 1e-3
-    for bi, kvh in [(0, 0), (31, 5), (63, 7)]:
+    for bi, kvh in [(0, 0), (b // 2 - 1, 5), (b - 1, 7)]:
         ks = k[bi:bi + 1, kvh:kvh + 1].float().cpu().numpy()
         vs = v[bi:bi + 1, kvh:kvh + 1].float().cpu().numpy()
         qs = q[bi:bi + 1, kvh * 4:(kvh + 1) * 4].cpu().numpy()
