@@ -136,6 +136,7 @@ SIGNATURES = {
     "aljabr_rocm_dequantize": (_I, [_P, _P, _P, _LL, _I, _I]),
     "aljabr_rocm_quantize": (_I, [_P, _P, _P, _LL, _I, _I]),
     "aljabr_rocm_attention_gqa": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I]),
+    "aljabr_rocm_attention_gqa_noalloc": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I]),
     "aljabr_rocm_matvec_tb_pair": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
     "aljabr_rocm_matvec_tb_triple": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I]),
     "aljabr_rocm_matvec_tb_triple_batch": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I]),

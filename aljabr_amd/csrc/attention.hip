@@ -18,6 +18,7 @@
 // combines splits. Scores use exp2 with log2(e) folded into the query.
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
 
 #include "device.hpp"
 #include "internal.hpp"
@@ -543,6 +544,12 @@ int enqueue_attention(const AttnParams &p_in) {
     const long long max_splits = (keys + 63) / 64;
     if (want > max_splits) want = max_splits;
     if (want < 1) want = 1;
+    const size_t split_bytes = static_cast<size_t>(p.B) * p.Hq * p.Sq * (p.D + 2) * sizeof(float);
+    if (p.scratch_only) {
+        // Partials only in the caller's buffer: as many splits as it holds.
+        const long long fit = p.scratch ? static_cast<long long>(p.scratch_bytes / split_bytes) : 0;
+        if (want > fit) want = fit < 2 ? 1 : fit;
+    }
     int splits = static_cast<int>(want);
     int chunk = (keys + splits - 1) / splits;
     chunk = (chunk + 15) & ~15;
@@ -550,9 +557,11 @@ int enqueue_attention(const AttnParams &p_in) {
     if (splits < 1) splits = 1;
     float *part = nullptr;
     if (splits > 1) {
-        const size_t bytes = static_cast<size_t>(p.B) * p.Hq * p.Sq * splits * (p.D + 2) * sizeof(float);
-        part = p.scratch && bytes <= p.scratch_bytes ? p.scratch : static_cast<float *>(stream_scratch(bytes));
-        if (!part) return ALJABR_ROCM_ERR_BUFFER;
+        const size_t bytes = static_cast<size_t>(splits) * split_bytes;
+        if (p.scratch && bytes <= p.scratch_bytes) part = p.scratch;
+        else if (!p.scratch_only) part = static_cast<float *>(stream_scratch(bytes));
+        if (!part) return p.scratch_only ? fail(ALJABR_ROCM_ERR_BUFFER, "attention: split partials exceed the caller's scratch")
+                                         : ALJABR_ROCM_ERR_BUFFER;
     }
     if (p.D == 64)
         return p.kv_f16 ? launch_paged<64, true>(p, G, splits, chunk, part, s)
@@ -603,6 +612,86 @@ extern "C" int aljabr_rocm_attention_gqa(void *out, const void *Q, const void *K
     int rc = enqueue_attention(p);
     if (rc) return rc;
     return finish_launch("attention_gqa");
+}
+
+// ---- allocation-free attention ---------------------------------------------
+//
+// aljabr_rocm_attention_gqa_noalloc keeps its split partials in `scratch`, a
+// file-scope device array that every GPU the library runs on holds until the
+// process ends (kNoAllocScratchBytes each). Host code never passes the
+// array's name to a kernel: it is a host-side stand-in, not a device address.
+// The device address comes from hipGetSymbolAddress, once per device, with
+// that device current, and is kept per device. Calls on one GPU share the
+// array, so calls that overlap in time on one GPU race; every slot a call
+// reads was written by the same call (the split kernel writes every split's
+// partials before the merge reads them), so nothing needs clearing.
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;   // 8 MiB per GPU
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up once).
+int noalloc_scratch(float **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(ALJABR_ROCM_ERR_DEVICE, "device ordinal %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(ALJABR_ROCM_ERR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = static_cast<float *>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return ALJABR_ROCM_OK;
+}
+
+}  // namespace
+
+extern "C" int aljabr_rocm_attention_gqa_noalloc(void *out, const void *Q, const void *K, const void *V,
+                                                 const void *mask, int B, int Hq, int Hkv, int Sq, int Sk, int D,
+                                                 int kvType, float scale, int causal) {
+    ALJ_CHECK_READY();
+    ALJ_REQUIRE(out && Q && K && V, "out, Q, K and V must be non-null device pointers");
+    ALJ_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Sq > 0 && Sk > 0 && D > 0 && Hq % Hkv == 0,
+                "GQA expects Q[B,Hq,Sq,D], K/V[B,Hkv,Sk,D] with Hq divisible by Hkv");
+    if (kvType != ALJABR_ROCM_TYPE_F32 && kvType != ALJABR_ROCM_TYPE_F16)
+        return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "attention: K/V type %d is not F32 or F16", kvType);
+    if (mask)
+        return fail(ALJABR_ROCM_ERR_UNSUPPORTED,
+                    "attention_gqa_noalloc takes no mask (its check copies a flag to the host); use "
+                    "aljabr_rocm_attention_gqa");
+    // Two splits of partials for every query row must fit the array, so that
+    // the split count can always be lowered to what it holds.
+    const size_t rows = static_cast<size_t>(B) * Hq * Sq;
+    if (rows * 2 * (static_cast<size_t>(D) + 2) * sizeof(float) > kNoAllocScratchBytes)
+        return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT,
+                    "attention_gqa_noalloc: B*Hq*Sq*2*(D+2)*4 = %zu bytes exceeds its %zu-byte scratch",
+                    rows * 2 * (static_cast<size_t>(D) + 2) * sizeof(float), kNoAllocScratchBytes);
+    float *buf = nullptr;
+    int rc = noalloc_scratch(&buf);
+    if (rc) return rc;
+    AttnParams p{};
+    p.out = static_cast<float *>(out);
+    p.q = static_cast<const float *>(Q);
+    p.k = K;
+    p.v = V;
+    p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.Sq = Sq; p.Sk = Sk; p.D = D; p.cap = Sk;
+    p.scale = scale > 0.0f ? scale : static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));
+    p.causal = causal != 0;
+    p.kv_f16 = kvType == ALJABR_ROCM_TYPE_F16;
+    p.scratch = buf;
+    p.scratch_bytes = kNoAllocScratchBytes;
+    p.scratch_only = 1;
+    rc = enqueue_attention(p);
+    if (rc) return rc;
+    return finish_launch("attention_gqa_noalloc");
 }
 
 namespace aljabr {

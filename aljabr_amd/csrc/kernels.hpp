@@ -31,6 +31,7 @@ struct AttnParams {
     long long q_sb, q_sh, q_sq;   // element strides of q and out (0: [B][Hq][Sq][D])
     float *scratch;         // split partials: caller-owned (graph-safe) when it holds attention_scratch_bytes(),
     size_t scratch_bytes;   // else (null or too small) the stream's scratch
+    int scratch_only;       // never use the stream's scratch: fewer splits when the partials would not fit
 };
 
 int enqueue_attention(const AttnParams &p);

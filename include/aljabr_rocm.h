@@ -186,6 +186,20 @@ int aljabr_rocm_attention_gqa(void *out, const void *Q, const void *K, const voi
                               const void *mask, int B, int Hq, int Hkv, int Sq,
                               int Sk, int D, int kvType, float scale, int causal);
 
+/* No counterpart in the reference: aljabr_rocm_attention_gqa for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments and results, mask must be
+ * NULL (-3 otherwise). The split partials live in an 8 MiB device array each
+ * GPU holds until the process ends: B*Hq*Sq*2*(D+2)*4 bytes must fit in it
+ * (-2 otherwise), and the split count is lowered to what it holds. No device
+ * or host allocation happens (the calling thread's stream is the one set with
+ * aljabr_rocm_set_stream; without one, a thread's first call to the library
+ * creates its stream). Calls that overlap in time on one GPU share the array
+ * and race. */
+int aljabr_rocm_attention_gqa_noalloc(void *out, const void *Q, const void *K, const void *V,
+                                      const void *mask, int B, int Hq, int Hkv, int Sq,
+                                      int Sk, int D, int kvType, float scale, int causal);
+
 /* Paged-KV attention with the argument lists of the Metal bridge
  * (MTLC/aljabr_metal_attention.h:14-36, semantics of aljabr_metal_attention_impl,
  * MTLC/aljabr_metal_attention.m:146-355): Q and out [B,T,H,D] fp32; K/V caches
