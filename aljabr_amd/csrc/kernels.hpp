@@ -81,6 +81,10 @@ int enqueue_nf4_rows(float *C, const float *A, const uint8_t *Bq, const float *a
 // Q4_0 codes (K % 2048 == 0, K <= 16384; NF4 block size >= 32, 16-byte
 // aligned codes; Q4_0/Q8_0 rows 4-byte aligned, K-quant rows 16-byte
 // aligned). `type` is an ALJABR_ROCM_TYPE_* id.
+// C[M][N] = A[M][K] . W^T for M = 2..4 NF4 tokens on the batch-1 rows kernel
+// (fp32); ALJABR_ROCM_ERR_UNSUPPORTED (nothing launched) outside its limits.
+int enqueue_rows_nf4_mt(float *C, const float *A, const uint8_t *W, const float *absmax, int K, int N, int bs_shift,
+                        int M);
 int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax, int K, int N, int type,
                  int bs_shift);
 // One weight matrix of a fused batch-1 NF4 launch: y[0..n) = W[n][K] . x'.

@@ -461,6 +461,12 @@ namespace aljabr {
 // M > 8 slices run the small-M kernels per slice of 8 tokens (weights are
 // re-read per slice); the MFMA path takes over at its threshold.
 int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M) {
+    // M = 2..4 on the batch-1 rows kernel (fp32, the weights streamed once).
+    if (M >= 2 && M <= 4) {
+        const int shift = log2_exact(bs);
+        if (shift >= 0 && enqueue_rows_nf4_mt(C, A, Bq, absmax, K, N, shift, M) == ALJABR_ROCM_OK)
+            return ALJABR_ROCM_OK;
+    }
     // M >= 2 on the matrix cores when the shape allows, 64 tokens per pass.
     if (M >= 2 && mfma_enabled()) {
         const int shift = log2_exact(bs);

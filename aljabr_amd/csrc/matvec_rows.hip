@@ -647,6 +647,204 @@ bool rows_shape_ok(const float *A, int K) {
     return K % kChunk == 0 && S >= 1 && S <= 8 && aligned(A, 16);
 }
 
+
+// The batch-1 structure for MT = 2..4 NF4 tokens (a short prompt chunk or a
+// small decode batch) in fp32: the same rows, pair table and activation
+// staging, and every code byte's table lookup feeds the FMAs of all MT
+// tokens, so the weights stream once and each token costs one FMA per
+// weight. The activations of a round of R = 8/S tokens are staged together,
+// one token per row group; K chunks of the MT tokens live in registers.
+template <int T, int PF, int MT>
+__global__ __launch_bounds__(512) void rows_mt_kernel(RowsArgs a) {
+    constexpr int W = 8;
+    constexpr int TP = T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : T <= 16 ? 16 : 32;
+    static_assert(MT >= 2 && MT <= 4 && T <= 32, "tile shape");
+    extern __shared__ float4 smem[];
+    float *part = reinterpret_cast<float *>(reinterpret_cast<char *>(smem) + kLdsBytes);   // [W][MT][TP]
+    f32x4 *xwin = reinterpret_cast<f32x4 *>(reinterpret_cast<char *>(smem) + kMainBytes);
+    float2 *tbl2 = reinterpret_cast<float2 *>(smem);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int S = a.S;
+    const int chunk = wave % S;
+    const int grp = wave / S;
+    const int R = 8 / S;                         // tokens staged per round (one per row group)
+    const int rounds = (MT + R - 1) / R;
+    const bool helper = grp >= a.G;
+    const int row0 = (blockIdx.x * a.G + grp) * T;
+    const int xoff = chunk * kChunk;
+
+    // Round 0's activations first, then the weight prologue.
+    f32x4 xl[8];
+    const bool stage0 = !helper && grp < MT;
+    if (stage0) {
+        const f32x4 *xw = reinterpret_cast<const f32x4 *>(a.x + static_cast<size_t>(grp) * a.K + xoff);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xl[j] = xw[64 * j + lane];
+    }
+    const LaneOffsets lo = lane_offsets<kFmtNF4>(lane, a.bs_shift);
+    RowWords<kFmtNF4> rw[T];
+    if (!helper) {
+#pragma unroll
+        for (int t = 0; t < PF && t < T; ++t) load_row<kFmtNF4, kEStore, T>(rw[t], a, min(row0 + t, a.N - 1), chunk, lo);
+    }
+    build_pair_table<kFmtNF4, W * 64>(tbl2, tid);
+
+    float xv[MT][32];
+    for (int rd = 0; rd < rounds; ++rd) {
+        const int m = rd * R + grp;              // the token this wave stages
+        const bool stager = !helper && grp < R && m < MT;
+        if (stager) {
+            if (rd > 0) {
+                const f32x4 *xw = reinterpret_cast<const f32x4 *>(a.x + static_cast<size_t>(m) * a.K + xoff);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xl[j] = xw[64 * j + lane];
+            }
+            // Token slot grp of this round, chunk `chunk`: 512 float4s,
+            // swizzled as in rows_kernel (conflict-free both ways).
+            f32x4 *win = xwin + (grp * S + chunk) * 512;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int f = 64 * j + lane;
+                win[(f >> 3) * 8 + ((f & 7) ^ ((f >> 3) & 7))] = xl[j];
+            }
+        }
+        __syncthreads();
+        if (!helper) {
+#pragma unroll
+            for (int mm = 0; mm < MT; ++mm) {
+                if (mm / R != rd) continue;      // uniform: staged in another round
+                const f32x4 *win = xwin + ((mm % R) * S + chunk) * 512;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int f = lane * 8 + i;
+                    const f32x4 v = win[(f >> 3) * 8 + ((f & 7) ^ ((f >> 3) & 7))];
+                    xv[mm][4 * i + 0] = v.x;
+                    xv[mm][4 * i + 1] = v.y;
+                    xv[mm][4 * i + 2] = v.z;
+                    xv[mm][4 * i + 3] = v.w;
+                }
+            }
+        }
+        if (rd + 1 < rounds) __syncthreads();    // the next round overwrites the windows
+    }
+
+    if (!helper) {
+        const uint32_t cl = (lane & 31) * 8;
+        float acc[MT][TP];
+#pragma unroll
+        for (int mm = 0; mm < MT; ++mm)
+#pragma unroll
+            for (int t = 0; t < TP; ++t) acc[mm][t] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            if (t + PF < T) load_row<kFmtNF4, kEStore, T>(rw[t + PF], a, min(row0 + t + PF, a.N - 1), chunk, lo);
+            const uint32_t wv[4] = {rw[t].q.x, rw[t].q.y, rw[t].q.z, rw[t].q.w};
+            float p0[MT], p1[MT];
+#pragma unroll
+            for (int mm = 0; mm < MT; ++mm) p0[mm] = p1[mm] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float2 e[4];
+                e[0] = pair_at(nullptr, pair_addr<0>(wv[i], cl));
+                e[1] = pair_at(nullptr, pair_addr<1>(wv[i], cl));
+                e[2] = pair_at(nullptr, pair_addr<2>(wv[i], cl));
+                e[3] = pair_at(nullptr, pair_addr<3>(wv[i], cl));
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+#pragma unroll
+                    for (int mm = 0; mm < MT; ++mm) {
+                        p0[mm] = fmaf(e[b].x, xv[mm][8 * i + 2 * b], p0[mm]);
+                        p1[mm] = fmaf(e[b].y, xv[mm][8 * i + 2 * b + 1], p1[mm]);
+                    }
+            }
+#pragma unroll
+            for (int mm = 0; mm < MT; ++mm) {
+                acc[mm][t] = (p0[mm] + p1[mm]) * rw[t].s;
+                asm volatile("" : "+v"(acc[mm][t]));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int mm = 0; mm < MT; ++mm) {
+            const float tot = wave_sum_rows<TP>(acc[mm]);
+            if (lane < TP) part[(wave * MT + mm) * TP + wave_rows_index<TP>(lane)] = tot;
+        }
+    }
+    __syncthreads();
+    const int r = row0 + lane;
+    if (!helper && chunk == 0 && lane < T && r < a.N) {
+#pragma unroll
+        for (int mm = 0; mm < MT; ++mm) {
+            float v = 0.0f;
+            for (int c = 0; c < S; ++c) v += part[((grp * S + c) * MT + mm) * TP + lane];
+            a.seg[0].y[static_cast<size_t>(mm) * a.N + r] = v;
+        }
+    }
+}
+
+template <int T, int PF, int MT>
+void launch_mt_cfg(const RowsArgs &args, hipStream_t s) {
+    const void *fn = reinterpret_cast<const void *>(rows_mt_kernel<T, PF, MT>);
+    constexpr int TP = T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : T <= 16 ? 16 : 32;
+    const size_t lds = kLdsBytes + 8 * MT * TP * sizeof(float);
+    static bool lds_set = false;
+    if (!lds_set) {
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+        lds_set = true;
+    }
+    const int rows_per_wg = args.G * T;
+    hipLaunchKernelGGL((rows_mt_kernel<T, PF, MT>), dim3((args.N + rows_per_wg - 1) / rows_per_wg), dim3(512), lds,
+                       s, args);
+}
+
+template <int MT>
+void launch_mt(const RowsArgs &args, int T, hipStream_t s) {
+    switch (T) {
+    case 32: launch_mt_cfg<32, 3, MT>(args, s); break;
+    case 28: launch_mt_cfg<28, 3, MT>(args, s); break;
+    case 24: launch_mt_cfg<24, 3, MT>(args, s); break;
+    case 20: launch_mt_cfg<20, 3, MT>(args, s); break;
+    case 16: launch_mt_cfg<16, 3, MT>(args, s); break;
+    case 14: launch_mt_cfg<14, 3, MT>(args, s); break;
+    case 12: launch_mt_cfg<12, 3, MT>(args, s); break;
+    case 10: launch_mt_cfg<10, 3, MT>(args, s); break;
+    case 8: launch_mt_cfg<8, 3, MT>(args, s); break;
+    case 6: launch_mt_cfg<6, 3, MT>(args, s); break;
+    case 4: launch_mt_cfg<4, 2, MT>(args, s); break;
+    default: launch_mt_cfg<2, 2, MT>(args, s); break;
+    }
+}
+
+}  // namespace
+
+// C[M][N] for M = 2..4 NF4 tokens (fp32, the batch-1 rows kernel's shape
+// limits); ALJABR_ROCM_ERR_UNSUPPORTED for anything else.
+int enqueue_rows_nf4_mt(float *C, const float *A, const uint8_t *W, const float *absmax, int K, int N, int bs_shift,
+                        int M) {
+    if (M < 2 || M > 4 || !rows_shape_ok(A, K) || bs_shift < 5 || bs_shift > 11 || !aligned(W, 16))
+        return ALJABR_ROCM_ERR_UNSUPPORTED;
+    RowsArgs args{};
+    args.seg[0] = RowsSeg{W, absmax, C, N};
+    args.seg[1].end = args.seg[2].end = 0x7fffffff;
+    args.x = A;
+    args.N = N;
+    args.K = K;
+    args.bs_shift = bs_shift;
+    args.S = K / kChunk;
+    args.G = 8 / args.S;
+    const int T = pick_rows_t(N, args.S, 16);   // MT x T accumulators stay in registers
+    hipStream_t s = current_stream();
+    switch (M) {
+    case 2: launch_mt<2>(args, T, s); break;
+    case 3: launch_mt<3>(args, T, s); break;
+    default: launch_mt<4>(args, T, s); break;
+    }
+    return ALJABR_ROCM_OK;
+}
+
+namespace {
 }  // namespace
 
 int enqueue_rows(float *C, const float *A, const uint8_t *W, const float *absmax, int K, int N, int type,

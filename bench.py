@@ -112,9 +112,26 @@ def time_mlp(abi, torch, stream, mats, steps: int, warmup: int):
     return start.elapsed_time(end)   # ms
 
 
+def _cpu_rate(fn, nbytes: int, seconds: float):
+    """Repeat fn() for about `seconds`; returns (GB/s of algorithmic bytes, runs, seconds)."""
+    fn()                                          # warm
+    done, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        done += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return nbytes * done / dt / 1e9, done, dt
+
+
 def cpu_baseline(seconds: float):
-    """Oracle (C restatement of the reference CPU path) on a bounded sample:
-    repeated MLP steps (gate, up, down NF4 matvecs at batch 1) for ~`seconds`."""
+    """The oracle (C restatement of the reference CPU path, OpenMP row chunks =
+    2 x threads as GgufParallelConfig) on bounded samples: the NF4 MLP step
+    at all host cores for ~`seconds` (the reported value), then single-thread
+    and all-core rates of the NF4 matvec, the Q4_0 matvec (14336x4096) and
+    GQA decode attention (B=1 and 16, S=4096, fp16 K/V widened to fp32) for
+    ~2 s each. The reference's own Java Vector-API path cannot run here."""
     import numpy as np
     import oracle
     threads = oracle.threads()
@@ -123,36 +140,57 @@ def cpu_baseline(seconds: float):
         codes, absmax = oracle.nf4_quantize(oracle.normal(100 + i, n * k, 0.0, 0.02), BLOCK)
         mats.append((codes, absmax, n, k))
     xs = {K_MODEL: oracle.normal(7, K_MODEL), FFN: oracle.normal(8, FFN)}
-    oracle.nf4_matvec(*mats[0][:2], xs[K_MODEL], FFN, K_MODEL, BLOCK, threads)   # warm
-    done, t0 = 0, time.perf_counter()
-    while True:
+    step_bytes = sum(nf4_bytes(n, k) for _, _, n, k in mats)
+
+    def mlp():
         for codes, absmax, n, k in mats:
             oracle.nf4_matvec(codes, absmax, xs[k], n, k, BLOCK, threads)
-        done += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = time.perf_counter() - t0
-    step_bytes = sum(nf4_bytes(n, k) for _, _, n, k in mats)
-    return {"value": round(step_bytes * done / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+    gbs, done, dt = _cpu_rate(mlp, step_bytes, seconds)
+    extra = {}
+    c0, a0 = mats[0][0], mats[0][1]
+    for t in (1, threads):
+        r, _, _ = _cpu_rate(lambda: oracle.nf4_matvec(c0, a0, xs[K_MODEL], FFN, K_MODEL, BLOCK, t),
+                            nf4_bytes(FFN, K_MODEL), 2.0)
+        extra[f"nf4_14336x4096_m1_{t}t_GBs"] = round(r, 3)
+    q = oracle.quantize(oracle.QTYPE_Q4_0, oracle.normal(200, FFN * K_MODEL, 0.0, 0.02))
+    for t in (1, threads):
+        r, _, _ = _cpu_rate(lambda: oracle.q_matvec(oracle.QTYPE_Q4_0, q, xs[K_MODEL], FFN, K_MODEL, t),
+                            q.size + 4 * (FFN + K_MODEL), 2.0)
+        extra[f"q4_0_14336x4096_m1_{t}t_GBs"] = round(r, 3)
+    hq, hkv, d, s = 32, 8, 128, 4096
+    for b in (1, 16):
+        qv = oracle.normal(300 + b, b * hq * d).reshape(b, hq, 1, d)
+        kv = oracle.normal(310 + b, b * hkv * s * d).astype(np.float16).astype(np.float32).reshape(b, hkv, s, d)
+        vv = oracle.normal(320 + b, b * hkv * s * d).astype(np.float16).astype(np.float32).reshape(b, hkv, s, d)
+        nbytes = 2 * b * hkv * s * d * 2 + 2 * b * hq * d * 4      # fp16 K/V as the GPU reads them
+        for t in (1, threads):
+            r, _, _ = _cpu_rate(lambda: oracle.attention_gqa(qv, kv, vv, None, True, t), nbytes, 2.0)
+            extra[f"attention_b{b}_s{s}_{t}t_GBs"] = round(r, 3)
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"{done} MLP steps (3 NF4 matvecs each: 14336x4096, 14336x4096, 4096x14336, batch 1), "
-                      f"{dt:.1f} s, oracle C restatement, OpenMP row chunks = 2 x {threads} threads"}
+                      f"{dt:.1f} s, oracle C restatement, OpenMP row chunks = 2 x {threads} threads",
+            "per_kernel": extra,
+            "per_kernel_sample": "about 2 s per entry: 1 thread and all host threads; attention bytes count "
+                                 "K/V at fp16 (the GPU's format) though the oracle reads them widened"}
 
 
 def small_m_bench(abi, torch, stream, ms=(1, 4, 16, 64), launches=60):
     """NF4 small-M GEMM at the MLP shapes, M tokens per
-    launch (M >= 2 runs on the matrix cores). Weights rotate over >= 512 MB.
-    Returns per-shape, per-M launch time, algorithmic GB/s and TFLOP/s."""
+    launch (M <= 4 on the rows kernel in fp32, M >= 5 on the matrix cores),
+    and configs[0]'s 4096x4096 matvec at M = 1. Weights rotate over >= 512 MB.
+    Returns per-shape, per-M launch time, algorithmic GB/s, TFLOP/s and the
+    fraction of HBM peak."""
     lib = abi.load()
     out = {}
-    for n, k in ((FFN, K_MODEL), (K_MODEL, FFN)):
+    for n, k, mlist in ((K_MODEL, K_MODEL, (1,)), (FFN, K_MODEL, ms), (K_MODEL, FFN, ms)):
         per = n * k // 2 + n * k // BLOCK * 4
         copies = max(2, -(-520_000_000 // per))
         from aljabr_amd.llama import nf4_quantize_device
         g = torch.Generator(device="cuda:0").manual_seed(3)
         bufs = [nf4_quantize_device(torch.randn(n * k, generator=g, device="cuda:0").mul_(0.02), BLOCK)
                 for _ in range(copies)]
-        for m in ms:
+        for m in mlist:
             x = torch.randn(m * k, device="cuda:0")
             y = torch.empty(m * n, device="cuda:0")
             torch.cuda.synchronize()
@@ -174,6 +212,7 @@ def small_m_bench(abi, torch, stream, ms=(1, 4, 16, 64), launches=60):
             us = start.elapsed_time(end) * 1000.0 / launches
             alg = per + m * (k + n) * 4
             out[f"{n}x{k}_m{m}"] = {"us": round(us, 2), "GBs": round(alg / us / 1e3, 1),
+                                    "frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 3),
                                     "TFLOPs": round(2.0 * m * n * k / us / 1e6, 1)}
         del bufs
         torch.cuda.empty_cache()

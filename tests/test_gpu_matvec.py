@@ -266,3 +266,23 @@ def test_batched_passes_stay_in_bounds(rocm, dev, oracle, fmt, m):
     assert np.all(got[m * n:] == np.float32(-12345.5)), "rows past M were written"
     for i in range(m):
         assert rel_l2(got[i * n:(i + 1) * n], y_ref[i * n:(i + 1) * n]) <= TOL, i
+
+
+# NF4 with M = 2..4 tokens runs the batch-1 rows kernel with every lookup
+# feeding each token (fp32 throughout): every token row within 1e-5 of the
+# oracle, at the Llama MLP shapes, one K chunk, seven K chunks (one helper
+# wave) and a row count that does not fill the last workgroup.
+@pytest.mark.parametrize("n,k", [(14336, 4096), (4096, 14336), (300, 2048), (77, 10240)])
+@pytest.mark.parametrize("m", [2, 3, 4])
+def test_nf4_small_m_fp32_rows(rocm, dev, oracle, n, k, m):
+    codes, absmax = _nf4_case(oracle, n, k, seed=5)
+    x = oracle.normal(81 + m, m * k)
+    y_ref = np.asarray(oracle.nf4_matvec(codes, absmax, x, n, k, 64)).reshape(m, n)
+    c, a, xd = dev.put(codes), dev.put(absmax), dev.put(x)
+    y = dev.put(np.full((m + 1) * n, -7.5, np.float32))
+    rocm.call("aljabr_rocm_matvec_tb_batch_nf4", dev.ptr(y), dev.ptr(xd), dev.ptr(c), dev.ptr(a), k, n, 64, m)
+    got = dev.get(y)
+    assert np.all(got[m * n:] == np.float32(-7.5))
+    got = got[:m * n].reshape(m, n)
+    for i in range(m):
+        assert rel_l2(got[i], y_ref[i]) <= 1e-5, i
