@@ -119,15 +119,26 @@ int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const 
 // or Q6_K (absmax and bs_shift for NF4 only).
 int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
                        int bs_shift, int epilogue, const RowsRope *rope = nullptr);
-// NF4 small-M GEMM on MFMA (2 <= M <= 64, K % 512 == 0, block size 64). With
-// `accumulate` the products are added to C as it is (C += A . W^T), so a
-// caller that has C cleared or holding a residual saves the clearing launch.
+// NF4 small-M GEMM on MFMA (M >= 2 in passes of 32 tokens, K % 256 == 0,
+// block size 64), fp32-accurate and deterministic: C = A . W^T, or with
+// `add` C += A . W^T (a residual). When K is split over workgroups the
+// partial sums go to `part` (nf4_mfma_scratch_floats(min(M, 32), N, K)
+// floats) or, when that is null or too small, to the stream's scratch, and
+// a second kernel adds the slices in order.
 int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
-                     int M, bool accumulate = false);
+                     int M, bool add = false, float *part = nullptr, size_t part_floats = 0);
 // The same over up to three matrices of one K stacked in one launch (all but
 // the last with a multiple of 32 rows); outs[i].y is [M][outs[i].n].
-int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M,
-                           bool accumulate);
+int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M, bool add,
+                           float *part = nullptr, size_t part_floats = 0);
+size_t nf4_mfma_scratch_floats(int M, int N, int K);
+// The plan enqueue_nf4_mfma_multi uses for N stacked rows over K on `cus`
+// CUs (row tiles per wave, sub-slices per K slice), and one pass of at most
+// 32 tokens under an explicit plan (segments as enqueue_nf4_mfma_multi,
+// already validated).
+void nf4_mfma_plan(int N, int K, int cus, int &nt, int &q);
+int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, int M, bool add, float *part,
+                          size_t part_floats, int nt, int q);
 // fp16-weight small-M GEMM on MFMA (2 <= M <= 32, K in {512, 1024, 2048,
 // 4096}, W and A 16-byte aligned); deterministic (no atomics).
 int enqueue_f16_mfma(float *C, const float *A, const uint16_t *W, int K, int N, int M);

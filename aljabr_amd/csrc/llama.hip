@@ -71,6 +71,8 @@ struct aljabr_rocm_llama {
     float2 *rope_cs = nullptr;   // [max_seq][head_dim/2] RoPE cos/sin, filled at creation
     float *attn_scratch = nullptr;   // split-attention partials (owned: a captured graph keeps the address)
     size_t attn_scratch_bytes = 0;
+    float *mm_part = nullptr;        // K-slice partials of the batched NF4 GEMMs
+    size_t mm_part_floats = 0;
     bool rows_fused = false;   // batch-1 layers as fused NF4 launches (shapes and alignment allow it)
     // Captured decode steps, by batch size (and the logits buffer they write).
     struct Graph {
@@ -237,7 +239,16 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
     const size_t kvd = static_cast<size_t>(c.n_kv_heads) * c.head_dim;
     const size_t qd = static_cast<size_t>(c.n_heads) * c.head_dim;
     const size_t cache_elems = static_cast<size_t>(L) * B * kvd * c.max_seq;
+    // Partials of the batched NF4 GEMMs (passes of at most 32 tokens).
+    size_t mm_floats = 0;
+    if (c.max_batch >= 2) {
+        const int bp = c.max_batch < 32 ? c.max_batch : 32;
+        const int shapes[4][2] = {{static_cast<int>(qd + 2 * kvd), c.dim}, {c.dim, static_cast<int>(qd)},
+                                  {2 * c.ffn, c.dim}, {c.dim, c.ffn}};
+        for (const auto &sh : shapes) mm_floats = std::max(mm_floats, nf4_mfma_scratch_floats(bp, sh[0], sh[1]));
+    }
     const size_t bytes = 2 * ((cache_elems * 2 + 255) & ~size_t(255)) +
+                         ((mm_floats * 4 + 255) & ~size_t(255)) +
                          ((B * c.dim * 4 + 255) & ~size_t(255)) * 2 + ((B * qd * 4 + 255) & ~size_t(255)) * 2 +
                          ((B * kvd * 4 + 255) & ~size_t(255)) * 2 + ((B * c.ffn * 4 + 255) & ~size_t(255)) * 3 +
                          ((B * c.vocab * 4 + 255) & ~size_t(255)) + ((B * 4 + 255) & ~size_t(255)) * 4 +
@@ -269,6 +280,10 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
     m->next_out = carve<int>(cur, B);
     m->attn_scratch_bytes = attention_scratch_bytes(c.max_batch, c.n_heads, 1, c.head_dim, c.max_seq);
     m->attn_scratch = carve<float>(cur, m->attn_scratch_bytes / sizeof(float));
+    if (c.max_batch >= 2) {
+        m->mm_part_floats = mm_floats;
+        m->mm_part = carve<float>(cur, mm_floats);
+    }
     // The RoPE angles of every cache position, computed once: the decode
     // step then reads cos/sin instead of evaluating double pow/cos/sin.
     m->rope_cs = carve<float2>(cur, static_cast<size_t>(c.max_seq) * (c.head_dim / 2));
@@ -827,8 +842,9 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
     // cleared, or which holds the residual); otherwise y is written, or the
     // products go to `tmp` and one add follows.
     auto mm = [&](float *y, const float *x, const T &t, int K, int N, bool residual, float *tmp) -> int {
-        if (t.type == ALJABR_ROCM_TYPE_NF4 && B >= 2 && B <= 64 && shift >= 0 && m->all_nf4) {
-            const int r = enqueue_nf4_mfma(y, x, t.w, t.s, K, N, shift, B, true);
+        if (t.type == ALJABR_ROCM_TYPE_NF4 && B >= 2 && shift >= 0 && m->all_nf4) {
+            const int r = enqueue_nf4_mfma(y, x, t.w, t.s, K, N, shift, B, residual, m->mm_part,
+                                           m->mm_part_floats);
             if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
         }
         if (kquant_mfma_type(t.type) && B >= 2 && B <= kquant_mfma_max_m(t.type)) {
@@ -922,17 +938,21 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                      weight_bytes(tq, qd, dim, bs) + weight_bytes(tk, kvd, dim, bs) + weight_bytes(tv, kvd, dim, bs) +
                          (2.0 * dim + qd) * f4 + 2.0 * kvd * 2.0);
         } else {
+            // The NF4 matrix-core GEMMs write their outputs; the K-quant ones
+            // add into them, so for those the RMSNorm launch clears them.
             const ZeroList z{{m->q, m->k, m->v},
                              {static_cast<long long>(B) * qd, static_cast<long long>(B) * kvd,
                               static_cast<long long>(B) * kvd}};
-            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, attn_norm, B, dim, c.eps, &z));
-            ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * (qd + 2.0 * kvd)) * f4);
+            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, attn_norm, B, dim, c.eps, m->all_nf4 ? nullptr : &z));
+            if (m->all_nf4) ALJ_MARK("rmsnorm", (B * 2.0 * dim + dim) * f4);
+            else ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * (qd + 2.0 * kvd)) * f4);
             // Q, K and V in one matrix-core launch where the shapes allow.
             const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq), qd},
                                     {m->k, W(m->wk), S(m->wk), kvd},
                                     {m->v, W(m->wv), S(m->wv), kvd}};
-            rc = m->all_nf4 && B >= 2 && B <= 64 ? enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, true)
-                                                 : ALJABR_ROCM_ERR_UNSUPPORTED;
+            rc = m->all_nf4 && B >= 2 ? enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, false, m->mm_part,
+                                                               m->mm_part_floats)
+                                      : ALJABR_ROCM_ERR_UNSUPPORTED;
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
                 float *const ys[3] = {m->q, m->k, m->v};
                 const T *const ts[3] = {&m->wq[l], &m->wk[l], &m->wv[l]};
@@ -1008,12 +1028,14 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         } else {
             const ZeroList z{{m->gate, m->up, nullptr},
                              {static_cast<long long>(B) * ffn, static_cast<long long>(B) * ffn, 0}};
-            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, ffn_norm, B, dim, c.eps, &z));
-            ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * 2.0 * ffn) * f4);
+            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, ffn_norm, B, dim, c.eps, m->all_nf4 ? nullptr : &z));
+            if (m->all_nf4) ALJ_MARK("rmsnorm", (B * 2.0 * dim + dim) * f4);
+            else ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * 2.0 * ffn) * f4);
             const RowsOut gu[2] = {{m->gate, W(m->w_gate), S(m->w_gate), ffn},
                                    {m->up, W(m->w_up), S(m->w_up), ffn}};
-            rc = m->all_nf4 && B >= 2 && B <= 64 ? enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, true)
-                                                 : ALJABR_ROCM_ERR_UNSUPPORTED;
+            rc = m->all_nf4 && B >= 2 ? enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, false, m->mm_part,
+                                                               m->mm_part_floats)
+                                      : ALJABR_ROCM_ERR_UNSUPPORTED;
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
                 float *const ys[2] = {m->gate, m->up};
                 const T *const ts[2] = {&m->w_gate[l], &m->w_up[l]};

@@ -1,33 +1,36 @@
-// matmul_mfma.hip - NF4 small-M GEMM on the matrix cores:
-// Y[M,N] = X[M,K] . W[N,K]^T for 2 <= M <= 64 (a prompt chunk or a decode
-// batch), W in NF4 (STC/DequantizationKernel.java:84-102). Replaces the
-// reference's per-token loop over the matvec (MTLJ/MetalComputeBackend.java:
-// 435-470): W is read from HBM once for all M tokens.
+// matmul_mfma.hip - NF4 small-M GEMM on the matrix cores, fp32-accurate and
+// deterministic: Y[M,N] = X[M,K] . W[N,K]^T (or Y += ...) for 2 <= M <= 32
+// tokens per pass (a prompt chunk or a decode batch), W in NF4
+// (STC/DequantizationKernel.java:84-102). Replaces the reference's per-token
+// loop over the matvec (MTLJ/MetalComputeBackend.java:435-470): W is read
+// from HBM once for all tokens of a pass.
 //
-// MFMA v_mfma_f32_32x32x16_f16 with A = X (32 token rows per m-tile) and
-// B = W^T (32 weight rows per wave as the 32 output columns), fp32
-// accumulation. Both operands are fp16: NF4 levels rounded to fp16 (relative
-// error <= 2^-11) and activations rounded to fp16; the per-block absmax stays
-// fp32 and is applied to the fp32 accumulators once per 64-element block
-// (C += s * C_block), so no product is rounded through fp16 twice.
+// Precision. MFMA v_mfma_f32_32x32x16_f16 with A = X (32 token rows) and
+// B = W^T (32 weight rows per wave as the output columns), fp32 accumulation.
+// Neither operand is rounded: activations are split x = xh + xl (xh =
+// fp16(x), xl = fp16(x - xh)) and NF4 levels L = H + R (H = fp16(L),
+// R = fp16(L - H)), and each product is xh.H + xl.H + xh.R; the dropped
+// xl.R term and the fp16 rounding of R are below 2^-22 of the product. The
+// per-64-element absmax multiplies the fp32 accumulators once per block.
 //
-// Decode: a code byte (two weights) indexes a 256-entry table of packed fp16
-// level pairs in LDS, which is exactly one B-operand register. The table is
-// replicated 64 times, entry e of replica r at byte e*256 + r*4, so lane l
-// reads replica l and a wave never conflicts; the address is one v_perm_b32.
+// Decode. A code byte (two weights) indexes a 256-entry LDS table holding
+// the byte's H pair and R pair (the hi and lo B registers), replicated 32
+// times: the H pair of replica r at byte e*256 + 4r, the R pair at
+// e*256 + 128 + 4r, so the 32 lanes of a half-wave read 32 distinct banks.
+// The address is one v_perm_b32 of the code dword and the lane's offset.
 //
-// Operand layout (32x32x16): lane l supplies A[m = l%32][8*(l/32) + e] and
-// B[8*(l/32) + e][n = l%32], e = 0..7; accumulator r of lane l is
-// C[8*(r/4) + 4*(l/32) + r%4][l%32]. The contraction index k' is mapped to
-// the real K so that one MFMA step covers 16 elements of one 64-element
-// block, and each lane reads 16 contiguous code bytes per block: for block
-// b of a 256-element iteration and step j (0..3) of the block, lane half h
-// supplies k = 64b + 32h + 8j + e.
+// Work split. A workgroup is 8 waves; wave w owns 32 rows of the
+// workgroup's 256-row group and runs a slice of consecutive 256-element K
+// sub-slices. Weight codes are loaded coalesced (8 lanes per 128-byte row
+// segment), four sub-slices ahead in registers, and turned into the MFMA B
+// layout through a per-wave LDS stage; each sub-slice's activations (hi and
+// lo) are staged once per workgroup in LDS.
 //
-// Work split: a workgroup is 8 waves x 32 rows = 256 rows of W and one
-// K-slice of KS elements; slices add their partial sums into Y with
-// hardware float atomics (Y is zeroed first), so results are exact up to
-// fp32 summation order, which varies between runs.
+// Determinism. With several K slices, each workgroup stores its partial
+// tile and a second kernel sums the slices in slice order into Y (or adds
+// them to it): no float atomics, the same result on every run.
+#include <type_traits>
+
 #include "device.hpp"
 #include "internal.hpp"
 #include "kernels.hpp"
@@ -38,12 +41,28 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
 
 constexpr int kMmWaves = 8;
 constexpr int kMmThreads = kMmWaves * 64;
-constexpr int kMmRowsPerWg = kMmWaves * 32;
-constexpr int kTableBytes = 256 * 64 * 4;       // 256 entries x 64 replicas x fp16 pair
+constexpr int kGroupRows = kMmWaves * 32;        // rows of a workgroup
+constexpr int kSub = 256;                        // K sub-slice (elements) staged at a time
+constexpr int kRS = kSub + 8;                    // activation row stride in halves (16-byte pad)
+
+// LDS layout (bytes; dynamic LDS starts at address 0, the kernel has no
+// static LDS): the decode table, the activation tile (hi rows, then lo
+// rows), per-wave code staging (32 rows x 144 bytes) and per-wave scale
+// staging (32 rows x 4 floats).
+constexpr uint32_t kTableBytes = 256 * 256;
+constexpr uint32_t kXOff = kTableBytes;
+constexpr uint32_t kXLo = 32 * kRS * 2;          // lo rows after the hi rows
+constexpr uint32_t kCOff = kXOff + 2 * kXLo;
+constexpr uint32_t kCRow = 144;
+constexpr uint32_t kSOff = kCOff + kMmWaves * 32 * kCRow;
+constexpr uint32_t kLdsBytes = kSOff + kMmWaves * 32 * 16;
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget of a CU");
 
 // Up to three weight matrices of the same K stacked as one row space (the
 // decode step's Q/K/V or gate/up in one launch): segment s owns stacked rows
@@ -56,11 +75,12 @@ struct MmArgs {
     const float *absmax[3];
     int end[3];
     int nseg;
-    int M, N, K, bs_shift;   // N: stacked rows
+    int M, N, K;           // N: stacked rows
+    int add;               // Y += instead of Y = (one slice)
+    int q;                 // sub-slices per slice (the last slice may hold fewer)
+    float *part;           // [slice][M][N] partial sums when gridDim.x > 1
 };
 
-// The segment of a tile starting at stacked row r0 (past the end: the last
-// segment, with local rows past its end).
 struct TileRef {
     const uint8_t *w;
     const float *absmax;
@@ -68,16 +88,32 @@ struct TileRef {
     int local0, n;
 };
 
+__device__ __forceinline__ int segment_of(const int (&end)[3], int nseg, int r) {
+    const int s = (r >= end[0]) + (r >= end[1]);
+    return s > nseg - 1 ? nseg - 1 : s;
+}
+
+// An argument value pinned in scalar registers: selecting between pinned
+// values stays a select (folded into one load at a computed address, the
+// argument block would be copied to scratch memory).
+template <typename T>
+__device__ __forceinline__ T pin(T v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
+// The segment of stacked row r0 (uniform across the wave).
 __device__ __forceinline__ TileRef tile_ref(const MmArgs &a, int r0) {
-    int s = (r0 >= a.end[0]) + (r0 >= a.end[1]);
+    const int e0 = pin(a.end[0]), e1 = pin(a.end[1]), e2 = pin(a.end[2]);
+    int s = (r0 >= e0) + (r0 >= e1);
     if (s > a.nseg - 1) s = a.nseg - 1;
-    const int start = s == 0 ? 0 : s == 1 ? a.end[0] : a.end[1];
+    const int start = s == 0 ? 0 : s == 1 ? e0 : e1;
     TileRef t;
-    t.w = s == 0 ? a.w[0] : s == 1 ? a.w[1] : a.w[2];
-    t.absmax = s == 0 ? a.absmax[0] : s == 1 ? a.absmax[1] : a.absmax[2];
-    t.y = s == 0 ? a.y[0] : s == 1 ? a.y[1] : a.y[2];
+    t.w = s == 0 ? pin(a.w[0]) : s == 1 ? pin(a.w[1]) : pin(a.w[2]);
+    t.absmax = s == 0 ? pin(a.absmax[0]) : s == 1 ? pin(a.absmax[1]) : pin(a.absmax[2]);
+    t.y = s == 0 ? pin(a.y[0]) : s == 1 ? pin(a.y[1]) : pin(a.y[2]);
     t.local0 = r0 - start;
-    t.n = (s == 0 ? a.end[0] : s == 1 ? a.end[1] : a.end[2]) - start;
+    t.n = (s == 0 ? e0 : s == 1 ? e1 : e2) - start;
     return t;
 }
 
@@ -87,279 +123,500 @@ __device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
 }
 
-// B fragment (8 fp16 weights) for code dword `w`: byte t holds elements
-// 2t (high nibble) and 2t+1 (low nibble). Table entry e of replica r is at
-// byte e*256 + r*4: v_perm puts the code byte in bits 8-15 and r*4 (cl) in
-// bits 0-7.
-__device__ __forceinline__ uint32_t pair16_at(const char *tbl, uint32_t addr) {
-    return *reinterpret_cast<const uint32_t *>(tbl + addr);
-}
-__device__ __forceinline__ half8 decode8(uint32_t w, uint32_t cl, const char *tbl) {
-    u32x4v r;
-    r.x = pair16_at(tbl, __builtin_amdgcn_perm(w, cl, 0x0C0C0400u));
-    r.y = pair16_at(tbl, __builtin_amdgcn_perm(w, cl, 0x0C0C0500u));
-    r.z = pair16_at(tbl, __builtin_amdgcn_perm(w, cl, 0x0C0C0600u));
-    r.w = pair16_at(tbl, __builtin_amdgcn_perm(w, cl, 0x0C0C0700u));
-    return __builtin_bit_cast(half8, r);
+// fp16 residual of a level: L - fp16(L), rounded to fp16.
+__device__ __forceinline__ float level_rest(float l) {
+    return l - static_cast<float>(static_cast<_Float16>(l));
 }
 
-// Pair table: dword slot i = e*64 + r. Thread tid (of 512) fills slots
-// tid + 512k (k < 32): e = tid/64 + 8k, so its low nibble is tid/64 + 8*(k
-// odd) and its high nibble k/2.
-__device__ __forceinline__ void build_pair16_table(uint32_t *tbl_s, int tid) {
-    const float lo_a = nf4_level_sel(tid >> 6), lo_b = nf4_level_sel((tid >> 6) + 8);
+typedef uint32_t __attribute__((address_space(3))) lds_u32;
+typedef u32x2v __attribute__((address_space(3))) lds_u32x2;
+typedef u32x4v __attribute__((address_space(3))) lds_u32x4;
+typedef f32x2 __attribute__((address_space(3))) lds_f32x2;
+typedef f32x4 __attribute__((address_space(3))) lds_f32x4;
+typedef half8 __attribute__((address_space(3))) lds_half8;
+
+template <typename T>
+__device__ __forceinline__ T *lds(uint32_t addr) {
+    return reinterpret_cast<T *>(static_cast<uintptr_t>(addr));
+}
+
+// Global-memory loads through explicitly global pointers (a pointer that
+// went through a pinned register would otherwise load as FLAT, whose
+// counters force full waits).
+template <typename T>
+__device__ __forceinline__ T gload(const void *p) {
+    typedef const T __attribute__((address_space(1))) gT;
+    return *(gT *)(p);
+}
+template <typename T>
+__device__ __forceinline__ T gload_stream(const void *p) {
+    typedef const T __attribute__((address_space(1))) gT;
+    return __builtin_nontemporal_load((gT *)(p));
+}
+
+// Table entry e (code byte: even element in the high nibble), replica r:
+// {H(e>>4), H(e&15)} at e*256 + 4r and {R(e>>4), R(e&15)} 128 bytes on.
+// Thread tid (of 512) fills replica tid%32 of entries tid/32 + 16k, k < 16:
+// their low nibble is tid/32 and their high nibble k.
+__device__ __forceinline__ void build_table(int tid) {
     constexpr float kNF4[16] = {
         -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
         -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
         0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
         0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+    const float lo = nf4_level_sel((tid >> 5) & 15);
+    const uint32_t base = static_cast<uint32_t>(tid >> 5) * 256 + (tid & 31) * 4;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) tbl_s[tid + kMmThreads * k] = pack_half2(kNF4[k >> 1], (k & 1) ? lo_b : lo_a);
+    for (int k = 0; k < 16; ++k) {
+        const float hi = kNF4[k];
+        *lds<lds_u32>(base + k * 16 * 256) = pack_half2(hi, lo);
+        *lds<lds_u32>(base + k * 16 * 256 + 128) = pack_half2(level_rest(hi), level_rest(lo));
+    }
 }
 
-// Loads of one work unit, coalesced (8 lanes read a whole 128-byte row
-// segment; the MFMA layout would touch 32 lines per instruction and stall
-// the texture path): instruction i covers rows 8i + lane/8 of the wave's
-// 32-row tile, bytes 16*(lane%8) of iteration it's segment. The first unit
-// of a tile also loads its SB scales: lane covers row lane/2, half lane%2.
-template <int ITERS, int SB>
-__device__ __forceinline__ void issue_unit(u32x4 (&q)[4], float (&sc)[SB / 2], const MmArgs &a, const TileRef &tr,
-                                           int it, int ks0, int lane) {
-    if (it == 0) {
-        const int srow = min(tr.local0 + (lane >> 1), tr.n - 1);
-        const float *sp = tr.absmax + ((static_cast<size_t>(srow) * a.K + ks0) >> 6) + (SB / 2) * (lane & 1);
-        if constexpr (SB / 2 == 4) {
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(sp);
-            sc[0] = v.x; sc[1] = v.y; sc[2] = v.z; sc[3] = v.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < SB / 2; ++j) sc[j] = sp[j];
-        }
-    }
-    const size_t row_bytes = static_cast<size_t>(a.K) >> 1;
+// B fragments (8 weights, hi and residual) of code dword `w`: byte t holds
+// elements 2t (high nibble) and 2t+1 (low nibble). `ch` is the lane's H
+// offset within an entry (4*(lane%32)); the R pair sits 128 bytes on and is
+// read as a relaxed atomic, which keeps the two reads separate (merged into
+// one paired read they would land in adjacent registers and need moves),
+// so one v_perm address serves both and every read lands in its fragment
+// register.
+__device__ __forceinline__ void decode8(uint32_t w, uint32_t ch, half8 &bh, half8 &br) {
+    const uint32_t a0 = __builtin_amdgcn_perm(w, ch, 0x0C0C0400u);
+    const uint32_t a1 = __builtin_amdgcn_perm(w, ch, 0x0C0C0500u);
+    const uint32_t a2 = __builtin_amdgcn_perm(w, ch, 0x0C0C0600u);
+    const uint32_t a3 = __builtin_amdgcn_perm(w, ch, 0x0C0C0700u);
+    u32x4v h, r;
+    h.x = *lds<lds_u32>(a0);
+    h.y = *lds<lds_u32>(a1);
+    h.z = *lds<lds_u32>(a2);
+    h.w = *lds<lds_u32>(a3);
+    r.x = __hip_atomic_load(lds<lds_u32>(a0 + 128), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    r.y = __hip_atomic_load(lds<lds_u32>(a1 + 128), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    r.z = __hip_atomic_load(lds<lds_u32>(a2 + 128), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    r.w = __hip_atomic_load(lds<lds_u32>(a3 + 128), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    bh = __builtin_bit_cast(half8, h);
+    br = __builtin_bit_cast(half8, r);
+}
+
+// One work unit: a wave's 32 weight rows x one 256-element sub-slice (128
+// code bytes and 4 scales per row), loaded coalesced: load i covers rows
+// 8i + lane/8, bytes 16*(lane%8) of the row's segment; the scale pair of a
+// lane is row lane/2, scales 2*(lane%2) and +1.
+struct Unit {
+    u32x4 q[4];
+    f32x2 s;
+};
+
+// A lane's load addresses for a tile at K offset 0: the four code rows it
+// loads (rows 8i + lane/8, bytes 16*(lane%8)) and its scale pair (row
+// lane/2, scales 2*(lane%2)); a unit at K offset k0 adds k0/2 bytes to the
+// codes and k0/64 floats to the scales.
+struct UnitBase {
+    const uint8_t *q[4];
+    const float *s;
+};
+
+__device__ __forceinline__ UnitBase unit_base(const TileRef &tr, int K, int lane) {
+    const size_t row_bytes = static_cast<size_t>(K) >> 1;
+    UnitBase b;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int row = min(tr.local0 + 8 * i + (lane >> 3), tr.n - 1);
-        q[i] = *reinterpret_cast<const u32x4 *>(tr.w + row * row_bytes + (ks0 >> 1) + 128 * it + 16 * (lane & 7));
+        b.q[i] = tr.w + static_cast<size_t>(row) * row_bytes + 16 * (lane & 7);
     }
+    const int srow = min(tr.local0 + (lane >> 1), tr.n - 1);
+    b.s = tr.absmax + static_cast<size_t>(srow) * (K >> 6) + 2 * (lane & 1);
+    return b;
+}
+
+// All-ones when `real`, else zero, through an opaque register so the
+// compiler keeps one load instruction with a masked address (a branch per
+// case would break the exact wait counts).
+__device__ __forceinline__ uintptr_t real_mask(bool real) {
+    uint32_t r = real ? 1u : 0u;
+    asm volatile("" : "+v"(r));
+    return static_cast<uintptr_t>(0) - static_cast<uintptr_t>(r);
+}
+
+// Loads of the unit at K offset k0 (uniform); a dummy unit (past the
+// slice's end) loads the base of `dummy` in every lane instead: one line.
+__device__ __forceinline__ void issue_unit(Unit &u, const UnitBase &b, int k0, bool real, const void *dummy) {
+    const uintptr_t mask = real_mask(real), d = reinterpret_cast<uintptr_t>(dummy);
+    const auto pick = [&](const void *p) {
+        return reinterpret_cast<const void *>((reinterpret_cast<uintptr_t>(p) & mask) | (d & ~mask));
+    };
+    u.s = gload<f32x2>(pick(b.s + (k0 >> 6)));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u.q[i] = gload_stream<u32x4>(pick(b.q[i] + (k0 >> 1)));
     __builtin_amdgcn_sched_barrier(0);           // keep units in issue order
 }
 
-template <int MT, int KS>
-constexpr size_t mm_lds_bytes() {
-    // x slice (fp16, padded rows) + per-wave code staging (32 rows x 144 B)
-    // + per-wave scale staging (32 rows x KS/64 floats).
-    return static_cast<size_t>(32 * MT) * (KS + 8) * 2 + kMmWaves * 32 * 144 + kMmWaves * 32 * (KS / 64) * 4;
+// Activations as four float4 chunks per thread, coalesced: chunk c =
+// tid + 512j is token row c/64 = tid/64 + 8j, elements 4*(tid%64) .. +4 of
+// the sub-slice. Rows >= M load row 0: they only feed output rows >= M,
+// which are never stored.
+struct XBase {
+    const float *p[4];
+};
+
+__device__ __forceinline__ XBase x_base(const float *x, int M, int K, int tid) {
+    XBase b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = (tid >> 6) + 8 * j;
+        b.p[j] = x + static_cast<size_t>(m < M ? m : 0) * K + 4 * (tid & 63);
+    }
+    return b;
 }
 
-template <int MT, int KS, int NT>
+__device__ __forceinline__ void load_x(f32x4 (&xr)[4], const XBase &b, int k0, bool real, const float *dummy) {
+    const uintptr_t mask = real_mask(real), d = reinterpret_cast<uintptr_t>(dummy);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        xr[j] = gload<f32x4>(reinterpret_cast<const void *>((reinterpret_cast<uintptr_t>(b.p[j] + k0) & mask) |
+                                                            (d & ~mask)));
+    // Issued where written: sunk below the MFMA work, these loads would
+    // share registers with it and stall it on their return.
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Stage the activations as hi and lo halves (consecutive lanes write
+// consecutive 8-byte pieces of a row): hi = fp16(x) and lo = fp16(x - hi),
+// both rounded toward zero (packed conversions); x - hi is exact in fp32
+// and lo keeps its leading 11 bits, below 2^-22 of x.
+__device__ __forceinline__ void stage_x(const f32x4 (&xr)[4], int tid) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = (tid >> 6) + 8 * j;
+        const f32x4 v = xr[j];
+        typedef __fp16 half2v __attribute__((ext_vector_type(2)));
+        const half2v h01 = __builtin_amdgcn_cvt_pkrtz(v.x, v.y);
+        const half2v h23 = __builtin_amdgcn_cvt_pkrtz(v.z, v.w);
+        const half2v l01 = __builtin_amdgcn_cvt_pkrtz(v.x - static_cast<float>(h01.x), v.y - static_cast<float>(h01.y));
+        const half2v l23 = __builtin_amdgcn_cvt_pkrtz(v.z - static_cast<float>(h23.x), v.w - static_cast<float>(h23.y));
+        const uint32_t addr = kXOff + (m * kRS + 4 * (tid & 63)) * 2;
+        *lds<lds_u32x2>(addr) = u32x2v{__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)};
+        *lds<lds_u32x2>(addr + kXLo) = u32x2v{__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
+    }
+}
+
+// A unit's codes and scales in the MFMA B layout, through the wave's
+// staging rows: lane (nl, h) = (lane%32, lane/32) takes bytes 32b + 16h of
+// row nl for block b (elements 64b + 32h .. +32) and row nl's four scales.
+// The staging rows are the wave's own and its LDS operations run in order,
+// so no barrier is needed (and a second unit may reuse them at once).
+__device__ __forceinline__ void to_mfma_layout(const Unit &u, u32x4v (&qm)[4], f32x4 &sc, uint32_t cst, uint32_t sst,
+                                               int lane) {
+    const int nl = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *lds<lds_u32x4>(cst + (8 * i + (lane >> 3)) * kCRow + 16 * (lane & 7)) = u.q[i];
+    *lds<lds_f32x2>(sst + (lane >> 1) * 16 + 8 * (lane & 1)) = u.s;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) qm[b] = *lds<lds_u32x4>(cst + nl * kCRow + 32 * b + 16 * h);
+    sc = *lds<lds_f32x4>(sst + nl * 16);
+}
+
+// acc[t] += blockwise-scaled product of unit t (NT units: the wave's row
+// tiles, one sub-slice) with the staged activations. Each A fragment is
+// read once for all NT tiles; the tiles' MFMA chains interleave. `arow` is
+// the LDS address of the lane's A row plus its half.
+template <int NT>
+__device__ __forceinline__ void compute_units(f32x16 (&acc)[NT], const Unit *u, uint32_t arow, uint32_t cst,
+                                              uint32_t sst, int lane, uint32_t ch) {
+    u32x4v qm[NT][4];
+    f32x4 sc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) to_mfma_layout(u[t], qm[t], sc[t], cst, sst, lane);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        f32x16 cb[NT];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t e = arow + (64 * b + 8 * j) * 2;
+            const half8 ah = *lds<lds_half8>(e);
+            const half8 al = *lds<lds_half8>(e + kXLo);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const uint32_t w = j == 0 ? qm[t][b].x : j == 1 ? qm[t][b].y : j == 2 ? qm[t][b].z : qm[t][b].w;
+                half8 bh, br;
+                decode8(w, ch, bh, br);
+                cb[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, j == 0 ? f32x16{} : cb[t], 0, 0, 0);
+                cb[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, cb[t], 0, 0, 0);
+                cb[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, br, cb[t], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float sblk = b == 0 ? sc[t].x : b == 1 ? sc[t].y : b == 2 ? sc[t].z : sc[t].w;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[t][r] = fmaf(sblk, cb[t][r], acc[t][r]);
+        }
+        // One block at a time: otherwise the scheduler hoists every block's
+        // table reads and runs out of registers.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Wave w owns row tiles t < NT of the workgroup's row group (256*NT rows):
+// rows group0 + 256t + 32w. A unit is (sub-slice i, tile t); ring slot
+// (i*NT + t) % R holds it.
+template <int NT>
 __global__ __launch_bounds__(kMmThreads) void nf4_mm_kernel(MmArgs a) {
-    constexpr int ITERS = KS / 256;
-    constexpr int SB = KS / 64;                  // 64-element blocks (absmax scales) per row and slice
-    constexpr int RS = KS + 8;                   // x row stride in halves (16-byte pad: conflict-free reads)
-    extern __shared__ uint8_t smem[];
-    __shared__ uint32_t tbl_s[kTableBytes / 4];  // static: its LDS address is a known constant
-    const char *tbl = reinterpret_cast<const char *>(tbl_s);
-    _Float16 *xs = reinterpret_cast<_Float16 *>(smem);
+    // Ring of weight units in registers: four sub-slices ahead with one
+    // tile, one sub-slice (two units) ahead with two (the register budget).
+    constexpr int R = NT == 1 ? 4 : 2;
+    constexpr int SP = R / NT;                   // sub-slices per ring pass
+    static_assert(NT == 1 || NT == 2, "one or two row tiles per wave");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: segment choice in scalar registers
     const int h = lane >> 5;
-    const int nl = lane & 31;                    // this lane's output column (weight row) in a tile
-    uint8_t *cstage = smem + static_cast<size_t>(32 * MT) * RS * 2 + wave * (32 * 144);
-    float *sstage = reinterpret_cast<float *>(smem + static_cast<size_t>(32 * MT) * RS * 2 + kMmWaves * 32 * 144) +
-                    wave * (32 * SB);
-    const int ks0 = blockIdx.y * KS;
-
-    // Activation slice.
-    constexpr int XF4 = 32 * MT * (KS / 4) / kMmThreads;
-    static_assert(32 * MT * (KS / 4) % kMmThreads == 0, "x slice split");
-    f32x4 xv[XF4];
-#pragma unroll
-    for (int j = 0; j < XF4; ++j) {
-        const int i = tid + kMmThreads * j;
-        const int m = min(i / (KS / 4), a.M - 1), c = i % (KS / 4);
-        xv[j] = *reinterpret_cast<const f32x4 *>(a.x + static_cast<size_t>(m) * a.K + ks0 + 4 * c);
-    }
-
-    // x slice -> fp16 rows [32*MT][KS] (rows >= M are zero). Staged before
-    // the weight loads go out: behind 30 MB of weight requests the activation
-    // loads would wait several microseconds.
-#pragma unroll
-    for (int j = 0; j < XF4; ++j) {
-        const int i = tid + kMmThreads * j;
-        const int m = i / (KS / 4), c = i % (KS / 4);
-        f32x4 v = xv[j];
-        if (m >= a.M) v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        *reinterpret_cast<uint2 *>(xs + m * RS + 4 * c) = make_uint2(pack_half2(v.x, v.y), pack_half2(v.z, v.w));
-    }
-    __builtin_amdgcn_sched_barrier(0);           // the weight loads must not move above this
-
-    // Weights, all issued up front and coalesced (whole 128-byte row segments per
-    // 8 lanes; the MFMA layout would touch 32 lines per instruction and stall
-    // the texture path): codes of iteration it, instruction i: row
-    // 8i + lane/8 of the wave's tile, bytes 16*(lane%8) of the segment; the
-    // row's SB scales: lane covers row lane/2, half lane%2.
-    // Work units u = (tile t = u / ITERS, iteration it = u % ITERS); loads run
-    // W units ahead of the unit being computed, so the memory queue holds a
-    // few units per wave instead of the whole slice (issuing everything at
-    // once stalls the wave at issue until most of it has arrived).
-    constexpr int U = NT * ITERS;
-    constexpr int W = 2;
+    const int nl = lane & 31;                    // this lane's token row (A) and weight row (B) in a tile
+    const int slice = blockIdx.x;
+    const int sub0 = slice * a.q;
+    const int nsub = min(a.q, (a.K / kSub) - sub0);   // sub-slices of this slice (>= 1)
+    const int kw0 = sub0 * kSub;                 // this workgroup's first K element
+    const int group0 = blockIdx.y * (kGroupRows * NT);
     TileRef tr[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) tr[t] = tile_ref(a, blockIdx.x * (kMmRowsPerWg * NT) + t * kMmRowsPerWg + wave * 32);
-    u32x4 qc[U][4];
-    float sc[NT][SB / 2];
-#pragma unroll
-    for (int u = 0; u < W && u < U; ++u) issue_unit<ITERS, SB>(qc[u], sc[u / ITERS], a, tr[u / ITERS], u % ITERS, ks0, lane);
+    for (int t = 0; t < NT; ++t) tr[t] = tile_ref(a, group0 + t * kGroupRows + wave * 32);
+    const float *const x = a.x;
+    const int M = a.M, K = a.K;
 
-    build_pair16_table(tbl_s, tid);
-    __syncthreads();
+    // Activations one sub-slice ahead, weight units a ring pass ahead. Issue
+    // order per sub-slice: activations, then its weight units; the prologue
+    // issues in the same order so the loop's wait counts hold from its first
+    // pass.
+    // Loads past the slice's end (a ring refill beyond its last sub-slice)
+    // are dummies of one line each, so every pass issues the same sequence
+    // and the compiler's wait counts stay exact.
+    const XBase xb = x_base(x, M, K, tid);
+    UnitBase ub[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) ub[t] = unit_base(tr[t], K, lane);
+    f32x4 xr[4];
+    Unit ring[R];
+    load_x(xr, xb, kw0, true, x);
+#pragma unroll
+    for (int r = 0; r < R; ++r) issue_unit(ring[r], ub[r % NT], kw0 + (r / NT) * kSub, r / NT < nsub, tr[r % NT].w);
+    build_table(tid);
 
-    const uint32_t cl = lane * 4;
-    f32x16 acc[MT];
+    const uint32_t ch = nl * 4;
+    uint32_t arow = kXOff + (nl * kRS + 32 * h) * 2;
+    asm volatile("" : "+v"(arow));               // one base register: element offsets stay immediates
+    const uint32_t cst = kCOff + wave * 32 * kCRow, sst = kSOff + wave * 32 * 16;
+    f32x16 acc[NT];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        if (u + W < U)
-            issue_unit<ITERS, SB>(qc[u + W], sc[(u + W) / ITERS], a, tr[(u + W) / ITERS], (u + W) % ITERS, ks0,
-                                      lane);
-        const int t = u / ITERS, it = u % ITERS;
-        if (it == 0) {
-            // Scales of this tile to the MFMA layout: row nl, all SB blocks.
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int j = 0; j < SB / 2; ++j) sstage[(lane >> 1) * SB + (SB / 2) * (lane & 1) + j] = sc[t][j];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[mt][r] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+
+    // Sub-slice i = p0 + PS: stage its activations between two barriers,
+    // fetch i+1's, compute its NT units (ring slots PS*NT ..) and refill
+    // those slots with the units of sub-slice i + SP. Past the slice's end
+    // the loads are dummies and nothing is computed.
+    auto step = [&](int p0, auto ps) {
+        constexpr int PS = decltype(ps)::value;
+        const int i = p0 + PS;
+        if (i < nsub) {
+            __syncthreads();                     // every wave is done with sub-slice i-1's activations
+            stage_x(xr, tid);
+            __syncthreads();                     // sub-slice i's activations (and the table) visible
         }
-        // Codes to the MFMA layout through the wave's staging rows (144-byte
-        // stride: conflict-free both ways): lane (nl, h) takes bytes
-        // 32b + 16h of row nl for block b.
+        load_x(xr, xb, kw0 + (i + 1) * kSub, i + 1 < nsub, x);
+        if (i < nsub) compute_units<NT>(acc, ring + PS * NT, arow, cst, sst, lane, ch);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<u32x4 *>(cstage + (8 * i + (lane >> 3)) * 144 + 16 * (lane & 7)) = qc[u][i];
-        u32x4 qm[4];
+        for (int t = 0; t < NT; ++t) issue_unit(ring[PS * NT + t], ub[t], kw0 + (i + SP) * kSub, i + SP < nsub, tr[t].w);
+    };
+    for (int p0 = 0; p0 < nsub; p0 += SP) {
+        step(p0, std::integral_constant<int, 0>{});
+        if constexpr (SP == 4) {
+            step(p0, std::integral_constant<int, 1>{});
+            step(p0, std::integral_constant<int, 2>{});
+            step(p0, std::integral_constant<int, 3>{});
+        }
+    }
+
+    // Accumulator r of lane l is C[token 8*(r/4) + 4*h + r%4][row nl].
 #pragma unroll
-        for (int b = 0; b < 4; ++b) qm[b] = *reinterpret_cast<const u32x4 *>(cstage + nl * 144 + 32 * b + 16 * h);
+    for (int t = 0; t < NT; ++t) {
+        const int n = tr[t].local0 + nl;
+        if (n >= tr[t].n) continue;
+        if (gridDim.x == 1) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const float sblk = sstage[nl * SB + 4 * it + b];
-            const uint32_t wd[4] = {qm[b].x, qm[b].y, qm[b].z, qm[b].w};
-            f32x16 cb[MT];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const half8 bf = decode8(wd[j], cl, tbl);
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const _Float16 *xp = xs + (32 * mt + nl) * RS + 256 * it + 64 * b + 32 * h + 8 * j;
-                    const half8 af = *reinterpret_cast<const half8 *>(xp);
-                    cb[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, j == 0 ? f32x16{} : cb[mt], 0, 0, 0);
+            for (int r = 0; r < 16; ++r) {
+                const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m < a.M) {
+                    float *yp = tr[t].y + static_cast<size_t>(m) * tr[t].n + n;
+                    *yp = a.add ? *yp + acc[t][r] : acc[t][r];
                 }
             }
+        } else {
+            float *const ps = a.part + static_cast<size_t>(slice) * a.M * a.N + group0 + t * kGroupRows + wave * 32 + nl;
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[mt][r] = fmaf(sblk, cb[mt][r], acc[mt][r]);
-            // One block at a time: otherwise the scheduler hoists every
-            // block's table reads and runs out of registers.
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (it == ITERS - 1) {
-            const int n = tr[t].local0 + nl;
-            if (n < tr[t].n) {
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int m = 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
-                        if (m < a.M) unsafeAtomicAdd(tr[t].y + static_cast<size_t>(m) * tr[t].n + n, acc[mt][r]);
-                    }
+            for (int r = 0; r < 16; ++r) {
+                const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m < a.M) ps[static_cast<size_t>(m) * a.N] = acc[t][r];
             }
         }
     }
 }
 
-__global__ void zero_f32_kernel(float *p, long long n) {
-    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0.0f;
-}
+// Y (+)= the slices' partial sums, added in slice order: thread per output
+// element (m, stacked row n).
+struct ReduceArgs {
+    float *y[3];
+    int end[3];
+    int nseg;
+    int M, N, slices, add;
+    const float *part;
+};
 
-template <int MT, int KS, int NT>
-void launch_mm(const MmArgs &args, hipStream_t s) {
-    static bool lds_set = false;                 // the attribute is per kernel, per process
-    const void *fn = reinterpret_cast<const void *>(nf4_mm_kernel<MT, KS, NT>);
-    const size_t lds = mm_lds_bytes<MT, KS>();   // + the static table
-    if (!lds_set) {
-        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        lds_set = true;
+__global__ __launch_bounds__(256) void nf4_mm_reduce_kernel(ReduceArgs r) {
+    const long long idx = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= static_cast<long long>(r.M) * r.N) return;
+    const int m = static_cast<int>(idx / r.N), n = static_cast<int>(idx % r.N);
+    const float *p = r.part + idx;
+    const size_t stride = static_cast<size_t>(r.M) * r.N;
+    float v = 0.0f;
+    int s = 0;
+    for (; s + 4 <= r.slices; s += 4) {
+        const float p0 = p[s * stride], p1 = p[(s + 1) * stride], p2 = p[(s + 2) * stride], p3 = p[(s + 3) * stride];
+        v += p0;
+        v += p1;
+        v += p2;
+        v += p3;
     }
-    const dim3 grid((args.N + kMmRowsPerWg * NT - 1) / (kMmRowsPerWg * NT), args.K / KS), block(kMmThreads);
-    hipLaunchKernelGGL((nf4_mm_kernel<MT, KS, NT>), grid, block, lds, s, args);
+    for (; s < r.slices; ++s) v += p[s * stride];
+    const int seg = segment_of(r.end, r.nseg, n);
+    const int start = seg == 0 ? 0 : seg == 1 ? r.end[0] : r.end[1];
+    const int sn = (seg == 0 ? r.end[0] : seg == 1 ? r.end[1] : r.end[2]) - start;
+    float *yp = (seg == 0 ? r.y[0] : seg == 1 ? r.y[1] : r.y[2]) + static_cast<size_t>(m) * sn + (n - start);
+    *yp = r.add ? *yp + v : v;
 }
 
 }  // namespace
 
-// M in [2, 64], K % 512 == 0, block size 64, codes, absmax and x 16-byte aligned.
-// K-slices of 512 (M <= 32) or 256 (two m-tiles) keep every operand of a
-// slice in registers without spills.
-int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M,
-                           bool accumulate) {
-    if (nseg < 1 || nseg > 3 || M < 2 || M > 64 || K % 512 != 0 || bs_shift != 6 || !aligned(A, 16))
-        return ALJABR_ROCM_ERR_UNSUPPORTED;
+// Scratch floats the GEMM's partials need for M tokens over K with stacked
+// rows N (the most any plan can use: one slice per sub-slice).
+size_t nf4_mfma_scratch_floats(int M, int N, int K) {
+    return static_cast<size_t>(K / kSub) * M * N;
+}
+
+// Row tiles per wave and sub-slices per slice for N stacked rows over K on
+// `cus` CUs: two tiles per wave (each activation fragment read from LDS
+// feeds two tiles) once the 512-row groups number at least 16, and the
+// fewest slices that still give every CU a workgroup (one workgroup fits a
+// CU).
+void nf4_mfma_plan(int N, int K, int cus, int &nt, int &q) {
+    const int nsub = K / kSub;
+    nt = (N + 2LL * kGroupRows - 1) / (2LL * kGroupRows) >= 16 ? 2 : 1;
+    const long long groups = (N + static_cast<long long>(kGroupRows) * nt - 1) / (static_cast<long long>(kGroupRows) * nt);
+    q = nsub;
+    for (int cand = 1; cand < nsub; ++cand) {
+        if (groups * ((nsub + cand - 1) / cand) <= cus) {
+            q = cand;
+            break;
+        }
+    }
+}
+
+// The GEMM pass with an explicit plan (nt = 1 or 2 row tiles per wave,
+// q >= 1 sub-slices per slice).
+int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, int M, bool add, float *part,
+                          size_t part_floats, int nt, int q) {
     MmArgs args{};
+    ReduceArgs red{};
     long long end = 0;
     for (int i = 0; i < 3; ++i) {
         if (i < nseg) {
             const RowsOut &o = outs[i];
-            if (o.n <= 0 || !aligned(o.w, 16) || !aligned(o.absmax, 16) || (i < nseg - 1 && o.n % 32 != 0))
-                return ALJABR_ROCM_ERR_UNSUPPORTED;
             end += o.n;
             if (end > 0x7fff0000LL) return ALJABR_ROCM_ERR_UNSUPPORTED;
-            args.y[i] = o.y;
+            args.y[i] = red.y[i] = o.y;
             args.w[i] = o.w;
             args.absmax[i] = o.absmax;
-            args.end[i] = static_cast<int>(end);
+            args.end[i] = red.end[i] = static_cast<int>(end);
         } else {
-            args.end[i] = 0x7fffffff;
+            args.end[i] = red.end[i] = 0x7fffffff;
         }
     }
-    args.nseg = nseg;
+    if ((nt != 1 && nt != 2) || q < 1 || M < 1 || M > 32) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    args.nseg = red.nseg = nseg;
     args.x = A;
-    args.M = M;
-    args.N = static_cast<int>(end);
+    args.M = red.M = M;
+    args.N = red.N = static_cast<int>(end);
     args.K = K;
-    args.bs_shift = bs_shift;
+    const int nsub = K / kSub;
+    if (q > nsub) q = nsub;
+    args.q = q;
+    const int slices = (nsub + q - 1) / q;
+    const long long groups = (args.N + static_cast<long long>(kGroupRows) * nt - 1) / (static_cast<long long>(kGroupRows) * nt);
+    if (groups > 65535) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    args.add = slices == 1 && add;
+    if (slices > 1) {
+        const size_t need = static_cast<size_t>(slices) * M * args.N;
+        args.part = part && need <= part_floats ? part : static_cast<float *>(stream_scratch(need * sizeof(float)));
+        if (!args.part) return ALJABR_ROCM_ERR_BUFFER;
+    }
     hipStream_t s = current_stream();
-    if (!accumulate)   // the K-slices add into the outputs
+    static bool lds_set = false;                 // the attribute is per kernel, per process
+    if (!lds_set) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(nf4_mm_kernel<1>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsBytes));
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(nf4_mm_kernel<2>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsBytes));
+        lds_set = true;
+    }
+    const dim3 grid(slices, static_cast<unsigned>(groups));
+    if (nt == 2) hipLaunchKernelGGL(nf4_mm_kernel<2>, grid, dim3(kMmThreads), kLdsBytes, s, args);
+    else hipLaunchKernelGGL(nf4_mm_kernel<1>, grid, dim3(kMmThreads), kLdsBytes, s, args);
+    if (slices > 1) {
+        red.slices = slices;
+        red.add = add ? 1 : 0;
+        red.part = args.part;
+        const long long total = static_cast<long long>(M) * args.N;
+        hipLaunchKernelGGL(nf4_mm_reduce_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s,
+                           red);
+    }
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M, bool add,
+                           float *part, size_t part_floats) {
+    if (nseg < 1 || nseg > 3 || M < 2 || K % kSub != 0 || bs_shift != 6 || !aligned(A, 16))
+        return ALJABR_ROCM_ERR_UNSUPPORTED;
+    long long n = 0;
+    for (int i = 0; i < nseg; ++i) {
+        if (outs[i].n <= 0 || !aligned(outs[i].w, 16) || !aligned(outs[i].absmax, 8) ||
+            (i < nseg - 1 && outs[i].n % 32 != 0))
+            return ALJABR_ROCM_ERR_UNSUPPORTED;
+        n += outs[i].n;
+    }
+    if (n > 0x7fff0000LL) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    int nt = 1, q = 1;
+    nf4_mfma_plan(static_cast<int>(n), K, device_cu_count() > 0 ? device_cu_count() : 256, nt, q);
+    // Passes of up to 32 tokens (one m-tile); a pass's outputs are the rows
+    // m0 .. m0 + mm - 1 of each segment.
+    for (int m0 = 0; m0 < M; m0 += 32) {
+        const int mm = M - m0 < 32 ? M - m0 : 32;
+        RowsOut o[3];
         for (int i = 0; i < nseg; ++i) {
-            const long long total = static_cast<long long>(M) * outs[i].n;
-            hipLaunchKernelGGL(zero_f32_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s,
-                               outs[i].y, total);
+            o[i] = outs[i];
+            o[i].y = outs[i].y + static_cast<size_t>(m0) * outs[i].n;
         }
-    const int N = args.N;
-    const int wgs_n = (N + kMmRowsPerWg - 1) / kMmRowsPerWg;
-    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-    // One generation of workgroups (one per CU): the fewest row tiles per
-    // wave (1, 2 or 4) that fit all row tiles x K-slices on the CUs.
-    const long long units = static_cast<long long>(wgs_n) * (K / (M <= 32 ? 512 : 256));
-    const int nt = units <= cus ? 1 : units <= 2LL * cus ? 2 : 4;
-    if (M <= 32) {                               // (four tiles would spill at one m-tile)
-        if (nt == 1) launch_mm<1, 512, 1>(args, s);
-        else launch_mm<1, 512, 2>(args, s);
-    } else {
-        if (nt == 1) launch_mm<2, 256, 1>(args, s);
-        else if (nt == 2) launch_mm<2, 256, 2>(args, s);
-        else launch_mm<2, 256, 4>(args, s);
+        const int rc =
+            nf4_mfma_pass_planned(o, nseg, A + static_cast<size_t>(m0) * K, K, mm, add, part, part_floats, nt, q);
+        if (rc != ALJABR_ROCM_OK) return rc;
     }
     return ALJABR_ROCM_OK;
 }
 
 int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
-                     int M, bool accumulate) {
+                     int M, bool add, float *part, size_t part_floats) {
     const RowsOut o{C, Bq, absmax, N};
-    return enqueue_nf4_mfma_multi(&o, 1, A, K, bs_shift, M, accumulate);
+    return enqueue_nf4_mfma_multi(&o, 1, A, K, bs_shift, M, add, part, part_floats);
 }
 
 }  // namespace aljabr

@@ -467,26 +467,12 @@ int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float 
         if (shift >= 0 && enqueue_rows_nf4_mt(C, A, Bq, absmax, K, N, shift, M) == ALJABR_ROCM_OK)
             return ALJABR_ROCM_OK;
     }
-    // M >= 2 on the matrix cores when the shape allows, 64 tokens per pass.
+    // M >= 2 on the matrix cores when the shape allows (fp32-accurate,
+    // deterministic; passes of 32 tokens).
     if (M >= 2 && mfma_enabled()) {
         const int shift = log2_exact(bs);
-        bool ok = true;
-        for (int m0 = 0; m0 < M && ok; m0 += 64) {
-            const int mm = M - m0 < 64 ? M - m0 : 64;
-            if (mm < 2) break;                   // a last single row takes the batch-1 path below
-            const int rc = enqueue_nf4_mfma(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, Bq,
-                                            absmax, K, N, shift, mm);
-            if (rc != ALJABR_ROCM_OK) {
-                if (m0 != 0) return rc;          // the shape checks do not depend on m0
-                ok = false;
-            }
-        }
-        if (ok) {
-            const int done = M - (M % 64 == 1 ? 1 : 0);
-            if (done == M) return ALJABR_ROCM_OK;
-            return enqueue_nf4_small(C + static_cast<size_t>(done) * N, A + static_cast<size_t>(done) * K, Bq,
-                                     absmax, K, N, bs, 1);
-        }
+        const int rc = enqueue_nf4_mfma(C, A, Bq, absmax, K, N, shift, M);
+        if (rc != ALJABR_ROCM_ERR_UNSUPPORTED) return rc;
     }
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mm = M - m0 < 8 ? M - m0 : 8;

@@ -182,7 +182,7 @@ def test_decode_graph_replays_match_eager(rocm, dev, oracle, ci, batch):
     cur = (np.array([5, 17, 1999], np.int32) % cfg["vocab"])[:batch]
     le = torch.empty(batch * cfg["vocab"], dtype=torch.float32, device="cuda:0")
     lg = [torch.empty_like(le), torch.empty_like(le)]
-    tol = 0.0 if batch == 1 else 1e-5
+    tol = 0.0                                   # deterministic at every batch (no float atomics)
     for step in range(6):
         pos = np.full(batch, step, np.int32)
         te = eager.decode(dev.put(cur), dev.put(pos), batch, logits=le)
