@@ -71,7 +71,7 @@ struct aljabr_rocm_llama {
     float2 *rope_cs = nullptr;   // [max_seq][head_dim/2] RoPE cos/sin, filled at creation
     float *attn_scratch = nullptr;   // split-attention partials (owned: a captured graph keeps the address)
     size_t attn_scratch_bytes = 0;
-    float *mm_part = nullptr;        // K-slice partials of the batched NF4 GEMMs
+    float *mm_part = nullptr;        // K-slice partials of the batched matrix-core GEMMs
     size_t mm_part_floats = 0;
     bool rows_fused = false;   // batch-1 layers as fused NF4 launches (shapes and alignment allow it)
     // Captured decode steps, by batch size (and the logits buffer they write).
@@ -239,13 +239,17 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
     const size_t kvd = static_cast<size_t>(c.n_kv_heads) * c.head_dim;
     const size_t qd = static_cast<size_t>(c.n_heads) * c.head_dim;
     const size_t cache_elems = static_cast<size_t>(L) * B * kvd * c.max_seq;
-    // Partials of the batched NF4 GEMMs (passes of at most 32 tokens).
+    // K-slice partials of the batched matrix-core GEMMs (passes of at most
+    // 32 tokens): the NF4 bound of every layer shape, and the K-quant bound
+    // (one slice per 512 elements) of the output head, whose NF4 plan has a
+    // single slice.
     size_t mm_floats = 0;
     if (c.max_batch >= 2) {
         const int bp = c.max_batch < 32 ? c.max_batch : 32;
         const int shapes[4][2] = {{static_cast<int>(qd + 2 * kvd), c.dim}, {c.dim, static_cast<int>(qd)},
                                   {2 * c.ffn, c.dim}, {c.dim, c.ffn}};
         for (const auto &sh : shapes) mm_floats = std::max(mm_floats, nf4_mfma_scratch_floats(bp, sh[0], sh[1]));
+        mm_floats = std::max(mm_floats, static_cast<size_t>(c.dim / 512) * bp * static_cast<size_t>(c.vocab));
     }
     const size_t bytes = 2 * ((cache_elems * 2 + 255) & ~size_t(255)) +
                          ((mm_floats * 4 + 255) & ~size_t(255)) +
@@ -849,7 +853,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         }
         if (kquant_mfma_type(t.type) && B >= 2 && B <= kquant_mfma_max_m(t.type)) {
             const KqOut o{y, t.w, N};
-            const int r = enqueue_kquant_mfma_multi(&o, 1, x, K, t.type, B, true);
+            const int r = enqueue_kquant_mfma_multi(&o, 1, x, K, t.type, B, true, m->mm_part, m->mm_part_floats);
             if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
         }
         if (!residual) return enqueue_matmul_typed(y, x, t.w, t.s, t.type, bs, K, N, B);
@@ -867,7 +871,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             if (kquant_mfma_type(ts[i]->type) && B >= 2 && B <= kquant_mfma_max_m(ts[i]->type)) {
                 KqOut o[3];
                 for (int k = i; k < j; ++k) o[k - i] = KqOut{ys[k], ts[k]->w, ns[k]};
-                r = enqueue_kquant_mfma_multi(o, j - i, x, K, ts[i]->type, B, true);
+                r = enqueue_kquant_mfma_multi(o, j - i, x, K, ts[i]->type, B, true, m->mm_part, m->mm_part_floats);
             }
             if (r == ALJABR_ROCM_ERR_UNSUPPORTED) {
                 for (int k = i; k < j; ++k) {

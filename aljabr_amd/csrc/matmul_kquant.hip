@@ -43,8 +43,9 @@
 // K-slice of KS elements; a work unit is the wave's 32 rows x 256 elements
 // (one K-quant super-block, eight Q4_0/Q8_0 blocks: 144, 210, 144 and 272
 // bytes a row). Weights are loaded coalesced (whole row segments per lane
-// group) and transposed through per-wave LDS rows, two units ahead; K-slices
-// add their partial sums into Y with float atomics (Y is zeroed first).
+// group) and transposed through per-wave LDS rows, two units ahead. With
+// several K-slices each stores its partial tile and enqueue_slice_sum adds
+// the slices in order (deterministic: no float atomics).
 #include "device.hpp"
 #include "internal.hpp"
 #include "kernels.hpp"
@@ -75,6 +76,8 @@ struct KqArgs {
     int end[3];
     int nseg;
     int M, N, K;   // N: stacked rows
+    int add;       // one K slice: Y += instead of Y =
+    float *part;   // several K slices: [slice][M][N] partial sums
 };
 
 // The segment of the tile starting at stacked row r0.
@@ -446,19 +449,29 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
         if (sbl == SBS - 1) {
             const int n = tr[t].local0 + nl;
             if (n < tr[t].n) {
+                if (gridDim.y == 1) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int m = 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (m < a.M) unsafeAtomicAdd(tr[t].y + static_cast<size_t>(m) * tr[t].n + n, acc[r]);
+                    for (int r = 0; r < 16; ++r) {
+                        const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+                        if (m < a.M) {
+                            float *yp = tr[t].y + static_cast<size_t>(m) * tr[t].n + n;
+                            *yp = a.add ? *yp + acc[r] : acc[r];
+                        }
+                    }
+                } else {
+                    // This slice's partial tile; the slice sum adds the
+                    // slices in order.
+                    float *ps = a.part + static_cast<size_t>(blockIdx.y) * a.M * a.N + blockIdx.x * (kRowsPerWg * NT) +
+                                t * kRowsPerWg + wave * 32 + nl;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+                        if (m < a.M) ps[static_cast<size_t>(m) * a.N] = acc[r];
+                    }
                 }
             }
         }
     }
-}
-
-__global__ void kq_zero_kernel(float *p, long long n) {
-    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0.0f;
 }
 
 template <int F, int KS, int NT, int MT>
@@ -494,7 +507,8 @@ int kquant_mfma_max_m(int type) {
 // 2 <= M <= kquant_mfma_max_m(type), K % 512 == 0, A and weights 16-byte
 // aligned, up to three matrices of one type (all but the last with a
 // multiple of 32 rows).
-int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate) {
+int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate,
+                              float *part, size_t part_floats) {
     if (!kquant_mfma_type(type) || nseg < 1 || nseg > 3 || M < 2 || M > kquant_mfma_max_m(type) || K % 512 != 0 ||
         !aligned(A, 16))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
@@ -519,12 +533,15 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
     args.N = static_cast<int>(end);
     args.K = K;
     hipStream_t s = current_stream();
-    if (!accumulate)   // the K-slices add into the outputs
-        for (int i = 0; i < nseg; ++i) {
-            const long long total = static_cast<long long>(M) * outs[i].n;
-            hipLaunchKernelGGL(kq_zero_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s,
-                               outs[i].y, total);
-        }
+    const int slices = K / 512;
+    args.add = slices == 1 && accumulate;
+    if (slices > 1) {
+        const size_t need = static_cast<size_t>(slices) * M * args.N;
+        args.part = part && need <= part_floats
+                        ? part
+                        : static_cast<float *>(stream_scratch(need * sizeof(float), kScratchPartials));
+        if (!args.part) return ALJABR_ROCM_ERR_BUFFER;
+    }
     const int wgs_n = (args.N + kRowsPerWg - 1) / kRowsPerWg;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     const long long units = static_cast<long long>(wgs_n) * (K / 512);
@@ -534,6 +551,10 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
     case ALJABR_ROCM_TYPE_Q6_K: launch_kq_nt<kFQ6K, 32>(args, two, s); break;
     case ALJABR_ROCM_TYPE_Q4_0: launch_kq_nt<kFQ40, 8>(args, two, s); break;
     default: launch_kq_nt<kFQ80, 8>(args, two, s); break;
+    }
+    if (slices > 1) {
+        float *ys[3] = {args.y[0], args.y[1], args.y[2]};
+        return enqueue_slice_sum(ys, args.end, nseg, M, args.N, args.part, slices, accumulate);
     }
     return ALJABR_ROCM_OK;
 }

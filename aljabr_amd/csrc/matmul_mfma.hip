@@ -464,7 +464,7 @@ __global__ __launch_bounds__(kMmThreads) void nf4_mm_kernel(MmArgs a) {
 }
 
 // Y (+)= the slices' partial sums, added in slice order: thread per output
-// element (m, stacked row n).
+// element (m, stacked row n). Shared by the NF4 and K-quant GEMMs.
 struct ReduceArgs {
     float *y[3];
     int end[3];
@@ -527,26 +527,25 @@ void nf4_mfma_plan(int N, int K, int cus, int &nt, int &q) {
 int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, int M, bool add, float *part,
                           size_t part_floats, int nt, int q) {
     MmArgs args{};
-    ReduceArgs red{};
     long long end = 0;
     for (int i = 0; i < 3; ++i) {
         if (i < nseg) {
             const RowsOut &o = outs[i];
             end += o.n;
             if (end > 0x7fff0000LL) return ALJABR_ROCM_ERR_UNSUPPORTED;
-            args.y[i] = red.y[i] = o.y;
+            args.y[i] = o.y;
             args.w[i] = o.w;
             args.absmax[i] = o.absmax;
-            args.end[i] = red.end[i] = static_cast<int>(end);
+            args.end[i] = static_cast<int>(end);
         } else {
-            args.end[i] = red.end[i] = 0x7fffffff;
+            args.end[i] = 0x7fffffff;
         }
     }
     if ((nt != 1 && nt != 2) || q < 1 || M < 1 || M > 32) return ALJABR_ROCM_ERR_UNSUPPORTED;
-    args.nseg = red.nseg = nseg;
+    args.nseg = nseg;
     args.x = A;
-    args.M = red.M = M;
-    args.N = red.N = static_cast<int>(end);
+    args.M = M;
+    args.N = static_cast<int>(end);
     args.K = K;
     const int nsub = K / kSub;
     if (q > nsub) q = nsub;
@@ -557,7 +556,9 @@ int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, 
     args.add = slices == 1 && add;
     if (slices > 1) {
         const size_t need = static_cast<size_t>(slices) * M * args.N;
-        args.part = part && need <= part_floats ? part : static_cast<float *>(stream_scratch(need * sizeof(float)));
+        args.part = part && need <= part_floats
+                        ? part
+                        : static_cast<float *>(stream_scratch(need * sizeof(float), kScratchPartials));
         if (!args.part) return ALJABR_ROCM_ERR_BUFFER;
     }
     hipStream_t s = current_stream();
@@ -572,14 +573,26 @@ int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, 
     const dim3 grid(slices, static_cast<unsigned>(groups));
     if (nt == 2) hipLaunchKernelGGL(nf4_mm_kernel<2>, grid, dim3(kMmThreads), kLdsBytes, s, args);
     else hipLaunchKernelGGL(nf4_mm_kernel<1>, grid, dim3(kMmThreads), kLdsBytes, s, args);
-    if (slices > 1) {
-        red.slices = slices;
-        red.add = add ? 1 : 0;
-        red.part = args.part;
-        const long long total = static_cast<long long>(M) * args.N;
-        hipLaunchKernelGGL(nf4_mm_reduce_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s,
-                           red);
+    if (slices > 1) return enqueue_slice_sum(args.y, args.end, nseg, M, args.N, args.part, slices, add);
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_slice_sum(float *const *ys, const int *ends, int nseg, int M, int N, const float *part, int slices,
+                      bool add) {
+    ReduceArgs red{};
+    for (int i = 0; i < 3; ++i) {
+        red.y[i] = i < nseg ? ys[i] : nullptr;
+        red.end[i] = i < nseg ? ends[i] : 0x7fffffff;
     }
+    red.nseg = nseg;
+    red.M = M;
+    red.N = N;
+    red.slices = slices;
+    red.add = add ? 1 : 0;
+    red.part = part;
+    const long long total = static_cast<long long>(M) * N;
+    hipLaunchKernelGGL(nf4_mm_reduce_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                       current_stream(), red);
     return ALJABR_ROCM_OK;
 }
 

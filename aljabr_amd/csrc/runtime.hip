@@ -30,7 +30,7 @@ struct Context {
     int cu_count = 0;
     std::atomic<uint64_t> generation{0};   // bumps on every (re)init so stale thread state is dropped
     std::vector<hipStream_t> owned_streams;                  // one per thread, created lazily
-    std::unordered_map<hipStream_t, Scratch> scratch;        // per stream
+    std::unordered_map<hipStream_t, Scratch[kScratchSlots]> scratch;   // per stream and slot
 };
 
 Context &ctx() {
@@ -106,11 +106,11 @@ int finish_launch(const char *what) {
     return ALJABR_ROCM_OK;
 }
 
-void *stream_scratch(size_t bytes) {
+void *stream_scratch(size_t bytes, int slot) {
     Context &c = ctx();
     hipStream_t s = current_stream();
     std::lock_guard<std::mutex> lock(c.mu);
-    Scratch &sc = c.scratch[s];
+    Scratch &sc = c.scratch[s][slot];
     if (sc.bytes >= bytes) return sc.ptr;
     // Growing: the old buffer may still be read by queued work on this stream.
     if (sc.ptr) {
@@ -221,7 +221,8 @@ int aljabr_rocm_shutdown(void) {
     (void)hipSetDevice(c.device);
     (void)hipDeviceSynchronize();
     for (auto &kv : c.scratch)
-        if (kv.second.ptr) (void)hipFree(kv.second.ptr);
+        for (Scratch &sc : kv.second)
+            if (sc.ptr) (void)hipFree(sc.ptr);
     c.scratch.clear();
     for (hipStream_t s : c.owned_streams) (void)hipStreamDestroy(s);
     c.owned_streams.clear();

@@ -169,9 +169,9 @@ def test_decode_profile_matches_decode(rocm, dev, oracle, ci, batch):
 def test_decode_graph_replays_match_eager(rocm, dev, oracle, ci, batch):
     """The captured whole-step graph against eager steps of a twin session:
     six replays (the first call captures), each followed by eager work and a
-    synchronisation, every replay checked (tokens equal, logits equal up to
-    the matrix cores' atomic summation order), and a change of logits buffer
-    (a second capture)."""
+    synchronisation, every replay checked (tokens and logits bit-identical:
+    every launch sums in a fixed order), and a change of logits buffer (a
+    second capture)."""
     import torch
     from aljabr_amd.llama import DeviceLlama, upload_weights
     cfg = CONFIGS[ci]

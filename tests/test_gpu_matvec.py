@@ -100,6 +100,29 @@ def test_gguf_mfma_small_m(rocm, dev, oracle, qtype, n, k, m):
         assert rel_l2(got[i * n:(i + 1) * n], y_ref[i * n:(i + 1) * n]) <= TOL, i
 
 
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0", "q4_k", "q6_k"])
+def test_gguf_mfma_is_deterministic(rocm, dev, oracle, qtype):
+    """The K-quant matrix-core GEMM twice over 8 K slices gives the same bits
+    (the slices' partials are summed in slice order, no float atomics)."""
+    n, k = 4096, 4096
+    m = 8 if qtype in ("q4_0", "q8_0") else 32
+    qt, ot = {"q4_0": (rocm.TYPE_Q4_0, oracle.QTYPE_Q4_0), "q8_0": (rocm.TYPE_Q8_0, oracle.QTYPE_Q8_0),
+              "q4_k": (rocm.TYPE_Q4_K, oracle.QTYPE_Q4_K), "q6_k": (rocm.TYPE_Q6_K, oracle.QTYPE_Q6_K)}[qtype]
+    if qtype in ("q4_0", "q8_0"):
+        enc = oracle.quantize(ot, oracle.normal(71, n * k, 0.0, 0.02))
+    else:   # no K-quant encoder: random super-blocks (as the concurrency test)
+        enc = oracle.random_k_blocks(ot, n * k // 256, 71, scale=0.5 / np.sqrt(k) / (200 if qtype == "q4_k" else 1000))
+    x = oracle.normal(73, m * k)
+    wd, xd = dev.put(enc), dev.put(x)
+    outs = []
+    for _ in range(2):
+        y = dev.empty(m * n)
+        rocm.call("aljabr_rocm_matvec_tb_batch", dev.ptr(y), dev.ptr(xd), dev.ptr(wd), k, n, qt, m)
+        outs.append(dev.get(y))
+    assert np.array_equal(outs[0], outs[1])
+    assert rel_l2(outs[0], oracle.q_matvec(ot, enc, x, n, k).ravel()) <= TOL
+
+
 # NF4 small-M GEMM on the matrix cores (passes of 32 tokens, K % 256 == 0;
 # M = 2..4 with K % 2048 == 0 take the fp32 rows kernel): M across the pass
 # boundaries (32, 33, 64, 65, 100), ragged N, K of one to 56 sub-slices, the
