@@ -115,6 +115,91 @@ __device__ __forceinline__ void key_range(const AttnParams &p, int sk, int qi, i
     }
 }
 
+// Merge the split partials of one query row with NTH threads: D/4 lanes take
+// one split's o as float4s, so NTH/(D/4) splits are read at once; each lane
+// group folds its splits (in split order) with online rescaling, and the
+// groups are combined through `st` ([NTH/(D/4)][D + 2] floats of LDS).
+template <int D, int NTH>
+__device__ __forceinline__ void merge_row(const AttnParams &p, const float *__restrict__ part_o,
+                                          const float *__restrict__ part_ml, int splits, long long row, float *st) {
+    constexpr int LPS = D / 4;          // lanes per split
+    constexpr int SG = NTH / LPS;       // splits in flight
+    const int qi = static_cast<int>(row % p.Sq);
+    const int h = static_cast<int>((row / p.Sq) % p.Hq);
+    const int bb = static_cast<int>(row / (static_cast<long long>(p.Sq) * p.Hq));
+    float *out = p.out + bb * p.q_sb + h * p.q_sh + qi * p.q_sq;
+    const int sg = threadIdx.x / LPS, j = threadIdx.x % LPS;
+    const float *po = part_o + row * splits * D;
+    const float *pm = part_ml + row * splits * 2;
+    float m = -INFINITY, l = 0.0f;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // Eight splits per trip with all their loads issued before any is used
+    // (one memory round trip per trip instead of one per split).
+    constexpr int U = 8;
+    for (int s0 = sg; s0 < splits; s0 += U * SG) {
+        float ms[U], ls[U];
+        float4 os[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = s0 + u * SG;
+            const int sc = s < splits ? s : sg;                 // in-range row, ignored below
+            ms[u] = pm[2 * sc];
+            ls[u] = pm[2 * sc + 1];
+            os[u] = *reinterpret_cast<const float4 *>(po + sc * D + 4 * j);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (s0 + u * SG >= splits) break;
+            const float mn = fmaxf(m, ms[u]);
+            if (mn == -INFINITY) continue;
+            const float a = m == -INFINITY ? 0.0f : exp2f(m - mn);
+            const float b = ms[u] == -INFINITY ? 0.0f : exp2f(ms[u] - mn);
+            l = fmaf(l, a, ls[u] * b);
+            o.x = fmaf(o.x, a, os[u].x * b);
+            o.y = fmaf(o.y, a, os[u].y * b);
+            o.z = fmaf(o.z, a, os[u].z * b);
+            o.w = fmaf(o.w, a, os[u].w * b);
+            m = mn;
+        }
+    }
+    float *my = st + sg * (D + 2);
+    my[4 * j] = o.x;
+    my[4 * j + 1] = o.y;
+    my[4 * j + 2] = o.z;
+    my[4 * j + 3] = o.w;
+    if (j == 0) {
+        my[D] = m;
+        my[D + 1] = l;
+    }
+    __syncthreads();
+    for (int dd = threadIdx.x; dd < D; dd += NTH) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < SG; ++g) M = fmaxf(M, st[g * (D + 2) + D]);
+        float L = 0.0f, O = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int g = 0; g < SG; ++g) {
+                const float mg = st[g * (D + 2) + D];
+                if (mg == -INFINITY) continue;
+                const float w = exp2f(mg - M);
+                L = fmaf(st[g * (D + 2) + D + 1], w, L);
+                O = fmaf(st[g * (D + 2) + dd], w, O);
+            }
+        }
+        out[dd] = L == 0.0f ? 0.0f : O / (L + p.norm_eps);
+    }
+    __syncthreads();                    // `st` is free again
+}
+
+// Merge split partials: one 256-thread workgroup per query row.
+template <int D>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, const float *__restrict__ part_o,
+                                                        const float *__restrict__ part_ml, int splits) {
+    __shared__ float st[(256 / (D / 4)) * (D + 2)];
+    merge_row<D, 256>(p, part_o, part_ml, splits, blockIdx.x, st);
+}
+
 template <int D, int G, bool F16, int WAVES, bool PAGED>
 __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, int splits, int chunk,
                                                                 float *__restrict__ part_o,
@@ -281,20 +366,29 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
     }
     __syncthreads();
 
-    // Merge the NG group states; one thread per (head, dim).
+    // Merge the NG group states; one thread per (head, dim). All NG states
+    // are read before any is used (the reads overlap instead of queueing
+    // behind each other); an empty group (m = -inf, l = o = 0) weighs 0.
     for (int idx = threadIdx.x; idx < G * D; idx += WAVES * 64) {
         const int g = idx / D, dd = idx % D;
+        float mg[NG], lg[NG], og[NG];
+#pragma unroll
+        for (int gr = 0; gr < NG; ++gr) {
+            const float *st = smem + (gr * G + g) * (D + 2);
+            mg[gr] = st[D];
+            lg[gr] = st[D + 1];
+            og[gr] = st[dd];
+        }
         float M = -INFINITY;
-        for (int gr = 0; gr < NG; ++gr) M = fmaxf(M, smem[(gr * G + g) * (D + 2) + D]);
+#pragma unroll
+        for (int gr = 0; gr < NG; ++gr) M = fmaxf(M, mg[gr]);
         float L = 0.0f, O = 0.0f;
         if (M != -INFINITY) {
+#pragma unroll
             for (int gr = 0; gr < NG; ++gr) {
-                const float *st = smem + (gr * G + g) * (D + 2);
-                const float mg = st[D];
-                if (mg == -INFINITY) continue;
-                const float w = exp2f(mg - M);
-                L = fmaf(st[D + 1], w, L);
-                O = fmaf(st[dd], w, O);
+                const float w = mg[gr] == -INFINITY ? 0.0f : exp2f(mg[gr] - M);
+                L = fmaf(lg[gr], w, L);
+                O = fmaf(og[gr], w, O);
             }
         }
         const int h = kvh * G + g;
@@ -308,83 +402,6 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
                 part_ml[(row * splits + split) * 2 + 1] = L;
             }
         }
-    }
-}
-
-// Merge split partials: one 256-thread workgroup per query row. D/4 lanes
-// take one split's o as float4s, so 256/(D/4) splits are read at once; each
-// lane group folds its splits with online rescaling, and the groups are
-// combined through LDS.
-template <int D>
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, const float *__restrict__ part_o,
-                                                        const float *__restrict__ part_ml, int splits) {
-    constexpr int LPS = D / 4;          // lanes per split
-    constexpr int SG = 256 / LPS;       // splits in flight
-    __shared__ float st[SG][D + 2];
-    const long long row = blockIdx.x;   // (b * Hq + h) * Sq + qi
-    const int qi = static_cast<int>(row % p.Sq);
-    const int h = static_cast<int>((row / p.Sq) % p.Hq);
-    const int bb = static_cast<int>(row / (static_cast<long long>(p.Sq) * p.Hq));
-    float *out = p.out + bb * p.q_sb + h * p.q_sh + qi * p.q_sq;
-    const int sg = threadIdx.x / LPS, j = threadIdx.x % LPS;
-    const float *po = part_o + row * splits * D;
-    const float *pm = part_ml + row * splits * 2;
-    float m = -INFINITY, l = 0.0f;
-    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    // Eight splits per trip with all their loads issued before any is used
-    // (one memory round trip per trip instead of one per split).
-    constexpr int U = 8;
-    for (int s0 = sg; s0 < splits; s0 += U * SG) {
-        float ms[U], ls[U];
-        float4 os[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int s = s0 + u * SG;
-            const int sc = s < splits ? s : sg;                 // in-range row, ignored below
-            ms[u] = pm[2 * sc];
-            ls[u] = pm[2 * sc + 1];
-            os[u] = *reinterpret_cast<const float4 *>(po + sc * D + 4 * j);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (s0 + u * SG >= splits) break;
-            const float mn = fmaxf(m, ms[u]);
-            if (mn == -INFINITY) continue;
-            const float a = m == -INFINITY ? 0.0f : exp2f(m - mn);
-            const float b = ms[u] == -INFINITY ? 0.0f : exp2f(ms[u] - mn);
-            l = fmaf(l, a, ls[u] * b);
-            o.x = fmaf(o.x, a, os[u].x * b);
-            o.y = fmaf(o.y, a, os[u].y * b);
-            o.z = fmaf(o.z, a, os[u].z * b);
-            o.w = fmaf(o.w, a, os[u].w * b);
-            m = mn;
-        }
-    }
-    st[sg][4 * j] = o.x;
-    st[sg][4 * j + 1] = o.y;
-    st[sg][4 * j + 2] = o.z;
-    st[sg][4 * j + 3] = o.w;
-    if (j == 0) {
-        st[sg][D] = m;
-        st[sg][D + 1] = l;
-    }
-    __syncthreads();
-    for (int dd = threadIdx.x; dd < D; dd += 256) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int g = 0; g < SG; ++g) M = fmaxf(M, st[g][D]);
-        float L = 0.0f, O = 0.0f;
-        if (M != -INFINITY) {
-#pragma unroll
-            for (int g = 0; g < SG; ++g) {
-                const float mg = st[g][D];
-                if (mg == -INFINITY) continue;
-                const float w = exp2f(mg - M);
-                L = fmaf(st[g][D + 1], w, L);
-                O = fmaf(st[g][dd], w, O);
-            }
-        }
-        out[dd] = L == 0.0f ? 0.0f : O / (L + p.norm_eps);
     }
 }
 
