@@ -190,6 +190,27 @@ SIGNATURES = {
                                               ctypes.POINTER(_I)]),
     "aljabr_rocm_llama_hidden": (_I, [_P, ctypes.POINTER(_P)]),
     "aljabr_rocm_llama_kv_cache": (_I, [_P, ctypes.POINTER(_P), ctypes.POINTER(_P)]),
+    "aljabr_rocm_init_kv_cache": (_I, [_I, _I, _P]),
+    "aljabr_rocm_sync_kv_cache": (_I, [_I, _I, _P, _P]),
+    "aljabr_rocm_register_norm_buffer": (_I, [_I, _P, _SZ]),
+    "aljabr_rocm_register_rope_freqs": (_I, [_I, _P, _I]),
+    "aljabr_rocm_register_decode_layer": (_I, [_I, _I] + [_P] * 7 + [_I] * 7 + [_I] * 10 + [_F, _I, _F, _F]
+                                          + [_I] * 5),
+    "aljabr_rocm_register_output": (_I, [_P, _P, _I, _I, _I, _F]),
+    "aljabr_rocm_register_token_embd": (_I, [_P, _I, _I, _F]),
+    "aljabr_rocm_decode_step": (_I, [_I, _I, _F, _P, _P]),
+    "aljabr_rocm_decode_step_token": (_I, [_I, _I, _F, _I, _P]),
+    "aljabr_rocm_set_decode_activation": (_I, [_I]),
+    "aljabr_rocm_reset_decode_state": (_I, []),
+    "aljabr_rocm_wo_ffn_next_qkv_fused": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, _P, _P, _I, _F, _F, _P, _P, _P,
+                                               _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
+                                               _I, _I, _I]),
+    "aljabr_rocm_wo_ffn_fused": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, _I, _P, _I, _P, _I, _I, _F, _P, _P, _P,
+                                      _I, _I, _I, _I, _I]),
+    "aljabr_rocm_wo_ffn_logits_fused": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, _P, _P, _I, _F, _F, _P, _P, _P,
+                                             _I, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _F]),
+    "aljabr_rocm_wo_ffn_reset_x": (None, []),
+    "aljabr_rocm_wo_ffn_fused_layer_batch": (_I, [_P, _P, _I, _I, _F, _I]),
 }
 
 

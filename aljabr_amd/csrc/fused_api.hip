@@ -48,10 +48,12 @@ __global__ void gated_act_kernel(float *__restrict__ out, const float *__restric
     out[i] = isfinite(y) ? y : 0.0f;
 }
 
+}  // namespace
+
 // C_i[batch][N_i] = A[batch][K] . B_i^T for i < n: one stacked launch when
 // every matrix has the same type and the shape allows, else one per matrix.
-int enqueue_multi(float *const *C, const float *A, const uint8_t *const *B, int K, const int *N, const int *type,
-                  int n, int batch) {
+int enqueue_matmul_multi(float *const *C, const float *A, const uint8_t *const *B, int K, const int *N,
+                         const int *type, int n, int batch) {
     bool same = true;
     for (int i = 1; i < n; ++i) same = same && type[i] == type[0];
     if (same && batch == 1 && type[0] != ALJABR_ROCM_TYPE_F32 && type[0] != ALJABR_ROCM_TYPE_F16) {
@@ -72,6 +74,15 @@ int enqueue_multi(float *const *C, const float *A, const uint8_t *const *B, int 
     }
     return ALJABR_ROCM_OK;
 }
+
+int enqueue_gated_act(float *out, const float *gate, const float *up, long long n, int kind) {
+    if (n <= 0) return ALJABR_ROCM_OK;
+    hipLaunchKernelGGL(gated_act_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                       current_stream(), out, gate, up, n, kind == 2 ? 1 : 0);
+    return ALJABR_ROCM_OK;
+}
+
+namespace {
 
 int check_multi(const void *const *C, const void *A, const void *const *B, int K, const int *N, const int *type,
                 int n, int batch, const char *what) {
@@ -101,7 +112,7 @@ int multi_entry(void *const *C, const void *A, const void *const *B, int K, cons
         c[i] = static_cast<float *>(C[i]);
         b[i] = static_cast<const uint8_t *>(B[i]);
     }
-    rc = enqueue_multi(c, static_cast<const float *>(A), b, K, N, type, n, batch);
+    rc = enqueue_matmul_multi(c, static_cast<const float *>(A), b, K, N, type, n, batch);
     if (rc != ALJABR_ROCM_OK) return rc;
     return finish_launch(what);
 }
@@ -128,13 +139,12 @@ int ffn_entry(void *outDown, const void *inA, const void *gateW, const void *upW
     float *gate = scratch, *up = scratch + hs, *h = scratch + 2 * hs;
     float *gu[2] = {gate, up};
     const uint8_t *gw[2] = {static_cast<const uint8_t *>(gateW), static_cast<const uint8_t *>(upW)};
-    rc = enqueue_multi(gu, static_cast<const float *>(inA), gw, dim, gu_n, gu_t, 2, batch);
+    rc = enqueue_matmul_multi(gu, static_cast<const float *>(inA), gw, dim, gu_n, gu_t, 2, batch);
     if (rc != ALJABR_ROCM_OK) return rc;
-    hipLaunchKernelGGL(gated_act_kernel, dim3(static_cast<unsigned>((hn + 255) / 256)), dim3(256), 0,
-                       current_stream(), h, gate, up, hn, activationKind == 2 ? 1 : 0);
+    enqueue_gated_act(h, gate, up, hn, activationKind);
     float *od[1] = {static_cast<float *>(outDown)};
     const uint8_t *dw[1] = {static_cast<const uint8_t *>(downW)};
-    rc = enqueue_multi(od, h, dw, ffnDim, d_n, d_t, 1, batch);
+    rc = enqueue_matmul_multi(od, h, dw, ffnDim, d_n, d_t, 1, batch);
     if (rc != ALJABR_ROCM_OK) return rc;
     return finish_launch("ffn_gated_fused");
 }

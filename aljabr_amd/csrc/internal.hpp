@@ -43,6 +43,10 @@ void *stream_scratch(size_t bytes, int slot = 0);
 // Number of compute units of the initialised device (for grid sizing).
 int device_cu_count();
 
+// Frees the registered whole-step decode model (KV caches, uploads,
+// activations); called by aljabr_rocm_shutdown.
+void step_state_release();
+
 inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // log2 of a power of two, -1 for anything else.

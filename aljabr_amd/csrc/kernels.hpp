@@ -116,6 +116,7 @@ constexpr int kRowsStore = 0;    // y = W x'
 constexpr int kRowsAdd = 1;      // y += W x' (residual; no norm prologue)
 constexpr int kRowsSwiGLU = 2;   // outs = {gate, up}: outs[0].y = silu(Wg x') * (Wu x')
 constexpr int kRowsRopeKV = 3;   // outs = {q, k, v}: q rotated into outs[0].y; k rotated and v appended to the caches
+constexpr int kRowsGeGLU = 4;    // as kRowsSwiGLU with the Metal FFN's tanh GELU: gelu(Wg x') * (Wu x')
 // Batch-1 NF4 matvec of up to three matrices sharing K and the activations
 // (stacked rows, one launch). x' = RMSNorm(x) with weight norm_w when norm_w
 // is non-null (over the K elements), else x. Same shape limits as
@@ -167,6 +168,15 @@ int enqueue_rmsnorm(float *out, const float *x, const float *w, int rows, int le
 int enqueue_rope(float *x, const int *pos, int rows, int n_heads, int head_dim, float base);
 int enqueue_swiglu(float *dst, const float *gate, const float *up, long long n);
 int enqueue_add(float *a, const float *b, long long n);
+// out = act(gate) * up of the Metal FFN kernels (kind 2: tanh GELU, else
+// SiLU, with their cut-offs; a non-finite product becomes 0).
+int enqueue_gated_act(float *out, const float *gate, const float *up, long long n, int kind);
+// C_i[batch][N_i] = A[batch][K] . B_i^T for i < n (n <= 3) over any GGUF
+// weight types: matrices of one type share one stacked launch where the
+// shape allows (the batch-1 rows kernel, the matrix-core GEMM at batch >= 2),
+// else one launch each.
+int enqueue_matmul_multi(float *const *C, const float *A, const uint8_t *const *B, int K, const int *N,
+                         const int *type, int n, int batch);
 int enqueue_argmax(int *out, const float *x, int rows, int cols);
 int enqueue_embed(float *x, const float *embed, const int *tokens, int batch, int dim, int vocab);
 // x[b] = row tokens[b] of a [vocab][dim] table of type F32, F16, Q4_0, Q8_0,

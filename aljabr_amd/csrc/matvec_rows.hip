@@ -130,6 +130,7 @@ struct RowsArgs {
     float rope_base;
     const float2 *rope_cs;   // [cap][D/2] cos/sin table, or null
     int N, K, bs_shift, S, G;
+    int gelu;                // kESwiGLU: the tanh GELU of the Metal FFN instead of SiLU
 };
 
 // Segment of stacked row r and its row within the segment. The row map
@@ -379,6 +380,17 @@ __device__ __forceinline__ float silu_ref(float g) {
     return g / (1.0f + static_cast<float>(exp(-static_cast<double>(g))));
 }
 
+// GELU(g) * u of the Metal FFN (MTLC/aljabr_metal_kernel_source.m:91-108):
+// tanh GELU, 0 at or below -10 and g at or above 10; a non-finite product is 0.
+__device__ __forceinline__ float geglu_metal(float g, float u) {
+    float act;
+    if (g <= -10.0f) act = 0.0f;
+    else if (g >= 10.0f) act = g;
+    else act = 0.5f * g * (1.0f + tanhf(0.79788456f * (g + 0.044715f * g * g * g)));
+    const float y = act * u;
+    return isfinite(y) ? y : 0.0f;
+}
+
 // Split-half RoPE of the pair (i, i + D/2) at position `pos`, the same
 // arithmetic as the stand-alone RoPE kernel (GGUFVectorOps.rope :383-440).
 __device__ __forceinline__ void rope_rotate(float &x0, float &x1, const float2 *table, int cap, int pos, int i,
@@ -550,7 +562,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
             if (lane < T / 2) {
                 float u = 0.0f;
                 for (int c = 0; c < S; ++c) u += part[grp * S + c][lane + T / 2];
-                a.seg[0].y[row_ref<EPI, T>(a, r).local] = silu_ref(v) * u;
+                a.seg[0].y[row_ref<EPI, T>(a, r).local] = a.gelu ? geglu_metal(v, u) : silu_ref(v) * u;
             }
         } else if ((lane & 1) == 0) {
             // RoPE pairs (r, r + 1): T is even and row0 even, so both are this
@@ -899,7 +911,9 @@ int launch_fused(RowsArgs &args, int T, int epilogue, bool norm, hipStream_t s) 
         launch_rows<FMT, kXPlain, kEAdd>(args, T, s);
         return ALJABR_ROCM_OK;
     case kRowsSwiGLU:
+    case kRowsGeGLU:
         if (!norm) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        args.gelu = epilogue == kRowsGeGLU;
         launch_rows<FMT, kXNorm, kESwiGLU>(args, T, s);
         return ALJABR_ROCM_OK;
     default:
@@ -925,7 +939,7 @@ int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, 
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     if (norm_w && !aligned(norm_w, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     RowsArgs args{};
-    if (epilogue == kRowsSwiGLU) {
+    if (epilogue == kRowsSwiGLU || epilogue == kRowsGeGLU) {
         // gate (segment 0) and up (segment 1) interleaved row by row.
         if (nseg != 2 || outs[0].n != outs[1].n) return ALJABR_ROCM_ERR_UNSUPPORTED;
     } else if (epilogue == kRowsRopeKV) {
@@ -977,7 +991,7 @@ int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, 
     args.S = K / kChunk;
     int T = pick_rows_t(args.N, args.S, 32);
     if (T & 1) ++T;                              // the paired epilogues need both rows of a pair in one wave
-    if (epilogue == kRowsSwiGLU && (outs[0].n % (T / 2)) != 0)
+    if ((epilogue == kRowsSwiGLU || epilogue == kRowsGeGLU) && (outs[0].n % (T / 2)) != 0)
         return ALJABR_ROCM_ERR_UNSUPPORTED;      // every wave's gate run must be whole
     hipStream_t s = current_stream();
     const bool norm = norm_w != nullptr;

@@ -216,6 +216,9 @@ int aljabr_rocm_is_initialized(void) { return ctx().initialized.load() ? 1 : 0; 
 
 int aljabr_rocm_shutdown(void) {
     Context &c = ctx();
+    // The registered decode model's buffers first (its lock is taken before
+    // this context's by every path).
+    if (c.initialized.load()) step_state_release();
     std::lock_guard<std::mutex> lock(c.mu);
     if (!c.initialized.load()) return ALJABR_ROCM_OK;
     (void)hipSetDevice(c.device);

@@ -518,6 +518,120 @@ int aljabr_rocm_llama_hidden(aljabr_rocm_llama *model, void **hidden);
  * (the role of KVCacheSession's committed prefix, core/aljabr-core/.../cache/KVCacheSession.java:95-105). */
 int aljabr_rocm_llama_kv_cache(aljabr_rocm_llama *model, void **k_cache, void **v_cache);
 
+/* ======================================================================== */
+/* Registered whole-step decode and fused layers (the Metal ABI's            */
+/* MTLC/aljabr_metal_matvec_api.h:161-282, which the GGUF runner binds:      */
+/* GJB/GgufMetalDecodeRegistration.java:17-146, GgufDecodePass.java:124-245) */
+/* ======================================================================== */
+/*
+ * One process-wide model, as the reference keeps it: a KV cache, norm slots,
+ * per-layer weights and the output registered once, then one call per token.
+ * Calls are serialised and each is finished on the calling thread's stream
+ * before it returns. Every data pointer may be host or device memory: device
+ * weights and norms are used in place and must stay valid; host weights are
+ * uploaded on first use and cached by address until
+ * aljabr_rocm_reset_decode_state or aljabr_rocm_shutdown (do not change them
+ * in place); host norms are copied when registered; inputs are copied in and
+ * outputs copied back each call. Weight types: ALJABR_ROCM_TYPE_F32, F16,
+ * Q4_0, Q8_0, Q4_K, Q6_K (the reference also takes BF16; -3 here). Failures
+ * return the library's negative statuses (the reference's own negative codes
+ * differ per function; its callers test rc == 0 or rc >= 0).
+ */
+
+/* fp32 caches of nLayers layers, [maxSeq][layerStrides[l]] each, zeroed
+ * (aljabr_metal_init_kv_cache, MTLC/aljabr_metal_matvec_api.m:3282-3304).
+ * Up to 256 layers (the reference: 64). */
+int aljabr_rocm_init_kv_cache(int nLayers, int maxSeq, const int *layerStrides);
+/* Copies seqLen rows of a layer's K and/or V prefix (either may be NULL)
+ * into its cache (MTLC/aljabr_metal_matvec_api.m:3306-3316). */
+int aljabr_rocm_sync_kv_cache(int layer, int seqLen, const float *kData, const float *vData);
+/* Norm slot weights, every layer's row back to back: 0 post-attention, 1
+ * FFN, 2 post-FFN, 3 attention norm ([layers][dim]); 4 Q and 5 K head norms
+ * ([layers][max head_dim]) (MTLC/aljabr_metal_matvec_api.m:3318-3327). */
+int aljabr_rocm_register_norm_buffer(int slot, const void *ptr, size_t bytes);
+/* RoPE divisors of a layer: pair i's angle is divided by freqData[i] when it
+ * is positive (MTLC/aljabr_metal_matvec_api.m:3329-3346). */
+int aljabr_rocm_register_rope_freqs(int layer, const float *freqData, int freqLen);
+/* One decoder layer (MTLC/aljabr_metal_matvec_api.m:3348-3425): wK NULL
+ * shares the cache of the kvLayerIndex chain's first layer with K; wK
+ * without wV uses the raw K projection as V. n0 = wO_K = nH*headDim, n1 = n2
+ * = nKVH*headDim, wO_N the model width. attnScale <= 0: 1 with head norms,
+ * else 1/sqrt(headDim). outScale applies when positive and not 1. The decode
+ * step needs each layer's stride equal to nKVH*headDim (-3 otherwise). */
+int aljabr_rocm_register_decode_layer(int layer, int kvLayerIndex, const void *wQ, const void *wK, const void *wV,
+                                      const void *wO, const void *gate, const void *up, const void *down, int typeQ,
+                                      int typeK, int typeV, int typeWO, int typeGate, int typeUp, int typeDown, int n0,
+                                      int n1, int n2, int wO_K, int wO_N, int ffnDim, int nH, int nKVH, int headDim,
+                                      int stride, float freqBase, int isSwa, float outScale, float attnScale,
+                                      int hasPostAttnNorm, int hasPostFfnNorm, int hasQNorm, int hasKNorm,
+                                      int hasUnitVNorm);
+/* Output norm [outputK] and projection [outputN][outputK]; cap > 0 applies
+ * cap * tanh(logit / cap) (MTLC/aljabr_metal_matvec_api.m:3427-3455). */
+int aljabr_rocm_register_output(const float *outputNormW, const void *outputW, int typeOutputW, int outputK,
+                                int outputN, float cap);
+/* Token embedding [vocab = registered outputN][dim], rows multiplied by
+ * scale (MTLC/aljabr_metal_matvec_api.m:4090-4118; the reference decodes
+ * Q4_K only, this takes every weight type above). */
+int aljabr_rocm_register_token_embd(const void *embdW, int typeEmbdW, int dim, float scale);
+/* One token through every registered layer and the logits
+ * (aljabr_metal_decode_step, MTLC/aljabr_metal_matvec_api.m:3574-4083,
+ * :4121-4137): x_in [dim] is the layer-0 input; sliding-window layers see
+ * the last slidingWindow positions (<= 0: all). Writes logits_out [outputN]
+ * when not NULL and returns the greedy token (0 when no output is
+ * registered) or a negative status. The FFN activation is the reference
+ * step's tanh GELU unless aljabr_rocm_set_decode_activation says otherwise. */
+int aljabr_rocm_decode_step(int pos, int slidingWindow, float eps, const float *x_in, float *logits_out);
+/* The same from a token id through the registered embedding. */
+int aljabr_rocm_decode_step_token(int pos, int slidingWindow, float eps, int tokenId, float *logits_out);
+/* The FFN activation of the registered decode step and of nothing else: 2
+ * tanh GELU (the reference step's, the default), 1 SiLU. No counterpart in
+ * the reference, whose step always applies GELU (MTLC/aljabr_metal_matvec_api.m:
+ * 3902-3953); SiLU models (Llama) need it. */
+int aljabr_rocm_set_decode_activation(int activationKind);
+/* Forget the registered model and free everything it holds (caches, norm
+ * copies, uploads, activations). No counterpart in the reference, whose
+ * registry only grows. */
+int aljabr_rocm_reset_decode_state(void);
+/* x[wO_N] = layer residual: xb = wO . attn_full, optional post-attention
+ * norm, x += xb, FFN over ffnNorm(x) with activationKind (1 SiLU, 2 GELU),
+ * optional post-FFN norm, x += xb, x *= outScale; then, with hasNext and
+ * nextWQ, the next layer's attention norm and Q/K/V into nextQ/nextK/nextV
+ * (aljabr_metal_wo_ffn_next_qkv_fused, MTLC/aljabr_metal_matvec_api.m:
+ * 2198-2658). */
+int aljabr_rocm_wo_ffn_next_qkv_fused(float *x, const float *attn_full, const void *wO, int typeWO, int wO_K,
+                                      int wO_N, const float *postAttnW, int hasPostAttnNorm, const float *ffnNormW,
+                                      const float *postFfnW, int hasPostFfnNorm, float eps, float outScale,
+                                      const void *gateW, const void *upW, const void *downW, int typeGate, int typeUp,
+                                      int typeDown, int ffnDim, int activationKind, int hasNext,
+                                      const float *nextAttnNormW, float *nextQ, float *nextK, float *nextV,
+                                      const void *nextWQ, const void *nextWK, const void *nextWV, int nextTypeQ,
+                                      int nextTypeK, int nextTypeV, int nextN0, int nextN1, int nextN2);
+/* The layer alone, outScale 1; the addOne flags are ignored as the
+ * reference ignores them (MTLC/aljabr_metal_matvec_api.m:2660-2675). */
+int aljabr_rocm_wo_ffn_fused(float *x, const float *attn_full, const void *wO, int typeWO, int wO_K, int wO_N,
+                             const float *postAttnW, int hasPostAttnNorm, int addOnePostAttn, const float *ffnNormW,
+                             int addOneFfnNorm, const float *postFfnW, int hasPostFfnNorm, int addOnePostFfn, float eps,
+                             const void *gateW, const void *upW, const void *downW, int typeGate, int typeUp,
+                             int typeDown, int ffnDim, int activationKind);
+/* The last layer, then the output norm, logits [outputN] and softcap cap
+ * (outputK must equal wO_N); x gets the residual when not NULL
+ * (MTLC/aljabr_metal_matvec_api.m:2704-3145). */
+int aljabr_rocm_wo_ffn_logits_fused(float *x, const float *attn_full, const void *wO, int typeWO, int wO_K, int wO_N,
+                                    const float *postAttnW, int hasPostAttnNorm, const float *ffnNormW,
+                                    const float *postFfnW, int hasPostFfnNorm, float eps, float outScale,
+                                    const void *gateW, const void *upW, const void *downW, int typeGate, int typeUp,
+                                    int typeDown, int ffnDim, int activationKind, const float *outputNormW,
+                                    const void *outputW, int typeOutputW, int outputK, int outputN, float *logits,
+                                    float cap);
+/* A no-op: each call owns its residual (MTLC/aljabr_metal_matvec_api.m:2677). */
+void aljabr_rocm_wo_ffn_reset_x(void);
+/* The registered layer's wO + norms + FFN + residual + outScale for
+ * batchSize rows: x [batchSize][wO_N] in and out, attn_full
+ * [batchSize][wO_K] (aljabr_metal_wo_ffn_fused_layer_batch,
+ * MTLC/aljabr_metal_matvec_api.m:4202-4350). */
+int aljabr_rocm_wo_ffn_fused_layer_batch(float *x, const float *attn_full, int layer, int batchSize, float eps,
+                                         int activationKind);
+
 #ifdef __cplusplus
 }
 #endif

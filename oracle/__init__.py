@@ -91,6 +91,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "orc_decode_attention": (None, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F]),
         "orc_llama_decode": (_I32, [_P, _P, _I32, _I32, _P, _P, _P, _P, ctypes.c_int]),
         "orc_llama_decode_typed": (_I32, [_P, _P, _I32, _I32, _P, _P, _P, _P, ctypes.c_int]),
+        "orc_step_decode": (_I32, [_P, _I32, _I32, _F, _I32, _P, _P, _P, ctypes.c_int]),
         "orc_fill_normal": (None, [ctypes.c_uint64, _F, _F, _P, _I64]),
         "orc_fill_uniform_int": (None, [ctypes.c_uint64, _I32, _P, _I64]),
         "orc_max_threads": (ctypes.c_int, []),
@@ -514,3 +515,115 @@ class TypedLlamaOracle:
                                            _ptr(self.k_cache), _ptr(self.v_cache), _ptr(logits), _ptr(hidden),
                                            nthreads or threads())
         return int(nxt), logits, hidden
+
+
+# ---- Metal whole-step decode ----------------------------------------------
+
+class _StepLayer(ctypes.Structure):
+    _fields_ = [(n, _Tensor) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")] + \
+        [(n, _I32) for n in ("kv_layer", "n0", "n1", "n2", "wo_k", "wo_n", "ffn", "n_heads", "n_kv_heads",
+                             "head_dim")] + \
+        [("freq_base", _F), ("is_swa", _I32), ("out_scale", _F), ("attn_scale", _F)] + \
+        [(n, _I32) for n in ("has_post_attn_norm", "has_post_ffn_norm", "has_q_norm", "has_k_norm",
+                             "has_unit_v_norm")] + \
+        [("rope_freqs", _P), ("rope_freqs_len", _I32)]
+
+
+class _StepModel(ctypes.Structure):
+    _fields_ = [("layers", _I32), ("layer", ctypes.POINTER(_StepLayer)), ("norm", _P * 6),
+                ("k_cache", _P), ("v_cache", _P), ("kv_stride", _P), ("out_norm", _P), ("out_w", _Tensor),
+                ("out_k", _I32), ("out_n", _I32), ("cap", _F), ("embd", _Tensor), ("embd_rows", _I32),
+                ("embd_scale", _F), ("activation", _I32)]
+
+
+STEP_FLAGS = ("has_post_attn_norm", "has_post_ffn_norm", "has_q_norm", "has_k_norm", "has_unit_v_norm")
+
+
+class StepOracle:
+    """The Metal whole-step decode restated (orc_step_decode). ``model`` is a
+    dict: ``dim``, ``max_seq``, ``activation`` (1 SiLU, 2 GELU), ``layers``
+    (a list of dicts with (type, array) pairs for wq, wk, wv, wo, gate, up,
+    down -- wk / wv may be None --, kv_layer, n_heads, n_kv_heads, head_dim,
+    ffn, freq_base, is_swa, out_scale, attn_scale, the has_* flags and
+    rope_freqs (array or None)), ``norm`` (six flat fp32 arrays or None, the
+    norm slots), ``out_norm``, ``out_w`` ((type, array) or None), ``vocab``,
+    ``cap``, ``embd`` ((type, array) or None) and ``embd_scale``."""
+
+    def __init__(self, model: dict):
+        self._keep = []
+        dim = model["dim"]
+        n = len(model["layers"])
+
+        def tensor(pair):
+            if pair is None:
+                return _Tensor(None, None, 0, 0)
+            t, arr = pair
+            arr = np.ascontiguousarray(arr)
+            self._keep.append(arr)
+            return _Tensor(arr.ctypes.data, None, t, 0)
+
+        def keep(a, dtype=np.float32):
+            a = np.ascontiguousarray(a, dtype)
+            self._keep.append(a)
+            return a
+
+        layers = (_StepLayer * n)()
+        self.k_cache, self.v_cache, strides = [], [], []
+        for i, c in enumerate(model["layers"]):
+            L = layers[i]
+            for key in ("wq", "wk", "wv", "wo", "gate", "up", "down"):
+                setattr(L, key, tensor(c.get(key)))
+            nh, nkv, hd = c["n_heads"], c["n_kv_heads"], c["head_dim"]
+            L.kv_layer = c.get("kv_layer", i)
+            L.n0, L.n1, L.n2 = nh * hd, nkv * hd, nkv * hd
+            L.wo_k, L.wo_n, L.ffn = nh * hd, dim, c["ffn"]
+            L.n_heads, L.n_kv_heads, L.head_dim = nh, nkv, hd
+            L.freq_base = c.get("freq_base", 10000.0)
+            L.is_swa = int(c.get("is_swa", 0))
+            L.out_scale = c.get("out_scale", 1.0)
+            L.attn_scale = c.get("attn_scale", 0.0)
+            for f in STEP_FLAGS:
+                setattr(L, f, int(c.get(f, 0)))
+            if c.get("rope_freqs") is not None:
+                rf = keep(c["rope_freqs"])
+                L.rope_freqs, L.rope_freqs_len = rf.ctypes.data, rf.size
+            stride = nkv * hd
+            strides.append(stride)
+            kc = keep(np.zeros(model["max_seq"] * stride))
+            vc = keep(np.zeros(model["max_seq"] * stride))
+            self.k_cache.append(kc)
+            self.v_cache.append(vc)
+        self._keep.append(layers)
+        m = _StepModel()
+        m.layers = n
+        m.layer = layers
+        for slot in range(6):
+            arr = model["norm"][slot]
+            m.norm[slot] = keep(arr).ctypes.data if arr is not None else None
+        kp = (_P * n)(*[a.ctypes.data for a in self.k_cache])
+        vp = (_P * n)(*[a.ctypes.data for a in self.v_cache])
+        st = (_I32 * n)(*strides)
+        self._keep += [kp, vp, st]
+        m.k_cache, m.v_cache, m.kv_stride = ctypes.addressof(kp), ctypes.addressof(vp), ctypes.addressof(st)
+        if model.get("out_w") is not None:
+            m.out_norm = keep(model["out_norm"]).ctypes.data
+            m.out_w = tensor(model["out_w"])
+            m.out_k, m.out_n = dim, model["vocab"]
+        m.cap = model.get("cap", 0.0)
+        m.embd = tensor(model.get("embd"))
+        m.embd_rows = model.get("vocab", 0)
+        m.embd_scale = model.get("embd_scale", 1.0)
+        m.activation = model.get("activation", 2)
+        self.model = m
+        self.dim, self.vocab = dim, model.get("vocab", 0)
+
+    def decode(self, pos: int, window: int = 0, eps: float = 1e-6, token: int = -1, x_in=None,
+               nthreads: int | None = None):
+        """One position: returns (status or greedy token, residual x, logits)."""
+        x = np.empty(self.dim, np.float32)
+        logits = np.zeros(max(self.vocab, 1), np.float32)
+        xin = np.ascontiguousarray(x_in, np.float32) if x_in is not None else None
+        rc = lib().orc_step_decode(ctypes.byref(self.model), pos, window, eps, token,
+                                   xin.ctypes.data if xin is not None else None, _ptr(x), _ptr(logits),
+                                   nthreads or threads())
+        return int(rc), x, logits

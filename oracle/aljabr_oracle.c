@@ -1016,6 +1016,170 @@ int32_t orc_llama_decode(const orc_llama_cfg *cfg, const orc_llama_weights *w,
     return r;
 }
 
+/* ------------------------------------------------------------------------ */
+/* Metal whole-step decode (registered layers)                               */
+/* ------------------------------------------------------------------------ */
+
+/* act(gate) * up of the Metal FFN kernels (MTLC/aljabr_metal_kernel_source.m:
+ * 72-108): SiLU g / (1 + e^-g) with 0 at or below -20 and g at or above 20,
+ * or for kind 2 the tanh GELU with 0 at or below -10 and g at or above 10; a
+ * non-finite product becomes 0. */
+static void metal_gated_act(const float *gate, const float *up, float *out, int32_t n, int32_t kind) {
+    for (int32_t i = 0; i < n; i++) {
+        const float g = gate[i];
+        float act;
+        if (kind == 2) {
+            if (g <= -10.0f) act = 0.0f;
+            else if (g >= 10.0f) act = g;
+            else act = 0.5f * g * (1.0f + (float)tanh((double)(0.79788456f * (g + 0.044715f * g * g * g))));
+        } else {
+            if (g <= -20.0f) act = 0.0f;
+            else if (g >= 20.0f) act = g;
+            else act = g / (1.0f + (float)exp(-(double)g));
+        }
+        const float y = act * up[i];
+        out[i] = isfinite(y) ? y : 0.0f;
+    }
+}
+
+/* rows of `len`: x * 1/sqrt(mean(x^2) + eps) (* w when w is not NULL), the
+ * Metal rmsnorm_rows / rmsnorm_unit_rows kernels (MTLC/aljabr_metal_kernel_
+ * source.m:482-547) with addOne = 0. */
+static void metal_norm_rows(float *x, const float *w, int32_t rows, int32_t len, float eps) {
+    for (int32_t r = 0; r < rows; r++) {
+        float *p = x + (int64_t)r * len;
+        double ss = 0.0;
+        for (int32_t i = 0; i < len; i++) ss += (double)p[i] * p[i];
+        const float inv = (float)(1.0 / sqrt(ss / len + eps));
+        for (int32_t i = 0; i < len; i++) p[i] = w ? (p[i] * inv) * w[i] : p[i] * inv;
+    }
+}
+
+/* Split-half RoPE of `heads` rows at `pos`: freq = base^(-2i/D), theta =
+ * pos * freq / ff with ff = factors[i] when that is positive (the
+ * rope_freqs divisors) else 1; MTLC/aljabr_metal_kernel_source.m:845-884. */
+static void metal_rope(float *x, int32_t heads, int32_t hd, int32_t pos, float base, const float *factors,
+                       int32_t nfactors) {
+    const int32_t half = hd / 2;
+    for (int32_t i = 0; i < half; i++) {
+        const double freq = 1.0 / pow((double)base, 2.0 * i / (double)hd);
+        const float ff = (factors && i < nfactors) ? factors[i] : 1.0f;
+        const double theta = (double)pos * freq / (ff > 0.0f ? (double)ff : 1.0);
+        const float c = (float)cos(theta), s = (float)sin(theta);
+        for (int32_t h = 0; h < heads; h++) {
+            float *p = x + (int64_t)h * hd;
+            const float x0 = p[i], x1 = p[i + half];
+            p[i] = x0 * c - x1 * s;
+            p[i + half] = x0 * s + x1 * c;
+        }
+    }
+}
+
+static int tensor_present(const orc_tensor *t) { return t->data != NULL; }
+
+/* MTLC/aljabr_metal_matvec_api.m:3222-3266 (KV owner resolution) and
+ * :3574-4083 (aljabr_metal_decode_step_internal), one position: */
+int32_t orc_step_decode(const orc_step_model *m, int32_t pos, int32_t window, float eps, int32_t token,
+                        const float *x_in, float *x, float *logits, int threads) {
+    if (m->layers <= 0) return -1;
+    const orc_step_layer *L0 = &m->layer[0];
+    const int32_t dim = L0->wo_n;
+    int32_t max_q = 0, max_kv = 0, max_att = 0, max_ffn = 0, max_hd = 0;
+    for (int32_t l = 0; l < m->layers; l++) {
+        const orc_step_layer *c = &m->layer[l];
+        if (c->n0 > max_q) max_q = c->n0;
+        if (c->n1 > max_kv) max_kv = c->n1;
+        if (c->n2 > max_kv) max_kv = c->n2;
+        if (c->wo_k > max_att) max_att = c->wo_k;
+        if (c->ffn > max_ffn) max_ffn = c->ffn;
+        if (c->head_dim > max_hd) max_hd = c->head_dim;
+    }
+    if (!m->norm[1] || !m->norm[3]) return -3;            /* ffn and attn norms are required */
+    /* the input: an embedding row (decode_step_token) or x_in */
+    if (token >= 0) {
+        if (!tensor_present(&m->embd) || token >= m->embd_rows) return -6;
+        typed_row(&m->embd, token, dim, x);
+        if (m->embd_scale != 1.0f)
+            for (int32_t i = 0; i < dim; i++) x[i] *= m->embd_scale;
+    } else {
+        if (!x_in) return -5;
+        memcpy(x, x_in, (size_t)dim * 4);
+    }
+    float *xb = (float *)calloc((size_t)(dim > max_att ? dim : max_att), 4);
+    float *q = (float *)calloc((size_t)max_q + 1, 4), *kk = (float *)calloc((size_t)max_kv + 1, 4);
+    float *vv = (float *)calloc((size_t)max_kv + 1, 4), *att = (float *)calloc((size_t)max_att + 1, 4);
+    float *scores = (float *)calloc((size_t)pos + 1, 4), *gate = (float *)calloc((size_t)max_ffn, 4);
+    float *up = (float *)calloc((size_t)max_ffn, 4), *hb = (float *)calloc((size_t)max_ffn, 4);
+    int32_t rc = 0;
+    for (int32_t l = 0; l < m->layers && rc == 0; l++) {
+        const orc_step_layer *c = &m->layer[l];
+        const int32_t hd = c->head_dim;
+        const int has_k = tensor_present(&c->wk), has_v = tensor_present(&c->wv);
+        orc_rmsnorm(x, m->norm[3] + (int64_t)l * dim, xb, dim, eps);          /* attn norm, slot 3 */
+        typed_mv(&c->wq, xb, c->n0, dim, q, threads);
+        if (has_k) typed_mv(&c->wk, xb, c->n1, dim, kk, threads);
+        if (has_v) typed_mv(&c->wv, xb, c->n2, dim, vv, threads);
+        if (has_k && !has_v) {                                              /* K as V: the raw projection */
+            if (c->n1 <= 0 || c->n1 != c->n2) { rc = -6; break; }
+            memcpy(vv, kk, (size_t)c->n1 * 4);
+        }
+        if (c->has_q_norm && m->norm[4]) metal_norm_rows(q, m->norm[4] + (int64_t)l * max_hd, c->n_heads, hd, eps);
+        if (c->has_k_norm && m->norm[5] && has_k)
+            metal_norm_rows(kk, m->norm[5] + (int64_t)l * max_hd, c->n_kv_heads, hd, eps);
+        if (c->has_unit_v_norm && (has_k || has_v)) metal_norm_rows(vv, NULL, c->n_kv_heads, hd, eps);
+        metal_rope(q, c->n_heads, hd, pos, c->freq_base, c->rope_freqs, c->rope_freqs_len);
+        if (has_k) metal_rope(kk, c->n_kv_heads, hd, pos, c->freq_base, c->rope_freqs, c->rope_freqs_len);
+        if (has_k && m->k_cache[l] && m->v_cache[l]) {                     /* this layer owns a cache */
+            const int32_t kvw = c->n_kv_heads * hd;                       /* stride >= kvw */
+            memcpy(m->k_cache[l] + (int64_t)pos * m->kv_stride[l], kk, (size_t)kvw * 4);
+            memcpy(m->v_cache[l] + (int64_t)pos * m->kv_stride[l], vv, (size_t)kvw * 4);
+        }
+        /* the KV owner: follow kv_layer links to a layer with a K projection */
+        int32_t owner = c->kv_layer, hops = 0;
+        while (owner >= 0 && owner < m->layers && hops++ < m->layers) {
+            const orc_step_layer *cand = &m->layer[owner];
+            if (tensor_present(&cand->wk) || cand->kv_layer == owner) break;
+            owner = cand->kv_layer;
+        }
+        if (owner < 0 || owner >= m->layers || !m->k_cache[owner] || !m->v_cache[owner] ||
+            !tensor_present(&m->layer[owner].wk)) { rc = -4; break; }
+        const orc_step_layer *oc = &m->layer[owner];
+        if (oc->head_dim != hd || oc->n_kv_heads != c->n_kv_heads || m->kv_stride[owner] < c->n_kv_heads * hd) {
+            rc = -5;
+            break;
+        }
+        const int32_t seq = pos + 1;
+        const int32_t start = (c->is_swa && window > 0 && seq > window) ? seq - window : 0;
+        float scale = c->attn_scale;
+        if (scale <= 0.0f) scale = (c->has_q_norm || c->has_k_norm) ? 1.0f : (float)(1.0 / sqrt((double)hd));
+        orc_decode_attention(q, att, scores, m->k_cache[owner], m->v_cache[owner], m->kv_stride[owner],
+                             oc->n_kv_heads, c->n_heads, hd, seq, start, scale);
+        typed_mv(&c->wo, att, dim, c->wo_k, xb, threads);
+        if (c->has_post_attn_norm && m->norm[0]) metal_norm_rows(xb, m->norm[0] + (int64_t)l * dim, 1, dim, eps);
+        for (int32_t i = 0; i < dim; i++) x[i] += xb[i];
+        orc_rmsnorm(x, m->norm[1] + (int64_t)l * dim, xb, dim, eps);           /* ffn norm, slot 1 */
+        typed_mv(&c->gate, xb, c->ffn, dim, gate, threads);
+        typed_mv(&c->up, xb, c->ffn, dim, up, threads);
+        metal_gated_act(gate, up, hb, c->ffn, m->activation);
+        typed_mv(&c->down, hb, dim, c->ffn, xb, threads);
+        if (c->has_post_ffn_norm && m->norm[2]) metal_norm_rows(xb, m->norm[2] + (int64_t)l * dim, 1, dim, eps);
+        const int scale_out = c->out_scale > 0.0f && c->out_scale != 1.0f;
+        for (int32_t i = 0; i < dim; i++) {
+            const float v = x[i] + xb[i];
+            x[i] = scale_out ? v * c->out_scale : v;
+        }
+    }
+    int32_t best = 0;
+    if (rc == 0 && tensor_present(&m->out_w) && m->out_norm) {
+        orc_rmsnorm(x, m->out_norm, xb, m->out_k, eps);
+        typed_mv(&m->out_w, xb, m->out_n, m->out_k, logits, threads);
+        if (m->cap > 0.0f) orc_softcap(logits, m->out_n, m->cap);
+        for (int32_t i = 1; i < m->out_n; i++) if (logits[i] > logits[best]) best = i;
+    }
+    free(xb); free(q); free(kk); free(vv); free(att); free(scores); free(gate); free(up); free(hb);
+    return rc ? rc : best;
+}
+
 float orc_round_f16(float v) {
     uint32_t b = f32_to_bits(v);
     uint32_t sign = b & 0x80000000u;

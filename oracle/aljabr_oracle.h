@@ -232,6 +232,64 @@ int32_t orc_llama_decode_typed(const orc_llama_cfg *cfg, const orc_llama_typed *
                                float *v_cache, float *logits, float *hidden,
                                int threads);
 
+/* ---- Metal whole-step decode (registered layers) ------------------------ */
+
+/* One layer as aljabr_metal_register_decode_layer records it
+ * (MTLC/aljabr_metal_matvec_api.m:3348-3425): absent wk / wv have data NULL
+ * (a layer without wk attends to the cache of its kv_layer chain's owner;
+ * wk without wv uses the raw K projection as V); rope_freqs NULL: no
+ * frequency divisors. */
+typedef struct orc_step_layer {
+    orc_tensor wq, wk, wv, wo, gate, up, down;
+    int32_t kv_layer, n0, n1, n2, wo_k, wo_n, ffn, n_heads, n_kv_heads, head_dim;
+    float freq_base;
+    int32_t is_swa;
+    float out_scale, attn_scale;
+    int32_t has_post_attn_norm, has_post_ffn_norm, has_q_norm, has_k_norm, has_unit_v_norm;
+    const float *rope_freqs;
+    int32_t rope_freqs_len;
+} orc_step_layer;
+
+/* The registered model: norm slots as aljabr_metal_register_norm_buffer
+ * takes them (0 post-attention, 1 FFN, 2 post-FFN, 3 attention norm, each
+ * [layers][dim]; 4 Q and 5 K head norms [layers][max head_dim]; NULL: not
+ * registered), fp32 KV caches per layer [max_seq][kv_stride[l]] (NULL:
+ * none), the output norm and projection (out_w.data NULL: no logits) with
+ * softcap `cap` (<= 0: none), the token embedding (embd_rows rows of the
+ * model width, multiplied by embd_scale) and the FFN activation kind (1
+ * SiLU, 2 tanh GELU). */
+typedef struct orc_step_model {
+    int32_t layers;
+    const orc_step_layer *layer;
+    const float *norm[6];
+    float *const *k_cache, *const *v_cache;
+    const int32_t *kv_stride;
+    const float *out_norm;
+    orc_tensor out_w;
+    int32_t out_k, out_n;
+    float cap;
+    orc_tensor embd;
+    int32_t embd_rows;
+    float embd_scale;
+    int32_t activation;
+} orc_step_model;
+
+/* aljabr_metal_decode_step / _token at one position
+ * (MTLC/aljabr_metal_matvec_api.m:3574-4083): x = x_in (token < 0) or the
+ * embedding row of `token`; per layer attention norm, Q/K/V, K-as-V copy,
+ * Q/K head norms, unit V norm, RoPE with divisors, cache store, attention over
+ * the owner's cache (sliding window on SWA layers, scale attn_scale or 1 with
+ * head norms or 1/sqrt(D)), Wo, post-attention norm, residual, FFN norm,
+ * gated FFN, post-FFN norm, residual and output scale; then output norm,
+ * logits and softcap. Writes the final residual to x[dim] and logits[out_n];
+ * returns the greedy token, or the reference's negative codes (-3 required
+ * norms missing, -4 no KV owner, -5 KV geometry mismatch, -6 bad K-as-V or
+ * token). Pinned by tests/test_oracle_step.py: equal to orc_llama_decode_typed
+ * with the Gemma features off, and to an independent full-sequence numpy
+ * forward with every feature on, with planted mistakes caught. */
+int32_t orc_step_decode(const orc_step_model *m, int32_t pos, int32_t window, float eps, int32_t token,
+                        const float *x_in, float *x, float *logits, int threads);
+
 /* binary32 -> binary16 -> binary32 with round-to-nearest-even (IEEE). */
 float orc_round_f16(float v);
 
