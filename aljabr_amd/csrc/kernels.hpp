@@ -157,14 +157,7 @@ int enqueue_gguf_stream(float *C, const float *A, const uint8_t *B, int K, int N
 int enqueue_nf4_small(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M);
 int enqueue_gguf_small(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M);
 
-// Buffers (null entries skipped) that a kernel clears as a side job.
-struct ZeroList {
-    float *p[3];
-    long long n[3];
-};
-
-int enqueue_rmsnorm(float *out, const float *x, const float *w, int rows, int len, float eps,
-                    const ZeroList *zero = nullptr);
+int enqueue_rmsnorm(float *out, const float *x, const float *w, int rows, int len, float eps);
 int enqueue_rope(float *x, const int *pos, int rows, int n_heads, int head_dim, float base);
 int enqueue_swiglu(float *dst, const float *gate, const float *up, long long n);
 int enqueue_add(float *a, const float *b, long long n);

@@ -842,9 +842,9 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         for (int b = 0; b < B; ++b) keys += std::min(host_pos[b] + 1, c.max_seq);
     using T = aljabr_rocm_llama::T;
     // y = x . W^T or, with `residual`, y += x . W^T for B rows. NF4 and the
-    // GGUF block formats on the matrix cores accumulate into y (which the caller has
-    // cleared, or which holds the residual); otherwise y is written, or the
-    // products go to `tmp` and one add follows.
+    // GGUF block formats on the matrix cores add into y themselves when it
+    // holds the residual; otherwise y is written, or the products go to `tmp`
+    // and one add follows.
     auto mm = [&](float *y, const float *x, const T &t, int K, int N, bool residual, float *tmp) -> int {
         if (t.type == ALJABR_ROCM_TYPE_NF4 && B >= 2 && shift >= 0 && m->all_nf4) {
             const int r = enqueue_nf4_mfma(y, x, t.w, t.s, K, N, shift, B, residual, m->mm_part,
@@ -871,7 +871,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             if (kquant_mfma_type(ts[i]->type) && B >= 2 && B <= kquant_mfma_max_m(ts[i]->type)) {
                 KqOut o[3];
                 for (int k = i; k < j; ++k) o[k - i] = KqOut{ys[k], ts[k]->w, ns[k]};
-                r = enqueue_kquant_mfma_multi(o, j - i, x, K, ts[i]->type, B, true, m->mm_part, m->mm_part_floats);
+                r = enqueue_kquant_mfma_multi(o, j - i, x, K, ts[i]->type, B, false, m->mm_part, m->mm_part_floats);
             }
             if (r == ALJABR_ROCM_ERR_UNSUPPORTED) {
                 for (int k = i; k < j; ++k) {
@@ -942,14 +942,9 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                      weight_bytes(tq, qd, dim, bs) + weight_bytes(tk, kvd, dim, bs) + weight_bytes(tv, kvd, dim, bs) +
                          (2.0 * dim + qd) * f4 + 2.0 * kvd * 2.0);
         } else {
-            // The NF4 matrix-core GEMMs write their outputs; the K-quant ones
-            // add into them, so for those the RMSNorm launch clears them.
-            const ZeroList z{{m->q, m->k, m->v},
-                             {static_cast<long long>(B) * qd, static_cast<long long>(B) * kvd,
-                              static_cast<long long>(B) * kvd}};
-            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, attn_norm, B, dim, c.eps, m->all_nf4 ? nullptr : &z));
-            if (m->all_nf4) ALJ_MARK("rmsnorm", (B * 2.0 * dim + dim) * f4);
-            else ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * (qd + 2.0 * kvd)) * f4);
+            // Every GEMM below writes its outputs (none accumulates into them).
+            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, attn_norm, B, dim, c.eps));
+            ALJ_MARK("rmsnorm", (B * 2.0 * dim + dim) * f4);
             // Q, K and V in one matrix-core launch where the shapes allow.
             const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq), qd},
                                     {m->k, W(m->wk), S(m->wk), kvd},
@@ -965,8 +960,8 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }
-            ALJ_MARK("qkv_gemm", mm_bytes(m->wq[l], qd, dim, true) + mm_bytes(m->wk[l], kvd, dim, true) +
-                                     mm_bytes(m->wv[l], kvd, dim, true) - 2.0 * B * dim * f4);
+            ALJ_MARK("qkv_gemm", mm_bytes(m->wq[l], qd, dim, false) + mm_bytes(m->wk[l], kvd, dim, false) +
+                                     mm_bytes(m->wv[l], kvd, dim, false) - 2.0 * B * dim * f4);
         }
         if (!fused1) {
             rc = enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base, m->rope_cs);
@@ -1030,11 +1025,8 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             ALJ_TRY(enqueue_rows_fused(m->w_down[l].type, &d, 1, m->hb, nullptr, 0.0f, ffn, shift, kRowsAdd));
             ALJ_MARK("down_rows_add", mm_bytes(m->w_down[l], dim, ffn, true));
         } else {
-            const ZeroList z{{m->gate, m->up, nullptr},
-                             {static_cast<long long>(B) * ffn, static_cast<long long>(B) * ffn, 0}};
-            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, ffn_norm, B, dim, c.eps, m->all_nf4 ? nullptr : &z));
-            if (m->all_nf4) ALJ_MARK("rmsnorm", (B * 2.0 * dim + dim) * f4);
-            else ALJ_MARK("rmsnorm_clear", (B * 2.0 * dim + dim + B * 2.0 * ffn) * f4);
+            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, ffn_norm, B, dim, c.eps));
+            ALJ_MARK("rmsnorm", (B * 2.0 * dim + dim) * f4);
             const RowsOut gu[2] = {{m->gate, W(m->w_gate), S(m->w_gate), ffn},
                                    {m->up, W(m->w_up), S(m->w_up), ffn}};
             rc = m->all_nf4 && B >= 2 ? enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, false, m->mm_part,
@@ -1048,7 +1040,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }
-            ALJ_MARK("gate_up_gemm", mm_bytes(m->w_gate[l], ffn, dim, true) + mm_bytes(m->w_up[l], ffn, dim, true) -
+            ALJ_MARK("gate_up_gemm", mm_bytes(m->w_gate[l], ffn, dim, false) + mm_bytes(m->w_up[l], ffn, dim, false) -
                                          B * dim * f4);
             ALJ_TRY(enqueue_swiglu(m->hb, m->gate, m->up, static_cast<long long>(B) * ffn));
             ALJ_MARK("swiglu", B * 3.0 * ffn * f4);

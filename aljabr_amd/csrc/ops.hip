@@ -31,32 +31,9 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 
 // One workgroup per row. With len % 4 == 0 and 16-byte aligned rows every
 // thread issues its float4 loads back to back (four in flight) instead of one
-// dependent scalar load per trip. The workgroups also clear up to three
-// buffers (`zero`) for outputs that the next kernels accumulate into.
-__device__ __forceinline__ void zero_side_job(const ZeroList &zero) {
-    const long long gtid = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
-    const long long gsize = static_cast<long long>(gridDim.x) * kThreads;
-#pragma unroll
-    for (int b = 0; b < 3; ++b) {
-        float *p = zero.p[b];
-        if (!p) continue;
-        const long long n = zero.n[b];
-        if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
-            float4 *p4 = reinterpret_cast<float4 *>(p);
-            for (long long i = gtid; i < n / 4; i += gsize) p4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            for (long long i = (n / 4) * 4 + gtid; i < n; i += gsize) p[i] = 0.0f;
-        } else {
-            for (long long i = gtid; i < n; i += gsize) p[i] = 0.0f;
-        }
-    }
-}
-
-// Workgroups [0, rows) normalise one row each; workgroups beyond `rows` only
-// help with the clearing.
+// dependent scalar load per trip.
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(float *__restrict__ out, const float *__restrict__ x,
-                                                           const float *__restrict__ w, int rows, int len, float eps,
-                                                           ZeroList zero) {
-    zero_side_job(zero);
+                                                           const float *__restrict__ w, int rows, int len, float eps) {
     if (static_cast<int>(blockIdx.x) >= rows) return;
     __shared__ float red[kThreads / 64];
     const float *xr = x + static_cast<long long>(blockIdx.x) * len;
@@ -339,17 +316,8 @@ inline unsigned blocks_for(long long n) { return static_cast<unsigned>((n + kThr
 
 }  // namespace
 
-int enqueue_rmsnorm(float *out, const float *x, const float *w, int rows, int len, float eps, const ZeroList *zero) {
-    ZeroList z{};
-    long long zn = 0;
-    if (zero) {
-        z = *zero;
-        for (int b = 0; b < 3; ++b) zn += z.p[b] ? z.n[b] : 0;
-    }
-    // About 16 float4 stores per thread for the clearing.
-    const long long extra = (zn + 16LL * 4 * kThreads - 1) / (16LL * 4 * kThreads);
-    const unsigned grid = static_cast<unsigned>(rows + (extra > 1024 ? 1024 : extra));
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(grid), dim3(kThreads), 0, current_stream(), out, x, w, rows, len, eps, z);
+int enqueue_rmsnorm(float *out, const float *x, const float *w, int rows, int len, float eps) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, current_stream(), out, x, w, rows, len, eps);
     return ALJABR_ROCM_OK;
 }
 
