@@ -78,6 +78,7 @@ struct KqArgs {
     int M, N, K;   // N: stacked rows
     int add;       // one K slice: Y += instead of Y =
     float *part;   // several K slices: [slice][M][N] partial sums
+    int groups, slices;   // row groups (kRowsPerWg * NT rows each) and K slices of the launch
 };
 
 // The segment of the tile starting at stacked row r0.
@@ -261,7 +262,28 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
     const int h = lane >> 5;
     const int nl = lane & 31;
     uint8_t *st = stage_base + wave * (32 * G::STR);
-    const int ks0 = blockIdx.y * KS;
+    // XCD-aware order: workgroup L runs on XCD L % 8. A 512-element unit of
+    // these formats is not a whole number of 128-byte lines, so neighbouring
+    // K slices of a row read the line between them, and on two XCDs it came
+    // from HBM twice (1.3-1.5x the weight bytes measured). When the row-group
+    // count is a multiple of 8, slice-major order already keeps a row group
+    // on one XCD; otherwise XCD x takes the contiguous run [x * per,
+    // (x + 1) * per) of the (row group, slice) items in row-major order.
+    const int L = static_cast<int>(blockIdx.x);
+    const int total = a.groups * a.slices;
+    int rgrp, slice;
+    if ((a.groups & 7) == 0) {
+        if (L >= total) return;
+        slice = L / a.groups;
+        rgrp = L - slice * a.groups;
+    } else {
+        const int per = (total + 7) / 8;
+        const int item = (L & 7) * per + (L >> 3);
+        if (item >= total) return;
+        rgrp = item / a.slices;
+        slice = item - rgrp * a.slices;
+    }
+    const int ks0 = slice * KS;
 
     // Activation slice -> split fp16 rows (rows >= M zero); Q4_K also the
     // split sums of each 32-element sub-block.
@@ -298,7 +320,7 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
     constexpr int W = 2;
     KqTile tr[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) tr[t] = kq_tile(a, blockIdx.x * (kRowsPerWg * NT) + t * kRowsPerWg + wave * 32);
+    for (int t = 0; t < NT; ++t) tr[t] = kq_tile(a, rgrp * (kRowsPerWg * NT) + t * kRowsPerWg + wave * 32);
     u32x4 qc[U][G::LOADS];
 #pragma unroll
     for (int u = 0; u < W && u < U; ++u) issue_unit<F>(qc[u], a, tr[u / SBS], ks0 / 256 + u % SBS, lane);
@@ -449,7 +471,7 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
         if (sbl == SBS - 1) {
             const int n = tr[t].local0 + nl;
             if (n < tr[t].n) {
-                if (gridDim.y == 1) {
+                if (a.slices == 1) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int m = 8 * (r >> 2) + 4 * h + (r & 3);
@@ -461,7 +483,7 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
                 } else {
                     // This slice's partial tile; the slice sum adds the
                     // slices in order.
-                    float *ps = a.part + static_cast<size_t>(blockIdx.y) * a.M * a.N + blockIdx.x * (kRowsPerWg * NT) +
+                    float *ps = a.part + static_cast<size_t>(slice) * a.M * a.N + rgrp * (kRowsPerWg * NT) +
                                 t * kRowsPerWg + wave * 32 + nl;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
@@ -483,8 +505,12 @@ void launch_kq(const KqArgs &args, hipStream_t s) {
         (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         lds_set = true;
     }
-    const dim3 grid((args.N + kRowsPerWg * NT - 1) / (kRowsPerWg * NT), args.K / KS), block(kThreads);
-    hipLaunchKernelGGL((kq_mm_kernel<F, KS, NT, MT>), grid, block, lds, s, args);
+    KqArgs a = args;
+    a.groups = (args.N + kRowsPerWg * NT - 1) / (kRowsPerWg * NT);
+    a.slices = args.K / KS;
+    const int total = a.groups * a.slices;
+    const int grid = (a.groups & 7) == 0 ? total : 8 * ((total + 7) / 8);
+    hipLaunchKernelGGL((kq_mm_kernel<F, KS, NT, MT>), dim3(grid), dim3(kThreads), lds, s, a);
 }
 
 template <int F, int MT>

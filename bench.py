@@ -64,6 +64,8 @@ def parse() -> argparse.Namespace:
                     help="run only the NF4 small-M GEMM measurement (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill attention measurement (for profiling)")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="run only the GQA decode attention measurement (for profiling)")
     return ap.parse_args()
 
 
@@ -578,6 +580,8 @@ def main() -> None:
             print(json.dumps({"small_m_gemm": small_m_bench(abi, torch, stream)}), flush=True)
         elif args.prefill_only:
             print(json.dumps({"prefill_attention": prefill_bench(abi, torch, stream)}), flush=True)
+        elif args.attention_only:
+            print(json.dumps({"attention": attention_bench(abi, torch, stream)}), flush=True)
         elif args.gguf_decode_only:
             print(json.dumps({"decode_gguf_q4_k_m": gguf_decode_runs(args, abi, torch, stream)}), flush=True)
         else:
