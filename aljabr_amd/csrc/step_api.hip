@@ -555,30 +555,38 @@ int decode_step_locked(State &st, int pos, int window, float eps, const float *x
         if (c.k_norm && c.k.w && (rc = slot_row(st, 5, l, st.max_hd, &kn))) return rc;
         if (!c.post_attn) post_attn = nullptr;
         if (!c.post_ffn) post_ffn = nullptr;
-        // Q, K, V from the attention-normed residual.
+        // Q, K, V from the attention-normed residual: the matrices of one
+        // type share a batch-1 rows launch with the RMSNorm as its prologue;
+        // shapes that launch cannot take go through the normed copy in xb.
         float *q = st.q.f(), *k = st.k.f(), *v = st.v.f();
-        const bool same = (!c.k.w || c.k.type == c.q.type) && (!c.v.w || c.v.type == c.q.type);
-        bool done = false;
-        if (same) {
-            RowsOut outs[3];
-            int n = 0;
-            outs[n++] = RowsOut{q, c.q.w, nullptr, c.n0};
-            if (c.k.w) outs[n++] = RowsOut{k, c.k.w, nullptr, c.n1};
-            if (c.v.w) outs[n++] = RowsOut{v, c.v.w, nullptr, c.n2};
-            rc = enqueue_rows_fused(c.q.type, outs, n, x, attn_norm, eps, dim, 0, kRowsStore);
-            if (rc == ALJABR_ROCM_OK) done = true;
-            else if (rc != ALJABR_ROCM_ERR_UNSUPPORTED) return rc;
-        }
-        if (!done) {
-            float *xb = st.xb.f();
-            if ((rc = enqueue_rmsnorm(xb, x, attn_norm, 1, dim, eps))) return rc;
-            float *ys[3];
-            const uint8_t *ws[3];
-            int ns[3], ts[3], n = 0;
-            ys[n] = q; ws[n] = c.q.w; ns[n] = c.n0; ts[n++] = c.q.type;
-            if (c.k.w) { ys[n] = k; ws[n] = c.k.w; ns[n] = c.n1; ts[n++] = c.k.type; }
-            if (c.v.w) { ys[n] = v; ws[n] = c.v.w; ns[n] = c.n2; ts[n++] = c.v.type; }
-            if ((rc = enqueue_matmul_multi(ys, xb, ws, dim, ns, ts, n, 1))) return rc;
+        {
+            const Mat mats[3] = {c.q, c.k, c.v};
+            float *const ys[3] = {q, k, v};
+            const int ns[3] = {c.n0, c.n1, c.n2};
+            bool done[3] = {false, c.k.w == nullptr, c.v.w == nullptr};
+            bool xb_ready = false;
+            for (int i = 0; i < 3; ++i) {
+                if (done[i]) continue;
+                RowsOut outs[3];
+                int idx[3], n = 0;
+                for (int j = i; j < 3; ++j)
+                    if (!done[j] && mats[j].type == mats[i].type) {
+                        outs[n] = RowsOut{ys[j], mats[j].w, nullptr, ns[j]};
+                        idx[n++] = j;
+                    }
+                rc = enqueue_rows_fused(mats[i].type, outs, n, x, attn_norm, eps, dim, 0, kRowsStore);
+                if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                    if (!xb_ready) {
+                        if ((rc = enqueue_rmsnorm(st.xb.f(), x, attn_norm, 1, dim, eps))) return rc;
+                        xb_ready = true;
+                    }
+                    for (int j = 0; j < n; ++j)
+                        if ((rc = matmul(ys[idx[j]], st.xb.f(), mats[idx[j]], dim, ns[idx[j]], 1))) return rc;
+                } else if (rc != ALJABR_ROCM_OK) {
+                    return rc;
+                }
+                for (int j = 0; j < n; ++j) done[idx[j]] = true;
+            }
         }
         if (c.k.w && !c.v.w && (c.n1 <= 0 || c.n1 != c.n2))
             return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "decode_step: layer %d K-as-V needs n1 == n2", l);

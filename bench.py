@@ -66,6 +66,8 @@ def parse() -> argparse.Namespace:
                     help="run only the prefill attention measurement (for profiling)")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the GQA decode attention measurement (for profiling)")
+    ap.add_argument("--step-only", action="store_true",
+                    help="run only the registered whole-step (Metal ABI) decode measurement")
     return ap.parse_args()
 
 
@@ -554,6 +556,69 @@ def gguf_decode_runs(args, abi, torch, stream):
     return dec
 
 
+def registered_step_runs(args, abi, torch, stream, ctx: int = 2048):
+    """The Metal ABI's registered whole step (init_kv_cache, register_*,
+    decode_step_token) at the Llama-3-8B Q4_K_M shapes, batch 1, context
+    `ctx`: device weights, fp32 position-major KV caches prefilled with
+    N(0,1) rows through sync_kv_cache, SiLU FFN. Each call returns the greedy
+    token, so the time per token includes the call's own wait and host work
+    (wall clock), as the Java runner sees it."""
+    import ctypes
+    from aljabr_amd.llama import LLAMA3_8B
+    cfg = LLAMA3_8B
+    lib = abi.load()
+    log("registered whole step: Llama-3-8B Q4_K_M, batch 1")
+    w = gguf_weights(torch, cfg, Q4_K_M, seed=11)
+    L, dim, ffn = cfg["layers"], cfg["dim"], cfg["ffn"]
+    nh, nkv, hd = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
+    steps = max(args.decode_steps, 10)
+    max_seq = ctx + steps + 8
+    abi.call("aljabr_rocm_reset_decode_state")
+    strides = (ctypes.c_int * L)(*([nkv * hd] * L))
+    abi.call("aljabr_rocm_init_kv_cache", L, max_seq, strides)
+    g = torch.Generator(device="cuda:0").manual_seed(21)
+    prefix = torch.randn(ctx * nkv * hd, generator=g, device="cuda:0")
+    torch.cuda.synchronize()
+    for l in range(L):
+        abi.call("aljabr_rocm_sync_kv_cache", l, ctx, prefix.data_ptr(), prefix.data_ptr())
+    del prefix
+    attn_norm = torch.cat(w["attn_norm"]).contiguous()
+    ffn_norm = torch.cat(w["ffn_norm"]).contiguous()
+    torch.cuda.synchronize()
+    abi.call("aljabr_rocm_register_norm_buffer", 3, attn_norm.data_ptr(), attn_norm.numel() * 4)
+    abi.call("aljabr_rocm_register_norm_buffer", 1, ffn_norm.data_ptr(), ffn_norm.numel() * 4)
+    for l in range(L):
+        t = {k: w[k][l] for k in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")}
+        abi.call("aljabr_rocm_register_decode_layer", l, l,
+                 *[t[k][1].data_ptr() for k in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")],
+                 *[t[k][0] for k in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")],
+                 nh * hd, nkv * hd, nkv * hd, nh * hd, dim, ffn, nh, nkv, hd, nkv * hd, cfg["rope_base"], 0,
+                 1.0, 0.0, 0, 0, 0, 0, 0)
+    abi.call("aljabr_rocm_register_output", w["out_norm"].data_ptr(), w["lm_head"][1].data_ptr(), w["lm_head"][0],
+             dim, cfg["vocab"], 0.0)
+    abi.call("aljabr_rocm_register_token_embd", w["tok_embed"][1].data_ptr(), w["tok_embed"][0], dim, 1.0)
+    abi.call("aljabr_rocm_set_decode_activation", 1)
+    torch.cuda.synchronize()
+    tok = 17
+    for i in range(3):                              # warm-up positions ctx .. ctx+2
+        tok = lib.aljabr_rocm_decode_step_token(ctx + i, 0, cfg["eps"], tok, None)
+        if tok < 0:
+            abi.check(tok, "aljabr_rocm_decode_step_token")
+    t0 = time.perf_counter()
+    for i in range(steps):
+        tok = lib.aljabr_rocm_decode_step_token(ctx + 3 + i, 0, cfg["eps"], tok, None)
+        if tok < 0:
+            abi.check(tok, "aljabr_rocm_decode_step_token")
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
+    abi.call("aljabr_rocm_reset_decode_state")
+    del w, attn_norm, ffn_norm
+    torch.cuda.empty_cache()
+    return {"batch": 1, "context": ctx, "ms_per_token": round(ms, 3), "tokens_per_s": round(1000.0 / ms, 1),
+            "weights": "GGUF Q4_K_M layout (Q4_K; Q6_K attn_v, ffn_down, output), synthetic codes",
+            "kv_cache": "fp32 [max_seq][n_kv*head_dim] per layer (the Metal step's layout)",
+            "timing": "wall clock per decode_step_token call (each waits for its step and returns the token)"}
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -582,6 +647,8 @@ def main() -> None:
             print(json.dumps({"prefill_attention": prefill_bench(abi, torch, stream)}), flush=True)
         elif args.attention_only:
             print(json.dumps({"attention": attention_bench(abi, torch, stream)}), flush=True)
+        elif args.step_only:
+            print(json.dumps({"registered_step": registered_step_runs(args, abi, torch, stream)}), flush=True)
         elif args.gguf_decode_only:
             print(json.dumps({"decode_gguf_q4_k_m": gguf_decode_runs(args, abi, torch, stream)}), flush=True)
         else:
@@ -643,6 +710,7 @@ def run(args, abi, torch, stream) -> None:
     if not args.no_decode:
         result["decode"] = decode_runs(args, abi, torch, stream)
         result["decode_gguf_q4_k_m"] = gguf_decode_runs(args, abi, torch, stream)
+        result["registered_step"] = registered_step_runs(args, abi, torch, stream)
 
     if not args.no_cpu:
         log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
