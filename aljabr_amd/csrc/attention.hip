@@ -485,11 +485,21 @@ __global__ void mask_check_kernel(const float *__restrict__ mask, long long n, i
 
 __global__ void zero_i32_kernel(int *p) { *p = 0; }
 
-template <int D, int G, bool F16, bool PAGED>
+// WIDE: 8-wave workgroups (4 with G = 8) for grids of about one workgroup
+// per CU; 4-wave ones (2) otherwise.
+template <int D, int G, bool F16, bool PAGED, bool WIDE>
 int launch_split(const AttnParams &p, int splits, int chunk, float *part, hipStream_t s) {
-    constexpr int WAVES = (G <= 4) ? 4 : 2;
+    constexpr int WAVES = WIDE ? ((G <= 4) ? 8 : 4) : ((G <= 4) ? 4 : 2);
     constexpr int NG = (64 / (D / 8)) * WAVES;
     const size_t lds = static_cast<size_t>(NG) * G * (D + 2) * sizeof(float);
+    if constexpr (static_cast<size_t>(NG) * G * (D + 2) * sizeof(float) > 65536) {
+        static bool lds_set = false;             // the attribute is per kernel, per process
+        if (!lds_set) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_split_kernel<D, G, F16, WAVES, PAGED>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+            lds_set = true;
+        }
+    }
     const dim3 grid(splits, p.Hkv * p.Sq, p.B);
     const long long rows = static_cast<long long>(p.B) * p.Hq * p.Sq;
     // Partials: o as [rows][splits][D], then (m, l) as [rows][splits][2].
@@ -503,21 +513,24 @@ int launch_split(const AttnParams &p, int splits, int chunk, float *part, hipStr
     return ALJABR_ROCM_OK;
 }
 
-template <int D, bool F16, bool PAGED>
+template <int D, bool F16, bool PAGED, bool WIDE>
 int launch_g(const AttnParams &p, int G, int splits, int chunk, float *part, hipStream_t s) {
     switch (G) {
-    case 1: return launch_split<D, 1, F16, PAGED>(p, splits, chunk, part, s);
-    case 2: return launch_split<D, 2, F16, PAGED>(p, splits, chunk, part, s);
-    case 4: return launch_split<D, 4, F16, PAGED>(p, splits, chunk, part, s);
-    case 8: return launch_split<D, 8, F16, PAGED>(p, splits, chunk, part, s);
+    case 1: return launch_split<D, 1, F16, PAGED, WIDE>(p, splits, chunk, part, s);
+    case 2: return launch_split<D, 2, F16, PAGED, WIDE>(p, splits, chunk, part, s);
+    case 4: return launch_split<D, 4, F16, PAGED, WIDE>(p, splits, chunk, part, s);
+    case 8: return launch_split<D, 8, F16, PAGED, WIDE>(p, splits, chunk, part, s);
     default: return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "no split attention kernel for %d query heads per KV head", G);
     }
 }
 
 template <int D, bool F16>
-int launch_paged(const AttnParams &p, int G, int splits, int chunk, float *part, hipStream_t s) {
-    return p.block_table ? launch_g<D, F16, true>(p, G, splits, chunk, part, s)
-                         : launch_g<D, F16, false>(p, G, splits, chunk, part, s);
+int launch_paged(const AttnParams &p, int G, int splits, int chunk, float *part, bool wide, hipStream_t s) {
+    if (wide)
+        return p.block_table ? launch_g<D, F16, true, true>(p, G, splits, chunk, part, s)
+                             : launch_g<D, F16, false, true>(p, G, splits, chunk, part, s);
+    return p.block_table ? launch_g<D, F16, true, false>(p, G, splits, chunk, part, s)
+                         : launch_g<D, F16, false, false>(p, G, splits, chunk, part, s);
 }
 
 }  // namespace
@@ -552,11 +565,17 @@ int enqueue_attention(const AttnParams &p_in) {
             hipLaunchKernelGGL(attn_generic_kernel<false>, grid, dim3(64), 0, s, p);
         return ALJABR_ROCM_OK;
     }
-    // Enough workgroups to cover the CUs twice, chunks of >= 64 keys.
-    constexpr int per_cu = 2;
+    // Chunks of >= 64 keys. With at least two (sequence, KV head, query
+    // row) items per CU: 4-wave workgroups, enough splits to cover the CUs
+    // twice. With fewer: 8-wave workgroups, enough splits to cover them once
+    // (measured on MI355X: batch 32 x 8 KV heads at 2048 keys 60.9 -> 56.6 us,
+    // one split and no merge launch; batch 1 at 4096 keys 18.3 -> 16.8 us;
+    // batch 64 was faster with the 4-wave shape).
     const long long items = static_cast<long long>(p.B) * p.Hkv * p.Sq;
     const int keys = p.block_table ? p.max_blocks * p.block_size : (p.kv_len ? p.cap : p.Sk);
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const bool wide = items < 2LL * cus;
+    const int per_cu = wide ? 1 : 2;
     long long want = (static_cast<long long>(per_cu) * cus + items - 1) / items;
     const long long max_splits = (keys + 63) / 64;
     if (want > max_splits) want = max_splits;
@@ -581,10 +600,10 @@ int enqueue_attention(const AttnParams &p_in) {
                                          : ALJABR_ROCM_ERR_BUFFER;
     }
     if (p.D == 64)
-        return p.kv_f16 ? launch_paged<64, true>(p, G, splits, chunk, part, s)
-                        : launch_paged<64, false>(p, G, splits, chunk, part, s);
-    return p.kv_f16 ? launch_paged<128, true>(p, G, splits, chunk, part, s)
-                    : launch_paged<128, false>(p, G, splits, chunk, part, s);
+        return p.kv_f16 ? launch_paged<64, true>(p, G, splits, chunk, part, wide, s)
+                        : launch_paged<64, false>(p, G, splits, chunk, part, wide, s);
+    return p.kv_f16 ? launch_paged<128, true>(p, G, splits, chunk, part, wide, s)
+                    : launch_paged<128, false>(p, G, splits, chunk, part, wide, s);
 }
 
 }  // namespace aljabr
