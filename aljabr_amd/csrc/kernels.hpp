@@ -128,6 +128,27 @@ int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const 
 // or Q6_K (absmax and bs_shift for NF4 only).
 int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
                        int bs_shift, int epilogue, const RowsRope *rope = nullptr);
+// What the second kernel of a split-K GEMM does with the slice sums besides
+// (or instead of) writing them: the decode step's next element-wise launch,
+// applied to the stacked rows of the GEMM (slice_tails.hip).
+constexpr int kTailSwiGLU = 1;        // rows [0, n) gate, [n, 2n) up: out[m][i] = silu(gate) * up
+constexpr int kTailRopeAppend = 2;    // rows q (nh heads), k, v (nkv heads): out = rotated q; k (rotated) and v
+                                      // appended as fp16 at row pos[m] of caches [M][nkv][cap][head_dim]
+constexpr int kTailResidualNorm = 3;  // out[m] += sums (residual); xn[m] = RMSNorm(out[m]) * norm_w
+struct SliceTail {
+    int kind;
+    float *out;
+    int n;
+    uint16_t *kc, *vc;
+    const int *pos;
+    int nh, nkv, head_dim, cap;
+    float base;
+    const float2 *cs;
+    float *xn;
+    const float *norm_w;
+    float eps;
+};
+int enqueue_slice_tail(const SliceTail &t, const float *part, int slices, int M, int N);
 // NF4 small-M GEMM on MFMA (M >= 2 in passes of 32 tokens, K % 256 == 0,
 // block size 64), fp32-accurate and deterministic: C = A . W^T, or with
 // `add` C += A . W^T (a residual). When K is split over workgroups the
@@ -138,8 +159,10 @@ int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *a
                      int M, bool add = false, float *part = nullptr, size_t part_floats = 0);
 // The same over up to three matrices of one K stacked in one launch (all but
 // the last with a multiple of 32 rows); outs[i].y is [M][outs[i].n].
+// With `tail` (M <= 32) the outputs are not written: the slice sums go to
+// the tail kernel instead (outs[].y unused).
 int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M, bool add,
-                           float *part = nullptr, size_t part_floats = 0);
+                           float *part = nullptr, size_t part_floats = 0, const SliceTail *tail = nullptr);
 size_t nf4_mfma_scratch_floats(int M, int N, int K);
 // The plan enqueue_nf4_mfma_multi uses for N stacked rows over K on `cus`
 // CUs (row tiles per wave, sub-slices per K slice), and one pass of at most
@@ -147,7 +170,7 @@ size_t nf4_mfma_scratch_floats(int M, int N, int K);
 // already validated).
 void nf4_mfma_plan(int N, int K, int cus, int &nt, int &q);
 int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, int M, bool add, float *part,
-                          size_t part_floats, int nt, int q);
+                          size_t part_floats, int nt, int q, const SliceTail *tail = nullptr);
 // fp16-weight small-M GEMM on MFMA (2 <= M <= 32, K in {512, 1024, 2048,
 // 4096}, W and A 16-byte aligned); deterministic (no atomics).
 int enqueue_f16_mfma(float *C, const float *A, const uint16_t *W, int K, int N, int M);

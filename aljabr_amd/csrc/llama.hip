@@ -891,6 +891,12 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         return weight_bytes(t.type, N, K, bs) + B * (K + N * (add ? 2.0 : 1.0)) * f4;
     };
     const bool fused1 = B == 1 && m->rows_fused;
+    // Batches of 2..32 over NF4 weights: each GEMM's slice-sum kernel also runs
+    // the step that follows it (RoPE and the KV append, the residual add and
+    // the next RMSNorm, SwiGLU), so xb holds the next RMSNorm at every layer's
+    // start. A GEMM the matrix cores do not take falls back to the separate
+    // launches for that block only.
+    const bool tails = !fused1 && m->all_nf4 && B >= 2 && B <= 32 && shift == 6;
     hipLaunchKernelGGL(lengths_from_positions, dim3((B + 63) / 64), dim3(64), 0, s, m->kv_len, pos, B);
     if (m->tok_embed.type == ALJABR_ROCM_TYPE_F32)
         ALJ_TRY(enqueue_embed(m->x, reinterpret_cast<const float *>(m->tok_embed.w), tok, B, dim, c.vocab));
@@ -943,37 +949,63 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                          (2.0 * dim + qd) * f4 + 2.0 * kvd * 2.0);
         } else {
             // Every GEMM below writes its outputs (none accumulates into them).
-            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, attn_norm, B, dim, c.eps));
-            ALJ_MARK("rmsnorm", (B * 2.0 * dim + dim) * f4);
+            if (!tails || l == 0) {
+                ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, attn_norm, B, dim, c.eps));
+                ALJ_MARK("rmsnorm", (B * 2.0 * dim + dim) * f4);
+            }
             // Q, K and V in one matrix-core launch where the shapes allow.
             const RowsOut qkv[3] = {{m->q, W(m->wq), S(m->wq), qd},
                                     {m->k, W(m->wk), S(m->wk), kvd},
                                     {m->v, W(m->wv), S(m->wv), kvd}};
-            rc = m->all_nf4 && B >= 2 ? enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, false, m->mm_part,
-                                                               m->mm_part_floats)
-                                      : ALJABR_ROCM_ERR_UNSUPPORTED;
+            rc = ALJABR_ROCM_ERR_UNSUPPORTED;
+            if (tails) {
+                SliceTail t{};
+                t.kind = kTailRopeAppend;
+                t.out = m->q;
+                t.kc = kc;
+                t.vc = vc;
+                t.pos = pos;
+                t.nh = nh;
+                t.nkv = nkv;
+                t.head_dim = hd;
+                t.cap = c.max_seq;
+                t.base = c.rope_base;
+                t.cs = m->rope_cs;
+                rc = enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, false, m->mm_part, m->mm_part_floats, &t);
+                if (rc == ALJABR_ROCM_OK)
+                    ALJ_MARK("qkv_gemm_rope_append", mm_bytes(m->wq[l], qd, dim, false) +
+                                                         mm_bytes(m->wk[l], kvd, dim, false) +
+                                                         mm_bytes(m->wv[l], kvd, dim, false) - 2.0 * B * dim * f4 -
+                                                         B * 2.0 * kvd * f4 + B * 2.0 * kvd * 2.0);
+            }
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
-                float *const ys[3] = {m->q, m->k, m->v};
-                const T *const ts[3] = {&m->wq[l], &m->wk[l], &m->wv[l]};
-                const int ns[3] = {qd, kvd, kvd};
-                ALJ_TRY(mm_run(ys, ts, ns, 3, m->xb, dim));
+                rc = m->all_nf4 && B >= 2 ? enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, false, m->mm_part,
+                                                                   m->mm_part_floats)
+                                          : ALJABR_ROCM_ERR_UNSUPPORTED;
+                if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                    float *const ys[3] = {m->q, m->k, m->v};
+                    const T *const ts[3] = {&m->wq[l], &m->wk[l], &m->wv[l]};
+                    const int ns[3] = {qd, kvd, kvd};
+                    ALJ_TRY(mm_run(ys, ts, ns, 3, m->xb, dim));
+                } else if (rc != ALJABR_ROCM_OK) {
+                    return rc;
+                }
+                ALJ_MARK("qkv_gemm", mm_bytes(m->wq[l], qd, dim, false) + mm_bytes(m->wk[l], kvd, dim, false) +
+                                         mm_bytes(m->wv[l], kvd, dim, false) - 2.0 * B * dim * f4);
+                rc = enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base,
+                                         m->rope_cs);
+                if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                    ALJ_TRY(enqueue_rope(m->q, pos, B, nh, hd, c.rope_base));
+                    ALJ_TRY(enqueue_rope(m->k, pos, B, nkv, hd, c.rope_base));
+                    ALJ_TRY(enqueue_kv_append(kc, m->k, pos, B, nkv, hd, c.max_seq));
+                    ALJ_TRY(enqueue_kv_append(vc, m->v, pos, B, nkv, hd, c.max_seq));
+                } else if (rc != ALJABR_ROCM_OK) {
+                    return rc;
+                }
+                ALJ_MARK("rope_kv_append", B * (2.0 * qd + 2.0 * kvd) * f4 + B * 2.0 * kvd * 2.0);
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }
-            ALJ_MARK("qkv_gemm", mm_bytes(m->wq[l], qd, dim, false) + mm_bytes(m->wk[l], kvd, dim, false) +
-                                     mm_bytes(m->wv[l], kvd, dim, false) - 2.0 * B * dim * f4);
-        }
-        if (!fused1) {
-            rc = enqueue_rope_append(m->q, m->k, m->v, kc, vc, pos, B, nh, nkv, hd, c.max_seq, c.rope_base, m->rope_cs);
-            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
-                ALJ_TRY(enqueue_rope(m->q, pos, B, nh, hd, c.rope_base));
-                ALJ_TRY(enqueue_rope(m->k, pos, B, nkv, hd, c.rope_base));
-                ALJ_TRY(enqueue_kv_append(kc, m->k, pos, B, nkv, hd, c.max_seq));
-                ALJ_TRY(enqueue_kv_append(vc, m->v, pos, B, nkv, hd, c.max_seq));
-            } else if (rc != ALJABR_ROCM_OK) {
-                return rc;
-            }
-            ALJ_MARK("rope_kv_append", B * (2.0 * qd + 2.0 * kvd) * f4 + B * 2.0 * kvd * 2.0);
         }
         AttnParams ap{};
         ap.out = m->att;
@@ -996,8 +1028,30 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             ALJ_TRY(enqueue_rows_fused(m->wo[l].type, &o, 1, m->att, nullptr, 0.0f, qd, shift, kRowsAdd));
             ALJ_MARK("wo_rows_add", mm_bytes(m->wo[l], dim, qd, true));
         } else {
-            ALJ_TRY(mm(m->x, m->att, m->wo[l], qd, dim, true, m->xb));
-            ALJ_MARK("wo_gemm_add", mm_bytes(m->wo[l], dim, qd, true));
+            rc = ALJABR_ROCM_ERR_UNSUPPORTED;
+            if (tails) {
+                // x += Wo att, then xb = RMSNorm(x) with the FFN norm.
+                SliceTail t{};
+                t.kind = kTailResidualNorm;
+                t.out = m->x;
+                t.xn = m->xb;
+                t.norm_w = ffn_norm;
+                t.eps = c.eps;
+                const RowsOut o = {m->x, W(m->wo), S(m->wo), dim};
+                rc = enqueue_nf4_mfma_multi(&o, 1, m->att, qd, shift, B, false, m->mm_part, m->mm_part_floats, &t);
+                if (rc == ALJABR_ROCM_OK)
+                    ALJ_MARK("wo_gemm_add_rmsnorm", mm_bytes(m->wo[l], dim, qd, true) + (B * dim + dim) * f4);
+            }
+            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                ALJ_TRY(mm(m->x, m->att, m->wo[l], qd, dim, true, m->xb));
+                ALJ_MARK("wo_gemm_add", mm_bytes(m->wo[l], dim, qd, true));
+                if (tails) {
+                    ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, ffn_norm, B, dim, c.eps));
+                    ALJ_MARK("rmsnorm", (B * 2.0 * dim + dim) * f4);
+                }
+            } else if (rc != ALJABR_ROCM_OK) {
+                return rc;
+            }
         }
         // MLP: x += Wdown (silu(Wgate xb) * Wup xb), xb = RMSNorm(x).
         if (fused1) {
@@ -1025,31 +1079,75 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             ALJ_TRY(enqueue_rows_fused(m->w_down[l].type, &d, 1, m->hb, nullptr, 0.0f, ffn, shift, kRowsAdd));
             ALJ_MARK("down_rows_add", mm_bytes(m->w_down[l], dim, ffn, true));
         } else {
-            ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, ffn_norm, B, dim, c.eps));
-            ALJ_MARK("rmsnorm", (B * 2.0 * dim + dim) * f4);
+            if (!tails) {
+                ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, ffn_norm, B, dim, c.eps));
+                ALJ_MARK("rmsnorm", (B * 2.0 * dim + dim) * f4);
+            }
             const RowsOut gu[2] = {{m->gate, W(m->w_gate), S(m->w_gate), ffn},
                                    {m->up, W(m->w_up), S(m->w_up), ffn}};
-            rc = m->all_nf4 && B >= 2 ? enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, false, m->mm_part,
-                                                               m->mm_part_floats)
-                                      : ALJABR_ROCM_ERR_UNSUPPORTED;
+            rc = ALJABR_ROCM_ERR_UNSUPPORTED;
+            if (tails) {
+                SliceTail t{};
+                t.kind = kTailSwiGLU;
+                t.out = m->hb;
+                t.n = ffn;
+                rc = enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, false, m->mm_part, m->mm_part_floats, &t);
+                if (rc == ALJABR_ROCM_OK)
+                    ALJ_MARK("gate_up_gemm_swiglu", mm_bytes(m->w_gate[l], ffn, dim, false) +
+                                                        mm_bytes(m->w_up[l], ffn, dim, false) - B * dim * f4 -
+                                                        B * ffn * f4);
+            }
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
-                float *const ys[2] = {m->gate, m->up};
-                const T *const ts[2] = {&m->w_gate[l], &m->w_up[l]};
-                const int ns[2] = {ffn, ffn};
-                ALJ_TRY(mm_run(ys, ts, ns, 2, m->xb, dim));
+                rc = m->all_nf4 && B >= 2 ? enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, false, m->mm_part,
+                                                                   m->mm_part_floats)
+                                          : ALJABR_ROCM_ERR_UNSUPPORTED;
+                if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                    float *const ys[2] = {m->gate, m->up};
+                    const T *const ts[2] = {&m->w_gate[l], &m->w_up[l]};
+                    const int ns[2] = {ffn, ffn};
+                    ALJ_TRY(mm_run(ys, ts, ns, 2, m->xb, dim));
+                } else if (rc != ALJABR_ROCM_OK) {
+                    return rc;
+                }
+                ALJ_MARK("gate_up_gemm", mm_bytes(m->w_gate[l], ffn, dim, false) +
+                                             mm_bytes(m->w_up[l], ffn, dim, false) - B * dim * f4);
+                ALJ_TRY(enqueue_swiglu(m->hb, m->gate, m->up, static_cast<long long>(B) * ffn));
+                ALJ_MARK("swiglu", B * 3.0 * ffn * f4);
             } else if (rc != ALJABR_ROCM_OK) {
                 return rc;
             }
-            ALJ_MARK("gate_up_gemm", mm_bytes(m->w_gate[l], ffn, dim, false) + mm_bytes(m->w_up[l], ffn, dim, false) -
-                                         B * dim * f4);
-            ALJ_TRY(enqueue_swiglu(m->hb, m->gate, m->up, static_cast<long long>(B) * ffn));
-            ALJ_MARK("swiglu", B * 3.0 * ffn * f4);
-            ALJ_TRY(mm(m->x, m->hb, m->w_down[l], ffn, dim, true, m->xb));
-            ALJ_MARK("down_gemm_add", mm_bytes(m->w_down[l], dim, ffn, true));
+            // x += Wdown hb; with the tails also xb = the next RMSNorm of x
+            // (the next layer's attention norm, or the output norm).
+            const float *next_norm = l + 1 < c.layers ? m->attn_norm[l + 1] : m->out_norm;
+            rc = ALJABR_ROCM_ERR_UNSUPPORTED;
+            if (tails) {
+                SliceTail t{};
+                t.kind = kTailResidualNorm;
+                t.out = m->x;
+                t.xn = m->xb;
+                t.norm_w = next_norm;
+                t.eps = c.eps;
+                const RowsOut d = {m->x, W(m->w_down), S(m->w_down), dim};
+                rc = enqueue_nf4_mfma_multi(&d, 1, m->hb, ffn, shift, B, false, m->mm_part, m->mm_part_floats, &t);
+                if (rc == ALJABR_ROCM_OK)
+                    ALJ_MARK("down_gemm_add_rmsnorm", mm_bytes(m->w_down[l], dim, ffn, true) + (B * dim + dim) * f4);
+            }
+            if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                ALJ_TRY(mm(m->x, m->hb, m->w_down[l], ffn, dim, true, m->xb));
+                ALJ_MARK("down_gemm_add", mm_bytes(m->w_down[l], dim, ffn, true));
+                if (tails) {
+                    ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, next_norm, B, dim, c.eps));
+                    ALJ_MARK(l + 1 < c.layers ? "rmsnorm" : "final_rmsnorm", (B * 2.0 * dim + dim) * f4);
+                }
+            } else if (rc != ALJABR_ROCM_OK) {
+                return rc;
+            }
         }
     }
-    ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, m->out_norm, B, dim, c.eps));
-    ALJ_MARK("final_rmsnorm", (B * 2.0 * dim + dim) * f4);
+    if (!tails) {
+        ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, m->out_norm, B, dim, c.eps));
+        ALJ_MARK("final_rmsnorm", (B * 2.0 * dim + dim) * f4);
+    }
     ALJ_TRY(enqueue_matmul_typed(lg, m->xb, m->lm_head.w, m->lm_head.s, m->lm_head.type, bs, dim, c.vocab, B));
     ALJ_MARK(m->lm_head.type == ALJABR_ROCM_TYPE_F16 ? "lm_head_f16" : "lm_head", mm_bytes(m->lm_head, c.vocab, dim, false));
     ALJ_TRY(enqueue_argmax(next, lg, B, c.vocab));

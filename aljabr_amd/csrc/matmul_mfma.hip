@@ -78,7 +78,7 @@ struct MmArgs {
     int M, N, K;           // N: stacked rows
     int add;               // Y += instead of Y = (one slice)
     int q;                 // sub-slices per slice (the last slice may hold fewer)
-    float *part;           // [slice][M][N] partial sums when gridDim.x > 1
+    float *part;           // [slice][M][N] partial sums (several slices, or a tail kernel follows); null: Y directly
 };
 
 struct TileRef {
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(kMmThreads) void nf4_mm_kernel(MmArgs a) {
     for (int t = 0; t < NT; ++t) {
         const int n = tr[t].local0 + nl;
         if (n >= tr[t].n) continue;
-        if (gridDim.x == 1) {
+        if (a.part == nullptr) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = 8 * (r >> 2) + 4 * h + (r & 3);
@@ -525,7 +525,7 @@ void nf4_mfma_plan(int N, int K, int cus, int &nt, int &q) {
 // The GEMM pass with an explicit plan (nt = 1 or 2 row tiles per wave,
 // q >= 1 sub-slices per slice).
 int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, int M, bool add, float *part,
-                          size_t part_floats, int nt, int q) {
+                          size_t part_floats, int nt, int q, const SliceTail *tail) {
     MmArgs args{};
     long long end = 0;
     for (int i = 0; i < 3; ++i) {
@@ -554,7 +554,7 @@ int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, 
     const long long groups = (args.N + static_cast<long long>(kGroupRows) * nt - 1) / (static_cast<long long>(kGroupRows) * nt);
     if (groups > 65535) return ALJABR_ROCM_ERR_UNSUPPORTED;
     args.add = slices == 1 && add;
-    if (slices > 1) {
+    if (slices > 1 || tail) {
         const size_t need = static_cast<size_t>(slices) * M * args.N;
         args.part = part && need <= part_floats
                         ? part
@@ -573,6 +573,7 @@ int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, 
     const dim3 grid(slices, static_cast<unsigned>(groups));
     if (nt == 2) hipLaunchKernelGGL(nf4_mm_kernel<2>, grid, dim3(kMmThreads), kLdsBytes, s, args);
     else hipLaunchKernelGGL(nf4_mm_kernel<1>, grid, dim3(kMmThreads), kLdsBytes, s, args);
+    if (tail) return enqueue_slice_tail(*tail, args.part, slices, M, args.N);
     if (slices > 1) return enqueue_slice_sum(args.y, args.end, nseg, M, args.N, args.part, slices, add);
     return ALJABR_ROCM_OK;
 }
@@ -597,8 +598,8 @@ int enqueue_slice_sum(float *const *ys, const int *ends, int nseg, int M, int N,
 }
 
 int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M, bool add,
-                           float *part, size_t part_floats) {
-    if (nseg < 1 || nseg > 3 || M < 2 || K % kSub != 0 || bs_shift != 6 || !aligned(A, 16))
+                           float *part, size_t part_floats, const SliceTail *tail) {
+    if (nseg < 1 || nseg > 3 || M < 2 || K % kSub != 0 || bs_shift != 6 || !aligned(A, 16) || (tail && M > 32))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     long long n = 0;
     for (int i = 0; i < nseg; ++i) {
@@ -619,8 +620,8 @@ int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K,
             o[i] = outs[i];
             o[i].y = outs[i].y + static_cast<size_t>(m0) * outs[i].n;
         }
-        const int rc =
-            nf4_mfma_pass_planned(o, nseg, A + static_cast<size_t>(m0) * K, K, mm, add, part, part_floats, nt, q);
+        const int rc = nf4_mfma_pass_planned(o, nseg, A + static_cast<size_t>(m0) * K, K, mm, add, part, part_floats,
+                                             nt, q, tail);
         if (rc != ALJABR_ROCM_OK) return rc;
     }
     return ALJABR_ROCM_OK;
