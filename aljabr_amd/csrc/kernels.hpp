@@ -159,16 +159,16 @@ int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *a
                      int M, bool add = false, float *part = nullptr, size_t part_floats = 0);
 // The same over up to three matrices of one K stacked in one launch (all but
 // the last with a multiple of 32 rows); outs[i].y is [M][outs[i].n].
-// With `tail` (M <= 32) the outputs are not written: the slice sums go to
+// With `tail` (M <= 64) the outputs are not written: the slice sums go to
 // the tail kernel instead (outs[].y unused).
 int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M, bool add,
                            float *part = nullptr, size_t part_floats = 0, const SliceTail *tail = nullptr);
 size_t nf4_mfma_scratch_floats(int M, int N, int K);
 // The plan enqueue_nf4_mfma_multi uses for N stacked rows over K on `cus`
-// CUs (row tiles per wave, sub-slices per K slice), and one pass of at most
-// 32 tokens under an explicit plan (segments as enqueue_nf4_mfma_multi,
+// CUs and passes of M tokens (row tiles per wave, sub-slices per K slice),
+// and one pass of at most 64 tokens under an explicit plan (segments as enqueue_nf4_mfma_multi,
 // already validated).
-void nf4_mfma_plan(int N, int K, int cus, int &nt, int &q);
+void nf4_mfma_plan(int N, int K, int M, int cus, int &nt, int &q);
 int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, int M, bool add, float *part,
                           size_t part_floats, int nt, int q, const SliceTail *tail = nullptr);
 // fp16-weight small-M GEMM on MFMA (2 <= M <= 32, K in {512, 1024, 2048,

@@ -52,17 +52,24 @@ constexpr int kSub = 256;                        // K sub-slice (elements) stage
 constexpr int kRS = kSub + 8;                    // activation row stride in halves (16-byte pad)
 
 // LDS layout (bytes; dynamic LDS starts at address 0, the kernel has no
-// static LDS): the decode table, the activation tile (hi rows, then lo
-// rows), per-wave code staging (32 rows x 144 bytes) and per-wave scale
-// staging (32 rows x 4 floats).
-constexpr uint32_t kTableBytes = 256 * 256;
-constexpr uint32_t kXOff = kTableBytes;
-constexpr uint32_t kXLo = 32 * kRS * 2;          // lo rows after the hi rows
-constexpr uint32_t kCOff = kXOff + 2 * kXLo;
+// static LDS): the decode table, the activation tile of MT 32-token tiles
+// (hi rows, then lo rows), per-wave code staging (32 rows x 144 bytes) and
+// per-wave scale staging (32 rows x 4 floats). With two token tiles the
+// table keeps 16 replicas in 128-byte entries (32 KiB) so that the 64
+// activation rows fit.
 constexpr uint32_t kCRow = 144;
-constexpr uint32_t kSOff = kCOff + kMmWaves * 32 * kCRow;
-constexpr uint32_t kLdsBytes = kSOff + kMmWaves * 32 * 16;
-static_assert(kLdsBytes <= 160 * 1024, "LDS budget of a CU");
+template <int MT>
+struct Lds {
+    static constexpr uint32_t kReplicas = MT == 1 ? 32 : 16;
+    static constexpr uint32_t kEntry = 8 * kReplicas;                 // H pairs, then R pairs
+    static constexpr uint32_t kTableBytes = 256 * kEntry;
+    static constexpr uint32_t kXOff = kTableBytes;
+    static constexpr uint32_t kXLo = 32 * MT * kRS * 2;               // lo rows after the hi rows
+    static constexpr uint32_t kCOff = kXOff + 2 * kXLo;
+    static constexpr uint32_t kSOff = kCOff + kMmWaves * 32 * kCRow;
+    static constexpr uint32_t kBytes = kSOff + kMmWaves * 32 * 16;
+    static_assert(kBytes <= 160 * 1024, "LDS budget of a CU");
+};
 
 // Up to three weight matrices of the same K stacked as one row space (the
 // decode step's Q/K/V or gate/up in one launch): segment s owns stacked rows
@@ -155,22 +162,36 @@ __device__ __forceinline__ T gload_stream(const void *p) {
 }
 
 // Table entry e (code byte: even element in the high nibble), replica r:
-// {H(e>>4), H(e&15)} at e*256 + 4r and {R(e>>4), R(e&15)} 128 bytes on.
-// Thread tid (of 512) fills replica tid%32 of entries tid/32 + 16k, k < 16:
-// their low nibble is tid/32 and their high nibble k.
+// {H(e>>4), H(e&15)} at e*kEntry + 4r and {R(e>>4), R(e&15)} kEntry/2 bytes
+// on. With 32 replicas thread tid (of 512) fills replica tid%32 of entries
+// tid/32 + 16k, k < 16 (low nibble tid/32, high nibble k); with 16 replicas
+// replica tid%16 of entries tid/16 + 32k, k < 8 (low nibble (tid/16)%16,
+// high nibble tid/256 + 2k).
+template <int MT>
 __device__ __forceinline__ void build_table(int tid) {
     constexpr float kNF4[16] = {
         -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
         -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
         0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
         0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
-    const float lo = nf4_level_sel((tid >> 5) & 15);
-    const uint32_t base = static_cast<uint32_t>(tid >> 5) * 256 + (tid & 31) * 4;
+    if constexpr (MT == 1) {
+        const float lo = nf4_level_sel((tid >> 5) & 15);
+        const uint32_t base = static_cast<uint32_t>(tid >> 5) * 256 + (tid & 31) * 4;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const float hi = kNF4[k];
-        *lds<lds_u32>(base + k * 16 * 256) = pack_half2(hi, lo);
-        *lds<lds_u32>(base + k * 16 * 256 + 128) = pack_half2(level_rest(hi), level_rest(lo));
+        for (int k = 0; k < 16; ++k) {
+            const float hi = kNF4[k];
+            *lds<lds_u32>(base + k * 16 * 256) = pack_half2(hi, lo);
+            *lds<lds_u32>(base + k * 16 * 256 + 128) = pack_half2(level_rest(hi), level_rest(lo));
+        }
+    } else {
+        const float lo = nf4_level_sel((tid >> 4) & 15);
+        const uint32_t base = static_cast<uint32_t>(tid >> 4) * 128 + (tid & 15) * 4;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float hi = nf4_level_sel(2 * k + (tid >> 8));
+            *lds<lds_u32>(base + k * 32 * 128) = pack_half2(hi, lo);
+            *lds<lds_u32>(base + k * 32 * 128 + 64) = pack_half2(level_rest(hi), level_rest(lo));
+        }
     }
 }
 
@@ -181,20 +202,25 @@ __device__ __forceinline__ void build_table(int tid) {
 // one paired read they would land in adjacent registers and need moves),
 // so one v_perm address serves both and every read lands in its fragment
 // register.
+// With 16 replicas (MT = 2) `ch` is 8*(lane%16) and the permuted address is
+// halved: byte*128 + 4*(lane%16), entries of 128 bytes.
+template <int MT>
 __device__ __forceinline__ void decode8(uint32_t w, uint32_t ch, half8 &bh, half8 &br) {
-    const uint32_t a0 = __builtin_amdgcn_perm(w, ch, 0x0C0C0400u);
-    const uint32_t a1 = __builtin_amdgcn_perm(w, ch, 0x0C0C0500u);
-    const uint32_t a2 = __builtin_amdgcn_perm(w, ch, 0x0C0C0600u);
-    const uint32_t a3 = __builtin_amdgcn_perm(w, ch, 0x0C0C0700u);
+    constexpr uint32_t RO = Lds<MT>::kEntry / 2;
+    const int sh = MT == 1 ? 0 : 1;
+    const uint32_t a0 = __builtin_amdgcn_perm(w, ch, 0x0C0C0400u) >> sh;
+    const uint32_t a1 = __builtin_amdgcn_perm(w, ch, 0x0C0C0500u) >> sh;
+    const uint32_t a2 = __builtin_amdgcn_perm(w, ch, 0x0C0C0600u) >> sh;
+    const uint32_t a3 = __builtin_amdgcn_perm(w, ch, 0x0C0C0700u) >> sh;
     u32x4v h, r;
     h.x = *lds<lds_u32>(a0);
     h.y = *lds<lds_u32>(a1);
     h.z = *lds<lds_u32>(a2);
     h.w = *lds<lds_u32>(a3);
-    r.x = __hip_atomic_load(lds<lds_u32>(a0 + 128), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    r.y = __hip_atomic_load(lds<lds_u32>(a1 + 128), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    r.z = __hip_atomic_load(lds<lds_u32>(a2 + 128), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    r.w = __hip_atomic_load(lds<lds_u32>(a3 + 128), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    r.x = __hip_atomic_load(lds<lds_u32>(a0 + RO), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    r.y = __hip_atomic_load(lds<lds_u32>(a1 + RO), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    r.z = __hip_atomic_load(lds<lds_u32>(a2 + RO), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    r.w = __hip_atomic_load(lds<lds_u32>(a3 + RO), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     bh = __builtin_bit_cast(half8, h);
     br = __builtin_bit_cast(half8, r);
 }
@@ -256,24 +282,28 @@ __device__ __forceinline__ void issue_unit(Unit &u, const UnitBase &b, int k0, b
 // tid + 512j is token row c/64 = tid/64 + 8j, elements 4*(tid%64) .. +4 of
 // the sub-slice. Rows >= M load row 0: they only feed output rows >= M,
 // which are never stored.
+template <int MT>
 struct XBase {
-    const float *p[4];
+    const float *p[4 * MT];
 };
 
-__device__ __forceinline__ XBase x_base(const float *x, int M, int K, int tid) {
-    XBase b;
+template <int MT>
+__device__ __forceinline__ XBase<MT> x_base(const float *x, int M, int K, int tid) {
+    XBase<MT> b;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 4 * MT; ++j) {
         const int m = (tid >> 6) + 8 * j;
         b.p[j] = x + static_cast<size_t>(m < M ? m : 0) * K + 4 * (tid & 63);
     }
     return b;
 }
 
-__device__ __forceinline__ void load_x(f32x4 (&xr)[4], const XBase &b, int k0, bool real, const float *dummy) {
+template <int MT>
+__device__ __forceinline__ void load_x(f32x4 (&xr)[4 * MT], const XBase<MT> &b, int k0, bool real,
+                                       const float *dummy) {
     const uintptr_t mask = real_mask(real), d = reinterpret_cast<uintptr_t>(dummy);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4 * MT; ++j)
         xr[j] = gload<f32x4>(reinterpret_cast<const void *>((reinterpret_cast<uintptr_t>(b.p[j] + k0) & mask) |
                                                             (d & ~mask)));
     // Issued where written: sunk below the MFMA work, these loads would
@@ -285,9 +315,10 @@ __device__ __forceinline__ void load_x(f32x4 (&xr)[4], const XBase &b, int k0, b
 // consecutive 8-byte pieces of a row): hi = fp16(x) and lo = fp16(x - hi),
 // both rounded toward zero (packed conversions); x - hi is exact in fp32
 // and lo keeps its leading 11 bits, below 2^-22 of x.
-__device__ __forceinline__ void stage_x(const f32x4 (&xr)[4], int tid) {
+template <int MT>
+__device__ __forceinline__ void stage_x(const f32x4 (&xr)[4 * MT], int tid) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 4 * MT; ++j) {
         const int m = (tid >> 6) + 8 * j;
         const f32x4 v = xr[j];
         typedef __fp16 half2v __attribute__((ext_vector_type(2)));
@@ -295,9 +326,10 @@ __device__ __forceinline__ void stage_x(const f32x4 (&xr)[4], int tid) {
         const half2v h23 = __builtin_amdgcn_cvt_pkrtz(v.z, v.w);
         const half2v l01 = __builtin_amdgcn_cvt_pkrtz(v.x - static_cast<float>(h01.x), v.y - static_cast<float>(h01.y));
         const half2v l23 = __builtin_amdgcn_cvt_pkrtz(v.z - static_cast<float>(h23.x), v.w - static_cast<float>(h23.y));
-        const uint32_t addr = kXOff + (m * kRS + 4 * (tid & 63)) * 2;
+        const uint32_t addr = Lds<MT>::kXOff + (m * kRS + 4 * (tid & 63)) * 2;
         *lds<lds_u32x2>(addr) = u32x2v{__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)};
-        *lds<lds_u32x2>(addr + kXLo) = u32x2v{__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
+        *lds<lds_u32x2>(addr + Lds<MT>::kXLo) =
+            u32x2v{__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
     }
 }
 
@@ -317,40 +349,51 @@ __device__ __forceinline__ void to_mfma_layout(const Unit &u, u32x4v (&qm)[4], f
     sc = *lds<lds_f32x4>(sst + nl * 16);
 }
 
-// acc[t] += blockwise-scaled product of unit t (NT units: the wave's row
-// tiles, one sub-slice) with the staged activations. Each A fragment is
-// read once for all NT tiles; the tiles' MFMA chains interleave. `arow` is
-// the LDS address of the lane's A row plus its half.
-template <int NT>
-__device__ __forceinline__ void compute_units(f32x16 (&acc)[NT], const Unit *u, uint32_t arow, uint32_t cst,
+// acc[t][mt] += blockwise-scaled product of unit t (NT units: the wave's
+// row tiles, one sub-slice) with token tile mt of the staged activations.
+// Each A fragment is read once for all NT row tiles and each decoded B
+// fragment feeds all MT token tiles; the MFMA chains interleave. `arow` is
+// the LDS address of the lane's A row plus its half in token tile 0.
+template <int NT, int MT>
+__device__ __forceinline__ void compute_units(f32x16 (&acc)[NT][MT], const Unit *u, uint32_t arow, uint32_t cst,
                                               uint32_t sst, int lane, uint32_t ch) {
+    constexpr uint32_t kTileX = 32 * kRS * 2;     // bytes of one token tile's hi rows
     u32x4v qm[NT][4];
     f32x4 sc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) to_mfma_layout(u[t], qm[t], sc[t], cst, sst, lane);
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-        f32x16 cb[NT];
+        f32x16 cb[NT][MT];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t e = arow + (64 * b + 8 * j) * 2;
-            const half8 ah = *lds<lds_half8>(e);
-            const half8 al = *lds<lds_half8>(e + kXLo);
+            half8 ah[MT], al[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                ah[mt] = *lds<lds_half8>(e + mt * kTileX);
+                al[mt] = *lds<lds_half8>(e + mt * kTileX + Lds<MT>::kXLo);
+            }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const uint32_t w = j == 0 ? qm[t][b].x : j == 1 ? qm[t][b].y : j == 2 ? qm[t][b].z : qm[t][b].w;
                 half8 bh, br;
-                decode8(w, ch, bh, br);
-                cb[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, j == 0 ? f32x16{} : cb[t], 0, 0, 0);
-                cb[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, cb[t], 0, 0, 0);
-                cb[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, br, cb[t], 0, 0, 0);
+                decode8<MT>(w, ch, bh, br);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    f32x16 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[mt], bh, j == 0 ? f32x16{} : cb[t][mt], 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[mt], bh, c, 0, 0, 0);
+                    cb[t][mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[mt], br, c, 0, 0, 0);
+                }
             }
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const float sblk = b == 0 ? sc[t].x : b == 1 ? sc[t].y : b == 2 ? sc[t].z : sc[t].w;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[t][r] = fmaf(sblk, cb[t][r], acc[t][r]);
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[t][mt][r] = fmaf(sblk, cb[t][mt][r], acc[t][mt][r]);
         }
         // One block at a time: otherwise the scheduler hoists every block's
         // table reads and runs out of registers.
@@ -359,15 +402,17 @@ __device__ __forceinline__ void compute_units(f32x16 (&acc)[NT], const Unit *u, 
 }
 
 // Wave w owns row tiles t < NT of the workgroup's row group (256*NT rows):
-// rows group0 + 256t + 32w. A unit is (sub-slice i, tile t); ring slot
-// (i*NT + t) % R holds it.
-template <int NT>
+// rows group0 + 256t + 32w, against MT token tiles of 32 (tokens 32mt ..).
+// A unit is (sub-slice i, tile t); ring slot (i*NT + t) % R holds it.
+template <int NT, int MT>
 __global__ __launch_bounds__(kMmThreads) void nf4_mm_kernel(MmArgs a) {
     // Ring of weight units in registers: four sub-slices ahead with one
-    // tile, one sub-slice (two units) ahead with two (the register budget).
-    constexpr int R = NT == 1 ? 4 : 2;
+    // row tile and one token tile, else two units ahead (the register
+    // budget).
+    constexpr int R = NT == 1 && MT == 1 ? 4 : 2;
     constexpr int SP = R / NT;                   // sub-slices per ring pass
-    static_assert(NT == 1 || NT == 2, "one or two row tiles per wave");
+    static_assert((NT == 1 || NT == 2) && (MT == 1 || MT == 2) && NT * MT <= 2, "tiles per wave");
+    using L = Lds<MT>;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: segment choice in scalar registers
@@ -391,26 +436,28 @@ __global__ __launch_bounds__(kMmThreads) void nf4_mm_kernel(MmArgs a) {
     // Loads past the slice's end (a ring refill beyond its last sub-slice)
     // are dummies of one line each, so every pass issues the same sequence
     // and the compiler's wait counts stay exact.
-    const XBase xb = x_base(x, M, K, tid);
+    const XBase<MT> xb = x_base<MT>(x, M, K, tid);
     UnitBase ub[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) ub[t] = unit_base(tr[t], K, lane);
-    f32x4 xr[4];
+    f32x4 xr[4 * MT];
     Unit ring[R];
-    load_x(xr, xb, kw0, true, x);
+    load_x<MT>(xr, xb, kw0, true, x);
 #pragma unroll
     for (int r = 0; r < R; ++r) issue_unit(ring[r], ub[r % NT], kw0 + (r / NT) * kSub, r / NT < nsub, tr[r % NT].w);
-    build_table(tid);
+    build_table<MT>(tid);
 
-    const uint32_t ch = nl * 4;
-    uint32_t arow = kXOff + (nl * kRS + 32 * h) * 2;
+    const uint32_t ch = MT == 1 ? nl * 4 : (nl & 15) * 8;
+    uint32_t arow = L::kXOff + (nl * kRS + 32 * h) * 2;
     asm volatile("" : "+v"(arow));               // one base register: element offsets stay immediates
-    const uint32_t cst = kCOff + wave * 32 * kCRow, sst = kSOff + wave * 32 * 16;
-    f32x16 acc[NT];
+    const uint32_t cst = L::kCOff + wave * 32 * kCRow, sst = L::kSOff + wave * 32 * 16;
+    f32x16 acc[NT][MT];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[t][mt][r] = 0.0f;
 
     // Sub-slice i = p0 + PS: stage its activations between two barriers,
     // fetch i+1's, compute its NT units (ring slots PS*NT ..) and refill
@@ -421,16 +468,17 @@ __global__ __launch_bounds__(kMmThreads) void nf4_mm_kernel(MmArgs a) {
         const int i = p0 + PS;
         if (i < nsub) {
             __syncthreads();                     // every wave is done with sub-slice i-1's activations
-            stage_x(xr, tid);
+            stage_x<MT>(xr, tid);
             __syncthreads();                     // sub-slice i's activations (and the table) visible
         }
-        load_x(xr, xb, kw0 + (i + 1) * kSub, i + 1 < nsub, x);
-        if (i < nsub) compute_units<NT>(acc, ring + PS * NT, arow, cst, sst, lane, ch);
+        load_x<MT>(xr, xb, kw0 + (i + 1) * kSub, i + 1 < nsub, x);
+        if (i < nsub) compute_units<NT, MT>(acc, ring + PS * NT, arow, cst, sst, lane, ch);
 #pragma unroll
         for (int t = 0; t < NT; ++t) issue_unit(ring[PS * NT + t], ub[t], kw0 + (i + SP) * kSub, i + SP < nsub, tr[t].w);
     };
     for (int p0 = 0; p0 < nsub; p0 += SP) {
         step(p0, std::integral_constant<int, 0>{});
+        if constexpr (SP == 2) step(p0, std::integral_constant<int, 1>{});
         if constexpr (SP == 4) {
             step(p0, std::integral_constant<int, 1>{});
             step(p0, std::integral_constant<int, 2>{});
@@ -438,26 +486,31 @@ __global__ __launch_bounds__(kMmThreads) void nf4_mm_kernel(MmArgs a) {
         }
     }
 
-    // Accumulator r of lane l is C[token 8*(r/4) + 4*h + r%4][row nl].
+    // Accumulator r of token tile mt, lane l is C[token 32mt + 8*(r/4) +
+    // 4*h + r%4][row nl].
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int n = tr[t].local0 + nl;
         if (n >= tr[t].n) continue;
-        if (a.part == nullptr) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = 8 * (r >> 2) + 4 * h + (r & 3);
-                if (m < a.M) {
-                    float *yp = tr[t].y + static_cast<size_t>(m) * tr[t].n + n;
-                    *yp = a.add ? *yp + acc[t][r] : acc[t][r];
+        for (int mt = 0; mt < MT; ++mt) {
+            if (a.part == nullptr) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (m < a.M) {
+                        float *yp = tr[t].y + static_cast<size_t>(m) * tr[t].n + n;
+                        *yp = a.add ? *yp + acc[t][mt][r] : acc[t][mt][r];
+                    }
                 }
-            }
-        } else {
-            float *const ps = a.part + static_cast<size_t>(slice) * a.M * a.N + group0 + t * kGroupRows + wave * 32 + nl;
+            } else {
+                float *const ps =
+                    a.part + static_cast<size_t>(slice) * a.M * a.N + group0 + t * kGroupRows + wave * 32 + nl;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = 8 * (r >> 2) + 4 * h + (r & 3);
-                if (m < a.M) ps[static_cast<size_t>(m) * a.N] = acc[t][r];
+                for (int r = 0; r < 16; ++r) {
+                    const int m = 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (m < a.M) ps[static_cast<size_t>(m) * a.N] = acc[t][mt][r];
+                }
             }
         }
     }
@@ -505,13 +558,14 @@ size_t nf4_mfma_scratch_floats(int M, int N, int K) {
 }
 
 // Row tiles per wave and sub-slices per slice for N stacked rows over K on
-// `cus` CUs: two tiles per wave (each activation fragment read from LDS
-// feeds two tiles) once the 512-row groups number at least 16, and the
-// fewest slices that still give every CU a workgroup (one workgroup fits a
-// CU).
-void nf4_mfma_plan(int N, int K, int cus, int &nt, int &q) {
+// `cus` CUs, for passes of M tokens: two tiles per wave (each activation
+// fragment read from LDS feeds two tiles) once the 512-row groups number
+// at least 16 and a pass has one token tile (M <= 32; two token tiles take
+// the registers a second row tile would), and the fewest slices that still
+// give every CU a workgroup (one workgroup fits a CU).
+void nf4_mfma_plan(int N, int K, int M, int cus, int &nt, int &q) {
     const int nsub = K / kSub;
-    nt = (N + 2LL * kGroupRows - 1) / (2LL * kGroupRows) >= 16 ? 2 : 1;
+    nt = M <= 32 && (N + 2LL * kGroupRows - 1) / (2LL * kGroupRows) >= 16 ? 2 : 1;
     const long long groups = (N + static_cast<long long>(kGroupRows) * nt - 1) / (static_cast<long long>(kGroupRows) * nt);
     q = nsub;
     for (int cand = 1; cand < nsub; ++cand) {
@@ -522,8 +576,9 @@ void nf4_mfma_plan(int N, int K, int cus, int &nt, int &q) {
     }
 }
 
-// The GEMM pass with an explicit plan (nt = 1 or 2 row tiles per wave,
-// q >= 1 sub-slices per slice).
+// The GEMM pass of M <= 64 tokens with an explicit plan (nt = 1 or 2 row
+// tiles per wave, q >= 1 sub-slices per slice; nt = 1 when M > 32: two
+// token tiles).
 int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, int M, bool add, float *part,
                           size_t part_floats, int nt, int q, const SliceTail *tail) {
     MmArgs args{};
@@ -541,7 +596,7 @@ int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, 
             args.end[i] = 0x7fffffff;
         }
     }
-    if ((nt != 1 && nt != 2) || q < 1 || M < 1 || M > 32) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    if ((nt != 1 && nt != 2) || q < 1 || M < 1 || M > 64 || (M > 32 && nt != 1)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     args.nseg = nseg;
     args.x = A;
     args.M = M;
@@ -564,15 +619,18 @@ int nf4_mfma_pass_planned(const RowsOut *outs, int nseg, const float *A, int K, 
     hipStream_t s = current_stream();
     static bool lds_set = false;                 // the attribute is per kernel, per process
     if (!lds_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(nf4_mm_kernel<1>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsBytes));
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(nf4_mm_kernel<2>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsBytes));
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(nf4_mm_kernel<1, 1>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(Lds<1>::kBytes));
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(nf4_mm_kernel<2, 1>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(Lds<1>::kBytes));
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(nf4_mm_kernel<1, 2>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(Lds<2>::kBytes));
         lds_set = true;
     }
     const dim3 grid(slices, static_cast<unsigned>(groups));
-    if (nt == 2) hipLaunchKernelGGL(nf4_mm_kernel<2>, grid, dim3(kMmThreads), kLdsBytes, s, args);
-    else hipLaunchKernelGGL(nf4_mm_kernel<1>, grid, dim3(kMmThreads), kLdsBytes, s, args);
+    if (M > 32) hipLaunchKernelGGL((nf4_mm_kernel<1, 2>), grid, dim3(kMmThreads), Lds<2>::kBytes, s, args);
+    else if (nt == 2) hipLaunchKernelGGL((nf4_mm_kernel<2, 1>), grid, dim3(kMmThreads), Lds<1>::kBytes, s, args);
+    else hipLaunchKernelGGL((nf4_mm_kernel<1, 1>), grid, dim3(kMmThreads), Lds<1>::kBytes, s, args);
     if (tail) return enqueue_slice_tail(*tail, args.part, slices, M, args.N);
     if (slices > 1) return enqueue_slice_sum(args.y, args.end, nseg, M, args.N, args.part, slices, add);
     return ALJABR_ROCM_OK;
@@ -599,7 +657,7 @@ int enqueue_slice_sum(float *const *ys, const int *ends, int nseg, int M, int N,
 
 int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M, bool add,
                            float *part, size_t part_floats, const SliceTail *tail) {
-    if (nseg < 1 || nseg > 3 || M < 2 || K % kSub != 0 || bs_shift != 6 || !aligned(A, 16) || (tail && M > 32))
+    if (nseg < 1 || nseg > 3 || M < 2 || K % kSub != 0 || bs_shift != 6 || !aligned(A, 16) || (tail && M > 64))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     long long n = 0;
     for (int i = 0; i < nseg; ++i) {
@@ -609,12 +667,13 @@ int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K,
         n += outs[i].n;
     }
     if (n > 0x7fff0000LL) return ALJABR_ROCM_ERR_UNSUPPORTED;
-    int nt = 1, q = 1;
-    nf4_mfma_plan(static_cast<int>(n), K, device_cu_count() > 0 ? device_cu_count() : 256, nt, q);
-    // Passes of up to 32 tokens (one m-tile); a pass's outputs are the rows
-    // m0 .. m0 + mm - 1 of each segment.
-    for (int m0 = 0; m0 < M; m0 += 32) {
-        const int mm = M - m0 < 32 ? M - m0 : 32;
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    // Passes of up to 64 tokens (two token tiles); a pass's outputs are the
+    // rows m0 .. m0 + mm - 1 of each segment.
+    for (int m0 = 0; m0 < M; m0 += 64) {
+        const int mm = M - m0 < 64 ? M - m0 : 64;
+        int nt = 1, q = 1;
+        nf4_mfma_plan(static_cast<int>(n), K, mm, cus, nt, q);
         RowsOut o[3];
         for (int i = 0; i < nseg; ++i) {
             o[i] = outs[i];

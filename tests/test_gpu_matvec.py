@@ -123,17 +123,19 @@ def test_gguf_mfma_is_deterministic(rocm, dev, oracle, qtype):
     assert rel_l2(outs[0], oracle.q_matvec(ot, enc, x, n, k).ravel()) <= TOL
 
 
-# NF4 small-M GEMM on the matrix cores (passes of 32 tokens, K % 256 == 0;
-# M = 2..4 with K % 2048 == 0 take the fp32 rows kernel): M across the pass
-# boundaries (32, 33, 64, 65, 100), ragged N, K of one to 56 sub-slices, the
-# Llama MLP shapes, one K slice per workgroup and several (partials summed in
+# NF4 small-M GEMM on the matrix cores (passes of up to 64 tokens: one
+# 32-token tile, or two sharing each decoded weight fragment; K % 256 == 0;
+# M = 2..4 with K % 2048 == 0 take the fp32 rows kernel): M across the tile
+# and pass boundaries (32, 33, 40, 64, 65, 100, 129), ragged N, K of one to
+# 56 sub-slices, the Llama MLP shapes, one K slice per workgroup and several (partials summed in
 # slice order by a second kernel). Both paths are fp32 accurate: every token
 # row within 1e-5 of the oracle.
 @pytest.mark.parametrize("n,k,m", [(300, 1024, 2), (300, 1024, 3), (257, 2048, 8), (300, 1024, 31), (300, 1024, 32),
                                    (300, 1024, 33), (129, 512, 64), (300, 1024, 65), (77, 1536, 100),
                                    (14336, 4096, 16), (4096, 14336, 16), (4096, 14336, 64), (1000, 4096, 5),
                                    (300, 6144, 17),
-                                   (8200, 4096, 32), (14336, 4096, 33), (257, 2048, 2)])
+                                   (8200, 4096, 32), (14336, 4096, 33), (257, 2048, 2), (14336, 4096, 64),
+                                   (6144, 4096, 40), (300, 1024, 129)])
 def test_nf4_mfma_small_m(rocm, dev, oracle, n, k, m):
     codes, absmax = _nf4_case(oracle, n, k, seed=3)
     x = oracle.normal(71 + m, m * k)
@@ -148,7 +150,7 @@ def test_nf4_mfma_small_m(rocm, dev, oracle, n, k, m):
         assert rel_l2(got[i * n:(i + 1) * n], y_ref[i * n:(i + 1) * n]) <= 1e-5, i
 
 
-@pytest.mark.parametrize("n,k,m", [(14336, 4096, 16), (4096, 14336, 32), (6144, 4096, 7)])
+@pytest.mark.parametrize("n,k,m", [(14336, 4096, 16), (4096, 14336, 32), (6144, 4096, 7), (14336, 4096, 64)])
 def test_nf4_mfma_is_deterministic(rocm, dev, oracle, n, k, m):
     """The same GEMM twice gives the same bits (K slices are summed in a
     fixed order, no float atomics)."""
@@ -271,9 +273,10 @@ def test_matvec_argument_errors(rocm, dev):
 # Token-pass loops must cover exactly M rows: C rows at and past M keep a
 # sentinel and every row below M equals the oracle. M = 2..7 leave a short last
 # Q4_0/Q8_0 pass (8 tokens per pass), 10 a two-token pass, 31 and 33 a last
-# pass of 7 and a single trailing token, across every batched row format.
+# pass of 7 and a single trailing token, 47 a second NF4 token tile of 15
+# rows, across every batched row format.
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "q4_k", "q6_k", "nf4", "f16"])
-@pytest.mark.parametrize("m", [2, 3, 5, 10, 31, 33])
+@pytest.mark.parametrize("m", [2, 3, 5, 10, 31, 33, 47])
 def test_batched_passes_stay_in_bounds(rocm, dev, oracle, fmt, m):
     n, k, pad = 320, 1024, 3
     w = oracle.normal(101 + m, n * k, 0.0, 0.02)
