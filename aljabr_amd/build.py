@@ -25,7 +25,11 @@ HIPCC = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc
 # Packed-FP32 instructions are disabled for all device code (the compiler must
 # not form v_pk_{add,mul,fma}_f32); the host pass warns that it does not know
 # the feature, which is harmless.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Kernel-argument preload: the leading scalar arguments of a kernel (up to 14
+# dwords on gfx950) arrive in SGPRs at wave launch instead of being read from
+# the argument buffer; the compiler also emits the fallback that reads them.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm",
+                "-amdgpu-kernarg-preload-count=14"]
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function"]
 
 

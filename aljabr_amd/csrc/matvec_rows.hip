@@ -113,6 +113,7 @@ struct RowsSeg {
 constexpr int kXPlain = 0;     // x
 constexpr int kXNorm = 1;      // RMSNorm: (x * 1/sqrt(mean(x^2) + eps)) * norm_w
 constexpr int kEStore = 0;     // y = v
+constexpr int kEStore3 = 4;    // y = v, three stacked segments (segment 2's pointers read from the struct)
 constexpr int kEAdd = 1;       // y += v (residual)
 constexpr int kESwiGLU = 2;    // interleaved gate/up pairs: y = silu(gate) * up
 constexpr int kERopeKV = 3;    // Q/K/V pairs: RoPE on q (stored) and k, k and v appended to the fp16 caches
@@ -133,6 +134,66 @@ struct RowsArgs {
     int gelu;                // kESwiGLU: the tanh GELU of the Metal FFN instead of SiLU
 };
 
+// The arguments a wave needs before its first weight load: segments 0 and 1
+// (pointers and ends), the activations and the shape. rows_kernel takes them
+// as its leading scalar arguments, which the build preloads into SGPRs at wave
+// launch (14 dwords, the hardware limit); read from the argument struct they
+// cost two dependent scalar-memory round trips (the shape, then the
+// pointers), ~0.7 us before the first weight request under a full HBM queue.
+// K = S * 2048 on this path, so the shape packs into one word:
+// S | G << 4 | bs_shift << 9 | hd_shift << 14.
+struct RowsHot {
+    const float *x;
+    const uint8_t *w0, *w1, *w2;
+    const float *s0, *s1, *s2;   // NF4 absmax of segments 0, 1 and 2
+    int N, end0, end1;
+    int S, G, K, bs_shift, hd_shift;
+};
+
+__host__ __device__ inline int rows_shape_word(const RowsArgs &a) {
+    return a.S | (a.G << 4) | (a.bs_shift << 9) | (a.hd_shift << 14);
+}
+
+__device__ __forceinline__ RowsHot rows_hot(const float *x, const uint8_t *w0, const float *s0, const uint8_t *w1,
+                                            const float *s1, int N, int end0, int end1, int shape) {
+    RowsHot h;
+    h.x = x;
+    h.w0 = w0;
+    h.w1 = w1;
+    h.s0 = s0;
+    h.s1 = s1;
+    h.N = N;
+    h.end0 = end0;
+    h.end1 = end1;
+    h.S = shape & 15;
+    h.G = (shape >> 4) & 31;
+    h.K = h.S * kChunk;
+    h.bs_shift = (shape >> 9) & 31;
+    h.hd_shift = (shape >> 14) & 15;
+    h.w2 = w0;               // set by with_seg2 for three-segment launches
+    h.s2 = s0;
+    return h;
+}
+
+// Segment 2's pointers live only in the argument struct, so only the
+// epilogues of three-segment launches (kEStore3, kERopeKV) read them: every
+// other launch starts its loads without waiting for the struct.
+template <int EPI>
+__device__ __forceinline__ void with_seg2(RowsHot &h, const RowsArgs &a) {
+    if constexpr (EPI == kEStore3 || EPI == kERopeKV) {
+        h.w2 = a.seg[2].w;
+        h.s2 = a.seg[2].absmax;
+    }
+}
+
+__device__ __forceinline__ RowsHot rows_hot(const RowsArgs &a) {
+    RowsHot h = rows_hot(a.x, a.seg[0].w, a.seg[0].absmax, a.seg[1].w, a.seg[1].absmax, a.N, a.seg[0].end,
+                         a.seg[1].end, rows_shape_word(a));
+    h.w2 = a.seg[2].w;
+    h.s2 = a.seg[2].absmax;
+    return h;
+}
+
 // Segment of stacked row r and its row within the segment. The row map
 // follows from the epilogue at compile time (per-row runtime tests cost the
 // plain kernel over a microsecond): kESwiGLU interleaves two segments,
@@ -144,7 +205,7 @@ struct RowRef {
 };
 
 template <int EPI, int T>
-__device__ __forceinline__ RowRef row_ref(const RowsArgs &a, int r) {
+__device__ __forceinline__ RowRef row_ref(const RowsHot &h, int r) {
     RowRef f;
     if constexpr (EPI == kESwiGLU) {
         // A wave's T rows are T/2 consecutive gate rows, then the same T/2 up
@@ -154,12 +215,12 @@ __device__ __forceinline__ RowRef row_ref(const RowsArgs &a, int r) {
         f.s2 = false;
         f.local = blk * (T / 2) + (f.s1 ? t - T / 2 : t);
     } else {
-        f.s1 = r >= a.seg[0].end;
-        f.s2 = r >= a.seg[1].end;
-        f.local = r - (f.s2 ? a.seg[1].end : f.s1 ? a.seg[0].end : 0);
+        f.s1 = r >= h.end0;
+        f.s2 = r >= h.end1;
+        f.local = r - (f.s2 ? h.end1 : f.s1 ? h.end0 : 0);
         if constexpr (EPI == kERopeKV) {
             if (!f.s2) {
-                const int hd = 1 << a.hd_shift, q = f.local & (hd - 1);
+                const int hd = 1 << h.hd_shift, q = f.local & (hd - 1);
                 f.local = (f.local - q) + (q >> 1) + (q & 1) * (hd >> 1);
             }
         }
@@ -198,29 +259,29 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int lane, int bs_shift) {
 }
 
 template <int FMT, int EPI, int T>
-__device__ __forceinline__ void load_row(RowWords<FMT> &d, const RowsArgs &a, int row, int chunk,
+__device__ __forceinline__ void load_row(RowWords<FMT> &d, const RowsHot &h, const RowsArgs &a, int row, int chunk,
                                          const LaneOffsets &o) {
-    const RowRef f = row_ref<EPI, T>(a, row);
+    const RowRef f = row_ref<EPI, T>(h, row);
     const size_t local = static_cast<size_t>(f.local);
-    const uint8_t *w = seg_pick(f, a.seg[0].w, a.seg[1].w, a.seg[2].w);
+    const uint8_t *w = seg_pick(f, h.w0, h.w1, h.w2);
     if constexpr (FMT == kFmtNF4) {
         // bs divides K here (bs <= 2048 = the chunk), so the row's blocks
         // start at local * K / bs.
-        const float *absmax = seg_pick(f, a.seg[0].absmax, a.seg[1].absmax, a.seg[2].absmax);
-        const uint8_t *rw = w + local * (static_cast<size_t>(a.K) >> 1) + static_cast<size_t>(chunk) * (kChunk / 2);
+        const float *absmax = seg_pick(f, h.s0, h.s1, h.s2);
+        const uint8_t *rw = w + local * (static_cast<size_t>(h.K) >> 1) + static_cast<size_t>(chunk) * (kChunk / 2);
         const uint8_t *rs = reinterpret_cast<const uint8_t *>(
-            absmax + ((local * static_cast<size_t>(a.K) + static_cast<size_t>(chunk) * kChunk) >> a.bs_shift));
+            absmax + ((local * static_cast<size_t>(h.K) + static_cast<size_t>(chunk) * kChunk) >> h.bs_shift));
         d.q = load_stream16(rw + o.w);
         d.s = *reinterpret_cast<const float *>(rs + o.s);
     } else if constexpr (kquant_fmt(FMT)) {
         constexpr int BB = FMT == kFmtQ4K ? kQ4KBytes : kQ6KBytes;
-        const uint8_t *rw = w + local * (static_cast<size_t>(a.K >> 8) * BB) + static_cast<size_t>(chunk) * (8 * BB);
+        const uint8_t *rw = w + local * (static_cast<size_t>(h.K >> 8) * BB) + static_cast<size_t>(chunk) * (8 * BB);
         const int j = __lane_id() & 7;
         if constexpr (FMT == kFmtQ4K) load_q4k(d, rw + o.w, j);
         else load_q6k(d, rw + o.w, j);
     } else {
         constexpr int BB = FMT == kFmtQ4 ? 18 : 34;
-        const uint8_t *rw = w + local * (static_cast<size_t>(a.K >> 5) * BB) + static_cast<size_t>(chunk) * (64 * BB);
+        const uint8_t *rw = w + local * (static_cast<size_t>(h.K >> 5) * BB) + static_cast<size_t>(chunk) * (64 * BB);
         const uint8_t *p = rw + o.w;
         if constexpr (FMT == kFmtQ4) {
             d.a = load_stream16_a4(p);
@@ -408,7 +469,10 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
 // and PF rows stay in flight afterwards: a deeper prologue keeps HBM busy
 // while the activations arrive, a shallower steady state measured faster.
 template <int FMT, int T, int PF, int W, int XOP, int EPI, int P0>
-__global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
+__global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint8_t *w0, const float *s0,
+                                                      const uint8_t *w1, const float *s1, int N, int end0, int end1,
+                                                      int shape, RowsArgs a) {
+    RowsHot h = rows_hot(x, w0, s0, w1, s1, N, end0, end1, shape);
     static_assert(T >= 1 && T <= 32 && PF >= 1 && P0 >= PF && (W == 8 || W == 16), "tile shape");
     constexpr int TP = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : T <= 16 ? 16 : 32;   // butterfly width
     extern __shared__ float4 smem[];    // see kMainBytes
@@ -419,12 +483,12 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     const int lane = tid & 63;
     // Wave-uniform in a scalar register, so row and segment arithmetic is scalar.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int S = a.S;
+    const int S = h.S;
     const int chunk = wave % S;
     const int grp = wave / S;
     float2 *tbl2 = reinterpret_cast<float2 *>(smem);
 
-    if (grp >= a.G) {
+    if (grp >= h.G) {
         // Helper wave (when S does not divide W): takes part in the table
         // build and meets the same workgroup barriers, nothing else.
         if constexpr (pair_table_fmt(FMT)) build_pair_table<FMT, W * 64>(tbl2, tid);
@@ -438,9 +502,10 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     // Each wave streams the T contiguous rows row0 .. row0 + T-1 of the
     // stacked row space (measured a few percent faster on MI355X than
     // interleaving rows across the grid).
-    const int row0 = (blockIdx.x * a.G + grp) * T;
+    const int row0 = (blockIdx.x * h.G + grp) * T;
     const int rstride = 1;
-    const LaneOffsets lo = lane_offsets<FMT>(lane, a.bs_shift);
+    const LaneOffsets lo = lane_offsets<FMT>(lane, h.bs_shift);
+    with_seg2<EPI>(h, a);
 
     // Activations first (vmcnt retires in order: waiting for them then
     // leaves the weight loads in flight).
@@ -449,7 +514,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) xl[j] = xm[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (stager) {
-        const f32x4 *xw = reinterpret_cast<const f32x4 *>(a.x + xoff);
+        const f32x4 *xw = reinterpret_cast<const f32x4 *>(h.x + xoff);
 #pragma unroll
         for (int j = 0; j < 8; ++j) xl[j] = xw[64 * j + lane];
         if constexpr (XOP == kXNorm) {
@@ -460,7 +525,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     }
     RowWords<FMT> rw[T];
 #pragma unroll
-    for (int t = 0; t < P0 && t < T; ++t) load_row<FMT, EPI, T>(rw[t], a, min(row0 + t * rstride, a.N - 1), chunk, lo);
+    for (int t = 0; t < P0 && t < T; ++t) load_row<FMT, EPI, T>(rw[t], h, a, min(row0 + t * rstride, h.N - 1), chunk, lo);
     // The table does not depend on the loads: build it while they fly.
     if constexpr (pair_table_fmt(FMT)) build_pair_table<FMT, W * 64>(tbl2, tid);
 
@@ -485,7 +550,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
             float tot = 0.0f;
             for (int c = 0; c < S; ++c) tot += ssq[c];
             const float inv =
-                1.0f / static_cast<float>(sqrt(static_cast<double>(tot / static_cast<float>(a.K) + a.eps)));
+                1.0f / static_cast<float>(sqrt(static_cast<double>(tot / static_cast<float>(h.K) + a.eps)));
 #pragma unroll
             for (int j = 0; j < 8; ++j) xl[j] = (xl[j] * inv) * xm[j];
         }
@@ -535,7 +600,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         if (t + PF < T && t + PF >= P0)
-            load_row<FMT, EPI, T>(rw[t + PF], a, min(row0 + (t + PF) * rstride, a.N - 1), chunk, lo);
+            load_row<FMT, EPI, T>(rw[t + PF], h, a, min(row0 + (t + PF) * rstride, h.N - 1), chunk, lo);
         float scale;
         const float dot = row_dot<FMT>(rw[t], xv, xsum, xsum2, odd, cl, tbl, scale);
         acc[t] = dot * scale;
@@ -549,11 +614,11 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
     __syncthreads();                                         // 2: partials written
     // The S chunk waves of group g are waves g*S .. g*S+S-1.
     const int r = row0 + lane;
-    if (chunk == 0 && lane < T && r < a.N) {
+    if (chunk == 0 && lane < T && r < h.N) {
         float v = 0.0f;
         for (int c = 0; c < S; ++c) v += part[grp * S + c][lane];
-        if constexpr (EPI == kEStore || EPI == kEAdd) {
-            const RowRef f = row_ref<EPI, T>(a, r);
+        if constexpr (EPI == kEStore || EPI == kEStore3 || EPI == kEAdd) {
+            const RowRef f = row_ref<EPI, T>(h, r);
             float *y = seg_pick(f, a.seg[0].y, a.seg[1].y, a.seg[2].y);
             if constexpr (EPI == kEAdd) y[f.local] += v;
             else y[f.local] = v;
@@ -562,7 +627,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
             if (lane < T / 2) {
                 float u = 0.0f;
                 for (int c = 0; c < S; ++c) u += part[grp * S + c][lane + T / 2];
-                a.seg[0].y[row_ref<EPI, T>(a, r).local] = a.gelu ? geglu_metal(v, u) : silu_ref(v) * u;
+                a.seg[0].y[row_ref<EPI, T>(h, r).local] = a.gelu ? geglu_metal(v, u) : silu_ref(v) * u;
             }
         } else if ((lane & 1) == 0) {
             // RoPE pairs (r, r + 1): T is even and row0 even, so both are this
@@ -570,11 +635,11 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
             float v1 = 0.0f;
             for (int c = 0; c < S; ++c) v1 += part[grp * S + c][lane + 1];
             {
-                const RowRef f = row_ref<EPI, T>(a, r);
+                const RowRef f = row_ref<EPI, T>(h, r);
                 const int p = a.pos[0];
                 const bool in_cache = p >= 0 && p < a.cap;
-                const int hd = 1 << a.hd_shift;
-                const int h = f.local >> a.hd_shift, i = f.local & (hd - 1);
+                const int hd = 1 << h.hd_shift;
+                const int hh = f.local >> h.hd_shift, i = f.local & (hd - 1);
                 if (!f.s1 && !f.s2) {                    // q: rotate, store fp32
                     rope_rotate(v, v1, a.rope_cs, a.cap, p, i, hd, a.rope_base);
                     a.seg[0].y[f.local] = v;
@@ -582,12 +647,12 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(RowsArgs a) {
                 } else if (!f.s2) {                      // k: rotate, append fp16
                     rope_rotate(v, v1, a.rope_cs, a.cap, p, i, hd, a.rope_base);
                     if (in_cache) {
-                        uint16_t *dst = a.kc + (static_cast<size_t>(h) * a.cap + p) * hd + i;
+                        uint16_t *dst = a.kc + (static_cast<size_t>(hh) * a.cap + p) * hd + i;
                         dst[0] = f32_to_f16_bits(v);
                         dst[hd >> 1] = f32_to_f16_bits(v1);
                     }
                 } else if (in_cache) {                   // v: rows local, local + 1, append fp16
-                    uint16_t *dst = a.vc + (static_cast<size_t>(h) * a.cap + p) * hd + i;
+                    uint16_t *dst = a.vc + (static_cast<size_t>(hh) * a.cap + p) * hd + i;
                     dst[0] = f32_to_f16_bits(v);
                     dst[1] = f32_to_f16_bits(v1);
                 }
@@ -608,7 +673,9 @@ void launch_cfg(const RowsArgs &args, hipStream_t s) {
     }
     const int rows_per_wg = args.G * T;
     const dim3 grid((args.N + rows_per_wg - 1) / rows_per_wg), block(W * 64);
-    hipLaunchKernelGGL((rows_kernel<FMT, T, PF, W, XOP, EPI, P0>), grid, block, lds, s, args);
+    hipLaunchKernelGGL((rows_kernel<FMT, T, PF, W, XOP, EPI, P0>), grid, block, lds, s, args.x, args.seg[0].w,
+                       args.seg[0].absmax, args.seg[1].w, args.seg[1].absmax, args.N, args.seg[0].end, args.seg[1].end,
+                       rows_shape_word(args), args);
 }
 
 // T rows per wave (2..32), 8 waves; loads PF rows ahead: 3 when a wave's
@@ -696,10 +763,11 @@ __global__ __launch_bounds__(512) void rows_mt_kernel(RowsArgs a) {
         for (int j = 0; j < 8; ++j) xl[j] = xw[64 * j + lane];
     }
     const LaneOffsets lo = lane_offsets<kFmtNF4>(lane, a.bs_shift);
+    const RowsHot h = rows_hot(a);
     RowWords<kFmtNF4> rw[T];
     if (!helper) {
 #pragma unroll
-        for (int t = 0; t < PF && t < T; ++t) load_row<kFmtNF4, kEStore, T>(rw[t], a, min(row0 + t, a.N - 1), chunk, lo);
+        for (int t = 0; t < PF && t < T; ++t) load_row<kFmtNF4, kEStore, T>(rw[t], h, a, min(row0 + t, a.N - 1), chunk, lo);
     }
     build_pair_table<kFmtNF4, W * 64>(tbl2, tid);
 
@@ -751,7 +819,7 @@ __global__ __launch_bounds__(512) void rows_mt_kernel(RowsArgs a) {
             for (int t = 0; t < TP; ++t) acc[mm][t] = 0.0f;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            if (t + PF < T) load_row<kFmtNF4, kEStore, T>(rw[t + PF], a, min(row0 + t + PF, a.N - 1), chunk, lo);
+            if (t + PF < T) load_row<kFmtNF4, kEStore, T>(rw[t + PF], h, a, min(row0 + t + PF, a.N - 1), chunk, lo);
             const uint32_t wv[4] = {rw[t].q.x, rw[t].q.y, rw[t].q.z, rw[t].q.w};
             float p0[MT], p1[MT];
 #pragma unroll
@@ -903,8 +971,13 @@ template <int FMT>
 int launch_fused(RowsArgs &args, int T, int epilogue, bool norm, hipStream_t s) {
     switch (epilogue) {
     case kRowsStore:
-        if (norm) launch_rows<FMT, kXNorm, kEStore>(args, T, s);
-        else launch_rows<FMT, kXPlain, kEStore>(args, T, s);
+        if (args.seg[1].end < args.N) {          // three segments
+            if (norm) launch_rows<FMT, kXNorm, kEStore3>(args, T, s);
+            else launch_rows<FMT, kXPlain, kEStore3>(args, T, s);
+        } else {
+            if (norm) launch_rows<FMT, kXNorm, kEStore>(args, T, s);
+            else launch_rows<FMT, kXPlain, kEStore>(args, T, s);
+        }
         return ALJABR_ROCM_OK;
     case kRowsAdd:
         if (norm) return ALJABR_ROCM_ERR_UNSUPPORTED;
