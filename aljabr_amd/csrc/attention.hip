@@ -11,11 +11,12 @@
 // workgroup serves all G = Hq/Hkv query heads of its KV head, so every K/V
 // byte is read once per query row. Inside a workgroup, a key row of D fp16
 // values is read by D/8 lanes (16 bytes each); the wave's lane groups walk
-// interleaved keys in tiles of 4, keep (max, sum, o[8]) per head in
-// registers, and reduce q.k across the group's lanes with DPP. Group states
-// are merged through LDS; with one split the workgroup writes the normalised
-// output, otherwise (m, l, o) partials go to scratch and a merge kernel
-// combines splits. Scores use exp2 with log2(e) folded into the query.
+// interleaved keys in tiles of 4 (2 when a chunk is one trip), keep (max,
+// sum, o[8]) per head in registers, and reduce q.k across the group's lanes
+// with DPP. A wave's group states are folded by lane shuffles and the wave
+// states merged through LDS; with one split the workgroup writes the
+// normalised output, otherwise (m, l, o) partials go to scratch and a merge
+// kernel combines splits. Scores use exp2 with log2(e) folded into the query.
 #include <cmath>
 #include <cstdlib>
 #include <mutex>
@@ -29,7 +30,6 @@ namespace aljabr {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kTile = 4;
 
 template <int LPK>
 __device__ __forceinline__ float group_sum(float v) {
@@ -200,14 +200,17 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, const flo
     merge_row<D, 256>(p, part_o, part_ml, splits, blockIdx.x, st);
 }
 
-template <int D, int G, bool F16, int WAVES, bool PAGED>
+// KT keys per group per trip (the tile): 4, or 2 where a workgroup's chunk
+// is one trip of 2-key tiles (every group busy, half the serial work per
+// lane).
+template <int D, int G, bool F16, int WAVES, bool PAGED, int KT>
 __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, int splits, int chunk,
                                                                 float *__restrict__ part_o,
                                                                 float *__restrict__ part_ml) {
     constexpr int LPK = D / 8;                 // lanes per key row
     constexpr int GPW = 64 / LPK;              // key groups per wave
     constexpr int NG = GPW * WAVES;            // key groups per workgroup
-    extern __shared__ float smem[];            // [NG][G][D + 2]
+    extern __shared__ float smem[];            // [WAVES][G][D + 2]
 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y / p.Sq;
@@ -232,11 +235,11 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
             return head_base + static_cast<long long>(key) * D;
         }
     };
-    KvRaw<F16> kn[kTile], vn[kTile];
+    KvRaw<F16> kn[KT], vn[KT];
     int mem_end;                                 // keys below this are rows that exist
     auto issue = [&](int tbase) {
 #pragma unroll
-        for (int t = 0; t < kTile; ++t) {
+        for (int t = 0; t < KT; ++t) {
             const int key = tbase + t;
             const long long r = row_at(key < mem_end ? key : k_begin);
             kn[t] = load_raw<F16>(p.k, r);
@@ -250,12 +253,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
         // to k_begin, which must then be a row of the sequence).
         sk = max(p.kv_len[b], 0);
         mem_end = min(k_begin + chunk, sk);
-        if (k_begin < sk) issue(k_begin + grp * kTile);
+        if (k_begin < sk) issue(k_begin + grp * KT);
     } else {
         // Rows [k_begin, mem_end) exist in memory whatever the visible length,
         // so the first tile's loads go out before kv_len has arrived.
         mem_end = min(k_begin + chunk, p.kv_len ? p.cap : p.Sk);
-        issue(k_begin + grp * kTile);
+        issue(k_begin + grp * KT);
         sk = p.kv_len ? min(max(p.kv_len[b], 0), p.cap) : p.Sk;   // never past the cache
     }
     int k_lo, k_hi;
@@ -288,13 +291,15 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
     const float *mrow = p.mask ? p.mask + static_cast<long long>(qi) * p.Sk : nullptr;
 
     // Software pipeline: the next tile's K/V rows are loaded while this one
-    // is computed (the last trip loads a clamped, in-range tile it never
-    // uses: a conditional load would make the compiler drain the queue).
-    for (int t0 = k_begin + grp * kTile; t0 < k_end; t0 += NG * kTile) {
-        float kr[kTile][8], vr[kTile][8];
-        bool valid[kTile];
+    // is computed. Only a group with another trip loads one: the tile is the
+    // only load in flight at the loop head, so the wait there is the one the
+    // tile needs anyway, and a group's last trip leaves nothing in flight
+    // (a prefetch past the end would be waited for before the merge).
+    for (int t0 = k_begin + grp * KT; t0 < k_end; t0 += NG * KT) {
+        float kr[KT][8], vr[KT][8];
+        bool valid[KT];
 #pragma unroll
-        for (int t = 0; t < kTile; ++t) {
+        for (int t = 0; t < KT; ++t) {
             valid[t] = t0 + t < k_end && (!PAGED || t0 + t >= k_lo);   // only the paged rule has a lower bound
             raw_to_f32<F16>(kn[t], kr[t]);
             raw_to_f32<F16>(vn[t], vr[t]);
@@ -305,20 +310,20 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
 #pragma unroll
             for (int i = 0; i < 8; ++i) vr[t][i] = valid[t] ? vr[t][i] : 0.0f;
         }
-        issue(t0 + NG * kTile);
-        float add[kTile];
+        if (t0 + NG * KT < k_end) issue(t0 + NG * KT);
+        float add[KT];
 #pragma unroll
-        for (int t = 0; t < kTile; ++t) {
+        for (int t = 0; t < KT; ++t) {
             add[t] = 0.0f;
             if (mrow && valid[t]) add[t] = mrow[t0 + t] * kLog2e;
             if (!valid[t]) add[t] = -INFINITY;
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            float s[kTile];
+            float s[KT];
             float tmax = -INFINITY;
 #pragma unroll
-            for (int t = 0; t < kTile; ++t) {
+            for (int t = 0; t < KT; ++t) {
                 float d = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) d = fmaf(qv[g][i], kr[t][i], d);
@@ -335,9 +340,9 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
             if (mn == -INFINITY) continue;             // nothing visible yet
             const float alpha = m[g] == -INFINITY ? 0.0f : exp2f(m[g] - mn);
             float psum = 0.0f;
-            float pr[kTile];
+            float pr[KT];
 #pragma unroll
-            for (int t = 0; t < kTile; ++t) {
+            for (int t = 0; t < KT; ++t) {
                 pr[t] = s[t] == -INFINITY ? 0.0f : exp2f(s[t] - mn);
                 psum += pr[t];
             }
@@ -346,34 +351,58 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
             for (int i = 0; i < 8; ++i) {
                 float acc = o[g][i] * alpha;
 #pragma unroll
-                for (int t = 0; t < kTile; ++t) acc = fmaf(pr[t], vr[t][i], acc);
+                for (int t = 0; t < KT; ++t) acc = fmaf(pr[t], vr[t][i], acc);
                 o[g][i] = acc;
             }
             m[g] = mn;
         }
     }
 
-    // Publish group states: smem[grp][g][0..D) = o, [D] = m, [D+1] = l.
+    // Fold the wave's key groups into one state: lanes `off` apart hold the
+    // same dims of two groups (m and l are uniform within a group); an empty
+    // state (m = -inf, l = o = 0) weighs 0.
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float *st = smem + (grp * G + g) * (D + 2);
+    for (int off = 32; off >= LPK; off >>= 1) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) st[sub * 8 + i] = o[g][i];
-        if (sub == 0) {
-            st[D] = m[g];
-            st[D + 1] = l[g];
+        for (int g = 0; g < G; ++g) {
+            const float m2 = __shfl_xor(m[g], off);
+            const float l2 = __shfl_xor(l[g], off);
+            float o2[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o2[i] = __shfl_xor(o[g][i], off);
+            const float mn = fmaxf(m[g], m2);
+            const float a = m[g] == -INFINITY ? 0.0f : exp2f(m[g] - mn);
+            const float c = m2 == -INFINITY ? 0.0f : exp2f(m2 - mn);
+            l[g] = fmaf(l[g], a, l2 * c);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[g][i] = fmaf(o[g][i], a, o2[i] * c);
+            m[g] = mn;
+        }
+    }
+
+    // Publish wave states: smem[wave][g][0..D) = o, [D] = m, [D+1] = l.
+    if (lane < LPK) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float *st = smem + (wave * G + g) * (D + 2);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) st[sub * 8 + i] = o[g][i];
+            if (sub == 0) {
+                st[D] = m[g];
+                st[D + 1] = l[g];
+            }
         }
     }
     __syncthreads();
 
-    // Merge the NG group states; one thread per (head, dim). All NG states
+    // Merge the WAVES wave states; one thread per (head, dim). All states
     // are read before any is used (the reads overlap instead of queueing
-    // behind each other); an empty group (m = -inf, l = o = 0) weighs 0.
+    // behind each other).
     for (int idx = threadIdx.x; idx < G * D; idx += WAVES * 64) {
         const int g = idx / D, dd = idx % D;
-        float mg[NG], lg[NG], og[NG];
+        float mg[WAVES], lg[WAVES], og[WAVES];
 #pragma unroll
-        for (int gr = 0; gr < NG; ++gr) {
+        for (int gr = 0; gr < WAVES; ++gr) {
             const float *st = smem + (gr * G + g) * (D + 2);
             mg[gr] = st[D];
             lg[gr] = st[D + 1];
@@ -381,11 +410,11 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
         }
         float M = -INFINITY;
 #pragma unroll
-        for (int gr = 0; gr < NG; ++gr) M = fmaxf(M, mg[gr]);
+        for (int gr = 0; gr < WAVES; ++gr) M = fmaxf(M, mg[gr]);
         float L = 0.0f, O = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
-            for (int gr = 0; gr < NG; ++gr) {
+            for (int gr = 0; gr < WAVES; ++gr) {
                 const float w = mg[gr] == -INFINITY ? 0.0f : exp2f(mg[gr] - M);
                 L = fmaf(lg[gr], w, L);
                 O = fmaf(og[gr], w, O);
@@ -490,23 +519,20 @@ __global__ void zero_i32_kernel(int *p) { *p = 0; }
 template <int D, int G, bool F16, bool PAGED, bool WIDE>
 int launch_split(const AttnParams &p, int splits, int chunk, float *part, hipStream_t s) {
     constexpr int WAVES = WIDE ? ((G <= 4) ? 8 : 4) : ((G <= 4) ? 4 : 2);
-    constexpr int NG = (64 / (D / 8)) * WAVES;
-    const size_t lds = static_cast<size_t>(NG) * G * (D + 2) * sizeof(float);
-    if constexpr (static_cast<size_t>(NG) * G * (D + 2) * sizeof(float) > 65536) {
-        static bool lds_set = false;             // the attribute is per kernel, per process
-        if (!lds_set) {
-            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_split_kernel<D, G, F16, WAVES, PAGED>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-            lds_set = true;
-        }
-    }
+    constexpr int NG = (64 / (D / 8)) * WAVES;    // key groups per workgroup
+    const size_t lds = static_cast<size_t>(WAVES) * G * (D + 2) * sizeof(float);
+    static_assert(static_cast<size_t>(WAVES) * G * (D + 2) * sizeof(float) <= 65536, "static LDS limit");
     const dim3 grid(splits, p.Hkv * p.Sq, p.B);
     const long long rows = static_cast<long long>(p.B) * p.Hq * p.Sq;
     // Partials: o as [rows][splits][D], then (m, l) as [rows][splits][2].
     float *part_o = part;
     float *part_ml = part ? part + rows * splits * D : nullptr;
-    hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES, PAGED>), grid, dim3(WAVES * 64), lds, s, p, splits, chunk,
-                       part_o, part_ml);
+    if (WIDE && chunk <= 2 * NG)
+        hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES, PAGED, 2>), grid, dim3(WAVES * 64), lds, s, p, splits,
+                           chunk, part_o, part_ml);
+    else
+        hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES, PAGED, 4>), grid, dim3(WAVES * 64), lds, s, p, splits,
+                           chunk, part_o, part_ml);
     if (splits > 1)
         hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, p, part_o,
                            part_ml, splits);
