@@ -452,14 +452,6 @@ __device__ __forceinline__ float geglu_metal(float g, float u) {
     return isfinite(y) ? y : 0.0f;
 }
 
-// Split-half RoPE of the pair (i, i + D/2) at position `pos`, the same
-// arithmetic as the stand-alone RoPE kernel (GGUFVectorOps.rope :383-440).
-__device__ __forceinline__ void rope_rotate(float &x0, float &x1, const float2 *table, int cap, int pos, int i,
-                                            int head_dim, float base) {
-    float c, s;
-    rope_angle(table, cap, pos, i, head_dim, base, c, s);
-    rope_apply(x0, x1, c, s);
-}
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
@@ -566,6 +558,25 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint
         }
     }
     __syncthreads();                                         // 1: table built, x staged
+    // Epilogue operands that the last phase would otherwise fetch after the
+    // row sums (one dependent memory round trip at the end of every wave):
+    // the residual rows (kEAdd) and the RoPE position (kERopeKV; its cos/sin
+    // pair, split-half RoPE with the stand-alone RoPE kernel's arithmetic
+    // (GGUFVectorOps.rope :383-440), is requested at mid-loop once the
+    // position has arrived). Each output element belongs to one finishing
+    // lane, so reading it early is the same read.
+    const int r = row0 + lane;
+    const bool finisher = chunk == 0 && lane < T && r < h.N;
+    float y_old = 0.0f;
+    int rope_p = 0;
+    float rope_c = 1.0f, rope_s = 0.0f;
+    if constexpr (EPI == kEAdd) {
+        if (finisher) {
+            const RowRef f = row_ref<EPI, T>(h, r);
+            y_old = seg_pick(f, a.seg[0].y, a.seg[1].y, a.seg[2].y)[f.local];
+        }
+    }
+    if constexpr (EPI == kERopeKV) rope_p = a.pos[0];
     float xv[32];
     {
         const f32x4 *win = xwin + chunk * 512;
@@ -601,6 +612,13 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint
     for (int t = 0; t < T; ++t) {
         if (t + PF < T && t + PF >= P0)
             load_row<FMT, EPI, T>(rw[t + PF], h, a, min(row0 + (t + PF) * rstride, h.N - 1), chunk, lo);
+        if constexpr (EPI == kERopeKV) {
+            if (t == T / 2 && finisher && (lane & 1) == 0) {
+                const RowRef f = row_ref<EPI, T>(h, r);
+                const int hd = 1 << h.hd_shift;
+                if (!f.s2) rope_angle(a.rope_cs, a.cap, rope_p, f.local & (hd - 1), hd, a.rope_base, rope_c, rope_s);
+            }
+        }
         float scale;
         const float dot = row_dot<FMT>(rw[t], xv, xsum, xsum2, odd, cl, tbl, scale);
         acc[t] = dot * scale;
@@ -613,14 +631,13 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint
     if (lane < TP) part[wave][wave_rows_index<TP>(lane)] = tot;
     __syncthreads();                                         // 2: partials written
     // The S chunk waves of group g are waves g*S .. g*S+S-1.
-    const int r = row0 + lane;
-    if (chunk == 0 && lane < T && r < h.N) {
+    if (finisher) {
         float v = 0.0f;
         for (int c = 0; c < S; ++c) v += part[grp * S + c][lane];
         if constexpr (EPI == kEStore || EPI == kEStore3 || EPI == kEAdd) {
             const RowRef f = row_ref<EPI, T>(h, r);
             float *y = seg_pick(f, a.seg[0].y, a.seg[1].y, a.seg[2].y);
-            if constexpr (EPI == kEAdd) y[f.local] += v;
+            if constexpr (EPI == kEAdd) y[f.local] = y_old + v;
             else y[f.local] = v;
         } else if constexpr (EPI == kESwiGLU) {
             // Lane t < T/2 holds gate row i, lane t + T/2 up row i.
@@ -636,16 +653,16 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint
             for (int c = 0; c < S; ++c) v1 += part[grp * S + c][lane + 1];
             {
                 const RowRef f = row_ref<EPI, T>(h, r);
-                const int p = a.pos[0];
+                const int p = rope_p;
                 const bool in_cache = p >= 0 && p < a.cap;
                 const int hd = 1 << h.hd_shift;
                 const int hh = f.local >> h.hd_shift, i = f.local & (hd - 1);
                 if (!f.s1 && !f.s2) {                    // q: rotate, store fp32
-                    rope_rotate(v, v1, a.rope_cs, a.cap, p, i, hd, a.rope_base);
+                    rope_apply(v, v1, rope_c, rope_s);
                     a.seg[0].y[f.local] = v;
                     a.seg[0].y[f.local + (hd >> 1)] = v1;
                 } else if (!f.s2) {                      // k: rotate, append fp16
-                    rope_rotate(v, v1, a.rope_cs, a.cap, p, i, hd, a.rope_base);
+                    rope_apply(v, v1, rope_c, rope_s);
                     if (in_cache) {
                         uint16_t *dst = a.kc + (static_cast<size_t>(hh) * a.cap + p) * hd + i;
                         dst[0] = f32_to_f16_bits(v);
