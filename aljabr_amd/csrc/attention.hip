@@ -58,6 +58,22 @@ __device__ __forceinline__ KvRaw<F16> load_raw(const void *base, long long idx) 
     return r;
 }
 
+// All-zero bits (+0.0 values) unless `keep`: masks a raw K/V slice before
+// conversion, so the conversions can fold into the FMAs that read them.
+template <bool F16>
+__device__ __forceinline__ KvRaw<F16> masked(KvRaw<F16> x, bool keep) {
+    const uint32_t k = keep ? 0xffffffffu : 0u;
+    if constexpr (F16) {
+        x.u.x &= k; x.u.y &= k; x.u.z &= k; x.u.w &= k;
+    } else {
+        x.a = make_float4(__uint_as_float(__float_as_uint(x.a.x) & k), __uint_as_float(__float_as_uint(x.a.y) & k),
+                          __uint_as_float(__float_as_uint(x.a.z) & k), __uint_as_float(__float_as_uint(x.a.w) & k));
+        x.b = make_float4(__uint_as_float(__float_as_uint(x.b.x) & k), __uint_as_float(__float_as_uint(x.b.y) & k),
+                          __uint_as_float(__float_as_uint(x.b.z) & k), __uint_as_float(__float_as_uint(x.b.w) & k));
+    }
+    return x;
+}
+
 template <bool F16>
 __device__ __forceinline__ void raw_to_f32(const KvRaw<F16> &x, float (&r)[8]) {
     if constexpr (F16) {
@@ -120,14 +136,16 @@ __device__ __forceinline__ void key_range(const AttnParams &p, int sk, int qi, i
 // group folds its splits (in split order) with online rescaling, and the
 // groups are combined through `st` ([NTH/(D/4)][D + 2] floats of LDS).
 template <int D, int NTH>
-__device__ __forceinline__ void merge_row(const AttnParams &p, const float *__restrict__ part_o,
-                                          const float *__restrict__ part_ml, int splits, long long row, float *st) {
+__device__ __forceinline__ void merge_row(const float *__restrict__ part_o, const float *__restrict__ part_ml,
+                                          float *out_base, int splits, long long row, int Sq, int Hq, int q_sb,
+                                          int q_sh, int q_sq, float norm_eps, float *st) {
     constexpr int LPS = D / 4;          // lanes per split
     constexpr int SG = NTH / LPS;       // splits in flight
-    const int qi = static_cast<int>(row % p.Sq);
-    const int h = static_cast<int>((row / p.Sq) % p.Hq);
-    const int bb = static_cast<int>(row / (static_cast<long long>(p.Sq) * p.Hq));
-    float *out = p.out + bb * p.q_sb + h * p.q_sh + qi * p.q_sq;
+    const int qi = static_cast<int>(row % Sq);
+    const int h = static_cast<int>((row / Sq) % Hq);
+    const int bb = static_cast<int>(row / (static_cast<long long>(Sq) * Hq));
+    float *out = out_base + static_cast<long long>(bb) * q_sb + static_cast<long long>(h) * q_sh +
+                 static_cast<long long>(qi) * q_sq;
     const int sg = threadIdx.x / LPS, j = threadIdx.x % LPS;
     const float *po = part_o + row * splits * D;
     const float *pm = part_ml + row * splits * 2;
@@ -187,34 +205,44 @@ __device__ __forceinline__ void merge_row(const AttnParams &p, const float *__re
                 O = fmaf(st[g * (D + 2) + dd], w, O);
             }
         }
-        out[dd] = L == 0.0f ? 0.0f : O / (L + p.norm_eps);
+        out[dd] = L == 0.0f ? 0.0f : O / (L + norm_eps);
     }
     __syncthreads();                    // `st` is free again
 }
 
-// Merge split partials: one 256-thread workgroup per query row.
+// Merge split partials: one 256-thread workgroup per query row. Every
+// argument is a scalar (preloaded into SGPRs at wave launch): the partial
+// loads go out without an argument read first.
 template <int D>
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, const float *__restrict__ part_o,
-                                                        const float *__restrict__ part_ml, int splits) {
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part_o,
+                                                        const float *__restrict__ part_ml, float *out, int splits,
+                                                        int Sq, int Hq, int q_sb, int q_sh, int q_sq, float norm_eps) {
     __shared__ float st[(256 / (D / 4)) * (D + 2)];
-    merge_row<D, 256>(p, part_o, part_ml, splits, blockIdx.x, st);
+    merge_row<D, 256>(part_o, part_ml, out, splits, blockIdx.x, Sq, Hq, q_sb, q_sh, q_sq, norm_eps, st);
 }
 
 // KT keys per group per trip (the tile): 4, or 2 where a workgroup's chunk
 // is one trip of 2-key tiles (every group busy, half the serial work per
 // lane).
+// The arguments the first K/V and q loads need lead as scalars (preloaded
+// into SGPRs at wave launch, 14 dwords): the caches, q, the lengths, the
+// row stride cap (= the rows in memory: callers of the contiguous path pass
+// cap == Sk), Sq | Hkv << 16, the chunk and q's element strides (32-bit).
 template <int D, int G, bool F16, int WAVES, bool PAGED, int KT>
-__global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, int splits, int chunk,
-                                                                float *__restrict__ part_o,
+__global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(const void *kcache, const void *vcache,
+                                                                const float *q, const int *kv_len, int cap,
+                                                                int sq_hkv, int chunk, int q_sb, int q_sh, int q_sq,
+                                                                AttnParams p, int splits, float *__restrict__ part_o,
                                                                 float *__restrict__ part_ml) {
+    const int Sq = sq_hkv & 0xffff, Hkv = sq_hkv >> 16;
     constexpr int LPK = D / 8;                 // lanes per key row
     constexpr int GPW = 64 / LPK;              // key groups per wave
     constexpr int NG = GPW * WAVES;            // key groups per workgroup
     extern __shared__ float smem[];            // [WAVES][G][D + 2]
 
     const int split = blockIdx.x;
-    const int kvh = blockIdx.y / p.Sq;
-    const int qi = blockIdx.y % p.Sq;
+    const int kvh = blockIdx.y / Sq;
+    const int qi = blockIdx.y % Sq;
     const int b = blockIdx.z;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -223,13 +251,13 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
 
     const int k_begin = split * chunk;
     // Element offset of key row `key` (this lane's 8-value slice).
-    const long long head_base = (static_cast<long long>(b) * p.Hkv + kvh) * p.cap * D + sub * 8;
+    const long long head_base = (static_cast<long long>(b) * Hkv + kvh) * cap * D + sub * 8;
     const int *btab = PAGED ? p.block_table + static_cast<long long>(b) * p.max_blocks : nullptr;
     auto row_at = [&](int key) -> long long {
         if constexpr (PAGED) {
             const int blk = key / p.block_size;
             const int phys = max(btab[blk], 0);
-            return ((static_cast<long long>(phys) * p.Hkv + kvh) * p.block_size + (key - blk * p.block_size)) * D +
+            return ((static_cast<long long>(phys) * Hkv + kvh) * p.block_size + (key - blk * p.block_size)) * D +
                    sub * 8;
         } else {
             return head_base + static_cast<long long>(key) * D;
@@ -242,8 +270,21 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
         for (int t = 0; t < KT; ++t) {
             const int key = tbase + t;
             const long long r = row_at(key < mem_end ? key : k_begin);
-            kn[t] = load_raw<F16>(p.k, r);
-            vn[t] = load_raw<F16>(p.v, r);
+            kn[t] = load_raw<F16>(kcache, r);
+            vn[t] = load_raw<F16>(vcache, r);
+        }
+    };
+    // Query slices, loaded before the length is read (they do not depend on
+    // it) and scaled below.
+    float4 qa[G], qc[G];
+    auto load_q = [&]() {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int h = kvh * G + g;
+            const float *qp = q + static_cast<long long>(b) * q_sb + static_cast<long long>(h) * q_sh +
+                              static_cast<long long>(qi) * q_sq + sub * 8;
+            qa[g] = *reinterpret_cast<const float4 *>(qp);
+            qc[g] = *reinterpret_cast<const float4 *>(qp + 4);
         }
     };
     int sk;
@@ -251,15 +292,17 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
         // Blocks past the sequence's length may not exist: read the length
         // first, and a split past it loads nothing (clamped keys fall back
         // to k_begin, which must then be a row of the sequence).
-        sk = max(p.kv_len[b], 0);
+        load_q();
+        sk = max(kv_len[b], 0);
         mem_end = min(k_begin + chunk, sk);
         if (k_begin < sk) issue(k_begin + grp * KT);
     } else {
         // Rows [k_begin, mem_end) exist in memory whatever the visible length,
         // so the first tile's loads go out before kv_len has arrived.
-        mem_end = min(k_begin + chunk, p.kv_len ? p.cap : p.Sk);
+        mem_end = min(k_begin + chunk, cap);
         issue(k_begin + grp * KT);
-        sk = p.kv_len ? min(max(p.kv_len[b], 0), p.cap) : p.Sk;   // never past the cache
+        load_q();
+        sk = kv_len ? min(max(kv_len[b], 0), cap) : cap;          // never past the cache
     }
     int k_lo, k_hi;
     key_range(p, sk, qi, k_lo, k_hi);
@@ -271,10 +314,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
     const float qs = p.scale * kLog2e;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const int h = kvh * G + g;
-        const float *qp = p.q + b * p.q_sb + h * p.q_sh + qi * p.q_sq + sub * 8;
-        const float4 a = *reinterpret_cast<const float4 *>(qp);
-        const float4 c = *reinterpret_cast<const float4 *>(qp + 4);
+        const float4 a = qa[g], c = qc[g];
         qv[g][0] = a.x * qs; qv[g][1] = a.y * qs; qv[g][2] = a.z * qs; qv[g][3] = a.w * qs;
         qv[g][4] = c.x * qs; qv[g][5] = c.y * qs; qv[g][6] = c.z * qs; qv[g][7] = c.w * qs;
     }
@@ -302,13 +342,13 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(AttnParams p, in
         for (int t = 0; t < KT; ++t) {
             valid[t] = t0 + t < k_end && (!PAGED || t0 + t >= k_lo);   // only the paged rule has a lower bound
             raw_to_f32<F16>(kn[t], kr[t]);
-            raw_to_f32<F16>(vn[t], vr[t]);
             // Rows past the visible keys may hold anything (the first tile is
             // loaded before the length is known, and cache rows beyond a
             // sequence's length were never written): their values must not
-            // reach the sums, where 0 * NaN would still be NaN.
-#pragma unroll
-            for (int i = 0; i < 8; ++i) vr[t][i] = valid[t] ? vr[t][i] : 0.0f;
+            // reach the sums, where 0 * NaN would still be NaN. Masked as raw
+            // bits (four selects per key for fp16), so the conversions fold
+            // into the P.V FMAs.
+            raw_to_f32<F16>(masked<F16>(vn[t], valid[t]), vr[t]);
         }
         if (t0 + NG * KT < k_end) issue(t0 + NG * KT);
         float add[KT];
@@ -527,15 +567,17 @@ int launch_split(const AttnParams &p, int splits, int chunk, float *part, hipStr
     // Partials: o as [rows][splits][D], then (m, l) as [rows][splits][2].
     float *part_o = part;
     float *part_ml = part ? part + rows * splits * D : nullptr;
+    const int sq_hkv = p.Sq | (p.Hkv << 16);
+    const int qsb = static_cast<int>(p.q_sb), qsh = static_cast<int>(p.q_sh), qsq = static_cast<int>(p.q_sq);
     if (WIDE && chunk <= 2 * NG)
-        hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES, PAGED, 2>), grid, dim3(WAVES * 64), lds, s, p, splits,
-                           chunk, part_o, part_ml);
+        hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES, PAGED, 2>), grid, dim3(WAVES * 64), lds, s, p.k, p.v,
+                           p.q, p.kv_len, p.cap, sq_hkv, chunk, qsb, qsh, qsq, p, splits, part_o, part_ml);
     else
-        hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES, PAGED, 4>), grid, dim3(WAVES * 64), lds, s, p, splits,
-                           chunk, part_o, part_ml);
+        hipLaunchKernelGGL((attn_split_kernel<D, G, F16, WAVES, PAGED, 4>), grid, dim3(WAVES * 64), lds, s, p.k, p.v,
+                           p.q, p.kv_len, p.cap, sq_hkv, chunk, qsb, qsh, qsq, p, splits, part_o, part_ml);
     if (splits > 1)
-        hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, p, part_o,
-                           part_ml, splits);
+        hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, part_o,
+                           part_ml, p.out, splits, p.Sq, p.Hq, qsb, qsh, qsq, p.norm_eps);
     return ALJABR_ROCM_OK;
 }
 
@@ -579,9 +621,13 @@ int enqueue_attention(const AttnParams &p_in) {
         p.q_sb = static_cast<long long>(p.Hq) * p.Sq * p.D;
     }
     const int G = p.Hq / p.Hkv;
+    // The split kernel takes Sq and Hkv packed in one word, q's strides as
+    // 32-bit values and, for contiguous caches, cap as the rows in memory.
     const bool fast = (p.D == 64 || p.D == 128) && (G == 1 || G == 2 || G == 4 || G == 8) && aligned(p.q, 16) &&
                       aligned(p.out, 16) && aligned(p.k, 16) && aligned(p.v, 16) && p.q_sq % 4 == 0 &&
-                      p.q_sh % 4 == 0 && p.q_sb % 4 == 0;
+                      p.q_sh % 4 == 0 && p.q_sb % 4 == 0 && p.Sq <= 0xffff && p.Hkv <= 0x7fff &&
+                      p.q_sb <= 0x7fffffffLL && p.q_sh <= 0x7fffffffLL && p.q_sq <= 0x7fffffffLL &&
+                      (p.block_table || p.cap == p.Sk);
     if (!fast) {
         const long long n = static_cast<long long>(p.B) * p.Hq * p.Sq * p.D;
         const dim3 grid(static_cast<unsigned>((n + 63) / 64));
