@@ -31,6 +31,12 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// 2^x with one v_exp_f32 (exp2f adds a denormal-range fix-up of five more
+// instructions). Every use is a softmax weight relative to a running maximum
+// (x <= 0): a result below 2^-126 flushes to 0, a weight below 1e-38 of the
+// largest one, and 2^-inf = 0.
+__device__ __forceinline__ float exp2_w(float x) { return __builtin_amdgcn_exp2f(x); }
+
 template <int LPK>
 __device__ __forceinline__ float group_sum(float v) {
     // Sum over the LPK lanes of a key group (LPK = 8 or 16, aligned groups).
@@ -170,8 +176,8 @@ __device__ __forceinline__ void merge_row(const float *__restrict__ part_o, cons
             if (s0 + u * SG >= splits) break;
             const float mn = fmaxf(m, ms[u]);
             if (mn == -INFINITY) continue;
-            const float a = m == -INFINITY ? 0.0f : exp2f(m - mn);
-            const float b = ms[u] == -INFINITY ? 0.0f : exp2f(ms[u] - mn);
+            const float a = m == -INFINITY ? 0.0f : exp2_w(m - mn);
+            const float b = ms[u] == -INFINITY ? 0.0f : exp2_w(ms[u] - mn);
             l = fmaf(l, a, ls[u] * b);
             o.x = fmaf(o.x, a, os[u].x * b);
             o.y = fmaf(o.y, a, os[u].y * b);
@@ -200,7 +206,7 @@ __device__ __forceinline__ void merge_row(const float *__restrict__ part_o, cons
             for (int g = 0; g < SG; ++g) {
                 const float mg = st[g * (D + 2) + D];
                 if (mg == -INFINITY) continue;
-                const float w = exp2f(mg - M);
+                const float w = exp2_w(mg - M);
                 L = fmaf(st[g * (D + 2) + D + 1], w, L);
                 O = fmaf(st[g * (D + 2) + dd], w, O);
             }
@@ -378,12 +384,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(const void *kcac
             }
             const float mn = fmaxf(m[g], tmax);
             if (mn == -INFINITY) continue;             // nothing visible yet
-            const float alpha = m[g] == -INFINITY ? 0.0f : exp2f(m[g] - mn);
+            const float alpha = exp2_w(m[g] - mn);   // mn is finite here: m = -inf gives 0
             float psum = 0.0f;
             float pr[KT];
 #pragma unroll
             for (int t = 0; t < KT; ++t) {
-                pr[t] = s[t] == -INFINITY ? 0.0f : exp2f(s[t] - mn);
+                pr[t] = exp2_w(s[t] - mn);            // s = -inf (masked) gives 0
                 psum += pr[t];
             }
             l[g] = fmaf(l[g], alpha, psum);
@@ -411,8 +417,8 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(const void *kcac
 #pragma unroll
             for (int i = 0; i < 8; ++i) o2[i] = __shfl_xor(o[g][i], off);
             const float mn = fmaxf(m[g], m2);
-            const float a = m[g] == -INFINITY ? 0.0f : exp2f(m[g] - mn);
-            const float c = m2 == -INFINITY ? 0.0f : exp2f(m2 - mn);
+            const float a = m[g] == -INFINITY ? 0.0f : exp2_w(m[g] - mn);
+            const float c = m2 == -INFINITY ? 0.0f : exp2_w(m2 - mn);
             l[g] = fmaf(l[g], a, l2 * c);
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[g][i] = fmaf(o[g][i], a, o2[i] * c);
@@ -455,7 +461,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(const void *kcac
         if (M != -INFINITY) {
 #pragma unroll
             for (int gr = 0; gr < WAVES; ++gr) {
-                const float w = mg[gr] == -INFINITY ? 0.0f : exp2f(mg[gr] - M);
+                const float w = mg[gr] == -INFINITY ? 0.0f : exp2_w(mg[gr] - M);
                 L = fmaf(lg[gr], w, L);
                 O = fmaf(og[gr], w, O);
             }
