@@ -135,6 +135,13 @@ constexpr int kTailSwiGLU = 1;        // rows [0, n) gate, [n, 2n) up: out[m][i]
 constexpr int kTailRopeAppend = 2;    // rows q (nh heads), k, v (nkv heads): out = rotated q; k (rotated) and v
                                       // appended as fp16 at row pos[m] of caches [M][nkv][cap][head_dim]
 constexpr int kTailResidualNorm = 3;  // out[m] += sums (residual); xn[m] = RMSNorm(out[m]) * norm_w
+// kTailResidualScale: y += the slice sums, xn = y * norm_w (no row scale),
+// and per (row, column block) sums of squares of y to ssq[M][kSsqParts];
+// a later tail with `ssq` set applies RMSNorm's row scale 1/sqrt(mean + eps)
+// to its slice sums (W.(x*s*w) = s*(W.(x*w)) for a per-row scale s), which
+// spreads the residual step over many workgroups instead of one per row.
+constexpr int kTailResidualScale = 4;
+constexpr int kSsqParts = 8;
 struct SliceTail {
     int kind;
     float *out;
@@ -147,6 +154,10 @@ struct SliceTail {
     float *xn;
     const float *norm_w;
     float eps;
+    // Row scale of a preceding kTailResidualScale (SwiGLU and RoPE tails):
+    // ssq[M][kSsqParts] over rows of norm_n elements, or null for none.
+    float *ssq;
+    int norm_n;
 };
 int enqueue_slice_tail(const SliceTail &t, const float *part, int slices, int M, int N);
 // NF4 small-M GEMM on MFMA (M >= 2 in passes of 32 tokens, K % 256 == 0,

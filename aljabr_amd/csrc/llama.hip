@@ -73,6 +73,7 @@ struct aljabr_rocm_llama {
     size_t attn_scratch_bytes = 0;
     float *mm_part = nullptr;        // K-slice partials of the batched matrix-core GEMMs
     size_t mm_part_floats = 0;
+    float *tail_ssq = nullptr;       // [max_batch][kSsqParts] row-block sums of squares of the residual tails
     bool rows_fused = false;   // batch-1 layers as fused NF4 launches (shapes and alignment allow it)
     // Captured decode steps, by batch size (and the logits buffer they write).
     struct Graph {
@@ -259,7 +260,7 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
                          ((attention_scratch_bytes(c.max_batch, c.n_heads, 1, c.head_dim, c.max_seq) + 255) &
                           ~size_t(255)) +
                          ((static_cast<size_t>(c.max_seq) * (c.head_dim / 2) * sizeof(float2) + 255) & ~size_t(255)) +
-                         256;
+                         ((static_cast<size_t>(B) * kSsqParts * 4 + 255) & ~size_t(255)) + 256;
     hipError_t e = hipMalloc(&m->arena, bytes);
     if (e != hipSuccess) {
         delete m;
@@ -288,6 +289,7 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
         m->mm_part_floats = mm_floats;
         m->mm_part = carve<float>(cur, mm_floats);
     }
+    m->tail_ssq = carve<float>(cur, static_cast<size_t>(B) * kSsqParts);
     // The RoPE angles of every cache position, computed once: the decode
     // step then reads cos/sin instead of evaluating double pow/cos/sin.
     m->rope_cs = carve<float2>(cur, static_cast<size_t>(c.max_seq) * (c.head_dim / 2));
@@ -903,6 +905,11 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
     else
         ALJ_TRY(enqueue_embed_typed(m->x, m->tok_embed.w, m->tok_embed.type, tok, B, dim, c.vocab));
     ALJ_MARK("embed", weight_bytes(m->tok_embed.type, B, dim, bs) + B * dim * f4);
+    // With the GEMM tails, a residual tail may leave xb = x * norm_w without
+    // RMSNorm's row scale, and the row-block sums of squares in tail_ssq: the
+    // next GEMM's tail applies the scale to its products. A fallback that
+    // consumes xb directly normalizes it first.
+    bool xb_scaled = false;
     for (int l = 0; l < c.layers; ++l) {
         auto W = [&](const std::vector<T> &t) { return t[l].w; };
         auto S = [&](const std::vector<T> &t) { return t[l].s; };
@@ -971,6 +978,9 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                 t.cap = c.max_seq;
                 t.base = c.rope_base;
                 t.cs = m->rope_cs;
+                t.ssq = xb_scaled ? m->tail_ssq : nullptr;
+                t.norm_n = dim;
+                t.eps = c.eps;
                 rc = enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, false, m->mm_part, m->mm_part_floats, &t);
                 if (rc == ALJABR_ROCM_OK)
                     ALJ_MARK("qkv_gemm_rope_append", mm_bytes(m->wq[l], qd, dim, false) +
@@ -979,6 +989,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                                                          B * 2.0 * kvd * f4 + B * 2.0 * kvd * 2.0);
             }
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                if (xb_scaled) ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, attn_norm, B, dim, c.eps));
                 rc = m->all_nf4 && B >= 2 ? enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, false, m->mm_part,
                                                                    m->mm_part_floats)
                                           : ALJABR_ROCM_ERR_UNSUPPORTED;
@@ -1029,18 +1040,22 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             ALJ_MARK("wo_rows_add", mm_bytes(m->wo[l], dim, qd, true));
         } else {
             rc = ALJABR_ROCM_ERR_UNSUPPORTED;
+            xb_scaled = false;
             if (tails) {
-                // x += Wo att, then xb = RMSNorm(x) with the FFN norm.
+                // x += Wo att, then xb = x * the FFN norm with the row sums of
+                // squares for the gate/up tail (RMSNorm's row scale).
                 SliceTail t{};
-                t.kind = kTailResidualNorm;
+                t.kind = kTailResidualScale;
                 t.out = m->x;
                 t.xn = m->xb;
                 t.norm_w = ffn_norm;
-                t.eps = c.eps;
+                t.ssq = m->tail_ssq;
                 const RowsOut o = {m->x, W(m->wo), S(m->wo), dim};
                 rc = enqueue_nf4_mfma_multi(&o, 1, m->att, qd, shift, B, false, m->mm_part, m->mm_part_floats, &t);
-                if (rc == ALJABR_ROCM_OK)
+                if (rc == ALJABR_ROCM_OK) {
+                    xb_scaled = true;
                     ALJ_MARK("wo_gemm_add_rmsnorm", mm_bytes(m->wo[l], dim, qd, true) + (B * dim + dim) * f4);
+                }
             }
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
                 ALJ_TRY(mm(m->x, m->att, m->wo[l], qd, dim, true, m->xb));
@@ -1091,6 +1106,9 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                 t.kind = kTailSwiGLU;
                 t.out = m->hb;
                 t.n = ffn;
+                t.ssq = xb_scaled ? m->tail_ssq : nullptr;
+                t.norm_n = dim;
+                t.eps = c.eps;
                 rc = enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, false, m->mm_part, m->mm_part_floats, &t);
                 if (rc == ALJABR_ROCM_OK)
                     ALJ_MARK("gate_up_gemm_swiglu", mm_bytes(m->w_gate[l], ffn, dim, false) +
@@ -1098,6 +1116,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                                                         B * ffn * f4);
             }
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+                if (xb_scaled) ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, ffn_norm, B, dim, c.eps));
                 rc = m->all_nf4 && B >= 2 ? enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, false, m->mm_part,
                                                                    m->mm_part_floats)
                                           : ALJABR_ROCM_ERR_UNSUPPORTED;
@@ -1118,19 +1137,26 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             }
             // x += Wdown hb; with the tails also xb = the next RMSNorm of x
             // (the next layer's attention norm, or the output norm).
+            // Before the next layer: xb = x * its attention norm with the row
+            // sums of squares (its Q/K/V tail applies the row scale); before
+            // the output head: the full RMSNorm.
             const float *next_norm = l + 1 < c.layers ? m->attn_norm[l + 1] : m->out_norm;
             rc = ALJABR_ROCM_ERR_UNSUPPORTED;
+            xb_scaled = false;
             if (tails) {
                 SliceTail t{};
-                t.kind = kTailResidualNorm;
+                t.kind = l + 1 < c.layers ? kTailResidualScale : kTailResidualNorm;
                 t.out = m->x;
                 t.xn = m->xb;
                 t.norm_w = next_norm;
                 t.eps = c.eps;
+                t.ssq = m->tail_ssq;
                 const RowsOut d = {m->x, W(m->w_down), S(m->w_down), dim};
                 rc = enqueue_nf4_mfma_multi(&d, 1, m->hb, ffn, shift, B, false, m->mm_part, m->mm_part_floats, &t);
-                if (rc == ALJABR_ROCM_OK)
+                if (rc == ALJABR_ROCM_OK) {
+                    xb_scaled = l + 1 < c.layers;
                     ALJ_MARK("down_gemm_add_rmsnorm", mm_bytes(m->w_down[l], dim, ffn, true) + (B * dim + dim) * f4);
+                }
             }
             if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
                 ALJ_TRY(mm(m->x, m->hb, m->w_down[l], ffn, dim, true, m->xb));

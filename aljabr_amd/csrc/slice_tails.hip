@@ -6,7 +6,9 @@
 //   - SwiGLU of the stacked gate/up rows into the FFN activations;
 //   - RoPE of the stacked q/k rows, q stored, k and v appended to the fp16
 //     caches at each sequence's position;
-//   - the residual add of a Wo/down product followed by the next RMSNorm.
+//   - the residual add of a Wo/down product followed by the next RMSNorm,
+//     or, spread over column blocks, the residual add, y * norm_w and the
+//     blocks' sums of squares, whose row scale the next GEMM's tail applies.
 // Partials are [slice][M][N] over the GEMM's stacked rows N. The arithmetic
 // of each step is that of its stand-alone kernel (ops.hip).
 #include "device.hpp"
@@ -35,22 +37,36 @@ __device__ __forceinline__ float slice_total(const float *__restrict__ part, siz
 
 __device__ __forceinline__ uint16_t f16_bits(float v) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v)); }
 
+// RMSNorm's row scale 1/sqrt(mean(y^2) + eps) (the sqrt in double, as the
+// stand-alone RMSNorm) from the kSsqParts column-block sums of row m, added
+// in block order; 1 without sums.
+__device__ __forceinline__ float row_scale(const float *ssq, int m, int n, float eps) {
+    if (!ssq) return 1.0f;
+    float ss = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kSsqParts; ++p) ss += ssq[m * kSsqParts + p];
+    return 1.0f / static_cast<float>(sqrt(static_cast<double>(ss / static_cast<float>(n) + eps)));
+}
+
 // GGUFVectorOps.swiGLU (GLD/tensor/GGUFVectorOps.java:333-338): g / (1 + e^-g)
 // with the exponential in double, times up.
 __device__ __forceinline__ float swiglu_of(float g, float u) {
     return g / (1.0f + static_cast<float>(exp(-static_cast<double>(g)))) * u;
 }
 
-// hb[m][i] = swiglu(gate, up) of stacked rows i and n + i.
+// hb[m][i] = swiglu(gate, up) of stacked rows i and n + i (each times the
+// row scale of a preceding residual-scale tail, if any).
 __global__ __launch_bounds__(kThreads) void tail_swiglu_kernel(float *__restrict__ hb, const float *__restrict__ part,
-                                                               int slices, int M, int N, int n) {
+                                                               int slices, int M, int N, int n,
+                                                               const float *__restrict__ ssq, int norm_n, float eps) {
     const long long t = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
     if (t >= static_cast<long long>(M) * n) return;
     const int m = static_cast<int>(t / n), i = static_cast<int>(t - static_cast<long long>(m) * n);
     const size_t stride = static_cast<size_t>(M) * N;
     const size_t row = static_cast<size_t>(m) * N;
-    const float g = slice_total(part, stride, slices, row + i);
-    const float u = slice_total(part, stride, slices, row + n + i);
+    const float sc = row_scale(ssq, m, norm_n, eps);
+    const float g = slice_total(part, stride, slices, row + i) * sc;
+    const float u = slice_total(part, stride, slices, row + n + i) * sc;
     hb[t] = swiglu_of(g, u);
 }
 
@@ -61,7 +77,8 @@ __global__ __launch_bounds__(kThreads) void tail_swiglu_kernel(float *__restrict
 __global__ void tail_rope_append_kernel(float *__restrict__ q, uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
                                         const int *__restrict__ pos, const float *__restrict__ part, int slices, int M,
                                         int N, int nh, int nkv, int head_dim, int cap, float base,
-                                        const float2 *__restrict__ cs) {
+                                        const float2 *__restrict__ cs, const float *__restrict__ ssq, int norm_n,
+                                        float eps) {
     const int slot = blockIdx.x, m = blockIdx.y, i = threadIdx.x;
     const int half = head_dim / 2;
     const size_t stride = static_cast<size_t>(M) * N;
@@ -72,8 +89,9 @@ __global__ void tail_rope_append_kernel(float *__restrict__ q, uint16_t *__restr
     // The slot's first stacked row: q heads, then k heads, then v heads,
     // head_dim rows each.
     const size_t r0 = static_cast<size_t>(slot) * head_dim;
-    float x0 = slice_total(part, stride, slices, row + r0 + i);
-    float x1 = slice_total(part, stride, slices, row + r0 + i + half);
+    const float sc = row_scale(ssq, m, norm_n, eps);
+    float x0 = slice_total(part, stride, slices, row + r0 + i) * sc;
+    float x1 = slice_total(part, stride, slices, row + r0 + i + half) * sc;
     if (slot < nh) {
         rope_apply(x0, x1, c, s);
         float *x = q + (static_cast<long long>(m) * nh + slot) * head_dim;
@@ -164,24 +182,84 @@ __global__ __launch_bounds__(kNormThreads) void tail_residual_norm_kernel(float 
     }
 }
 
+// Workgroup (p, m), 128 threads: column block p (N / kSsqParts columns) of
+// row m: y += the summed partials (the residual), xn = y * w, and the block's
+// sum of squares of y to ssq[m][p].
+constexpr int kScaleThreads = 128;
+
+__global__ __launch_bounds__(kScaleThreads) void tail_residual_scale_kernel(float *__restrict__ y, float *__restrict__ xn,
+                                                                            const float *__restrict__ w,
+                                                                            float *__restrict__ ssq,
+                                                                            const float *__restrict__ part, int slices,
+                                                                            int M, int N) {
+    __shared__ float red[kScaleThreads / 64];
+    const int pb = blockIdx.x, m = blockIdx.y;
+    const int cols4 = N / (4 * kSsqParts);              // float4 columns per block
+    const size_t stride = static_cast<size_t>(M) * N;
+    const size_t row = static_cast<size_t>(m) * N;
+    float4 *yr = reinterpret_cast<float4 *>(y + row);
+    float4 *xr = reinterpret_cast<float4 *>(xn + row);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float ss = 0.0f;
+    for (int c = pb * cols4 + static_cast<int>(threadIdx.x); c < (pb + 1) * cols4; c += kScaleThreads) {
+        const float *p = part + row + 4 * static_cast<size_t>(c);
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        int sl = 0;
+        for (; sl + 8 <= slices; sl += 8) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4 *>(p + static_cast<size_t>(sl + j) * stride);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                acc.x += v[j].x;
+                acc.y += v[j].y;
+                acc.z += v[j].z;
+                acc.w += v[j].w;
+            }
+        }
+        for (; sl < slices; ++sl) {
+            const float4 v = *reinterpret_cast<const float4 *>(p + static_cast<size_t>(sl) * stride);
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        float4 x = yr[c];
+        x.x += acc.x;
+        x.y += acc.y;
+        x.z += acc.z;
+        x.w += acc.w;
+        yr[c] = x;
+        const float4 g = w4[c];
+        xr[c] = make_float4(x.x * g.x, x.y * g.y, x.z * g.z, x.w * g.w);
+        ss = fmaf(x.x, x.x, ss);
+        ss = fmaf(x.y, x.y, ss);
+        ss = fmaf(x.z, x.z, ss);
+        ss = fmaf(x.w, x.w, ss);
+    }
+    ss = tail_block_sum(ss, red);
+    if (threadIdx.x == 0) ssq[m * kSsqParts + pb] = ss;
+}
+
 }  // namespace
 
 int enqueue_slice_tail(const SliceTail &t, const float *part, int slices, int M, int N) {
     hipStream_t s = current_stream();
     switch (t.kind) {
     case kTailSwiGLU: {
-        if (2LL * t.n != N) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        if (2LL * t.n != N || (t.ssq && t.norm_n <= 0)) return ALJABR_ROCM_ERR_UNSUPPORTED;
         const long long total = static_cast<long long>(M) * t.n;
         hipLaunchKernelGGL(tail_swiglu_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
-                           dim3(kThreads), 0, s, t.out, part, slices, M, N, t.n);
+                           dim3(kThreads), 0, s, t.out, part, slices, M, N, t.n, t.ssq, t.norm_n, t.eps);
         return ALJABR_ROCM_OK;
     }
     case kTailRopeAppend: {
-        if (t.head_dim < 2 || (t.head_dim & 1) || t.head_dim / 2 > 1024 ||
+        if (t.head_dim < 2 || (t.head_dim & 1) || t.head_dim / 2 > 1024 || (t.ssq && t.norm_n <= 0) ||
             static_cast<long long>(t.nh + 2 * t.nkv) * t.head_dim != N)
             return ALJABR_ROCM_ERR_UNSUPPORTED;
         hipLaunchKernelGGL(tail_rope_append_kernel, dim3(t.nh + 2 * t.nkv, M), dim3(t.head_dim / 2), 0, s, t.out, t.kc,
-                           t.vc, t.pos, part, slices, M, N, t.nh, t.nkv, t.head_dim, t.cap, t.base, t.cs);
+                           t.vc, t.pos, part, slices, M, N, t.nh, t.nkv, t.head_dim, t.cap, t.base, t.cs, t.ssq,
+                           t.norm_n, t.eps);
         return ALJABR_ROCM_OK;
     }
     case kTailResidualNorm:
@@ -189,6 +267,13 @@ int enqueue_slice_tail(const SliceTail &t, const float *part, int slices, int M,
             return ALJABR_ROCM_ERR_UNSUPPORTED;
         hipLaunchKernelGGL(tail_residual_norm_kernel, dim3(M), dim3(kNormThreads), 0, s, t.out, t.xn, t.norm_w, t.eps,
                            part, slices, M, N);
+        return ALJABR_ROCM_OK;
+    case kTailResidualScale:
+        if (N % (4 * kSsqParts) != 0 || !t.ssq || !aligned(t.out, 16) || !aligned(t.xn, 16) ||
+            !aligned(t.norm_w, 16) || !aligned(part, 16))
+            return ALJABR_ROCM_ERR_UNSUPPORTED;
+        hipLaunchKernelGGL(tail_residual_scale_kernel, dim3(kSsqParts, M), dim3(kScaleThreads), 0, s, t.out, t.xn,
+                           t.norm_w, t.ssq, part, slices, M, N);
         return ALJABR_ROCM_OK;
     default: return ALJABR_ROCM_ERR_UNSUPPORTED;
     }
