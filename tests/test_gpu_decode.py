@@ -87,12 +87,19 @@ CONFIGS = [
     # prologue on Q/K/V and gate/up, silu epilogue, residual-add epilogues).
     dict(layers=2, dim=2048, ffn=4096, n_heads=16, n_kv_heads=4, head_dim=128, vocab=1000,
          nf4_block=64, rope_base=500000.0, eps=1e-5),
+    # FFN 1000: the gate/up rows are no multiple of 32 and the down
+    # projection's K no multiple of 256, so at batch >= 2 those products
+    # leave the matrix-core tails while Q/K/V and Wo keep them: the Wo tail
+    # leaves xb without RMSNorm's row scale and the gate/up fallback must
+    # normalize it first.
+    dict(layers=2, dim=512, ffn=1000, n_heads=8, n_kv_heads=2, head_dim=64, vocab=2000,
+         nf4_block=64, rope_base=500000.0, eps=1e-5),
 ]
 
-# (config, batch): batch >= 2 takes the matrix-core GEMMs that add into
-# cleared or residual outputs; batch 1 the fused launches (config 2) or the
+# (config, batch): batch >= 2 takes the matrix-core GEMMs (with their fused
+# tails where the shapes allow); batch 1 the fused launches (config 2) or the
 # unfused composition (configs 0 and 1).
-CASES = [(0, 3), (1, 3), (0, 1), (2, 1), (2, 2)]
+CASES = [(0, 3), (1, 3), (0, 1), (2, 1), (2, 2), (3, 3)]
 
 
 @pytest.mark.parametrize("ci,batch", CASES, ids=[f"cfg{c}-b{b}" for c, b in CASES])
