@@ -69,8 +69,9 @@ struct KqOut {
 // With several 512-element K slices the partial sums go to `part` (at least
 // (K / 512) * M * (stacked rows) floats) or, when that is null or too small,
 // to the stream's scratch; `accumulate` adds the product into the outputs.
+struct SliceTail;
 int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate,
-                              float *part = nullptr, size_t part_floats = 0);
+                              float *part = nullptr, size_t part_floats = 0, const SliceTail *tail = nullptr);
 // ys[s] (+)= the K slices' partial sums part[slice][m][stacked row] of
 // segment s (stacked rows [ends[s-1], ends[s])), added in slice order.
 int enqueue_slice_sum(float *const *ys, const int *ends, int nseg, int M, int N, const float *part, int slices,

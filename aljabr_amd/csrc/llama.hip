@@ -898,7 +898,26 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
     // the next RMSNorm, SwiGLU), so xb holds the next RMSNorm at every layer's
     // start. A GEMM the matrix cores do not take falls back to the separate
     // launches for that block only.
-    const bool tails = !fused1 && m->all_nf4 && B >= 2 && B <= 32 && shift == 6;
+    const bool tails = !fused1 && B >= 2 && B <= 32 && (!m->all_nf4 || shift == 6);
+    // One matrix-core GEMM over matrices of one type (NF4 or a K-quant) whose
+    // slice sums go to the tail kernel `t`; UNSUPPORTED when the types or
+    // shapes do not allow it (the caller then runs the separate launches).
+    auto gemm_tail = [&](const RowsOut *o, const T *const *ts, int nseg, const float *x, int K,
+                         const SliceTail *t) -> int {
+        const int ty = ts[0]->type;
+        for (int i = 1; i < nseg; ++i)
+            if (ts[i]->type != ty) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        if (ty == ALJABR_ROCM_TYPE_NF4)
+            return m->all_nf4 ? enqueue_nf4_mfma_multi(o, nseg, x, K, shift, B, false, m->mm_part, m->mm_part_floats, t)
+                              : ALJABR_ROCM_ERR_UNSUPPORTED;
+        if (!kquant_mfma_type(ty) || B > kquant_mfma_max_m(ty)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        KqOut k[3];
+        for (int i = 0; i < nseg; ++i) k[i] = KqOut{o[i].y, o[i].w, o[i].n};
+        return enqueue_kquant_mfma_multi(k, nseg, x, K, ty, B, false, m->mm_part, m->mm_part_floats, t);
+    };
+    // A residual tail defers RMSNorm's row scale only to a consumer whose
+    // matrices share one type (one launch, one tail).
+    auto same_type = [](const T &a, const T &b, const T &c) { return a.type == b.type && b.type == c.type; };
     hipLaunchKernelGGL(lengths_from_positions, dim3((B + 63) / 64), dim3(64), 0, s, m->kv_len, pos, B);
     if (m->tok_embed.type == ALJABR_ROCM_TYPE_F32)
         ALJ_TRY(enqueue_embed(m->x, reinterpret_cast<const float *>(m->tok_embed.w), tok, B, dim, c.vocab));
@@ -981,7 +1000,8 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                 t.ssq = xb_scaled ? m->tail_ssq : nullptr;
                 t.norm_n = dim;
                 t.eps = c.eps;
-                rc = enqueue_nf4_mfma_multi(qkv, 3, m->xb, dim, shift, B, false, m->mm_part, m->mm_part_floats, &t);
+                const T *const qts[3] = {&m->wq[l], &m->wk[l], &m->wv[l]};
+                rc = gemm_tail(qkv, qts, 3, m->xb, dim, &t);
                 if (rc == ALJABR_ROCM_OK)
                     ALJ_MARK("qkv_gemm_rope_append", mm_bytes(m->wq[l], qd, dim, false) +
                                                          mm_bytes(m->wk[l], kvd, dim, false) +
@@ -1043,17 +1063,21 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             xb_scaled = false;
             if (tails) {
                 // x += Wo att, then xb = x * the FFN norm with the row sums of
-                // squares for the gate/up tail (RMSNorm's row scale).
+                // squares for the gate/up tail (RMSNorm's row scale), or the
+                // full RMSNorm when gate and up differ in type.
+                const bool defer = same_type(m->w_gate[l], m->w_up[l], m->w_up[l]);
                 SliceTail t{};
-                t.kind = kTailResidualScale;
+                t.kind = defer ? kTailResidualScale : kTailResidualNorm;
                 t.out = m->x;
                 t.xn = m->xb;
                 t.norm_w = ffn_norm;
+                t.eps = c.eps;
                 t.ssq = m->tail_ssq;
                 const RowsOut o = {m->x, W(m->wo), S(m->wo), dim};
-                rc = enqueue_nf4_mfma_multi(&o, 1, m->att, qd, shift, B, false, m->mm_part, m->mm_part_floats, &t);
+                const T *const ots[1] = {&m->wo[l]};
+                rc = gemm_tail(&o, ots, 1, m->att, qd, &t);
                 if (rc == ALJABR_ROCM_OK) {
-                    xb_scaled = true;
+                    xb_scaled = defer;
                     ALJ_MARK("wo_gemm_add_rmsnorm", mm_bytes(m->wo[l], dim, qd, true) + (B * dim + dim) * f4);
                 }
             }
@@ -1109,7 +1133,8 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                 t.ssq = xb_scaled ? m->tail_ssq : nullptr;
                 t.norm_n = dim;
                 t.eps = c.eps;
-                rc = enqueue_nf4_mfma_multi(gu, 2, m->xb, dim, shift, B, false, m->mm_part, m->mm_part_floats, &t);
+                const T *const gts[2] = {&m->w_gate[l], &m->w_up[l]};
+                rc = gemm_tail(gu, gts, 2, m->xb, dim, &t);
                 if (rc == ALJABR_ROCM_OK)
                     ALJ_MARK("gate_up_gemm_swiglu", mm_bytes(m->w_gate[l], ffn, dim, false) +
                                                         mm_bytes(m->w_up[l], ffn, dim, false) - B * dim * f4 -
@@ -1144,17 +1169,19 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             rc = ALJABR_ROCM_ERR_UNSUPPORTED;
             xb_scaled = false;
             if (tails) {
+                const bool defer = l + 1 < c.layers && same_type(m->wq[l + 1], m->wk[l + 1], m->wv[l + 1]);
                 SliceTail t{};
-                t.kind = l + 1 < c.layers ? kTailResidualScale : kTailResidualNorm;
+                t.kind = defer ? kTailResidualScale : kTailResidualNorm;
                 t.out = m->x;
                 t.xn = m->xb;
                 t.norm_w = next_norm;
                 t.eps = c.eps;
                 t.ssq = m->tail_ssq;
                 const RowsOut d = {m->x, W(m->w_down), S(m->w_down), dim};
-                rc = enqueue_nf4_mfma_multi(&d, 1, m->hb, ffn, shift, B, false, m->mm_part, m->mm_part_floats, &t);
+                const T *const dts[1] = {&m->w_down[l]};
+                rc = gemm_tail(&d, dts, 1, m->hb, ffn, &t);
                 if (rc == ALJABR_ROCM_OK) {
-                    xb_scaled = l + 1 < c.layers;
+                    xb_scaled = defer;
                     ALJ_MARK("down_gemm_add_rmsnorm", mm_bytes(m->w_down[l], dim, ffn, true) + (B * dim + dim) * f4);
                 }
             }

@@ -532,11 +532,12 @@ int kquant_mfma_max_m(int type) {
 
 // 2 <= M <= kquant_mfma_max_m(type), K % 512 == 0, A and weights 16-byte
 // aligned, up to three matrices of one type (all but the last with a
-// multiple of 32 rows).
+// multiple of 32 rows). With `tail` (K >= 1024, not accumulating) the slice
+// sums go to the tail kernel instead of the outputs.
 int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate,
-                              float *part, size_t part_floats) {
+                              float *part, size_t part_floats, const SliceTail *tail) {
     if (!kquant_mfma_type(type) || nseg < 1 || nseg > 3 || M < 2 || M > kquant_mfma_max_m(type) || K % 512 != 0 ||
-        !aligned(A, 16))
+        !aligned(A, 16) || (tail && (accumulate || K < 1024)))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     KqArgs args{};
     long long end = 0;
@@ -578,6 +579,7 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
     case ALJABR_ROCM_TYPE_Q4_0: launch_kq_nt<kFQ40, 8>(args, two, s); break;
     default: launch_kq_nt<kFQ80, 8>(args, two, s); break;
     }
+    if (tail) return enqueue_slice_tail(*tail, args.part, slices, M, args.N);
     if (slices > 1) {
         float *ys[3] = {args.y[0], args.y[1], args.y[2]};
         return enqueue_slice_sum(ys, args.end, nseg, M, args.N, args.part, slices, accumulate);
