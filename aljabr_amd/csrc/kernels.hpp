@@ -72,6 +72,11 @@ struct KqOut {
 struct SliceTail;
 int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate,
                               float *part = nullptr, size_t part_floats = 0, const SliceTail *tail = nullptr);
+// The K slices' products only (K >= 1024), into part[slice][m][col0 + stacked
+// row] with row stride ld (part holds slices * M * ld floats, col0 % 32 == 0):
+// launches of different types stacked in one buffer, then one slice tail.
+int enqueue_kquant_mfma_parts(const KqOut *outs, int nseg, const float *A, int K, int type, int M, float *part,
+                              size_t part_floats, int ld, int col0);
 // ys[s] (+)= the K slices' partial sums part[slice][m][stacked row] of
 // segment s (stacked rows [ends[s-1], ends[s])), added in slice order.
 int enqueue_slice_sum(float *const *ys, const int *ends, int nseg, int M, int N, const float *part, int slices,

@@ -902,11 +902,42 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
     // One matrix-core GEMM over matrices of one type (NF4 or a K-quant) whose
     // slice sums go to the tail kernel `t`; UNSUPPORTED when the types or
     // shapes do not allow it (the caller then runs the separate launches).
+    auto kq_ok = [&](const T &w) { return kquant_mfma_type(w.type) && B <= kquant_mfma_max_m(w.type); };
     auto gemm_tail = [&](const RowsOut *o, const T *const *ts, int nseg, const float *x, int K,
                          const SliceTail *t) -> int {
         const int ty = ts[0]->type;
-        for (int i = 1; i < nseg; ++i)
-            if (ts[i]->type != ty) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        bool mixed = false;
+        for (int i = 1; i < nseg; ++i) mixed |= ts[i]->type != ty;
+        if (mixed) {
+            // K-quants of different types: one launch per run of one type,
+            // each into its columns of one partial-sum buffer, then the tail.
+            int n_all = 0;
+            for (int i = 0; i < nseg; ++i) {
+                if (!kq_ok(*ts[i])) return ALJABR_ROCM_ERR_UNSUPPORTED;
+                n_all += o[i].n;
+            }
+            const int slices = K / 512;
+            if (K % 512 != 0 || slices < 2 || static_cast<size_t>(slices) * B * n_all > m->mm_part_floats)
+                return ALJABR_ROCM_ERR_UNSUPPORTED;
+            for (int i = 0, col = 0; i < nseg;) {
+                int j = i + 1;
+                while (j < nseg && ts[j]->type == ts[i]->type) ++j;
+                KqOut k[3];
+                int n = 0;
+                for (int u = i; u < j; ++u) {
+                    k[u - i] = KqOut{o[u].y, o[u].w, o[u].n};
+                    n += o[u].n;
+                }
+                const int rc = enqueue_kquant_mfma_parts(k, j - i, x, K, ts[i]->type, B, m->mm_part,
+                                                         m->mm_part_floats, n_all, col);
+                // A refusal leaves nothing the fallback reads (it rewrites
+                // every output).
+                if (rc != ALJABR_ROCM_OK) return rc;
+                col += n;
+                i = j;
+            }
+            return enqueue_slice_tail(*t, m->mm_part, slices, B, n_all);
+        }
         if (ty == ALJABR_ROCM_TYPE_NF4)
             return m->all_nf4 ? enqueue_nf4_mfma_multi(o, nseg, x, K, shift, B, false, m->mm_part, m->mm_part_floats, t)
                               : ALJABR_ROCM_ERR_UNSUPPORTED;
@@ -915,9 +946,11 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         for (int i = 0; i < nseg; ++i) k[i] = KqOut{o[i].y, o[i].w, o[i].n};
         return enqueue_kquant_mfma_multi(k, nseg, x, K, ty, B, false, m->mm_part, m->mm_part_floats, t);
     };
-    // A residual tail defers RMSNorm's row scale only to a consumer whose
-    // matrices share one type (one launch, one tail).
-    auto same_type = [](const T &a, const T &b, const T &c) { return a.type == b.type && b.type == c.type; };
+    // A residual tail defers RMSNorm's row scale only to a consumer that
+    // takes a tail: matrices of one type, or K-quants the matrix cores take.
+    auto takes_tail = [&](const T &a, const T &b, const T &c) {
+        return (a.type == b.type && b.type == c.type) || (kq_ok(a) && kq_ok(b) && kq_ok(c));
+    };
     hipLaunchKernelGGL(lengths_from_positions, dim3((B + 63) / 64), dim3(64), 0, s, m->kv_len, pos, B);
     if (m->tok_embed.type == ALJABR_ROCM_TYPE_F32)
         ALJ_TRY(enqueue_embed(m->x, reinterpret_cast<const float *>(m->tok_embed.w), tok, B, dim, c.vocab));
@@ -1064,8 +1097,8 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             if (tails) {
                 // x += Wo att, then xb = x * the FFN norm with the row sums of
                 // squares for the gate/up tail (RMSNorm's row scale), or the
-                // full RMSNorm when gate and up differ in type.
-                const bool defer = same_type(m->w_gate[l], m->w_up[l], m->w_up[l]);
+                // full RMSNorm when gate and up cannot take a tail.
+                const bool defer = takes_tail(m->w_gate[l], m->w_up[l], m->w_up[l]);
                 SliceTail t{};
                 t.kind = defer ? kTailResidualScale : kTailResidualNorm;
                 t.out = m->x;
@@ -1169,7 +1202,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             rc = ALJABR_ROCM_ERR_UNSUPPORTED;
             xb_scaled = false;
             if (tails) {
-                const bool defer = l + 1 < c.layers && same_type(m->wq[l + 1], m->wk[l + 1], m->wv[l + 1]);
+                const bool defer = l + 1 < c.layers && takes_tail(m->wq[l + 1], m->wk[l + 1], m->wv[l + 1]);
                 SliceTail t{};
                 t.kind = defer ? kTailResidualScale : kTailResidualNorm;
                 t.out = m->x;

@@ -77,7 +77,8 @@ struct KqArgs {
     int nseg;
     int M, N, K;   // N: stacked rows
     int add;       // one K slice: Y += instead of Y =
-    float *part;   // several K slices: [slice][M][N] partial sums
+    float *part;   // several K slices: partial sums part[slice][m][col0 + stacked row], row stride ld
+    int ld, col0;
     int groups, slices;   // row groups (kRowsPerWg * NT rows each) and K slices of the launch
 };
 
@@ -483,12 +484,12 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
                 } else {
                     // This slice's partial tile; the slice sum adds the
                     // slices in order.
-                    float *ps = a.part + static_cast<size_t>(slice) * a.M * a.N + rgrp * (kRowsPerWg * NT) +
-                                t * kRowsPerWg + wave * 32 + nl;
+                    float *ps = a.part + static_cast<size_t>(slice) * a.M * a.ld + a.col0 +
+                                rgrp * (kRowsPerWg * NT) + t * kRowsPerWg + wave * 32 + nl;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int m = 8 * (r >> 2) + 4 * h + (r & 3);
-                        if (m < a.M) ps[static_cast<size_t>(m) * a.N] = acc[r];
+                        if (m < a.M) ps[static_cast<size_t>(m) * a.ld] = acc[r];
                     }
                 }
             }
@@ -530,16 +531,16 @@ int kquant_mfma_max_m(int type) {
     return type == ALJABR_ROCM_TYPE_Q4_0 || type == ALJABR_ROCM_TYPE_Q8_0 ? 8 : 32;
 }
 
-// 2 <= M <= kquant_mfma_max_m(type), K % 512 == 0, A and weights 16-byte
-// aligned, up to three matrices of one type (all but the last with a
-// multiple of 32 rows). With `tail` (K >= 1024, not accumulating) the slice
-// sums go to the tail kernel instead of the outputs.
-int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate,
-                              float *part, size_t part_floats, const SliceTail *tail) {
+namespace {
+
+// The launch arguments of up to three matrices of one type (all but the last
+// with a multiple of 32 rows): 2 <= M <= kquant_mfma_max_m(type),
+// K % 512 == 0, A and weights 16-byte aligned.
+int kq_multi_args(const KqOut *outs, int nseg, const float *A, int K, int type, int M, KqArgs &args) {
     if (!kquant_mfma_type(type) || nseg < 1 || nseg > 3 || M < 2 || M > kquant_mfma_max_m(type) || K % 512 != 0 ||
-        !aligned(A, 16) || (tail && (accumulate || K < 1024)))
+        !aligned(A, 16))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
-    KqArgs args{};
+    args = KqArgs{};
     long long end = 0;
     for (int i = 0; i < 3; ++i) {
         if (i < nseg) {
@@ -559,6 +560,33 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
     args.M = M;
     args.N = static_cast<int>(end);
     args.K = K;
+    args.ld = args.N;
+    return ALJABR_ROCM_OK;
+}
+
+void kq_launch(const KqArgs &args, int type, hipStream_t s) {
+    const int wgs_n = (args.N + kRowsPerWg - 1) / kRowsPerWg;
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const long long units = static_cast<long long>(wgs_n) * (args.K / 512);
+    const bool two = units > cus;
+    switch (type) {
+    case ALJABR_ROCM_TYPE_Q4_K: launch_kq_nt<kFQ4K, 32>(args, two, s); break;
+    case ALJABR_ROCM_TYPE_Q6_K: launch_kq_nt<kFQ6K, 32>(args, two, s); break;
+    case ALJABR_ROCM_TYPE_Q4_0: launch_kq_nt<kFQ40, 8>(args, two, s); break;
+    default: launch_kq_nt<kFQ80, 8>(args, two, s); break;
+    }
+}
+
+}  // namespace
+
+// With `tail` (K >= 1024, not accumulating) the slice sums go to the tail
+// kernel instead of the outputs.
+int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate,
+                              float *part, size_t part_floats, const SliceTail *tail) {
+    KqArgs args;
+    const int rc = kq_multi_args(outs, nseg, A, K, type, M, args);
+    if (rc != ALJABR_ROCM_OK) return rc;
+    if (tail && (accumulate || K < 1024)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     hipStream_t s = current_stream();
     const int slices = K / 512;
     args.add = slices == 1 && accumulate;
@@ -569,21 +597,28 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
                         : static_cast<float *>(stream_scratch(need * sizeof(float), kScratchPartials));
         if (!args.part) return ALJABR_ROCM_ERR_BUFFER;
     }
-    const int wgs_n = (args.N + kRowsPerWg - 1) / kRowsPerWg;
-    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-    const long long units = static_cast<long long>(wgs_n) * (K / 512);
-    const bool two = units > cus;
-    switch (type) {
-    case ALJABR_ROCM_TYPE_Q4_K: launch_kq_nt<kFQ4K, 32>(args, two, s); break;
-    case ALJABR_ROCM_TYPE_Q6_K: launch_kq_nt<kFQ6K, 32>(args, two, s); break;
-    case ALJABR_ROCM_TYPE_Q4_0: launch_kq_nt<kFQ40, 8>(args, two, s); break;
-    default: launch_kq_nt<kFQ80, 8>(args, two, s); break;
-    }
+    kq_launch(args, type, s);
     if (tail) return enqueue_slice_tail(*tail, args.part, slices, M, args.N);
     if (slices > 1) {
         float *ys[3] = {args.y[0], args.y[1], args.y[2]};
         return enqueue_slice_sum(ys, args.end, nseg, M, args.N, args.part, slices, accumulate);
     }
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_kquant_mfma_parts(const KqOut *outs, int nseg, const float *A, int K, int type, int M, float *part,
+                              size_t part_floats, int ld, int col0) {
+    KqArgs args;
+    const int rc = kq_multi_args(outs, nseg, A, K, type, M, args);
+    if (rc != ALJABR_ROCM_OK) return rc;
+    const int slices = K / 512;
+    if (slices < 2 || !part || col0 < 0 || col0 % 32 != 0 || static_cast<long long>(col0) + args.N > ld ||
+        static_cast<size_t>(slices) * M * ld > part_floats)
+        return ALJABR_ROCM_ERR_UNSUPPORTED;
+    args.part = part;
+    args.ld = ld;
+    args.col0 = col0;
+    kq_launch(args, type, current_stream());
     return ALJABR_ROCM_OK;
 }
 
