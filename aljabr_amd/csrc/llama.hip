@@ -976,11 +976,20 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                                     {m->v, W(m->wv), S(m->wv), kvd}};
             const int tq = m->wq[l].type, tk = m->wk[l].type, tv = m->wv[l].type;
             const RowsRope rope{pos, kc, vc, c.max_seq, hd, c.rope_base, m->rope_cs, c.n_kv_heads};
-            // One launch per run of one type (a Q6_K attn_v beside Q4_K q and
-            // k takes two), the other segments left empty.
+            // One launch per run of one type, the other segments left empty,
+            // except Q4_K q and k beside a Q6_K v (a Q4_K_M model), which share
+            // one launch of two row formats.
             const int types[3] = {tq, tk, tv};
+            bool launched = false;
+            if (tq == tk && tv != tq) {
+                rc = enqueue_rows_rope_mixed(tq, tv, qkv, m->x, attn_norm, c.eps, dim, &rope);
+                if (rc != ALJABR_ROCM_ERR_UNSUPPORTED) {
+                    if (rc != ALJABR_ROCM_OK) return rc;
+                    launched = true;
+                }
+            }
             rc = ALJABR_ROCM_OK;
-            for (int i = 0; i < 3 && rc == ALJABR_ROCM_OK;) {
+            for (int i = 0; i < 3 && rc == ALJABR_ROCM_OK && !launched;) {
                 int j = i + 1;
                 while (j < 3 && types[j] == types[i]) ++j;
                 RowsOut part[3] = {qkv[0], qkv[1], qkv[2]};

@@ -460,11 +460,10 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
 // P0 rows are requested before the set-up (table build, activation staging)
 // and PF rows stay in flight afterwards: a deeper prologue keeps HBM busy
 // while the activations arrive, a shallower steady state measured faster.
+// One workgroup's rows: workgroup `blk` of a launch covering the stacked rows
+// [row_base, row_end) in format FMT.
 template <int FMT, int T, int PF, int W, int XOP, int EPI, int P0>
-__global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint8_t *w0, const float *s0,
-                                                      const uint8_t *w1, const float *s1, int N, int end0, int end1,
-                                                      int shape, RowsArgs a) {
-    RowsHot h = rows_hot(x, w0, s0, w1, s1, N, end0, end1, shape);
+__device__ __forceinline__ void rows_body(RowsHot h, const RowsArgs &a, unsigned blk, int row_base, int row_end) {
     static_assert(T >= 1 && T <= 32 && PF >= 1 && P0 >= PF && (W == 8 || W == 16), "tile shape");
     constexpr int TP = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : T <= 16 ? 16 : 32;   // butterfly width
     extern __shared__ float4 smem[];    // see kMainBytes
@@ -494,7 +493,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint
     // Each wave streams the T contiguous rows row0 .. row0 + T-1 of the
     // stacked row space (measured a few percent faster on MI355X than
     // interleaving rows across the grid).
-    const int row0 = (blockIdx.x * h.G + grp) * T;
+    const int row0 = row_base + static_cast<int>((blk * h.G + grp) * T);
     const int rstride = 1;
     const LaneOffsets lo = lane_offsets<FMT>(lane, h.bs_shift);
     with_seg2<EPI>(h, a);
@@ -517,7 +516,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint
     }
     RowWords<FMT> rw[T];
 #pragma unroll
-    for (int t = 0; t < P0 && t < T; ++t) load_row<FMT, EPI, T>(rw[t], h, a, min(row0 + t * rstride, h.N - 1), chunk, lo);
+    for (int t = 0; t < P0 && t < T; ++t) load_row<FMT, EPI, T>(rw[t], h, a, min(row0 + t * rstride, row_end - 1), chunk, lo);
     // The table does not depend on the loads: build it while they fly.
     if constexpr (pair_table_fmt(FMT)) build_pair_table<FMT, W * 64>(tbl2, tid);
 
@@ -566,7 +565,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint
     // position has arrived). Each output element belongs to one finishing
     // lane, so reading it early is the same read.
     const int r = row0 + lane;
-    const bool finisher = chunk == 0 && lane < T && r < h.N;
+    const bool finisher = chunk == 0 && lane < T && r < row_end;
     float y_old = 0.0f;
     int rope_p = 0;
     float rope_c = 1.0f, rope_s = 0.0f;
@@ -611,7 +610,7 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         if (t + PF < T && t + PF >= P0)
-            load_row<FMT, EPI, T>(rw[t + PF], h, a, min(row0 + (t + PF) * rstride, h.N - 1), chunk, lo);
+            load_row<FMT, EPI, T>(rw[t + PF], h, a, min(row0 + (t + PF) * rstride, row_end - 1), chunk, lo);
         if constexpr (EPI == kERopeKV) {
             if (t == T / 2 && finisher && (lane & 1) == 0) {
                 const RowRef f = row_ref<EPI, T>(h, r);
@@ -676,6 +675,30 @@ __global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint
             }
         }
     }
+}
+
+template <int FMT, int T, int PF, int W, int XOP, int EPI, int P0>
+__global__ __launch_bounds__(W * 64) void rows_kernel(const float *x, const uint8_t *w0, const float *s0,
+                                                      const uint8_t *w1, const float *s1, int N, int end0, int end1,
+                                                      int shape, RowsArgs a) {
+    rows_body<FMT, T, PF, W, XOP, EPI, P0>(rows_hot(x, w0, s0, w1, s1, N, end0, end1, shape), a, blockIdx.x, 0, N);
+}
+
+// Two row formats in one launch (8 waves): workgroups [0, nb0) take the
+// stacked rows [0, end1) in format F0, T0 rows per wave, the rest take
+// [end1, N) in format F1, T1 rows per wave; the branch is per workgroup. Q
+// and K of one type beside V of another (a Q4_K_M model's Q6_K V) then share
+// one activation staging, RMSNorm and launch. nb0 rides in the shape word's
+// bits 18 and up, so the branch waits for no argument read.
+template <int F0, int T0, int PF0, int F1, int T1, int PF1, int XOP, int EPI>
+__global__ __launch_bounds__(512) void rows_mix_kernel(const float *x, const uint8_t *w0, const float *s0,
+                                                       const uint8_t *w1, const float *s1, int N, int end0, int end1,
+                                                       int shape, RowsArgs a) {
+    const RowsHot h = rows_hot(x, w0, s0, w1, s1, N, end0, end1, shape);
+    const int nb0 = static_cast<int>(static_cast<unsigned>(shape) >> 18);
+    const unsigned blk = blockIdx.x;
+    if (blk < static_cast<unsigned>(nb0)) rows_body<F0, T0, PF0, 8, XOP, EPI, PF0>(h, a, blk, 0, end1);
+    else rows_body<F1, T1, PF1, 8, XOP, EPI, PF1>(h, a, blk - nb0, end1, N);
 }
 
 template <int FMT, int T, int PF, int W, int XOP, int EPI, int P0 = PF>
@@ -1020,15 +1043,19 @@ int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const 
     return enqueue_rows_fused(ALJABR_ROCM_TYPE_NF4, outs, nseg, x, norm_w, eps, K, bs_shift, epilogue, rope);
 }
 
-int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
-                       int bs_shift, int epilogue, const RowsRope *rope) {
+namespace {
+
+// The launch arguments of a fused rows launch (segments, epilogue operands,
+// shape), or UNSUPPORTED.
+int fused_args(int type, const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
+               int bs_shift, int epilogue, const RowsRope *rope, RowsArgs &args) {
     if (nseg < 1 || nseg > 3 || !rows_shape_ok(x, K)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     if (type == ALJABR_ROCM_TYPE_NF4 && (bs_shift < 5 || bs_shift > 11)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     if (type != ALJABR_ROCM_TYPE_NF4 && type != ALJABR_ROCM_TYPE_Q4_0 && type != ALJABR_ROCM_TYPE_Q8_0 &&
         type != ALJABR_ROCM_TYPE_Q4_K && type != ALJABR_ROCM_TYPE_Q6_K)
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     if (norm_w && !aligned(norm_w, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
-    RowsArgs args{};
+    args = RowsArgs{};
     if (epilogue == kRowsSwiGLU || epilogue == kRowsGeGLU) {
         // gate (segment 0) and up (segment 1) interleaved row by row.
         if (nseg != 2 || outs[0].n != outs[1].n) return ALJABR_ROCM_ERR_UNSUPPORTED;
@@ -1079,6 +1106,76 @@ int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, 
     args.K = K;
     args.bs_shift = bs_shift;
     args.S = K / kChunk;
+    args.G = 8 / args.S;
+    return ALJABR_ROCM_OK;
+}
+
+template <int F0, int T0, int F1, int T1>
+void launch_mix(const RowsArgs &args, int nb0, int nb1, hipStream_t s) {
+    constexpr int PF0 = T0 <= 4 ? 2 : 3, PF1 = T1 <= 4 ? 2 : 3;
+    constexpr int TPM = T0 > T1 ? (T0 <= 4 ? 4 : 8) : (T1 <= 4 ? 4 : 8);
+    const void *fn = reinterpret_cast<const void *>(rows_mix_kernel<F0, T0, PF0, F1, T1, PF1, kXNorm, kERopeKV>);
+    static bool lds_set = false;                 // the attribute is per kernel, per process
+    if (!lds_set) {
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+        lds_set = true;
+    }
+    const size_t lds = kLdsBytes + (8 * TPM + 8) * sizeof(float);
+    hipLaunchKernelGGL((rows_mix_kernel<F0, T0, PF0, F1, T1, PF1, kXNorm, kERopeKV>), dim3(nb0 + nb1), dim3(512), lds,
+                       s, args.x, args.seg[0].w, args.seg[0].absmax, args.seg[1].w, args.seg[1].absmax, args.N,
+                       args.seg[0].end, args.seg[1].end, rows_shape_word(args) | (nb0 << 18), args);
+}
+
+template <int F0, int F1, int T0>
+void launch_mix_t1(const RowsArgs &args, int T1, int nb0, int nb1, hipStream_t s) {
+    if (T1 == 2) launch_mix<F0, T0, F1, 2>(args, nb0, nb1, s);
+    else if (T1 == 4) launch_mix<F0, T0, F1, 4>(args, nb0, nb1, s);
+    else launch_mix<F0, T0, F1, 8>(args, nb0, nb1, s);
+}
+
+}  // namespace
+
+// Q and K (segments 0 and 1) in Q4_K beside V (segment 2) in Q6_K: RMSNorm,
+// the products, RoPE and the cache append in one launch. T0 is the one-type
+// launch's rows per wave for the first two segments; T1 (2, 4 or 8) the
+// smallest that keeps both parts' workgroups within one per CU. UNSUPPORTED
+// for other types or shapes (the caller then launches per type).
+int enqueue_rows_rope_mixed(int type01, int type2, const RowsOut *outs, const float *x, const float *norm_w,
+                            float eps, int K, const RowsRope *rope) {
+    if (type01 != ALJABR_ROCM_TYPE_Q4_K || type2 != ALJABR_ROCM_TYPE_Q6_K || !norm_w) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    if (outs[0].n <= 0 || outs[1].n <= 0 || outs[2].n <= 0) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    RowsArgs args;
+    const int rc = fused_args(type01, outs, 3, x, norm_w, eps, K, 0, kRowsRopeKV, rope, args);
+    if (rc != ALJABR_ROCM_OK) return rc;
+    if (args.S > 2) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const int n0 = args.seg[1].end, n1 = args.N - n0;
+    const int T0 = pick_rows_t(n0, args.S, 8);   // even, 2..8
+    const int nb0 = (n0 + args.G * T0 - 1) / (args.G * T0);
+    int T1 = 0, nb1 = 0;
+    for (int t = 2; t <= 8; t *= 2) {
+        nb1 = (n1 + args.G * t - 1) / (args.G * t);
+        if (nb0 + nb1 <= cus) {
+            T1 = t;
+            break;
+        }
+    }
+    if (!T1 || nb0 >= (1 << 13)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    hipStream_t s = current_stream();
+    switch (T0) {
+    case 2: launch_mix_t1<kFmtQ4K, kFmtQ6K, 2>(args, T1, nb0, nb1, s); break;
+    case 4: launch_mix_t1<kFmtQ4K, kFmtQ6K, 4>(args, T1, nb0, nb1, s); break;
+    case 6: launch_mix_t1<kFmtQ4K, kFmtQ6K, 6>(args, T1, nb0, nb1, s); break;
+    default: launch_mix_t1<kFmtQ4K, kFmtQ6K, 8>(args, T1, nb0, nb1, s); break;
+    }
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
+                       int bs_shift, int epilogue, const RowsRope *rope) {
+    RowsArgs args;
+    const int rc = fused_args(type, outs, nseg, x, norm_w, eps, K, bs_shift, epilogue, rope, args);
+    if (rc != ALJABR_ROCM_OK) return rc;
     int T = pick_rows_t(args.N, args.S, 32);
     if (T & 1) ++T;                              // the paired epilogues need both rows of a pair in one wave
     if ((epilogue == kRowsSwiGLU || epilogue == kRowsGeGLU) && (outs[0].n % (T / 2)) != 0)

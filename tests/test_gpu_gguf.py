@@ -20,6 +20,11 @@ CFG = dict(layers=2, dim=512, ffn=1536, n_heads=8, n_kv_heads=2, head_dim=64, vo
            rope_base=500000.0, eps=1e-5)
 CFG_BIG = dict(layers=2, dim=2048, ffn=4096, n_heads=16, n_kv_heads=4, head_dim=128, vocab=512, max_seq=16,
                rope_base=500000.0, eps=1e-5)
+# Llama-3-8B attention width (32/8 heads of 128 over 4096): the batch-1 Q/K/V
+# launch of two row formats at the shipped tile shape (6 Q4_K rows per wave,
+# 8 Q6_K rows per wave, 246 workgroups).
+CFG_WIDE = dict(layers=2, dim=4096, ffn=2048, n_heads=32, n_kv_heads=8, head_dim=128, vocab=512, max_seq=16,
+                rope_base=500000.0, eps=1e-5)
 # Q4_K_M-like mix; every supported type; tied LM head; K % 2048 (batch-1 rows kernels).
 MIXES = {
     "q4_k_m": (CFG, dict(tok_embed=gw.Q4_K, wq=gw.Q4_K, wk=gw.Q4_K, wv=gw.Q6_K, wo=gw.Q4_K, w_gate=gw.Q4_K,
@@ -28,6 +33,8 @@ MIXES = {
                             w_up=gw.Q4_K, w_down=gw.Q8_0, lm_head=gw.F16)),
     "tied_f16": (CFG, dict(tok_embed=gw.F16, wq=gw.Q8_0, wk=gw.Q8_0, wv=gw.Q8_0, wo=gw.Q8_0, w_gate=gw.Q4_0,
                            w_up=gw.Q4_0, w_down=gw.Q4_0, lm_head=None)),
+    "rows_k4096_q4_k_m": (CFG_WIDE, dict(tok_embed=gw.Q4_K, wq=gw.Q4_K, wk=gw.Q4_K, wv=gw.Q6_K, wo=gw.Q4_K,
+                                         w_gate=gw.Q4_K, w_up=gw.Q4_K, w_down=gw.Q6_K, lm_head=gw.Q6_K)),
     "rows_k2048": (CFG_BIG, dict(tok_embed=gw.Q6_K, wq=gw.Q4_K, wk=gw.Q4_K, wv=gw.Q6_K, wo=gw.Q4_K,
                                  w_gate=gw.Q4_K, w_up=gw.Q4_K, w_down=gw.Q6_K, lm_head=gw.Q6_K)),
     # Batch-1 fused launches per format: one-type Q/K/V (RoPE + append
@@ -71,7 +78,8 @@ def _run_against_oracle(dev, oracle, model, cfg, weights, batch, steps=5, graph=
 
 
 @pytest.mark.parametrize("name,batch", [("q4_k_m", 1), ("q4_k_m", 3), ("all_types", 1), ("all_types", 2),
-                                        ("tied_f16", 2), ("rows_k2048", 1), ("rows_k2048", 3), ("rows_q8", 1),
+                                        ("tied_f16", 2), ("rows_k2048", 1), ("rows_k2048", 3), ("rows_k4096_q4_k_m", 1),
+                                        ("rows_k4096_q4_k_m", 2), ("rows_q8", 1),
                                         ("rows_q6_mixed", 1), ("rows_q6_mixed", 2)])
 def test_gguf_file_decode_matches_oracle(rocm, dev, oracle, tmp_path, name, batch):
     from aljabr_amd.llama import DeviceLlama
