@@ -134,10 +134,11 @@ int enqueue_nf4_rows_fused(const RowsOut *outs, int nseg, const float *x, const 
 // or Q6_K (absmax and bs_shift for NF4 only).
 int enqueue_rows_fused(int type, const RowsOut *outs, int nseg, const float *x, const float *norm_w, float eps, int K,
                        int bs_shift, int epilogue, const RowsRope *rope = nullptr);
-// RMSNorm + Q and K in type01 + V in type2 + RoPE and the cache append in one
-// launch (kRowsRopeKV; Q4_K beside Q6_K), or UNSUPPORTED.
-int enqueue_rows_rope_mixed(int type01, int type2, const RowsOut *outs, const float *x, const float *norm_w,
-                            float eps, int K, const RowsRope *rope);
+// RMSNorm + Q and K in type01 + V in type2 in one launch (Q4_K beside Q6_K),
+// with RoPE and the cache append (kRowsRopeKV) or stored (kRowsStore), or
+// UNSUPPORTED.
+int enqueue_rows_mixed(int type01, int type2, const RowsOut *outs, const float *x, const float *norm_w, float eps,
+                       int K, int epilogue, const RowsRope *rope = nullptr);
 // What the second kernel of a split-K GEMM does with the slice sums besides
 // (or instead of) writing them: the decode step's next element-wise launch,
 // applied to the stacked rows of the GEMM (slice_tails.hip).

@@ -982,7 +982,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             const int types[3] = {tq, tk, tv};
             bool launched = false;
             if (tq == tk && tv != tq) {
-                rc = enqueue_rows_rope_mixed(tq, tv, qkv, m->x, attn_norm, c.eps, dim, &rope);
+                rc = enqueue_rows_mixed(tq, tv, qkv, m->x, attn_norm, c.eps, dim, kRowsRopeKV, &rope);
                 if (rc != ALJABR_ROCM_ERR_UNSUPPORTED) {
                     if (rc != ALJABR_ROCM_OK) return rc;
                     launched = true;

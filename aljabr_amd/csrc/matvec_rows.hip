@@ -1110,42 +1110,55 @@ int fused_args(int type, const RowsOut *outs, int nseg, const float *x, const fl
     return ALJABR_ROCM_OK;
 }
 
-template <int F0, int T0, int F1, int T1>
+template <int F0, int T0, int F1, int T1, int EPI>
 void launch_mix(const RowsArgs &args, int nb0, int nb1, hipStream_t s) {
     constexpr int PF0 = T0 <= 4 ? 2 : 3, PF1 = T1 <= 4 ? 2 : 3;
     constexpr int TPM = T0 > T1 ? (T0 <= 4 ? 4 : 8) : (T1 <= 4 ? 4 : 8);
-    const void *fn = reinterpret_cast<const void *>(rows_mix_kernel<F0, T0, PF0, F1, T1, PF1, kXNorm, kERopeKV>);
+    const void *fn = reinterpret_cast<const void *>(rows_mix_kernel<F0, T0, PF0, F1, T1, PF1, kXNorm, EPI>);
     static bool lds_set = false;                 // the attribute is per kernel, per process
     if (!lds_set) {
         (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
         lds_set = true;
     }
     const size_t lds = kLdsBytes + (8 * TPM + 8) * sizeof(float);
-    hipLaunchKernelGGL((rows_mix_kernel<F0, T0, PF0, F1, T1, PF1, kXNorm, kERopeKV>), dim3(nb0 + nb1), dim3(512), lds,
+    hipLaunchKernelGGL((rows_mix_kernel<F0, T0, PF0, F1, T1, PF1, kXNorm, EPI>), dim3(nb0 + nb1), dim3(512), lds,
                        s, args.x, args.seg[0].w, args.seg[0].absmax, args.seg[1].w, args.seg[1].absmax, args.N,
                        args.seg[0].end, args.seg[1].end, rows_shape_word(args) | (nb0 << 18), args);
 }
 
-template <int F0, int F1, int T0>
+template <int F0, int F1, int T0, int EPI>
 void launch_mix_t1(const RowsArgs &args, int T1, int nb0, int nb1, hipStream_t s) {
-    if (T1 == 2) launch_mix<F0, T0, F1, 2>(args, nb0, nb1, s);
-    else if (T1 == 4) launch_mix<F0, T0, F1, 4>(args, nb0, nb1, s);
-    else launch_mix<F0, T0, F1, 8>(args, nb0, nb1, s);
+    if (T1 == 2) launch_mix<F0, T0, F1, 2, EPI>(args, nb0, nb1, s);
+    else if (T1 == 4) launch_mix<F0, T0, F1, 4, EPI>(args, nb0, nb1, s);
+    else launch_mix<F0, T0, F1, 8, EPI>(args, nb0, nb1, s);
+}
+
+template <int EPI>
+void launch_mix_t0(const RowsArgs &args, int T0, int T1, int nb0, int nb1, hipStream_t s) {
+    switch (T0) {
+    case 2: launch_mix_t1<kFmtQ4K, kFmtQ6K, 2, EPI>(args, T1, nb0, nb1, s); break;
+    case 4: launch_mix_t1<kFmtQ4K, kFmtQ6K, 4, EPI>(args, T1, nb0, nb1, s); break;
+    case 6: launch_mix_t1<kFmtQ4K, kFmtQ6K, 6, EPI>(args, T1, nb0, nb1, s); break;
+    default: launch_mix_t1<kFmtQ4K, kFmtQ6K, 8, EPI>(args, T1, nb0, nb1, s); break;
+    }
 }
 
 }  // namespace
 
-// Q and K (segments 0 and 1) in Q4_K beside V (segment 2) in Q6_K: RMSNorm,
-// the products, RoPE and the cache append in one launch. T0 is the one-type
-// launch's rows per wave for the first two segments; T1 (2, 4 or 8) the
-// smallest that keeps both parts' workgroups within one per CU. UNSUPPORTED
-// for other types or shapes (the caller then launches per type).
-int enqueue_rows_rope_mixed(int type01, int type2, const RowsOut *outs, const float *x, const float *norm_w,
-                            float eps, int K, const RowsRope *rope) {
-    if (type01 != ALJABR_ROCM_TYPE_Q4_K || type2 != ALJABR_ROCM_TYPE_Q6_K || !norm_w) return ALJABR_ROCM_ERR_UNSUPPORTED;
+// Q and K (segments 0 and 1) in Q4_K beside V (segment 2) in Q6_K: RMSNorm
+// and the products in one launch, with RoPE and the cache append
+// (kRowsRopeKV) or stored (kRowsStore). T0 is the one-type launch's rows per
+// wave for the first two segments; T1 (2, 4 or 8) the smallest that keeps
+// both parts' workgroups within one per CU. UNSUPPORTED for other types,
+// epilogues or shapes (the caller then launches per type).
+int enqueue_rows_mixed(int type01, int type2, const RowsOut *outs, const float *x, const float *norm_w, float eps,
+                       int K, int epilogue, const RowsRope *rope) {
+    if (type01 != ALJABR_ROCM_TYPE_Q4_K || type2 != ALJABR_ROCM_TYPE_Q6_K || !norm_w ||
+        (epilogue != kRowsRopeKV && epilogue != kRowsStore))
+        return ALJABR_ROCM_ERR_UNSUPPORTED;
     if (outs[0].n <= 0 || outs[1].n <= 0 || outs[2].n <= 0) return ALJABR_ROCM_ERR_UNSUPPORTED;
     RowsArgs args;
-    const int rc = fused_args(type01, outs, 3, x, norm_w, eps, K, 0, kRowsRopeKV, rope, args);
+    const int rc = fused_args(type01, outs, 3, x, norm_w, eps, K, 0, epilogue, rope, args);
     if (rc != ALJABR_ROCM_OK) return rc;
     if (args.S > 2) return ALJABR_ROCM_ERR_UNSUPPORTED;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
@@ -1162,12 +1175,8 @@ int enqueue_rows_rope_mixed(int type01, int type2, const RowsOut *outs, const fl
     }
     if (!T1 || nb0 >= (1 << 13)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     hipStream_t s = current_stream();
-    switch (T0) {
-    case 2: launch_mix_t1<kFmtQ4K, kFmtQ6K, 2>(args, T1, nb0, nb1, s); break;
-    case 4: launch_mix_t1<kFmtQ4K, kFmtQ6K, 4>(args, T1, nb0, nb1, s); break;
-    case 6: launch_mix_t1<kFmtQ4K, kFmtQ6K, 6>(args, T1, nb0, nb1, s); break;
-    default: launch_mix_t1<kFmtQ4K, kFmtQ6K, 8>(args, T1, nb0, nb1, s); break;
-    }
+    if (epilogue == kRowsRopeKV) launch_mix_t0<kERopeKV>(args, T0, T1, nb0, nb1, s);
+    else launch_mix_t0<kEStore3>(args, T0, T1, nb0, nb1, s);
     return ALJABR_ROCM_OK;
 }
 

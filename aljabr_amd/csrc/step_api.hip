@@ -565,6 +565,13 @@ int decode_step_locked(State &st, int pos, int window, float eps, const float *x
             const int ns[3] = {c.n0, c.n1, c.n2};
             bool done[3] = {false, c.k.w == nullptr, c.v.w == nullptr};
             bool xb_ready = false;
+            if (c.k.w && c.v.w && c.q.type == c.k.type && c.v.type != c.q.type) {
+                // Q4_K q and k beside a Q6_K v: one launch of two row formats.
+                const RowsOut outs[3] = {{q, c.q.w, nullptr, c.n0}, {k, c.k.w, nullptr, c.n1}, {v, c.v.w, nullptr, c.n2}};
+                rc = enqueue_rows_mixed(c.q.type, c.v.type, outs, x, attn_norm, eps, dim, kRowsStore);
+                if (rc == ALJABR_ROCM_OK) done[0] = done[1] = done[2] = true;
+                else if (rc != ALJABR_ROCM_ERR_UNSUPPORTED) return rc;
+            }
             for (int i = 0; i < 3; ++i) {
                 if (done[i]) continue;
                 RowsOut outs[3];
