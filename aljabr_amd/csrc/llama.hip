@@ -893,10 +893,10 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         return weight_bytes(t.type, N, K, bs) + B * (K + N * (add ? 2.0 : 1.0)) * f4;
     };
     const bool fused1 = B == 1 && m->rows_fused;
-    // Batches of 2..32 over NF4 weights: each GEMM's slice-sum kernel also runs
-    // the step that follows it (RoPE and the KV append, the residual add and
-    // the next RMSNorm, SwiGLU), so xb holds the next RMSNorm at every layer's
-    // start. A GEMM the matrix cores do not take falls back to the separate
+    // Batches of 2..32 over NF4 (block 64) or K-quant weights: each GEMM's
+    // slice-sum kernel also runs the step that follows it (RoPE and the KV
+    // append, the residual add and the next RMSNorm or its row-block sums,
+    // SwiGLU). A GEMM the matrix cores do not take falls back to the separate
     // launches for that block only.
     const bool tails = !fused1 && B >= 2 && B <= 32 && (!m->all_nf4 || shift == 6);
     // One matrix-core GEMM over matrices of one type (NF4 or a K-quant) whose
