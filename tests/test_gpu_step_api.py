@@ -128,11 +128,12 @@ def _typed(oracle, t, n, k, seed):
     return t, w.astype(np.float32)
 
 
-def _wide_model(oracle, activation, qkv_types, seed=900, max_seq=96):
+def _wide_model(oracle, activation, qkv_types, seed=900, max_seq=96, dim=2048, ffn=4096, nh=16, nkv=4):
     """Two layers at width 2048 (16 query heads, 4 KV heads of 128, FFN
-    4096, vocab 1024): layer 0 takes the types in qkv_types, Q4_K wO and
-    gate/up, Q6_K down; layer 1 Q4_K Q/K, Q6_K V (a Q4_K_M mix), Q8_0 FFN."""
-    dim, ffn, nh, nkv, hd, vocab = 2048, 4096, 16, 4, 128, 1024
+    4096, vocab 1024) unless given: layer 0 takes the types in qkv_types, Q4_K
+    wO and gate/up, Q6_K down; layer 1 Q4_K Q/K, Q6_K V (a Q4_K_M mix), Q8_0
+    FFN."""
+    hd, vocab = 128, 1024
     layers = []
     specs = [(qkv_types, Q4_K, (Q4_K, Q4_K, Q6_K)), ((Q4_K, Q4_K, Q6_K), Q4_K, (Q8_0, Q8_0, Q8_0))]
     for l, (qkv, wo_t, ffn_t) in enumerate(specs):
@@ -150,20 +151,26 @@ def _wide_model(oracle, activation, qkv_types, seed=900, max_seq=96):
                 out_w=_typed(oracle, Q6_K, vocab, dim, seed + 53), embd=_typed(oracle, Q6_K, vocab, dim, seed + 54))
 
 
-@pytest.mark.parametrize("activation,qkv_types", [(1, (Q4_K, Q4_K, Q4_K)), (2, (Q8_0, Q8_0, Q8_0))],
-                         ids=["silu_q4k", "gelu_q8"])
-def test_wide_quantized_step_with_synced_prefix(rocm, dev, oracle, activation, qkv_types):
+# The last case has Llama-3-8B's attention width (32/8 heads of 128 over 4096):
+# layer 1's Q4_K Q/K beside its Q6_K V run as one two-format rows launch at
+# the decode shape's tiles (6 Q4_K rows per wave, 8 Q6_K rows per wave).
+@pytest.mark.parametrize("activation,qkv_types,shape,P",
+                         [(1, (Q4_K, Q4_K, Q4_K), (2048, 4096, 16, 4), 70),
+                          (2, (Q8_0, Q8_0, Q8_0), (2048, 4096, 16, 4), 70),
+                          (1, (Q4_K, Q4_K, Q6_K), (4096, 2048, 32, 8), 20)],
+                         ids=["silu_q4k", "gelu_q8", "silu_q4k_m_width4096"])
+def test_wide_quantized_step_with_synced_prefix(rocm, dev, oracle, activation, qkv_types, shape, P):
     """The oracle decodes positions 0..P-1; its caches are loaded with
     sync_kv_cache; both then decode P..P+7 from tokens."""
-    model = _wide_model(oracle, activation, qkv_types)
-    P = 70
+    dim, ffn, nh, nkv = shape
+    model = _wide_model(oracle, activation, qkv_types, dim=dim, ffn=ffn, nh=nh, nkv=nkv)
     tokens = oracle.uniform_int(23, model["vocab"], P + 8)
     orc = oracle.StepOracle(model)
     for p in range(P):
         orc.decode(p, 0, EPS, token=int(tokens[p]))
     reg = Registry(rocm, dev, model, host=False)
     for l in range(2):
-        stride = 4 * 128
+        stride = nkv * 128
         k = np.ascontiguousarray(orc.k_cache[l][: P * stride])
         v = np.ascontiguousarray(orc.v_cache[l][: P * stride])
         rocm.call("aljabr_rocm_sync_kv_cache", l, P, k.ctypes.data, v.ctypes.data)
