@@ -77,6 +77,11 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
 // launches of different types stacked in one buffer, then one slice tail.
 int enqueue_kquant_mfma_parts(const KqOut *outs, int nseg, const float *A, int K, int type, int M, float *part,
                               size_t part_floats, int ld, int col0);
+// The same for two types in one launch (Q4_K matrices, then Q6_K ones, all
+// over the same x): part[slice][m][stacked row of both] with row stride the
+// rows of both, or UNSUPPORTED (other types, or more workgroups than CUs).
+int enqueue_kquant_mfma_parts2(const KqOut *outs0, int nseg0, int type0, const KqOut *outs1, int nseg1, int type1,
+                               const float *A, int K, int M, float *part, size_t part_floats);
 // ys[s] (+)= the K slices' partial sums part[slice][m][stacked row] of
 // segment s (stacked rows [ends[s-1], ends[s])), added in slice order.
 int enqueue_slice_sum(float *const *ys, const int *ends, int nseg, int M, int N, const float *part, int slices,

@@ -919,6 +919,20 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             const int slices = K / 512;
             if (K % 512 != 0 || slices < 2 || static_cast<size_t>(slices) * B * n_all > m->mm_part_floats)
                 return ALJABR_ROCM_ERR_UNSUPPORTED;
+            // Two runs (Q4_K q and k, then a Q6_K v): one launch of both.
+            int j0 = 1;
+            while (j0 < nseg && ts[j0]->type == ty) ++j0;
+            bool two_runs = j0 < nseg;
+            for (int u = j0 + 1; u < nseg; ++u) two_runs &= ts[u]->type == ts[j0]->type;
+            if (two_runs) {
+                KqOut k0[3], k1[3];
+                for (int u = 0; u < nseg; ++u)
+                    (u < j0 ? k0[u] : k1[u - j0]) = KqOut{o[u].y, o[u].w, o[u].n};
+                const int rc = enqueue_kquant_mfma_parts2(k0, j0, ty, k1, nseg - j0, ts[j0]->type, x, K, B, m->mm_part,
+                                                          m->mm_part_floats);
+                if (rc == ALJABR_ROCM_OK) return enqueue_slice_tail(*t, m->mm_part, slices, B, n_all);
+                if (rc != ALJABR_ROCM_ERR_UNSUPPORTED) return rc;
+            }
             for (int i = 0, col = 0; i < nseg;) {
                 int j = i + 1;
                 while (j < nseg && ts[j]->type == ts[i]->type) ++j;

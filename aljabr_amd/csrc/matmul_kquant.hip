@@ -46,6 +46,8 @@
 // group) and transposed through per-wave LDS rows, two units ahead. With
 // several K-slices each stores its partial tile and enqueue_slice_sum adds
 // the slices in order (deterministic: no float atomics).
+#include <algorithm>
+
 #include "device.hpp"
 #include "internal.hpp"
 #include "kernels.hpp"
@@ -242,8 +244,9 @@ __device__ __forceinline__ void stage_unit(uint8_t *st, const u32x4 (&q)[KqGeom<
     }
 }
 
+// Workgroup L of a launch over the (row group, K slice) items of `a`.
 template <int F, int KS, int NT, int MT>
-__global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
+__device__ __forceinline__ void kq_body(const KqArgs &a, int L) {
     using G = KqGeom<F>;
     constexpr bool Q6 = F == kFQ6K;
     constexpr bool SUMS = F == kFQ4K;            // the min term needs sub-block sums of x
@@ -270,7 +273,6 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
     // count is a multiple of 8, slice-major order already keeps a row group
     // on one XCD; otherwise XCD x takes the contiguous run [x * per,
     // (x + 1) * per) of the (row group, slice) items in row-major order.
-    const int L = static_cast<int>(blockIdx.x);
     const int total = a.groups * a.slices;
     int rgrp, slice;
     if ((a.groups & 7) == 0) {
@@ -498,6 +500,22 @@ __global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
 }
 
 template <int F, int KS, int NT, int MT>
+__global__ __launch_bounds__(kThreads) void kq_mm_kernel(KqArgs a) {
+    kq_body<F, KS, NT, MT>(a, static_cast<int>(blockIdx.x));
+}
+
+// Two formats in one launch: workgroups [0, nb0) take a0's items, the rest
+// a1's (nb0 is a multiple of 8, so both parts keep their XCD order). Q and K
+// of one K-quant beside V of another fill the chip together instead of V's
+// few workgroups running alone.
+template <int F0, int F1, int KS, int MT>
+__global__ __launch_bounds__(kThreads) void kq_mm_mix_kernel(KqArgs a0, KqArgs a1, int nb0) {
+    const int L = static_cast<int>(blockIdx.x);
+    if (L < nb0) kq_body<F0, KS, 1, MT>(a0, L);
+    else kq_body<F1, KS, 1, MT>(a1, L - nb0);
+}
+
+template <int F, int KS, int NT, int MT>
 void launch_kq(const KqArgs &args, hipStream_t s) {
     static bool lds_set = false;                 // the attribute is per kernel, per process
     const void *fn = reinterpret_cast<const void *>(kq_mm_kernel<F, KS, NT, MT>);
@@ -619,6 +637,49 @@ int enqueue_kquant_mfma_parts(const KqOut *outs, int nseg, const float *A, int K
     args.ld = ld;
     args.col0 = col0;
     kq_launch(args, type, current_stream());
+    return ALJABR_ROCM_OK;
+}
+
+int enqueue_kquant_mfma_parts2(const KqOut *outs0, int nseg0, int type0, const KqOut *outs1, int nseg1, int type1,
+                               const float *A, int K, int M, float *part, size_t part_floats) {
+    if (type0 != ALJABR_ROCM_TYPE_Q4_K || type1 != ALJABR_ROCM_TYPE_Q6_K) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    KqArgs a0, a1;
+    int rc = kq_multi_args(outs0, nseg0, A, K, type0, M, a0);
+    if (rc != ALJABR_ROCM_OK) return rc;
+    rc = kq_multi_args(outs1, nseg1, A, K, type1, M, a1);
+    if (rc != ALJABR_ROCM_OK) return rc;
+    const int slices = K / 512;
+    const long long ld = static_cast<long long>(a0.N) + a1.N;
+    if (slices < 2 || !part || a0.N % 32 != 0 || ld > 0x7fff0000LL ||
+        static_cast<size_t>(slices) * M * static_cast<size_t>(ld) > part_floats)
+        return ALJABR_ROCM_ERR_UNSUPPORTED;
+    a0.part = a1.part = part;
+    a0.ld = a1.ld = static_cast<int>(ld);
+    a0.col0 = 0;
+    a1.col0 = a0.N;
+    KqArgs *as[2] = {&a0, &a1};
+    int grid[2];
+    for (int i = 0; i < 2; ++i) {
+        KqArgs &a = *as[i];
+        a.groups = (a.N + kRowsPerWg - 1) / kRowsPerWg;
+        a.slices = slices;
+        const int total = a.groups * a.slices;
+        grid[i] = (a.groups & 7) == 0 ? total : 8 * ((total + 7) / 8);
+    }
+    // One tile per wave (the single-format launch's choice while its items
+    // fit the CUs), both parts resident at once.
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    if (grid[0] + grid[1] > cus) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    constexpr int F0 = kFQ4K, F1 = kFQ6K;
+    const void *fn = reinterpret_cast<const void *>(kq_mm_mix_kernel<F0, F1, 512, 32>);
+    const size_t lds = std::max(kq_lds_bytes<F0, 512>(), kq_lds_bytes<F1, 512>());
+    static bool lds_set = false;
+    if (!lds_set) {
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        lds_set = true;
+    }
+    hipLaunchKernelGGL((kq_mm_mix_kernel<F0, F1, 512, 32>), dim3(grid[0] + grid[1]), dim3(kThreads), lds,
+                       current_stream(), a0, a1, grid[0]);
     return ALJABR_ROCM_OK;
 }
 
