@@ -533,8 +533,9 @@ void launch_kq(const KqArgs &args, hipStream_t s) {
 }
 
 template <int F, int MT>
-void launch_kq_nt(const KqArgs &args, bool two, hipStream_t s) {
-    if (two) launch_kq<F, 512, 2, MT>(args, s);
+void launch_kq_nt(const KqArgs &args, int ks, bool two, hipStream_t s) {
+    if (ks == 256) launch_kq<F, 256, 1, MT>(args, s);
+    else if (two) launch_kq<F, 512, 2, MT>(args, s);
     else launch_kq<F, 512, 1, MT>(args, s);
 }
 
@@ -582,16 +583,25 @@ int kq_multi_args(const KqOut *outs, int nseg, const float *A, int K, int type, 
     return ALJABR_ROCM_OK;
 }
 
-void kq_launch(const KqArgs &args, int type, hipStream_t s) {
+// K slice of a launch: 512 elements, or 256 when 512-element slices would
+// leave at least half the CUs without a workgroup (twice the workgroups,
+// each with half the slice).
+int kq_slice(int N, int K) {
+    const int wgs_n = (N + kRowsPerWg - 1) / kRowsPerWg;
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    return 2LL * wgs_n * (K / 512) <= cus ? 256 : 512;
+}
+
+void kq_launch(const KqArgs &args, int type, int ks, hipStream_t s) {
     const int wgs_n = (args.N + kRowsPerWg - 1) / kRowsPerWg;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     const long long units = static_cast<long long>(wgs_n) * (args.K / 512);
     const bool two = units > cus;
     switch (type) {
-    case ALJABR_ROCM_TYPE_Q4_K: launch_kq_nt<kFQ4K, 32>(args, two, s); break;
-    case ALJABR_ROCM_TYPE_Q6_K: launch_kq_nt<kFQ6K, 32>(args, two, s); break;
-    case ALJABR_ROCM_TYPE_Q4_0: launch_kq_nt<kFQ40, 8>(args, two, s); break;
-    default: launch_kq_nt<kFQ80, 8>(args, two, s); break;
+    case ALJABR_ROCM_TYPE_Q4_K: launch_kq_nt<kFQ4K, 32>(args, ks, two, s); break;
+    case ALJABR_ROCM_TYPE_Q6_K: launch_kq_nt<kFQ6K, 32>(args, ks, two, s); break;
+    case ALJABR_ROCM_TYPE_Q4_0: launch_kq_nt<kFQ40, 8>(args, ks, two, s); break;
+    default: launch_kq_nt<kFQ80, 8>(args, ks, two, s); break;
     }
 }
 
@@ -606,7 +616,8 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
     if (rc != ALJABR_ROCM_OK) return rc;
     if (tail && (accumulate || K < 1024)) return ALJABR_ROCM_ERR_UNSUPPORTED;
     hipStream_t s = current_stream();
-    const int slices = K / 512;
+    const int ks = kq_slice(args.N, K);
+    const int slices = K / ks;
     args.add = slices == 1 && accumulate;
     if (slices > 1) {
         const size_t need = static_cast<size_t>(slices) * M * args.N;
@@ -615,7 +626,7 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
                         : static_cast<float *>(stream_scratch(need * sizeof(float), kScratchPartials));
         if (!args.part) return ALJABR_ROCM_ERR_BUFFER;
     }
-    kq_launch(args, type, s);
+    kq_launch(args, type, ks, s);
     if (tail) return enqueue_slice_tail(*tail, args.part, slices, M, args.N);
     if (slices > 1) {
         float *ys[3] = {args.y[0], args.y[1], args.y[2]};
@@ -636,7 +647,7 @@ int enqueue_kquant_mfma_parts(const KqOut *outs, int nseg, const float *A, int K
     args.part = part;
     args.ld = ld;
     args.col0 = col0;
-    kq_launch(args, type, current_stream());
+    kq_launch(args, type, 512, current_stream());
     return ALJABR_ROCM_OK;
 }
 
