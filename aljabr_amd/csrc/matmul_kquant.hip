@@ -533,10 +533,17 @@ void launch_kq(const KqArgs &args, hipStream_t s) {
 }
 
 template <int F, int MT>
-void launch_kq_nt(const KqArgs &args, int ks, bool two, hipStream_t s) {
-    if (ks == 256) launch_kq<F, 256, 1, MT>(args, s);
-    else if (two) launch_kq<F, 512, 2, MT>(args, s);
-    else launch_kq<F, 512, 1, MT>(args, s);
+void launch_kq_nt(const KqArgs &args, int ks, int nt, hipStream_t s) {
+    constexpr bool kFour = F == kFQ4K || F == kFQ40;
+    if (ks == 256) {
+        launch_kq<F, 256, 1, MT>(args, s);
+    } else if (nt == 4 && kFour) {
+        if constexpr (kFour) launch_kq<F, 512, 4, MT>(args, s);
+    } else if (nt >= 2) {
+        launch_kq<F, 512, 2, MT>(args, s);
+    } else {
+        launch_kq<F, 512, 1, MT>(args, s);
+    }
 }
 
 }  // namespace
@@ -595,13 +602,18 @@ int kq_slice(int N, int K) {
 void kq_launch(const KqArgs &args, int type, int ks, hipStream_t s) {
     const int wgs_n = (args.N + kRowsPerWg - 1) / kRowsPerWg;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    // Row tiles per wave: 1, 2 when one leaves more workgroups than CUs, 4
+    // when two still do (one round of workgroups instead of a ragged second;
+    // Q4_K and Q4_0 only: Q6_K's and Q8_0's four-tile kernels reach the
+    // register limit).
     const long long units = static_cast<long long>(wgs_n) * (args.K / 512);
-    const bool two = units > cus;
+    const bool four_ok = type == ALJABR_ROCM_TYPE_Q4_K || type == ALJABR_ROCM_TYPE_Q4_0;
+    const int nt = units <= cus ? 1 : (units + 1) / 2 <= cus || !four_ok ? 2 : 4;
     switch (type) {
-    case ALJABR_ROCM_TYPE_Q4_K: launch_kq_nt<kFQ4K, 32>(args, ks, two, s); break;
-    case ALJABR_ROCM_TYPE_Q6_K: launch_kq_nt<kFQ6K, 32>(args, ks, two, s); break;
-    case ALJABR_ROCM_TYPE_Q4_0: launch_kq_nt<kFQ40, 8>(args, ks, two, s); break;
-    default: launch_kq_nt<kFQ80, 8>(args, ks, two, s); break;
+    case ALJABR_ROCM_TYPE_Q4_K: launch_kq_nt<kFQ4K, 32>(args, ks, nt, s); break;
+    case ALJABR_ROCM_TYPE_Q6_K: launch_kq_nt<kFQ6K, 32>(args, ks, nt, s); break;
+    case ALJABR_ROCM_TYPE_Q4_0: launch_kq_nt<kFQ40, 8>(args, ks, nt, s); break;
+    default: launch_kq_nt<kFQ80, 8>(args, ks, nt, s); break;
     }
 }
 
