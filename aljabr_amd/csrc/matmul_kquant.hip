@@ -603,7 +603,7 @@ void kq_launch(const KqArgs &args, int type, int ks, hipStream_t s) {
     const int wgs_n = (args.N + kRowsPerWg - 1) / kRowsPerWg;
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     // Row tiles per wave: 1, 2 when one leaves more workgroups than CUs, 4
-    // when two still do (one round of workgroups instead of a ragged second;
+    // when two still do (every workgroup resident at once instead of a ragged second batch;
     // Q4_K and Q4_0 only: Q6_K's and Q8_0's four-tile kernels reach the
     // register limit).
     const long long units = static_cast<long long>(wgs_n) * (args.K / 512);
