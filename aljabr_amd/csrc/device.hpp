@@ -127,6 +127,41 @@ __device__ __forceinline__ void rope_cos_sin(int pos, int i, int head_dim, float
     s = static_cast<float>(sin(static_cast<double>(theta)));
 }
 
+// Sum of p[s * stride] over the K slices s = 0 .. slices-1 (slices >= 1),
+// added in slice order, with U = 4, 8 or 16 loads in flight per trip (the
+// smallest that covers the slices, 16 beyond): a trip's indices past the
+// last slice re-read the last one (in bounds) and are not added. The split-K
+// partial sums of a small-M GEMM are read this way by the kernel after it,
+// one memory round trip per 16 slices.
+__device__ __forceinline__ void slice_add(float &a, float v) { a += v; }
+__device__ __forceinline__ void slice_add(float4 &a, const float4 &v) {
+    a.x += v.x;
+    a.y += v.y;
+    a.z += v.z;
+    a.w += v.w;
+}
+
+template <int U, class V>
+__device__ __forceinline__ V slice_sum_u(const V *p, size_t stride, int slices) {
+    V acc{};
+    for (int s0 = 0; s0 < slices; s0 += U) {
+        V v[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) v[j] = p[static_cast<size_t>(min(s0 + j, slices - 1)) * stride];
+#pragma unroll
+        for (int j = 0; j < U; ++j)
+            if (s0 + j < slices) slice_add(acc, v[j]);
+    }
+    return acc;
+}
+
+template <class V>
+__device__ __forceinline__ V slice_sum(const V *p, size_t stride, int slices) {
+    if (slices <= 4) return slice_sum_u<4>(p, stride, slices);
+    if (slices <= 8) return slice_sum_u<8>(p, stride, slices);
+    return slice_sum_u<16>(p, stride, slices);
+}
+
 // Rotation of (x0, x1) by the angle with cosine c and sine s, each product
 // rounded separately.
 __device__ __forceinline__ void rope_apply(float &x0, float &x1, float c, float s) {

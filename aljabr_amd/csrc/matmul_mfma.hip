@@ -530,18 +530,7 @@ __global__ __launch_bounds__(256) void nf4_mm_reduce_kernel(ReduceArgs r) {
     const long long idx = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     if (idx >= static_cast<long long>(r.M) * r.N) return;
     const int m = static_cast<int>(idx / r.N), n = static_cast<int>(idx % r.N);
-    const float *p = r.part + idx;
-    const size_t stride = static_cast<size_t>(r.M) * r.N;
-    float v = 0.0f;
-    int s = 0;
-    for (; s + 4 <= r.slices; s += 4) {
-        const float p0 = p[s * stride], p1 = p[(s + 1) * stride], p2 = p[(s + 2) * stride], p3 = p[(s + 3) * stride];
-        v += p0;
-        v += p1;
-        v += p2;
-        v += p3;
-    }
-    for (; s < r.slices; ++s) v += p[s * stride];
+    const float v = slice_sum(r.part + idx, static_cast<size_t>(r.M) * r.N, r.slices);
     const int seg = segment_of(r.end, r.nseg, n);
     const int start = seg == 0 ? 0 : seg == 1 ? r.end[0] : r.end[1];
     const int sn = (seg == 0 ? r.end[0] : seg == 1 ? r.end[1] : r.end[2]) - start;

@@ -22,17 +22,7 @@ constexpr int kThreads = 256;
 
 // Sum of one element's slices in slice order, eight loads in flight.
 __device__ __forceinline__ float slice_total(const float *__restrict__ part, size_t stride, int slices, size_t idx) {
-    float v = 0.0f;
-    int s = 0;
-    for (; s + 8 <= slices; s += 8) {
-        float t[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) t[j] = part[static_cast<size_t>(s + j) * stride + idx];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v += t[j];
-    }
-    for (; s < slices; ++s) v += part[static_cast<size_t>(s) * stride + idx];
-    return v;
+    return slice_sum(part + idx, stride, slices);
 }
 
 __device__ __forceinline__ uint16_t f16_bits(float v) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v)); }
@@ -139,29 +129,10 @@ __global__ __launch_bounds__(kNormThreads) void tail_residual_norm_kernel(float 
     float4 *yr = reinterpret_cast<float4 *>(y + row);
     float ss = 0.0f;
     for (int c = threadIdx.x; c < N / 4; c += kNormThreads) {
-        const float *p = part + row + 4 * static_cast<size_t>(c);
-        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        int sl = 0;
-        for (; sl + 8 <= slices; sl += 8) {
-            float4 v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4 *>(p + static_cast<size_t>(sl + j) * stride);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                acc.x += v[j].x;
-                acc.y += v[j].y;
-                acc.z += v[j].z;
-                acc.w += v[j].w;
-            }
-        }
-        for (; sl < slices; ++sl) {
-            const float4 v = *reinterpret_cast<const float4 *>(p + static_cast<size_t>(sl) * stride);
-            acc.x += v.x;
-            acc.y += v.y;
-            acc.z += v.z;
-            acc.w += v.w;
-        }
+        // The residual row is requested with the partials (one round trip).
         float4 x = yr[c];
+        const float4 acc =
+            slice_sum(reinterpret_cast<const float4 *>(part + row + 4 * static_cast<size_t>(c)), stride / 4, slices);
         x.x += acc.x;
         x.y += acc.y;
         x.z += acc.z;
@@ -202,29 +173,10 @@ __global__ __launch_bounds__(kScaleThreads) void tail_residual_scale_kernel(floa
     const float4 *w4 = reinterpret_cast<const float4 *>(w);
     float ss = 0.0f;
     for (int c = pb * cols4 + static_cast<int>(threadIdx.x); c < (pb + 1) * cols4; c += kScaleThreads) {
-        const float *p = part + row + 4 * static_cast<size_t>(c);
-        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        int sl = 0;
-        for (; sl + 8 <= slices; sl += 8) {
-            float4 v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4 *>(p + static_cast<size_t>(sl + j) * stride);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                acc.x += v[j].x;
-                acc.y += v[j].y;
-                acc.z += v[j].z;
-                acc.w += v[j].w;
-            }
-        }
-        for (; sl < slices; ++sl) {
-            const float4 v = *reinterpret_cast<const float4 *>(p + static_cast<size_t>(sl) * stride);
-            acc.x += v.x;
-            acc.y += v.y;
-            acc.z += v.z;
-            acc.w += v.w;
-        }
+        // The residual row is requested with the partials (one round trip).
         float4 x = yr[c];
+        const float4 acc =
+            slice_sum(reinterpret_cast<const float4 *>(part + row + 4 * static_cast<size_t>(c)), stride / 4, slices);
         x.x += acc.x;
         x.y += acc.y;
         x.z += acc.z;
