@@ -174,6 +174,10 @@ struct SliceTail {
     // ssq[M][kSsqParts] over rows of norm_n elements, or null for none.
     float *ssq;
     int norm_n;
+    // Also the output as the NF4 matrix-core GEMM's fp16 A image (the layout
+    // nf4_xpack_kernel writes; rows >= M left as they are), when the next
+    // GEMM consumes it: the SwiGLU and residual tails; null for none.
+    uint16_t *xpack;
 };
 int enqueue_slice_tail(const SliceTail &t, const float *part, int slices, int M, int N);
 // NF4 small-M GEMM on MFMA (M >= 2 in passes of 32 tokens, K % 256 == 0,
@@ -188,8 +192,13 @@ int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *a
 // the last with a multiple of 32 rows); outs[i].y is [M][outs[i].n].
 // With `tail` (M <= 64) the outputs are not written: the slice sums go to
 // the tail kernel instead (outs[].y unused).
+// `xpacked`: A already as the GEMM's fp16 A image (a tail's xpack, M <= 64),
+// or null.
 int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M, bool add,
-                           float *part = nullptr, size_t part_floats = 0, const SliceTail *tail = nullptr);
+                           float *part = nullptr, size_t part_floats = 0, const SliceTail *tail = nullptr,
+                           const uint16_t *xpacked = nullptr);
+// Bytes of the fp16 A image for M <= 64 tokens over K (K % 64 == 0).
+size_t nf4_xpack_bytes(int M, int K);
 size_t nf4_mfma_scratch_floats(int M, int N, int K);
 // The plan enqueue_nf4_mfma_multi uses for N stacked rows over K on `cus`
 // CUs and passes of M tokens (row tiles per wave, sub-slices per K slice),

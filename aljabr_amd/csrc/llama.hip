@@ -74,6 +74,10 @@ struct aljabr_rocm_llama {
     float *mm_part = nullptr;        // K-slice partials of the batched matrix-core GEMMs
     size_t mm_part_floats = 0;
     float *tail_ssq = nullptr;       // [max_batch][kSsqParts] row-block sums of squares of the residual tails
+    // xb and hb as the NF4 GEMM's fp16 A image, written by the tails that
+    // produce them (batches of 2..64): the next GEMM then skips its packing
+    // launch. Null when the session has none.
+    uint16_t *xb_pack = nullptr, *hb_pack = nullptr;
     bool rows_fused = false;   // batch-1 layers as fused NF4 launches (shapes and alignment allow it)
     // Captured decode steps, by batch size (and the logits buffer they write).
     struct Graph {
@@ -252,6 +256,11 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
         for (const auto &sh : shapes) mm_floats = std::max(mm_floats, nf4_mfma_scratch_floats(bp, sh[0], sh[1]));
         mm_floats = std::max(mm_floats, static_cast<size_t>(c.dim / 512) * bp * static_cast<size_t>(c.vocab));
     }
+    // The A images of xb and hb for the NF4 GEMMs (batches of 2..64).
+    const bool packs = m->all_nf4 && c.max_batch >= 2 && c.max_batch <= 64 && c.dim % 64 == 0 && c.ffn % 64 == 0;
+    const size_t pack_bytes = packs ? ((nf4_xpack_bytes(c.max_batch, c.dim) + 255) & ~size_t(255)) +
+                                          ((nf4_xpack_bytes(c.max_batch, c.ffn) + 255) & ~size_t(255))
+                                    : 0;
     const size_t bytes = 2 * ((cache_elems * 2 + 255) & ~size_t(255)) +
                          ((mm_floats * 4 + 255) & ~size_t(255)) +
                          ((B * c.dim * 4 + 255) & ~size_t(255)) * 2 + ((B * qd * 4 + 255) & ~size_t(255)) * 2 +
@@ -260,7 +269,7 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
                          ((attention_scratch_bytes(c.max_batch, c.n_heads, 1, c.head_dim, c.max_seq) + 255) &
                           ~size_t(255)) +
                          ((static_cast<size_t>(c.max_seq) * (c.head_dim / 2) * sizeof(float2) + 255) & ~size_t(255)) +
-                         ((static_cast<size_t>(B) * kSsqParts * 4 + 255) & ~size_t(255)) + 256;
+                         ((static_cast<size_t>(B) * kSsqParts * 4 + 255) & ~size_t(255)) + 256 + pack_bytes;
     hipError_t e = hipMalloc(&m->arena, bytes);
     if (e != hipSuccess) {
         delete m;
@@ -290,6 +299,10 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
         m->mm_part = carve<float>(cur, mm_floats);
     }
     m->tail_ssq = carve<float>(cur, static_cast<size_t>(B) * kSsqParts);
+    if (packs) {
+        m->xb_pack = carve<uint16_t>(cur, nf4_xpack_bytes(c.max_batch, c.dim) / 2);
+        m->hb_pack = carve<uint16_t>(cur, nf4_xpack_bytes(c.max_batch, c.ffn) / 2);
+    }
     // The RoPE angles of every cache position, computed once: the decode
     // step then reads cos/sin instead of evaluating double pow/cos/sin.
     m->rope_cs = carve<float2>(cur, static_cast<size_t>(c.max_seq) * (c.head_dim / 2));
@@ -904,7 +917,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
     // shapes do not allow it (the caller then runs the separate launches).
     auto kq_ok = [&](const T &w) { return kquant_mfma_type(w.type) && B <= kquant_mfma_max_m(w.type); };
     auto gemm_tail = [&](const RowsOut *o, const T *const *ts, int nseg, const float *x, int K,
-                         const SliceTail *t) -> int {
+                         const SliceTail *t, const uint16_t *xpacked = nullptr) -> int {
         const int ty = ts[0]->type;
         bool mixed = false;
         for (int i = 1; i < nseg; ++i) mixed |= ts[i]->type != ty;
@@ -953,7 +966,8 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             return enqueue_slice_tail(*t, m->mm_part, slices, B, n_all);
         }
         if (ty == ALJABR_ROCM_TYPE_NF4)
-            return m->all_nf4 ? enqueue_nf4_mfma_multi(o, nseg, x, K, shift, B, false, m->mm_part, m->mm_part_floats, t)
+            return m->all_nf4 ? enqueue_nf4_mfma_multi(o, nseg, x, K, shift, B, false, m->mm_part, m->mm_part_floats, t,
+                                                       xpacked)
                               : ALJABR_ROCM_ERR_UNSUPPORTED;
         if (!kquant_mfma_type(ty) || B > kquant_mfma_max_m(ty)) return ALJABR_ROCM_ERR_UNSUPPORTED;
         KqOut k[3];
@@ -976,6 +990,10 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
     // next GEMM's tail applies the scale to its products. A fallback that
     // consumes xb directly normalizes it first.
     bool xb_scaled = false;
+    // Whether xb_pack / hb_pack hold xb / hb (the tail that wrote xb or hb
+    // also wrote its A image).
+    const bool packs = m->xb_pack && B <= 64;
+    bool xb_packed = false, hb_packed = false;
     for (int l = 0; l < c.layers; ++l) {
         auto W = [&](const std::vector<T> &t) { return t[l].w; };
         auto S = [&](const std::vector<T> &t) { return t[l].s; };
@@ -1057,7 +1075,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                 t.norm_n = dim;
                 t.eps = c.eps;
                 const T *const qts[3] = {&m->wq[l], &m->wk[l], &m->wv[l]};
-                rc = gemm_tail(qkv, qts, 3, m->xb, dim, &t);
+                rc = gemm_tail(qkv, qts, 3, m->xb, dim, &t, xb_packed ? m->xb_pack : nullptr);
                 if (rc == ALJABR_ROCM_OK)
                     ALJ_MARK("qkv_gemm_rope_append", mm_bytes(m->wq[l], qd, dim, false) +
                                                          mm_bytes(m->wk[l], kvd, dim, false) +
@@ -1129,9 +1147,11 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                 t.norm_w = ffn_norm;
                 t.eps = c.eps;
                 t.ssq = m->tail_ssq;
+                t.xpack = packs ? m->xb_pack : nullptr;
                 const RowsOut o = {m->x, W(m->wo), S(m->wo), dim};
                 const T *const ots[1] = {&m->wo[l]};
                 rc = gemm_tail(&o, ots, 1, m->att, qd, &t);
+                xb_packed = rc == ALJABR_ROCM_OK && packs;
                 if (rc == ALJABR_ROCM_OK) {
                     xb_scaled = defer;
                     ALJ_MARK("wo_gemm_add_rmsnorm", mm_bytes(m->wo[l], dim, qd, true) + (B * dim + dim) * f4);
@@ -1189,8 +1209,10 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                 t.ssq = xb_scaled ? m->tail_ssq : nullptr;
                 t.norm_n = dim;
                 t.eps = c.eps;
+                t.xpack = packs ? m->hb_pack : nullptr;
                 const T *const gts[2] = {&m->w_gate[l], &m->w_up[l]};
-                rc = gemm_tail(gu, gts, 2, m->xb, dim, &t);
+                rc = gemm_tail(gu, gts, 2, m->xb, dim, &t, xb_packed ? m->xb_pack : nullptr);
+                hb_packed = rc == ALJABR_ROCM_OK && packs;
                 if (rc == ALJABR_ROCM_OK)
                     ALJ_MARK("gate_up_gemm_swiglu", mm_bytes(m->w_gate[l], ffn, dim, false) +
                                                         mm_bytes(m->w_up[l], ffn, dim, false) - B * dim * f4 -
@@ -1233,9 +1255,11 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                 t.norm_w = next_norm;
                 t.eps = c.eps;
                 t.ssq = m->tail_ssq;
+                t.xpack = packs && defer ? m->xb_pack : nullptr;
                 const RowsOut d = {m->x, W(m->w_down), S(m->w_down), dim};
                 const T *const dts[1] = {&m->w_down[l]};
-                rc = gemm_tail(&d, dts, 1, m->hb, ffn, &t);
+                rc = gemm_tail(&d, dts, 1, m->hb, ffn, &t, hb_packed ? m->hb_pack : nullptr);
+                xb_packed = rc == ALJABR_ROCM_OK && packs && defer;
                 if (rc == ALJABR_ROCM_OK) {
                     xb_scaled = defer;
                     ALJ_MARK("down_gemm_add_rmsnorm", mm_bytes(m->w_down[l], dim, ffn, true) + (B * dim + dim) * f4);

@@ -1,9 +1,14 @@
-// matmul_mfma.hip - NF4 small-M GEMM on the matrix cores, fp32-accurate and
-// deterministic: Y[M,N] = X[M,K] . W[N,K]^T (or Y += ...) for 2 <= M <= 32
-// tokens per pass (a prompt chunk or a decode batch), W in NF4
+// matmul_mfma.hip - NF4 small-M GEMM on the matrix cores, deterministic:
+// Y[M,N] = X[M,K] . W[N,K]^T (or Y += ...) for passes of up to 64 tokens (a
+// prompt chunk or a decode batch), W in NF4
 // (STC/DequantizationKernel.java:84-102). Replaces the reference's per-token
 // loop over the matvec (MTLJ/MetalComputeBackend.java:435-470): W is read
 // from HBM once for all tokens of a pass.
+//
+// Two kernels: nf4_gemm_kernel (below the first one; K % 1024 == 0) keeps
+// the activations in registers and is the one the decode step and the
+// batched ABI run; nf4_mm_kernel, described here, stages them in LDS and
+// takes the other shapes (K % 256 == 0).
 //
 // Precision. MFMA v_mfma_f32_32x32x16_f16 with A = X (32 token rows) and
 // B = W^T (32 weight rows per wave as the output columns), fp32 accumulation.
@@ -29,6 +34,7 @@
 // Determinism. With several K slices, each workgroup stores its partial
 // tile and a second kernel sums the slices in slice order into Y (or adds
 // them to it): no float atomics, the same result on every run.
+#include <atomic>
 #include <type_traits>
 
 #include "device.hpp"
@@ -538,10 +544,503 @@ __global__ __launch_bounds__(256) void nf4_mm_reduce_kernel(ReduceArgs r) {
     *yp = r.add ? *yp + v : v;
 }
 
+// ---------------------------------------------------------------------------
+// NF4 GEMM with the activations held in registers (nf4_gemm_kernel), for
+// K % 1024 == 0 and passes of up to 64 tokens.
+//
+// Precision: the activations are rounded to fp16 (to nearest; an A image
+// built once per call by nf4_xpack_kernel, or written by the decode step's
+// tail that produced them) and each NF4 level is exact as H + R (H = fp16 of
+// the level, R = fp16 of the rest): one table entry per code byte holds both
+// pairs, a B fragment is {H0 H1 R0 R1 H2 H3 R2 R3} of four weights and the A
+// fragment repeats each activation pair against it, so every product is
+// x16 * (H + R) accumulated in fp32. A token row is within the activations'
+// rounding of the fp32 result (~2e-4 relative).
+//
+// Work split: slice s of K (blockIdx.x) spans 8 waves x KS = 64*NB
+// elements; wave w owns [(8s + w)*KS, +KS) and keeps that range of all M
+// token rows in registers as A fragments, loaded once. The workgroup walks
+// 16-row tiles t = blockIdx.y + i*gridDim.y. Each wave streams its K range of
+// the tiles' 16 weight rows (codes and absmax) into a private ring of D tile
+// slots in LDS with LDS-DMA loads (no staging registers, so nothing in flight
+// crosses the loop in registers), waits for the oldest slot with an explicit
+// vmcnt, reads it into registers, refills it D tiles ahead, then decodes
+// through the LDS table (the next dword's reads issued before the current
+// dword's MFMAs), runs each 64-element block into fresh accumulators (two
+// independent MFMA chains per token tile) and adds them scaled by the
+// block's absmax. The 8 waves' 16 x M partial tiles are summed in wave order
+// through LDS and written (or stored as the slice's partials for the
+// slice-sum or tail kernel): deterministic, no atomics.
+//
+// v_mfma_f32_16x16x32_f16: lane l = 16g + i supplies A[i][8g + e] and
+// B[8g + e][i] (e < 8); accumulator r of lane l is C[4g + r][i]. A is the
+// activations (i = token), B the weights (i = weight row). K order: in block
+// b (elements kw + 64b ..), lane group g covers elements 16g .. 16g+15 (the
+// 8 code bytes 8g .. 8g+7 of the row's 32-byte block segment) in four MFMAs
+// of four elements each, so each MFMA stays inside one absmax block.
+//
+// Slot image (per tile, per wave): NB/2 code windows of 1 KiB (window j =
+// blocks 2j, 2j+1 of the 16 rows: DMA lane l loads row l%16, bytes
+// 16*(l/16) .. +16 of the row's 64-byte window, landing at 16*l), then the
+// 16 x NB absmax floats row-major. A lane's 8 code bytes of block b sit at
+// 1024*(b/2) + 16*(16*(2*(b%2) + g/2) + i) + 8*(g%2): the 64 lanes of one
+// block read 512 contiguous bytes.
+
+typedef float f32x4m __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2m __attribute__((ext_vector_type(2)));
+typedef u32x2m __attribute__((address_space(3))) lds_u32x2m;
+typedef f32x4m __attribute__((address_space(3))) lds_f32x4m;
+
+constexpr int kGemmWaves = 8;
+constexpr int kGemmThreads = kGemmWaves * 64;
+constexpr uint32_t kGemmTable = Lds<1>::kTableBytes;      // the pair table, 32 replicas
+constexpr uint32_t kGemmLdsMax = 160 * 1024;
+
+template <int MT, int NB>
+struct GemmLds {
+    // Partial tiles [wave][mt][r][lane] floats, two buffers.
+    static constexpr uint32_t kRedBuf = kGemmWaves * MT * 4 * 64 * 4;
+    static constexpr uint32_t kRedOff = kGemmTable;
+    static constexpr uint32_t kRingOff = kRedOff + 2 * kRedBuf;
+    static constexpr uint32_t kCodeBytes = 512 * NB;                    // 16 rows x 32 bytes per block
+    static constexpr uint32_t kSlot = kCodeBytes + 64 * NB;             // + 16 x NB absmax floats
+    static constexpr int kD = static_cast<int>((kGemmLdsMax - kRingOff) / (kGemmWaves * kSlot));
+    static constexpr int D = kD > 4 ? 4 : kD;                           // tiles in flight per wave
+    static constexpr uint32_t kBytes = kRingOff + kGemmWaves * D * kSlot;
+    static constexpr int kDma = NB / 2 + (NB + 3) / 4;                  // DMA instructions per tile
+    static_assert(NB % 2 == 0 && D >= 2 && kBytes <= kGemmLdsMax, "LDS budget of a CU");
+};
+
+struct GemmArgs {
+    const float *x;          // [M][K]
+    const u32x4v *xp;        // the activations' fp16 fragment image (nf4_xpack_kernel)
+    const uint8_t *w[3];
+    const float *absmax[3];
+    float *y[3];
+    int end[3];              // stacked-row ends; every segment but the last a multiple of 16 rows
+    int nseg;
+    int M, N, K;
+    int add;                 // Y += (one slice, no partial buffer)
+    float *part;             // [slices][M][N] partial sums, or null: Y directly
+    int tiles;               // ceil(N / 16)
+};
+
+struct GemmTile {
+    const uint8_t *w;
+    const float *absmax;
+    float *y;
+    int local0, n;
+};
+
+// Branch-free select of a uniform segment index s in {0, 1, 2}: masks and
+// adds on scalar values, so neither a branch nor an indexed read of the
+// argument block is formed.
+template <typename T>
+__device__ __forceinline__ T seg_pick(T v0, T v1, T v2, int s) {
+    const uint64_t a0 = (uint64_t)v0, a1 = (uint64_t)v1, a2 = (uint64_t)v2;
+    const uint64_t m1 = 0 - static_cast<uint64_t>(s >= 1), m2 = 0 - static_cast<uint64_t>(s >= 2);
+    return (T)(a0 + ((a1 - a0) & m1) + ((a2 - a1) & m2));
+}
+
+__device__ __forceinline__ GemmTile gemm_tile(const GemmArgs &a, int r0) {
+    const int e0 = a.end[0], e1 = a.end[1], e2 = a.end[2];
+    int s = (r0 >= e0) + (r0 >= e1);
+    s = s > a.nseg - 1 ? a.nseg - 1 : s;
+    GemmTile t;
+    t.w = seg_pick(a.w[0], a.w[1], a.w[2], s);
+    t.absmax = seg_pick(a.absmax[0], a.absmax[1], a.absmax[2], s);
+    t.y = seg_pick(a.y[0], a.y[1], a.y[2], s);
+    const int start = seg_pick(0, e0, e1, s);
+    t.local0 = r0 - start;
+    t.n = seg_pick(e0, e1, e2, s) - start;
+    return t;
+}
+
+// s_waitcnt with only the vector-memory count limited (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// LDS-DMA loads (global_load_lds: 16 or 4 bytes per lane, landing at
+// `lds_base` + size * lane). Written as inline assembly: the compiler models
+// the builtin like a FLAT access that also counts on the LDS counter and
+// then waits for every outstanding LDS read before using any of them, which
+// would serialize the table lookups; the hardware counts these loads on the
+// vector-memory counter only, and every wait for their data here is an
+// explicit vmcnt. M0 carries the LDS address (latched at issue, one wait
+// state after it is written) and is restored afterwards.
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds_base) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "s"(lds_base), "v"(g)
+                 : "memory");
+}
+__device__ __forceinline__ void dma4(const void *g, uint32_t lds_base) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %2, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "s"(lds_base), "v"(g)
+                 : "memory");
+}
+
+// LDS-DMA loads of one tile (this wave's K range of rows 16t .. 16t+15) into
+// the slot at LDS byte `slot` (uniform): NB/2 16-byte code loads per lane,
+// then the absmax floats (4 bytes per lane; lanes past 16*NB floats idle).
+template <int NB>
+__device__ __forceinline__ void gemm_dma(const GemmArgs &a, int tile, int kw, uint32_t slot, int lane) {
+    const GemmTile tr = gemm_tile(a, tile * 16);
+    const int crow = min(tr.local0 + (lane & 15), tr.n - 1);
+    const uint8_t *qp = tr.w + static_cast<size_t>(crow) * (a.K >> 1) + (kw >> 1) + 16 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < NB / 2; ++j) dma16(qp + 64 * j, slot + 1024 * j);
+#pragma unroll
+    for (int j = 0; j < (NB + 3) / 4; ++j) {
+        const int f = lane + 64 * j;             // float f of the tile image: row f / NB, block f % NB
+        const int srow = min(tr.local0 + f / NB, tr.n - 1);
+        const float *sp = tr.absmax + static_cast<size_t>(srow) * (a.K >> 6) + (kw >> 6) + f % NB;
+        if (16 * NB % 64 == 0 || f < 16 * NB) dma4(sp, slot + 512 * NB + 256 * j);
+    }
+}
+
+// The activation-stationary GEMM's decode table: 256 entries (a code byte:
+// the even element in the high nibble) of 8 bytes, the byte's fp16 level
+// pair {H(e >> 4), H(e & 15)} and residual pair {R(e >> 4), R(e & 15)}
+// (H = the level rounded to nearest fp16, R = fp16(level - H); H + R is the
+// fp32 level to within 2^-22 of it), in 32 replicas: entry e, replica r at
+// e*256 + 8r. Thread tid (of 512) fills replica tid % 32 of entries
+// e0 + 16j (e0 = tid / 32 < 16, j < 16): the high nibble j is a constant of
+// the unrolled loop, the low nibble e0.
+__device__ __forceinline__ void build_table_hr(int tid) {
+    constexpr float kNF4[16] = {
+        -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+        -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+        0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+        0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+    const uint32_t r = static_cast<uint32_t>(tid & 31) * 8;
+    const int e0 = tid >> 5;
+    const float lo = nf4_level_sel(e0);
+    const float lo_r = level_rest(lo);
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        *lds<lds_u32x2m>(static_cast<uint32_t>(16 * j + e0) * 256 + r) =
+            u32x2m{pack_half2(kNF4[j], lo), pack_half2(level_rest(kNF4[j]), lo_r)};
+}
+
+// B fragments of code dword `w` through build_table_hr: byte t's entry
+// (address: one v_perm of the byte into bits 8..15 beside ch = 8 * (lane %
+// 32)) lands as {H pair, R pair}; bytes 0, 1 form the first fragment
+// (K slots H0 H1 R0 R1 H2 H3 R2 R3 of the dword's elements 0..3), bytes 2, 3
+// the second (elements 4..7).
+__device__ __forceinline__ void decode8_hr(uint32_t w, uint32_t ch, half8 &f0, half8 &f1) {
+    const u32x2m e0 = *lds<lds_u32x2m>(__builtin_amdgcn_perm(w, ch, 0x0C0C0400u));
+    const u32x2m e1 = *lds<lds_u32x2m>(__builtin_amdgcn_perm(w, ch, 0x0C0C0500u));
+    const u32x2m e2 = *lds<lds_u32x2m>(__builtin_amdgcn_perm(w, ch, 0x0C0C0600u));
+    const u32x2m e3 = *lds<lds_u32x2m>(__builtin_amdgcn_perm(w, ch, 0x0C0C0700u));
+    f0 = __builtin_bit_cast(half8, u32x4v{e0.x, e0.y, e1.x, e1.y});
+    f1 = __builtin_bit_cast(half8, u32x4v{e2.x, e2.y, e3.x, e3.y});
+}
+
+// The activations as the GEMM's A operand, once per call: fp16 (rounded to
+// nearest) in the order the fragments need, [mt][64-element block kb][jj]
+// [lane] as 8 fp16 per entry: lane l = 16g + i holds token 16mt + i (zero
+// past M), elements 64kb + 16g + 8jj .. +8. A wave of the GEMM loads each
+// piece as 1 KiB contiguous and duplicates each element pair in registers
+// (the K slots x0 x1 x0 x1 x2 x3 x2 x3 that meet H0 H1 R0 R1 H2 H3 R2 R3).
+__global__ __launch_bounds__(256) void nf4_xpack_kernel(const float *x, u32x4v *xp, int M, int K, int total) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    const int lane = idx & 63, jj = (idx >> 6) & 1, kbs = K >> 6;
+    const int kb = (idx >> 7) % kbs, mt = (idx >> 7) / kbs;
+    const int m = 16 * mt + (lane & 15);
+    f32x4m lo4 = {0.0f, 0.0f, 0.0f, 0.0f}, hi4 = lo4;
+    if (m < M) {
+        const float *src = x + static_cast<size_t>(m) * K + 64 * kb + 16 * (lane >> 4) + 8 * jj;
+        lo4 = gload<f32x4m>(src);
+        hi4 = gload<f32x4m>(src + 4);
+    }
+    xp[(static_cast<size_t>(mt * kbs + kb) * 2 + jj) * 64 + lane] =
+        u32x4v{pack_half2(lo4.x, lo4.y), pack_half2(lo4.z, lo4.w), pack_half2(hi4.x, hi4.y), pack_half2(hi4.z, hi4.w)};
+}
+
+template <int MT, int NB>
+__global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
+    constexpr int KS = 64 * NB;
+    using GL = GemmLds<MT, NB>;
+    constexpr int D = GL::D;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i16 = lane & 15, g = lane >> 4;
+    const int kw = (static_cast<int>(blockIdx.x) * kGemmWaves + wave) * KS;
+    const int stride = gridDim.y;
+    const int last = a.tiles - 1;
+    const uint32_t ring = GL::kRingOff + wave * D * GL::kSlot;
+
+    // The first D tiles' weight loads go out first, then the wave's A
+    // fragments: 16-byte loads of the fragment image, 1 KiB contiguous per
+    // instruction (hi part, lo part 1 KiB on).
+    int tile = blockIdx.y;
+#pragma unroll
+    for (int d = 0; d < D; ++d) gemm_dma<NB>(a, min(tile + d * stride, last), kw, ring + d * GL::kSlot, lane);
+    // A operands: block b of token tile mt as four fragments, one per
+    // pair of code bytes (element pairs duplicated: x0 x1 x0 x1 x2 x3 x2 x3).
+    half8 ax[MT][NB][4];
+    {
+        const int kbs = a.K >> 6;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const u32x4v v =
+                        gload<u32x4v>(a.xp + (static_cast<size_t>(mt * kbs + (kw >> 6) + b) * 2 + jj) * 64 + lane);
+                    ax[mt][b][2 * jj] = __builtin_bit_cast(half8, u32x4v{v.x, v.x, v.y, v.y});
+                    ax[mt][b][2 * jj + 1] = __builtin_bit_cast(half8, u32x4v{v.z, v.z, v.w, v.w});
+                }
+    }
+    build_table_hr(tid);
+    // The fragments are consumed here, before the loop: the loop's own waits
+    // (explicit vmcnt for the LDS-DMA loads, which the compiler does not
+    // count) then never include one for them.
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) asm volatile("" ::"v"(ax[mt][b][0]), "v"(ax[mt][b][1]), "v"(ax[mt][b][2]),
+                                                  "v"(ax[mt][b][3]));
+    lds_barrier();                               // the table
+
+    const uint32_t ch = static_cast<uint32_t>(lane & 31) * 8;
+    // Lane's code offset within a slot for block 0 (block b adds
+    // 1024*(b/2) + 512*(b%2)) and its row's absmax offset.
+    const uint32_t coff = 16 * (16 * (g >> 1) + i16) + 8 * (g & 1);
+    const uint32_t soff = GL::kCodeBytes + 4 * NB * i16;
+    int slot = 0;
+    int buf = 0;
+    for (;;) {
+        const uint32_t sb = ring + slot * GL::kSlot;
+        wait_vmcnt<(D - 1) * GL::kDma>();        // this tile's DMA loads have landed
+        u32x2m q[NB];
+        float sc[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) q[b] = *lds<lds_u32x2m>(sb + coff + 1024 * (b >> 1) + 512 * (b & 1));
+#pragma unroll
+        for (int b = 0; b < NB; b += 4) {
+            if (b + 4 <= NB) {
+                const f32x4m v = *lds<lds_f32x4m>(sb + soff + 4 * b);
+                sc[b] = v.x; sc[b + 1] = v.y; sc[b + 2] = v.z; sc[b + 3] = v.w;
+            } else {
+                const f32x2 v = *lds<lds_f32x2>(sb + soff + 4 * b);
+                sc[b] = v.x; sc[b + 1] = v.y;
+            }
+        }
+        wait_lgkmcnt0();                         // the slot is read: refill it D tiles ahead
+        gemm_dma<NB>(a, min(tile + D * stride, last), kw, sb, lane);
+
+        // Per block b: dwords 2b (.x) and 2b+1 (.y) of the codes, each decoded
+        // by four table reads into two B fragments; the reads of dword d+2
+        // go out before the MFMAs of dword d (at most 12 reads outstanding:
+        // the LDS counter tracks 15). Each dword's two MFMAs form one chain,
+        // the block's two chains are added and scaled into acc one block
+        // later.
+        f32x4m acc[MT], f[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4m{0.0f, 0.0f, 0.0f, 0.0f};
+        const f32x4m z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+        half8 hb[4][2];
+        decode8_hr(q[0].x, ch, hb[0][0], hb[0][1]);
+        decode8_hr(q[0].y, ch, hb[1][0], hb[1][1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int cb = (2 * b) & 3;
+            f32x4m fx[MT], fy[MT];
+            if (b + 1 < NB) decode8_hr(q[b + 1].x, ch, hb[(cb + 2) & 3][0], hb[(cb + 2) & 3][1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                fx[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][0], hb[cb][0], z4, 0, 0, 0);
+                fx[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][1], hb[cb][1], fx[mt], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (b + 1 < NB) decode8_hr(q[b + 1].y, ch, hb[(cb + 3) & 3][0], hb[(cb + 3) & 3][1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                fy[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][2], hb[cb + 1][0], z4, 0, 0, 0);
+                fy[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][3], hb[cb + 1][1], fy[mt], 0, 0, 0);
+            }
+            // The previous block's products are ready by now: scale them in.
+            if (b > 0) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    acc[mt].x = fmaf(sc[b - 1], f[mt].x, acc[mt].x);
+                    acc[mt].y = fmaf(sc[b - 1], f[mt].y, acc[mt].y);
+                    acc[mt].z = fmaf(sc[b - 1], f[mt].z, acc[mt].z);
+                    acc[mt].w = fmaf(sc[b - 1], f[mt].w, acc[mt].w);
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) f[mt] = fx[mt] + fy[mt];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            acc[mt].x = fmaf(sc[NB - 1], f[mt].x, acc[mt].x);
+            acc[mt].y = fmaf(sc[NB - 1], f[mt].y, acc[mt].y);
+            acc[mt].z = fmaf(sc[NB - 1], f[mt].z, acc[mt].z);
+            acc[mt].w = fmaf(sc[NB - 1], f[mt].w, acc[mt].w);
+        }
+
+        // The waves' partial tiles through LDS, summed in wave order: lane l
+        // of wave w stores its 4 accumulators of token tile mt as one 16-byte
+        // piece at ((w*MT + mt)*64 + l)*16; thread o reads piece o/4, element
+        // o%4 of every wave (consecutive threads, consecutive addresses).
+        const uint32_t rb = GL::kRedOff + buf * GL::kRedBuf;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) *lds<lds_f32x4m>(rb + ((wave * MT + mt) * 64 + lane) * 16) = acc[mt];
+        lds_barrier();
+        const GemmTile tr = gemm_tile(a, tile * 16);
+#pragma unroll
+        for (int o0 = 0; o0 < 256 * MT; o0 += kGemmThreads) {
+            const int o = o0 + tid;
+            if (256 * MT % kGemmThreads != 0 && o >= 256 * MT) break;
+            const int mt = o >> 8, lq = (o >> 2) & 63, r = o & 3;
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kGemmWaves; ++w) v += __uint_as_float(*lds<lds_u32>(rb + (w * MT * 64 * 4 + o) * 4));
+            const int token = 16 * mt + 4 * (lq >> 4) + r, n = lq & 15, local = tr.local0 + n;
+            if (token < a.M && local < tr.n) {
+                typedef float __attribute__((address_space(1))) gf32;
+                if (a.part != nullptr) {
+                    *(gf32 *)(a.part + (static_cast<size_t>(blockIdx.x) * a.M + token) * a.N + tile * 16 + n) = v;
+                } else {
+                    gf32 *yp = (gf32 *)(tr.y + static_cast<size_t>(token) * tr.n + local);
+                    *yp = a.add ? *yp + v : v;
+                }
+            }
+        }
+        buf ^= 1;
+        slot = slot + 1 == D ? 0 : slot + 1;
+        tile += stride;
+        if (tile > last) break;
+    }
+    wait_vmcnt<0>();                             // no LDS-DMA write may land after the wave ends
+}
+
 }  // namespace
 
-// Scratch floats the GEMM's partials need for M tokens over K with stacked
-// rows N (the most any plan can use: one slice per sub-slice).
+// The activation-stationary NF4 GEMM's plan for N stacked rows over K with
+// passes of M <= 64 tokens on `cus` CUs: MT 16-token tiles, NB 64-element
+// blocks per wave (K % (512 * NB) == 0; MT * NB <= 8 keeps the fragments in
+// registers), `slices` = K / (512 * NB) workgroup K slices and `groups`
+// workgroups per slice, each walking every groups-th 16-row tile. False when
+// the shape does not fit the kernel.
+bool nf4_gemm_plan(int N, int K, int M, int cus, int &mt, int &nb, int &slices, int &groups) {
+    if (M < 1 || M > 64 || K % 1024 != 0 || N < 1) return false;
+    mt = (M + 15) / 16;
+    const int nbmax = 8 / mt;
+    const int kc = K / 512;
+    static const int cand[] = {8, 4, 2};
+    nb = 0;
+    for (int c : cand)
+        if (c <= nbmax && kc % c == 0) {
+            nb = c;
+            break;
+        }
+    if (nb == 0) return false;
+    slices = kc / nb;
+    const int tiles = (N + 15) / 16;
+    int gr = cus / slices;
+    if (gr < 1) gr = 1;
+    if (gr > tiles) gr = tiles;
+    const int per = (tiles + gr - 1) / gr;
+    groups = (tiles + per - 1) / per;
+    return groups <= 65535;
+}
+
+size_t nf4_xpack_bytes(int M, int K) { return static_cast<size_t>((M + 15) / 16) * K * 32; }
+
+int nf4_gemm_pass(const RowsOut *outs, int nseg, const float *A, int K, int M, bool add, float *part,
+                  size_t part_floats, const SliceTail *tail, const uint16_t *xpacked) {
+    GemmArgs args{};
+    long long end = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (i < nseg) {
+            const RowsOut &o = outs[i];
+            if (i < nseg - 1 && o.n % 16 != 0) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            end += o.n;
+            if (end > 0x7fff0000LL) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            args.y[i] = o.y;
+            args.w[i] = o.w;
+            args.absmax[i] = o.absmax;
+            args.end[i] = static_cast<int>(end);
+        } else {
+            args.end[i] = 0x7fffffff;
+        }
+    }
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    int mt = 0, nb = 0, slices = 0, groups = 0;
+    if (!nf4_gemm_plan(static_cast<int>(end), K, M, cus, mt, nb, slices, groups)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    args.nseg = nseg;
+    args.x = A;
+    args.M = M;
+    args.N = static_cast<int>(end);
+    args.K = K;
+    args.tiles = (args.N + 15) / 16;
+    args.add = slices == 1 && add;
+    // One buffer: the slice partials (when K is split or a tail follows),
+    // then the activations' fp16 fragment image (mt * K * 32 bytes, 256-byte
+    // aligned): the caller's `part` when it holds both, else the stream's.
+    const size_t pfl = slices > 1 || tail ? static_cast<size_t>(slices) * M * args.N : 0;
+    const size_t xoff = (pfl + 63) & ~static_cast<size_t>(63);
+    const size_t need = xpacked ? pfl : xoff + static_cast<size_t>(mt) * K * 8;
+    float *buf = !need ? nullptr
+                 : part && need <= part_floats ? part
+                                               : static_cast<float *>(stream_scratch(need * sizeof(float), kScratchPartials));
+    if (need && !buf) return ALJABR_ROCM_ERR_BUFFER;
+    args.part = pfl ? buf : nullptr;
+    args.xp = xpacked ? reinterpret_cast<const u32x4v *>(xpacked) : reinterpret_cast<const u32x4v *>(buf + xoff);
+    const dim3 grid(static_cast<unsigned>(slices), static_cast<unsigned>(groups));
+    hipStream_t s = current_stream();
+    if (!xpacked) {
+        const int total = mt * (K / 64) * 128;
+        hipLaunchKernelGGL(nf4_xpack_kernel, dim3((total + 255) / 256), dim3(256), 0, s, A,
+                           reinterpret_cast<u32x4v *>(buf + xoff), M, K, total);
+    }
+    const void *fn = nullptr;
+    uint32_t lds_bytes = 0;
+#define ALJ_GEMM_CASE(MT_, NB_)                                                          \
+    if (mt == MT_ && nb == NB_) {                                                        \
+        fn = reinterpret_cast<const void *>(nf4_gemm_kernel<MT_, NB_>);                  \
+        lds_bytes = GemmLds<MT_, NB_>::kBytes;                                           \
+    }
+    ALJ_GEMM_CASE(1, 2) ALJ_GEMM_CASE(1, 4) ALJ_GEMM_CASE(1, 8)
+    ALJ_GEMM_CASE(2, 2) ALJ_GEMM_CASE(2, 4)
+    ALJ_GEMM_CASE(3, 2)
+    ALJ_GEMM_CASE(4, 2)
+#undef ALJ_GEMM_CASE
+    if (!fn) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    static std::atomic<bool> lds_set[5][9];      // per (MT, NB): the attribute is per kernel, per process
+    if (!lds_set[mt][nb].load(std::memory_order_acquire)) {
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_bytes));
+        lds_set[mt][nb].store(true, std::memory_order_release);
+    }
+    void *kargs[] = {&args};
+    hipError_t e = hipLaunchKernel(fn, grid, dim3(kGemmThreads), kargs, lds_bytes, s);
+    if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "nf4 gemm launch: %s", hipGetErrorString(e));
+    if (tail) return enqueue_slice_tail(*tail, args.part, slices, M, args.N);
+    if (slices > 1) return enqueue_slice_sum(args.y, args.end, nseg, M, args.N, args.part, slices, add);
+    return ALJABR_ROCM_OK;
+}
+
 size_t nf4_mfma_scratch_floats(int M, int N, int K) {
     return static_cast<size_t>(K / kSub) * M * N;
 }
@@ -645,7 +1144,7 @@ int enqueue_slice_sum(float *const *ys, const int *ends, int nseg, int M, int N,
 }
 
 int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K, int bs_shift, int M, bool add,
-                           float *part, size_t part_floats, const SliceTail *tail) {
+                           float *part, size_t part_floats, const SliceTail *tail, const uint16_t *xpacked) {
     if (nseg < 1 || nseg > 3 || M < 2 || K % kSub != 0 || bs_shift != 6 || !aligned(A, 16) || (tail && M > 64))
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     long long n = 0;
@@ -667,6 +1166,16 @@ int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K,
         for (int i = 0; i < nseg; ++i) {
             o[i] = outs[i];
             o[i].y = outs[i].y + static_cast<size_t>(m0) * outs[i].n;
+        }
+        // The register-resident kernel where the shape fits it, else the
+        // LDS-staged one (K % 256 == 0, fp32-accurate).
+        {
+            const int rc = nf4_gemm_pass(o, nseg, A + static_cast<size_t>(m0) * K, K, mm, add, part, part_floats, tail,
+                                         M <= 64 ? xpacked : nullptr);
+            if (rc != ALJABR_ROCM_ERR_UNSUPPORTED) {
+                if (rc != ALJABR_ROCM_OK) return rc;
+                continue;
+            }
         }
         const int rc = nf4_mfma_pass_planned(o, nseg, A + static_cast<size_t>(m0) * K, K, mm, add, part, part_floats,
                                              nt, q, tail);

@@ -27,6 +27,22 @@ __device__ __forceinline__ float slice_total(const float *__restrict__ part, siz
 
 __device__ __forceinline__ uint16_t f16_bits(float v) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v)); }
 
+// Index (in fp16 elements) of element (m, c) of an [M][K] activation in the
+// NF4 GEMM's A image: [m/16][c/64][(c%16)/8][lane 16*((c%64)/16) + m%16]
+// [c%8] (matmul_mfma.hip, nf4_xpack_kernel).
+__device__ __forceinline__ size_t xpack_index(int m, int c, int K) {
+    const size_t entry = (static_cast<size_t>(m >> 4) * (K >> 6) + (c >> 6)) * 2 + ((c >> 3) & 1);
+    return (entry * 64 + 16 * ((c >> 4) & 3) + (m & 15)) * 8 + (c & 7);
+}
+
+// Four consecutive elements (c % 4 == 0) as fp16 (rounded to nearest): one
+// 8-byte store.
+__device__ __forceinline__ void xpack_store4(uint16_t *xp, int m, int c, int K, float4 v) {
+    const uint32_t lo = f16_bits(v.x) | (static_cast<uint32_t>(f16_bits(v.y)) << 16);
+    const uint32_t hi = f16_bits(v.z) | (static_cast<uint32_t>(f16_bits(v.w)) << 16);
+    *reinterpret_cast<uint2 *>(xp + xpack_index(m, c, K)) = make_uint2(lo, hi);
+}
+
 // RMSNorm's row scale 1/sqrt(mean(y^2) + eps) (the sqrt in double, as the
 // stand-alone RMSNorm) from the kSsqParts column-block sums of row m, added
 // in block order; 1 without sums.
@@ -48,7 +64,8 @@ __device__ __forceinline__ float swiglu_of(float g, float u) {
 // row scale of a preceding residual-scale tail, if any).
 __global__ __launch_bounds__(kThreads) void tail_swiglu_kernel(float *__restrict__ hb, const float *__restrict__ part,
                                                                int slices, int M, int N, int n,
-                                                               const float *__restrict__ ssq, int norm_n, float eps) {
+                                                               const float *__restrict__ ssq, int norm_n, float eps,
+                                                               uint16_t *__restrict__ xp) {
     const long long t = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
     if (t >= static_cast<long long>(M) * n) return;
     const int m = static_cast<int>(t / n), i = static_cast<int>(t - static_cast<long long>(m) * n);
@@ -57,7 +74,9 @@ __global__ __launch_bounds__(kThreads) void tail_swiglu_kernel(float *__restrict
     const float sc = row_scale(ssq, m, norm_n, eps);
     const float g = slice_total(part, stride, slices, row + i) * sc;
     const float u = slice_total(part, stride, slices, row + n + i) * sc;
-    hb[t] = swiglu_of(g, u);
+    const float h = swiglu_of(g, u);
+    hb[t] = h;
+    if (xp) xp[xpack_index(m, i, n)] = f16_bits(h);
 }
 
 // Workgroup (slot, m), head_dim/2 threads: slots [0, nh) are query heads
@@ -121,7 +140,7 @@ constexpr int kNormThreads = 1024;
 __global__ __launch_bounds__(kNormThreads) void tail_residual_norm_kernel(float *__restrict__ y, float *__restrict__ xn,
                                                                           const float *__restrict__ w, float eps,
                                                                           const float *__restrict__ part, int slices,
-                                                                          int M, int N) {
+                                                                          int M, int N, uint16_t *__restrict__ xp) {
     __shared__ float red[kNormThreads / 64];
     const int m = blockIdx.x;
     const size_t stride = static_cast<size_t>(M) * N;
@@ -149,7 +168,9 @@ __global__ __launch_bounds__(kNormThreads) void tail_residual_norm_kernel(float 
     const float4 *w4 = reinterpret_cast<const float4 *>(w);
     for (int c = threadIdx.x; c < N / 4; c += kNormThreads) {
         const float4 x = yr[c], g = w4[c];
-        xr[c] = make_float4((x.x * scale) * g.x, (x.y * scale) * g.y, (x.z * scale) * g.z, (x.w * scale) * g.w);
+        const float4 o = make_float4((x.x * scale) * g.x, (x.y * scale) * g.y, (x.z * scale) * g.z, (x.w * scale) * g.w);
+        xr[c] = o;
+        if (xp) xpack_store4(xp, m, 4 * c, N, o);
     }
 }
 
@@ -162,7 +183,7 @@ __global__ __launch_bounds__(kScaleThreads) void tail_residual_scale_kernel(floa
                                                                             const float *__restrict__ w,
                                                                             float *__restrict__ ssq,
                                                                             const float *__restrict__ part, int slices,
-                                                                            int M, int N) {
+                                                                            int M, int N, uint16_t *__restrict__ xp) {
     __shared__ float red[kScaleThreads / 64];
     const int pb = blockIdx.x, m = blockIdx.y;
     const int cols4 = N / (4 * kSsqParts);              // float4 columns per block
@@ -183,7 +204,9 @@ __global__ __launch_bounds__(kScaleThreads) void tail_residual_scale_kernel(floa
         x.w += acc.w;
         yr[c] = x;
         const float4 g = w4[c];
-        xr[c] = make_float4(x.x * g.x, x.y * g.y, x.z * g.z, x.w * g.w);
+        const float4 o = make_float4(x.x * g.x, x.y * g.y, x.z * g.z, x.w * g.w);
+        xr[c] = o;
+        if (xp) xpack_store4(xp, m, 4 * c, N, o);
         ss = fmaf(x.x, x.x, ss);
         ss = fmaf(x.y, x.y, ss);
         ss = fmaf(x.z, x.z, ss);
@@ -199,10 +222,11 @@ int enqueue_slice_tail(const SliceTail &t, const float *part, int slices, int M,
     hipStream_t s = current_stream();
     switch (t.kind) {
     case kTailSwiGLU: {
-        if (2LL * t.n != N || (t.ssq && t.norm_n <= 0)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+        if (2LL * t.n != N || (t.ssq && t.norm_n <= 0) || (t.xpack && (t.n % 64 != 0 || M > 64)))
+            return ALJABR_ROCM_ERR_UNSUPPORTED;
         const long long total = static_cast<long long>(M) * t.n;
         hipLaunchKernelGGL(tail_swiglu_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
-                           dim3(kThreads), 0, s, t.out, part, slices, M, N, t.n, t.ssq, t.norm_n, t.eps);
+                           dim3(kThreads), 0, s, t.out, part, slices, M, N, t.n, t.ssq, t.norm_n, t.eps, t.xpack);
         return ALJABR_ROCM_OK;
     }
     case kTailRopeAppend: {
@@ -215,17 +239,18 @@ int enqueue_slice_tail(const SliceTail &t, const float *part, int slices, int M,
         return ALJABR_ROCM_OK;
     }
     case kTailResidualNorm:
-        if (N % 4 != 0 || !aligned(t.out, 16) || !aligned(t.xn, 16) || !aligned(t.norm_w, 16) || !aligned(part, 16))
+        if (N % 4 != 0 || !aligned(t.out, 16) || !aligned(t.xn, 16) || !aligned(t.norm_w, 16) || !aligned(part, 16) ||
+            (t.xpack && (N % 64 != 0 || M > 64 || !aligned(t.xpack, 8))))
             return ALJABR_ROCM_ERR_UNSUPPORTED;
         hipLaunchKernelGGL(tail_residual_norm_kernel, dim3(M), dim3(kNormThreads), 0, s, t.out, t.xn, t.norm_w, t.eps,
-                           part, slices, M, N);
+                           part, slices, M, N, t.xpack);
         return ALJABR_ROCM_OK;
     case kTailResidualScale:
         if (N % (4 * kSsqParts) != 0 || !t.ssq || !aligned(t.out, 16) || !aligned(t.xn, 16) ||
-            !aligned(t.norm_w, 16) || !aligned(part, 16))
+            !aligned(t.norm_w, 16) || !aligned(part, 16) || (t.xpack && (N % 64 != 0 || M > 64 || !aligned(t.xpack, 8))))
             return ALJABR_ROCM_ERR_UNSUPPORTED;
         hipLaunchKernelGGL(tail_residual_scale_kernel, dim3(kSsqParts, M), dim3(kScaleThreads), 0, s, t.out, t.xn,
-                           t.norm_w, t.ssq, part, slices, M, N);
+                           t.norm_w, t.ssq, part, slices, M, N, t.xpack);
         return ALJABR_ROCM_OK;
     default: return ALJABR_ROCM_ERR_UNSUPPORTED;
     }

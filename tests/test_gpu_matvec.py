@@ -10,6 +10,8 @@ from conftest import rel_l2
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
+# Per token row, NF4 on the matrix cores (fp16-rounded activations, exact levels).
+NF4_MFMA_ROW_TOL = 3e-4
 
 # (N, K): square, gate/up (14336x4096) and down (4096x14336) Llama-3-8B shapes,
 # plus small and ragged shapes.
@@ -123,13 +125,17 @@ def test_gguf_mfma_is_deterministic(rocm, dev, oracle, qtype):
     assert rel_l2(outs[0], oracle.q_matvec(ot, enc, x, n, k).ravel()) <= TOL
 
 
-# NF4 small-M GEMM on the matrix cores (passes of up to 64 tokens: one
-# 32-token tile, or two sharing each decoded weight fragment; K % 256 == 0;
-# M = 2..4 with K % 2048 == 0 take the fp32 rows kernel): M across the tile
-# and pass boundaries (32, 33, 40, 64, 65, 100, 129), ragged N, K of one to
-# 56 sub-slices, the Llama MLP shapes, one K slice per workgroup and several (partials summed in
-# slice order by a second kernel). Both paths are fp32 accurate: every token
-# row within 1e-5 of the oracle.
+# NF4 small-M GEMM on the matrix cores (passes of up to 64 tokens; M = 2..4
+# with K % 2048 == 0 take the fp32 rows kernel): M across the 16-token tile
+# and pass boundaries (31, 32, 33, 40, 64, 65, 100, 129), ragged N, the Llama
+# MLP shapes, one K slice per workgroup and several (partials summed in slice
+# order by a second kernel). K % 1024 == 0 runs nf4_gemm_kernel: activations
+# rounded to fp16 (to nearest), levels exact (fp16 level + fp16 residual),
+# fp32 accumulation, so a token row is within the activations' rounding of
+# the fp32 oracle: ~2e-4 relative L2 (measured <= 2.3e-4; bound here 3e-4,
+# inside the 1e-3 contract); other K (512, 1536) run the fp32-accurate
+# nf4_mm_kernel. Every token row is checked on its own, so one wrong token
+# tile cannot hide in the total.
 @pytest.mark.parametrize("n,k,m", [(300, 1024, 2), (300, 1024, 3), (257, 2048, 8), (300, 1024, 31), (300, 1024, 32),
                                    (300, 1024, 33), (129, 512, 64), (300, 1024, 65), (77, 1536, 100),
                                    (14336, 4096, 16), (4096, 14336, 16), (4096, 14336, 64), (1000, 4096, 5),
@@ -145,9 +151,8 @@ def test_nf4_mfma_small_m(rocm, dev, oracle, n, k, m):
     rocm.call("aljabr_rocm_matvec_tb_batch_nf4", dev.ptr(y), dev.ptr(xd), dev.ptr(c), dev.ptr(a), k, n, 64, m)
     got = dev.get(y)
     assert rel_l2(got, y_ref) <= TOL
-    # every token row on its own, so one wrong m-tile cannot hide in the total
     for i in range(m):
-        assert rel_l2(got[i * n:(i + 1) * n], y_ref[i * n:(i + 1) * n]) <= 1e-5, i
+        assert rel_l2(got[i * n:(i + 1) * n], y_ref[i * n:(i + 1) * n]) <= NF4_MFMA_ROW_TOL, i
 
 
 @pytest.mark.parametrize("n,k,m", [(14336, 4096, 16), (4096, 14336, 32), (6144, 4096, 7), (14336, 4096, 64)])
@@ -165,7 +170,7 @@ def test_nf4_mfma_is_deterministic(rocm, dev, oracle, n, k, m):
     assert np.array_equal(outs[0], outs[1])
     y_ref = np.asarray(oracle.nf4_matvec(codes, absmax, x, n, k, 64)).reshape(m, n)
     for i in range(m):
-        assert rel_l2(outs[0][i * n:(i + 1) * n], y_ref[i]) <= 1e-5, i
+        assert rel_l2(outs[0][i * n:(i + 1) * n], y_ref[i]) <= NF4_MFMA_ROW_TOL, i
 
 
 # Batch-1 rows kernels (K % 2048 == 0): every K-chunk count S = K/2048 from 1
