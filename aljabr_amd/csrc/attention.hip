@@ -732,37 +732,68 @@ extern "C" int aljabr_rocm_attention_gqa(void *out, const void *Q, const void *K
 //
 // aljabr_rocm_attention_gqa_noalloc keeps its split partials in `scratch`, a
 // file-scope device array that every GPU the library runs on holds until the
-// process ends (kNoAllocScratchBytes each). Host code never passes the
-// array's name to a kernel: it is a host-side stand-in, not a device address.
-// The device address comes from hipGetSymbolAddress, once per device, with
-// that device current, and is kept per device. Calls on one GPU share the
-// array, so calls that overlap in time on one GPU race; every slot a call
-// reads was written by the same call (the split kernel writes every split's
-// partials before the merge reads them), so nothing needs clearing.
+// process ends (kNoAllocSlots slots of kNoAllocSlotBytes each). Host code
+// never passes the array's name to a kernel: it is a host-side stand-in, not
+// a device address. The device address comes from hipGetSymbolAddress, once
+// per device, with that device current, and is kept per device.
+//
+// Each slot belongs to one stream at a time, so calls on different streams
+// never share partials: calls on one stream are ordered by the stream, and
+// up to kNoAllocSlots streams per GPU run concurrently. A further stream
+// takes the least recently used slot after the device has drained (so the
+// slot's previous stream has finished with it). The slot is chosen and the
+// work enqueued under one lock. Every slot a call reads was written by the
+// same call (the split kernel writes every split's partials before the merge
+// reads them), so nothing needs clearing.
 namespace {
 
-constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;   // 8 MiB per GPU
-static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+constexpr int kNoAllocSlots = 4;
+constexpr size_t kNoAllocSlotBytes = size_t(8) << 20;      // 8 MiB per slot, 32 MiB per GPU
+static __device__ __align__(256) float scratch[kNoAllocSlots * kNoAllocSlotBytes / sizeof(float)];
 
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-float *g_scratch_ptr[kMaxDevices] = {};
+struct NoAllocDevice {
+    float *base = nullptr;                  // device address of `scratch` on this device
+    hipStream_t owner[kNoAllocSlots] = {};
+    bool taken[kNoAllocSlots] = {};
+    uint64_t last_use[kNoAllocSlots] = {};
+    uint64_t clock = 0;
+};
+std::mutex g_scratch_mu;                    // guards g_noalloc and spans slot choice + enqueue
+NoAllocDevice g_noalloc[kMaxDevices];
 
-// Device address of `scratch` on the current device (looked up once).
-int noalloc_scratch(float **out) {
+// The slot of stream `s` on the current device (caller holds g_scratch_mu).
+int noalloc_slot(hipStream_t s, float **out) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
     if (dev < 0 || dev >= kMaxDevices) return fail(ALJABR_ROCM_ERR_DEVICE, "device ordinal %d out of range", dev);
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (!g_scratch_ptr[dev]) {
+    NoAllocDevice &d = g_noalloc[dev];
+    if (!d.base) {
         void *ptr = nullptr;
         e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !ptr)
             return fail(ALJABR_ROCM_ERR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-        g_scratch_ptr[dev] = static_cast<float *>(ptr);
+        d.base = static_cast<float *>(ptr);
     }
-    *out = g_scratch_ptr[dev];
+    int pick = -1;
+    for (int i = 0; i < kNoAllocSlots && pick < 0; ++i)
+        if (d.taken[i] && d.owner[i] == s) pick = i;
+    for (int i = 0; i < kNoAllocSlots && pick < 0; ++i)
+        if (!d.taken[i]) pick = i;
+    if (pick < 0) {
+        pick = 0;
+        for (int i = 1; i < kNoAllocSlots; ++i)
+            if (d.last_use[i] < d.last_use[pick]) pick = i;
+        e = hipDeviceSynchronize();
+        if (e != hipSuccess)
+            return fail(ALJABR_ROCM_ERR_DEVICE, "attention_gqa_noalloc: draining the device for a slot: %s",
+                        hipGetErrorString(e));
+    }
+    d.owner[pick] = s;
+    d.taken[pick] = true;
+    d.last_use[pick] = ++d.clock;
+    *out = d.base + static_cast<size_t>(pick) * (kNoAllocSlotBytes / sizeof(float));
     return ALJABR_ROCM_OK;
 }
 
@@ -781,16 +812,13 @@ extern "C" int aljabr_rocm_attention_gqa_noalloc(void *out, const void *Q, const
         return fail(ALJABR_ROCM_ERR_UNSUPPORTED,
                     "attention_gqa_noalloc takes no mask (its check copies a flag to the host); use "
                     "aljabr_rocm_attention_gqa");
-    // Two splits of partials for every query row must fit the array, so that
+    // Two splits of partials for every query row must fit a slot, so that
     // the split count can always be lowered to what it holds.
     const size_t rows = static_cast<size_t>(B) * Hq * Sq;
-    if (rows * 2 * (static_cast<size_t>(D) + 2) * sizeof(float) > kNoAllocScratchBytes)
+    if (rows * 2 * (static_cast<size_t>(D) + 2) * sizeof(float) > kNoAllocSlotBytes)
         return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT,
-                    "attention_gqa_noalloc: B*Hq*Sq*2*(D+2)*4 = %zu bytes exceeds its %zu-byte scratch",
-                    rows * 2 * (static_cast<size_t>(D) + 2) * sizeof(float), kNoAllocScratchBytes);
-    float *buf = nullptr;
-    int rc = noalloc_scratch(&buf);
-    if (rc) return rc;
+                    "attention_gqa_noalloc: B*Hq*Sq*2*(D+2)*4 = %zu bytes exceeds its %zu-byte scratch slot",
+                    rows * 2 * (static_cast<size_t>(D) + 2) * sizeof(float), kNoAllocSlotBytes);
     AttnParams p{};
     p.out = static_cast<float *>(out);
     p.q = static_cast<const float *>(Q);
@@ -800,11 +828,17 @@ extern "C" int aljabr_rocm_attention_gqa_noalloc(void *out, const void *Q, const
     p.scale = scale > 0.0f ? scale : static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));
     p.causal = causal != 0;
     p.kv_f16 = kvType == ALJABR_ROCM_TYPE_F16;
-    p.scratch = buf;
-    p.scratch_bytes = kNoAllocScratchBytes;
+    p.scratch_bytes = kNoAllocSlotBytes;
     p.scratch_only = 1;
-    rc = enqueue_attention(p);
-    if (rc) return rc;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        float *buf = nullptr;
+        int rc = noalloc_slot(current_stream(), &buf);
+        if (rc) return rc;
+        p.scratch = buf;
+        rc = enqueue_attention(p);
+        if (rc) return rc;
+    }
     return finish_launch("attention_gqa_noalloc");
 }
 

@@ -32,13 +32,17 @@ int finish_launch(const char *what);
 
 // Device scratch owned by the library for the calling thread's stream; grows
 // monotonically. Stream order makes reuse by later calls on the same stream
-// safe. Returns nullptr (and records an error) on allocation failure. Slots
+// safe. Returns nullptr (and records an error) on allocation failure, and
+// while the stream is being captured (a graph would keep an address a later
+// growth frees). Slots
 // are separate buffers: kScratchPartials holds the matrix-core GEMMs' K-slice
 // partials, so a caller that keeps its own data in slot 0 across a GEMM call
 // is not overwritten.
 constexpr int kScratchSlots = 2;
 constexpr int kScratchPartials = 1;
 void *stream_scratch(size_t bytes, int slot = 0);
+// Bytes of stream scratch held for the calling thread's stream (all slots).
+size_t stream_scratch_held();
 
 // Number of compute units of the initialised device (for grid sizing).
 int device_cu_count();

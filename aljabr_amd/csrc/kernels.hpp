@@ -42,22 +42,32 @@ size_t attention_scratch_bytes(int B, int Hq, int Sq, int D, int keys);
 // Small-M GEMMs use the matrix-core kernels unless ALJABR_ROCM_MFMA=0.
 bool mfma_enabled();
 // C[M][N] = A[M][K] . W[N][K]^T for any M (slices or MFMA chosen inside).
-int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M);
-int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M);
+// `part`/`part_floats`: a caller-owned buffer for the matrix-core kernels'
+// K-slice partials (nf4_mfma_scratch_floats / kquant_mfma_scratch_floats of
+// the pass); when null or too small they take the stream's scratch.
+int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M,
+                       float *part = nullptr, size_t part_floats = 0);
+int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M,
+                        float *part = nullptr, size_t part_floats = 0);
 int enqueue_matmul_f32(float *C, const float *A, const float *W, int K, int N, int M);
 // Any weight type of the library (NF4 with its absmax and block size, GGUF
 // F32/F16/Q4_0/Q8_0/Q4_K/Q6_K).
 int enqueue_matmul_typed(float *C, const float *A, const void *W, const float *absmax, int type, int bs, int K, int N,
-                         int M);
+                         int M, float *part = nullptr, size_t part_floats = 0);
 // GGUF Q4_K / Q6_K rows (K % 256 == 0, A and W 16-byte aligned), any M.
-int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M);
+int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M,
+                          float *part = nullptr, size_t part_floats = 0);
 // GGUF block-format (Q4_K, Q6_K, Q4_0, Q8_0) small-M GEMM on MFMA
 // (2 <= M <= kquant_mfma_max_m(type): 32 for the K-quants, 8 for Q4_0 and
 // Q8_0; K % 512 == 0, A and W 16-byte aligned; ALJABR_ROCM_ERR_UNSUPPORTED
 // otherwise, nothing enqueued).
 bool kquant_mfma_type(int type);
 int kquant_mfma_max_m(int type);
-int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M);
+int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M,
+                        float *part = nullptr, size_t part_floats = 0);
+// Floats of `part` one enqueue_kquant_mfma_multi launch of M tokens over N
+// stacked rows and K needs (0: a single K slice).
+size_t kquant_mfma_scratch_floats(int M, int N, int K);
 // The same over up to three matrices of one type and K stacked in one launch
 // (all but the last with a multiple of 32 rows); outs[i].y is [M][outs[i].n].
 // With `accumulate` the products are added to the outputs as they are.
@@ -180,12 +190,15 @@ struct SliceTail {
     uint16_t *xpack;
 };
 int enqueue_slice_tail(const SliceTail &t, const float *part, int slices, int M, int N);
-// NF4 small-M GEMM on MFMA (M >= 2 in passes of 32 tokens, K % 256 == 0,
-// block size 64), fp32-accurate and deterministic: C = A . W^T, or with
-// `add` C += A . W^T (a residual). When K is split over workgroups the
-// partial sums go to `part` (nf4_mfma_scratch_floats(min(M, 32), N, K)
-// floats) or, when that is null or too small, to the stream's scratch, and
-// a second kernel adds the slices in order.
+// NF4 small-M GEMM on MFMA (M >= 2 in passes of 64 tokens, K % 256 == 0,
+// block size 64), deterministic: C = A . W^T, or with `add` C += A . W^T (a
+// residual). K % 1024 == 0 runs the register-resident kernel (activations
+// rounded to fp16, levels exact: about 2e-4 relative per row), other K the
+// fp32-accurate LDS-staged one. When K is split over workgroups the partial
+// sums (and the fp16 activation image) go to `part`
+// (nf4_mfma_scratch_floats(M, N, K) floats) or, when that is null or too
+// small, to the stream's scratch, and a second kernel adds the slices in
+// order.
 int enqueue_nf4_mfma(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs_shift,
                      int M, bool add = false, float *part = nullptr, size_t part_floats = 0);
 // The same over up to three matrices of one K stacked in one launch (all but
@@ -199,6 +212,8 @@ int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K,
                            const uint16_t *xpacked = nullptr);
 // Bytes of the fp16 A image for M <= 64 tokens over K (K % 64 == 0).
 size_t nf4_xpack_bytes(int M, int K);
+// Floats of `part` enqueue_nf4_mfma_multi needs for M tokens over N stacked
+// rows and K (every pass, with or without a tail, xpacked null).
 size_t nf4_mfma_scratch_floats(int M, int N, int K);
 // The plan enqueue_nf4_mfma_multi uses for N stacked rows over K on `cus`
 // CUs and passes of M tokens (row tiles per wave, sub-slices per K slice),

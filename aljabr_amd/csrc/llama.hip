@@ -244,17 +244,31 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
     const size_t kvd = static_cast<size_t>(c.n_kv_heads) * c.head_dim;
     const size_t qd = static_cast<size_t>(c.n_heads) * c.head_dim;
     const size_t cache_elems = static_cast<size_t>(L) * B * kvd * c.max_seq;
-    // K-slice partials of the batched matrix-core GEMMs (passes of at most
-    // 32 tokens): the NF4 bound of every layer shape, and the K-quant bound
-    // (one slice per 512 elements) of the output head, whose NF4 plan has a
-    // single slice.
+    // K-slice partials of every matrix-core GEMM a step of 2..max_batch
+    // tokens launches (stacked Q/K/V and gate/up, each projection alone, the
+    // output head), so that no launch takes the stream's scratch: a captured
+    // step keeps the addresses it was captured with.
     size_t mm_floats = 0;
     if (c.max_batch >= 2) {
-        const int bp = c.max_batch < 32 ? c.max_batch : 32;
-        const int shapes[4][2] = {{static_cast<int>(qd + 2 * kvd), c.dim}, {c.dim, static_cast<int>(qd)},
-                                  {2 * c.ffn, c.dim}, {c.dim, c.ffn}};
-        for (const auto &sh : shapes) mm_floats = std::max(mm_floats, nf4_mfma_scratch_floats(bp, sh[0], sh[1]));
-        mm_floats = std::max(mm_floats, static_cast<size_t>(c.dim / 512) * bp * static_cast<size_t>(c.vocab));
+        bool layer_nf4 = false, layer_kq = false;
+        for (int l = 0; l < L; ++l)
+            for (const auto *v : {&m->wq, &m->wk, &m->wv, &m->wo, &m->w_gate, &m->w_up, &m->w_down}) {
+                layer_nf4 = layer_nf4 || (*v)[l].type == ALJABR_ROCM_TYPE_NF4;
+                layer_kq = layer_kq || kquant_mfma_type((*v)[l].type);
+            }
+        const int ki = static_cast<int>(kvd), qi = static_cast<int>(qd);
+        const int shapes[8][2] = {{qi + 2 * ki, c.dim}, {qi, c.dim}, {ki, c.dim}, {c.dim, qi},
+                                  {2 * c.ffn, c.dim}, {c.ffn, c.dim}, {c.dim, c.ffn}, {c.vocab, c.dim}};
+        for (int i = 0; i < 8; ++i) {
+            const bool head = i == 7;
+            const bool nf4 = head ? m->lm_head.type == ALJABR_ROCM_TYPE_NF4 : layer_nf4;
+            const bool kq = head ? kquant_mfma_type(m->lm_head.type) : layer_kq;
+            if (kq)
+                mm_floats = std::max(mm_floats, kquant_mfma_scratch_floats(std::min(c.max_batch, 32), shapes[i][0],
+                                                                           shapes[i][1]));
+            for (int b = 2; nf4 && b <= c.max_batch; ++b)
+                mm_floats = std::max(mm_floats, nf4_mfma_scratch_floats(b, shapes[i][0], shapes[i][1]));
+        }
     }
     // The A images of xb and hb for the NF4 GEMMs (batches of 2..64).
     const bool packs = m->all_nf4 && c.max_batch >= 2 && c.max_batch <= 64 && c.dim % 64 == 0 && c.ffn % 64 == 0;
@@ -871,8 +885,8 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
             const int r = enqueue_kquant_mfma_multi(&o, 1, x, K, t.type, B, true, m->mm_part, m->mm_part_floats);
             if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
         }
-        if (!residual) return enqueue_matmul_typed(y, x, t.w, t.s, t.type, bs, K, N, B);
-        const int r = enqueue_matmul_typed(tmp, x, t.w, t.s, t.type, bs, K, N, B);
+        if (!residual) return enqueue_matmul_typed(y, x, t.w, t.s, t.type, bs, K, N, B, m->mm_part, m->mm_part_floats);
+        const int r = enqueue_matmul_typed(tmp, x, t.w, t.s, t.type, bs, K, N, B, m->mm_part, m->mm_part_floats);
         if (r != ALJABR_ROCM_OK) return r;
         return enqueue_add(y, tmp, static_cast<long long>(B) * N);
     };
@@ -1125,6 +1139,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         ap.kv_f16 = 1;
         ap.scratch = m->attn_scratch;
         ap.scratch_bytes = m->attn_scratch_bytes;
+        ap.scratch_only = 1;
         ALJ_TRY(enqueue_attention(ap));
         ALJ_MARK("attention", keys * nkv * hd * 2.0 * 2.0 + B * 2.0 * qd * f4);
         // x += Wo att.
@@ -1281,7 +1296,8 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         ALJ_TRY(enqueue_rmsnorm(m->xb, m->x, m->out_norm, B, dim, c.eps));
         ALJ_MARK("final_rmsnorm", (B * 2.0 * dim + dim) * f4);
     }
-    ALJ_TRY(enqueue_matmul_typed(lg, m->xb, m->lm_head.w, m->lm_head.s, m->lm_head.type, bs, dim, c.vocab, B));
+    ALJ_TRY(enqueue_matmul_typed(lg, m->xb, m->lm_head.w, m->lm_head.s, m->lm_head.type, bs, dim, c.vocab, B,
+                                 m->mm_part, m->mm_part_floats));
     ALJ_MARK(m->lm_head.type == ALJABR_ROCM_TYPE_F16 ? "lm_head_f16" : "lm_head", mm_bytes(m->lm_head, c.vocab, dim, false));
     ALJ_TRY(enqueue_argmax(next, lg, B, c.vocab));
     ALJ_MARK("argmax", B * static_cast<double>(c.vocab) * f4);

@@ -706,9 +706,16 @@ int enqueue_kquant_mfma_parts2(const KqOut *outs0, int nseg0, int type0, const K
     return ALJABR_ROCM_OK;
 }
 
-int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M) {
+int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M, float *part,
+                        size_t part_floats) {
     const KqOut o{C, W, N};
-    return enqueue_kquant_mfma_multi(&o, 1, A, K, type, M, false);
+    return enqueue_kquant_mfma_multi(&o, 1, A, K, type, M, false, part, part_floats);
+}
+
+size_t kquant_mfma_scratch_floats(int M, int N, int K) {
+    if (M < 2 || N < 1 || K % 512 != 0) return 0;
+    const int slices = K / kq_slice(N, K);
+    return slices > 1 ? static_cast<size_t>(slices) * M * N : 0;
 }
 
 }  // namespace aljabr

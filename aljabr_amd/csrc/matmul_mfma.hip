@@ -1041,8 +1041,31 @@ int nf4_gemm_pass(const RowsOut *outs, int nseg, const float *A, int K, int M, b
     return ALJABR_ROCM_OK;
 }
 
+// The largest buffer a pass of enqueue_nf4_mfma_multi takes: for the
+// register-resident kernel the slice partials (counted as when a tail
+// follows) and the fp16 activation image after them, for the LDS-staged one
+// the slice partials.
 size_t nf4_mfma_scratch_floats(int M, int N, int K) {
-    return static_cast<size_t>(K / kSub) * M * N;
+    if (M < 2 || N < 1 || K % kSub != 0) return 0;
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    size_t need = 0;
+    for (int m0 = 0; m0 < M; m0 += 64) {
+        const int mm = M - m0 < 64 ? M - m0 : 64;
+        int mt = 0, nb = 0, slices = 0, groups = 0;
+        size_t p;
+        if (nf4_gemm_plan(N, K, mm, cus, mt, nb, slices, groups)) {
+            const size_t pfl = static_cast<size_t>(slices) * mm * N;
+            p = ((pfl + 63) & ~static_cast<size_t>(63)) + static_cast<size_t>(mt) * K * 8;
+        } else {
+            int nt = 1, q = 1;
+            nf4_mfma_plan(N, K, mm, cus, nt, q);
+            const int nsub = K / kSub;
+            if (q > nsub) q = nsub;
+            p = static_cast<size_t>((nsub + q - 1) / q) * mm * N;
+        }
+        if (p > need) need = p;
+    }
+    return need;
 }
 
 // Row tiles per wave and sub-slices per slice for N stacked rows over K on

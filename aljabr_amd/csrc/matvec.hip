@@ -460,18 +460,19 @@ namespace aljabr {
 
 // M > 8 slices run the small-M kernels per slice of 8 tokens (weights are
 // re-read per slice); the MFMA path takes over at its threshold.
-int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M) {
+int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float *absmax, int K, int N, int bs, int M,
+                       float *part, size_t part_floats) {
     // M = 2..4 on the batch-1 rows kernel (fp32, the weights streamed once).
     if (M >= 2 && M <= 4) {
         const int shift = log2_exact(bs);
         if (shift >= 0 && enqueue_rows_nf4_mt(C, A, Bq, absmax, K, N, shift, M) == ALJABR_ROCM_OK)
             return ALJABR_ROCM_OK;
     }
-    // M >= 2 on the matrix cores when the shape allows (fp32-accurate,
-    // deterministic; passes of 32 tokens).
+    // M >= 2 on the matrix cores when the shape allows (deterministic;
+    // passes of 64 tokens).
     if (M >= 2 && mfma_enabled()) {
         const int shift = log2_exact(bs);
-        const int rc = enqueue_nf4_mfma(C, A, Bq, absmax, K, N, shift, M);
+        const int rc = enqueue_nf4_mfma(C, A, Bq, absmax, K, N, shift, M, false, part, part_floats);
         if (rc != ALJABR_ROCM_ERR_UNSUPPORTED) return rc;
     }
     for (int m0 = 0; m0 < M; m0 += 8) {
@@ -483,8 +484,10 @@ int enqueue_matmul_nf4(float *C, const float *A, const uint8_t *Bq, const float 
     return ALJABR_ROCM_OK;
 }
 
-int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M) {
-    if (type == ALJABR_ROCM_TYPE_Q4_K || type == ALJABR_ROCM_TYPE_Q6_K) return enqueue_matmul_kquant(C, A, B, K, N, type, M);
+int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N, int type, int M, float *part,
+                        size_t part_floats) {
+    if (type == ALJABR_ROCM_TYPE_Q4_K || type == ALJABR_ROCM_TYPE_Q6_K)
+        return enqueue_matmul_kquant(C, A, B, K, N, type, M, part, part_floats);
     // Q4_0 / Q8_0 with M >= 2 on the matrix cores (K % 512, 16-byte aligned),
     // 8 tokens per pass; a last single token takes the batch-1 path.
     if ((type == ALJABR_ROCM_TYPE_Q4_0 || type == ALJABR_ROCM_TYPE_Q8_0) && M >= 2 && K % 512 == 0 &&
@@ -493,7 +496,7 @@ int enqueue_matmul_gguf(float *C, const float *A, const uint8_t *B, int K, int N
         while (M - m0 >= 2) {
             const int mm = M - m0 < 8 ? M - m0 : 8;
             const int rc = enqueue_kquant_mfma(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, B, K,
-                                               N, type, mm);
+                                               N, type, mm, part, part_floats);
             if (rc != ALJABR_ROCM_OK) return rc;
             m0 += mm;                            // the pass covered exactly mm tokens
         }
@@ -540,16 +543,16 @@ int enqueue_matmul_f32(float *C, const float *A, const float *W, int K, int N, i
 }
 
 int enqueue_matmul_typed(float *C, const float *A, const void *W, const float *absmax, int type, int bs, int K, int N,
-                         int M) {
+                         int M, float *part, size_t part_floats) {
     const uint8_t *w = static_cast<const uint8_t *>(W);
     switch (type) {
-    case ALJABR_ROCM_TYPE_NF4: return enqueue_matmul_nf4(C, A, w, absmax, K, N, bs, M);
+    case ALJABR_ROCM_TYPE_NF4: return enqueue_matmul_nf4(C, A, w, absmax, K, N, bs, M, part, part_floats);
     case ALJABR_ROCM_TYPE_F32: return enqueue_matmul_f32(C, A, static_cast<const float *>(W), K, N, M);
     case ALJABR_ROCM_TYPE_F16:
     case ALJABR_ROCM_TYPE_Q4_0:
     case ALJABR_ROCM_TYPE_Q8_0:
     case ALJABR_ROCM_TYPE_Q4_K:
-    case ALJABR_ROCM_TYPE_Q6_K: return enqueue_matmul_gguf(C, A, w, K, N, type, M);
+    case ALJABR_ROCM_TYPE_Q6_K: return enqueue_matmul_gguf(C, A, w, K, N, type, M, part, part_floats);
     default: return ALJABR_ROCM_ERR_UNSUPPORTED;
     }
 }

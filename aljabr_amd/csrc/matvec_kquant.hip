@@ -110,7 +110,8 @@ void launch_kquant_mv(float *C, const float *A, const uint8_t *W, int K, int N, 
 
 // C[M][N] = A[M][K] . W^T for Q4_K / Q6_K rows (K % 256 == 0, A and W 16-byte
 // aligned); batch 1 with K % 2048 == 0 takes the rows kernel.
-int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M) {
+int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int N, int type, int M, float *part,
+                          size_t part_floats) {
     if ((type != ALJABR_ROCM_TYPE_Q4_K && type != ALJABR_ROCM_TYPE_Q6_K) || K % 256 != 0 || N < 1 || M < 1)
         return ALJABR_ROCM_ERR_UNSUPPORTED;
     if (!aligned(A, 16) || !aligned(W, 16))
@@ -124,7 +125,7 @@ int enqueue_matmul_kquant(float *C, const float *A, const uint8_t *W, int K, int
         while (M - m0 >= 2) {
             const int mm = M - m0 < 32 ? M - m0 : 32;
             const int rc = enqueue_kquant_mfma(C + static_cast<size_t>(m0) * N, A + static_cast<size_t>(m0) * K, W,
-                                               K, N, type, mm);
+                                               K, N, type, mm, part, part_floats);
             if (rc != ALJABR_ROCM_OK) return rc;
             m0 += mm;
         }

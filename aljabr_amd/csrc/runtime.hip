@@ -109,6 +109,15 @@ int finish_launch(const char *what) {
 void *stream_scratch(size_t bytes, int slot) {
     Context &c = ctx();
     hipStream_t s = current_stream();
+    // A captured graph would keep this buffer's address while a later,
+    // larger request on the stream frees it: work under capture brings its
+    // own buffers.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t ce = hipStreamIsCapturing(s, &cs);
+    if (ce != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        fail(ALJABR_ROCM_ERR_BUFFER, "stream scratch requested while the stream is being captured");
+        return nullptr;
+    }
     std::lock_guard<std::mutex> lock(c.mu);
     Scratch &sc = c.scratch[s][slot];
     if (sc.bytes >= bytes) return sc.ptr;
@@ -129,6 +138,17 @@ void *stream_scratch(size_t bytes, int slot) {
     sc.ptr = p;
     sc.bytes = want;
     return p;
+}
+
+size_t stream_scratch_held() {
+    Context &c = ctx();
+    const hipStream_t s = current_stream();
+    std::lock_guard<std::mutex> lock(c.mu);
+    const auto it = c.scratch.find(s);
+    if (it == c.scratch.end()) return 0;
+    size_t total = 0;
+    for (const Scratch &sc : it->second) total += sc.bytes;
+    return total;
 }
 
 int device_cu_count() { return ctx().cu_count; }
@@ -238,6 +258,13 @@ int aljabr_rocm_set_stream(void *hip_stream) {
     ThreadState &t = tls();
     t.has_override = hip_stream != nullptr;
     t.override_stream = static_cast<hipStream_t>(hip_stream);
+    return ALJABR_ROCM_OK;
+}
+
+int aljabr_rocm_stream_scratch_bytes(size_t *bytes) {
+    if (!bytes) return fail(ALJABR_ROCM_ERR_BAD_ARGUMENT, "bytes is null");
+    ALJ_CHECK_READY();
+    *bytes = stream_scratch_held();
     return ALJABR_ROCM_OK;
 }
 

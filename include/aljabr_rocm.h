@@ -100,6 +100,11 @@ int aljabr_rocm_get_stream(void **hip_stream);
 /* 1 (default): compute calls return after completion; 0: stream-ordered. Per thread. */
 int aljabr_rocm_set_sync_mode(int synchronous);
 int aljabr_rocm_synchronize(void);
+/* Bytes of device scratch the library holds for the calling thread's stream
+ * (grown on demand by calls that bring no buffer of their own; never taken
+ * while the stream is being captured). No counterpart in the reference: a
+ * diagnostic for callers that capture or budget device memory. */
+int aljabr_rocm_stream_scratch_bytes(size_t *bytes);
 
 /* Device allocation backing RocmDeviceStorage; the final TensorStorage.release()
  * maps to aljabr_rocm_free (plugins/ml/aljabr-tensor/.../memory/TensorStorage.java:21-41). */
@@ -189,13 +194,16 @@ int aljabr_rocm_attention_gqa(void *out, const void *Q, const void *K, const voi
 /* No counterpart in the reference: aljabr_rocm_attention_gqa for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Same arguments and results, mask must be
- * NULL (-3 otherwise). The split partials live in an 8 MiB device array each
- * GPU holds until the process ends: B*Hq*Sq*2*(D+2)*4 bytes must fit in it
- * (-2 otherwise), and the split count is lowered to what it holds. No device
- * or host allocation happens (the calling thread's stream is the one set with
- * aljabr_rocm_set_stream; without one, a thread's first call to the library
- * creates its stream). Calls that overlap in time on one GPU share the array
- * and race. */
+ * NULL (-3 otherwise). The split partials live in a 32 MiB device array each
+ * GPU holds until the process ends, four 8 MiB slots: B*Hq*Sq*2*(D+2)*4 bytes
+ * must fit in a slot (-2 otherwise), and the split count is lowered to what it
+ * holds. No device or host allocation happens (the calling thread's stream is
+ * the one set with aljabr_rocm_set_stream; without one, a thread's first call
+ * to the library creates its stream). Each slot serves one stream at a time:
+ * calls on one stream are ordered by it, up to four streams per GPU run
+ * concurrently, and a fifth stream waits for the device to drain before it
+ * takes the least recently used slot (so it must not be called while another
+ * stream of the process is being captured). */
 int aljabr_rocm_attention_gqa_noalloc(void *out, const void *Q, const void *K, const void *V,
                                       const void *mask, int B, int Hq, int Hkv, int Sq,
                                       int Sk, int D, int kvType, float scale, int causal);
