@@ -234,8 +234,24 @@ struct Mat {
     int type = 0;
 };
 
+// A host weight buffer uploaded once: keyed by its address, byte count and
+// type, so a different model at a reused address with another size or type
+// never reads the old copy.
+struct UploadKey {
+    const void *p;
+    size_t bytes;
+    int type;
+    bool operator==(const UploadKey &o) const { return p == o.p && bytes == o.bytes && type == o.type; }
+};
+struct UploadKeyHash {
+    size_t operator()(const UploadKey &k) const {
+        return std::hash<const void *>()(k.p) ^ (std::hash<size_t>()(k.bytes) * 31u) ^ (static_cast<size_t>(k.type) << 7);
+    }
+};
+
 struct Layer {
     bool set = false;
+    std::vector<UploadKey> uploads;     // host weights this registration uploaded
     int kv_layer = 0, owner = 0;
     Mat q, k, v, o, gate, up, down;
     int n0 = 0, n1 = 0, n2 = 0, wo_k = 0, wo_n = 0, ffn = 0, nh = 0, nkv = 0, hd = 0, stride = 0;
@@ -255,7 +271,7 @@ struct NormSlot {
 
 struct Upload {
     DevBuf buf;
-    size_t bytes = 0;
+    int owners = 0;              // registrations (layers, output, embedding) holding it
 };
 
 struct State {
@@ -280,7 +296,8 @@ struct State {
     int activation = 2;
     // activations
     DevBuf x, xb, att, q, k, v, gate, up, hb, logits, ints, staging, next_norm;
-    std::unordered_map<const void *, Upload> uploads;
+    std::vector<UploadKey> out_uploads, embd_uploads;
+    std::unordered_map<UploadKey, Upload, UploadKeyHash> uploads;
 
     void release_all() {
         for (auto &b : kv_k) b.release();
@@ -314,6 +331,8 @@ struct State {
             b->release();
         for (auto &u : uploads) u.second.buf.release();
         uploads.clear();
+        out_uploads.clear();
+        embd_uploads.clear();
     }
 };
 
@@ -323,8 +342,11 @@ State &state() {
 }
 
 // Device view of weights: device memory in place, host memory uploaded once
-// (by address; a larger request for the same address uploads again).
-int device_weights(State &st, const void *p, size_t bytes, const uint8_t **out) {
+// per (address, bytes, type). With `owner` the upload is held by that
+// registration (listed there, released by drop_uploads when it is
+// registered again); without, it stays cached for later calls.
+int device_weights(State &st, const void *p, size_t bytes, int type, const uint8_t **out,
+                   std::vector<UploadKey> *owner = nullptr) {
     if (!p) {
         *out = nullptr;
         return ALJABR_ROCM_OK;
@@ -333,17 +355,38 @@ int device_weights(State &st, const void *p, size_t bytes, const uint8_t **out) 
         *out = static_cast<const uint8_t *>(p);
         return ALJABR_ROCM_OK;
     }
-    Upload &u = st.uploads[p];
-    if (u.buf.p && u.bytes >= bytes) {
-        *out = static_cast<const uint8_t *>(u.buf.p);
-        return ALJABR_ROCM_OK;
+    const UploadKey key{p, bytes, type};
+    Upload &u = st.uploads[key];
+    if (!u.buf.p) {
+        if (!u.buf.ensure(bytes)) {
+            st.uploads.erase(key);
+            return fail(ALJABR_ROCM_ERR_BUFFER, "weight upload: cannot allocate %zu bytes", bytes);
+        }
+        const hipError_t e = hipMemcpy(u.buf.p, p, bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            st.uploads.erase(key);
+            return fail(ALJABR_ROCM_ERR_DEVICE, "weight upload: %s", hipGetErrorString(e));
+        }
     }
-    if (!u.buf.ensure(bytes)) return fail(ALJABR_ROCM_ERR_BUFFER, "weight upload: cannot allocate %zu bytes", bytes);
-    const hipError_t e = hipMemcpy(u.buf.p, p, bytes, hipMemcpyHostToDevice);
-    if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "weight upload: %s", hipGetErrorString(e));
-    u.bytes = bytes;
+    if (owner) {
+        ++u.owners;
+        owner->push_back(key);
+    }
     *out = static_cast<const uint8_t *>(u.buf.p);
     return ALJABR_ROCM_OK;
+}
+
+// A registration is replaced: its uploads lose an owner, and those no other
+// registration holds are freed (the host buffers may hold other weights now).
+void drop_uploads(State &st, std::vector<UploadKey> &keys) {
+    for (const UploadKey &k : keys) {
+        auto it = st.uploads.find(k);
+        if (it != st.uploads.end() && --it->second.owners <= 0) {
+            it->second.buf.release();
+            st.uploads.erase(it);
+        }
+    }
+    keys.clear();
 }
 
 // Copy `bytes` from host or device memory into device memory (stream order).
@@ -725,10 +768,10 @@ int adhoc_layer(State &st, const AdHoc &a, hipStream_t s, size_t &used) {
     g.type = a.typeGate;
     u.type = a.typeUp;
     d.type = a.typeDown;
-    if ((rc = device_weights(st, a.wO, matrix_bytes(a.typeWO, a.wO_N, a.wO_K), &o.w)) ||
-        (rc = device_weights(st, a.gateW, matrix_bytes(a.typeGate, a.ffnDim, a.wO_N), &g.w)) ||
-        (rc = device_weights(st, a.upW, matrix_bytes(a.typeUp, a.ffnDim, a.wO_N), &u.w)) ||
-        (rc = device_weights(st, a.downW, matrix_bytes(a.typeDown, a.wO_N, a.ffnDim), &d.w)))
+    if ((rc = device_weights(st, a.wO, matrix_bytes(a.typeWO, a.wO_N, a.wO_K), a.typeWO, &o.w)) ||
+        (rc = device_weights(st, a.gateW, matrix_bytes(a.typeGate, a.ffnDim, a.wO_N), a.typeGate, &g.w)) ||
+        (rc = device_weights(st, a.upW, matrix_bytes(a.typeUp, a.ffnDim, a.wO_N), a.typeUp, &u.w)) ||
+        (rc = device_weights(st, a.downW, matrix_bytes(a.typeDown, a.wO_N, a.ffnDim), a.typeDown, &d.w)))
         return rc;
     const size_t db = static_cast<size_t>(a.wO_N) * 4;
     // x, attn_full and up to four norm vectors staged.
@@ -887,17 +930,25 @@ int aljabr_rocm_register_decode_layer(int layer, int kvLayerIndex, const void *w
         (rc = check_mat(down, typeDown, wO_N, ffnDim, "down")))
         return rc;
     Layer &c = st.layer[layer];
+    // Registering again replaces the layer: its old uploads are dropped first
+    // (a failed registration leaves the layer unregistered).
+    c.set = false;
+    drop_uploads(st, c.uploads);
+    st.geometry_ready = false;
     Mat mq, mk, mv, mo, mg, mu, md;
     mq.type = typeQ; mk.type = typeK; mv.type = typeV; mo.type = typeWO;
     mg.type = typeGate; mu.type = typeUp; md.type = typeDown;
-    if ((rc = device_weights(st, wQ, matrix_bytes(typeQ, n0, wO_N), &mq.w)) ||
-        (rc = device_weights(st, wK, matrix_bytes(typeK, n1, wO_N), &mk.w)) ||
-        (rc = device_weights(st, wV, matrix_bytes(typeV, n2, wO_N), &mv.w)) ||
-        (rc = device_weights(st, wO, matrix_bytes(typeWO, wO_N, wO_K), &mo.w)) ||
-        (rc = device_weights(st, gate, matrix_bytes(typeGate, ffnDim, wO_N), &mg.w)) ||
-        (rc = device_weights(st, up, matrix_bytes(typeUp, ffnDim, wO_N), &mu.w)) ||
-        (rc = device_weights(st, down, matrix_bytes(typeDown, wO_N, ffnDim), &md.w)))
+    auto *own = &c.uploads;
+    if ((rc = device_weights(st, wQ, matrix_bytes(typeQ, n0, wO_N), typeQ, &mq.w, own)) ||
+        (rc = device_weights(st, wK, matrix_bytes(typeK, n1, wO_N), typeK, &mk.w, own)) ||
+        (rc = device_weights(st, wV, matrix_bytes(typeV, n2, wO_N), typeV, &mv.w, own)) ||
+        (rc = device_weights(st, wO, matrix_bytes(typeWO, wO_N, wO_K), typeWO, &mo.w, own)) ||
+        (rc = device_weights(st, gate, matrix_bytes(typeGate, ffnDim, wO_N), typeGate, &mg.w, own)) ||
+        (rc = device_weights(st, up, matrix_bytes(typeUp, ffnDim, wO_N), typeUp, &mu.w, own)) ||
+        (rc = device_weights(st, down, matrix_bytes(typeDown, wO_N, ffnDim), typeDown, &md.w, own))) {
+        drop_uploads(st, c.uploads);
         return rc;
+    }
     c.set = true;
     c.kv_layer = kvLayerIndex;
     c.q = mq; c.k = mk; c.v = mv; c.o = mo; c.gate = mg; c.up = mu; c.down = md;
@@ -922,7 +973,11 @@ int aljabr_rocm_register_output(const float *outputNormW, const void *outputW, i
     if (rc) return rc;
     Mat w;
     w.type = typeOutputW;
-    if ((rc = device_weights(st, outputW, matrix_bytes(typeOutputW, outputN, outputK), &w.w))) return rc;
+    st.out_w = Mat();
+    drop_uploads(st, st.out_uploads);
+    if ((rc = device_weights(st, outputW, matrix_bytes(typeOutputW, outputN, outputK), typeOutputW, &w.w,
+                             &st.out_uploads)))
+        return rc;
     if (outputNormW && is_device_ptr(outputNormW)) {
         st.out_norm_owned.release();
         st.out_norm = outputNormW;
@@ -955,7 +1010,10 @@ int aljabr_rocm_register_token_embd(const void *embdW, int typeEmbdW, int dim, f
     if (rc) return rc;
     Mat w;
     w.type = typeEmbdW;
-    if ((rc = device_weights(st, embdW, matrix_bytes(typeEmbdW, st.out_n, dim), &w.w))) return rc;
+    st.embd = Mat();
+    drop_uploads(st, st.embd_uploads);
+    if ((rc = device_weights(st, embdW, matrix_bytes(typeEmbdW, st.out_n, dim), typeEmbdW, &w.w, &st.embd_uploads)))
+        return rc;
     st.embd = w;
     st.embd_dim = dim;
     st.embd_vocab = st.out_n;
@@ -1032,7 +1090,7 @@ int aljabr_rocm_wo_ffn_next_qkv_fused(float *x, const float *attn_full, const vo
                 if (!ws[i]) continue;
                 if ((rc = check_mat(ws[i], ts[i], ns[i], wO_N, "next Q/K/V"))) return rc;
                 Mat m;
-                if ((rc = device_weights(st, ws[i], matrix_bytes(ts[i], ns[i], wO_N), &m.w))) return rc;
+                if ((rc = device_weights(st, ws[i], matrix_bytes(ts[i], ns[i], wO_N), ts[i], &m.w))) return rc;
                 ys[n] = outs[i]; dw[n] = m.w; yn[n] = ns[i]; yt[n] = ts[i]; idx[n++] = i;
             }
             rc = ALJABR_ROCM_OK;
@@ -1086,7 +1144,8 @@ int aljabr_rocm_wo_ffn_logits_fused(float *x, const float *attn_full, const void
         if ((rc = adhoc_layer(st, a, s, used))) return rc;
         Mat w;
         w.type = typeOutputW;
-        if ((rc = device_weights(st, outputW, matrix_bytes(typeOutputW, outputN, outputK), &w.w))) return rc;
+        if ((rc = device_weights(st, outputW, matrix_bytes(typeOutputW, outputN, outputK), typeOutputW, &w.w)))
+            return rc;
         rc = ALJABR_ROCM_OK;
         const float *nw = view_in(st, outputNormW, static_cast<size_t>(outputK) * 4, used, s, rc);
         if (rc) return rc;
@@ -1112,6 +1171,9 @@ int aljabr_rocm_wo_ffn_fused_layer_batch(float *x, const float *attn_full, int l
         if (!st.norm[1].p) return fail(ALJABR_ROCM_ERR_UNSUPPORTED, "wo_ffn_fused_layer_batch: the FFN norm (slot 1) is required");
         int rc = prepare(st, batchSize);
         if (rc) return rc;
+        // The activation buffers hold rows of the model width (layer 0's).
+        ALJ_REQUIRE(c.wo_n == st.dim, "wo_ffn_fused_layer_batch: layer %d's width %d is not the model width %d", layer,
+                    c.wo_n, st.dim);
         const int dim = c.wo_n;
         const float *ffn_norm, *post_attn, *post_ffn;
         if ((rc = slot_row(st, 1, layer, dim, &ffn_norm)) || (rc = slot_row(st, 0, layer, dim, &post_attn)) ||

@@ -66,10 +66,12 @@ def _prefill(model, seed: int, keep_host: bool = True):
     return host
 
 
-def _oracle_for(oracle, cfg, host, kc, vc, b, max_seq):
-    """LlamaOracle of sequence b with its caches set from the device caches
-    (position-major fp32 [layers][max_seq][n_kv * head_dim])."""
-    ref = oracle.LlamaOracle(dict(cfg, max_seq=max_seq), host)
+def _oracle_for(oracle, cfg, host, kc, vc, b, max_seq, typed=False):
+    """LlamaOracle (TypedLlamaOracle when `typed`) of sequence b with its
+    caches set from the device caches (position-major fp32
+    [layers][max_seq][n_kv * head_dim])."""
+    make = oracle.TypedLlamaOracle if typed else oracle.LlamaOracle
+    ref = make(dict(cfg, max_seq=max_seq), host)
     L, kvd = cfg["layers"], cfg["n_kv_heads"] * cfg["head_dim"]
     ref.k_cache[:] = kc[:, b].transpose(0, 2, 1, 3).reshape(L * max_seq * kvd).astype(np.float32)
     ref.v_cache[:] = vc[:, b].transpose(0, 2, 1, 3).reshape(L * max_seq * kvd).astype(np.float32)
@@ -116,6 +118,73 @@ def test_llama3_width_decode_matches_oracle(rocm, dev, oracle, llama3_two_layers
         got_hidden = dev.get(hid).reshape(batch, -1)
         for b in range(batch):
             ref_tok, ref_logits, ref_hidden = refs[b].decode(int(cur[b]), int(pos[b]))
+            assert rel_l2(got_hidden[b], ref_hidden) <= TOL, (step, b)
+            assert rel_l2(got_logits[b], ref_logits) <= TOL, (step, b)
+            assert got_tok[b] == ref_tok or \
+                ref_logits[ref_tok] - ref_logits[got_tok[b]] <= 1e-3 * np.abs(ref_logits).max(), (step, b)
+            cur[b] = ref_tok
+        pos = pos + 1
+    model.close()
+
+
+# GGUF Q4_K_M's mix: Q4_K everywhere but the V and down projections and the
+# output head (Q6_K).
+Q4_K_M = dict(tok_embed=12, wq=12, wk=12, wv=14, wo=12, w_gate=12, w_up=12, w_down=14, lm_head=14)
+
+
+@pytest.fixture(scope="module")
+def llama3_q4_k_m(rocm, oracle):
+    """Two Llama-3-8B-width layers of random K-quant super-blocks (the GGUF
+    test models' scales), as oracle weights and as device tensors."""
+    import torch
+    import gguf_writer as gw
+    from aljabr_amd.llama import LLAMA3_8B
+    cfg = dict(LLAMA3_8B, layers=2, max_seq=2112)
+    print("\n[llama3 width q4_k_m] drawing 2-layer weights", flush=True)
+    _, _, host = gw.llama_model(oracle, cfg, Q4_K_M, seed=9)
+
+    def put(arr):
+        return torch.from_numpy(np.ascontiguousarray(arr)).to("cuda:0")
+
+    dev_w = {"tok_embed": (host["tok_embed"][0], put(host["tok_embed"][1])),
+             "lm_head": (host["lm_head"][0], put(host["lm_head"][1])),
+             "out_norm": put(host["out_norm"]),
+             "attn_norm": [put(a) for a in host["attn_norm"]], "ffn_norm": [put(a) for a in host["ffn_norm"]]}
+    for key in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
+        dev_w[key] = [(t, put(a)) for t, a in host[key]]
+    torch.cuda.synchronize()
+    yield cfg, dev_w, host
+    del dev_w
+    torch.cuda.empty_cache()
+
+
+def test_llama3_width_q4_k_m_decode_matches_oracle(rocm, dev, oracle, llama3_q4_k_m):
+    """The GGUF Q4_K_M mix at B = 32 (the K-quant matrix-core GEMMs with
+    their fused tails, two formats per Q/K/V launch) from prefilled caches at
+    positions 100, 161, ..., 1930 and 2047, two steps: hidden state and
+    logits of every sequence within 1e-3 of the typed oracle."""
+    import torch
+    from aljabr_amd.llama import DeviceLlama
+    cfg, dev_w, host = llama3_q4_k_m
+    batch, max_seq = 32, cfg["max_seq"]
+    model = DeviceLlama.typed(cfg, dev_w, max_batch=batch, max_seq=max_seq)
+    kc, vc = _prefill(model, seed=77)
+    pos = np.array([100 + 61 * b for b in range(batch - 1)] + [2047], np.int32)
+    refs = [_oracle_for(oracle, cfg, host, kc, vc, b, max_seq, typed=True) for b in range(batch)]
+    del kc, vc
+    cur = oracle.uniform_int(91, cfg["vocab"], batch).astype(np.int32)
+    logits = torch.empty(batch * cfg["vocab"], dtype=torch.float32, device="cuda:0")
+    hid = torch.empty(batch * cfg["dim"], dtype=torch.float32, device="cuda:0")
+    for step in range(2):
+        print(f"[llama3 width q4_k_m] step {step} positions {pos.min()}..{pos.max()}", flush=True)
+        nxt = model.decode(dev.put(cur), dev.put(pos), batch, logits=logits)
+        got_tok = dev.get(nxt)
+        rocm.call("aljabr_rocm_memcpy_d2d", hid.data_ptr(), model.hidden_ptr(), batch * cfg["dim"] * 4)
+        got_logits = dev.get(logits).reshape(batch, -1)
+        got_hidden = dev.get(hid).reshape(batch, -1)
+        for b in range(batch):
+            ref_tok, ref_logits, ref_hidden = refs[b].decode(int(cur[b]), int(pos[b]))
+            assert np.isfinite(got_logits[b]).all(), (step, b)
             assert rel_l2(got_hidden[b], ref_hidden) <= TOL, (step, b)
             assert rel_l2(got_logits[b], ref_logits) <= TOL, (step, b)
             assert got_tok[b] == ref_tok or \

@@ -42,15 +42,8 @@ class Registry:
             if arr is not None:
                 rocm.call("aljabr_rocm_register_norm_buffer", slot, self.buf(arr), arr.nbytes)
         for l, c in enumerate(layers):
-            nh, nkv, hd = c["n_heads"], c["n_kv_heads"], c["head_dim"]
             mats = ("wq", "wk", "wv", "wo", "gate", "up", "down")
-            ptrs = [self.buf(c[m][1]) if c.get(m) is not None else None for m in mats]
-            types = [c[m][0] if c.get(m) is not None else 0 for m in mats]
-            rocm.call("aljabr_rocm_register_decode_layer", l, c.get("kv_layer", l), *ptrs, *types, nh * hd, nkv * hd,
-                      nkv * hd, nh * hd, dim, c["ffn"], nh, nkv, hd, nkv * hd, c.get("freq_base", 10000.0),
-                      int(c.get("is_swa", 0)), c.get("out_scale", 1.0), c.get("attn_scale", 0.0),
-                      *[int(c.get(f, 0)) for f in ("has_post_attn_norm", "has_post_ffn_norm", "has_q_norm",
-                                                   "has_k_norm", "has_unit_v_norm")])
+            self.register_layer(l, c, dim, [self.buf(c[m][1]) if c.get(m) is not None else None for m in mats])
             if c.get("rope_freqs") is not None:
                 rocm.call("aljabr_rocm_register_rope_freqs", l, self.buf(c["rope_freqs"]), c["rope_freqs"].size)
         rocm.call("aljabr_rocm_register_output", self.buf(model["out_norm"]), self.buf(model["out_w"][1]),
@@ -60,6 +53,19 @@ class Registry:
         rocm.call("aljabr_rocm_set_decode_activation", model["activation"])
         self.dim, self.vocab = dim, model["vocab"]
         self.logits_dev = dev.empty(self.vocab)
+
+    def register_layer(self, l, c, dim, ptrs, wo_n=None):
+        """register_decode_layer for layer `l` of config `c` with the weight
+        pointers `ptrs` (wq, wk, wv, wo, gate, up, down)."""
+        nh, nkv, hd = c["n_heads"], c["n_kv_heads"], c["head_dim"]
+        mats = ("wq", "wk", "wv", "wo", "gate", "up", "down")
+        types = [c[m][0] if c.get(m) is not None else 0 for m in mats]
+        self.rocm.call("aljabr_rocm_register_decode_layer", l, c.get("kv_layer", l), *ptrs, *types, nh * hd,
+                       nkv * hd, nkv * hd, nh * hd, wo_n or dim, c["ffn"], nh, nkv, hd, nkv * hd,
+                       c.get("freq_base", 10000.0), int(c.get("is_swa", 0)), c.get("out_scale", 1.0),
+                       c.get("attn_scale", 0.0),
+                       *[int(c.get(f, 0)) for f in ("has_post_attn_norm", "has_post_ffn_norm", "has_q_norm",
+                                                    "has_k_norm", "has_unit_v_norm")])
 
     def buf(self, a):
         a = np.ascontiguousarray(a)
@@ -335,5 +341,62 @@ def test_wo_ffn_fused_layer_batch(rocm, dev, oracle, batch):
         L = dict(dim=dim, k=sm.NH * sm.HD, ffn=sm.FFN, wo=c["wo"], gate=c["gate"], up=c["up"], down=c["down"])
         ref = _layer_ref(oracle, x.astype(np.float64), att.astype(np.float64), L, norms, 2, c.get("out_scale", 1.0))
         assert rel_l2(xin, ref) <= TOL, layer
+    del reg
+    rocm.call("aljabr_rocm_reset_decode_state")
+
+
+def test_reregistered_layer_reads_new_host_weights(rocm, dev, oracle):
+    """Host weights are uploaded once per registration: a layer registered
+    again from the same host addresses (same sizes and types) after the
+    caller rewrote them computes with the new contents, not a stale copy."""
+    model, _ = sm.gemma_like(oracle)
+    reg = Registry(rocm, dev, model, host=True)
+    lib = rocm.load()
+    dim, batch = sm.DIM, 3
+    c = model["layers"][0]
+    mats = ("wq", "wk", "wv", "wo", "gate", "up", "down")
+    own = {m: np.array(c[m][1], copy=True) for m in mats if c.get(m) is not None}
+    ptrs = [own[m].ctypes.data if m in own else None for m in mats]
+    norms = {"ffn": model["norm"][1].reshape(-1, dim)[0]}
+    if c.get("has_post_attn_norm"):
+        norms["post_attn"] = model["norm"][0].reshape(-1, dim)[0]
+    if c.get("has_post_ffn_norm"):
+        norms["post_ffn"] = model["norm"][2].reshape(-1, dim)[0]
+    x = oracle.normal(61, batch * dim).reshape(batch, dim)
+    att = oracle.normal(62, batch * sm.NH * sm.HD).reshape(batch, -1)
+    for rnd in range(2):
+        if rnd == 1:                              # same buffers, new weights
+            for i, m in enumerate(("wo", "gate", "up", "down")):
+                assert c[m][0] == F32
+                own[m][...] = oracle.normal(63 + i, own[m].size, 0.0, 0.1).reshape(own[m].shape)
+        reg.register_layer(0, c, dim, ptrs)
+        xin = np.ascontiguousarray(x.copy())
+        rocm.check(lib.aljabr_rocm_wo_ffn_fused_layer_batch(xin.ctypes.data, att.ctypes.data, 0, batch, EPS, 2),
+                   "wo_ffn_fused_layer_batch")
+        L = dict(dim=dim, k=sm.NH * sm.HD, ffn=sm.FFN, **{m: (F32, own[m]) for m in ("wo", "gate", "up", "down")})
+        ref = _layer_ref(oracle, x.astype(np.float64), att.astype(np.float64), L, norms, 2, c.get("out_scale", 1.0))
+        assert rel_l2(xin, ref) <= TOL, rnd
+    del reg
+    rocm.call("aljabr_rocm_reset_decode_state")
+
+
+def test_layer_batch_refuses_a_layer_wider_than_the_model(rocm, dev, oracle):
+    """The batch Wo/FFN call works on rows of the model width (layer 0's);
+    a layer registered wider is refused before anything runs."""
+    model, _ = sm.gemma_like(oracle)
+    reg = Registry(rocm, dev, model, host=True)
+    lib = rocm.load()
+    wide = sm.DIM + 32
+    c = dict(n_heads=2, n_kv_heads=1, head_dim=16, ffn=64, kv_layer=1,
+             **{m: (F32, None) for m in ("wq", "wk", "wv", "wo", "gate", "up", "down")})
+    shapes = dict(wq=(32, wide), wk=(16, wide), wv=(16, wide), wo=(wide, 32), gate=(64, wide), up=(64, wide),
+                  down=(wide, 64))
+    ptrs = [reg.buf(np.full(shapes[m], 0.01, np.float32)) for m in ("wq", "wk", "wv", "wo", "gate", "up", "down")]
+    reg.register_layer(1, c, sm.DIM, ptrs, wo_n=wide)
+    x = np.zeros(2 * wide, np.float32)
+    att = np.zeros(2 * 32, np.float32)
+    assert lib.aljabr_rocm_wo_ffn_fused_layer_batch(x.ctypes.data, att.ctypes.data, 1, 2, EPS, 2) \
+        == rocm.ERR_BAD_ARGUMENT
+    assert "width" in rocm.last_error()
     del reg
     rocm.call("aljabr_rocm_reset_decode_state")

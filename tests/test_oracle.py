@@ -431,3 +431,25 @@ def test_gated_activation_closed_forms(oracle):
     e = oracle.gated_activation(g, u, 2)
     np.testing.assert_array_equal(e[3:5], [12.0, 0.0])
     assert abs(oracle.gated_activation(np.float32([1.0]), np.float32([1.0]), 0)[0] - 1 / (1 + np.exp(-1))) < 1e-7
+
+
+def test_gelu_against_erf_form_and_its_constant(oracle):
+    """GELU (kind 2) is the tanh form of x * Phi(x). Against the erf form
+    0.5 x (1 + erf(x / sqrt 2)) it stays within the tanh form's known largest
+    deviation (about 4.73e-4 absolute, near |x| = 2.70; bound 5e-4); a
+    dropped cubic term or a wrong inner constant misses by about 0.03. And it
+    equals the tanh form rebuilt here from sqrt(2 / pi) and 0.044715 to fp32
+    rounding."""
+    import math
+    x = np.linspace(-12.0, 12.0, 48001).astype(np.float32)
+    got = oracle.gated_activation(x, np.ones_like(x), 2).astype(np.float64)
+    xd = x.astype(np.float64)
+    erf_form = np.array([0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0))) for v in xd])
+    assert np.max(np.abs(got - erf_form)) <= 5e-4
+    k = math.sqrt(2.0 / math.pi)
+    tanh_form = 0.5 * xd * (1.0 + np.tanh(k * (xd + 0.044715 * xd ** 3)))
+    assert np.max(np.abs(got - tanh_form) / np.maximum(1.0, np.abs(tanh_form))) <= 2e-7
+    # The gate times `up`, not the activation alone.
+    u = np.linspace(-3.0, 3.0, x.size).astype(np.float32)
+    np.testing.assert_allclose(oracle.gated_activation(x, u, 2), (tanh_form * u).astype(np.float32), rtol=2e-6,
+                               atol=1e-7)
