@@ -116,6 +116,7 @@ SIGNATURES = {
     "aljabr_rocm_set_stream": (_I, [_P]),
     "aljabr_rocm_get_stream": (_I, [ctypes.POINTER(_P)]),
     "aljabr_rocm_stream_scratch_bytes": (_I, [ctypes.POINTER(ctypes.c_size_t)]),
+    "aljabr_rocm_stream_read_probe": (_I, [_P, ctypes.c_size_t, _P, _I]),
     "aljabr_rocm_set_sync_mode": (_I, [_I]),
     "aljabr_rocm_synchronize": (_I, []),
     "aljabr_rocm_alloc": (_I, [_SZ, ctypes.POINTER(_P)]),

@@ -44,7 +44,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=2000,
-                    help="untimed MLP steps first (the GPU takes ~15 ms of load to reach its steady clocks)")
+                    help="untimed MLP steps right before the timed ones")
+    ap.add_argument("--clock-warmup-ms", type=float, default=300.0,
+                    help="untimed MLP steps for at least this long before the --warmup steps (the GPU needs "
+                         "~15 ms of load to reach its steady clocks); reported as clock_warmup_ms")
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough for 512 MB)")
     ap.add_argument("--no-decode", action="store_true", help="skip the Llama decode measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -68,6 +71,10 @@ def parse() -> argparse.Namespace:
                     help="run only the GQA decode attention measurement (for profiling)")
     ap.add_argument("--step-only", action="store_true",
                     help="run only the registered whole-step (Metal ABI) decode measurement")
+    ap.add_argument("--stream-ceiling", action="store_true",
+                    help="only time a plain streaming read of rotating 33 MB buffers (the batch-1 ceiling)")
+    ap.add_argument("--ceiling-workgroups", type=int, default=0,
+                    help="with --stream-ceiling: only this workgroup count (0: the sweep)")
     return ap.parse_args()
 
 
@@ -87,7 +94,10 @@ def make_mlp_copies(abi, torch, copies: int):
     return mats
 
 
-def time_mlp(abi, torch, stream, mats, steps: int, warmup: int):
+def time_mlp(abi, torch, stream, mats, steps: int, warmup: int, clock_warmup_ms: float):
+    """Milliseconds of `steps` MLP steps, after untimed steps for at least
+    `clock_warmup_ms` of wall time and then `warmup` more; returns (ms,
+    clock warm-up ms, clock warm-up steps)."""
     lib = abi.load()
     x = torch.randn(K_MODEL, device="cuda:0")
     h = torch.randn(FFN, device="cuda:0")
@@ -103,17 +113,27 @@ def time_mlp(abi, torch, stream, mats, steps: int, warmup: int):
                 abi.check(rc, "aljabr_rocm_matvec_tb_nf4")
 
     with torch.cuda.stream(stream):
+        # Clock warm-up: batches of 100 steps until the wall clock says so.
+        done, t0 = 0, time.perf_counter()
+        while True:
+            for _ in range(100):
+                step(done)
+                done += 1
+            torch.cuda.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= clock_warmup_ms:
+                break
+        clock_ms = (time.perf_counter() - t0) * 1e3
         for i in range(warmup):
-            step(i)
+            step(done + i)
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
         for i in range(steps):
-            step(warmup + i)
+            step(done + warmup + i)
         end.record(stream)
         end.synchronize()
     torch.cuda.synchronize()
-    return start.elapsed_time(end)   # ms
+    return start.elapsed_time(end), clock_ms, done
 
 
 def _cpu_rate(fn, nbytes: int, seconds: float):
@@ -129,13 +149,15 @@ def _cpu_rate(fn, nbytes: int, seconds: float):
     return nbytes * done / dt / 1e9, done, dt
 
 
-def cpu_baseline(seconds: float):
+def cpu_baseline(seconds: float, llama_host=None):
     """The oracle (C restatement of the reference CPU path, OpenMP row chunks =
     2 x threads as GgufParallelConfig) on bounded samples: the NF4 MLP step
     at all host cores for ~`seconds` (the reported value), then single-thread
-    and all-core rates of the NF4 matvec, the Q4_0 matvec (14336x4096) and
-    GQA decode attention (B=1 and 16, S=4096, fp16 K/V widened to fp32) for
-    ~2 s each. The reference's own Java Vector-API path cannot run here."""
+    and all-core rates of the NF4, Q4_0, Q8_0 and Q4_K matvecs (14336x4096)
+    and GQA decode attention (B=1 and 16, S=4096, fp16 K/V widened to fp32)
+    for ~2 s each, and, given the Llama-3-8B NF4 model's host weights, two
+    batch-1 decode tokens of the whole step at all cores. The reference's own
+    Java Vector-API path cannot run here."""
     import numpy as np
     import oracle
     threads = oracle.threads()
@@ -156,11 +178,16 @@ def cpu_baseline(seconds: float):
         r, _, _ = _cpu_rate(lambda: oracle.nf4_matvec(c0, a0, xs[K_MODEL], FFN, K_MODEL, BLOCK, t),
                             nf4_bytes(FFN, K_MODEL), 2.0)
         extra[f"nf4_14336x4096_m1_{t}t_GBs"] = round(r, 3)
-    q = oracle.quantize(oracle.QTYPE_Q4_0, oracle.normal(200, FFN * K_MODEL, 0.0, 0.02))
-    for t in (1, threads):
-        r, _, _ = _cpu_rate(lambda: oracle.q_matvec(oracle.QTYPE_Q4_0, q, xs[K_MODEL], FFN, K_MODEL, t),
-                            q.size + 4 * (FFN + K_MODEL), 2.0)
-        extra[f"q4_0_14336x4096_m1_{t}t_GBs"] = round(r, 3)
+    w32 = oracle.normal(200, FFN * K_MODEL, 0.0, 0.02)
+    for name, qt, q in (("q4_0", oracle.QTYPE_Q4_0, oracle.quantize(oracle.QTYPE_Q4_0, w32)),
+                        ("q8_0", oracle.QTYPE_Q8_0, oracle.quantize(oracle.QTYPE_Q8_0, w32)),
+                        ("q4_k", oracle.QTYPE_Q4_K, oracle.random_k_blocks(oracle.QTYPE_Q4_K, FFN * K_MODEL // 256,
+                                                                           201))):
+        for t in (1, threads):
+            r, _, _ = _cpu_rate(lambda: oracle.q_matvec(qt, q, xs[K_MODEL], FFN, K_MODEL, t),
+                                q.size + 4 * (FFN + K_MODEL), 2.0)
+            extra[f"{name}_14336x4096_m1_{t}t_GBs"] = round(r, 3)
+    del w32
     hq, hkv, d, s = 32, 8, 128, 4096
     for b in (1, 16):
         qv = oracle.normal(300 + b, b * hq * d).reshape(b, hq, 1, d)
@@ -170,13 +197,25 @@ def cpu_baseline(seconds: float):
         for t in (1, threads):
             r, _, _ = _cpu_rate(lambda: oracle.attention_gqa(qv, kv, vv, None, True, t), nbytes, 2.0)
             extra[f"attention_b{b}_s{s}_{t}t_GBs"] = round(r, 3)
+    decode = None
+    if llama_host is not None:
+        from aljabr_amd.llama import LLAMA3_8B
+        ref = oracle.LlamaOracle(dict(LLAMA3_8B, max_seq=8), llama_host)
+        t0 = time.perf_counter()
+        tok, _, _ = ref.decode(17, 0, threads)
+        ref.decode(tok, 1, threads)
+        dt2 = time.perf_counter() - t0
+        decode = {"tokens_per_s": round(2.0 / dt2, 3), "ms_per_token": round(dt2 * 500.0, 1), "cores": threads,
+                  "sample": "2 batch-1 decode tokens (positions 0, 1) of the Llama-3-8B NF4 model the GPU decode "
+                            "bench runs (32 layers, fp16 LM head), oracle.LlamaOracle at all threads"}
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"{done} MLP steps (3 NF4 matvecs each: 14336x4096, 14336x4096, 4096x14336, batch 1), "
                       f"{dt:.1f} s, oracle C restatement, OpenMP row chunks = 2 x {threads} threads",
             "per_kernel": extra,
             "per_kernel_sample": "about 2 s per entry: 1 thread and all host threads; attention bytes count "
-                                 "K/V at fp16 (the GPU's format) though the oracle reads them widened"}
+                                 "K/V at fp16 (the GPU's format) though the oracle reads them widened",
+            "decode_llama3_8b_nf4_b1": decode}
 
 
 def small_m_bench(abi, torch, stream, ms=(1, 4, 16, 64), launches=60):
@@ -421,6 +460,49 @@ def traffic_record(kernel: str):
     return int(rec["bytes_per_launch"]) if rec else None
 
 
+CEILING_BYTES = FFN * K_MODEL // 2 + FFN * K_MODEL // BLOCK * 4   # codes + absmax of one 14336x4096 matrix
+
+
+def stream_ceiling(abi, torch, stream, launches: int = 300, wgs=(256, 512, 1024, 2048, 4096, 8192)):
+    """A plain streaming read (aljabr_rocm_stream_read_probe) of rotating
+    buffers of one NF4 14336x4096 matrix's bytes (codes + absmax, 33,030,144
+    B), enough of them for 512 MB as the MLP step rotates its copies: the
+    read-only rate one launch of that size reaches, per workgroup count."""
+    lib = abi.load()
+    copies = max(2, -(-512_000_000 // CEILING_BYTES))
+    bufs = [torch.randint(0, 255, (CEILING_BYTES,), dtype=torch.uint8, device="cuda:0") for _ in range(copies)]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
+    torch.cuda.synchronize()
+    out = {"bytes_per_launch": CEILING_BYTES, "copies": copies, "launches": launches, "by_workgroups": {}}
+    best = None
+    with torch.cuda.stream(stream):
+        for wg in wgs:
+            def go(i):
+                rc = lib.aljabr_rocm_stream_read_probe(bufs[i % copies].data_ptr(), CEILING_BYTES, sink.data_ptr(),
+                                                       wg)
+                if rc:
+                    abi.check(rc, "aljabr_rocm_stream_read_probe")
+            for i in range(launches):
+                go(i)
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for i in range(launches):
+                go(i)
+            end.record(stream)
+            end.synchronize()
+            us = start.elapsed_time(end) * 1e3 / launches
+            gbs = CEILING_BYTES / us / 1e3
+            out["by_workgroups"][str(wg)] = {"us": round(us, 3), "GBs": round(gbs, 1),
+                                             "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            if best is None or us < best[1]:
+                best = (wg, us, gbs)
+    out.update(best_workgroups=best[0], us=round(best[1], 3), GBs=round(best[2], 1),
+               frac=round(best[2] / HBM_PEAK_GBS, 4))
+    del bufs
+    torch.cuda.empty_cache()
+    return out
+
+
 def copy_probe(torch, stream) -> None:
     """A plain device copy of known size, for calibrating the HBM counters."""
     n = 64 << 20                                   # 64 Mi floats = 256 MiB each way
@@ -495,8 +577,20 @@ def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, make_mode
             "profiled_ms": round(prof_us / 1e3, 3), "kernels": kernels}
 
 
-def decode_runs(args, abi, torch, stream):
-    """random-init Llama-3-8B-shaped NF4 decode at batch 1 and 32, context 2048."""
+def host_weights(torch, weights: dict) -> dict:
+    """Device weights (random_weights layout) as the oracle's numpy arrays."""
+    import numpy as np
+
+    def get(t):
+        a = t.cpu().numpy()
+        return a.view(np.uint16) if t.dtype == torch.float16 else a
+    return {k: [get(t) for t in v] if isinstance(v, list) else get(v) for k, v in weights.items()}
+
+
+def decode_runs(args, abi, torch, stream, keep_host: bool = False):
+    """random-init Llama-3-8B-shaped NF4 decode at batch
+    1 and 32, context 2048. With keep_host also returns the weights as host
+    arrays (the CPU baseline's oracle decode runs on the same model)."""
     from aljabr_amd.llama import LLAMA3_8B, DeviceLlama, random_weights
     log("building random-init Llama-3-8B-shaped NF4 model")
     t0 = time.perf_counter()
@@ -507,9 +601,10 @@ def decode_runs(args, abi, torch, stream):
         log(f"decode batch {batch}, context 2048")
         dec.append(decode_bench(abi, torch, stream, batch, 2048, args.decode_steps,
                                 lambda b, s: DeviceLlama(LLAMA3_8B, weights, max_batch=b, max_seq=s), LLAMA3_8B))
+    host = host_weights(torch, weights) if keep_host else None
     del weights
     torch.cuda.empty_cache()
-    return dec
+    return (dec, host) if keep_host else dec
 
 
 # GGUF Q4_K_M layout of a Llama-3-8B file: Q4_K projections and embedding,
@@ -649,6 +744,9 @@ def main() -> None:
             print(json.dumps({"attention": attention_bench(abi, torch, stream)}), flush=True)
         elif args.step_only:
             print(json.dumps({"registered_step": registered_step_runs(args, abi, torch, stream)}), flush=True)
+        elif args.stream_ceiling:
+            wgs = (args.ceiling_workgroups,) if args.ceiling_workgroups > 0 else (256, 512, 1024, 2048, 4096, 8192)
+            print(json.dumps({"stream_ceiling": stream_ceiling(abi, torch, stream, wgs=wgs)}), flush=True)
         elif args.gguf_decode_only:
             print(json.dumps({"decode_gguf_q4_k_m": gguf_decode_runs(args, abi, torch, stream)}), flush=True)
         else:
@@ -660,8 +758,9 @@ def run(args, abi, torch, stream) -> None:
     copies = args.copies or max(2, -(-512_000_000 // step_bytes))
     log(f"building {copies} NF4 MLP weight copies ({copies * step_bytes / 1e6:.0f} MB)")
     mats = make_mlp_copies(abi, torch, copies)
-    log(f"timing {args.steps} steps after {args.warmup} warmup")
-    ms = time_mlp(abi, torch, stream, mats, args.steps, args.warmup)
+    log(f"timing {args.steps} steps after >= {args.clock_warmup_ms:.0f} ms of clock warm-up and {args.warmup} "
+        "warmup steps")
+    ms, clock_ms, clock_steps = time_mlp(abi, torch, stream, mats, args.steps, args.warmup, args.clock_warmup_ms)
     launches = 3 * args.steps
     per_launch_ms = ms / launches
     gbs = step_bytes * args.steps / (ms / 1e3) / 1e9
@@ -669,6 +768,8 @@ def run(args, abi, torch, stream) -> None:
     achieved = per_launch_bytes / (per_launch_ms / 1e3) / 1e9
     del mats
     torch.cuda.empty_cache()
+    log("stream ceiling: plain reads of the same 33 MB")
+    ceiling = stream_ceiling(abi, torch, stream)
 
     result = {
         "metric": "NF4 matvec HBM GB/s (% peak) + Llama-3-8B-shape NF4 decode tokens/s, 1 GPU",
@@ -677,6 +778,8 @@ def run(args, abi, torch, stream) -> None:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_warmup_ms": round(clock_ms, 1),
+        "clock_warmup_steps": clock_steps,
         "ms_per_step": round(ms / args.steps, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -692,29 +795,35 @@ def run(args, abi, torch, stream) -> None:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_record(KERNEL),
                      "kernel": KERNEL, "bytes_per_launch": per_launch_bytes,
-                     "avg_launch_us": round(per_launch_ms * 1e3, 3)},
+                     "avg_launch_us": round(per_launch_ms * 1e3, 3),
+                     "stream_ceiling_us": ceiling["us"], "stream_ceiling_frac": ceiling["frac"]},
     }
-
+    tail = {}
     if not args.no_extra:
         log("small-M NF4 GEMM (M = 1, 4, 16, 64)")
-        result["small_m_gemm"] = small_m_bench(abi, torch, stream)
+        tail["small_m_gemm"] = small_m_bench(abi, torch, stream)
         log("GQA decode attention")
-        result["attention"] = attention_bench(abi, torch, stream)
+        tail["attention"] = attention_bench(abi, torch, stream)
         log("GGUF Q4_0 / Q8_0 matvec (M = 1, 8)")
-        result["gguf_q4_0_q8_0"] = gguf_q_bench(abi, torch, stream)
+        tail["gguf_q4_0_q8_0"] = gguf_q_bench(abi, torch, stream)
         log("GGUF K-quant matvec (Q4_K, Q6_K; M = 1, 4, 8)")
         result["gguf_kquant"] = kquant_bench(abi, torch, stream)
         log("prefill attention (T = S = 512, 2048, 8192)")
         result["prefill_attention"] = prefill_bench(abi, torch, stream)
 
+    llama_host = None
     if not args.no_decode:
-        result["decode"] = decode_runs(args, abi, torch, stream)
+        result["decode"], llama_host = decode_runs(args, abi, torch, stream, keep_host=not args.no_cpu)
         result["decode_gguf_q4_k_m"] = gguf_decode_runs(args, abi, torch, stream)
         result["registered_step"] = registered_step_runs(args, abi, torch, stream)
 
+    result["stream_ceiling"] = {k: ceiling[k] for k in ("bytes_per_launch", "best_workgroups", "us", "GBs", "frac")}
     if not args.no_cpu:
         log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, llama_host)
+    del llama_host
+    # The configs[0], [1] and [3] figures close the line.
+    result.update(tail)
     print(json.dumps(result), flush=True)
 
 

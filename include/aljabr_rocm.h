@@ -105,6 +105,11 @@ int aljabr_rocm_synchronize(void);
  * while the stream is being captured). No counterpart in the reference: a
  * diagnostic for callers that capture or budget device memory. */
 int aljabr_rocm_stream_scratch_bytes(size_t *bytes);
+/* Reads `bytes` (a multiple of 16) of device memory at `src` once, with
+ * `workgroups` workgroups of 256 lanes, and writes nothing to `sink` in
+ * practice (one 4-byte word at most). No counterpart in the reference: the
+ * plain streaming read the batch-1 matvec kernels are measured against. */
+int aljabr_rocm_stream_read_probe(const void *src, size_t bytes, void *sink, int workgroups);
 
 /* Device allocation backing RocmDeviceStorage; the final TensorStorage.release()
  * maps to aljabr_rocm_free (plugins/ml/aljabr-tensor/.../memory/TensorStorage.java:21-41). */
