@@ -769,11 +769,57 @@ __global__ __launch_bounds__(256) void nf4_xpack_kernel(const float *x, u32x4v *
         u32x4v{pack_half2(lo4.x, lo4.y), pack_half2(lo4.z, lo4.w), pack_half2(hi4.x, hi4.y), pack_half2(hi4.z, hi4.w)};
 }
 
-template <int MT, int NB>
+// A 16-byte global load whose completion the compiler does not track: the
+// caller waits for it with an explicit vmcnt and passes the value through
+// settle() before any use.
+__device__ __forceinline__ u32x4v gload_untracked(const u32x4v *p) {
+    u32x4v v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+// After the explicit wait: ties the loaded registers to this point, so no
+// instruction reads them earlier.
+__device__ __forceinline__ void settle(u32x4v &v) { asm volatile("" : "+v"(v)); }
+
+// The tile's 16 x MT*16 partial sums of the 8 waves through LDS at `rb`,
+// summed in wave order and written to the slice partials or the outputs.
+// Lane l of wave w stored accumulator mt at ((w*MT + mt)*64 + l)*16.
+template <int MT>
+__device__ __forceinline__ void gemm_tile_out(const GemmArgs &a, uint32_t rb, int tile, int tid) {
+    const GemmTile tr = gemm_tile(a, tile * 16);
+#pragma unroll
+    for (int o0 = 0; o0 < 256 * MT; o0 += kGemmThreads) {
+        const int o = o0 + tid;
+        if (256 * MT % kGemmThreads != 0 && o >= 256 * MT) break;
+        const int mt = o >> 8, lq = (o >> 2) & 63, r = o & 3;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kGemmWaves; ++w) v += __uint_as_float(*lds<lds_u32>(rb + (w * MT * 64 * 4 + o) * 4));
+        const int token = 16 * mt + 4 * (lq >> 4) + r, n = lq & 15, local = tr.local0 + n;
+        if (token < a.M && local < tr.n) {
+            typedef float __attribute__((address_space(1))) gf32;
+            if (a.part != nullptr) {
+                *(gf32 *)(a.part + (static_cast<size_t>(blockIdx.x) * a.M + token) * a.N + tile * 16 + n) = v;
+            } else {
+                gf32 *yp = (gf32 *)(tr.y + static_cast<size_t>(token) * tr.n + local);
+                *yp = a.add ? *yp + v : v;
+            }
+        }
+    }
+}
+
+// RT == 0: the waves' partial tiles meet in LDS after every tile (two
+// buffers, one barrier per tile). RT > 0 (the host guarantees that a
+// workgroup walks at most RT tiles): each wave keeps its partial tiles in
+// registers and they meet once, after the last tile, in the LDS the table and
+// the ring no longer need; the waves then run the whole loop without a
+// barrier.
+template <int MT, int NB, int RT>
 __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
     constexpr int KS = 64 * NB;
     using GL = GemmLds<MT, NB>;
     constexpr int D = GL::D;
+    static_assert(RT == 0 || RT * kGemmWaves * MT * 1024 <= GL::kBytes, "final reduction fits the LDS");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -783,38 +829,43 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
     const int last = a.tiles - 1;
     const uint32_t ring = GL::kRingOff + wave * D * GL::kSlot;
 
-    // The first D tiles' weight loads go out first, then the wave's A
-    // fragments: 16-byte loads of the fragment image, 1 KiB contiguous per
-    // instruction (hi part, lo part 1 KiB on).
+    // The wave's A fragments first (16-byte loads of the fragment image,
+    // 1 KiB contiguous per instruction; block b of token tile mt as two
+    // pieces), then the first D tiles' weight loads: the fragments arrive
+    // first and the loop starts while the tiles are still in flight.
     int tile = blockIdx.y;
-#pragma unroll
-    for (int d = 0; d < D; ++d) gemm_dma<NB>(a, min(tile + d * stride, last), kw, ring + d * GL::kSlot, lane);
-    // A operands: block b of token tile mt as four fragments, one per
-    // pair of code bytes (element pairs duplicated: x0 x1 x0 x1 x2 x3 x2 x3).
-    half8 ax[MT][NB][4];
-    {
-        const int kbs = a.K >> 6;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int b = 0; b < NB; ++b)
-#pragma unroll
-                for (int jj = 0; jj < 2; ++jj) {
-                    const u32x4v v =
-                        gload<u32x4v>(a.xp + (static_cast<size_t>(mt * kbs + (kw >> 6) + b) * 2 + jj) * 64 + lane);
-                    ax[mt][b][2 * jj] = __builtin_bit_cast(half8, u32x4v{v.x, v.x, v.y, v.y});
-                    ax[mt][b][2 * jj + 1] = __builtin_bit_cast(half8, u32x4v{v.z, v.z, v.w, v.w});
-                }
-    }
-    build_table_hr(tid);
-    // The fragments are consumed here, before the loop: the loop's own waits
-    // (explicit vmcnt for the LDS-DMA loads, which the compiler does not
-    // count) then never include one for them.
+    const int kbs = a.K >> 6;
+    u32x4v raw[MT][NB][2];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) asm volatile("" ::"v"(ax[mt][b][0]), "v"(ax[mt][b][1]), "v"(ax[mt][b][2]),
-                                                  "v"(ax[mt][b][3]));
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+                raw[mt][b][jj] = gload_untracked(a.xp + (static_cast<size_t>(mt * kbs + (kw >> 6) + b) * 2 + jj) * 64 + lane);
+#pragma unroll
+    for (int d = 0; d < D; ++d) gemm_dma<NB>(a, min(tile + d * stride, last), kw, ring + d * GL::kSlot, lane);
+    build_table_hr(tid);
+    wait_vmcnt<D * GL::kDma>();                  // the A fragment loads (issued first) have landed
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) settle(raw[mt][b][jj]);
+    // Element pairs duplicated: x0 x1 x0 x1 x2 x3 x2 x3 against H0 H1 R0 R1
+    // H2 H3 R2 R3.
+    half8 ax[MT][NB][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const u32x4v v = raw[mt][b][jj];
+                ax[mt][b][2 * jj] = __builtin_bit_cast(half8, u32x4v{v.x, v.x, v.y, v.y});
+                ax[mt][b][2 * jj + 1] = __builtin_bit_cast(half8, u32x4v{v.z, v.z, v.w, v.w});
+            }
     lds_barrier();                               // the table
 
     const uint32_t ch = static_cast<uint32_t>(lane & 31) * 8;
@@ -824,6 +875,8 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
     const uint32_t soff = GL::kCodeBytes + 4 * NB * i16;
     int slot = 0;
     int buf = 0;
+    f32x4m keep[RT > 0 ? RT : 1][MT];
+    int nt = 0;
     for (;;) {
         const uint32_t sb = ring + slot * GL::kSlot;
         wait_vmcnt<(D - 1) * GL::kDma>();        // this tile's DMA loads have landed
@@ -899,40 +952,46 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
             acc[mt].w = fmaf(sc[NB - 1], f[mt].w, acc[mt].w);
         }
 
-        // The waves' partial tiles through LDS, summed in wave order: lane l
-        // of wave w stores its 4 accumulators of token tile mt as one 16-byte
-        // piece at ((w*MT + mt)*64 + l)*16; thread o reads piece o/4, element
-        // o%4 of every wave (consecutive threads, consecutive addresses).
-        const uint32_t rb = GL::kRedOff + buf * GL::kRedBuf;
+        if constexpr (RT > 0) {
+            // Kept in registers (the index is uniform and unrolled).
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) *lds<lds_f32x4m>(rb + ((wave * MT + mt) * 64 + lane) * 16) = acc[mt];
-        lds_barrier();
-        const GemmTile tr = gemm_tile(a, tile * 16);
+            for (int t = 0; t < RT; ++t)
+                if (t == nt)
 #pragma unroll
-        for (int o0 = 0; o0 < 256 * MT; o0 += kGemmThreads) {
-            const int o = o0 + tid;
-            if (256 * MT % kGemmThreads != 0 && o >= 256 * MT) break;
-            const int mt = o >> 8, lq = (o >> 2) & 63, r = o & 3;
-            float v = 0.0f;
+                    for (int mt = 0; mt < MT; ++mt) keep[t][mt] = acc[mt];
+            ++nt;
+        } else {
+            // The waves' partial tiles through LDS, summed in wave order:
+            // lane l of wave w stores its 4 accumulators of token tile mt as
+            // one 16-byte piece at ((w*MT + mt)*64 + l)*16; thread o reads
+            // piece o/4, element o%4 of every wave (consecutive threads,
+            // consecutive addresses).
+            const uint32_t rb = GL::kRedOff + buf * GL::kRedBuf;
 #pragma unroll
-            for (int w = 0; w < kGemmWaves; ++w) v += __uint_as_float(*lds<lds_u32>(rb + (w * MT * 64 * 4 + o) * 4));
-            const int token = 16 * mt + 4 * (lq >> 4) + r, n = lq & 15, local = tr.local0 + n;
-            if (token < a.M && local < tr.n) {
-                typedef float __attribute__((address_space(1))) gf32;
-                if (a.part != nullptr) {
-                    *(gf32 *)(a.part + (static_cast<size_t>(blockIdx.x) * a.M + token) * a.N + tile * 16 + n) = v;
-                } else {
-                    gf32 *yp = (gf32 *)(tr.y + static_cast<size_t>(token) * tr.n + local);
-                    *yp = a.add ? *yp + v : v;
-                }
-            }
+            for (int mt = 0; mt < MT; ++mt) *lds<lds_f32x4m>(rb + ((wave * MT + mt) * 64 + lane) * 16) = acc[mt];
+            lds_barrier();
+            gemm_tile_out<MT>(a, rb, tile, tid);
         }
         buf ^= 1;
         slot = slot + 1 == D ? 0 : slot + 1;
         tile += stride;
         if (tile > last) break;
     }
-    wait_vmcnt<0>();                             // no LDS-DMA write may land after the wave ends
+    wait_vmcnt<0>();                             // no LDS-DMA write may land after the wave ends (or in the reduction)
+    if constexpr (RT > 0) {
+        // Every wave is past its last table read and ring slot: the whole
+        // LDS holds tile t's partials at t * 8 * MT KiB.
+        lds_barrier();
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+            if (t < nt)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    *lds<lds_f32x4m>(t * (kGemmWaves * MT * 1024) + ((wave * MT + mt) * 64 + lane) * 16) = keep[t][mt];
+        lds_barrier();
+        for (int t = 0; t < nt; ++t)
+            gemm_tile_out<MT>(a, t * (kGemmWaves * MT * 1024), blockIdx.y + t * stride, tid);
+    }
 }
 
 }  // namespace
@@ -1015,23 +1074,32 @@ int nf4_gemm_pass(const RowsOut *outs, int nseg, const float *A, int K, int M, b
         hipLaunchKernelGGL(nf4_xpack_kernel, dim3((total + 255) / 256), dim3(256), 0, s, A,
                            reinterpret_cast<u32x4v *>(buf + xoff), M, K, total);
     }
+    // Partial tiles kept in registers to the end when a workgroup walks at
+    // most RT tiles and the RT x MT accumulators fit beside the fragments
+    // (RT = 4, or 8 for MT = 1 with NB <= 4; MT = 2 only with NB = 2), else
+    // summed after every tile.
+    const int per = (args.tiles + groups - 1) / groups;
+    const int rt = mt == 1 ? (per <= 4 ? 4 : per <= 8 && nb <= 4 ? 8 : 0) : mt == 2 && nb == 2 && per <= 4 ? 4 : 0;
     const void *fn = nullptr;
     uint32_t lds_bytes = 0;
-#define ALJ_GEMM_CASE(MT_, NB_)                                                          \
-    if (mt == MT_ && nb == NB_) {                                                        \
-        fn = reinterpret_cast<const void *>(nf4_gemm_kernel<MT_, NB_>);                  \
+#define ALJ_GEMM_CASE(MT_, NB_, RT_)                                                     \
+    if (mt == MT_ && nb == NB_ && rt == RT_) {                                           \
+        fn = reinterpret_cast<const void *>(nf4_gemm_kernel<MT_, NB_, RT_>);             \
         lds_bytes = GemmLds<MT_, NB_>::kBytes;                                           \
     }
-    ALJ_GEMM_CASE(1, 2) ALJ_GEMM_CASE(1, 4) ALJ_GEMM_CASE(1, 8)
-    ALJ_GEMM_CASE(2, 2) ALJ_GEMM_CASE(2, 4)
-    ALJ_GEMM_CASE(3, 2)
-    ALJ_GEMM_CASE(4, 2)
+    ALJ_GEMM_CASE(1, 2, 0) ALJ_GEMM_CASE(1, 4, 0) ALJ_GEMM_CASE(1, 8, 0)
+    ALJ_GEMM_CASE(1, 2, 4) ALJ_GEMM_CASE(1, 4, 4) ALJ_GEMM_CASE(1, 8, 4)
+    ALJ_GEMM_CASE(1, 2, 8) ALJ_GEMM_CASE(1, 4, 8)
+    ALJ_GEMM_CASE(2, 2, 0) ALJ_GEMM_CASE(2, 4, 0)
+    ALJ_GEMM_CASE(2, 2, 4)
+    ALJ_GEMM_CASE(3, 2, 0)
+    ALJ_GEMM_CASE(4, 2, 0)
 #undef ALJ_GEMM_CASE
     if (!fn) return ALJABR_ROCM_ERR_UNSUPPORTED;
-    static std::atomic<bool> lds_set[5][9];      // per (MT, NB): the attribute is per kernel, per process
-    if (!lds_set[mt][nb].load(std::memory_order_acquire)) {
+    static std::atomic<bool> lds_set[5][9][9];   // per (MT, NB, RT): the attribute is per kernel, per process
+    if (!lds_set[mt][nb][rt].load(std::memory_order_acquire)) {
         (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_bytes));
-        lds_set[mt][nb].store(true, std::memory_order_release);
+        lds_set[mt][nb][rt].store(true, std::memory_order_release);
     }
     void *kargs[] = {&args};
     hipError_t e = hipLaunchKernel(fn, grid, dim3(kGemmThreads), kargs, lds_bytes, s);

@@ -65,6 +65,8 @@ def parse() -> argparse.Namespace:
                     help="run only the GGUF Q4_0/Q8_0 and K-quant matvec/GEMM measurements (for profiling)")
     ap.add_argument("--small-m-only", action="store_true",
                     help="run only the NF4 small-M GEMM measurement (for profiling)")
+    ap.add_argument("--small-m", type=str, default="1,4,16,32,64",
+                    help="with --small-m-only: the token counts M to time (comma-separated)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill attention measurement (for profiling)")
     ap.add_argument("--attention-only", action="store_true",
@@ -218,7 +220,7 @@ def cpu_baseline(seconds: float, llama_host=None):
             "decode_llama3_8b_nf4_b1": decode}
 
 
-def small_m_bench(abi, torch, stream, ms=(1, 4, 16, 64), launches=60):
+def small_m_bench(abi, torch, stream, ms=(1, 4, 16, 32, 64), launches=60):
     """NF4 small-M GEMM at the MLP shapes, M tokens per
     launch (M <= 4 on the rows kernel in fp32, M >= 5 on the matrix cores),
     and configs[0]'s 4096x4096 matvec at M = 1. Weights rotate over >= 512 MB.
@@ -737,7 +739,8 @@ def main() -> None:
             print(json.dumps({"gguf_q4_0_q8_0": gguf_q_bench(abi, torch, stream),
                               "gguf_kquant": kquant_bench(abi, torch, stream)}), flush=True)
         elif args.small_m_only:
-            print(json.dumps({"small_m_gemm": small_m_bench(abi, torch, stream)}), flush=True)
+            ms = tuple(int(v) for v in args.small_m.split(","))
+            print(json.dumps({"small_m_gemm": small_m_bench(abi, torch, stream, ms=ms)}), flush=True)
         elif args.prefill_only:
             print(json.dumps({"prefill_attention": prefill_bench(abi, torch, stream)}), flush=True)
         elif args.attention_only:
@@ -800,7 +803,7 @@ def run(args, abi, torch, stream) -> None:
     }
     tail = {}
     if not args.no_extra:
-        log("small-M NF4 GEMM (M = 1, 4, 16, 64)")
+        log("small-M NF4 GEMM (M = 1, 4, 16, 32, 64)")
         tail["small_m_gemm"] = small_m_bench(abi, torch, stream)
         log("GQA decode attention")
         tail["attention"] = attention_bench(abi, torch, stream)
