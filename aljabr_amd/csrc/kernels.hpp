@@ -212,6 +212,14 @@ int enqueue_nf4_mfma_multi(const RowsOut *outs, int nseg, const float *A, int K,
                            const uint16_t *xpacked = nullptr);
 // Bytes of the fp16 A image for M <= 64 tokens over K (K % 64 == 0).
 size_t nf4_xpack_bytes(int M, int K);
+// GGUF Q4_0 / Q8_0 GEMM pass of M <= 16 tokens with the activations held in
+// registers (K % 2048 == 0, A 16-byte aligned; up to three stacked matrices
+// of one type, all but the last a multiple of 16 rows; fp32-accurate,
+// deterministic). With several K slices or a tail the partial sums go to
+// `part` (K / 2048 * M * (stacked rows) floats suffice) or the stream's
+// scratch. ALJABR_ROCM_ERR_UNSUPPORTED when the shape does not fit.
+int gguf_gemm_pass(const RowsOut *outs, int nseg, const float *A, int K, int type, int M, bool add, float *part,
+                   size_t part_floats, const SliceTail *tail);
 // Floats of `part` enqueue_nf4_mfma_multi needs for M tokens over N stacked
 // rows and K (every pass, with or without a tail, xpacked null).
 size_t nf4_mfma_scratch_floats(int M, int N, int K);

@@ -627,6 +627,13 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
     const int rc = kq_multi_args(outs, nseg, A, K, type, M, args);
     if (rc != ALJABR_ROCM_OK) return rc;
     if (tail && (accumulate || K < 1024)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    if (type == ALJABR_ROCM_TYPE_Q4_0 || type == ALJABR_ROCM_TYPE_Q8_0) {
+        // The activation-stationary kernel where the shape fits it.
+        RowsOut o[3];
+        for (int i = 0; i < nseg; ++i) o[i] = RowsOut{outs[i].y, outs[i].w, nullptr, outs[i].n};
+        const int r = gguf_gemm_pass(o, nseg, A, K, type, M, accumulate, part, part_floats, tail);
+        if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
+    }
     hipStream_t s = current_stream();
     const int ks = kq_slice(args.N, K);
     const int slices = K / ks;

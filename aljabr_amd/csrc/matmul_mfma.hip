@@ -665,6 +665,22 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
+// Waits until at most min(n, J) tiles of KD vector-memory loads each are
+// still in flight (n uniform): the tiles issued after the awaited one, fewer
+// than the ring depth near the end of a workgroup's walk, where no load is
+// issued past its last tile.
+template <int KD, int J>
+__device__ __forceinline__ void wait_tiles(int n) {
+    if constexpr (J == 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (n >= J)
+            wait_vmcnt<J * KD>();
+        else
+            wait_tiles<KD, J - 1>(n);
+    }
+}
+
 // LDS-DMA loads (global_load_lds: 16 or 4 bytes per lane, landing at
 // `lds_base` + size * lane). Written as inline assembly: the compiler models
 // the builtin like a FLAT access that also counts on the LDS counter and
@@ -834,6 +850,7 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
     // pieces), then the first D tiles' weight loads: the fragments arrive
     // first and the loop starts while the tiles are still in flight.
     int tile = blockIdx.y;
+    int left = (last - tile) / stride;           // tiles of the walk after the current one
     const int kbs = a.K >> 6;
     u32x4v raw[MT][NB][2];
 #pragma unroll
@@ -844,9 +861,10 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
             for (int jj = 0; jj < 2; ++jj)
                 raw[mt][b][jj] = gload_untracked(a.xp + (static_cast<size_t>(mt * kbs + (kw >> 6) + b) * 2 + jj) * 64 + lane);
 #pragma unroll
-    for (int d = 0; d < D; ++d) gemm_dma<NB>(a, min(tile + d * stride, last), kw, ring + d * GL::kSlot, lane);
+    for (int d = 0; d < D; ++d)
+        if (d <= left) gemm_dma<NB>(a, tile + d * stride, kw, ring + d * GL::kSlot, lane);
     build_table_hr(tid);
-    wait_vmcnt<D * GL::kDma>();                  // the A fragment loads (issued first) have landed
+    wait_tiles<GL::kDma, D>(left + 1);           // the A fragment loads (issued first) have landed
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -879,7 +897,7 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
     int nt = 0;
     for (;;) {
         const uint32_t sb = ring + slot * GL::kSlot;
-        wait_vmcnt<(D - 1) * GL::kDma>();        // this tile's DMA loads have landed
+        wait_tiles<GL::kDma, D - 1>(left);       // this tile's DMA loads have landed
         u32x2m q[NB];
         float sc[NB];
 #pragma unroll
@@ -895,7 +913,7 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
             }
         }
         wait_lgkmcnt0();                         // the slot is read: refill it D tiles ahead
-        gemm_dma<NB>(a, min(tile + D * stride, last), kw, sb, lane);
+        if (left >= D) gemm_dma<NB>(a, tile + D * stride, kw, sb, lane);
 
         // Per block b: dwords 2b (.x) and 2b+1 (.y) of the codes, each decoded
         // by four table reads into two B fragments; the reads of dword d+2
@@ -975,7 +993,7 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
         buf ^= 1;
         slot = slot + 1 == D ? 0 : slot + 1;
         tile += stride;
-        if (tile > last) break;
+        if (--left < 0) break;
     }
     wait_vmcnt<0>();                             // no LDS-DMA write may land after the wave ends (or in the reduction)
     if constexpr (RT > 0) {
@@ -991,6 +1009,226 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
         lds_barrier();
         for (int t = 0; t < nt; ++t)
             gemm_tile_out<MT>(a, t * (kGemmWaves * MT * 1024), blockIdx.y + t * stride, tid);
+    }
+}
+
+// ---- GGUF Q4_0 / Q8_0 GEMM with the activations held in registers -------
+//
+// The NF4 GEMM's structure for the 32-element GGUF blocks (18-byte Q4_0 {fp16
+// d, 16 code bytes}, 34-byte Q8_0 {fp16 d, 32 int8}), passes of up to 16
+// tokens: wave w of K slice s owns the elements [(8s + w)*KB, +KB) (KB = 32 *
+// NBK, NBK a multiple of 8 so that a row's share starts 16-byte aligned) and
+// keeps that range of the 16 token rows as fp16 hi and lo A fragments (x = hi
+// + lo to 2^-22); each 16-row tile's share of the weights (16 rows x NBK
+// blocks) streams into the wave's LDS ring by LDS-DMA, one MFMA pair per
+// block (hi, then lo, against the same B) into a fresh 16 x 16 tile that the
+// block's d scales into the accumulators. B holds the block's codes as exact
+// fp16 integers (Q4_0: q - 8; Q8_0: q), built from the code bytes with v_perm
+// against a constant 0x64 byte and one packed fp16 add (no table), so the
+// result is the fp32 matvec to ~2^-22 per product. Partial tiles meet across
+// the waves as in the NF4 kernel.
+//
+// MFMA 16x16x32 per block: lane l = 16g + i supplies A[i][8g + e] (token i,
+// block elements 8g..8g+7) and B[8g + e][i] (row i). Q4_0 elements 0..15 are
+// the low nibbles of code bytes 0..15 and 16..31 the high nibbles, so lane
+// group g reads code bytes 8(g & 1) .. +7 and takes nibble g >> 1; Q8_0 lane
+// group g reads bytes 8g .. 8g+7.
+//
+// Slot image: the DMA instruction j, lane l loads 16-byte piece 4j + l/16 of
+// row l % 16's share, landing at 1024j + 16l: byte c of row r sits at
+// 256*(c/16) + 16r + c%16 (lanes past the share re-read its last piece into
+// the slot's tail).
+
+template <int F> struct GgFmt {                  // F: 0 = Q4_0, 1 = Q8_0
+    static constexpr int BB = F == 0 ? 18 : 34;
+};
+
+template <int F, int NBK>
+struct GgLds {
+    static constexpr int RB = NBK * GgFmt<F>::BB;                        // a row's share, bytes
+    static constexpr int PR = RB / 16;                                   // its 16-byte pieces
+    static constexpr int kDma = (PR + 3) / 4;                            // DMA instructions per tile
+    static constexpr uint32_t kSlot = kDma * 1024;
+    static constexpr uint32_t kRedBuf = kGemmWaves * 4 * 64 * 4;         // one token tile
+    static constexpr uint32_t kRedOff = 0;
+    static constexpr uint32_t kRingOff = 2 * kRedBuf;
+    static constexpr int kD = static_cast<int>((kGemmLdsMax - kRingOff) / (kGemmWaves * kSlot));
+    static constexpr int D = kD > 4 ? 4 : kD;
+    static constexpr uint32_t kBytes = kRingOff + kGemmWaves * D * kSlot;
+    static_assert(RB % 16 == 0 && D >= 2 && kBytes <= kGemmLdsMax, "ring of at least two tiles");
+};
+
+template <int F, int NBK>
+__device__ __forceinline__ void gg_dma(const GemmArgs &a, int tile, int kw, uint32_t slot, int lane) {
+    using GL = GgLds<F, NBK>;
+    const GemmTile tr = gemm_tile(a, tile * 16);
+    const int crow = min(tr.local0 + (lane & 15), tr.n - 1);
+    const uint8_t *rp = tr.w + static_cast<size_t>(crow) * (static_cast<size_t>(a.K >> 5) * GgFmt<F>::BB) +
+                        static_cast<size_t>(kw >> 5) * GgFmt<F>::BB;
+#pragma unroll
+    for (int j = 0; j < GL::kDma; ++j) {
+        const int p = 4 * j + (lane >> 4);
+        dma16(rp + 16 * (p < GL::PR ? p : GL::PR - 1), slot + 1024 * j);
+    }
+}
+
+// Dword of row r's share at byte c (c % 4 == 0) in the slot image.
+__device__ __forceinline__ uint32_t gg_word(uint32_t sb, int r, int c) {
+    return *lds<lds_u32>(sb + 256 * (c >> 4) + 16 * r + (c & 15));
+}
+
+// Halves 0x64bb of bytes 2t and 2t+1 of `w` (v_perm against a constant
+// 0x64 byte): 1024 + byte, exact.
+template <int T>
+__device__ __forceinline__ uint32_t gg_magic(uint32_t w) {
+    return __builtin_amdgcn_perm(0x64646464u, w, 0x04000400u | ((2u * T + 1u) << 16) | (2u * T));
+}
+__device__ __forceinline__ uint32_t gg_hadd(uint32_t v, uint32_t c) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v) + __builtin_bit_cast(h2, c));
+}
+
+template <int F, int NBK, int RT>
+__global__ __launch_bounds__(kGemmThreads) void gguf_gemm_kernel(GemmArgs a) {
+    constexpr int KB = 32 * NBK;
+    using GL = GgLds<F, NBK>;
+    constexpr int D = GL::D;
+    constexpr int BB = GgFmt<F>::BB;
+    static_assert(RT == 0 || RT * kGemmWaves * 1024 <= GL::kBytes, "final reduction fits the LDS");
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i16 = lane & 15, g = lane >> 4;
+    const int kw = (static_cast<int>(blockIdx.x) * kGemmWaves + wave) * KB;
+    const int stride = gridDim.y;
+    const int last = a.tiles - 1;
+    const uint32_t ring = GL::kRingOff + wave * D * GL::kSlot;
+
+    // The activations first (token i16, block elements 8g .. 8g+7 of each
+    // block: two 16-byte loads per block; lanes of rows past M load nothing
+    // and hold zeros), then the first D tiles' weights.
+    int tile = blockIdx.y;
+    int left = (last - tile) / stride;           // tiles of the walk after the current one
+    const bool live = i16 < a.M;
+    const float *xr = a.x + static_cast<size_t>(live ? i16 : 0) * a.K + kw + 8 * g;
+    u32x4v raw[NBK][2];
+#pragma unroll
+    for (int b = 0; b < NBK; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) raw[b][h] = u32x4v{0u, 0u, 0u, 0u};
+    if (live) {
+#pragma unroll
+        for (int b = 0; b < NBK; ++b)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) raw[b][h] = gload_untracked(reinterpret_cast<const u32x4v *>(xr + 32 * b + 4 * h));
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (d <= left) gg_dma<F, NBK>(a, tile + d * stride, kw, ring + d * GL::kSlot, lane);
+    wait_tiles<GL::kDma, D>(left + 1);           // the activation loads (issued first) have landed
+#pragma unroll
+    for (int b = 0; b < NBK; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) settle(raw[b][h]);
+    half8 ah[NBK], al[NBK];
+#pragma unroll
+    for (int b = 0; b < NBK; ++b) {
+        float v[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            v[4 * h + 0] = __uint_as_float(raw[b][h].x);
+            v[4 * h + 1] = __uint_as_float(raw[b][h].y);
+            v[4 * h + 2] = __uint_as_float(raw[b][h].z);
+            v[4 * h + 3] = __uint_as_float(raw[b][h].w);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const _Float16 hi = static_cast<_Float16>(v[e]);
+            ah[b][e] = hi;
+            al[b][e] = static_cast<_Float16>(v[e] - static_cast<float>(hi));
+        }
+    }
+
+    // Q4_0: nibble g >> 1 of code bytes 8(g & 1) ..; Q8_0: bytes 8g ..
+    const int cg = F == 0 ? 8 * (g & 1) : 8 * g;
+    const uint32_t nsh = F == 0 ? 4u * static_cast<uint32_t>(g >> 1) : 0u;
+    const uint32_t bias = F == 0 ? 0xE408E408u : 0xE480E480u;   // fp16 -1032 (Q4_0) / -1152 (Q8_0) pairs
+    int slot = 0;
+    int buf = 0;
+    f32x4m keep[RT > 0 ? RT : 1];
+    int nt = 0;
+    for (;;) {
+        const uint32_t sb = ring + slot * GL::kSlot;
+        wait_tiles<GL::kDma, D - 1>(left);       // this tile's DMA loads have landed
+        // The tile's code words and scales into registers, then the slot is
+        // refilled D tiles ahead.
+        uint32_t cw[NBK][2];
+        float dsc[NBK];
+#pragma unroll
+        for (int b = 0; b < NBK; ++b) {
+            const int c = BB * b + 2 + cg;       // c % 4 is (2b + 2) % 4 for both formats
+            if (((2 * b + 2) & 3) == 0) {
+                cw[b][0] = gg_word(sb, i16, c);
+                cw[b][1] = gg_word(sb, i16, c + 4);
+            } else {
+                const uint32_t w0 = gg_word(sb, i16, c - 2), w1 = gg_word(sb, i16, c + 2),
+                               w2 = gg_word(sb, i16, c + 6);
+                cw[b][0] = __builtin_amdgcn_alignbyte(w1, w0, 2);
+                cw[b][1] = __builtin_amdgcn_alignbyte(w2, w1, 2);
+            }
+            const uint32_t dw = gg_word(sb, i16, (BB * b) & ~3);
+            dsc[b] = f16_bits_to_f32((BB * b) & 2 ? dw >> 16 : dw & 0xffffu);
+        }
+        wait_lgkmcnt0();
+        if (left >= D) gg_dma<F, NBK>(a, tile + D * stride, kw, sb, lane);
+
+        f32x4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        const f32x4m z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int b = 0; b < NBK; ++b) {
+            uint32_t w0 = cw[b][0], w1 = cw[b][1];
+            if constexpr (F == 0) {
+                w0 = (w0 >> nsh) & 0x0f0f0f0fu;
+                w1 = (w1 >> nsh) & 0x0f0f0f0fu;
+            } else {
+                w0 ^= 0x80808080u;
+                w1 ^= 0x80808080u;
+            }
+            const u32x4v bq = {gg_hadd(gg_magic<0>(w0), bias), gg_hadd(gg_magic<1>(w0), bias),
+                               gg_hadd(gg_magic<0>(w1), bias), gg_hadd(gg_magic<1>(w1), bias)};
+            const half8 bf = __builtin_bit_cast(half8, bq);
+            f32x4m c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[b], bf, z4, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[b], bf, c, 0, 0, 0);
+            acc.x = fmaf(dsc[b], c.x, acc.x);
+            acc.y = fmaf(dsc[b], c.y, acc.y);
+            acc.z = fmaf(dsc[b], c.z, acc.z);
+            acc.w = fmaf(dsc[b], c.w, acc.w);
+        }
+
+        if constexpr (RT > 0) {
+#pragma unroll
+            for (int t = 0; t < RT; ++t)
+                if (t == nt) keep[t] = acc;
+            ++nt;
+        } else {
+            const uint32_t rb = GL::kRedOff + buf * GL::kRedBuf;
+            *lds<lds_f32x4m>(rb + (wave * 64 + lane) * 16) = acc;
+            lds_barrier();
+            gemm_tile_out<1>(a, rb, tile, tid);
+        }
+        buf ^= 1;
+        slot = slot + 1 == D ? 0 : slot + 1;
+        tile += stride;
+        if (--left < 0) break;
+    }
+    wait_vmcnt<0>();                             // no LDS-DMA write may land after the wave ends (or in the reduction)
+    if constexpr (RT > 0) {
+        lds_barrier();
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+            if (t < nt) *lds<lds_f32x4m>(t * (kGemmWaves * 1024) + (wave * 64 + lane) * 16) = keep[t];
+        lds_barrier();
+        for (int t = 0; t < nt; ++t) gemm_tile_out<1>(a, t * (kGemmWaves * 1024), blockIdx.y + t * stride, tid);
     }
 }
 
@@ -1104,6 +1342,85 @@ int nf4_gemm_pass(const RowsOut *outs, int nseg, const float *A, int K, int M, b
     void *kargs[] = {&args};
     hipError_t e = hipLaunchKernel(fn, grid, dim3(kGemmThreads), kargs, lds_bytes, s);
     if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "nf4 gemm launch: %s", hipGetErrorString(e));
+    if (tail) return enqueue_slice_tail(*tail, args.part, slices, M, args.N);
+    if (slices > 1) return enqueue_slice_sum(args.y, args.end, nseg, M, args.N, args.part, slices, add);
+    return ALJABR_ROCM_OK;
+}
+
+// GGUF Q4_0 / Q8_0 pass of M <= 16 tokens on gguf_gemm_kernel: K slices of
+// 8 waves x 512 elements (Q4_0, K % 4096 == 0) or x 256 (K % 2048 == 0), the
+// workgroups of a slice walking every groups-th 16-row tile; one slice
+// writes (or adds into) the outputs, several store partials for the slice
+// sum or the tail. UNSUPPORTED when the shape does not fit.
+int gguf_gemm_pass(const RowsOut *outs, int nseg, const float *A, int K, int type, int M, bool add, float *part,
+                   size_t part_floats, const SliceTail *tail) {
+    if ((type != ALJABR_ROCM_TYPE_Q4_0 && type != ALJABR_ROCM_TYPE_Q8_0) || M < 1 || M > 16 || nseg < 1 ||
+        nseg > 3 || !aligned(A, 16))
+        return ALJABR_ROCM_ERR_UNSUPPORTED;
+    // Q8_0's 34-byte blocks leave no registers for 16 blocks a wave.
+    const int nbk = K % 4096 == 0 && type == ALJABR_ROCM_TYPE_Q4_0 ? 16 : K % 2048 == 0 ? 8 : 0;
+    if (nbk == 0) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    GemmArgs args{};
+    long long end = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (i < nseg) {
+            const RowsOut &o = outs[i];
+            if (o.n <= 0 || (i < nseg - 1 && o.n % 16 != 0)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            end += o.n;
+            if (end > 0x7fff0000LL) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            args.y[i] = o.y;
+            args.w[i] = o.w;
+            args.end[i] = static_cast<int>(end);
+        } else {
+            args.end[i] = 0x7fffffff;
+        }
+    }
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const int slices = K / (8 * 32 * nbk);
+    const int tiles = static_cast<int>((end + 15) / 16);
+    int gr = cus / slices;
+    if (gr < 1) gr = 1;
+    if (gr > tiles) gr = tiles;
+    const int per = (tiles + gr - 1) / gr;
+    const int groups = (tiles + per - 1) / per;
+    // A walk of one or two tiles pays the activation loads and the wave
+    // reduction for too few weight bytes: the LDS-staged kernel does better.
+    if (per < 3 || groups > 65535) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    args.nseg = nseg;
+    args.x = A;
+    args.M = M;
+    args.N = static_cast<int>(end);
+    args.K = K;
+    args.tiles = tiles;
+    args.add = slices == 1 && add && !tail;
+    const size_t pfl = slices > 1 || tail ? static_cast<size_t>(slices) * M * args.N : 0;
+    float *buf = !pfl ? nullptr
+                 : part && pfl <= part_floats ? part
+                                              : static_cast<float *>(stream_scratch(pfl * sizeof(float), kScratchPartials));
+    if (pfl && !buf) return ALJABR_ROCM_ERR_BUFFER;
+    args.part = buf;
+    const int rt = per <= 4 ? 4 : per <= 8 && nbk == 8 ? 8 : 0;
+    const int f = type == ALJABR_ROCM_TYPE_Q4_0 ? 0 : 1;
+    const void *fn = nullptr;
+    uint32_t lds_bytes = 0;
+#define ALJ_GG_CASE(F_, NBK_, RT_)                                                       \
+    if (f == F_ && nbk == NBK_ && rt == RT_) {                                           \
+        fn = reinterpret_cast<const void *>(gguf_gemm_kernel<F_, NBK_, RT_>);            \
+        lds_bytes = GgLds<F_, NBK_>::kBytes;                                             \
+    }
+    ALJ_GG_CASE(0, 16, 0) ALJ_GG_CASE(0, 16, 4) ALJ_GG_CASE(0, 8, 0) ALJ_GG_CASE(0, 8, 4) ALJ_GG_CASE(0, 8, 8)
+    ALJ_GG_CASE(1, 8, 0) ALJ_GG_CASE(1, 8, 4) ALJ_GG_CASE(1, 8, 8)
+#undef ALJ_GG_CASE
+    if (!fn) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    static std::atomic<bool> lds_set[2][17][9];  // per (format, NBK, RT): the attribute is per kernel, per process
+    if (!lds_set[f][nbk][rt].load(std::memory_order_acquire)) {
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_bytes));
+        lds_set[f][nbk][rt].store(true, std::memory_order_release);
+    }
+    void *kargs[] = {&args};
+    const hipError_t e = hipLaunchKernel(fn, dim3(static_cast<unsigned>(slices), static_cast<unsigned>(groups)),
+                                         dim3(kGemmThreads), kargs, lds_bytes, current_stream());
+    if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "gguf gemm launch: %s", hipGetErrorString(e));
     if (tail) return enqueue_slice_tail(*tail, args.part, slices, M, args.N);
     if (slices > 1) return enqueue_slice_sum(args.y, args.end, nseg, M, args.N, args.part, slices, add);
     return ALJABR_ROCM_OK;

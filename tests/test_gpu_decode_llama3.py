@@ -128,20 +128,26 @@ def test_llama3_width_decode_matches_oracle(rocm, dev, oracle, llama3_two_layers
 
 
 # GGUF Q4_K_M's mix: Q4_K everywhere but the V and down projections and the
-# output head (Q6_K).
-Q4_K_M = dict(tok_embed=12, wq=12, wk=12, wv=14, wo=12, w_gate=12, w_up=12, w_down=14, lm_head=14)
+# output head (Q6_K). The Q4_0 mix (Q8_0 V, down and head) runs the Q4_0 /
+# Q8_0 matrix-core GEMMs: stacked Q/K and gate/up (with the SwiGLU tail), the
+# 7-slice down projection with the residual tail.
+MIXES = {
+    "q4_k_m": dict(tok_embed=12, wq=12, wk=12, wv=14, wo=12, w_gate=12, w_up=12, w_down=14, lm_head=14),
+    "q4_0": dict(tok_embed=2, wq=2, wk=2, wv=8, wo=2, w_gate=2, w_up=2, w_down=8, lm_head=8),
+}
 
 
-@pytest.fixture(scope="module")
-def llama3_q4_k_m(rocm, oracle):
-    """Two Llama-3-8B-width layers of random K-quant super-blocks (the GGUF
-    test models' scales), as oracle weights and as device tensors."""
+@pytest.fixture(scope="module", params=sorted(MIXES))
+def llama3_q4_k_m(rocm, oracle, request):
+    """Two Llama-3-8B-width layers of random GGUF blocks (the GGUF test
+    models' scales) in one of the mixes, as oracle weights and as device
+    tensors."""
     import torch
     import gguf_writer as gw
     from aljabr_amd.llama import LLAMA3_8B
     cfg = dict(LLAMA3_8B, layers=2, max_seq=2112)
-    print("\n[llama3 width q4_k_m] drawing 2-layer weights", flush=True)
-    _, _, host = gw.llama_model(oracle, cfg, Q4_K_M, seed=9)
+    print(f"\n[llama3 width {request.param}] drawing 2-layer weights", flush=True)
+    _, _, host = gw.llama_model(oracle, cfg, MIXES[request.param], seed=9)
 
     def put(arr):
         return torch.from_numpy(np.ascontiguousarray(arr)).to("cuda:0")
@@ -159,8 +165,8 @@ def llama3_q4_k_m(rocm, oracle):
 
 
 def test_llama3_width_q4_k_m_decode_matches_oracle(rocm, dev, oracle, llama3_q4_k_m):
-    """The GGUF Q4_K_M mix at B = 32 (the K-quant matrix-core GEMMs with
-    their fused tails, two formats per Q/K/V launch) from prefilled caches at
+    """A GGUF mix at B = 32 (the quantized matrix-core GEMMs with their fused
+    tails; Q4_K_M's two formats per Q/K/V launch) from prefilled caches at
     positions 100, 161, ..., 1930 and 2047, two steps: hidden state and
     logits of every sequence within 1e-3 of the typed oracle."""
     import torch
@@ -176,7 +182,7 @@ def test_llama3_width_q4_k_m_decode_matches_oracle(rocm, dev, oracle, llama3_q4_
     logits = torch.empty(batch * cfg["vocab"], dtype=torch.float32, device="cuda:0")
     hid = torch.empty(batch * cfg["dim"], dtype=torch.float32, device="cuda:0")
     for step in range(2):
-        print(f"[llama3 width q4_k_m] step {step} positions {pos.min()}..{pos.max()}", flush=True)
+        print(f"[llama3 width gguf] step {step} positions {pos.min()}..{pos.max()}", flush=True)
         nxt = model.decode(dev.put(cur), dev.put(pos), batch, logits=logits)
         got_tok = dev.get(nxt)
         rocm.call("aljabr_rocm_memcpy_d2d", hid.data_ptr(), model.hidden_ptr(), batch * cfg["dim"] * 4)
