@@ -144,7 +144,7 @@ __device__ __forceinline__ void key_range(const AttnParams &p, int sk, int qi, i
 template <int D, int NTH>
 __device__ __forceinline__ void merge_row(const float *__restrict__ part_o, const float *__restrict__ part_ml,
                                           float *out_base, int splits, long long row, int Sq, int Hq, int q_sb,
-                                          int q_sh, int q_sq, float norm_eps, float *st) {
+                                          int q_sh, int q_sq, float norm_eps, float *st, uint16_t *xpack = nullptr) {
     constexpr int LPS = D / 4;          // lanes per split
     constexpr int SG = NTH / LPS;       // splits in flight
     const int qi = static_cast<int>(row % Sq);
@@ -211,7 +211,9 @@ __device__ __forceinline__ void merge_row(const float *__restrict__ part_o, cons
                 O = fmaf(st[g * (D + 2) + dd], w, O);
             }
         }
-        out[dd] = L == 0.0f ? 0.0f : O / (L + norm_eps);
+        const float val = L == 0.0f ? 0.0f : O / (L + norm_eps);
+        out[dd] = val;
+        if (xpack) xpack[xpack_index(bb, h * D + dd, Hq * D)] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(val));
     }
     __syncthreads();                    // `st` is free again
 }
@@ -222,9 +224,10 @@ __device__ __forceinline__ void merge_row(const float *__restrict__ part_o, cons
 template <int D>
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part_o,
                                                         const float *__restrict__ part_ml, float *out, int splits,
-                                                        int Sq, int Hq, int q_sb, int q_sh, int q_sq, float norm_eps) {
+                                                        int Sq, int Hq, int q_sb, int q_sh, int q_sq, float norm_eps,
+                                                        uint16_t *xpack) {
     __shared__ float st[(256 / (D / 4)) * (D + 2)];
-    merge_row<D, 256>(part_o, part_ml, out, splits, blockIdx.x, Sq, Hq, q_sb, q_sh, q_sq, norm_eps, st);
+    merge_row<D, 256>(part_o, part_ml, out, splits, blockIdx.x, Sq, Hq, q_sb, q_sh, q_sq, norm_eps, st, xpack);
 }
 
 // KT keys per group per trip (the tile): 4, or 2 where a workgroup's chunk
@@ -469,7 +472,10 @@ __global__ __launch_bounds__(WAVES * 64) void attn_split_kernel(const void *kcac
         const int h = kvh * G + g;
         const long long row = (static_cast<long long>(b) * p.Hq + h) * p.Sq + qi;
         if (splits == 1) {
-            p.out[b * p.q_sb + h * p.q_sh + qi * p.q_sq + dd] = L == 0.0f ? 0.0f : O / (L + p.norm_eps);
+            const float val = L == 0.0f ? 0.0f : O / (L + p.norm_eps);
+            p.out[b * p.q_sb + h * p.q_sh + qi * p.q_sq + dd] = val;
+            if (p.xpack)
+                p.xpack[xpack_index(b, h * D + dd, p.Hq * D)] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(val));
         } else {
             part_o[(row * splits + split) * D + dd] = O;
             if (dd == 0) {
@@ -583,7 +589,7 @@ int launch_split(const AttnParams &p, int splits, int chunk, float *part, hipStr
                            p.q, p.kv_len, p.cap, sq_hkv, chunk, qsb, qsh, qsq, p, splits, part_o, part_ml);
     if (splits > 1)
         hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, part_o,
-                           part_ml, p.out, splits, p.Sq, p.Hq, qsb, qsh, qsq, p.norm_eps);
+                           part_ml, p.out, splits, p.Sq, p.Hq, qsb, qsh, qsq, p.norm_eps, p.xpack);
     return ALJABR_ROCM_OK;
 }
 
@@ -634,6 +640,9 @@ int enqueue_attention(const AttnParams &p_in) {
                       p.q_sh % 4 == 0 && p.q_sb % 4 == 0 && p.Sq <= 0xffff && p.Hkv <= 0x7fff &&
                       p.q_sb <= 0x7fffffffLL && p.q_sh <= 0x7fffffffLL && p.q_sq <= 0x7fffffffLL &&
                       (p.block_table || p.cap == p.Sk);
+    if (p.xpack && (!fast || p.Sq != 1 || p.q_sh != p.D || p.q_sb != static_cast<long long>(p.Hq) * p.D ||
+                    (p.Hq * p.D) % 64 != 0 || !aligned(p.xpack, 16)))
+        return ALJABR_ROCM_ERR_UNSUPPORTED;
     if (!fast) {
         const long long n = static_cast<long long>(p.B) * p.Hq * p.Sq * p.D;
         const dim3 grid(static_cast<unsigned>((n + 63) / 64));

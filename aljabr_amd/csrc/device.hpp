@@ -189,6 +189,14 @@ __device__ __forceinline__ uint32_t funnel_shift_right(uint32_t hi, uint32_t lo,
     return __builtin_amdgcn_alignbit(hi, lo, shift);
 }
 
+// Index (in fp16 elements) of element (m, c) of an [M][K] activation in the
+// NF4 GEMM's fp16 A-fragment image: [m/16][c/64][(c%16)/8][lane
+// 16*((c%64)/16) + m%16][c%8] (matmul_mfma.hip, nf4_xpack_kernel).
+__device__ __forceinline__ size_t xpack_index(int m, int c, int K) {
+    const size_t entry = (static_cast<size_t>(m >> 4) * (K >> 6) + (c >> 6)) * 2 + ((c >> 3) & 1);
+    return (entry * 64 + 16 * ((c >> 4) & 3) + (m & 15)) * 8 + (c & 7);
+}
+
 // binary16 -> binary32 exactly as GgufQuantTables.f16ToF32Slow: integer-only,
 // so the result does not depend on the FP16 denormal mode; NaN -> 0x7FC00000.
 __device__ __forceinline__ float f16_bits_to_f32_exact(uint32_t h) {

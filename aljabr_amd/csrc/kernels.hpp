@@ -32,6 +32,10 @@ struct AttnParams {
     float *scratch;         // split partials: caller-owned (graph-safe) when it holds attention_scratch_bytes(),
     size_t scratch_bytes;   // else (null or too small) the stream's scratch
     int scratch_only;       // never use the stream's scratch: fewer splits when the partials would not fit
+    // With Sq == 1 and out as [B][Hq*D]: the output also as the NF4 GEMM's
+    // fp16 A image over K = Hq*D (rows past B untouched); enqueue_attention
+    // returns UNSUPPORTED, before any launch, where its kernels cannot write it.
+    uint16_t *xpack;
 };
 
 int enqueue_attention(const AttnParams &p);
@@ -252,7 +256,12 @@ int enqueue_gated_act(float *out, const float *gate, const float *up, long long 
 // else one launch each.
 int enqueue_matmul_multi(float *const *C, const float *A, const uint8_t *const *B, int K, const int *N,
                          const int *type, int n, int batch);
-int enqueue_argmax(int *out, const float *x, int rows, int cols);
+// Argmax of each row (ties to the lowest index, NaN never taken, 0 for a row
+// with nothing above -inf). With `part` of at least argmax_part_bytes(rows,
+// cols) bytes (8-byte aligned) it runs as chunk maxima plus a final pass (no
+// workgroup reads a whole wide row), else one workgroup per row.
+int enqueue_argmax(int *out, const float *x, int rows, int cols, void *part = nullptr, size_t part_bytes = 0);
+size_t argmax_part_bytes(int rows, int cols);
 int enqueue_embed(float *x, const float *embed, const int *tokens, int batch, int dim, int vocab);
 // x[b] = row tokens[b] of a [vocab][dim] table of type F32, F16, Q4_0, Q8_0,
 // Q4_K or Q6_K, decoded bit-exactly (dim a multiple of the type's block).

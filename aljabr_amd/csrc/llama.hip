@@ -78,6 +78,7 @@ struct aljabr_rocm_llama {
     // produce them (batches of 2..64): the next GEMM then skips its packing
     // launch. Null when the session has none.
     uint16_t *xb_pack = nullptr, *hb_pack = nullptr;
+    uint16_t *att_pack = nullptr;    // the attention output's A image, written by the attention kernels
     bool rows_fused = false;   // batch-1 layers as fused NF4 launches (shapes and alignment allow it)
     // Captured decode steps, by batch size (and the logits buffer they write).
     struct Graph {
@@ -270,11 +271,14 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
                 mm_floats = std::max(mm_floats, nf4_mfma_scratch_floats(b, shapes[i][0], shapes[i][1]));
         }
     }
-    // The A images of xb and hb for the NF4 GEMMs (batches of 2..64).
+    // The A images of xb, hb and the attention output for the NF4 GEMMs
+    // (batches of 2..64).
     const bool packs = m->all_nf4 && c.max_batch >= 2 && c.max_batch <= 64 && c.dim % 64 == 0 && c.ffn % 64 == 0;
-    const size_t pack_bytes = packs ? ((nf4_xpack_bytes(c.max_batch, c.dim) + 255) & ~size_t(255)) +
-                                          ((nf4_xpack_bytes(c.max_batch, c.ffn) + 255) & ~size_t(255))
-                                    : 0;
+    const bool att_packs = packs && qd % 64 == 0;
+    const size_t pack_bytes = (packs ? ((nf4_xpack_bytes(c.max_batch, c.dim) + 255) & ~size_t(255)) +
+                                           ((nf4_xpack_bytes(c.max_batch, c.ffn) + 255) & ~size_t(255))
+                                     : 0) +
+                              (att_packs ? (nf4_xpack_bytes(c.max_batch, static_cast<int>(qd)) + 255) & ~size_t(255) : 0);
     const size_t bytes = 2 * ((cache_elems * 2 + 255) & ~size_t(255)) +
                          ((mm_floats * 4 + 255) & ~size_t(255)) +
                          ((B * c.dim * 4 + 255) & ~size_t(255)) * 2 + ((B * qd * 4 + 255) & ~size_t(255)) * 2 +
@@ -317,6 +321,7 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
         m->xb_pack = carve<uint16_t>(cur, nf4_xpack_bytes(c.max_batch, c.dim) / 2);
         m->hb_pack = carve<uint16_t>(cur, nf4_xpack_bytes(c.max_batch, c.ffn) / 2);
     }
+    if (att_packs) m->att_pack = carve<uint16_t>(cur, nf4_xpack_bytes(c.max_batch, static_cast<int>(qd)) / 2);
     // The RoPE angles of every cache position, computed once: the decode
     // step then reads cos/sin instead of evaluating double pow/cos/sin.
     m->rope_cs = carve<float2>(cur, static_cast<size_t>(c.max_seq) * (c.head_dim / 2));
@@ -1140,7 +1145,16 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         ap.scratch = m->attn_scratch;
         ap.scratch_bytes = m->attn_scratch_bytes;
         ap.scratch_only = 1;
-        ALJ_TRY(enqueue_attention(ap));
+        // With the Wo GEMM tail ahead, the attention kernels also write the
+        // output's A image (no packing launch before the GEMM).
+        ap.xpack = tails && packs && !fused1 ? m->att_pack : nullptr;
+        rc = ap.xpack ? enqueue_attention(ap) : ALJABR_ROCM_ERR_UNSUPPORTED;
+        const bool att_packed = rc == ALJABR_ROCM_OK;
+        if (rc == ALJABR_ROCM_ERR_UNSUPPORTED) {
+            ap.xpack = nullptr;
+            rc = enqueue_attention(ap);
+        }
+        ALJ_TRY(rc);
         ALJ_MARK("attention", keys * nkv * hd * 2.0 * 2.0 + B * 2.0 * qd * f4);
         // x += Wo att.
         if (fused1) {
@@ -1165,7 +1179,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
                 t.xpack = packs ? m->xb_pack : nullptr;
                 const RowsOut o = {m->x, W(m->wo), S(m->wo), dim};
                 const T *const ots[1] = {&m->wo[l]};
-                rc = gemm_tail(&o, ots, 1, m->att, qd, &t);
+                rc = gemm_tail(&o, ots, 1, m->att, qd, &t, att_packed ? m->att_pack : nullptr);
                 xb_packed = rc == ALJABR_ROCM_OK && packs;
                 if (rc == ALJABR_ROCM_OK) {
                     xb_scaled = defer;
@@ -1299,7 +1313,9 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
     ALJ_TRY(enqueue_matmul_typed(lg, m->xb, m->lm_head.w, m->lm_head.s, m->lm_head.type, bs, dim, c.vocab, B,
                                  m->mm_part, m->mm_part_floats));
     ALJ_MARK(m->lm_head.type == ALJABR_ROCM_TYPE_F16 ? "lm_head_f16" : "lm_head", mm_bytes(m->lm_head, c.vocab, dim, false));
-    ALJ_TRY(enqueue_argmax(next, lg, B, c.vocab));
+    // The attention split buffer is free by now (stream order): the argmax's
+    // chunk results go there.
+    ALJ_TRY(enqueue_argmax(next, lg, B, c.vocab, m->attn_scratch, m->attn_scratch_bytes));
     ALJ_MARK("argmax", B * static_cast<double>(c.vocab) * f4);
 #undef ALJ_MARK
 #undef ALJ_TRY

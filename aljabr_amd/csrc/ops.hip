@@ -205,6 +205,80 @@ __device__ __forceinline__ void argmax_take(float v, int i, float &best, int &bi
     }
 }
 
+// Wide rows in two launches: workgroup (c, r) finds the maximum of chunk c
+// (kArgmaxChunk columns) of row r with the lowest index among equal values
+// and stores it; one wave per row then takes the best of its chunks' results
+// by the same rule. NaN is never taken, and a row with nothing above -inf
+// yields 0, as in argmax_kernel. The result does not depend on the order in
+// which candidates meet (value first, then the lower index).
+constexpr int kArgmaxChunk = 2048;
+constexpr int kArgmaxThreads = 256;
+struct ArgmaxPart {
+    float v;
+    int i;
+};
+
+__device__ __forceinline__ void argmax_wave(float &best, int &bi) {
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int oi = __shfl_xor(bi, off);
+        argmax_take(ov, oi, best, bi);
+    }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_chunk_kernel(ArgmaxPart *__restrict__ part,
+                                                                      const float *__restrict__ x, int cols) {
+    __shared__ float sv[kArgmaxThreads / 64];
+    __shared__ int si[kArgmaxThreads / 64];
+    const float *row = x + static_cast<long long>(blockIdx.y) * cols;
+    const int c0 = blockIdx.x * kArgmaxChunk;
+    const int c1 = min(c0 + kArgmaxChunk, cols);
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    if ((cols & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+        // float4 j of the chunk: columns c0 + 4j .. +3 (c1 - c0 is a multiple of 4).
+        const float4 *r4 = reinterpret_cast<const float4 *>(row + c0);
+        const int n4 = (c1 - c0) >> 2;
+        float4 v[kArgmaxChunk / 4 / kArgmaxThreads];
+#pragma unroll
+        for (int u = 0; u < kArgmaxChunk / 4 / kArgmaxThreads; ++u) {
+            const int j = threadIdx.x + u * kArgmaxThreads;
+            v[u] = j < n4 ? r4[j] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        }
+#pragma unroll
+        for (int u = 0; u < kArgmaxChunk / 4 / kArgmaxThreads; ++u) {
+            const int i = c0 + 4 * (threadIdx.x + u * kArgmaxThreads);
+            argmax_take(v[u].x, i, best, bi);
+            argmax_take(v[u].y, i + 1, best, bi);
+            argmax_take(v[u].z, i + 2, best, bi);
+            argmax_take(v[u].w, i + 3, best, bi);
+        }
+    } else {
+        for (int i = c0 + static_cast<int>(threadIdx.x); i < c1; i += kArgmaxThreads) argmax_take(row[i], i, best, bi);
+    }
+    argmax_wave(best, bi);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[w] = best;
+        si[w] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < kArgmaxThreads / 64; ++k) argmax_take(sv[k], si[k], best, bi);
+        part[static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x] = ArgmaxPart{best, bi};
+    }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(int *__restrict__ out, const ArgmaxPart *__restrict__ part,
+                                                          int chunks) {
+    const ArgmaxPart *pr = part + static_cast<size_t>(blockIdx.x) * chunks;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int c = threadIdx.x; c < chunks; c += 64) argmax_take(pr[c].v, pr[c].i, best, bi);
+    argmax_wave(best, bi);
+    if (threadIdx.x == 0) out[blockIdx.x] = bi == 0x7fffffff ? 0 : bi;
+}
+
 // One 1024-thread workgroup per row; ties resolve to the lowest index. Rows
 // of 16-byte aligned float4s are read eight loads per thread per trip.
 __global__ __launch_bounds__(1024) void argmax_kernel(int *__restrict__ out, const float *__restrict__ x, int cols) {
@@ -339,9 +413,23 @@ int enqueue_add(float *a, const float *b, long long n) {
     return ALJABR_ROCM_OK;
 }
 
-int enqueue_argmax(int *out, const float *x, int rows, int cols) {
+int enqueue_argmax(int *out, const float *x, int rows, int cols, void *part, size_t part_bytes) {
+    const int chunks = (cols + kArgmaxChunk - 1) / kArgmaxChunk;
+    if (part && chunks > 1 && static_cast<size_t>(rows) * chunks * sizeof(ArgmaxPart) <= part_bytes &&
+        aligned(part, 8)) {
+        ArgmaxPart *pp = static_cast<ArgmaxPart *>(part);
+        hipLaunchKernelGGL(argmax_chunk_kernel, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(rows)),
+                           dim3(kArgmaxThreads), 0, current_stream(), pp, x, cols);
+        hipLaunchKernelGGL(argmax_final_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, current_stream(), out,
+                           pp, chunks);
+        return ALJABR_ROCM_OK;
+    }
     hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(1024), 0, current_stream(), out, x, cols);
     return ALJABR_ROCM_OK;
+}
+
+size_t argmax_part_bytes(int rows, int cols) {
+    return static_cast<size_t>(rows) * ((cols + kArgmaxChunk - 1) / kArgmaxChunk) * sizeof(ArgmaxPart);
 }
 
 int enqueue_embed(float *x, const float *embed, const int *tokens, int batch, int dim, int vocab) {
@@ -439,7 +527,15 @@ int aljabr_rocm_argmax(void *out_i32, const void *x, int rows, int cols) {
     ALJ_CHECK_READY();
     ALJ_REQUIRE(out_i32 && x, "out and x must be non-null device pointers");
     ALJ_REQUIRE(rows > 0 && cols > 0, "bad dimensions rows=%d cols=%d", rows, cols);
-    enqueue_argmax(static_cast<int *>(out_i32), static_cast<const float *>(x), rows, cols);
+    // The chunk results in the stream's scratch, except under graph capture
+    // (the scratch may not grow then): one workgroup per row instead.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusActive;
+    void *part = nullptr;
+    const size_t pb = argmax_part_bytes(rows, cols);
+    if (cols > kArgmaxChunk && hipStreamIsCapturing(current_stream(), &cs) == hipSuccess &&
+        cs == hipStreamCaptureStatusNone)
+        part = stream_scratch(pb, kScratchPartials);
+    enqueue_argmax(static_cast<int *>(out_i32), static_cast<const float *>(x), rows, cols, part, part ? pb : 0);
     return finish_launch("argmax");
 }
 

@@ -27,14 +27,6 @@ __device__ __forceinline__ float slice_total(const float *__restrict__ part, siz
 
 __device__ __forceinline__ uint16_t f16_bits(float v) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v)); }
 
-// Index (in fp16 elements) of element (m, c) of an [M][K] activation in the
-// NF4 GEMM's A image: [m/16][c/64][(c%16)/8][lane 16*((c%64)/16) + m%16]
-// [c%8] (matmul_mfma.hip, nf4_xpack_kernel).
-__device__ __forceinline__ size_t xpack_index(int m, int c, int K) {
-    const size_t entry = (static_cast<size_t>(m >> 4) * (K >> 6) + (c >> 6)) * 2 + ((c >> 3) & 1);
-    return (entry * 64 + 16 * ((c >> 4) & 3) + (m & 15)) * 8 + (c & 7);
-}
-
 // Four consecutive elements (c % 4 == 0) as fp16 (rounded to nearest): one
 // 8-byte store.
 __device__ __forceinline__ void xpack_store4(uint16_t *xp, int m, int c, int K, float4 v) {

@@ -47,13 +47,24 @@ def test_swiglu_and_add(rocm, dev, oracle, n):
     assert np.array_equal(dev.get(gd), (g + u).astype(np.float32))
 
 
-def test_argmax_first_index_on_ties(rocm, dev, oracle):
-    x = oracle.normal(6, 3 * 128256).reshape(3, -1)
-    x[1, 17] = x[1, 99999] = 50.0
-    xd, out = dev.put(x), dev.empty(3, np.int32)
-    rocm.call("aljabr_rocm_argmax", dev.ptr(out), dev.ptr(xd), 3, x.shape[1])
+@pytest.mark.parametrize("cols", [128256, 5003, 2048, 1000])
+def test_argmax_first_index_on_ties(rocm, dev, oracle, cols):
+    """Chunked (wide rows: chunk maxima, then one wave per row) and
+    one-workgroup (rows of at most one chunk) forms; float4 and scalar reads
+    (cols % 4); ties across chunks, NaN never taken, an all -inf row gives 0."""
+    x = oracle.normal(6 + cols, 6 * cols).reshape(6, -1)
+    x[1, 17] = x[1, cols - 3] = 50.0                  # tie: the lower index wins
+    x[2, :] = -np.inf
+    x[3, ::7] = np.nan
+    x[3, cols // 2] = 40.0
+    x[4, :] = 0.0
+    x[4, cols - 1] = -0.0
+    x[5, cols - 1] = 60.0
+    xd, out = dev.put(x), dev.empty(6, np.int32)
+    rocm.call("aljabr_rocm_argmax", dev.ptr(out), dev.ptr(xd), 6, cols)
     got = dev.get(out)
-    assert got[0] == int(np.argmax(x[0])) and got[1] == 17 and got[2] == int(np.argmax(x[2]))
+    want = [int(np.argmax(x[0])), 17, 0, cols // 2, 0, cols - 1]
+    assert list(got) == want
 
 
 def _host_model(oracle, cfg, seed):
