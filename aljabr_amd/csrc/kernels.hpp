@@ -224,6 +224,15 @@ size_t nf4_xpack_bytes(int M, int K);
 // scratch. ALJABR_ROCM_ERR_UNSUPPORTED when the shape does not fit.
 int gguf_gemm_pass(const RowsOut *outs, int nseg, const float *A, int K, int type, int M, bool add, float *part,
                    size_t part_floats, const SliceTail *tail);
+// Q4_K GEMM pass of M <= 64 tokens with the activations held in registers
+// as fp16 (rounded once: an A image built first, or `xpacked`; K % 4096 ==
+// 0, A 16-byte aligned, up to three stacked matrices, all but the last a
+// multiple of 16 rows; deterministic). Partials and the image go to `part`
+// (q4k_gemm_scratch_floats(M, N, K) floats suffice) or the stream's scratch.
+// ALJABR_ROCM_ERR_UNSUPPORTED when the shape does not fit.
+int q4k_gemm_pass(const RowsOut *outs, int nseg, const float *A, int K, int M, bool add, float *part,
+                  size_t part_floats, const SliceTail *tail, const uint16_t *xpacked);
+size_t q4k_gemm_scratch_floats(int M, int N, int K);
 // Floats of `part` enqueue_nf4_mfma_multi needs for M tokens over N stacked
 // rows and K (every pass, with or without a tail, xpacked null).
 size_t nf4_mfma_scratch_floats(int M, int N, int K);

@@ -633,6 +633,11 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
         for (int i = 0; i < nseg; ++i) o[i] = RowsOut{outs[i].y, outs[i].w, nullptr, outs[i].n};
         const int r = gguf_gemm_pass(o, nseg, A, K, type, M, accumulate, part, part_floats, tail);
         if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
+    } else if (type == ALJABR_ROCM_TYPE_Q4_K) {
+        RowsOut o[3];
+        for (int i = 0; i < nseg; ++i) o[i] = RowsOut{outs[i].y, outs[i].w, nullptr, outs[i].n};
+        const int r = q4k_gemm_pass(o, nseg, A, K, M, accumulate, part, part_floats, tail, nullptr);
+        if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
     }
     hipStream_t s = current_stream();
     const int ks = kq_slice(args.N, K);
@@ -722,7 +727,10 @@ int enqueue_kquant_mfma(float *C, const float *A, const uint8_t *W, int K, int N
 size_t kquant_mfma_scratch_floats(int M, int N, int K) {
     if (M < 2 || N < 1 || K % 512 != 0) return 0;
     const int slices = K / kq_slice(N, K);
-    return slices > 1 ? static_cast<size_t>(slices) * M * N : 0;
+    const size_t kq = slices > 1 ? static_cast<size_t>(slices) * M * N : 0;
+    // The Q4_K register-resident kernel's partials and fp16 A image.
+    const size_t q4k = q4k_gemm_scratch_floats(M, N, K);
+    return kq > q4k ? kq : q4k;
 }
 
 }  // namespace aljabr

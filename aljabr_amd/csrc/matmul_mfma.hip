@@ -1232,6 +1232,206 @@ __global__ __launch_bounds__(kGemmThreads) void gguf_gemm_kernel(GemmArgs a) {
     }
 }
 
+// ---- GGUF Q4_K GEMM with the activations held in registers --------------
+//
+// The NF4 GEMM's structure (the same fp16 A-fragment image, the same
+// rounding of the activations to fp16 once) for Q4_K super-blocks: wave w of
+// K slice s owns super-block 8s + w of every row (256 elements, 144 bytes:
+// f16 d, f16 dmin, 12 bytes of 6-bit scale and min codes, qs[128] with
+// elements 64c + l and 64c + 32 + l in the low and high nibble of byte
+// 32c + l). A 64-element block c of the image holds, for lane l = 16g + i,
+// elements 64c + 16g + 8jj + e (jj < 2, e < 8) of token i: the low nibbles of
+// bytes 32c + 16(g%2) + 8jj + e when g < 2 (sub-block 2c), the high ones when
+// g >= 2 (sub-block 2c + 1). B fragments are exact fp16 integers with the
+// scale folded in, q*sc (<= 15*63 = 945: one packed fp16 FMA of the magic
+// 1024 + q, exact), and a second pair of MFMAs against the min code m (<= 63)
+// gives sum(x*m); the accumulators take d * (the first) - dmin * (the
+// second), the min term only where one of the block's two min codes is
+// non-zero (a zero min code adds nothing whatever dmin holds). The rows'
+// shares of a tile (16 x 144 bytes) arrive by LDS-DMA exactly as the Q4_0
+// ones with 8 blocks (the same slot image).
+__device__ __forceinline__ uint32_t gg_hfma(uint32_t v, uint32_t s, uint32_t c) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, v), __builtin_bit_cast(h2, s),
+                                                                  __builtin_bit_cast(h2, c)));
+}
+
+// LDS of the Q4_K GEMM: the per-tile reduction buffers of MT token tiles,
+// then the per-wave rings of NSB * 144-byte row shares (the Q4_0 slot of
+// 8 * NSB blocks).
+template <int MT, int NSB>
+struct Q4kLds {
+    static constexpr int kDma = GgLds<0, 8 * NSB>::kDma;
+    static constexpr uint32_t kSlot = GgLds<0, 8 * NSB>::kSlot;
+    static constexpr uint32_t kRedBuf = kGemmWaves * MT * 1024;
+    static constexpr uint32_t kRedOff = 0;
+    static constexpr uint32_t kRingOff = 2 * kRedBuf;
+    static constexpr int kD = static_cast<int>((kGemmLdsMax - kRingOff) / (kGemmWaves * kSlot));
+    static constexpr int D = kD > 4 ? 4 : kD;
+    static constexpr uint32_t kBytes = kRingOff + kGemmWaves * D * kSlot;
+    static_assert(D >= 2 && kBytes <= kGemmLdsMax, "ring of at least two tiles");
+};
+
+// The 6-bit scale and min codes of sub-blocks 2c and 2c+1 from the scale
+// words w1 = bytes 4..7, w2 = 8..11, w3 = 12..15 of a Q4_K super-block.
+__device__ __forceinline__ void q4k_codes6(uint32_t w1, uint32_t w2, uint32_t w3, int c, uint32_t &sc0,
+                                           uint32_t &sc1, uint32_t &mn0, uint32_t &mn1) {
+    const uint32_t o = 16 * (c & 1);
+    if (c < 2) {
+        sc0 = __builtin_amdgcn_ubfe(w1, o, 6);
+        sc1 = __builtin_amdgcn_ubfe(w1, o + 8, 6);
+        mn0 = __builtin_amdgcn_ubfe(w2, o, 6);
+        mn1 = __builtin_amdgcn_ubfe(w2, o + 8, 6);
+    } else {
+        sc0 = __builtin_amdgcn_ubfe(w3, o, 4) | (__builtin_amdgcn_ubfe(w1, o + 6, 2) << 4);
+        sc1 = __builtin_amdgcn_ubfe(w3, o + 8, 4) | (__builtin_amdgcn_ubfe(w1, o + 14, 2) << 4);
+        mn0 = __builtin_amdgcn_ubfe(w3, o + 4, 4) | (__builtin_amdgcn_ubfe(w2, o + 6, 2) << 4);
+        mn1 = __builtin_amdgcn_ubfe(w3, o + 12, 4) | (__builtin_amdgcn_ubfe(w2, o + 14, 2) << 4);
+    }
+}
+
+template <int MT, int NSB, int RT>
+__global__ __launch_bounds__(kGemmThreads) void q4k_gemm_kernel(GemmArgs a) {
+    using GL = Q4kLds<MT, NSB>;
+    constexpr int D = GL::D;
+    static_assert(RT == 0 || RT * kGemmWaves * MT * 1024 <= GL::kBytes, "final reduction fits the LDS");
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i16 = lane & 15, g = lane >> 4;
+    const int kw = (static_cast<int>(blockIdx.x) * kGemmWaves + wave) * 256 * NSB;
+    const int stride = gridDim.y;
+    const int last = a.tiles - 1;
+    const uint32_t ring = GL::kRingOff + wave * D * GL::kSlot;
+    constexpr int NC = 4 * NSB;                  // 64-element blocks per wave
+
+    // The A fragments first (NC 64-element blocks per token tile, two
+    // 16-byte loads each), then the first D tiles' weights.
+    int tile = blockIdx.y;
+    int left = (last - tile) / stride;           // tiles of the walk after the current one
+    const int kbs = a.K >> 6;
+    u32x4v raw[MT][NC][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+                raw[mt][c][jj] = gload_untracked(a.xp + (static_cast<size_t>(mt * kbs + (kw >> 6) + c) * 2 + jj) * 64 + lane);
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (d <= left) gg_dma<0, 8 * NSB>(a, tile + d * stride, kw, ring + d * GL::kSlot, lane);
+    wait_tiles<GL::kDma, D>(left + 1);           // the fragment loads (issued first) have landed
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) settle(raw[mt][c][jj]);
+
+    const uint32_t nsh = 4u * static_cast<uint32_t>(g >> 1);
+    int slot = 0;
+    int buf = 0;
+    f32x4m keep[RT > 0 ? RT : 1][MT];
+    int nt = 0;
+    for (;;) {
+        const uint32_t sb = ring + slot * GL::kSlot;
+        wait_tiles<GL::kDma, D - 1>(left);       // this tile's DMA loads have landed
+        // Row i16's header of each super-block (bytes 144u .. 144u+15: d,
+        // dmin, the scale codes; 16-byte piece 9u) and its 16 code bytes of
+        // each pair (bytes 144u + 16 + 32c + 16(g%2) ..), then the slot is
+        // refilled D tiles ahead.
+        u32x4v hdr[NSB];
+        u32x4v qw[NC];
+#pragma unroll
+        for (int u = 0; u < NSB; ++u) {
+            hdr[u] = *lds<lds_u32x4>(sb + 256 * (9 * u) + 16 * i16);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                qw[4 * u + c] = *lds<lds_u32x4>(sb + 256 * (9 * u + 1 + 2 * c + (g & 1)) + 16 * i16);
+        }
+        wait_lgkmcnt0();
+        if (left >= D) gg_dma<0, 8 * NSB>(a, tile + D * stride, kw, sb, lane);
+
+        f32x4m acc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4m{0.0f, 0.0f, 0.0f, 0.0f};
+        const f32x4m z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+            const int u = cc >> 2, c = cc & 3;
+            const float dd = f16_bits_to_f32(hdr[u].x & 0xffffu);
+            const float dmin = f16_bits_to_f32(hdr[u].x >> 16);
+            uint32_t sc0, sc1, mn0, mn1;
+            q4k_codes6(hdr[u].y, hdr[u].z, hdr[u].w, c, sc0, sc1, mn0, mn1);
+            const uint32_t sc = g < 2 ? sc0 : sc1, mn = g < 2 ? mn0 : mn1;
+            // fp16 pairs: sc (exact), -1024*sc (exact), mn (exact).
+            const uint32_t sch = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(static_cast<float>(sc))));
+            const uint32_t sc2 = sch | (sch << 16);
+            const uint32_t nbh = static_cast<uint32_t>(
+                __builtin_bit_cast(uint16_t, static_cast<_Float16>(-1024.0f * static_cast<float>(sc))));
+            const uint32_t nb2 = nbh | (nbh << 16);
+            const uint32_t mnh = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(static_cast<float>(mn))));
+            const uint32_t mn2 = mnh | (mnh << 16);
+            const half8 bm = __builtin_bit_cast(half8, u32x4v{mn2, mn2, mn2, mn2});
+            const uint32_t w[4] = {qw[cc].x, qw[cc].y, qw[cc].z, qw[cc].w};
+            half8 bq[2];
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const uint32_t w0 = (w[2 * jj] >> nsh) & 0x0f0f0f0fu, w1 = (w[2 * jj + 1] >> nsh) & 0x0f0f0f0fu;
+                bq[jj] = __builtin_bit_cast(half8, u32x4v{gg_hfma(gg_magic<0>(w0), sc2, nb2), gg_hfma(gg_magic<1>(w0), sc2, nb2),
+                                                          gg_hfma(gg_magic<0>(w1), sc2, nb2), gg_hfma(gg_magic<1>(w1), sc2, nb2)});
+            }
+            const bool has_min = (mn0 | mn1) != 0;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const half8 x0 = __builtin_bit_cast(half8, raw[mt][cc][0]), x1 = __builtin_bit_cast(half8, raw[mt][cc][1]);
+                f32x4m cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, bq[0], z4, 0, 0, 0);
+                cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, bq[1], cq, 0, 0, 0);
+                f32x4m cm = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, bm, z4, 0, 0, 0);
+                cm = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, bm, cm, 0, 0, 0);
+                const float dm = has_min ? dmin : 0.0f;
+                acc[mt].x = fmaf(dd, cq.x, acc[mt].x) - (has_min ? dm * cm.x : 0.0f);
+                acc[mt].y = fmaf(dd, cq.y, acc[mt].y) - (has_min ? dm * cm.y : 0.0f);
+                acc[mt].z = fmaf(dd, cq.z, acc[mt].z) - (has_min ? dm * cm.z : 0.0f);
+                acc[mt].w = fmaf(dd, cq.w, acc[mt].w) - (has_min ? dm * cm.w : 0.0f);
+            }
+        }
+
+        if constexpr (RT > 0) {
+#pragma unroll
+            for (int t = 0; t < RT; ++t)
+                if (t == nt)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) keep[t][mt] = acc[mt];
+            ++nt;
+        } else {
+            const uint32_t rb = GL::kRedOff + buf * GL::kRedBuf;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) *lds<lds_f32x4m>(rb + ((wave * MT + mt) * 64 + lane) * 16) = acc[mt];
+            lds_barrier();
+            gemm_tile_out<MT>(a, rb, tile, tid);
+        }
+        buf ^= 1;
+        slot = slot + 1 == D ? 0 : slot + 1;
+        tile += stride;
+        if (--left < 0) break;
+    }
+    wait_vmcnt<0>();                             // no LDS-DMA write may land after the wave ends (or in the reduction)
+    if constexpr (RT > 0) {
+        lds_barrier();
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+            if (t < nt)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    *lds<lds_f32x4m>(t * (kGemmWaves * MT * 1024) + ((wave * MT + mt) * 64 + lane) * 16) = keep[t][mt];
+        lds_barrier();
+        for (int t = 0; t < nt; ++t)
+            gemm_tile_out<MT>(a, t * (kGemmWaves * MT * 1024), blockIdx.y + t * stride, tid);
+    }
+}
+
 }  // namespace
 
 // The activation-stationary NF4 GEMM's plan for N stacked rows over K with
@@ -1424,6 +1624,99 @@ int gguf_gemm_pass(const RowsOut *outs, int nseg, const float *A, int K, int typ
     if (tail) return enqueue_slice_tail(*tail, args.part, slices, M, args.N);
     if (slices > 1) return enqueue_slice_sum(args.y, args.end, nseg, M, args.N, args.part, slices, add);
     return ALJABR_ROCM_OK;
+}
+
+// Q4_K pass of M <= 64 tokens on q4k_gemm_kernel: K slices of 8 waves x NSB
+// 256-element super-blocks (NSB 2 for up to 32 tokens, else 1; K % 4096 ==
+// 0: with one super-block per wave the extra slices and their sum cost more
+// than the LDS-staged kernel's time on the Llama shapes), the workgroups of a
+// slice walking
+// every groups-th 16-row tile; the fp16 A image built first (or passed in
+// `xpacked`), one buffer holding the slice partials (several slices or a
+// tail) and the image, as nf4_gemm_pass. UNSUPPORTED when the shape does not
+// fit or a workgroup's walk is shorter than three tiles.
+int q4k_gemm_pass(const RowsOut *outs, int nseg, const float *A, int K, int M, bool add, float *part,
+                  size_t part_floats, const SliceTail *tail, const uint16_t *xpacked) {
+    if (M < 1 || M > 64 || nseg < 1 || nseg > 3 || K % 4096 != 0 || !aligned(A, 16)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    GemmArgs args{};
+    long long end = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (i < nseg) {
+            const RowsOut &o = outs[i];
+            if (o.n <= 0 || (i < nseg - 1 && o.n % 16 != 0)) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            end += o.n;
+            if (end > 0x7fff0000LL) return ALJABR_ROCM_ERR_UNSUPPORTED;
+            args.y[i] = o.y;
+            args.w[i] = o.w;
+            args.end[i] = static_cast<int>(end);
+        } else {
+            args.end[i] = 0x7fffffff;
+        }
+    }
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const int mt = (M + 15) / 16;
+    const int nsb = mt <= 2 ? 2 : 1;
+    const int slices = K / (2048 * nsb);
+    const int tiles = static_cast<int>((end + 15) / 16);
+    int gr = cus / slices;
+    if (gr < 1) gr = 1;
+    if (gr > tiles) gr = tiles;
+    const int per = (tiles + gr - 1) / gr;
+    const int groups = (tiles + per - 1) / per;
+    if (per < 3 || groups > 65535) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    args.nseg = nseg;
+    args.x = A;
+    args.M = M;
+    args.N = static_cast<int>(end);
+    args.K = K;
+    args.tiles = tiles;
+    args.add = slices == 1 && add && !tail;
+    const size_t pfl = slices > 1 || tail ? static_cast<size_t>(slices) * M * args.N : 0;
+    const size_t xoff = (pfl + 63) & ~static_cast<size_t>(63);
+    const size_t need = xpacked ? pfl : xoff + static_cast<size_t>(mt) * K * 8;
+    float *buf = !need ? nullptr
+                 : part && need <= part_floats ? part
+                                               : static_cast<float *>(stream_scratch(need * sizeof(float), kScratchPartials));
+    if (need && !buf) return ALJABR_ROCM_ERR_BUFFER;
+    args.part = pfl ? buf : nullptr;
+    args.xp = xpacked ? reinterpret_cast<const u32x4v *>(xpacked) : reinterpret_cast<const u32x4v *>(buf + xoff);
+    hipStream_t s = current_stream();
+    const int rt = mt == 1 ? (per <= 4 ? 4 : per <= 8 ? 8 : 0) : mt == 2 && nsb == 1 && per <= 4 ? 4 : 0;
+    const void *fn = nullptr;
+    uint32_t lds_bytes = 0;
+#define ALJ_Q4K_CASE(MT_, NSB_, RT_)                                                      \
+    if (mt == MT_ && nsb == NSB_ && rt == RT_) {                                           \
+        fn = reinterpret_cast<const void *>(q4k_gemm_kernel<MT_, NSB_, RT_>);              \
+        lds_bytes = Q4kLds<MT_, NSB_>::kBytes;                                             \
+    }
+    ALJ_Q4K_CASE(1, 2, 0) ALJ_Q4K_CASE(1, 2, 4) ALJ_Q4K_CASE(1, 2, 8) ALJ_Q4K_CASE(2, 2, 0)
+    ALJ_Q4K_CASE(3, 1, 0) ALJ_Q4K_CASE(4, 1, 0)
+#undef ALJ_Q4K_CASE
+    if (!fn) return ALJABR_ROCM_ERR_UNSUPPORTED;
+    if (!xpacked) {
+        const int total = mt * (K / 64) * 128;
+        hipLaunchKernelGGL(nf4_xpack_kernel, dim3((total + 255) / 256), dim3(256), 0, s, A,
+                           reinterpret_cast<u32x4v *>(buf + xoff), M, K, total);
+    }
+    static std::atomic<bool> lds_set[5][3][9];   // per (MT, NSB, RT): the attribute is per kernel, per process
+    if (!lds_set[mt][nsb][rt].load(std::memory_order_acquire)) {
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_bytes));
+        lds_set[mt][nsb][rt].store(true, std::memory_order_release);
+    }
+    void *kargs[] = {&args};
+    const hipError_t e = hipLaunchKernel(fn, dim3(static_cast<unsigned>(slices), static_cast<unsigned>(groups)),
+                                         dim3(kGemmThreads), kargs, lds_bytes, s);
+    if (e != hipSuccess) return fail(ALJABR_ROCM_ERR_DEVICE, "q4_k gemm launch: %s", hipGetErrorString(e));
+    if (tail) return enqueue_slice_tail(*tail, args.part, slices, M, args.N);
+    if (slices > 1) return enqueue_slice_sum(args.y, args.end, nseg, M, args.N, args.part, slices, add);
+    return ALJABR_ROCM_OK;
+}
+
+size_t q4k_gemm_scratch_floats(int M, int N, int K) {
+    if (M < 1 || K % 4096 != 0) return 0;
+    const int m = M > 64 ? 64 : M;
+    const size_t pfl = static_cast<size_t>(K / (m <= 32 ? 4096 : 2048)) * m * N;
+    return ((pfl + 63) & ~static_cast<size_t>(63)) + static_cast<size_t>((m + 15) / 16) * K * 8;
 }
 
 // The largest buffer a pass of enqueue_nf4_mfma_multi takes: for the
