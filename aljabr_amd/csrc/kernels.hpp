@@ -83,9 +83,12 @@ struct KqOut {
 // With several 512-element K slices the partial sums go to `part` (at least
 // (K / 512) * M * (stacked rows) floats) or, when that is null or too small,
 // to the stream's scratch; `accumulate` adds the product into the outputs.
+// `xpacked`: A's fp16 image (nf4_xpack_bytes layout) for the Q4_K
+// register-resident kernel where it takes the shape (ignored otherwise).
 struct SliceTail;
 int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate,
-                              float *part = nullptr, size_t part_floats = 0, const SliceTail *tail = nullptr);
+                              float *part = nullptr, size_t part_floats = 0, const SliceTail *tail = nullptr,
+                              const uint16_t *xpacked = nullptr);
 // The K slices' products only (K >= 1024), into part[slice][m][col0 + stacked
 // row] with row stride ld (part holds slices * M * ld floats, col0 % 32 == 0):
 // launches of different types stacked in one buffer, then one slice tail.

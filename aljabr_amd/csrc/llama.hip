@@ -272,9 +272,14 @@ int create_session(const aljabr_rocm_llama_config &c, const aljabr_rocm_llama_te
         }
     }
     // The A images of xb, hb and the attention output for the NF4 GEMMs
-    // (batches of 2..64).
-    const bool packs = m->all_nf4 && c.max_batch >= 2 && c.max_batch <= 64 && c.dim % 64 == 0 && c.ffn % 64 == 0;
-    const bool att_packs = packs && qd % 64 == 0;
+    // (batches of 2..64), and of xb for Q4_K gate/up projections on the
+    // register-resident kernel (K = dim a multiple of 4096).
+    bool q4k_ffn = c.dim % 4096 == 0;
+    for (int l = 0; l < L; ++l)
+        q4k_ffn = q4k_ffn && m->w_gate[l].type == ALJABR_ROCM_TYPE_Q4_K && m->w_up[l].type == ALJABR_ROCM_TYPE_Q4_K;
+    const bool packs = (m->all_nf4 || q4k_ffn) && c.max_batch >= 2 && c.max_batch <= 64 && c.dim % 64 == 0 &&
+                       c.ffn % 64 == 0;
+    const bool att_packs = m->all_nf4 && packs && qd % 64 == 0;
     const size_t pack_bytes = (packs ? ((nf4_xpack_bytes(c.max_batch, c.dim) + 255) & ~size_t(255)) +
                                            ((nf4_xpack_bytes(c.max_batch, c.ffn) + 255) & ~size_t(255))
                                      : 0) +
@@ -991,7 +996,7 @@ int decode_step(aljabr_rocm_llama *m, const int *tok, const int *pos, int B, flo
         if (!kquant_mfma_type(ty) || B > kquant_mfma_max_m(ty)) return ALJABR_ROCM_ERR_UNSUPPORTED;
         KqOut k[3];
         for (int i = 0; i < nseg; ++i) k[i] = KqOut{o[i].y, o[i].w, o[i].n};
-        return enqueue_kquant_mfma_multi(k, nseg, x, K, ty, B, false, m->mm_part, m->mm_part_floats, t);
+        return enqueue_kquant_mfma_multi(k, nseg, x, K, ty, B, false, m->mm_part, m->mm_part_floats, t, xpacked);
     };
     // A residual tail defers RMSNorm's row scale only to a consumer that
     // takes a tail: matrices of one type, or K-quants the matrix cores take.

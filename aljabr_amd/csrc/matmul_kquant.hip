@@ -622,7 +622,7 @@ void kq_launch(const KqArgs &args, int type, int ks, hipStream_t s) {
 // With `tail` (K >= 1024, not accumulating) the slice sums go to the tail
 // kernel instead of the outputs.
 int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K, int type, int M, bool accumulate,
-                              float *part, size_t part_floats, const SliceTail *tail) {
+                              float *part, size_t part_floats, const SliceTail *tail, const uint16_t *xpacked) {
     KqArgs args;
     const int rc = kq_multi_args(outs, nseg, A, K, type, M, args);
     if (rc != ALJABR_ROCM_OK) return rc;
@@ -636,7 +636,7 @@ int enqueue_kquant_mfma_multi(const KqOut *outs, int nseg, const float *A, int K
     } else if (type == ALJABR_ROCM_TYPE_Q4_K) {
         RowsOut o[3];
         for (int i = 0; i < nseg; ++i) o[i] = RowsOut{outs[i].y, outs[i].w, nullptr, outs[i].n};
-        const int r = q4k_gemm_pass(o, nseg, A, K, M, accumulate, part, part_floats, tail, nullptr);
+        const int r = q4k_gemm_pass(o, nseg, A, K, M, accumulate, part, part_floats, tail, xpacked);
         if (r != ALJABR_ROCM_ERR_UNSUPPORTED) return r;
     }
     hipStream_t s = current_stream();
