@@ -78,12 +78,14 @@ def test_kquant_matvec(rocm, dev, oracle, qtype, n, k, m):
 # Matrix-core path (2 <= M <= 32 per pass, K % 512 == 0): M across the pass
 # boundary (33 = 32 + a batch-1 row, 40 = 32 + 8), ragged N, the MLP shapes
 # (256- and 512-element K slices; 28672 rows take four row tiles per wave in
-# Q4_K; the stacked gate/up of Llama-3-8B at the full 32-token pass), and the
-# Q4_K header cases (NaN dmin with zero min codes, dmin 0, -0).
+# Q4_K; the stacked gate/up of Llama-3-8B at the full 32-token pass), ragged
+# N over K = 8192 with one and two 16-token tiles (Q4_K's register-resident
+# kernel), and the Q4_K header cases (NaN dmin with zero min codes, dmin 0,
+# -0).
 @pytest.mark.parametrize("qtype", ["q4_k", "q6_k"])
 @pytest.mark.parametrize("n,k,m", [(300, 512, 2), (257, 1024, 5), (300, 2048, 16), (77, 1536, 31), (129, 4096, 32),
                                    (300, 1024, 33), (100, 3072, 40), (14336, 4096, 8), (4096, 14336, 32),
-                                   (28672, 4096, 8), (28672, 4096, 32)])
+                                   (28672, 4096, 8), (28672, 4096, 32), (12345, 8192, 5), (12345, 8192, 20)])
 def test_kquant_mfma(rocm, dev, oracle, qtype, n, k, m):
     qt = TYPES[qtype]
     blocks = _blocks(oracle, qt, n, k, seed=3 * n + k + m)

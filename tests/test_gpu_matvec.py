@@ -82,11 +82,14 @@ def test_gguf_matvec(rocm, dev, oracle, qtype, n, k, m):
 # GGUF Q4_0 / Q8_0 small-M GEMM on the matrix cores (2 <= M <= 8 per pass,
 # K % 512 == 0): M = 2..8 in one pass, 9..32 in several, 33 (four passes and
 # a last batch-1 row), ragged N, one and several K-slices, workgroups of one,
-# two and (28672 rows, Q4_0) four row tiles, and the Llama shapes.
+# two and (28672 rows, Q4_0) four row tiles, the Llama shapes, and ragged N
+# over K = 8192 on the register-resident kernel (several K slices, a last
+# partial row tile, 8 and 8 + 5 tokens).
 @pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("n,k,m", [(300, 1024, 2), (300, 1024, 3), (257, 2048, 8), (300, 1024, 9), (77, 512, 31),
                                    (300, 1536, 32), (300, 1024, 33), (4096, 14336, 8), (14336, 4096, 8),
-                                   (14336, 4096, 32), (1000, 4096, 5), (28672, 4096, 8)])
+                                   (14336, 4096, 32), (1000, 4096, 5), (28672, 4096, 8), (12345, 8192, 8),
+                                   (12345, 8192, 13)])
 def test_gguf_mfma_small_m(rocm, dev, oracle, qtype, n, k, m):
     qt, ot = {"q4_0": (rocm.TYPE_Q4_0, oracle.QTYPE_Q4_0), "q8_0": (rocm.TYPE_Q8_0, oracle.QTYPE_Q8_0)}[qtype]
     w = oracle.normal(53 + n + k, n * k, 0.0, 0.02)
