@@ -48,6 +48,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--clock-warmup-ms", type=float, default=300.0,
                     help="untimed MLP steps for at least this long before the --warmup steps (the GPU needs "
                          "~15 ms of load to reach its steady clocks); reported as clock_warmup_ms")
+    ap.add_argument("--section-pause-s", type=float, default=2.0,
+                    help="idle seconds before each later section of the default run, so that none is timed in the "
+                         "slowed state a long memory-bound section leaves behind (each section then runs its own "
+                         "untimed warm-up launches); reported as section_pause_s")
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough for 512 MB)")
     ap.add_argument("--no-decode", action="store_true", help="skip the Llama decode measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -802,22 +806,40 @@ def run(args, abi, torch, stream) -> None:
                      "stream_ceiling_us": ceiling["us"], "stream_ceiling_frac": ceiling["frac"]},
     }
     tail = {}
+    # A memory-bound section leaves the GPU measurably slower for a second or
+    # so (measured: Q4_0 14336x4096 at M = 1 8.7 us, 9.6 us right after the
+    # attention grid, 8.8 us after a 2 s pause), so every later section starts
+    # after an idle pause and then runs its own untimed warm-up launches.
+    result["section_pause_s"] = args.section_pause_s
+
+    def pause():
+        torch.cuda.synchronize()
+        time.sleep(args.section_pause_s)
+
     if not args.no_extra:
         log("small-M NF4 GEMM (M = 1, 4, 16, 32, 64)")
+        pause()
         tail["small_m_gemm"] = small_m_bench(abi, torch, stream)
         log("GQA decode attention")
+        pause()
         tail["attention"] = attention_bench(abi, torch, stream)
         log("GGUF Q4_0 / Q8_0 matvec (M = 1, 8)")
+        pause()
         tail["gguf_q4_0_q8_0"] = gguf_q_bench(abi, torch, stream)
         log("GGUF K-quant matvec (Q4_K, Q6_K; M = 1, 4, 8)")
+        pause()
         result["gguf_kquant"] = kquant_bench(abi, torch, stream)
         log("prefill attention (T = S = 512, 2048, 8192)")
+        pause()
         result["prefill_attention"] = prefill_bench(abi, torch, stream)
 
     llama_host = None
     if not args.no_decode:
+        pause()
         result["decode"], llama_host = decode_runs(args, abi, torch, stream, keep_host=not args.no_cpu)
+        pause()
         result["decode_gguf_q4_k_m"] = gguf_decode_runs(args, abi, torch, stream)
+        pause()
         result["registered_step"] = registered_step_runs(args, abi, torch, stream)
 
     result["stream_ceiling"] = {k: ceiling[k] for k in ("bytes_per_launch", "best_workgroups", "us", "GBs", "frac")}
