@@ -918,10 +918,10 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
         // Per block b: dwords 2b (.x) and 2b+1 (.y) of the codes, each decoded
         // by four table reads into two B fragments; the reads of dword d+2
         // go out before the MFMAs of dword d (at most 12 reads outstanding:
-        // the LDS counter tracks 15). Each dword's two MFMAs form one chain,
-        // the block's two chains are added and scaled into acc one block
-        // later.
-        f32x4m acc[MT], f[MT];
+        // the LDS counter tracks 15). The block's four MFMAs form one chain
+        // per token tile (two buffers, by block parity), scaled into acc one
+        // block later.
+        f32x4m acc[MT], f[2][MT];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4m{0.0f, 0.0f, 0.0f, 0.0f};
         const f32x4m z4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -932,42 +932,42 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const int cb = (2 * b) & 3;
-            f32x4m fx[MT], fy[MT];
+            f32x4m (&fc)[MT] = f[b & 1];
             if (b + 1 < NB) decode8_hr(q[b + 1].x, ch, hb[(cb + 2) & 3][0], hb[(cb + 2) & 3][1]);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                fx[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][0], hb[cb][0], z4, 0, 0, 0);
-                fx[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][1], hb[cb][1], fx[mt], 0, 0, 0);
+                fc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][0], hb[cb][0], z4, 0, 0, 0);
+                fc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][1], hb[cb][1], fc[mt], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
             if (b + 1 < NB) decode8_hr(q[b + 1].y, ch, hb[(cb + 3) & 3][0], hb[(cb + 3) & 3][1]);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                fy[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][2], hb[cb + 1][0], z4, 0, 0, 0);
-                fy[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][3], hb[cb + 1][1], fy[mt], 0, 0, 0);
+                fc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][2], hb[cb + 1][0], fc[mt], 0, 0, 0);
+                fc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[mt][b][3], hb[cb + 1][1], fc[mt], 0, 0, 0);
             }
             // The previous block's products are ready by now: scale them in.
             if (b > 0) {
+                const f32x4m (&fp)[MT] = f[(b - 1) & 1];
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    acc[mt].x = fmaf(sc[b - 1], f[mt].x, acc[mt].x);
-                    acc[mt].y = fmaf(sc[b - 1], f[mt].y, acc[mt].y);
-                    acc[mt].z = fmaf(sc[b - 1], f[mt].z, acc[mt].z);
-                    acc[mt].w = fmaf(sc[b - 1], f[mt].w, acc[mt].w);
+                    acc[mt].x = fmaf(sc[b - 1], fp[mt].x, acc[mt].x);
+                    acc[mt].y = fmaf(sc[b - 1], fp[mt].y, acc[mt].y);
+                    acc[mt].z = fmaf(sc[b - 1], fp[mt].z, acc[mt].z);
+                    acc[mt].w = fmaf(sc[b - 1], fp[mt].w, acc[mt].w);
                 }
             }
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) f[mt] = fx[mt] + fy[mt];
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            acc[mt].x = fmaf(sc[NB - 1], f[mt].x, acc[mt].x);
-            acc[mt].y = fmaf(sc[NB - 1], f[mt].y, acc[mt].y);
-            acc[mt].z = fmaf(sc[NB - 1], f[mt].z, acc[mt].z);
-            acc[mt].w = fmaf(sc[NB - 1], f[mt].w, acc[mt].w);
+            const f32x4m fl = f[(NB - 1) & 1][mt];
+            acc[mt].x = fmaf(sc[NB - 1], fl.x, acc[mt].x);
+            acc[mt].y = fmaf(sc[NB - 1], fl.y, acc[mt].y);
+            acc[mt].z = fmaf(sc[NB - 1], fl.z, acc[mt].z);
+            acc[mt].w = fmaf(sc[NB - 1], fl.w, acc[mt].w);
         }
 
         if constexpr (RT > 0) {
