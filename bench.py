@@ -39,6 +39,23 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+# A timed region's launches go out from Python through ctypes at ~4.5 us each
+# (more right after a synchronize), the order of one of the kernels timed
+# here (4-9 us). Started on an idle GPU, a region therefore also times the
+# host's enqueue rate: the GPU waits for the first launch and then runs on a
+# queue only a launch or two deep. A GPU spin queued on the stream just
+# before the start event (~0.4 ms at 2.4 GHz) lets the host enqueue the
+# region's launches while the GPU is busy; the start event fires when the
+# spin ends, so the region times exactly its launches, back to back.
+HEAD_START_CYCLES = 1_000_000
+
+
+def head_start(torch) -> None:
+    """Queue the untimed GPU spin on the current stream (call right before a
+    timed region's start event, after any synchronize)."""
+    torch.cuda._sleep(HEAD_START_CYCLES)
+
+
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -100,10 +117,11 @@ def make_mlp_copies(abi, torch, copies: int):
     return mats
 
 
-def time_mlp(abi, torch, stream, mats, steps: int, warmup: int, clock_warmup_ms: float):
+def time_mlp(abi, torch, stream, mats, steps: int, warmup: int, clock_warmup_ms: float, idle_start: bool = False):
     """Milliseconds of `steps` MLP steps, after untimed steps for at least
     `clock_warmup_ms` of wall time and then `warmup` more; returns (ms,
-    clock warm-up ms, clock warm-up steps)."""
+    clock warm-up ms, clock warm-up steps, ms of a second `steps`-step region
+    started on an idle GPU without the head start, or None)."""
     lib = abi.load()
     x = torch.randn(K_MODEL, device="cuda:0")
     h = torch.randn(FFN, device="cuda:0")
@@ -133,13 +151,25 @@ def time_mlp(abi, torch, stream, mats, steps: int, warmup: int, clock_warmup_ms:
             step(done + i)
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        head_start(torch)
         start.record(stream)
         for i in range(steps):
             step(done + warmup + i)
         end.record(stream)
         end.synchronize()
+        idle_ms = None
+        if idle_start:
+            # The same region as it times without the head start.
+            torch.cuda.synchronize()
+            s2, e2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s2.record(stream)
+            for i in range(steps):
+                step(done + warmup + steps + i)
+            e2.record(stream)
+            e2.synchronize()
+            idle_ms = s2.elapsed_time(e2)
     torch.cuda.synchronize()
-    return start.elapsed_time(end), clock_ms, done
+    return start.elapsed_time(end), clock_ms, done, idle_ms
 
 
 def _cpu_rate(fn, nbytes: int, seconds: float):
@@ -253,6 +283,7 @@ def small_m_bench(abi, torch, stream, ms=(1, 4, 16, 32, 64), launches=60):
             for i in range(5):
                 launch(i)
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            head_start(torch)
             start.record(stream)
             for i in range(launches):
                 launch(i)
@@ -302,6 +333,7 @@ def gguf_q_bench(abi, torch, stream, ms=(1, 8), launches=60):
                 for i in range(20):
                     launch(i)
                 start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                head_start(torch)
                 start.record(stream)
                 for i in range(launches):
                     launch(i)
@@ -358,6 +390,7 @@ def kquant_bench(abi, torch, stream, ms=(1, 4, 8), launches=60):
                 for i in range(20):
                     launch(i)
                 start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                head_start(torch)
                 start.record(stream)
                 for i in range(launches):
                     launch(i)
@@ -402,6 +435,7 @@ def attention_bench(abi, torch, stream, launches=20):
         for i in range(3):
             launch(i)
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        head_start(torch)
         start.record(stream)
         for i in range(launches):
             launch(i)
@@ -438,6 +472,7 @@ def prefill_bench(abi, torch, stream, launches=5):
                 abi.check(rc, "aljabr_rocm_fa4_attention")
         launch()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        head_start(torch)
         start.record(stream)
         for _ in range(launches):
             launch()
@@ -491,6 +526,7 @@ def stream_ceiling(abi, torch, stream, launches: int = 300, wgs=(256, 512, 1024,
             for i in range(launches):
                 go(i)
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            head_start(torch)
             start.record(stream)
             for i in range(launches):
                 go(i)
@@ -553,6 +589,7 @@ def decode_bench(abi, torch, stream, batch: int, ctx: int, steps: int, make_mode
             positions = [torch.full((batch,), first_pos + 1 + i, dtype=torch.int32, device="cuda:0")
                          for i in range(steps)]
             torch.cuda.synchronize()
+            head_start(torch)
             start.record(stream)
             for i in range(steps):
                 tok = step_fn(tok, positions[i], batch)
@@ -767,7 +804,8 @@ def run(args, abi, torch, stream) -> None:
     mats = make_mlp_copies(abi, torch, copies)
     log(f"timing {args.steps} steps after >= {args.clock_warmup_ms:.0f} ms of clock warm-up and {args.warmup} "
         "warmup steps")
-    ms, clock_ms, clock_steps = time_mlp(abi, torch, stream, mats, args.steps, args.warmup, args.clock_warmup_ms)
+    ms, clock_ms, clock_steps, idle_ms = time_mlp(abi, torch, stream, mats, args.steps, args.warmup,
+                                                  args.clock_warmup_ms, idle_start=True)
     launches = 3 * args.steps
     per_launch_ms = ms / launches
     gbs = step_bytes * args.steps / (ms / 1e3) / 1e9
@@ -788,6 +826,12 @@ def run(args, abi, torch, stream) -> None:
         "clock_warmup_ms": round(clock_ms, 1),
         "clock_warmup_steps": clock_steps,
         "ms_per_step": round(ms / args.steps, 5),
+        "timed_region": f"{args.steps} steps after a synchronize and a ~0.4 ms GPU spin queued ahead of the start "
+                        "event (the launches are enqueued while the GPU spins; the spin is not timed)",
+        "idle_start": {"ms_per_step": round(idle_ms / args.steps, 5),
+                       "avg_launch_us": round(idle_ms / (3 * args.steps) * 1e3, 3),
+                       "note": "the same region started on an idle GPU (no spin): it also times the host's "
+                               "enqueue of the first launches"},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
