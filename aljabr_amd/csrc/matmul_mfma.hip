@@ -595,6 +595,7 @@ constexpr int kGemmWaves = 8;
 constexpr int kGemmThreads = kGemmWaves * 64;
 constexpr uint32_t kGemmTable = Lds<1>::kTableBytes;      // the pair table, 32 replicas
 constexpr uint32_t kGemmLdsMax = 160 * 1024;
+constexpr int kAFirstTiles = 8;                               // see nf4_gemm_kernel's prologue
 
 template <int MT, int NB>
 struct GemmLds {
@@ -847,8 +848,12 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
 
     // The wave's A fragments first (16-byte loads of the fragment image,
     // 1 KiB contiguous per instruction; block b of token tile mt as two
-    // pieces), then the first D tiles' weight loads: the fragments arrive
-    // first and the loop starts while the tiles are still in flight.
+    // pieces), then the first D tiles' weight loads. On a short walk (at most
+    // kAFirstTiles tiles) the fragments land before any weight load is
+    // issued, so they do not queue behind the chip-wide flood of ring loads
+    // and the first tile starts earlier; a longer walk gains more from having
+    // its first tiles in flight during that wait (measured on the decode
+    // step's Wo, Q/K/V, down and gate/up walks of 2, 3, 8 and 14 tiles).
     int tile = blockIdx.y;
     int left = (last - tile) / stride;           // tiles of the walk after the current one
     const int kbs = a.K >> 6;
@@ -860,11 +865,18 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
                 raw[mt][b][jj] = gload_untracked(a.xp + (static_cast<size_t>(mt * kbs + (kw >> 6) + b) * 2 + jj) * 64 + lane);
+    if (left < kAFirstTiles) {
+        build_table_hr(tid);
+        wait_vmcnt<0>();                         // the A fragment loads have landed
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-        if (d <= left) gemm_dma<NB>(a, tile + d * stride, kw, ring + d * GL::kSlot, lane);
-    build_table_hr(tid);
-    wait_tiles<GL::kDma, D>(left + 1);           // the A fragment loads (issued first) have landed
+        for (int d = 0; d < D; ++d)
+            if (d <= left) gemm_dma<NB>(a, tile + d * stride, kw, ring + d * GL::kSlot, lane);
+    } else {
+#pragma unroll
+        for (int d = 0; d < D; ++d) gemm_dma<NB>(a, tile + d * stride, kw, ring + d * GL::kSlot, lane);
+        build_table_hr(tid);
+        wait_vmcnt<D * GL::kDma>();              // the A fragment loads (issued first) have landed
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
