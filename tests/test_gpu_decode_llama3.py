@@ -200,6 +200,38 @@ def test_llama3_width_q4_k_m_decode_matches_oracle(rocm, dev, oracle, llama3_q4_
     model.close()
 
 
+def test_llama3_width_gguf_graph_replays_match_eager(rocm, dev, llama3_q4_k_m):
+    """A GGUF mix at B = 32 replayed from a captured step graph against eager
+    steps of a twin session (the same device weights, caches filled with the
+    same values): tokens and logits bit-identical at every step. Inside the
+    graph: the quantized matrix-core GEMMs, their slice tails, and for Q4_K_M
+    the fp16 activation image the residual tails write for the Q4_K gate/up
+    GEMM."""
+    import torch
+    from aljabr_amd.llama import DeviceLlama
+    cfg, dev_w, _ = llama3_q4_k_m
+    batch, max_seq = 32, cfg["max_seq"]
+    eager = DeviceLlama.typed(cfg, dev_w, max_batch=batch, max_seq=max_seq)
+    graph = DeviceLlama.typed(cfg, dev_w, max_batch=batch, max_seq=max_seq)
+    for m in (eager, graph):
+        _prefill(m, 78, keep_host=False)
+    pos = np.array([100 + 61 * b for b in range(batch - 1)] + [2040], np.int32)
+    cur = np.random.default_rng(5).integers(0, cfg["vocab"], batch).astype(np.int32)
+    le = torch.empty(batch * cfg["vocab"], dtype=torch.float32, device="cuda:0")
+    lg = torch.empty_like(le)
+    for step in range(4):
+        print(f"[llama3 width gguf graph] step {step} positions {pos.min()}..{pos.max()}", flush=True)
+        te = dev.get(eager.decode(dev.put(cur), dev.put(pos), batch, logits=le))
+        tg = dev.get(graph.decode_graph(dev.put(cur), dev.put(pos), batch, logits=lg))
+        got_e, got_g = dev.get(le), dev.get(lg)
+        assert np.all(np.isfinite(got_e)), step
+        assert np.array_equal(te, tg) and np.array_equal(got_e, got_g), step
+        cur = te.astype(np.int32)
+        pos = pos + 1
+    eager.close()
+    graph.close()
+
+
 @pytest.fixture(scope="module")
 def llama3_full(rocm):
     import torch
