@@ -78,20 +78,16 @@ __device__ __forceinline__ KScales q4k_scales(const u32x4 &hdr, int j) {
     const float d = f16_bits_to_f32(hdr.x & 0xffffu);
     const float dmin = f16_bits_to_f32(hdr.x >> 16);
     // Sub-blocks 2c and 2c+1 (c = j/2) sit in bytes k = 2(c%2) and k+1 of
-    // each scale dword; 4..7 (j >= 4) split their codes over three bytes.
+    // each scale dword; 4..7 (j >= 4) split their codes over three bytes: a
+    // low nibble of the third dword and the top two bits of the first
+    // (scales) or second (mins). Both cases are formed branch-free as one
+    // dword of 6-bit codes per lane, so a wave runs one path.
     const uint32_t o = 16 * ((j >> 1) & 1);
-    uint32_t sc0, sc1, mn0, mn1;
-    if (j < 4) {
-        sc0 = __builtin_amdgcn_ubfe(hdr.y, o, 6);
-        sc1 = __builtin_amdgcn_ubfe(hdr.y, o + 8, 6);
-        mn0 = __builtin_amdgcn_ubfe(hdr.z, o, 6);
-        mn1 = __builtin_amdgcn_ubfe(hdr.z, o + 8, 6);
-    } else {
-        sc0 = __builtin_amdgcn_ubfe(hdr.w, o, 4) | (__builtin_amdgcn_ubfe(hdr.y, o + 6, 2) << 4);
-        sc1 = __builtin_amdgcn_ubfe(hdr.w, o + 8, 4) | (__builtin_amdgcn_ubfe(hdr.y, o + 14, 2) << 4);
-        mn0 = __builtin_amdgcn_ubfe(hdr.w, o + 4, 4) | (__builtin_amdgcn_ubfe(hdr.z, o + 6, 2) << 4);
-        mn1 = __builtin_amdgcn_ubfe(hdr.w, o + 12, 4) | (__builtin_amdgcn_ubfe(hdr.z, o + 14, 2) << 4);
-    }
+    const bool split = j >= 4;
+    const uint32_t sa = split ? (hdr.w & 0x0f0f0f0fu) | ((hdr.y >> 2) & 0x30303030u) : hdr.y;
+    const uint32_t ma = split ? ((hdr.w >> 4) & 0x0f0f0f0fu) | ((hdr.z >> 2) & 0x30303030u) : hdr.z;
+    const uint32_t sc0 = __builtin_amdgcn_ubfe(sa, o, 6), sc1 = __builtin_amdgcn_ubfe(sa, o + 8, 6);
+    const uint32_t mn0 = __builtin_amdgcn_ubfe(ma, o, 6), mn1 = __builtin_amdgcn_ubfe(ma, o + 8, 6);
     KScales r;
     r.dlo = d * static_cast<float>(sc0);
     r.dhi = d * static_cast<float>(sc1);
