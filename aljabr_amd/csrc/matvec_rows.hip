@@ -21,12 +21,14 @@
 //     l%32 and a wave's reads never conflict; and the address is one v_perm_b32
 //     (code byte into bits 8-15, the lane's r*8 into bits 0-7). Per weight:
 //     half a v_perm, half an LDS read, one FMA.
-//   * Q8_0 converts with v_cvt_f32_ubyte on q^0x80 (= q+128) and subtracts
-//     128*sum(x) per block: one convert and one FMA per weight.
-//   * Q4_K / Q6_K mask the nibbles (and merge Q6_K's two high bits) four
-//     bytes at a time and convert with v_cvt_f32_ubyte; the per-sub-block
-//     scale is applied to the lane's two partial dots, the Q4_K min and the
-//     Q6_K -32 offset through the lane's activation sums.
+//   * Q8_0 converts each signed code byte with one sign-extending byte
+//     convert (v_cvt_f32_i32 with an SDWA byte select): one convert and one
+//     FMA per weight.
+//   * Q4_K takes the pair table of raw nibbles; Q6_K masks the nibbles and
+//     merges its two high bits four bytes at a time and converts with
+//     v_cvt_f32_ubyte. The per-sub-block scale is applied to the lane's two
+//     partial dots, the Q4_K min and the Q6_K -32 offset through the lane's
+//     activation sums.
 //   * Activations are staged once per workgroup with coalesced loads through
 //     a swizzled LDS window (conflict-free), then live in registers: lane l
 //     owns the 32 weights [32l, 32l+32) of its wave's 2048-element K chunk.
@@ -39,7 +41,7 @@
 // waves (waves beyond S*G only help with set-up). Q4_0/Q8_0 rows are read per lane PAIR:
 // lanes 2m and 2m+1 own blocks 2m, 2m+1, 36 (Q4_0) or 68 (Q8_0) bytes that
 // start 4-byte aligned when K % 64 == 0, so each lane loads dwords that lie
-// inside its pair and realigns its block with v_alignbit.
+// inside its pair and realigns its block with one v_perm per word.
 #include "device.hpp"
 #include "internal.hpp"
 #include "kernels.hpp"
@@ -312,7 +314,7 @@ __device__ __forceinline__ float2 pair_at(const char *, uint32_t addr) {
 // sum over the lane's 32 weights of w*x, before the row/block scale.
 template <int FMT>
 __device__ __forceinline__ float row_dot(const RowWords<FMT> &d, const float (&xv)[32], float xsum, float xsum2,
-                                         bool odd, uint32_t cl, const char *tbl, float &scale) {
+                                         uint32_t align_sel, uint32_t cl, const char *tbl, float &scale) {
     if constexpr (kquant_fmt(FMT)) {
         // xsum / xsum2: sums of the lane's low / high activations.
         const int j = __lane_id() & 7;
@@ -374,10 +376,13 @@ __device__ __forceinline__ float row_dot(const RowWords<FMT> &d, const float (&x
         } else {
             dw[4] = d.b.x; dw[5] = d.b.y; dw[6] = d.b.z; dw[7] = d.b.w; dw[8] = d.c;
         }
+        // One v_perm per word with the lane's selector: bytes 2..5 of
+        // (dw[i+1]:dw[i]) in even lanes, dw[i+1] in odd ones; the selector's
+        // low half picks d the same way (bytes 0-1 or 2-3 of dw[0]).
         uint32_t qw[NW];
 #pragma unroll
-        for (int i = 0; i < NW; ++i) qw[i] = odd ? dw[i + 1] : funnel_shift_right(dw[i + 1], dw[i], 16);
-        scale = f16_bits_to_f32(odd ? (dw[0] >> 16) : (dw[0] & 0xffffu));
+        for (int i = 0; i < NW; ++i) qw[i] = __builtin_amdgcn_perm(dw[i + 1], dw[i], align_sel);
+        scale = f16_bits_to_f32(__builtin_amdgcn_perm(0u, dw[0], (align_sel & 0xffffu) - 0x0202u + 0x0c0c0000u));
         if constexpr (FMT == kFmtQ4) {
             float p0 = 0.0f, p1 = 0.0f;
 #pragma unroll
@@ -400,13 +405,15 @@ __device__ __forceinline__ float row_dot(const RowWords<FMT> &d, const float (&x
             float p0 = 0.0f, p1 = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const uint32_t u = qw[i] ^ 0x80808080u;      // int8 q -> q + 128 as u8
-                p0 = fmaf(static_cast<float>(u & 0xffu), xv[4 * i + 0], p0);
-                p1 = fmaf(static_cast<float>((u >> 8) & 0xffu), xv[4 * i + 1], p1);
-                p0 = fmaf(static_cast<float>((u >> 16) & 0xffu), xv[4 * i + 2], p0);
-                p1 = fmaf(static_cast<float>(u >> 24), xv[4 * i + 3], p1);
+                // Signed codes converted directly: one sign-extending byte
+                // convert per weight (an SDWA byte select).
+                const uint32_t u = qw[i];
+                p0 = fmaf(static_cast<float>(static_cast<int8_t>(u & 0xffu)), xv[4 * i + 0], p0);
+                p1 = fmaf(static_cast<float>(static_cast<int8_t>((u >> 8) & 0xffu)), xv[4 * i + 1], p1);
+                p0 = fmaf(static_cast<float>(static_cast<int8_t>((u >> 16) & 0xffu)), xv[4 * i + 2], p0);
+                p1 = fmaf(static_cast<float>(static_cast<int8_t>(u >> 24)), xv[4 * i + 3], p1);
             }
-            return fmaf(-128.0f, xsum, p0 + p1);
+            return p0 + p1;
         }
     }
 }
@@ -590,10 +597,7 @@ __device__ __forceinline__ void rows_body(RowsHot h, const RowsArgs &a, unsigned
         }
     }
     float xsum = 0.0f, xsum2 = 0.0f;
-    if constexpr (FMT == kFmtQ8) {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) xsum += xv[i];
-    } else if constexpr (kquant_fmt(FMT)) {
+    if constexpr (kquant_fmt(FMT)) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             xsum += xv[i];
@@ -603,7 +607,9 @@ __device__ __forceinline__ void rows_body(RowsHot h, const RowsArgs &a, unsigned
 
     const char *tbl = reinterpret_cast<const char *>(smem);
     const uint32_t cl = (lane & 31) * 8;
-    const bool odd = lane & 1;
+    // Q4_0/Q8_0 realignment selector (v_perm): odd lanes' codes start at
+    // dw[1], even lanes' 2 bytes into dw[0].
+    const uint32_t align_sel = (lane & 1) ? 0x07060504u : 0x05040302u;
     float acc[TP];
 #pragma unroll
     for (int t = T; t < TP; ++t) acc[t] = 0.0f;
@@ -619,7 +625,7 @@ __device__ __forceinline__ void rows_body(RowsHot h, const RowsArgs &a, unsigned
             }
         }
         float scale;
-        const float dot = row_dot<FMT>(rw[t], xv, xsum, xsum2, odd, cl, tbl, scale);
+        const float dot = row_dot<FMT>(rw[t], xv, xsum, xsum2, align_sel, cl, tbl, scale);
         acc[t] = dot * scale;
         // Keep the written pipeline: without these the compiler defers every
         // row's arithmetic to the end and holds all lookups in registers.
