@@ -725,9 +725,9 @@ void launch_cfg(const RowsArgs &args, hipStream_t s) {
 }
 
 // T rows per wave (2..32), 8 waves; loads PF rows ahead: 3 when a wave's
-// chunk row is most of its row (S <= 2; 2 for Q4_0, whose 14336 x 4096
-// matvec takes 8.45 us against 8.67 with 3), 4 for longer rows (measured on
-// the Llama MLP shapes: 14336 x 4096 and 4096 x 14336).
+// chunk row is most of its row (S <= 2), 4 for longer rows; Q4_0 and Q4_K
+// 2 and (Q4_K) 3 (measured on the Llama MLP shapes, 14336 x 4096 and
+// 4096 x 14336: Q4_0 8.67 -> 8.40 us, Q4_K 9.3 -> 8.95 and 11.0 -> 10.8 us).
 template <int FMT, int XOP, int EPI, int PF>
 void launch_rows_pf(const RowsArgs &args, int T, hipStream_t s) {
     switch (T) {
@@ -750,9 +750,10 @@ void launch_rows_pf(const RowsArgs &args, int T, hipStream_t s) {
 template <int FMT, int XOP, int EPI>
 void launch_rows(RowsArgs args, int T, hipStream_t s) {
     args.G = 8 / args.S;
-    constexpr int kPfShort = FMT == kFmtQ4 ? 2 : 3;
+    constexpr int kPfShort = FMT == kFmtQ4 || FMT == kFmtQ4K ? 2 : 3;
+    constexpr int kPfLong = FMT == kFmtQ4K ? 3 : 4;
     if (args.S <= 2) launch_rows_pf<FMT, XOP, EPI, kPfShort>(args, T, s);
-    else launch_rows_pf<FMT, XOP, EPI, 4>(args, T, s);
+    else launch_rows_pf<FMT, XOP, EPI, kPfLong>(args, T, s);
 }
 
 // Rows per wave: the per-workgroup set-up (activation staging, the 64 KiB
